@@ -1,0 +1,112 @@
+/*
+ * knurlogic_amd -- C ABI of the MI355X (gfx950) quantized-weight kernels.
+ *
+ * The drop-in boundary for the reference's quantized-weight hot path.  In
+ * the reference (Knurlogic 0.1.9) that path sits behind mlx's Python ops
+ * (mx.quantize / mx.dequantize / mx.quantized_matmul / mx.gather_qmm, mlx
+ * 0.32.3 pinned at pyproject.toml:32) and the reference's own 8-bit-KV decode
+ * kernel (src/knurlogic/engine/kvattn.py:256-291).  Each entry point below
+ * replaces one of those; the Python mirror (knurlogic_amd/ops.py) binds
+ * them with ctypes.
+ *
+ * Conventions
+ *   - Every compute entry point returns 0 on success or a negative code
+ *     (-1 bad argument, -2 HIP error, -3 workspace too small) and leaves a
+ *     message for kmi_last_error() (thread-local).
+ *   - The caller allocates every input, output and workspace buffer (device
+ *     memory); the library never allocates or frees.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
+ *     and is stream-ordered: nothing is synchronised.
+ *   - dtype codes: 0 bfloat16, 1 float16, 2 float32.
+ *   - Packed affine layout (mlx's): element j of a row lives in uint32 word
+ *     j / (32/bits) at bit offset (j % (32/bits)) * bits; scales and biases
+ *     hold one value per group of `group_size` consecutive elements of a row.
+ */
+#ifndef KNURLOGIC_AMD_H
+#define KNURLOGIC_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KMI_ABI_VERSION 1
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* kmi_last_error(void);
+
+/* KMI_ABI_VERSION of the built library. */
+int kmi_abi_version(void);
+
+/*
+ * mx.quantize(w, group_size, bits, mode="affine") over the last axis of a
+ * row-major [rows, cols] tensor.  Replaces mlx's affine quantizer as called
+ * at src/knurlogic/engine/kvquant.py:46-47 (KV append) and
+ * src/knurlogic/engine/families/glm5/architecture/glm5_next/_mlx_vlm/models/
+ * switch_layers.py:38-48 (weights).
+ *   w       [rows, cols] of `dtype`
+ *   wq      [rows, cols*bits/32] uint32 out
+ *   scales, biases [rows, cols/group_size] of `dtype` out
+ * bits in {2, 4, 8}; group_size in {32, 64, 128}.
+ */
+int kmi_quantize_affine(const void* w, int dtype, int64_t rows, int64_t cols,
+                        int group_size, int bits, uint32_t* wq, void* scales,
+                        void* biases, void* stream);
+
+/*
+ * mx.dequantize(wq, scales, biases, group_size, bits, mode="affine",
+ * dtype=out_dtype), as called at src/knurlogic/engine/kvquant.py:50-51.
+ *   rounding 0: out = T(T(scale*q) + bias)  (op-by-op, the default)
+ *   rounding 1: out = T(fma(scale, q, bias))
+ */
+int kmi_dequantize_affine(const uint32_t* wq, const void* scales, const void* biases,
+                          int scale_dtype, int64_t rows, int64_t cols, int group_size,
+                          int bits, void* out, int out_dtype, int rounding, void* stream);
+
+/*
+ * mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits)
+ * -- nn.QuantizedLinear's op (swapped in at
+ * src/knurlogic/engine/model/load_model.py:124-144; wrapped at
+ * src/knurlogic/engine/matmul_padding.py:94-105):
+ *   y[M, N] = x[M, K] @ What[N, K]^T,  What = scale * q + bias,
+ * fp32 accumulation, y rounded once to `dtype`.  x, scales, biases, y share
+ * `dtype`.  Decode shapes (M <= 16) run the streaming GEMV kernel, larger M
+ * the LDS-tiled MFMA GEMM.  Each output row depends only on its own input row.
+ * `workspace` (kmi_qmm_workspace_bytes) holds split-K partials; it may be
+ * NULL when that size is 0.
+ */
+int kmi_qmm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
+            const void* scales, const void* biases, int dtype, int group_size,
+            int bits, void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+size_t kmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits);
+
+/*
+ * mx.gather_qmm(x, w, scales, biases, lhs_indices, rhs_indices,
+ * transpose=True, group_size, bits, sorted_indices) -- QuantizedSwitchLinear's
+ * op (src/knurlogic/engine/families/glm5/architecture/glm5_next/_mlx_vlm/
+ * models/switch_layers.py:71-86), with the broadcast index pairs already
+ * flattened by the caller:
+ *   for p < P, m < M:  y[p, m, :] = x[lhs[p], m, :] @ What[rhs[p]]^T
+ *   x [X, M, K], w [E, N, K*bits/32], scales/biases [E, N, K/group_size],
+ *   lhs/rhs [P] int32, y [P, M, N].
+ * Rows are grouped by expert on the GPU (counting sort into `workspace`), so
+ * each routed expert's packed weights are streamed once per call whether or
+ * not `sorted_indices` holds; the flag is accepted for signature parity.
+ */
+int kmi_gather_qmm(const void* x, int64_t X, int64_t M, int64_t K, const uint32_t* w,
+                   const void* scales, const void* biases, int64_t E, int64_t N,
+                   const int32_t* lhs, const int32_t* rhs, int64_t P, int dtype,
+                   int group_size, int bits, int sorted_indices, void* y,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+size_t kmi_gather_qmm_workspace_bytes(int64_t P, int64_t M, int64_t E, int64_t K,
+                                      int64_t N, int group_size, int bits);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KNURLOGIC_AMD_H */

@@ -1,0 +1,11 @@
+"""knurlogic_amd: the reference's quantized-weight hot path on MI355X.
+
+Drop-in torch-tensor mirrors of mlx's quantized ops and of the module
+classes that call them, backed by hand-written gfx950 HIP kernels behind a
+C ABI (include/knurlogic_amd.h, libknurlogic_amd.so).
+"""
+from .ops import (ROUND_FUSED, ROUND_OP_BY_OP, dequantize, gather_qmm, quantize,
+                  quantized_matmul)
+
+__all__ = ["quantize", "dequantize", "quantized_matmul", "gather_qmm",
+           "ROUND_OP_BY_OP", "ROUND_FUSED"]

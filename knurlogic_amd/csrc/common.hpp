@@ -1,0 +1,126 @@
+// Shared device/host helpers for the gfx950 quantized-weight kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+namespace kmi {
+
+// dtype codes of the C ABI (include/knurlogic_amd.h)
+enum Dtype : int { BF16 = 0, F16 = 1, F32 = 2 };
+
+// ---- error reporting: thread-local message, negative return codes ---------
+enum Err : int {
+    OK = 0,
+    EINVAL_ARG = -1,   // bad shape / unsupported combination
+    EHIP = -2,         // a HIP runtime call failed
+    EWORKSPACE = -3,   // workspace missing or too small
+};
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define KMI_CHECK_ARG(cond, ...)                 \
+    do {                                         \
+        if (!(cond)) {                           \
+            ::kmi::set_error(__VA_ARGS__);       \
+            return ::kmi::EINVAL_ARG;            \
+        }                                        \
+    } while (0)
+
+#define KMI_CHECK_LAUNCH(what)                                               \
+    do {                                                                     \
+        hipError_t e_ = hipGetLastError();                                   \
+        if (e_ != hipSuccess) {                                              \
+            ::kmi::set_error("%s: launch failed: %s", what, hipGetErrorString(e_)); \
+            return ::kmi::EHIP;                                              \
+        }                                                                    \
+    } while (0)
+
+// ---- bf16 / fp16 <-> fp32 (bit exact, round to nearest even) ----------------
+
+__host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(((uint32_t)h) << 16);
+}
+
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+// Storage type tags: the kernels are templated on how an element of the
+// activation / scale dtype is stored and converted.
+struct TBF16 {
+    using storage = uint16_t;
+    static __device__ __forceinline__ float load(storage v) { return bf16_to_f32(v); }
+    static __device__ __forceinline__ storage store(float f) { return f32_to_bf16(f); }
+    static __device__ __forceinline__ float round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+};
+struct TF16 {
+    using storage = uint16_t;
+    static __device__ __forceinline__ float load(storage v) { return f16_to_f32(v); }
+    static __device__ __forceinline__ storage store(float f) { return f32_to_f16(f); }
+    static __device__ __forceinline__ float round(float f) { return f16_to_f32(f32_to_f16(f)); }
+};
+struct TF32 {
+    using storage = float;
+    static __device__ __forceinline__ float load(storage v) { return v; }
+    static __device__ __forceinline__ storage store(float f) { return f; }
+    static __device__ __forceinline__ float round(float f) { return f; }
+};
+
+// ---- MFMA operand vector types ------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// 16x16x32 bf16 MFMA, fp32 accumulate (gfx950).  Lane l holds A[m = l%16]
+// [k-run l/16], B[k-run l/16][n = l%16]; D[m = 4*(l/16)+i][n = l%16] in
+// item i.  A and B share the k-run mapping, so any permutation of k
+// applied to both leaves the product unchanged.
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// Two bytes of a word -> two bf16 (exact: integers 0..255 need 8 significant bits).
+__device__ __forceinline__ uint32_t bytes_to_bf16x2(uint32_t w, int lo_byte) {
+    // (float)(byte) selects v_cvt_f32_ubyteN
+    const float a = (float)((w >> (8 * lo_byte)) & 0xffu);
+    const float b = (float)((w >> (8 * lo_byte + 8)) & 0xffu);
+    // high halves of the two floats: the bf16 bit patterns (truncation is exact)
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+
+// 4-bit nibbles -> bf16 "128 + q" pairs.  Register r holds nibbles r (low
+// half) and r+4 (high half) of the word: k order [0,4,1,5,2,6,3,7].
+__device__ __forceinline__ u32x4 nibbles_to_bf16_magic(uint32_t w) {
+    const uint32_t M = 0x000F000Fu, E = 0x43004300u;
+    u32x4 r;
+    r.x = (w & M) | E;
+    r.y = ((w >> 4) & M) | E;
+    r.z = ((w >> 8) & M) | E;
+    r.w = ((w >> 12) & M) | E;
+    return r;
+}
+
+// ---- misc ---------------------------------------------------------------------
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace kmi

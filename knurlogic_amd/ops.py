@@ -1,0 +1,210 @@
+"""mlx's quantized ops, on torch tensors in MI355X memory.
+
+Same names, argument meaning, defaults and packed layout as mlx 0.32.3's
+``mx.quantize`` / ``mx.dequantize`` / ``mx.quantized_matmul`` /
+``mx.gather_qmm`` (the ops the reference reaches at
+src/knurlogic/engine/kvquant.py:46-51, src/knurlogic/engine/matmul_padding.py:94-105
+and src/knurlogic/engine/families/glm5/architecture/glm5_next/_mlx_vlm/
+models/switch_layers.py:38-48,71-86).  Shape errors raise ``ValueError`` as
+mlx does.  Every op runs a HIP kernel of libknurlogic_amd.so on the
+tensors' device and stream; nothing falls back to the CPU.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _abi
+
+DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+#: dequantize rounding: T(T(s*q) + b) (mlx's op-by-op order) or T(fma(s, q, b))
+ROUND_OP_BY_OP = 0
+ROUND_FUSED = 1
+
+
+def _lib():
+    return _abi.load()
+
+
+def _on_gpu(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("knurlogic_amd ops take tensors in GPU memory "
+                             f"(got a tensor on {t.device})")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _check_mode(mode: str):
+    if mode != "affine":
+        raise ValueError(f"mode {mode!r}: only 'affine' is implemented")
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+
+
+def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4,
+             mode: str = "affine"):
+    """``mx.quantize``: (wq uint32 [..., K*bits/32], scales, biases
+    [..., K/group_size]) in w's dtype, groups along the last axis."""
+    _check_mode(mode)
+    _on_gpu(w)
+    if w.dtype not in DTYPE_CODE:
+        raise ValueError(f"quantize: dtype {w.dtype} not in bf16/fp16/fp32")
+    if w.ndim < 1 or w.shape[-1] % group_size or (w.shape[-1] * bits) % 32:
+        raise ValueError(f"quantize: the last axis ({w.shape[-1] if w.ndim else None}) "
+                         f"must be a multiple of the group size {group_size}")
+    w = w.contiguous()
+    cols = w.shape[-1]
+    rows = w.numel() // cols if cols else 0
+    lead = tuple(w.shape[:-1])
+    wq = torch.empty(*lead, cols * bits // 32, dtype=torch.uint32, device=w.device)
+    scales = torch.empty(*lead, cols // group_size, dtype=w.dtype, device=w.device)
+    biases = torch.empty_like(scales)
+    L = _lib()
+    _abi.check(L.kmi_quantize_affine(_ptr(w), DTYPE_CODE[w.dtype], rows, cols, group_size,
+                                     bits, _ptr(wq), _ptr(scales), _ptr(biases), _stream(w)),
+               "quantize")
+    return wq, scales, biases
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | None = None,
+               group_size: int = 64, bits: int = 4, mode: str = "affine",
+               dtype: torch.dtype | None = None, rounding: int = ROUND_OP_BY_OP):
+    """``mx.dequantize``: scale * q + bias in ``dtype`` (default: scales'
+    dtype).  ``rounding`` picks the storage rounding order."""
+    _check_mode(mode)
+    if biases is None:
+        raise ValueError("dequantize: affine mode needs biases")
+    _on_gpu(w, scales, biases)
+    out_dtype = dtype or scales.dtype
+    if out_dtype not in DTYPE_CODE or scales.dtype not in DTYPE_CODE:
+        raise ValueError(f"dequantize: dtype {out_dtype} / scales {scales.dtype}")
+    if w.dtype not in (torch.uint32, torch.int32):
+        raise ValueError(f"dequantize: packed weights must be uint32 (got {w.dtype})")
+    cols = w.shape[-1] * 32 // bits
+    if scales.shape[:-1] != w.shape[:-1] or scales.shape[-1] * group_size != cols \
+            or biases.shape != scales.shape:
+        raise ValueError(f"dequantize: shapes {tuple(w.shape)}, scales {tuple(scales.shape)}, "
+                         f"biases {tuple(biases.shape)} do not match group {group_size}, bits {bits}")
+    if biases.dtype != scales.dtype:
+        raise ValueError("dequantize: scales and biases must share a dtype")
+    w, scales, biases = w.contiguous(), scales.contiguous(), biases.contiguous()
+    rows = w.numel() // w.shape[-1] if w.shape[-1] else 0
+    out = torch.empty(*w.shape[:-1], cols, dtype=out_dtype, device=w.device)
+    L = _lib()
+    _abi.check(L.kmi_dequantize_affine(_ptr(w), _ptr(scales), _ptr(biases),
+                                       DTYPE_CODE[scales.dtype], rows, cols, group_size, bits,
+                                       _ptr(out), DTYPE_CODE[out_dtype], int(rounding),
+                                       _stream(w)), "dequantize")
+    return out
+
+
+def _check_affine_operands(x, w, scales, biases, group_size, bits, what):
+    if biases is None:
+        raise ValueError(f"{what}: affine mode needs biases")
+    _on_gpu(x, w, scales, biases)
+    if x.dtype != scales.dtype or biases.dtype != scales.dtype:
+        raise ValueError(f"{what}: x ({x.dtype}), scales ({scales.dtype}) and biases "
+                         f"({biases.dtype}) must share a dtype")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{what}: only bfloat16 activations are implemented (got {x.dtype})")
+    K = x.shape[-1]
+    if w.shape[-1] * 32 // bits != K:
+        raise ValueError(f"{what}: x has {K} features but w packs "
+                         f"{w.shape[-1] * 32 // bits} at {bits} bits")
+    if scales.shape[-1] * group_size != K or scales.shape != biases.shape \
+            or scales.shape[:-1] != w.shape[:-1]:
+        raise ValueError(f"{what}: scales {tuple(scales.shape)} / biases "
+                         f"{tuple(biases.shape)} do not match w {tuple(w.shape)} "
+                         f"at group {group_size}")
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: torch.Tensor | None = None, transpose: bool = True,
+                     group_size: int = 64, bits: int = 4, mode: str = "affine"):
+    """``mx.quantized_matmul``: x [..., K] @ What^T with What [N, K]
+    (transpose=True), fp32 accumulation, the result in x's dtype."""
+    _check_mode(mode)
+    if not transpose:
+        raise ValueError("quantized_matmul: transpose=False is not implemented")
+    if w.ndim != 2:
+        raise ValueError("quantized_matmul: w must be 2-D (use gather_qmm for experts)")
+    _check_affine_operands(x, w, scales, biases, group_size, bits, "quantized_matmul")
+    K = x.shape[-1]
+    N = w.shape[0]
+    x2 = x.contiguous()
+    M = x2.numel() // K if K else 0
+    y = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=x.device)
+    L = _lib()
+    nbytes = L.kmi_qmm_workspace_bytes(M, K, N, group_size, bits)
+    ws = _workspace(nbytes, x.device)
+    _abi.check(L.kmi_qmm(_ptr(x2), M, K, N, _ptr(w.contiguous()), _ptr(scales.contiguous()),
+                         _ptr(biases.contiguous()), DTYPE_CODE[x.dtype], group_size, bits,
+                         _ptr(y), _ptr(ws), nbytes, _stream(x)), "quantized_matmul")
+    return y
+
+
+def _flat_indices(x, w, lhs_indices, rhs_indices):
+    """mx.gather_qmm's index semantics: lhs defaults to every batch element
+    of x, rhs to every batch element of w; the two broadcast together."""
+    dev = x.device
+    xbatch = tuple(x.shape[:-2])
+    wbatch = tuple(w.shape[:-2])
+    if lhs_indices is None:
+        lhs_indices = torch.arange(math.prod(xbatch), device=dev, dtype=torch.int32).reshape(xbatch)
+    if rhs_indices is None:
+        rhs_indices = torch.arange(math.prod(wbatch), device=dev, dtype=torch.int32).reshape(wbatch)
+    lhs = torch.as_tensor(lhs_indices, device=dev)
+    rhs = torch.as_tensor(rhs_indices, device=dev)
+    if lhs.dtype.is_floating_point or rhs.dtype.is_floating_point:
+        raise ValueError("gather_qmm: indices must be integers")
+    lhs, rhs = torch.broadcast_tensors(lhs, rhs)
+    shape = tuple(lhs.shape)
+    return (lhs.reshape(-1).to(torch.int32).contiguous(),
+            rhs.reshape(-1).to(torch.int32).contiguous(), shape)
+
+
+def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+               biases: torch.Tensor | None = None, lhs_indices=None, rhs_indices=None,
+               transpose: bool = True, group_size: int = 64, bits: int = 4,
+               mode: str = "affine", sorted_indices: bool = False):
+    """``mx.gather_qmm``: out[i] = x[lhs[i]] @ What[rhs[i]]^T for x
+    [..., M, K] and w [..., N, K*bits/32]; out [*broadcast(lhs, rhs), M, N].
+    Rows are grouped by expert on the GPU whatever ``sorted_indices`` says,
+    so each routed expert's weights are read once."""
+    _check_mode(mode)
+    if not transpose:
+        raise ValueError("gather_qmm: transpose=False is not implemented")
+    if x.ndim < 2 or w.ndim < 3:
+        raise ValueError("gather_qmm: x needs [..., M, K] and w [..., N, K*bits/32]")
+    _check_affine_operands(x, w, scales, biases, group_size, bits, "gather_qmm")
+    M, K = x.shape[-2], x.shape[-1]
+    N = w.shape[-2]
+    E = math.prod(w.shape[:-2])
+    Xb = math.prod(x.shape[:-2])
+    lhs, rhs, ishape = _flat_indices(x, w, lhs_indices, rhs_indices)
+    P = lhs.numel()
+    y = torch.empty(*ishape, M, N, dtype=x.dtype, device=x.device)
+    if P == 0:
+        return y
+    L = _lib()
+    nbytes = L.kmi_gather_qmm_workspace_bytes(P, M, E, K, N, group_size, bits)
+    ws = _workspace(nbytes, x.device)
+    _abi.check(L.kmi_gather_qmm(_ptr(x.contiguous()), Xb, M, K, _ptr(w.contiguous()),
+                                _ptr(scales.contiguous()), _ptr(biases.contiguous()), E, N,
+                                _ptr(lhs), _ptr(rhs), P, DTYPE_CODE[x.dtype], group_size, bits,
+                                int(bool(sorted_indices)), _ptr(y), _ptr(ws), nbytes,
+                                _stream(x)), "gather_qmm")
+    return y

@@ -1,0 +1,166 @@
+"""GPU parity: quantized_matmul (decode GEMV M <= 16, prefill GEMM M > 16)
+and gather_qmm through the C ABI, against the oracle on identical seeded
+inputs.  Bar: max |y - ref| / max |ref| <= 1e-2 and cosine >= 0.9999
+(fp32 accumulation, bf16 out)."""
+import functools
+
+import numpy as np
+import pytest
+import torch
+
+import knurlogic_amd as K
+import oracle as O
+from tests.util import assert_close, bf16_normal, to_numpy, to_torch, u32_to_torch
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def _weights(rng, shape, bits, group, dev):
+    w = bf16_normal(rng, shape, 0.02)
+    wq, s, b = O.quantize(w, group, bits)
+    return (wq, s, b), (u32_to_torch(wq, dev), to_torch(s, dev, BF), to_torch(b, dev, BF))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 64, 200])
+def test_qmm_small(dev, bits, group, M):
+    rng = np.random.default_rng(1000 * bits + group + M)
+    N, K_ = 320, 512
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (N, K_), bits, group, dev)
+    x = bf16_normal(rng, (M, K_))
+    y = K.quantized_matmul(to_torch(x, dev, BF), tw, ts, tb, True, group, bits)
+    assert y.shape == (M, N) and y.dtype == BF
+    ref = O.quantized_matmul(x, wq, s, b, True, group, bits, "float32")
+    assert_close(to_numpy(y), ref, what=f"M={M} bits={bits} g={group}")
+
+
+@functools.lru_cache(maxsize=4)
+def _big_weights(bits, shape):
+    w = bf16_normal(np.random.default_rng(7 + bits + shape[0]), shape, 0.02)
+    return O.quantize(w, 64, bits)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 16, 512])
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336)])
+def test_qmm_baseline_shapes(dev, bits, M, shape):
+    """The dense workload: W [14336, 4096] and its reverse, M = 1, 16, 512.
+    The oracle checks a band of output columns (all rows), the rest is
+    covered by the column-block structure of the kernels."""
+    N, K_ = shape
+    wq, s, b = _big_weights(bits, shape)
+    tw, ts, tb = u32_to_torch(wq, dev), to_torch(s, dev, BF), to_torch(b, dev, BF)
+    x = bf16_normal(np.random.default_rng(7 + bits + M + N), (M, K_))
+    y = to_numpy(K.quantized_matmul(to_torch(x, dev, BF), tw, ts, tb, True, 64, bits))
+    cols = np.r_[0:256, N // 2 - 128:N // 2 + 128, N - 256:N]
+    ref = O.quantized_matmul(x, wq[cols], s[cols], b[cols], True, 64, bits, "float32")
+    assert_close(y[:, cols], ref, what=f"{shape} M={M} bits={bits}")
+    assert np.isfinite(y).all()
+
+
+def test_rows_are_independent_bit_for_bit(dev):
+    """Row m of a call depends only on row m (the reference's padding
+    contract, tests/engine/test_per_chip_rounding.py:30-41): within each
+    kernel family a row's bits do not change with the other rows."""
+    rng = np.random.default_rng(11)
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (256, 512), 4, 64, dev)
+    x = to_torch(bf16_normal(rng, (16, 512)), dev, BF)
+    y16 = K.quantized_matmul(x, tw, ts, tb, True, 64, 4)
+    for m in (1, 5, 9):
+        ym = K.quantized_matmul(x[:m], tw, ts, tb, True, 64, 4)
+        assert torch.equal(ym, y16[:m])
+    x64 = to_torch(bf16_normal(rng, (96, 512)), dev, BF)
+    y96 = K.quantized_matmul(x64, tw, ts, tb, True, 64, 4)
+    y40 = K.quantized_matmul(x64[:40], tw, ts, tb, True, 64, 4)
+    assert torch.equal(y40, y96[:40])
+
+
+def test_linearity_at_full_size(dev):
+    """qmm(2x) == 2 qmm(x) bit for bit (power-of-two scaling is exact), and
+    qmm(x1 + x2) ~ qmm(x1) + qmm(x2), at the [14336, 4096] 4-bit shape."""
+    g = torch.Generator(device=dev).manual_seed(1)
+    w = (torch.randn(14336, 4096, device=dev, generator=g) * 0.02).to(BF)
+    wq, s, b = K.quantize(w, 64, 4)
+    x = torch.randn(16, 4096, device=dev, generator=g).to(BF)
+    y = K.quantized_matmul(x, wq, s, b)
+    assert torch.equal(K.quantized_matmul(x * 2, wq, s, b), y * 2)
+    x1 = torch.randn(1, 4096, device=dev, generator=g).to(BF)
+    x2 = torch.randn(1, 4096, device=dev, generator=g).to(BF)
+    ysum = K.quantized_matmul((x1.float() + x2.float()).to(BF), wq, s, b).float()
+    lin = K.quantized_matmul(x1, wq, s, b).float() + K.quantized_matmul(x2, wq, s, b).float()
+    # x1 + x2 is rounded to bf16 before the product: allow that and bf16 outputs
+    assert_close(ysum.cpu().numpy(), lin.cpu().numpy(), max_rel=2e-2, min_cos=0.999,
+                 what="linearity")
+
+
+def test_zero_rows_and_shape_errors(dev):
+    rng = np.random.default_rng(12)
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (64, 128), 4, 64, dev)
+    y = K.quantized_matmul(torch.zeros(0, 128, device=dev, dtype=BF), tw, ts, tb)
+    assert y.shape == (0, 64)
+    with pytest.raises(ValueError):
+        K.quantized_matmul(torch.zeros(2, 96, device=dev, dtype=BF), tw, ts, tb)
+    with pytest.raises(ValueError):
+        K.quantized_matmul(torch.zeros(2, 128, device=dev, dtype=BF), tw, ts, None)
+    with pytest.raises(ValueError):
+        K.quantized_matmul(torch.zeros(2, 128, dtype=BF), tw, ts, tb)   # CPU tensor
+
+
+# --- gather_qmm ----------------------------------------------------------------
+
+@pytest.mark.parametrize("T,k", [(1, 8), (5, 3), (16, 8), (40, 4)])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_unsorted_and_sorted(dev, T, k, bits):
+    rng = np.random.default_rng(T * 10 + k + bits)
+    E, N, K_ = 12, 96, 256
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (E, N, K_), bits, 64, dev)
+    x = bf16_normal(rng, (T, 1, 1, K_))
+    inds = rng.integers(0, E, (T, k)).astype(np.int32)
+    ref = O.gather_qmm(x, wq, s, b, rhs_indices=inds, bits=bits, out_dtype="float32")
+    tx = to_torch(x, dev, BF)
+    ti = torch.from_numpy(inds).to(dev)
+    y = K.gather_qmm(tx, tw, ts, tb, rhs_indices=ti, bits=bits)
+    assert y.shape == (T, k, 1, N)
+    assert_close(to_numpy(y), ref, what="unsorted")
+    # the sorted form SwitchGLU uses for T*k >= 64: x rows gathered by order // k
+    flat = inds.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    xs = x.reshape(T, 1, K_)[order // k]
+    ys = K.gather_qmm(to_torch(xs, dev, BF), tw, ts, tb,
+                      rhs_indices=torch.from_numpy(flat[order]).to(dev), bits=bits,
+                      sorted_indices=True)
+    assert ys.shape == (T * k, 1, N)
+    assert_close(to_numpy(ys)[np.argsort(order)].reshape(T, k, 1, N), ref, what="sorted")
+
+
+def test_gather_qmm_with_lhs_indices_and_bad_experts(dev):
+    rng = np.random.default_rng(21)
+    E, N, K_ = 4, 64, 128
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (E, N, K_), 4, 64, dev)
+    x = bf16_normal(rng, (3, 2, K_))                      # X=3 batches of M=2 rows
+    lhs = np.array([2, 0, 1, 2], np.int32)
+    rhs = np.array([1, 3, 0, 9], np.int32)                # expert 9 is out of range
+    y = K.gather_qmm(to_torch(x, dev, BF), tw, ts, tb, torch.from_numpy(lhs).to(dev),
+                     torch.from_numpy(rhs).to(dev))
+    assert y.shape == (4, 2, N)
+    got = to_numpy(y)
+    for p in range(3):
+        ref = O.quantized_matmul(x[lhs[p]], wq[rhs[p]], s[rhs[p]], b[rhs[p]], True, 64, 4, "float32")
+        assert_close(got[p], ref, what=f"pair {p}")
+    assert (got[3] == 0).all()
+
+
+def test_gather_qmm_moe_decode_shape(dev):
+    """The Qwen3.5-MoE expert shapes (128 experts, 2048 -> 768, 4-bit g64),
+    top-8 of 16 tokens: gate projection through gather_qmm."""
+    rng = np.random.default_rng(22)
+    E, N, K_, T, k = 128, 768, 2048, 16, 8
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (E, N, K_), 4, 64, dev)
+    x = bf16_normal(rng, (T, 1, 1, K_))
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    y = K.gather_qmm(to_torch(x, dev, BF), tw, ts, tb,
+                     rhs_indices=torch.from_numpy(inds).to(dev))
+    ref = O.gather_qmm(x, wq, s, b, rhs_indices=inds, out_dtype="float32")
+    assert_close(to_numpy(y), ref, what="moe decode")

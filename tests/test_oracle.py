@@ -1,0 +1,277 @@
+"""Pins the CPU oracle (CPU only, no GPU).
+
+Each test checks an oracle function against something that does not
+restate it: the reference's own golden vectors, closed-form known answers,
+invariants the mathematics fixes, or an independently written float64
+numpy path -- chosen so a plausible mistake (a dropped term, a wrong sign,
+index or rounding order) fails at least one of them.  Planted mistakes are
+planted in the oracle, here on the CPU.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle as O
+from tests.util import bf16_normal
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+# --- the reference's golden: Qwen3.5-MoE block, bf16, bit for bit -------------
+
+def _golden_block():
+    z = np.load(GOLD / "qwen35_moe_block.npz")
+    gu, dn = z["experts__gate_up_proj"], z["experts__down_proj"]
+    inter = gu.shape[1] // 2        # gate = first half of rows (qwen3_5_moe.py:41-45)
+    fns = (lambda xs, e: O.dense_linear(xs, gu[e, :inter]),
+           lambda xs, e: O.dense_linear(xs, gu[e, inter:]),
+           lambda xs, e: O.dense_linear(xs, dn[e]))
+    shared = (z["shared_expert__gate_proj__weight"], z["shared_expert__up_proj__weight"],
+              z["shared_expert__down_proj__weight"], z["shared_expert_gate__weight"])
+    return z, fns, shared
+
+
+def test_moe_block_matches_the_reference_golden_bit_for_bit():
+    z, fns, shared = _golden_block()
+    y = O.moe_block(z["x"], z["gate__weight"], fns, shared, k=int(z["top_k"]))
+    assert np.array_equal(y, z["expected"])
+
+
+def test_the_golden_catches_rounding_order_mistakes(monkeypatch):
+    z, fns, shared = _golden_block()
+    k = int(z["top_k"])
+
+    def twice_rounded_silu(g, dtype="bfloat16"):   # mlx's bf16 x*sigmoid(x)
+        g32 = np.asarray(g, np.float32)
+        sig = O.round_to(1.0 / (1.0 + np.exp(-g32.astype(np.float64))), dtype)
+        return O.round_to(g32 * sig, dtype)
+
+    def no_renorm(logits, kk, out_dtype="bfloat16"):
+        lg = np.asarray(logits, np.float64)
+        p = np.exp(lg - lg.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        order = np.argsort(-p, axis=-1, kind="stable")[..., :kk]
+        return order.astype(np.int32), O.round_to(np.take_along_axis(p, order, -1), out_dtype)
+
+    def unrounded_combine(y, s, dtype="bfloat16"):
+        return O.round_to((np.asarray(y, np.float64) * np.asarray(s, np.float64)[..., None])
+                          .sum(-2).astype(np.float32), dtype)
+
+    for name, bad in (("silu_rounded", twice_rounded_silu), ("route", no_renorm),
+                      ("combine", unrounded_combine)):
+        with monkeypatch.context() as m:
+            m.setattr(O, name, bad)
+            y = O.moe_block(z["x"], z["gate__weight"], fns, shared, k=k)
+        assert not np.array_equal(y, z["expected"]), name
+
+
+# --- affine quantize: known answers and invariants -----------------------------
+
+def test_quantize_known_answer_max_edge_negative_scale():
+    """Group max 15 has the larger magnitude: scale -1, bias 15, q = 15 - w;
+    the packed words then read 0x89ABCDEF / 0x01234567 (element j in word
+    j/8 at bits 4*(j%8), kvattn.py:128-131 of the reference)."""
+    w = np.tile(np.arange(16, dtype=np.float32), 4)[None]          # one group of 64
+    wq, s, b = O.quantize(w, 64, 4)
+    assert s[0, 0] == -1.0 and b[0, 0] == 15.0
+    assert wq[0, 0] == 0x89ABCDEF and wq[0, 1] == 0x01234567
+    assert np.array_equal(O.unpack_numpy(wq, 4)[0], (15 - w[0]).astype(np.uint32))
+
+
+def test_quantize_known_answer_min_edge_positive_scale():
+    w = -np.tile(np.arange(16, dtype=np.float32), 4)[None]
+    wq, s, b = O.quantize(w, 64, 4)
+    assert s[0, 0] == 1.0 and b[0, 0] == -15.0
+    assert np.array_equal(O.unpack_numpy(wq, 4)[0], (w[0] + 15).astype(np.uint32))
+
+
+def test_quantize_all_zero_group():
+    wq, s, b = O.quantize(np.zeros((1, 64), np.float32), 64, 8)
+    assert (wq == 0).all() and b[0, 0] == 0.0 and s[0, 0] == O.bf16_round(np.float32(-1e-7))
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_quantize_invariants(bits, group):
+    rng = np.random.default_rng(bits * 1000 + group)
+    w = bf16_normal(rng, (64, 512), 0.02)
+    wq, s, b = O.quantize(w, group, bits)
+    q = O.unpack_numpy(wq, bits).astype(np.int64)
+    assert q.min() >= 0 and q.max() <= 2 ** bits - 1
+    wh = O.dequantize_numpy_f64(wq, s, b, group, bits)
+    # round trip within |scale|/2 plus the bf16 rounding of the scale
+    # (unit roundoff 2^-8: <= 2^-8 |s| per code step) -- except where snapping the scale so 0
+    # is a code point shrank it and the far end of the range clipped at the
+    # top code: there the error is below one (snapped) step
+    sg = np.repeat(np.abs(s.astype(np.float64)), group, axis=-1)
+    n_bins = 2 ** bits - 1
+    err = np.abs(wh - w)
+    assert (err <= sg * (1.0 + 2.0 ** -7 * n_bins) + 1e-12).all()
+    over = err > sg * (0.5 + 2.0 ** -8 * (n_bins + 1)) + 1e-12
+    assert (q[over] == n_bins).all()
+    # the larger-magnitude edge of each group is stored as the bias: exact
+    g = w.reshape(64, -1, group)
+    edge = np.where(np.abs(g.min(-1)) > np.abs(g.max(-1)), g.min(-1), g.max(-1))
+    assert np.array_equal(b, edge.astype(np.float32))
+    # and reconstructs exactly at its own position (code 0)
+    idx = np.argmax(g == edge[..., None], axis=-1)
+    qe = np.take_along_axis(q.reshape(64, -1, group), idx[..., None], -1)[..., 0]
+    assert (qe == 0).all()
+
+
+def test_eight_bit_round_trip_is_within_the_references_bar():
+    """tests/engine/test_kvquant.py:37-43: an 8-bit fetch of N(0,1) bf16 is
+    within 0.05 of what went in."""
+    rng = np.random.default_rng(1)
+    x = bf16_normal(rng, (2, 40, 64))
+    wq, s, b = O.quantize(x, 64, 8)
+    assert np.abs(O.dequantize(wq, s, b, 64, 8) - x).max() < 0.05
+
+
+# --- dequantize: closed form, rounding order ----------------------------------
+
+def test_dequantize_closed_form():
+    codes = np.arange(16, dtype=np.uint32)
+    word0 = np.uint32(sum(int(c) << (4 * i) for i, c in enumerate(codes[:8])))
+    word1 = np.uint32(sum(int(c) << (4 * i) for i, c in enumerate(codes[8:])))
+    wq = np.array([[word0, word1] * 4], np.uint32)                 # 64 elements
+    out = O.dequantize(wq, np.array([[0.5]], np.float32), np.array([[-1.0]], np.float32), 64, 4)
+    assert np.array_equal(out[0], 0.5 * np.tile(np.arange(16), 4) - 1.0)
+
+
+def test_dequantize_rounding_orders_differ_where_they_must():
+    """s = 1 + 2^-7, q = 3, b = -2^-7: T(T(s*q)+b) = 3.03125 (two ties to
+    even), T(fma) = 3.015625 -- the switch is real."""
+    wq = np.array([[3] + [0] * 7], np.uint32)                       # element 0 -> q 3
+    s = np.array([[1.0078125]], np.float32)
+    b = np.array([[-0.0078125]], np.float32)
+    two = O.dequantize(wq, s, b, 64, 4, rounding=O.ROUND_OP_BY_OP)
+    one = O.dequantize(wq, s, b, 64, 4, rounding=O.ROUND_FUSED)
+    assert two[0, 0] == 3.03125 and one[0, 0] == 3.015625
+
+
+def test_dequantize_matches_numpy_within_one_rounding():
+    rng = np.random.default_rng(2)
+    w = bf16_normal(rng, (32, 256), 0.02)
+    for bits in (4, 8):
+        wq, s, b = O.quantize(w, 64, bits)
+        exact = O.dequantize_numpy_f64(wq, s, b, 64, bits)
+        fused = O.dequantize(wq, s, b, 64, bits, rounding=O.ROUND_FUSED)
+        assert np.array_equal(fused, O.bf16_round(exact.astype(np.float32)))
+        f32 = O.dequantize(wq, s, b, 64, bits, dtype="float32", rounding=O.ROUND_FUSED)
+        assert np.abs(f32 - exact).max() <= np.abs(exact).max() * 2 ** -23
+
+
+# --- quantized_matmul / gather_qmm ------------------------------------------------
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_equals_float64_brute_force(bits):
+    rng = np.random.default_rng(3)
+    w = bf16_normal(rng, (48, 256), 0.02)
+    x = bf16_normal(rng, (5, 256))
+    wq, s, b = O.quantize(w, 64, bits)
+    ref = x.astype(np.float64) @ O.dequantize_numpy_f64(wq, s, b, 64, bits).T
+    got = O.quantized_matmul(x, wq, s, b, True, 64, bits, "float32")
+    assert np.abs(got - ref).max() <= np.abs(ref).max() * 1e-6
+    # transpose=False: w quantized along its output axis
+    wt = bf16_normal(rng, (256, 64), 0.02)
+    wqt, st, bt = O.quantize(wt, 64, bits)
+    reft = x.astype(np.float64) @ O.dequantize_numpy_f64(wqt, st, bt, 64, bits)
+    gott = O.quantized_matmul(x, wqt, st, bt, False, 64, bits, "float32")
+    assert np.abs(gott - reft).max() <= np.abs(reft).max() * 1e-6
+
+
+def test_qmm_is_linear_and_row_independent():
+    rng = np.random.default_rng(4)
+    w = bf16_normal(rng, (64, 128), 0.02)
+    wq, s, b = O.quantize(w, 64, 4)
+    x = bf16_normal(rng, (7, 128))
+    y = O.quantized_matmul(x, wq, s, b, True, 64, 4, "float32")
+    assert np.array_equal(O.quantized_matmul(2 * x, wq, s, b, True, 64, 4, "float32"), 2 * y)
+    for m in range(7):
+        assert np.array_equal(O.quantized_matmul(x[m:m + 1], wq, s, b, True, 64, 4, "float32"),
+                              y[m:m + 1])
+
+
+def test_gather_qmm_is_per_row_expert_selection():
+    rng = np.random.default_rng(5)
+    E, N, K, T, k = 6, 32, 128, 5, 3
+    w = bf16_normal(rng, (E, N, K), 0.02)
+    wq, s, b = O.quantize(w, 64, 4)
+    x = bf16_normal(rng, (T, 1, 1, K))
+    inds = rng.integers(0, E, (T, k))
+    got = O.gather_qmm(x, wq, s, b, rhs_indices=inds, out_dtype="float32")
+    assert got.shape == (T, k, 1, N)
+    for t in range(T):
+        for j in range(k):
+            e = inds[t, j]
+            ref = x[t, 0].astype(np.float64) @ O.dequantize_numpy_f64(wq[e], s[e], b[e], 64, 4).T
+            assert np.abs(got[t, j] - ref).max() <= np.abs(ref).max() * 1e-6 + 1e-30
+
+
+# --- router --------------------------------------------------------------------
+
+def test_route_known_answer_and_ties():
+    inds, scores = O.route(np.array([[0.0, 1.0, 2.0, 3.0]], np.float32), 2, "float32")
+    assert list(inds[0]) == [3, 2]
+    e = np.exp([3.0, 2.0])
+    assert np.allclose(scores[0], e / e.sum(), rtol=1e-6)
+    inds, _ = O.route(np.zeros((1, 5), np.float32), 3)
+    assert list(inds[0]) == [0, 1, 2]
+
+
+# --- KV8 decode attention ---------------------------------------------------------
+
+def _kv_case(rng, B, H, Hk, L, N, D, g=64):
+    k = bf16_normal(rng, (B, Hk, N, D))
+    v = bf16_normal(rng, (B, Hk, N, D))
+    q = bf16_normal(rng, (B, H, L, D))
+    return q, O.quantize(k, g, 8), O.quantize(v, g, 8)
+
+
+@pytest.mark.parametrize("mask", [None, "causal", "holes"])
+def test_kv8_matches_float64_attention_over_the_dequantized_cache(mask):
+    rng = np.random.default_rng(6)
+    B, H, Hk, L, N, D = 2, 8, 2, 3, 150, 128
+    q, K, V = _kv_case(rng, B, H, Hk, L, N, D)
+    if mask == "holes":
+        m = np.ones((B, 1, L, N), bool)
+        m[..., np.arange(N) % 5 == 2] = False
+        m[1, 0, 0, :] = False                      # a row that sees no key
+        mask = m
+    kd = O.dequantize_numpy_f64(*K, 64, 8)
+    vd = O.dequantize_numpy_f64(*V, 64, 8)
+    scale = D ** -0.5
+    qs = (q * np.float32(scale)).astype(np.float64)  # q pre-scaled in fp32 (kvattn.py:101)
+    ref = O.sdpa_numpy_f64(qs, kd, vd, 1.0, mask)
+    got = O.kv8_decode(q, K, V, scale, mask, 64, 8, "float32")
+    assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+    if isinstance(mask, np.ndarray):
+        assert (got[1, :, 0] == 0).all()          # every key masked -> 0 (kvattn.py:11-12)
+
+
+def test_causal_rows_see_their_own_prefix():
+    """kvattn._mask_rows: row i of an L-row block sees keys <= N - L + i."""
+    m = O.mask_rows("causal", 1, 3, 6)
+    assert m[0].tolist() == [[1, 1, 1, 1, 0, 0], [1, 1, 1, 1, 1, 0], [1, 1, 1, 1, 1, 1]]
+    assert O.mask_rows("causal", 2, 1, 6) is None
+
+
+# --- VQ decode matmul ----------------------------------------------------------------
+
+@pytest.mark.parametrize("code_dtype,kc", [(np.uint8, 256), (np.uint16, 4096)])
+def test_vq_matmul_equals_decode_then_dense(code_dtype, kc):
+    rng = np.random.default_rng(7)
+    OUT, IN, dim = 40, 96, 8
+    cb = O.f16_round(rng.standard_normal((kc, dim)) * 0.02)
+    codes = rng.integers(0, kc, (OUT, IN // dim)).astype(code_dtype)
+    sc = O.f16_round(rng.uniform(0.5, 1.5, OUT))
+    x = bf16_normal(rng, (3, IN))
+    ref = x.astype(np.float64) @ O.vq_decode_numpy(codes, cb, sc).T
+    got = O.vq_matmul(x, codes, cb, sc, out_dtype="float32")
+    assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+    # one decoded element by hand
+    o, i = 3, 17
+    assert np.isclose(O.vq_decode_numpy(codes, cb, sc)[o, i],
+                      sc[o] * cb[codes[o, i // dim], i % dim])
