@@ -23,17 +23,31 @@ def sources():
     return sorted(SRC.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into one shared library; always rebuilds."""
-    tmp = OUT.with_suffix(".so.tmp")
-    cmd = ["hipcc", *FLAGS, *map(str, sources()), "-o", str(tmp)]
+def _run(cmd):
     r = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "packed-fp32-ops"
-    err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)
+    err = "\n".join(l for l in (r.stderr or "").splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
-    if verbose and err.strip():
-        print(err, file=sys.stderr)
+        raise RuntimeError(f"hipcc failed ({r.returncode}): {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build(verbose: bool = False, jobs: int = 8) -> Path:
+    """Compile every HIP source (in parallel, objects under _build/) and link
+    one shared library; always rebuilds."""
+    from concurrent.futures import ThreadPoolExecutor
+    objdir = HERE / "_build"
+    objdir.mkdir(exist_ok=True)
+    cflags = [f for f in FLAGS if f != "-shared"]
+    srcs = sources()
+    objs = [objdir / (p.stem + ".o") for p in srcs]
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        errs = list(ex.map(lambda so: _run(["hipcc", *cflags, "-c", str(so[0]), "-o", str(so[1])]),
+                           zip(srcs, objs)))
+    tmp = OUT.with_suffix(".so.tmp")
+    errs.append(_run(["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC",
+                      *map(str, objs), "-o", str(tmp)]))
+    if verbose and any(e.strip() for e in errs):
+        print("\n".join(e for e in errs if e.strip()), file=sys.stderr)
     os.replace(tmp, OUT)
     return OUT
 

@@ -120,6 +120,14 @@ __device__ __forceinline__ u32x4 nibbles_to_bf16_magic(uint32_t w) {
     return r;
 }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for
+// every outstanding global load of the wave (vmcnt(0)), which would drain a
+// weight stream issued before the barrier; here only LDS traffic
+// (lgkmcnt) is drained, so loads in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // ---- misc ---------------------------------------------------------------------
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
