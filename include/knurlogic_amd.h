@@ -105,6 +105,30 @@ int kmi_gather_qmm(const void* x, int64_t X, int64_t M, int64_t K, const uint32_
 size_t kmi_gather_qmm_workspace_bytes(int64_t P, int64_t M, int64_t E, int64_t K,
                                       int64_t N, int group_size, int bits);
 
+/*
+ * 8-bit-KV decode attention: the reference's kvattn.decode_sdpa
+ * (src/knurlogic/engine/kvattn.py:256-291, kernels :78-183) over the
+ * quantized cache triples that kvquant's caches hold
+ * (src/knurlogic/engine/kvquant.py:60-63):
+ *   q [B, H, L, D] contiguous (q_dtype); out [B, H, L, D] (q_dtype);
+ *   K = (kw u32 [B, Hk, N, D/4], ks, kb [B, Hk, N, D/group]), V likewise,
+ *   each of the six possibly a strided view (slab[..., :N, :]): strides[18]
+ *   holds the element strides (b, h, n) of kw, ks, kb, vw, vs, vb in that
+ *   order; the last axis is contiguous.  scale_dtype: dtype of ks/kb/vs/vb.
+ *   Query head h reads KV head h / (H/Hk); q is pre-multiplied by `scale`.
+ *   mask: [B, L, N] uint8 (1 = visible) or NULL; causal (L > 1): row l sees
+ *   keys n <= N - L + l.  A row that sees no key is 0.
+ * D in {128, 256}; (H/Hk)*L <= 64 (<= 32 at D = 256); 8-bit only.
+ */
+int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
+                   const uint32_t* kw, const void* ks, const void* kb,
+                   const uint32_t* vw, const void* vs, const void* vb,
+                   const int64_t* strides, int scale_dtype, int Hk, int N, int group,
+                   float scale, const uint8_t* mask, int causal, void* out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+size_t kmi_kv8_workspace_bytes(int B, int H, int Hk, int L, int N, int D);
+
 #ifdef __cplusplus
 }
 #endif

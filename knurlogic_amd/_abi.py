@@ -24,6 +24,9 @@ SIGNATURES = {
     "kmi_gather_qmm": (I, [P, I64, I64, I64, P, P, P, I64, I64, P, P, I64, I, I, I, I,
                            P, P, SZ, P]),
     "kmi_gather_qmm_workspace_bytes": (SZ, [I64, I64, I64, I64, I64, I, I]),
+    "kmi_kv8_decode": (I, [P, I, I, I, I, I, P, P, P, P, P, P, P, I, I, I, I,
+                           ctypes.c_float, P, I, P, P, SZ, P]),
+    "kmi_kv8_workspace_bytes": (SZ, [I, I, I, I, I, I]),
 }
 
 ABI_VERSION = 1

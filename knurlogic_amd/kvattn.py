@@ -1,0 +1,206 @@
+"""Decode attention read straight from an 8-bit KV cache, on MI355X.
+
+Mirrors the reference's src/knurlogic/engine/kvattn.py: ``decode_sdpa``
+(:256-291) computes mlx-sdpa semantics over the quantized (packed, scales,
+biases) triples -- q pre-scaled, softmax over the keys a row may see -- with
+one HIP kernel over the packed K/V (kmi_kv8_decode) instead of
+dequantizing the cache; ``supports`` (:213-238) is the routing rule;
+``sdpa`` (:301-320) is the dispatch a model's attention calls, which takes
+the kernel when handed exactly the keys the quantized cache just returned
+and otherwise falls back to dequantize + scaled-dot-product attention (both
+on the GPU); ``STATS`` counts hits and misses (:25-53).
+
+A query row whose every key is masked returns 0 here (the reference
+kernel's rule, :11-12), where a plain softmax would give NaN.
+"""
+from __future__ import annotations
+
+import logging
+import math
+
+import torch
+
+from . import _abi
+from .ops import DTYPE_CODE, _on_gpu, _ptr, _stream, dequantize
+
+logger = logging.getLogger(__name__)
+
+#: {on, hits, misses, last_miss}
+STATS: dict = {"on": True, "hits": 0, "misses": 0, "last_miss": None}
+_LOGGED: set = set()
+
+#: query rows per KV head (GQA ratio x query length) the kernel takes
+MAX_ROWS = 64
+
+
+def reset(on: bool = True) -> None:
+    STATS.update(on=bool(on), hits=0, misses=0, last_miss=None)
+    _LOGGED.clear()
+
+
+def count(hit: bool, why: str = "") -> None:
+    """One decode attention: through the kernel (hit) or not (miss)."""
+    if hit:
+        STATS["hits"] += 1
+    else:
+        STATS["misses"] += 1
+        STATS["last_miss"] = why
+    if hit not in _LOGGED:
+        _LOGGED.add(hit)
+        if hit:
+            logger.info("kv kernel: live -- 8-bit decode reads the packed K/V")
+        else:
+            logger.warning("kv kernel: a decode step fell back to dequantize + sdpa: %s", why)
+
+
+def _dims(q, K, V, bits):
+    B, H, L, D = q.shape
+    Hk = K[0].shape[1]
+    Dk = K[0].shape[3] * 32 // bits
+    Dv = V[0].shape[3] * 32 // bits
+    return B, H, L, D, Hk, Dk, Dv
+
+
+def supports(q, K, V, bits: int, group: int, mask=None, sinks=None) -> bool:
+    """Whether ``decode_sdpa`` takes these shapes (else the caller falls
+    back to dequantize + sdpa).  The rule of kvattn.supports, narrowed to
+    the head dims this build's kernel covers (128 and 256)."""
+    if bits != 8 or sinks is not None or q.dim() != 4:
+        return False
+    B, H, L, D, Hk, Dk, Dv = _dims(q, K, V, bits)
+    if Dk != D or Dv != D or D not in (128, 256) or H % Hk:
+        return False
+    if group % (D // 32) or D % group or group < 16 or K[0].shape[0] != B:
+        return False
+    for w, sc, bi in (K, V):
+        if sc.shape != bi.shape or tuple(sc.shape[:3]) != tuple(w.shape[:3]):
+            return False
+        if w.stride(-1) != 1 or sc.stride(-1) != 1 or bi.stride(-1) != 1:
+            return False
+        if sc.dtype != K[1].dtype or bi.dtype != K[1].dtype:
+            return False
+    R = (H // Hk) * L
+    if R > MAX_ROWS or (D == 256 and R > 32):
+        return False
+    if q.dtype not in DTYPE_CODE or K[1].dtype not in DTYPE_CODE:
+        return False
+    if mask is None or isinstance(mask, str):
+        return mask in (None, "causal")
+    if mask.dtype != torch.bool or mask.dim() > 4:
+        return False
+    if mask.dim() == 4 and mask.shape[1] != 1:
+        return False
+    return mask.shape[-1] == K[0].shape[2] and mask.shape[-2] in (1, L)
+
+
+def _mask_rows(mask, B, L, N, device):
+    """kvattn._mask_rows: (B, L, N) uint8, or None when every key is visible
+    or the causal rule is applied in the kernel."""
+    if mask is None or isinstance(mask, str):
+        return None
+    m = mask
+    if m.dim() == 4:
+        m = m[:, 0]
+    while m.dim() < 3:
+        m = m[None]
+    return m.expand(B, L, N).to(device=device, dtype=torch.uint8).contiguous()
+
+
+def decode_sdpa(q, K, V, scale: float, mask=None, group: int = 64, bits: int = 8,
+                same_layout: bool = False):
+    """Attention of q (B, H, L, D) over K, V -- each the quantized triple
+    (packed uint32, scales, biases) of shape (B, Hk, N, *), possibly strided
+    views -- with mlx sdpa's semantics.  Returns (B, H, L, D) in q's dtype.
+    ``same_layout`` is accepted for signature parity: biases are always
+    read at their own strides."""
+    if bits != 8:
+        raise ValueError("decode_sdpa: 8-bit K/V only")
+    _on_gpu(q, *K, *V)
+    if not supports(q, K, V, bits, group, mask):
+        raise ValueError(f"decode_sdpa: unsupported shapes q {tuple(q.shape)}, "
+                         f"K {tuple(K[0].shape)}, mask {getattr(mask, 'shape', mask)}")
+    B, H, L, D, Hk, _, _ = _dims(q, K, V, bits)
+    N = K[0].shape[2]
+    q = q.contiguous()
+    out = torch.empty_like(q)
+    m = _mask_rows(mask, B, L, N, q.device)
+    causal = 1 if (isinstance(mask, str) and mask == "causal" and L > 1) else 0
+    strides = []
+    for t in (*K, *V):
+        strides += [t.stride(0), t.stride(1), t.stride(2)]
+    st = torch.tensor(strides, dtype=torch.int64)      # host array, read by the launcher
+    L_ = _abi.load()
+    nbytes = L_.kmi_kv8_workspace_bytes(B, H, Hk, L, N, D)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=q.device)
+    _abi.check(L_.kmi_kv8_decode(
+        _ptr(q), DTYPE_CODE[q.dtype], B, H, L, D,
+        _ptr(K[0]), _ptr(K[1]), _ptr(K[2]), _ptr(V[0]), _ptr(V[1]), _ptr(V[2]),
+        st.data_ptr(), DTYPE_CODE[K[1].dtype], Hk, N, group, float(scale),
+        _ptr(m), causal, _ptr(out), _ptr(ws), nbytes, _stream(q)), "kv8_decode")
+    return out
+
+
+def dequant_sdpa(q, K, V, scale: float, mask=None, group: int = 64, bits: int = 8):
+    """The fallback the reference takes off the kernel: dequantize the cache
+    (on the GPU) and run scaled-dot-product attention in float32, rows that
+    see no key returning 0."""
+    kd = dequantize(*K, group_size=group, bits=bits, dtype=torch.float32)
+    vd = dequantize(*V, group_size=group, bits=bits, dtype=torch.float32)
+    B, H, L, D = q.shape
+    Hk, N = kd.shape[1], kd.shape[2]
+    rep = H // Hk
+    qf = q.float() * scale
+    kd = kd.repeat_interleave(rep, dim=1)
+    vd = vd.repeat_interleave(rep, dim=1)
+    s = qf @ kd.transpose(-1, -2)
+    if isinstance(mask, str):
+        if L > 1:
+            rows = torch.arange(N - L, N, device=q.device)[:, None]
+            s = s.masked_fill(~(rows >= torch.arange(N, device=q.device)[None]), -math.inf)
+    elif mask is not None:
+        mm = mask if mask.dim() == 4 else mask.reshape((1,) * (4 - mask.dim()) + tuple(mask.shape))
+        s = s.masked_fill(~mm.to(torch.bool), -math.inf)
+    mx = s.amax(dim=-1, keepdim=True)
+    ok = torch.isfinite(mx)
+    p = torch.where(ok, torch.exp(s - torch.where(ok, mx, torch.zeros_like(mx))), torch.zeros_like(s))
+    den = p.sum(-1, keepdim=True)
+    o = (p @ vd) / torch.where(den > 0, den, torch.ones_like(den))
+    return o.to(q.dtype)
+
+
+def sdpa(queries, keys, values, cache, scale, mask, sinks=None):
+    """The dispatch a model's attention calls (kvattn.sdpa): the 8-bit
+    kernel when ``cache`` just handed back exactly these keys for a short
+    query (its ``kv8_fetch``), else dequantize + sdpa over ``keys``/
+    ``values`` as given (dense tensors, or the quantized triples)."""
+    hit = getattr(cache, "kv8_fetch", None)
+    if hit is not None:
+        cache.kv8_fetch = None
+        kret, K, V, g = hit
+        if kret is not keys:
+            count(False, "keys changed between the cache and the attention")
+        elif not supports(queries, K, V, 8, g, mask, sinks):
+            count(False, f"unsupported: q {tuple(queries.shape)}, mask "
+                         f"{getattr(mask, 'shape', mask)}, sinks {sinks is not None}")
+        else:
+            count(True)
+            return decode_sdpa(queries, K, V, scale, mask, g, 8, same_layout=True)
+    if sinks is not None:
+        raise ValueError("sdpa: attention sinks are not implemented")
+    return _dense_sdpa(queries, keys, values, scale, mask)
+
+
+def _dense_sdpa(q, k, v, scale, mask):
+    B, H, L, D = q.shape
+    rep = H // k.shape[1]
+    kf = k.float().repeat_interleave(rep, dim=1)
+    vf = v.float().repeat_interleave(rep, dim=1)
+    s = (q.float() * scale) @ kf.transpose(-1, -2)
+    N = kf.shape[2]
+    if isinstance(mask, str):
+        if L > 1:
+            rows = torch.arange(N - L, N, device=q.device)[:, None]
+            s = s.masked_fill(~(rows >= torch.arange(N, device=q.device)[None]), -math.inf)
+    elif mask is not None:
+        s = s.masked_fill(~mask.to(torch.bool), -math.inf) if mask.dtype == torch.bool else s + mask
+    return torch.softmax(s, dim=-1).nan_to_num(0.0).matmul(vf).to(q.dtype)

@@ -264,16 +264,28 @@ void orc_kv8_decode(const float* q, int64_t B, int64_t H, int64_t L, int64_t D,
 #else
     (void)nthreads;
 #endif
-#pragma omp parallel
-    {
-        double* sc = (double*)malloc(sizeof(double) * (size_t)(N > 0 ? N : 1));
-        double* qs = (double*)malloc(sizeof(double) * (size_t)D);
-        double* o = (double*)malloc(sizeof(double) * (size_t)D);
-#pragma omp for schedule(static) collapse(3)
-        for (int64_t b = 0; b < B; b++)
-            for (int64_t h = 0; h < H; h++)
+    /* one (batch, KV head) per task: its K/V dequantized once, exactly */
+#pragma omp parallel for schedule(dynamic, 1) collapse(2)
+    for (int64_t b = 0; b < B; b++)
+        for (int64_t hk = 0; hk < Hk; hk++) {
+            double* kd = (double*)malloc(sizeof(double) * (size_t)(N * D + 1));
+            double* vd = (double*)malloc(sizeof(double) * (size_t)(N * D + 1));
+            double* sc = (double*)malloc(sizeof(double) * (size_t)(N + 1));
+            double* qs = (double*)malloc(sizeof(double) * (size_t)D);
+            double* o = (double*)malloc(sizeof(double) * (size_t)D);
+            for (int64_t n = 0; n < N; n++) {
+                const int64_t row = (b * Hk + hk) * N + n;
+                for (int64_t d = 0; d < D; d++) {
+                    kd[n * D + d] = (double)ks[row * gpr + d / group] *
+                                        (double)unpack_q(kw + row * wpr, d, bits) +
+                                    (double)kb[row * gpr + d / group];
+                    vd[n * D + d] = (double)vs[row * gpr + d / group] *
+                                        (double)unpack_q(vw + row * wpr, d, bits) +
+                                    (double)vb[row * gpr + d / group];
+                }
+            }
+            for (int64_t h = hk * rep; h < (hk + 1) * rep; h++)
                 for (int64_t l = 0; l < L; l++) {
-                    int64_t hk = h / rep;
                     const float* qr = q + ((b * H + h) * L + l) * D;
                     for (int64_t d = 0; d < D; d++) qs[d] = (double)(qr[d] * scale);
                     double mx = -INFINITY;
@@ -283,14 +295,9 @@ void orc_kv8_decode(const float* q, int64_t B, int64_t H, int64_t L, int64_t D,
                             sc[n] = -INFINITY;
                             continue;
                         }
-                        int64_t row = (b * Hk + hk) * N + n;
                         double s = 0.0;
-                        for (int64_t d = 0; d < D; d++) {
-                            double kv = (double)ks[row * gpr + d / group] *
-                                            (double)unpack_q(kw + row * wpr, d, bits) +
-                                        (double)kb[row * gpr + d / group];
-                            s += qs[d] * kv;
-                        }
+                        const double* kr = kd + n * D;
+                        for (int64_t d = 0; d < D; d++) s += qs[d] * kr[d];
                         sc[n] = s;
                         any = 1;
                         if (s > mx) mx = s;
@@ -304,22 +311,19 @@ void orc_kv8_decode(const float* q, int64_t B, int64_t H, int64_t L, int64_t D,
                     for (int64_t d = 0; d < D; d++) o[d] = 0.0;
                     for (int64_t n = 0; n < N; n++) {
                         if (sc[n] == -INFINITY) continue;
-                        double p = exp(sc[n] - mx);
+                        const double p = exp(sc[n] - mx);
                         den += p;
-                        int64_t row = (b * Hk + hk) * N + n;
-                        for (int64_t d = 0; d < D; d++) {
-                            double vv = (double)vs[row * gpr + d / group] *
-                                            (double)unpack_q(vw + row * wpr, d, bits) +
-                                        (double)vb[row * gpr + d / group];
-                            o[d] += p * vv;
-                        }
+                        const double* vr = vd + n * D;
+                        for (int64_t d = 0; d < D; d++) o[d] += p * vr[d];
                     }
                     for (int64_t d = 0; d < D; d++) orow[d] = (float)(o[d] / den);
                 }
-        free(sc);
-        free(qs);
-        free(o);
-    }
+            free(kd);
+            free(vd);
+            free(sc);
+            free(qs);
+            free(o);
+        }
 }
 
 /*
