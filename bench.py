@@ -110,6 +110,51 @@ def bench_dense(bits, M, N, K, cold, calls, dev):
             "bound": bound, "bytes": nbytes, "flops": flops}
 
 
+def kv8_bytes(B, H, Hk, L, N, D, gs=64):
+    kv = B * Hk * N * 2 * (D + (D // gs) * 2 * 2)       # K and V: bytes + bf16 scale/bias
+    return kv + 2 * 2 * B * H * L * D                    # q in, out
+
+
+def bench_kv8(B, H, Hk, L, N, D, cold, calls, dev):
+    """8-bit-KV decode attention over quantized K/V caches of N keys, causal
+    inside the L-token block; cold = K/V sets rotated past 1 GB."""
+    import torch
+    import knurlogic_amd as KA
+    from knurlogic_amd import kvattn
+    g = torch.Generator(device=dev).manual_seed(N + L)
+    per = kv8_bytes(B, H, Hk, 0, N, D)
+    n = max(4, math.ceil(ROTATE_BYTES / per)) if cold else 1
+    sets = []
+    for _ in range(n):
+        trip = []
+        for _kv in range(2):
+            t = torch.randn(B * Hk * N, D, device=dev, generator=g).to(torch.bfloat16)
+            wq, s, b = KA.quantize(t, group_size=64, bits=8)
+            del t
+            trip.append((wq.view(B, Hk, N, -1), s.view(B, Hk, N, -1), b.view(B, Hk, N, -1)))
+        sets.append(tuple(trip))
+    q = torch.randn(B, H, L, D, device=dev, generator=g).to(torch.bfloat16)
+    mask = "causal" if L > 1 else None
+    scale = D ** -0.5
+
+    def run():
+        for i in range(calls):
+            K, V = sets[i % n]
+            kvattn.decode_sdpa(q, K, V, scale, mask, 64, 8)
+
+    us = time_graph(run) / calls * 1e3
+    nbytes = kv8_bytes(B, H, Hk, L, N, D)
+    flops = 4.0 * B * H * L * N * D
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del sets
+    torch.cuda.empty_cache()
+    return {"op": "kv8_decode", "B": B, "H": H, "Hk": Hk, "L": L, "N": N, "D": D,
+            "cache": "cold" if cold else "warm", "us": round(us, 3),
+            "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2), "bound": "hbm",
+            "bytes": nbytes, "flops": flops}
+
+
 def cpu_baseline(seconds=10.0):
     """The oracle's quantized_matmul (C, OpenMP) on this host's cores, 4-bit
     M=1 [14336, 4096]: calls repeated until ~`seconds` of wall time."""
@@ -141,6 +186,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no detail table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="detail sections, comma-separated "
+                                                "(dense, kv8); default all")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the path is not sharded "
@@ -173,7 +220,13 @@ def main():
     gbs = nbytes / (us * 1e-6) / 1e9
 
     detail = []
-    if not args.quick:
+    only = set(args.only.split(",")) if args.only else {"dense", "kv8"}
+    if not args.quick and "kv8" in only:
+        for n_ in (8192, 32768):
+            for l_ in (1, 4):
+                for cold in (True, False):
+                    detail.append(bench_kv8(4, 32, 4, l_, n_, 128, cold, 50, dev))
+    if not args.quick and "dense" in only:
         for b_ in (4, 8):
             for shape in ((14336, 4096), (4096, 14336)):
                 for m in (1, 16, 512):

@@ -118,7 +118,9 @@ size_t kmi_gather_qmm_workspace_bytes(int64_t P, int64_t M, int64_t E, int64_t K
  *   Query head h reads KV head h / (H/Hk); q is pre-multiplied by `scale`.
  *   mask: [B, L, N] uint8 (1 = visible) or NULL; causal (L > 1): row l sees
  *   keys n <= N - L + l.  A row that sees no key is 0.
- * D in {128, 256}; (H/Hk)*L <= 64 (<= 32 at D = 256); 8-bit only.
+ * D in {128, 256}; group divides D and is at least D/4; (H/Hk)*L <= 64
+ * (<= 32 at D = 256); 8-bit only.  `workspace` (kmi_kv8_workspace_bytes)
+ * holds the per-block partials.
  */
 int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
                    const uint32_t* kw, const void* ks, const void* kb,

@@ -128,6 +128,19 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// ---- raw buffer resources --------------------------------------------------------
+// A load at byte offset >= `bytes` returns 0 instead of touching memory, so
+// tails need no branch.  Offsets are 32-bit: callers check that every offset
+// they form stays below 2^31.
+constexpr int RSRC_DWORD3 = 0x00020000;   // raw buffer, gfx9 family
+constexpr int AUX_NT = 2;                 // non-temporal: data read once per call
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+    const int64_t cap = 0x7fffffff;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)(bytes < cap ? bytes : cap),
+                                             RSRC_DWORD3);
+}
+
 // ---- misc ---------------------------------------------------------------------
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

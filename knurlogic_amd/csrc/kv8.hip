@@ -2,23 +2,31 @@
 // semantics (q pre-scaled, softmax over the keys each row may see, a row
 // that sees no key returns 0) read straight from the quantized cache.
 //
-// Work split: one workgroup = (batch b, KV head hk, a block of keys); its 4
-// waves each walk their own quarter of the block in steps of 32 keys,
-// keeping an online-softmax state for all R = (H/Hk)*L query rows of the KV
-// head -- every K/V byte is read from HBM once per call, whatever R is.
-// Per step a wave
-//   - loads 32 keys of K and V (16-byte loads, each 8-lane group covering a
-//     128-byte key row), dequantizes them in fp32 (scale*q + bias, one fp16
-//     rounding) into LDS: K^ as [key][d], V^ transposed as [d][key];
-//   - S^T[key, r] = K^ Q^T on v_mfma_f32_16x16x32_f16 (Q pre-scaled, fp16,
-//     held in registers for the whole call);
-//   - rescales its running sums and accumulates O^T[d, r] += V^T P^T on the
-//     same MFMA (P in fp16).
-// The 4 waves' states merge in LDS (in wave order: deterministic) into one
-// fp32 partial (o, m, l) per workgroup; kv8_combine merges the blocks'
-// partials (log-sum-exp) and writes q's dtype.
+// Work split: one workgroup = (batch b, KV head hk, a block of keys).  Its 4
+// waves take interleaved 32-key steps of the block (wave w: keys
+// 32*(4j + w) ..), each keeping an online-softmax state for all R = (H/Hk)*L
+// query rows of the KV head, so every K/V byte is read from HBM once per
+// call whatever R is.  Per step a wave
+//   - has the step's packed K/V, scales and biases already in registers (the
+//     raw buffer loads for step j+1 are issued before step j's math, and a
+//     key past N reads 0 instead of branching);
+//   - dequantizes K (fp32 scale*q + bias, one fp16 rounding) straight into
+//     v_mfma_f32_16x16x32_f16 A operands: lane (key l16, run jg) owns d in
+//     [jg*D/4, (jg+1)*D/4), so its bytes are contiguous and no LDS is used;
+//     the pre-scaled Q^T operands use the same d order, which leaves the dot
+//     products unchanged;
+//   - S^T[key, r] = K^ Q^T; online softmax per row (fp32, exp);
+//   - dequantizes V into a wave-private V^T tile in LDS ([d][32 keys],
+//     keys stored in the order the P^T operand holds them, so each MFMA A
+//     operand is one 16-byte read) and accumulates O^T[d, r] += V^T P^T.
+// The 4 waves' states merge in LDS (fixed order: deterministic) into one
+// partial per workgroup: o / l in fp16 (a convex combination of dequantized
+// V rows, so it is bounded like V) and (m, l) in fp32.  kv8_combine merges
+// the blocks' partials (log-sum-exp) and writes q's dtype.
 #include "common.hpp"
 #include "../../include/knurlogic_amd.h"
+
+#include <stdlib.h>
 
 namespace kmi {
 
@@ -27,21 +35,20 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 struct Kv8Args {
     const void* q;              // [B, H, L, D] contiguous, dtype qdt
-    const uint32_t* kw; const void* ks; const void* kb;
-    const uint32_t* vw; const void* vs; const void* vb;
-    int64_t st[6][3];           // element strides (b, h, n) of kw, ks, kb, vw, vs, vb
+    const void* base[6];        // kw, ks, kb, vw, vs, vb
+    int64_t st[6][3];           // element strides (b, h, n) of the six
+    int64_t ext[6];             // bytes from a (b, hk) origin through key N-1
     const uint8_t* mask;        // [B, L, N] (1 = key visible) or null
-    float* part;                // [B*Hk][nblk][R][D + 2]
-    int qdt, sdt;               // dtypes of q and of scales/biases
-    int B, H, Hk, L, N, D, group, R, causal, keys_per_wg, nblk;
+    _Float16* po;               // [B*Hk][nblk][R][D]  o / l of each block
+    float2* pml;                // [B*Hk][nblk][R]     (m, l) of each block
+    int qdt;
+    int B, H, Hk, L, N, group, R, causal, keys_per_wg, nblk;
     float scale;
 };
 
-__device__ __forceinline__ float load_any(const void* p, int64_t i, int dt) {
-    if (dt == BF16) return bf16_to_f32(((const uint16_t*)p)[i]);
-    if (dt == F16) return f16_to_f32(((const uint16_t*)p)[i]);
-    return ((const float*)p)[i];
-}
+constexpr int KV_WAVES = 4;
+constexpr int KV_STEP = 32;            // keys per wave step
+constexpr int KV_WG_KEYS = KV_WAVES * KV_STEP;
 
 __device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
     f16x2 v = {(_Float16)lo, (_Float16)hi};
@@ -53,61 +60,161 @@ __device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// Orders this wave's LDS writes before its later LDS reads.
 __device__ __forceinline__ void wave_lds_sync() {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
 }
 
-constexpr int KV_WAVES = 4;
-constexpr int KV_STEP = 32;            // keys per wave step
+template <class ST>
+__device__ __forceinline__ uint32_t load_scale_raw(__amdgpu_buffer_rsrc_t r, uint32_t elem) {
+    if constexpr (sizeof(typename ST::storage) == 4)
+        return __builtin_amdgcn_raw_buffer_load_b32(r, (int)(elem * 4u), 0, 0);
+    else
+        return __builtin_amdgcn_raw_buffer_load_b16(r, (int)(elem * 2u), 0, 0);
+}
 
-template <int D>
-struct KvLds {
-    static constexpr int KSTR = D + 8;          // fp16 per K^ row
-    static constexpr int VSTR = KV_STEP + 8;    // fp16 per V^T row
-    static constexpr int WAVE = KV_STEP * KSTR + D * VSTR;   // fp16 per wave
-};
+template <class ST>
+__device__ __forceinline__ float scale_val(uint32_t raw) {
+    if constexpr (sizeof(typename ST::storage) == 4) return __uint_as_float(raw);
+    else return ST::load((uint16_t)raw);
+}
+
+__device__ __forceinline__ float byte_f(uint32_t w, int e) { return (float)((w >> (8 * e)) & 0xffu); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_add(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
 
 template <int D, int RT>
-__global__ __launch_bounds__(256) void kv8_partial(Kv8Args a) {
-    constexpr int KSTEPS = D / 32;   // QK k-steps over d
-    constexpr int DT = D / 16;       // PV d-tiles
-    constexpr int PIECES = D / 16;   // 16-byte pieces per key row
-    constexpr int LOADS = 8 * PIECES / 64;   // (key quad, piece) items per lane per step
-    using Lds = KvLds<D>;
+struct KvShape {
+    static constexpr int DL = D / 4;             // d per lane run in QK
+    static constexpr int KC = DL / 16;           // 16-byte K chunks per lane and key
+    static constexpr int KSTEPS = D / 32;        // MFMA k-steps over d
+    static constexpr int DT = D / 16;            // PV d tiles
+    static constexpr int VP = D / 16;            // 16-byte pieces per V row
+    static constexpr int VIT = 8 * VP / 64;      // (key quad, piece) items per lane
+    static constexpr int OP = D + 4;             // fp32 per row of a merge slot
+    static constexpr size_t vt_bytes = (size_t)KV_WAVES * D * KV_STEP * 2;
+    static constexpr size_t merge_bytes = (size_t)(2 * KV_WAVES * 64 + 2 * 16 * RT * OP) * 4;
+    static constexpr size_t lds = vt_bytes > merge_bytes ? vt_bytes : merge_bytes;
+};
+
+// Two workgroups per CU where the state fits 256 registers (D = 128, up to
+// 32 rows); otherwise one, so the accumulators may also use AGPRs.
+template <int D, int RT>
+constexpr int kv8_min_blocks() { return (D == 128 && RT <= 2) ? 2 : 1; }
+
+template <int D, int RT, class ST>
+__global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv8Args a) {
+    using S_ = KvShape<D, RT>;
+    constexpr int DL = S_::DL, KC = S_::KC, KSTEPS = S_::KSTEPS, DT = S_::DT;
+    constexpr int VP = S_::VP, VIT = S_::VIT;
+    constexpr int ES = (int)sizeof(typename ST::storage);
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, jg = lane >> 4;
     const int bh = blockIdx.y, blk = blockIdx.x;
     const int b = bh / a.Hk, hk = bh % a.Hk;
     const int rep = a.H / a.Hk;
-    const int per_wave = a.keys_per_wg / KV_WAVES;
-    const int wkey0 = blk * a.keys_per_wg + wave * per_wave;
-    const int steps = per_wave / KV_STEP;
-    const int l16 = lane & 15, jg = lane >> 4;
+    const int R = a.R, N = a.N, L = a.L;
 
-    _Float16* kh = (_Float16*)smem + wave * Lds::WAVE;     // [32][KSTR]
-    _Float16* vt = kh + KV_STEP * Lds::KSTR;               // [D][VSTR]
+    // buffer views of this (b, hk): a key past N reads 0
+    __amdgpu_buffer_rsrc_t rs[6];
+#pragma unroll
+    for (int i = 0; i < 6; i++) {
+        const int es = (i == 0 || i == 3) ? 4 : ES;
+        rs[i] = make_rsrc((const char*)a.base[i] + (b * a.st[i][0] + hk * a.st[i][1]) * es, a.ext[i]);
+    }
+    const uint32_t kst = (uint32_t)a.st[0][2] * 4u, vst = (uint32_t)a.st[3][2] * 4u;
+    const uint32_t kss = (uint32_t)a.st[1][2], kbs = (uint32_t)a.st[2][2];
+    const uint32_t vss = (uint32_t)a.st[4][2], vbs = (uint32_t)a.st[5][2];
+    const uint32_t kgi = (uint32_t)((DL * jg) / a.group);   // K group of this lane's d run
 
-    // ---- Q^T operands (fp16, pre-scaled), lane column r ----------------------
-    u32x4 qop[RT][KSTEPS];
+    const int steps = a.keys_per_wg / KV_WG_KEYS;
+    const int kbase = blk * a.keys_per_wg + wave * KV_STEP;
+
+    // ---- raw step data, in flight one step ahead -------------------------------
+    u32x4 kr[2][KC];
+    uint32_t ksr[2], kbr[2];
+    u32x4 vr[VIT][4];
+    uint32_t vsr[VIT][4], vbr[VIT][4];
+
+    auto issue = [&](int j) {
+        const uint32_t n0 = (uint32_t)(kbase + j * KV_WG_KEYS);
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-        const int r = l16 + 16 * rt;
-        const bool rok = r < a.R;
-        const int h = hk * rep + (rok ? r / a.L : 0), lq = rok ? r % a.L : 0;
-        const int64_t qbase = (((int64_t)b * a.H + h) * a.L + lq) * a.D;
+        for (int nt = 0; nt < 2; nt++) {
+            const uint32_t n = n0 + 16u * nt + l16;
 #pragma unroll
-        for (int k = 0; k < KSTEPS; k++) {
-            const int d0 = 32 * k + 8 * jg;
-            u32x4 v;
+            for (int c = 0; c < KC; c++)
+                kr[nt][c] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rs[0], (int)(n * kst + (uint32_t)(DL * jg + 16 * c)), 0, AUX_NT);
+            ksr[nt] = load_scale_raw<ST>(rs[1], n * kss + kgi);
+            kbr[nt] = load_scale_raw<ST>(rs[2], n * kbs + kgi);
+        }
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float x0 = rok ? load_any(a.q, qbase + d0 + 2 * e, a.qdt) * a.scale : 0.f;
-                const float x1 = rok ? load_any(a.q, qbase + d0 + 2 * e + 1, a.qdt) * a.scale : 0.f;
-                v[e] = pack_f16(x0, x1);
+        for (int it = 0; it < VIT; it++) {
+            const int idx = lane + 64 * it;
+            const int quad = idx / VP, piece = idx % VP;
+            const uint32_t g = (uint32_t)((16 * piece) / a.group);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const uint32_t n = n0 + 4u * quad + kk;
+                vr[it][kk] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rs[3], (int)(n * vst + 16u * piece), 0, AUX_NT);
+                vsr[it][kk] = load_scale_raw<ST>(rs[4], n * vss + g);
+                vbr[it][kk] = load_scale_raw<ST>(rs[5], n * vbs + g);
             }
-            qop[rt][k] = v;
+        }
+    };
+    issue(0);
+
+    // ---- Q^T operands (fp16, pre-scaled): lane column r, d run jg ---------------
+    u32x4 qop[RT][KSTEPS];
+    {
+        const int qes = a.qdt == F32 ? 4 : 2;
+        const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q, (int64_t)a.B * a.H * L * D * qes);
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const int r = l16 + 16 * rt;
+            const bool rok = r < R;
+            const int rr = rok ? r : 0;
+            const int h = hk * rep + rr / L, lq = rr % L;
+            const uint32_t e0 = (uint32_t)((((b * a.H + h) * L + lq) * D) + DL * jg);
+#pragma unroll
+            for (int k = 0; k < KSTEPS; k++) {
+                float x[8];
+                if (a.qdt == F32) {
+                    const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)((e0 + 8 * k) * 4u), 0, 0);
+                    const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)((e0 + 8 * k) * 4u + 16u), 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        x[e] = __uint_as_float(lo[e]);
+                        x[4 + e] = __uint_as_float(hi[e]);
+                    }
+                } else {
+                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)((e0 + 8 * k) * 2u), 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint16_t lo = (uint16_t)(v[e] & 0xffffu), hi = (uint16_t)(v[e] >> 16);
+                        x[2 * e] = a.qdt == BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+                        x[2 * e + 1] = a.qdt == BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+                    }
+                }
+                u32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    o[e] = rok ? pack_f16(x[2 * e] * a.scale, x[2 * e + 1] * a.scale) : 0u;
+                qop[rt][k] = o;
+            }
         }
     }
 
@@ -121,101 +228,109 @@ __global__ __launch_bounds__(256) void kv8_partial(Kv8Args a) {
         for (int dt = 0; dt < DT; dt++) O[dt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    const int64_t kwb = b * a.st[0][0] + hk * a.st[0][1];
-    const int64_t ksb = b * a.st[1][0] + hk * a.st[1][1];
-    const int64_t kbb = b * a.st[2][0] + hk * a.st[2][1];
-    const int64_t vwb = b * a.st[3][0] + hk * a.st[3][1];
-    const int64_t vsb = b * a.st[4][0] + hk * a.st[4][1];
-    const int64_t vbb = b * a.st[5][0] + hk * a.st[5][1];
+    _Float16* vt = (_Float16*)smem + wave * D * KV_STEP;   // [D][32] V^T in P^T key order
+    const bool has_mask = a.mask != nullptr;
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.mask, (int64_t)a.B * L * N);
 
-    for (int s = 0; s < steps; s++) {
-        const int n0 = wkey0 + s * KV_STEP;
-        // ---- load + dequantize 32 keys of K and V into LDS -----------------
+    for (int j = 0; j < steps; j++) {
+        const int n0 = kbase + j * KV_WG_KEYS;
+
+        // ---- K^ -> MFMA A operands: kop[nt][2c + hh] = d run 16c + 8hh of the lane's DL
+        u32x4 kop[2][KSTEPS];
 #pragma unroll
-        for (int it = 0; it < LOADS; it++) {
-            const int idx = lane + 64 * it;
-            const int quad = idx / PIECES, piece = idx % PIECES;
-            const int g = (16 * piece) / a.group;
-            u32x4 kd[4], vd[4];
-            float ksc[4], kbi[4], vsc[4], vbi[4];
+        for (int nt = 0; nt < 2; nt++) {
+            const float s = scale_val<ST>(ksr[nt]), bi = scale_val<ST>(kbr[nt]);
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const int n = n0 + 4 * quad + kk;
-                const bool ok = n < a.N;
-                const int nn = ok ? n : 0;
-                kd[kk] = ok ? *(const u32x4*)(a.kw + kwb + nn * a.st[0][2] + 4 * piece) : u32x4{0u, 0u, 0u, 0u};
-                vd[kk] = ok ? *(const u32x4*)(a.vw + vwb + nn * a.st[3][2] + 4 * piece) : u32x4{0u, 0u, 0u, 0u};
-                ksc[kk] = ok ? load_any(a.ks, ksb + nn * a.st[1][2] + g, a.sdt) : 0.f;
-                kbi[kk] = ok ? load_any(a.kb, kbb + nn * a.st[2][2] + g, a.sdt) : 0.f;
-                vsc[kk] = ok ? load_any(a.vs, vsb + nn * a.st[4][2] + g, a.sdt) : 0.f;
-                vbi[kk] = ok ? load_any(a.vb, vbb + nn * a.st[5][2] + g, a.sdt) : 0.f;
-            }
-            // K^[key][d]: 16 fp16 per key row piece
+            for (int c = 0; c < KC; c++)
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                uint32_t o8[8];
+                for (int hh = 0; hh < 2; hh++) {
+                    u32x4 o;
 #pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    const uint32_t word = kd[kk][w];
-                    const float q0 = (float)(word & 0xffu), q1 = (float)((word >> 8) & 0xffu);
-                    const float q2 = (float)((word >> 16) & 0xffu), q3 = (float)(word >> 24);
-                    o8[2 * w] = pack_f16(__builtin_fmaf(ksc[kk], q0, kbi[kk]), __builtin_fmaf(ksc[kk], q1, kbi[kk]));
-                    o8[2 * w + 1] = pack_f16(__builtin_fmaf(ksc[kk], q2, kbi[kk]), __builtin_fmaf(ksc[kk], q3, kbi[kk]));
+                    for (int w2 = 0; w2 < 2; w2++) {
+                        const uint32_t wd = kr[nt][c][2 * hh + w2];
+                        o[2 * w2] = pack_f16(__builtin_fmaf(s, byte_f(wd, 0), bi), __builtin_fmaf(s, byte_f(wd, 1), bi));
+                        o[2 * w2 + 1] = pack_f16(__builtin_fmaf(s, byte_f(wd, 2), bi), __builtin_fmaf(s, byte_f(wd, 3), bi));
+                    }
+                    kop[nt][2 * c + hh] = o;
                 }
-                _Float16* dst = kh + (4 * quad + kk) * Lds::KSTR + 16 * piece;
-                *(u32x4*)dst = u32x4{o8[0], o8[1], o8[2], o8[3]};
-                *(u32x4*)(dst + 8) = u32x4{o8[4], o8[5], o8[6], o8[7]};
-            }
-            // V^T[d][key]: 4 keys of one d per 8-byte write
+        }
+        // ---- V^ -> V^T tile: quad q (keys 4q..4q+3) sits at fp16 offset 8(q&3) + 4(q>>2)
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
+        for (int it = 0; it < VIT; it++) {
+            const int idx = lane + 64 * it;
+            const int quad = idx / VP, piece = idx % VP;
+            const int slot = 8 * (quad & 3) + 4 * (quad >> 2);
+            float s[4], bi[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                s[kk] = scale_val<ST>(vsr[it][kk]);
+                bi[kk] = scale_val<ST>(vbr[it][kk]);
+            }
+#pragma unroll
+            for (int w = 0; w < 4; w++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     float f[4];
 #pragma unroll
-                    for (int kk = 0; kk < 4; kk++)
-                        f[kk] = __builtin_fmaf(vsc[kk], (float)((vd[kk][w] >> (8 * e)) & 0xffu), vbi[kk]);
+                    for (int kk = 0; kk < 4; kk++) f[kk] = __builtin_fmaf(s[kk], byte_f(vr[it][kk][w], e), bi[kk]);
                     const int d = 16 * piece + 4 * w + e;
-                    *(u32x2*)(vt + d * Lds::VSTR + 4 * quad) = u32x2{pack_f16(f[0], f[1]), pack_f16(f[2], f[3])};
+                    *(u32x2*)(vt + d * KV_STEP + slot) = u32x2{pack_f16(f[0], f[1]), pack_f16(f[2], f[3])};
                 }
-            }
-        }
-        wave_lds_sync();
-
-        // ---- S^T = K^ Q^T ------------------------------------------------------
-        f32x4 S[2][RT];
-#pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-#pragma unroll
-            for (int rt = 0; rt < RT; rt++) S[nt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int k = 0; k < KSTEPS; k++) {
-                const u32x4 A = *(const u32x4*)(kh + (16 * nt + l16) * Lds::KSTR + 32 * k + 8 * jg);
-#pragma unroll
-                for (int rt = 0; rt < RT; rt++) S[nt][rt] = mfma_f16(A, qop[rt][k], S[nt][rt]);
-            }
         }
 
-        // ---- online softmax over this step's keys, per row r -----------------
-        u32x4 P[RT];
+        // ---- which of this lane's 8 keys each row sees (mask bytes loaded before
+        // the prefetch, so waiting on them does not wait on the next step)
+        uint32_t mbits[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
             const int r = l16 + 16 * rt;
-            const int lq = r % a.L;
+            const int lq = (r < R ? r : 0) % L;
+            uint32_t bits = 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int n = n0 + 16 * (e >> 2) + 4 * jg + (e & 3);
+                bool ok = n < N && r < R;
+                if (a.causal) ok = ok && n <= N - L + lq;
+                bits |= (ok ? 1u : 0u) << e;
+            }
+            if (has_mask) {
+                const uint32_t row = (uint32_t)((b * L + lq) * N);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint32_t n = (uint32_t)(n0 + 16 * (e >> 2) + 4 * jg + (e & 3));
+                    const uint32_t mv = __builtin_amdgcn_raw_buffer_load_b8(rm, (int)(row + n), 0, 0);
+                    bits &= mv != 0 ? ~0u : ~(1u << e);
+                }
+            }
+            mbits[rt] = bits;
+        }
+        if (j + 1 < steps) issue(j + 1);   // next step's bytes stream in during this step's math
+        wave_lds_sync();
+
+        // ---- S^T = K^ Q^T --------------------------------------------------------
+        f32x4 S[2][RT];
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int k = 0; k < KSTEPS; k++) acc = mfma_f16(kop[nt][k], qop[rt][k], acc);
+                S[nt][rt] = acc;
+            }
+
+        // ---- online softmax over this step's keys, per row --------------------------
+        u32x4 P[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
             float sv[8];
             float bm = -INFINITY;
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int n = n0 + 16 * nt + 4 * jg + i;
-                    bool ok = n < a.N && r < a.R;
-                    if (a.causal) ok = ok && n <= a.N - a.L + lq;
-                    if (a.mask) ok = ok && a.mask[((int64_t)b * a.L + lq) * a.N + (ok ? n : 0)] != 0;
-                    const float v = ok ? S[nt][rt][i] : -INFINITY;
-                    sv[4 * nt + i] = v;
-                    bm = fmaxf(bm, v);
-                }
+            for (int e = 0; e < 8; e++) {
+                const float v = ((mbits[rt] >> e) & 1u) ? S[e >> 2][rt][e & 3] : -INFINITY;
+                sv[e] = v;
+                bm = fmaxf(bm, v);
+            }
             bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
             bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
             const float mn = fmaxf(m[rt], bm);
@@ -241,106 +356,160 @@ __global__ __launch_bounds__(256) void kv8_partial(Kv8Args a) {
             P[rt] = u32x4{pack_f16(p[0], p[1]), pack_f16(p[2], p[3]), pack_f16(p[4], p[5]), pack_f16(p[6], p[7])};
         }
 
-        // ---- O^T += V^T P^T  (key order: lane group j holds keys 4j..4j+3 and 16+4j..16+4j+3)
+        // ---- O^T += V^T P^T: lane (d row l16, run jg) reads the 8 keys P^T holds
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
-            const _Float16* row = vt + (16 * dt + l16) * Lds::VSTR;
-            const u32x2 lo = *(const u32x2*)(row + 4 * jg);
-            const u32x2 hi = *(const u32x2*)(row + 16 + 4 * jg);
-            const u32x4 A = u32x4{lo.x, lo.y, hi.x, hi.y};
+            const u32x4 A = *(const u32x4*)(vt + (16 * dt + l16) * KV_STEP + 8 * jg);
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) O[dt][rt] = mfma_f16(A, P[rt], O[dt][rt]);
         }
-        wave_lds_sync();   // the next step overwrites K^ / V^T
     }
 
-    // ---- merge the 4 waves (wave order), write this block's partial -------------
-    __syncthreads();
-    float* fs = (float*)smem;                       // reuses the K^/V^T area
-    float* mw = fs;                                 // [4][R]
-    float* lw = mw + KV_WAVES * 64;                 // [4][R]
-    float* osum = lw + KV_WAVES * 64;               // [R][D]
+    // ---- merge the 4 waves in a fixed order: (2 -> 0, 3 -> 1), then 1 -> 0 ------
+    __syncthreads();                                   // V^T tiles are dead; reuse the LDS
+    constexpr int OP = S_::OP, SLOT = 16 * RT * OP;
+    float* mw = (float*)smem;                          // [4][64]
+    float* lw = mw + KV_WAVES * 64;                    // [4][64]
+    float* slot = lw + KV_WAVES * 64;                  // [2][16*RT][OP]
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
-        const int r = l16 + 16 * rt;
-        if (jg == 0 && r < a.R) {
-            mw[wave * 64 + r] = m[rt];
-            lw[wave * 64 + r] = lsum[rt];
+        if (jg == 0) {
+            mw[wave * 64 + l16 + 16 * rt] = m[rt];
+            lw[wave * 64 + l16 + 16 * rt] = lsum[rt];
         }
     }
     __syncthreads();
-    float f[RT];
+    float Mr[RT], Lr[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         const int r = l16 + 16 * rt;
         float M = -INFINITY;
-        if (r < a.R)
-            for (int w = 0; w < KV_WAVES; w++) M = fmaxf(M, mw[w * 64 + r]);
-        f[rt] = (M == -INFINITY || m[rt] == -INFINITY) ? 0.f : __expf(m[rt] - M);
-    }
-    for (int w = 0; w < KV_WAVES; w++) {
-        if (wave == w) {
 #pragma unroll
-            for (int rt = 0; rt < RT; rt++) {
-                const int r = l16 + 16 * rt;
-                if (r >= a.R) continue;
-#pragma unroll
-                for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int d = 16 * dt + 4 * jg + i;
-                        const float v = O[dt][rt][i] * f[rt];
-                        osum[r * D + d] = (w == 0) ? v : osum[r * D + d] + v;
-                    }
-            }
-        }
-        __syncthreads();
-    }
-    float* out = a.part + ((int64_t)bh * a.nblk + blk) * a.R * (D + 2);
-    for (int i = tid; i < a.R * D; i += blockDim.x) out[(i / D) * (D + 2) + (i % D)] = osum[i];
-    for (int r = tid; r < a.R; r += blockDim.x) {
-        float M = -INFINITY;
         for (int w = 0; w < KV_WAVES; w++) M = fmaxf(M, mw[w * 64 + r]);
-        float L = 0.f;
-        if (M != -INFINITY)
+        float Ls = 0.f;
+        if (M != -INFINITY) {
+#pragma unroll
             for (int w = 0; w < KV_WAVES; w++) {
-                const float mwv = mw[w * 64 + r];
-                if (mwv != -INFINITY) L += lw[w * 64 + r] * __expf(mwv - M);
+                const float mv = mw[w * 64 + r];
+                if (mv != -INFINITY) Ls += lw[w * 64 + r] * __expf(mv - M);
             }
-        out[r * (D + 2) + D] = M;
-        out[r * (D + 2) + D + 1] = L;
+        }
+        Mr[rt] = M;
+        Lr[rt] = Ls;
+        const float f = m[rt] == -INFINITY ? 0.f : __expf(m[rt] - M);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) O[dt][rt] *= f;
+    }
+    if (wave >= 2) {
+        float* sl = slot + (wave - 2) * SLOT;
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+                *(f32x4*)(sl + (l16 + 16 * rt) * OP + 16 * dt + 4 * jg) = O[dt][rt];
+    }
+    __syncthreads();
+    if (wave < 2) {
+        float* sl = slot + wave * SLOT;
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                f32x4* p = (f32x4*)(sl + (l16 + 16 * rt) * OP + 16 * dt + 4 * jg);
+                O[dt][rt] += *p;
+                if (wave == 1) *p = O[dt][rt];   // same wave, same address: in order
+            }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const float* sl = slot + SLOT;
+        const int64_t pb = ((int64_t)bh * a.nblk + blk) * R;
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const int r = l16 + 16 * rt;
+            if (r >= R) continue;
+            const float inv = Lr[rt] > 0.f ? 1.f / Lr[rt] : 0.f;
+            _Float16* orow = a.po + (pb + r) * D;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                const f32x4 v = (O[dt][rt] + *(const f32x4*)(sl + r * OP + 16 * dt + 4 * jg)) * inv;
+                *(u32x2*)(orow + 16 * dt + 4 * jg) = u32x2{pack_f16(v[0], v[1]), pack_f16(v[2], v[3])};
+            }
+            if (jg == 0) a.pml[pb + r] = make_float2(Mr[rt], Lr[rt]);
+        }
     }
 }
 
-// out[b, h, l, d] = sum_blk w_blk o_blk[d] / sum_blk w_blk l_blk, w = exp(m_blk - max m);
-// 0 when no block saw a key (the reference kernel's rule).
-__global__ void kv8_combine(const float* __restrict__ part, int nblk, int R, int D, int H, int Hk,
-                            int L, int qdt, void* __restrict__ out) {
-    const int row = blockIdx.x;            // (b*Hk + hk) * R + r
+// out[b, h, l, :] = sum_blk w_blk o_blk / sum_blk w_blk, w_blk = l_blk exp(m_blk - max m),
+// with o_blk stored as o / l; 0 when no block saw a key (the reference kernel's rule).
+// One wave per (b, hk, row r); blocks merged 32 at a time with online rescaling,
+// each chunk's loads issued together.
+template <int D>
+__global__ __launch_bounds__(64) void kv8_combine(const _Float16* __restrict__ po,
+                                                  const float2* __restrict__ pml, int nblk, int R,
+                                                  int H, int Hk, int L, int qdt, void* __restrict__ out,
+                                                  int64_t po_bytes, int64_t pml_bytes) {
+    constexpr int PER = D / 64;          // d per lane (2 or 4)
+    constexpr int CH = 32;               // blocks per chunk
+    const int row = blockIdx.x;          // (b*Hk + hk) * R + r
     const int bh = row / R, r = row % R;
-    const int b = bh / Hk, hk = bh % Hk;
-    const int rep = H / Hk;
-    const int h = hk * rep + r / L, lq = r % L;
-    const float* p = part + ((int64_t)bh * nblk) * R * (D + 2) + (int64_t)r * (D + 2);
-    const int64_t bstride = (int64_t)R * (D + 2);
-    float M = -INFINITY;
-    for (int i = 0; i < nblk; i++) M = fmaxf(M, p[i * bstride + D]);
-    const int64_t oi = (((int64_t)b * H + h) * L + lq) * D;
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float num = 0.f, den = 0.f;
-        if (M != -INFINITY) {
-            for (int i = 0; i < nblk; i++) {
-                const float mi = p[i * bstride + D];
-                if (mi == -INFINITY) continue;
-                const float w = __expf(mi - M);
-                den += w * p[i * bstride + D + 1];
-                num += w * p[i * bstride + d];
+    const int lane = threadIdx.x;
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(po, po_bytes);
+    const __amdgpu_buffer_rsrc_t rml = make_rsrc(pml, pml_bytes);
+
+    float M = -INFINITY, den = 0.f, num[PER];
+#pragma unroll
+    for (int e = 0; e < PER; e++) num[e] = 0.f;
+    for (int i0 = 0; i0 < nblk; i0 += CH) {
+        uint32_t ov[CH][PER / 2];
+#pragma unroll
+        for (int t = 0; t < CH; t++) {
+            const uint32_t off = (uint32_t)((((int64_t)bh * nblk + i0 + t) * R + r) * D + lane * PER) * 2u;
+            if constexpr (PER == 2) {
+                ov[t][0] = __builtin_amdgcn_raw_buffer_load_b32(rp, (int)off, 0, 0);
+            } else {
+                const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rp, (int)off, 0, 0);
+                ov[t][0] = v.x;
+                ov[t][1] = v.y;
             }
         }
-        const float v = den > 0.f ? num / den : 0.f;
-        if (qdt == BF16) ((uint16_t*)out)[oi + d] = f32_to_bf16(v);
-        else if (qdt == F16) ((uint16_t*)out)[oi + d] = f32_to_f16(v);
-        else ((float*)out)[oi + d] = v;
+        const int i = i0 + lane;
+        const bool valid = lane < CH && i < nblk;
+        const u32x2 mlr = __builtin_amdgcn_raw_buffer_load_b64(
+            rml, (int)((uint32_t)(((int64_t)bh * nblk + (valid ? i : 0)) * R + r) * 8u), 0, 0);
+        const float mi = valid ? __uint_as_float(mlr.x) : -INFINITY;
+        const float li = valid ? __uint_as_float(mlr.y) : 0.f;
+        const float Mn = fmaxf(M, wave_max(mi));
+        if (Mn == -INFINITY) continue;               // nothing visible yet
+        const float alpha = M == -INFINITY ? 0.f : __expf(M - Mn);
+        den *= alpha;
+#pragma unroll
+        for (int e = 0; e < PER; e++) num[e] *= alpha;
+        const float w = mi == -INFINITY ? 0.f : li * __expf(mi - Mn);
+        den += w;
+#pragma unroll
+        for (int t = 0; t < CH; t++) {
+            const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), t));
+#pragma unroll
+            for (int e = 0; e < PER / 2; e++) {
+                const f16x2 hv = __builtin_bit_cast(f16x2, ov[t][e]);
+                num[2 * e] += c * (float)hv[0];
+                num[2 * e + 1] += c * (float)hv[1];
+            }
+        }
+        M = Mn;
+    }
+    den = wave_add(den);
+    const int b = bh / Hk, hk = bh % Hk;
+    const int h = hk * (H / Hk) + r / L, lq = r % L;
+    const int64_t oi = (((int64_t)b * H + h) * L + lq) * D + lane * PER;
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+        const float v = num[e] * inv;
+        if (qdt == BF16) ((uint16_t*)out)[oi + e] = f32_to_bf16(v);
+        else if (qdt == F16) ((uint16_t*)out)[oi + e] = f32_to_f16(v);
+        else ((float*)out)[oi + e] = v;
     }
 }
 
@@ -351,24 +520,59 @@ __global__ void fill_zero_u32(uint32_t* __restrict__ p, int64_t n) {
 
 struct Kv8Plan {
     int keys_per_wg, nblk, rt;
-    size_t lds;
+    size_t po_bytes, pml_off, pml_bytes, total;
 };
+
+// Workgroups per call the key blocks aim at (KMI_KV8_WGS overrides; read once).
+static int kv8_target_wgs() {
+    static int v = [] {
+        const char* e = getenv("KMI_KV8_WGS");
+        const int x = e ? atoi(e) : 0;
+        return x > 0 ? x : 512;
+    }();
+    return v;
+}
 
 static Kv8Plan plan_kv8(int B, int Hk, int N, int D, int R) {
     Kv8Plan p;
     p.rt = (R + 15) / 16;
-    // keys per workgroup: 4 waves x whole steps, ~1024 workgroups overall
     const int64_t pairs = (int64_t)B * Hk;
-    int64_t want_blk = ceil_div(1024, pairs);
-    int64_t kpw = ceil_div(N, want_blk);
-    kpw = ceil_div(kpw, KV_WAVES * KV_STEP) * KV_WAVES * KV_STEP;
-    if (kpw < KV_WAVES * KV_STEP) kpw = KV_WAVES * KV_STEP;
+    const int64_t want_blk = ceil_div(kv8_target_wgs(), pairs);
+    int64_t kpw = ceil_div(N > 0 ? N : 1, want_blk);
+    kpw = ceil_div(kpw, KV_WG_KEYS) * KV_WG_KEYS;
     p.keys_per_wg = (int)kpw;
-    p.nblk = (int)ceil_div(N, kpw);
-    const size_t waves = (size_t)KV_WAVES * (KV_STEP * (D + 8) + D * (KV_STEP + 8)) * 2;
-    const size_t merge = (size_t)(2 * KV_WAVES * 64 + R * D) * 4;
-    p.lds = waves > merge ? waves : merge;
+    p.nblk = (int)ceil_div(N > 0 ? N : 1, kpw);
+    const size_t rows = (size_t)pairs * p.nblk * R;
+    p.po_bytes = rows * D * 2;
+    p.pml_off = (p.po_bytes + 255) & ~(size_t)255;
+    p.pml_bytes = rows * sizeof(float2);
+    p.total = p.pml_off + p.pml_bytes;
     return p;
+}
+
+template <int D, int RT, class ST>
+static void launch_partial(const Kv8Args& a, dim3 grid, hipStream_t st) {
+    constexpr size_t lds = KvShape<D, RT>::lds;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute((const void*)kv8_partial<D, RT, ST>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        attr_set = true;
+    }
+    kv8_partial<D, RT, ST><<<grid, 256, lds, st>>>(a);
+}
+
+template <class ST>
+static void launch_partial_st(const Kv8Args& a, int D, int rt, dim3 grid, hipStream_t st) {
+    if (D == 128) {
+        if (rt == 1) launch_partial<128, 1, ST>(a, grid, st);
+        else if (rt == 2) launch_partial<128, 2, ST>(a, grid, st);
+        else if (rt == 3) launch_partial<128, 3, ST>(a, grid, st);
+        else launch_partial<128, 4, ST>(a, grid, st);
+    } else {
+        if (rt == 1) launch_partial<256, 1, ST>(a, grid, st);
+        else launch_partial<256, 2, ST>(a, grid, st);
+    }
 }
 
 }  // namespace kmi
@@ -380,8 +584,7 @@ extern "C" {
 size_t kmi_kv8_workspace_bytes(int B, int H, int Hk, int L, int N, int D) {
     if (B <= 0 || H <= 0 || Hk <= 0 || L <= 0 || N <= 0 || D <= 0 || H % Hk) return 0;
     const int R = (H / Hk) * L;
-    Kv8Plan p = plan_kv8(B, Hk, N, D, R);
-    return (size_t)B * Hk * p.nblk * R * (D + 2) * sizeof(float);
+    return plan_kv8(B, Hk, N, D, R).total;
 }
 
 int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
@@ -394,7 +597,8 @@ int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
     KMI_CHECK_ARG(q && kw && ks && kb && vw && vs && vb && out && strides, "kv8_decode: null pointer");
     KMI_CHECK_ARG(B > 0 && H > 0 && L > 0 && Hk > 0 && H % Hk == 0, "kv8_decode: bad head counts");
     KMI_CHECK_ARG(D == 128 || D == 256, "kv8_decode: head dim %d not in {128, 256}", D);
-    KMI_CHECK_ARG(group >= 16 && D % group == 0, "kv8_decode: group %d must divide D=%d and be >= 16", group, D);
+    KMI_CHECK_ARG(group >= D / 4 && D % group == 0,
+                  "kv8_decode: group %d must divide D=%d and be at least D/4", group, D);
     KMI_CHECK_ARG(q_dtype >= BF16 && q_dtype <= F32 && scale_dtype >= BF16 && scale_dtype <= F32,
                   "kv8_decode: bad dtype");
     const int R = (H / Hk) * L;
@@ -402,50 +606,59 @@ int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
     KMI_CHECK_ARG(!(D == 256 && R > 32), "kv8_decode: head dim 256 takes at most 32 rows per KV head");
     KMI_CHECK_ARG(N >= 0, "kv8_decode: N=%d", N);
     hipStream_t st = (hipStream_t)stream;
+    const int qes = q_dtype == F32 ? 4 : 2;
     if (N == 0) {   // no key: every row returns 0 (a fill kernel: graph-capture safe)
-        const int64_t words = (int64_t)B * H * L * D * (q_dtype == F32 ? 4 : 2) / 4;
+        const int64_t words = (int64_t)B * H * L * D * qes / 4;
         fill_zero_u32<<<(unsigned)ceil_div(words, 256), 256, 0, st>>>((uint32_t*)out, words);
         KMI_CHECK_LAUNCH("kv8_decode(empty)");
         return OK;
     }
     Kv8Plan p = plan_kv8(B, Hk, N, D, R);
-    const size_t need = (size_t)B * Hk * p.nblk * R * (D + 2) * sizeof(float);
-    if (!workspace || workspace_bytes < need) {
-        set_error("kv8_decode: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    if (!workspace || workspace_bytes < p.total) {
+        set_error("kv8_decode: workspace of %zu bytes needed, %zu given", p.total, workspace_bytes);
         return EWORKSPACE;
     }
+    // 32-bit buffer offsets: every byte offset the kernels form stays below 2^31
+    const int64_t lim = (int64_t)1 << 31;
+    const int sdes = scale_dtype == F32 ? 4 : 2;
+    const int64_t keys_formed = (int64_t)p.nblk * p.keys_per_wg;
     Kv8Args a = {};
-    a.q = q; a.kw = kw; a.ks = ks; a.kb = kb; a.vw = vw; a.vs = vs; a.vb = vb;
-    for (int i = 0; i < 6; i++)
-        for (int j = 0; j < 3; j++) a.st[i][j] = strides[3 * i + j];
-    a.mask = mask; a.part = (float*)workspace;
-    a.qdt = q_dtype; a.sdt = scale_dtype;
-    a.B = B; a.H = H; a.Hk = Hk; a.L = L; a.N = N; a.D = D; a.group = group; a.R = R;
+    const void* bases[6] = {kw, ks, kb, vw, vs, vb};
+    for (int i = 0; i < 6; i++) {
+        const int es = (i == 0 || i == 3) ? 4 : sdes;
+        const int64_t row = (i == 0 || i == 3) ? D / 4 : D / group;
+        for (int j = 0; j < 3; j++) {
+            KMI_CHECK_ARG(strides[3 * i + j] >= 0, "kv8_decode: negative stride");
+            a.st[i][j] = strides[3 * i + j];
+        }
+        a.base[i] = bases[i];
+        a.ext[i] = ((int64_t)(N - 1) * a.st[i][2] + row) * es;
+        KMI_CHECK_ARG((keys_formed * a.st[i][2] + row) * es < lim,
+                      "kv8_decode: K/V rows span more than 2 GiB per head");
+    }
+    KMI_CHECK_ARG((int64_t)B * H * L * D * qes < lim, "kv8_decode: q larger than 2 GiB");
+    KMI_CHECK_ARG((int64_t)B * L * (keys_formed + 1) < lim, "kv8_decode: mask larger than 2 GiB");
+    KMI_CHECK_ARG((int64_t)p.po_bytes + (int64_t)B * Hk * p.nblk * R * 8 < lim,
+                  "kv8_decode: partials larger than 2 GiB");
+    a.q = q; a.mask = mask;
+    a.po = (_Float16*)workspace;
+    a.pml = (float2*)((char*)workspace + p.pml_off);
+    a.qdt = q_dtype;
+    a.B = B; a.H = H; a.Hk = Hk; a.L = L; a.N = N; a.group = group; a.R = R;
     a.causal = causal && L > 1; a.keys_per_wg = p.keys_per_wg; a.nblk = p.nblk; a.scale = scale;
     dim3 grid((unsigned)p.nblk, (unsigned)(B * Hk));
-#define KMI_KV(DD, RR)                                                                          \
-    do {                                                                                        \
-        static bool attr_set = false;                                                           \
-        if (!attr_set) {                                                                        \
-            (void)hipFuncSetAttribute((const void*)kv8_partial<DD, RR>,                             \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);        \
-            attr_set = true;                                                                    \
-        }                                                                                       \
-        kv8_partial<DD, RR><<<grid, 256, p.lds, st>>>(a);                                       \
-    } while (0)
-    if (D == 128) {
-        if (p.rt == 1) KMI_KV(128, 1);
-        else if (p.rt == 2) KMI_KV(128, 2);
-        else if (p.rt == 3) KMI_KV(128, 3);
-        else KMI_KV(128, 4);
-    } else {
-        if (p.rt == 1) KMI_KV(256, 1);
-        else KMI_KV(256, 2);
-    }
-#undef KMI_KV
+    if (scale_dtype == BF16) launch_partial_st<TBF16>(a, D, p.rt, grid, st);
+    else if (scale_dtype == F16) launch_partial_st<TF16>(a, D, p.rt, grid, st);
+    else launch_partial_st<TF32>(a, D, p.rt, grid, st);
     KMI_CHECK_LAUNCH("kv8_partial");
-    kv8_combine<<<(unsigned)(B * Hk * R), D < 256 ? D : 256, 0, st>>>(a.part, p.nblk, R, D, H, Hk, L,
-                                                                       q_dtype, out);
+    if (D == 128)
+        kv8_combine<128><<<(unsigned)(B * Hk * R), 64, 0, st>>>(a.po, a.pml, p.nblk, R, H, Hk, L, q_dtype,
+                                                               out, (int64_t)p.po_bytes,
+                                                               (int64_t)p.pml_bytes);
+    else
+        kv8_combine<256><<<(unsigned)(B * Hk * R), 64, 0, st>>>(a.po, a.pml, p.nblk, R, H, Hk, L, q_dtype,
+                                                               out, (int64_t)p.po_bytes,
+                                                               (int64_t)p.pml_bytes);
     KMI_CHECK_LAUNCH("kv8_combine");
     return OK;
 }

@@ -15,15 +15,6 @@
 
 namespace kmi {
 
-constexpr int RSRC_DWORD3 = 0x00020000;   // raw buffer, gfx9 family
-constexpr int AUX_NT = 2;                 // non-temporal: the weights are read once
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
-    const int64_t cap = 0x7fffffff;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)(bytes < cap ? bytes : cap),
-                                             RSRC_DWORD3);
-}
-
 template <int BITS, int MT, int RPW, int S, int WV>
 __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
     constexpr int NT = 64 * WV;                   // threads per workgroup

@@ -64,13 +64,15 @@ def _dims(q, K, V, bits):
 def supports(q, K, V, bits: int, group: int, mask=None, sinks=None) -> bool:
     """Whether ``decode_sdpa`` takes these shapes (else the caller falls
     back to dequantize + sdpa).  The rule of kvattn.supports, narrowed to
-    the head dims this build's kernel covers (128 and 256)."""
+    the head dims this build's kernel covers (128 and 256) and to groups of
+    at least D/4 (kvquant's caches use 64, or 32 when D % 64 != 0)."""
     if bits != 8 or sinks is not None or q.dim() != 4:
         return False
     B, H, L, D, Hk, Dk, Dv = _dims(q, K, V, bits)
     if Dk != D or Dv != D or D not in (128, 256) or H % Hk:
         return False
-    if group % (D // 32) or D % group or group < 16 or K[0].shape[0] != B:
+    # the kernel's lanes own D/4-wide runs of a key row: one group per run
+    if D % group or group < D // 4 or K[0].shape[0] != B:
         return False
     for w, sc, bi in (K, V):
         if sc.shape != bi.shape or tuple(sc.shape[:3]) != tuple(w.shape[:3]):

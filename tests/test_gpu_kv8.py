@@ -64,8 +64,22 @@ def test_float32_and_float16_queries(dev, dtype):
     _check(*_case(dev, 2, 8, 2, 1, 900, 128, dtype=dtype), None, dtype=dtype)
 
 
-def test_group_32(dev):
-    _check(*_case(dev, 1, 8, 2, 1, 500, 128, g=32), None)
+@pytest.mark.parametrize("g", [32, 128])
+def test_other_group_sizes(dev, g):
+    _check(*_case(dev, 1, 8, 2, 1, 500, 128, g=g), None)
+
+
+def test_a_group_narrower_than_a_lane_run_falls_back(dev):
+    (q, K, V, g), (tq, tK, tV) = _case(dev, 1, 8, 2, 1, 64, 256, g=32)
+    assert not kvattn.supports(tq, tK, tV, 8, g)
+    got = kvattn.dequant_sdpa(tq, tK, tV, 256 ** -0.5, None, g, 8)
+    assert_close(to_numpy(got), O.kv8_decode(q, K, V, 256 ** -0.5, None, g, 8, "float32"), what="fallback")
+
+
+def test_many_blocks_per_head(dev):
+    """One (b, hk) pair over 20k keys: the combine merges more than one
+    chunk of block partials."""
+    _check(*_case(dev, 1, 16, 1, 1, 20000, 128, seed=9), None)
 
 
 @pytest.mark.parametrize("L", [1, 2])
