@@ -107,6 +107,54 @@ struct KvShape {
     static constexpr size_t lds = vt_bytes > merge_bytes ? vt_bytes : merge_bytes;
 };
 
+// Q^T operands of v_mfma_f32_16x16x32_f16 for rows r = l16 + 16 rt: the 8 q
+// values of d run (D/4)*jg + 8k, times `scale`, in fp16; rows past R are 0.
+// All loads are issued before any is used.
+template <class QT, int D, int RT>
+__device__ __forceinline__ void load_q(u32x4 (&qop)[RT][D / 32], const Kv8Args& a, int b, int hk,
+                                       int l16, int jg) {
+    constexpr int KSTEPS = D / 32, DL = D / 4;
+    constexpr int QES = (int)sizeof(typename QT::storage);
+    constexpr int V16 = QES / 2;                  // 16-byte loads per 8 values
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q, (int64_t)a.B * a.H * a.L * D * QES);
+    const int rep = a.H / a.Hk;
+    u32x4 raw[RT][KSTEPS][V16];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int r = l16 + 16 * rt;
+        const int rr = r < a.R ? r : 0;
+        const int h = hk * rep + rr / a.L, lq = rr % a.L;
+        const uint32_t e0 = (uint32_t)((((b * a.H + h) * a.L + lq) * D) + DL * jg);
+#pragma unroll
+        for (int k = 0; k < KSTEPS; k++)
+#pragma unroll
+            for (int v = 0; v < V16; v++)
+                raw[rt][k][v] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rq, (int)((e0 + 8 * k) * (uint32_t)QES + 16u * v), 0, 0);
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const bool rok = l16 + 16 * rt < a.R;
+#pragma unroll
+        for (int k = 0; k < KSTEPS; k++) {
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                if constexpr (QES == 4) {
+                    x[e] = __uint_as_float(raw[rt][k][e / 4][e % 4]);
+                } else {
+                    const uint32_t w = raw[rt][k][0][e / 2];
+                    x[e] = QT::load((uint16_t)(e % 2 ? w >> 16 : w & 0xffffu));
+                }
+            }
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = rok ? pack_f16(x[2 * e] * a.scale, x[2 * e + 1] * a.scale) : 0u;
+            qop[rt][k] = o;
+        }
+    }
+}
+
 // Two workgroups per CU where the state fits 256 registers (D = 128, up to
 // 32 rows); otherwise one, so the accumulators may also use AGPRs.
 template <int D, int RT>
@@ -124,15 +172,14 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
     const int l16 = lane & 15, jg = lane >> 4;
     const int bh = blockIdx.y, blk = blockIdx.x;
     const int b = bh / a.Hk, hk = bh % a.Hk;
-    const int rep = a.H / a.Hk;
     const int R = a.R, N = a.N, L = a.L;
 
     // buffer views of this (b, hk): a key past N reads 0
-    __amdgpu_buffer_rsrc_t rs[6];
+    const char* bp[6];
 #pragma unroll
     for (int i = 0; i < 6; i++) {
         const int es = (i == 0 || i == 3) ? 4 : ES;
-        rs[i] = make_rsrc((const char*)a.base[i] + (b * a.st[i][0] + hk * a.st[i][1]) * es, a.ext[i]);
+        bp[i] = (const char*)a.base[i] + (b * a.st[i][0] + hk * a.st[i][1]) * es;
     }
     const uint32_t kst = (uint32_t)a.st[0][2] * 4u, vst = (uint32_t)a.st[3][2] * 4u;
     const uint32_t kss = (uint32_t)a.st[1][2], kbs = (uint32_t)a.st[2][2];
@@ -148,8 +195,15 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
     u32x4 vr[VIT][4];
     uint32_t vsr[VIT][4], vbr[VIT][4];
 
+    // Loads of step j.  Issued unconditionally, so the loop carries no
+    // "loaded or not" state: past the last step the views have extent 0 and
+    // the loads return 0 without touching memory.
     auto issue = [&](int j) {
-        const uint32_t n0 = (uint32_t)(kbase + j * KV_WG_KEYS);
+        const bool live = j < steps;
+        __amdgpu_buffer_rsrc_t rs[6];
+#pragma unroll
+        for (int i = 0; i < 6; i++) rs[i] = make_rsrc(bp[i], live ? a.ext[i] : 0);
+        const uint32_t n0 = (uint32_t)(kbase + (live ? j : 0) * KV_WG_KEYS);
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
             const uint32_t n = n0 + 16u * nt + l16;
@@ -179,44 +233,9 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
 
     // ---- Q^T operands (fp16, pre-scaled): lane column r, d run jg ---------------
     u32x4 qop[RT][KSTEPS];
-    {
-        const int qes = a.qdt == F32 ? 4 : 2;
-        const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q, (int64_t)a.B * a.H * L * D * qes);
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) {
-            const int r = l16 + 16 * rt;
-            const bool rok = r < R;
-            const int rr = rok ? r : 0;
-            const int h = hk * rep + rr / L, lq = rr % L;
-            const uint32_t e0 = (uint32_t)((((b * a.H + h) * L + lq) * D) + DL * jg);
-#pragma unroll
-            for (int k = 0; k < KSTEPS; k++) {
-                float x[8];
-                if (a.qdt == F32) {
-                    const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)((e0 + 8 * k) * 4u), 0, 0);
-                    const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)((e0 + 8 * k) * 4u + 16u), 0, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        x[e] = __uint_as_float(lo[e]);
-                        x[4 + e] = __uint_as_float(hi[e]);
-                    }
-                } else {
-                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)((e0 + 8 * k) * 2u), 0, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const uint16_t lo = (uint16_t)(v[e] & 0xffffu), hi = (uint16_t)(v[e] >> 16);
-                        x[2 * e] = a.qdt == BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
-                        x[2 * e + 1] = a.qdt == BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
-                    }
-                }
-                u32x4 o;
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    o[e] = rok ? pack_f16(x[2 * e] * a.scale, x[2 * e + 1] * a.scale) : 0u;
-                qop[rt][k] = o;
-            }
-        }
-    }
+    if (a.qdt == F32) load_q<TF32, D, RT>(qop, a, b, hk, l16, jg);
+    else if (a.qdt == F16) load_q<TF16, D, RT>(qop, a, b, hk, l16, jg);
+    else load_q<TBF16, D, RT>(qop, a, b, hk, l16, jg);
 
     float m[RT], lsum[RT];
     f32x4 O[DT][RT];
@@ -234,6 +253,25 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
 
     for (int j = 0; j < steps; j++) {
         const int n0 = kbase + j * KV_WG_KEYS;
+        // mask bytes of this lane's 8 keys per row, loaded first and used at the
+        // softmax, so waiting on them does not wait on the next step's loads
+        uint32_t mraw[RT][8];
+        if (has_mask) {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                const int r = l16 + 16 * rt;
+                const uint32_t row = (uint32_t)((b * L + (r < R ? r : 0) % L) * N);
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    mraw[rt][e] = __builtin_amdgcn_raw_buffer_load_b8(
+                        rm, (int)(row + (uint32_t)(n0 + 16 * (e >> 2) + 4 * jg + (e & 3))), 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) mraw[rt][e] = 1u;
+        }
 
         // ---- K^ -> MFMA A operands: kop[nt][2c + hh] = d run 16c + 8hh of the lane's DL
         u32x4 kop[2][KSTEPS];
@@ -278,33 +316,7 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
                 }
         }
 
-        // ---- which of this lane's 8 keys each row sees (mask bytes loaded before
-        // the prefetch, so waiting on them does not wait on the next step)
-        uint32_t mbits[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) {
-            const int r = l16 + 16 * rt;
-            const int lq = (r < R ? r : 0) % L;
-            uint32_t bits = 0;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int n = n0 + 16 * (e >> 2) + 4 * jg + (e & 3);
-                bool ok = n < N && r < R;
-                if (a.causal) ok = ok && n <= N - L + lq;
-                bits |= (ok ? 1u : 0u) << e;
-            }
-            if (has_mask) {
-                const uint32_t row = (uint32_t)((b * L + lq) * N);
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const uint32_t n = (uint32_t)(n0 + 16 * (e >> 2) + 4 * jg + (e & 3));
-                    const uint32_t mv = __builtin_amdgcn_raw_buffer_load_b8(rm, (int)(row + n), 0, 0);
-                    bits &= mv != 0 ? ~0u : ~(1u << e);
-                }
-            }
-            mbits[rt] = bits;
-        }
-        if (j + 1 < steps) issue(j + 1);   // next step's bytes stream in during this step's math
+        issue(j + 1);   // next step's bytes stream in during this step's math
         wave_lds_sync();
 
         // ---- S^T = K^ Q^T --------------------------------------------------------
@@ -323,11 +335,15 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
         u32x4 P[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
+            const int r = l16 + 16 * rt;
+            const int lq = (r < R ? r : 0) % L;
             float sv[8];
             float bm = -INFINITY;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const float v = ((mbits[rt] >> e) & 1u) ? S[e >> 2][rt][e & 3] : -INFINITY;
+                const int n = n0 + 16 * (e >> 2) + 4 * jg + (e & 3);
+                const bool ok = (n < N) & (r < R) & (!a.causal | (n <= N - L + lq)) & (mraw[rt][e] != 0);
+                const float v = ok ? S[e >> 2][rt][e & 3] : -INFINITY;
                 sv[e] = v;
                 bm = fmaxf(bm, v);
             }
