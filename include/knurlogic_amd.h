@@ -131,6 +131,46 @@ int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
 
 size_t kmi_kv8_workspace_bytes(int B, int H, int Hk, int L, int N, int D);
 
+/*
+ * The MoE router of Qwen3.5-MoE's SparseMoeBlock
+ * (src/knurlogic/engine/families/qwen/architecture/qwen3_5.py:174-179):
+ * probs = softmax(logits) in float32; the top k in descending order (equal
+ * probabilities lower expert first); scores = those probabilities
+ * renormalized in float32 and rounded to `dtype`.
+ *   logits [T, E] of dtype; inds [T, k] int32 out; scores [T, k] dtype out.
+ * E <= 1024, k <= min(E, 64).
+ */
+int kmi_moe_route(const void* logits, int dtype, int64_t T, int E, int k, int32_t* inds,
+                  void* scores, void* stream);
+
+/*
+ * _SwiGLU (qwen3_5.py:39-40,108-112), SwitchGLU's activation between the
+ * gate/up and down projections:
+ *   out[r, i] = round(round(silu_f32(gate[r, i])) * up[r, i])
+ * gate/up rows have stride `ld` (elements; e.g. the two halves of one
+ * stacked gate|up projection); out [rows, I] contiguous.
+ */
+int kmi_swiglu(const void* gate, const void* up, int64_t ld, int dtype, int64_t rows,
+               int64_t I, void* out, void* stream);
+
+/*
+ * The weighted combine of the k expert outputs (qwen3_5.py:181-182,
+ * (y * scores[..., None]).sum(-2)):
+ *   out[t, h] = round(sum_s round(y[t, s, h] * scores[t, s]))
+ * y [T, k, H], scores [T, k], out [T, H], all of `dtype`.
+ */
+int kmi_moe_combine(const void* y, const void* scores, int dtype, int64_t T, int k, int64_t H,
+                    void* out, void* stream);
+
+/*
+ * SparseMoeBlock's shared expert added to the routed combine
+ * (qwen3_5.py:184-187): out[t, h] = round(y[t, h] +
+ * round(round(sigmoid_f32(gate[t])) * shared_y[t, h])).
+ * y, shared_y, out [T, H]; gate [T] (the shared_expert_gate logit).
+ */
+int kmi_moe_shared_add(const void* y, const void* gate, const void* shared_y, int dtype, int64_t T,
+                       int64_t H, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

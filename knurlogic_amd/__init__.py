@@ -4,8 +4,8 @@ Drop-in torch-tensor mirrors of mlx's quantized ops and of the module
 classes that call them, backed by hand-written gfx950 HIP kernels behind a
 C ABI (include/knurlogic_amd.h, libknurlogic_amd.so).
 """
-from .ops import (ROUND_FUSED, ROUND_OP_BY_OP, dequantize, gather_qmm, quantize,
-                  quantized_matmul)
+from .ops import (ROUND_FUSED, ROUND_OP_BY_OP, dequantize, gather_qmm, moe_combine, moe_route,
+                  moe_shared_add, quantize, quantized_matmul, swiglu)
 
-__all__ = ["quantize", "dequantize", "quantized_matmul", "gather_qmm",
-           "ROUND_OP_BY_OP", "ROUND_FUSED"]
+__all__ = ["quantize", "dequantize", "quantized_matmul", "gather_qmm", "moe_route", "swiglu",
+           "moe_combine", "moe_shared_add", "ROUND_OP_BY_OP", "ROUND_FUSED"]

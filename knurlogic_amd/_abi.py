@@ -27,6 +27,10 @@ SIGNATURES = {
     "kmi_kv8_decode": (I, [P, I, I, I, I, I, P, P, P, P, P, P, P, I, I, I, I,
                            ctypes.c_float, P, I, P, P, SZ, P]),
     "kmi_kv8_workspace_bytes": (SZ, [I, I, I, I, I, I]),
+    "kmi_moe_route": (I, [P, I, I64, I, I, P, P, P]),
+    "kmi_swiglu": (I, [P, P, I64, I, I64, I64, P, P]),
+    "kmi_moe_combine": (I, [P, P, I, I64, I, I64, P, P]),
+    "kmi_moe_shared_add": (I, [P, P, P, I, I64, I64, P, P]),
 }
 
 ABI_VERSION = 1

@@ -1,0 +1,224 @@
+// MoE glue around the expert matmuls, for gfx950: the router (softmax,
+// top-k, renormalize), the SwiGLU activation between the gate/up and down
+// projections, and the weighted combine of the k expert outputs -- the
+// reference's SparseMoeBlock / SwitchGLU arithmetic
+// (src/knurlogic/engine/families/qwen/architecture/qwen3_5.py:35-40,108-112,
+// 170-192), each rounding step where the reference rounds.
+#include "common.hpp"
+#include "../../include/knurlogic_amd.h"
+
+namespace kmi {
+
+template <class T>
+__device__ __forceinline__ float ld_dt(const void* p, int64_t i) {
+    return T::load(((const typename T::storage*)p)[i]);
+}
+template <class T>
+__device__ __forceinline__ void st_dt(void* p, int64_t i, float v) {
+    ((typename T::storage*)p)[i] = T::store(v);
+}
+
+// A float64 result rounded to float32 and kept there: the empty asm stops
+// the compiler from fusing this rounding with a later one to fp16 into a
+// single float64 -> fp16 rounding (the reference rounds twice).
+__device__ __forceinline__ float f64_to_f32(double v) {
+    float f = (float)v;
+    asm volatile("" : "+v"(f));
+    return f;
+}
+
+constexpr int ROUTE_MAX_E = 1024;            // experts a wave holds (16 per lane)
+constexpr int ROUTE_PER_LANE = ROUTE_MAX_E / 64;
+
+// One wave per token.  probs = softmax(logits) in float32 (computed in
+// float64 and rounded once); the k largest probabilities in descending
+// order, equal ones taken lower index first (softmax is monotone, so equal
+// probabilities come only from equal logits); scores = the selected
+// probabilities renormalized (float64, rounded to float32), then rounded to
+// the logits' dtype.
+template <class T>
+__global__ __launch_bounds__(256) void moe_route_kernel(const void* __restrict__ logits, int64_t T_, int E,
+                                                        int k, int32_t* __restrict__ inds,
+                                                        void* __restrict__ scores) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T_) return;
+    float lg[ROUTE_PER_LANE];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < ROUTE_PER_LANE; j++) {
+        const int e = lane + 64 * j;
+        lg[j] = e < E ? ld_dt<T>(logits, t * E + e) : -INFINITY;
+        mx = fmaxf(mx, lg[j]);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    double ex[ROUTE_PER_LANE];
+    double sum = 0.0;
+#pragma unroll
+    for (int j = 0; j < ROUTE_PER_LANE; j++) {
+        ex[j] = lane + 64 * j < E ? exp((double)lg[j] - (double)mx) : 0.0;
+        sum += ex[j];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    float p[ROUTE_PER_LANE];
+#pragma unroll
+    for (int j = 0; j < ROUTE_PER_LANE; j++) p[j] = lane + 64 * j < E ? f64_to_f32(ex[j] / sum) : -1.f;
+
+    double top_sum = 0.0;
+    float top_p = 0.f;       // lane s keeps the s-th selection
+    int top_e = 0;
+    for (int s = 0; s < k; s++) {
+        // this lane's best (largest p, then lowest expert)
+        float bp = -2.f;
+        int be = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < ROUTE_PER_LANE; j++)
+            if (p[j] > bp) { bp = p[j]; be = lane + 64 * j; }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float op = __shfl_xor(bp, o, 64);
+            const int oe = __shfl_xor(be, o, 64);
+            if (op > bp || (op == bp && oe < be)) { bp = op; be = oe; }
+        }
+        top_sum += (double)bp;
+        if (lane == s) { top_p = bp; top_e = be; }
+#pragma unroll
+        for (int j = 0; j < ROUTE_PER_LANE; j++)
+            if (lane + 64 * j == be) p[j] = -1.f;
+    }
+    if (lane < k) {
+        inds[t * k + lane] = top_e;
+        st_dt<T>(scores, t * k + lane, f64_to_f32((double)top_p / top_sum));
+    }
+}
+
+// act[r, i] = round(round(silu(gate[r, i])) * up[r, i]), silu in float32
+// (evaluated in float64, rounded once): _SwiGLU with qwen3_5.py's _silu.
+template <class T>
+__global__ __launch_bounds__(256) void swiglu_kernel(const void* __restrict__ gate, const void* __restrict__ up,
+                                                     int64_t ld_in, int64_t rows, int64_t I,
+                                                     void* __restrict__ out) {
+    const int64_t n = rows * I;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = idx / I, i = idx % I;
+        const double g = (double)ld_dt<T>(gate, r * ld_in + i);
+        const float s = T::round(f64_to_f32(g / (1.0 + exp(-g))));
+        st_dt<T>(out, idx, s * ld_dt<T>(up, r * ld_in + i));
+    }
+}
+
+// out[t, h] = round(sum_s round(y[t, s, h] * score[t, s])): each product
+// rounded to the dtype, the k products summed (float64, exact for k <= 16
+// bf16 values) and rounded once.
+template <class T>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict__ y, const void* __restrict__ scores,
+                                                          int64_t T_, int k, int64_t H, void* __restrict__ out) {
+    const int64_t n = T_ * H;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = idx / H, h = idx % H;
+        double acc = 0.0;
+        for (int s = 0; s < k; s++)
+            acc += (double)T::round(ld_dt<T>(y, (t * k + s) * H + h) * ld_dt<T>(scores, t * k + s));
+        st_dt<T>(out, idx, f64_to_f32(acc));
+    }
+}
+
+// out[t, h] = round(y[t, h] + round(round(sigmoid_f32(g[t])) * sy[t, h])):
+// SparseMoeBlock's shared expert, gated by sigmoid(shared_expert_gate(x))
+// and added to the routed experts' combine (qwen3_5.py:184-187).
+template <class T>
+__global__ __launch_bounds__(256) void moe_shared_add_kernel(const void* __restrict__ y, const void* __restrict__ g,
+                                                             const void* __restrict__ sy, int64_t T_, int64_t H,
+                                                             void* __restrict__ out) {
+    const int64_t n = T_ * H;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = idx / H;
+        const double gv = (double)ld_dt<T>(g, t);
+        const float sg = T::round(f64_to_f32(1.0 / (1.0 + exp(-gv))));
+        const float gated = T::round(sg * ld_dt<T>(sy, idx));
+        st_dt<T>(out, idx, ld_dt<T>(y, idx) + gated);
+    }
+}
+
+static unsigned grid_for(int64_t n) {
+    const int64_t g = ceil_div(n, 256);
+    return (unsigned)(g < 65536 ? (g > 0 ? g : 1) : 65536);
+}
+
+}  // namespace kmi
+
+using namespace kmi;
+
+extern "C" {
+
+int kmi_moe_route(const void* logits, int dtype, int64_t T, int E, int k, int32_t* inds,
+                  void* scores, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(dtype >= BF16 && dtype <= F32, "moe_route: bad dtype %d", dtype);
+    KMI_CHECK_ARG(T >= 0 && E >= 1 && E <= ROUTE_MAX_E, "moe_route: %d experts (1..%d)", E, ROUTE_MAX_E);
+    KMI_CHECK_ARG(k >= 1 && k <= E && k <= 64, "moe_route: top-%d of %d experts", k, E);
+    if (T == 0) return OK;
+    KMI_CHECK_ARG(logits && inds && scores, "moe_route: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned grid = (unsigned)ceil_div(T, 4);
+    if (dtype == BF16) moe_route_kernel<TBF16><<<grid, 256, 0, st>>>(logits, T, E, k, inds, scores);
+    else if (dtype == F16) moe_route_kernel<TF16><<<grid, 256, 0, st>>>(logits, T, E, k, inds, scores);
+    else moe_route_kernel<TF32><<<grid, 256, 0, st>>>(logits, T, E, k, inds, scores);
+    KMI_CHECK_LAUNCH("moe_route");
+    return OK;
+}
+
+int kmi_swiglu(const void* gate, const void* up, int64_t ld, int dtype, int64_t rows, int64_t I,
+               void* out, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(dtype >= BF16 && dtype <= F32, "swiglu: bad dtype %d", dtype);
+    KMI_CHECK_ARG(rows >= 0 && I >= 0 && ld >= I, "swiglu: bad sizes");
+    if (rows == 0 || I == 0) return OK;
+    KMI_CHECK_ARG(gate && up && out, "swiglu: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned grid = grid_for(rows * I);
+    if (dtype == BF16) swiglu_kernel<TBF16><<<grid, 256, 0, st>>>(gate, up, ld, rows, I, out);
+    else if (dtype == F16) swiglu_kernel<TF16><<<grid, 256, 0, st>>>(gate, up, ld, rows, I, out);
+    else swiglu_kernel<TF32><<<grid, 256, 0, st>>>(gate, up, ld, rows, I, out);
+    KMI_CHECK_LAUNCH("swiglu");
+    return OK;
+}
+
+int kmi_moe_combine(const void* y, const void* scores, int dtype, int64_t T, int k, int64_t H,
+                    void* out, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(dtype >= BF16 && dtype <= F32, "moe_combine: bad dtype %d", dtype);
+    KMI_CHECK_ARG(T >= 0 && k >= 1 && k <= 64 && H >= 0, "moe_combine: bad sizes");
+    if (T == 0 || H == 0) return OK;
+    KMI_CHECK_ARG(y && scores && out, "moe_combine: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned grid = grid_for(T * H);
+    if (dtype == BF16) moe_combine_kernel<TBF16><<<grid, 256, 0, st>>>(y, scores, T, k, H, out);
+    else if (dtype == F16) moe_combine_kernel<TF16><<<grid, 256, 0, st>>>(y, scores, T, k, H, out);
+    else moe_combine_kernel<TF32><<<grid, 256, 0, st>>>(y, scores, T, k, H, out);
+    KMI_CHECK_LAUNCH("moe_combine");
+    return OK;
+}
+
+int kmi_moe_shared_add(const void* y, const void* gate, const void* shared_y, int dtype, int64_t T,
+                       int64_t H, void* out, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(dtype >= BF16 && dtype <= F32, "moe_shared_add: bad dtype %d", dtype);
+    KMI_CHECK_ARG(T >= 0 && H >= 0, "moe_shared_add: bad sizes");
+    if (T == 0 || H == 0) return OK;
+    KMI_CHECK_ARG(y && gate && shared_y && out, "moe_shared_add: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned grid = grid_for(T * H);
+    if (dtype == BF16) moe_shared_add_kernel<TBF16><<<grid, 256, 0, st>>>(y, gate, shared_y, T, H, out);
+    else if (dtype == F16) moe_shared_add_kernel<TF16><<<grid, 256, 0, st>>>(y, gate, shared_y, T, H, out);
+    else moe_shared_add_kernel<TF32><<<grid, 256, 0, st>>>(y, gate, shared_y, T, H, out);
+    KMI_CHECK_LAUNCH("moe_shared_add");
+    return OK;
+}
+
+}  // extern "C"

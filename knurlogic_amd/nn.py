@@ -1,0 +1,201 @@
+"""Module mirrors of the layers that call the quantized ops.
+
+- ``QuantizedLinear``: mlx's nn.QuantizedLinear as swapped in by the
+  reference's loader (src/knurlogic/engine/model/load_model.py:124-144).
+- ``QuantizedSwitchLinear`` / ``SwitchGLU``: mlx-lm's switch layers
+  (vendored twin at src/knurlogic/engine/families/glm5/architecture/
+  glm5_next/_mlx_vlm/models/switch_layers.py:24-86,156-193).
+- ``MLP`` / ``SparseMoeBlock``: Qwen3.5-MoE's expert block with the
+  reference's rounding edits (src/knurlogic/engine/families/qwen/
+  architecture/qwen3_5.py:35-40,108-118,151-192).
+
+Tensors live in GPU memory (torch); every product and every elementwise
+step with a rounding rule runs in the HIP library.  A dense (unquantized)
+router or shared-expert gate goes through torch's GEMM.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .ops import (gather_qmm, moe_combine, moe_route, moe_shared_add, quantize,
+                  quantized_matmul, swiglu)
+
+
+class Linear:
+    """A dense linear layer y = x @ w^T (+ bias), the library GEMM of the
+    activation dtype (a router or gate the loader left unquantized)."""
+
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None = None):
+        self.weight, self.bias = weight, bias
+
+    def __call__(self, x):
+        y = x @ self.weight.t()
+        return y + self.bias if self.bias is not None else y
+
+
+class QuantizedLinear:
+    """nn.QuantizedLinear: y = quantized_matmul(x, w, scales, biases) (+ bias)."""
+
+    def __init__(self, weight, scales, biases, bias=None, group_size: int = 64, bits: int = 4,
+                 mode: str = "affine"):
+        self.weight, self.scales, self.biases, self.bias = weight, scales, biases, bias
+        self.group_size, self.bits, self.mode = group_size, bits, mode
+
+    @classmethod
+    def from_float(cls, w: torch.Tensor, bias=None, group_size: int = 64, bits: int = 4):
+        return cls(*quantize(w, group_size=group_size, bits=bits), bias, group_size, bits)
+
+    @property
+    def input_dims(self):
+        return self.scales.shape[-1] * self.group_size
+
+    @property
+    def output_dims(self):
+        return self.weight.shape[0]
+
+    def __call__(self, x):
+        y = quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
+                             group_size=self.group_size, bits=self.bits, mode=self.mode)
+        return y + self.bias if self.bias is not None else y
+
+
+class QuantizedSwitchLinear:
+    """QuantizedSwitchLinear (switch_layers.py:24-86): per-row expert matmul
+    through gather_qmm over weight [E, N, K*bits/32]."""
+
+    def __init__(self, weight, scales, biases, bias=None, group_size: int = 64, bits: int = 4,
+                 mode: str = "affine"):
+        self.weight, self.scales, self.biases, self.bias = weight, scales, biases, bias
+        self.group_size, self.bits, self.mode = group_size, bits, mode
+
+    @classmethod
+    def from_float(cls, w: torch.Tensor, bias=None, group_size: int = 64, bits: int = 4):
+        """w [E, N, K] -> the quantized layer (mx.quantize per expert row)."""
+        return cls(*quantize(w, group_size=group_size, bits=bits), bias, group_size, bits)
+
+    @property
+    def input_dims(self):
+        return self.scales.shape[2] * self.group_size
+
+    @property
+    def output_dims(self):
+        return self.weight.shape[1]
+
+    @property
+    def num_experts(self):
+        return self.weight.shape[0]
+
+    def __call__(self, x, indices, sorted_indices: bool = False):
+        y = gather_qmm(x, self.weight, self.scales, self.biases, rhs_indices=indices,
+                       transpose=True, group_size=self.group_size, bits=self.bits,
+                       mode=self.mode, sorted_indices=sorted_indices)
+        if self.bias is not None:
+            y = y + self.bias[indices.long()].unsqueeze(-2)
+        return y
+
+
+def _stackable(a: QuantizedSwitchLinear, b: QuantizedSwitchLinear) -> bool:
+    return (a.weight.shape == b.weight.shape and a.scales.shape == b.scales.shape
+            and a.group_size == b.group_size and a.bits == b.bits and a.bias is None
+            and b.bias is None and a.weight.dtype == b.weight.dtype and a.scales.dtype == b.scales.dtype)
+
+
+class SwitchGLU:
+    """SwitchGLU (switch_layers.py:156-193) with Qwen3.5's _SwiGLU
+    activation: per (token, slot) the expert's gate and up projections,
+    round(round(silu_f32(gate)) * up), and the down projection.
+
+    Gate and up are stacked into one [E, 2I, K] weight at construction, so
+    one gather_qmm streams both (each routed expert's bytes read once per
+    call); ``gate_proj`` / ``up_proj`` stay available as views of it.  The
+    reference sorts pairs by expert when indices.size >= 64 (:175); the
+    kernels group rows by expert on every call, and sorting only reorders
+    rows, so the result is the same either way."""
+
+    def __init__(self, gate_proj: QuantizedSwitchLinear, up_proj: QuantizedSwitchLinear,
+                 down_proj: QuantizedSwitchLinear):
+        self.down_proj = down_proj
+        self.fused = None
+        if _stackable(gate_proj, up_proj):
+            cat = lambda a, b: torch.cat([a, b], dim=1).contiguous()
+            self.fused = QuantizedSwitchLinear(cat(gate_proj.weight, up_proj.weight),
+                                               cat(gate_proj.scales, up_proj.scales),
+                                               cat(gate_proj.biases, up_proj.biases),
+                                               None, gate_proj.group_size, gate_proj.bits)
+            I = gate_proj.output_dims
+            view = lambda t, lo: t[:, lo:lo + I]
+            self.gate_proj = QuantizedSwitchLinear(view(self.fused.weight, 0), view(self.fused.scales, 0),
+                                                   view(self.fused.biases, 0), None,
+                                                   gate_proj.group_size, gate_proj.bits)
+            self.up_proj = QuantizedSwitchLinear(view(self.fused.weight, I), view(self.fused.scales, I),
+                                                 view(self.fused.biases, I), None,
+                                                 up_proj.group_size, up_proj.bits)
+        else:
+            self.gate_proj, self.up_proj = gate_proj, up_proj
+
+    @classmethod
+    def from_float(cls, gate_w, up_w, down_w, group_size: int = 64, bits: int = 4):
+        q = lambda w: QuantizedSwitchLinear.from_float(w, None, group_size, bits)
+        return cls(q(gate_w), q(up_w), q(down_w))
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        """x [..., H], indices [..., k] (int) -> [..., k, H]."""
+        lead, H = x.shape[:-1], x.shape[-1]
+        k = indices.shape[-1]
+        T = math.prod(lead)
+        P = T * k
+        x3 = x.reshape(T, 1, H)
+        rhs = indices.reshape(P).to(torch.int32)
+        tok = torch.arange(P, device=x.device, dtype=torch.int32) // k
+        if self.fused is not None:
+            f = self.fused
+            gu = gather_qmm(x3, f.weight, f.scales, f.biases, lhs_indices=tok, rhs_indices=rhs,
+                            group_size=f.group_size, bits=f.bits)              # [P, 1, 2I]
+            act = swiglu(gu)                                                   # [P, 1, I]
+        else:
+            g, u = self.gate_proj, self.up_proj
+            gate = gather_qmm(x3, g.weight, g.scales, g.biases, lhs_indices=tok, rhs_indices=rhs,
+                              group_size=g.group_size, bits=g.bits)
+            up = gather_qmm(x3, u.weight, u.scales, u.biases, lhs_indices=tok, rhs_indices=rhs,
+                            group_size=u.group_size, bits=u.bits)
+            act = swiglu(gate, up)
+        d = self.down_proj
+        pairs = torch.arange(P, device=x.device, dtype=torch.int32)
+        y = gather_qmm(act, d.weight, d.scales, d.biases, lhs_indices=pairs, rhs_indices=rhs,
+                       group_size=d.group_size, bits=d.bits)                   # [P, 1, H]
+        return y.reshape(*lead, k, y.shape[-1])
+
+
+class MLP:
+    """The shared expert (qwen3_5.py:115-118): down(_silu(gate(x)) * up(x))."""
+
+    def __init__(self, gate_proj, up_proj, down_proj):
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
+
+    def __call__(self, x):
+        return self.down_proj(swiglu(self.gate_proj(x), self.up_proj(x)))
+
+
+class SparseMoeBlock:
+    """Qwen3.5-MoE's SparseMoeBlock (qwen3_5.py:151-192): router (softmax in
+    float32, top-k, renormalize, round), SwitchGLU experts, the weighted
+    combine, plus the sigmoid-gated shared expert when present."""
+
+    def __init__(self, gate, switch_mlp: SwitchGLU, top_k: int, shared_expert: MLP | None = None,
+                 shared_expert_gate=None):
+        self.gate, self.switch_mlp, self.top_k = gate, switch_mlp, top_k
+        self.shared_expert, self.shared_expert_gate = shared_expert, shared_expert_gate
+        self.norm_topk_prob = True
+
+    def experts(self, x, logits):
+        """The routed part from given router logits: route, experts, combine."""
+        inds, scores = moe_route(logits, self.top_k)
+        return moe_combine(self.switch_mlp(x, inds), scores)
+
+    def __call__(self, x):
+        y = self.experts(x, self.gate(x))
+        if self.shared_expert is not None:
+            y = moe_shared_add(y, self.shared_expert_gate(x), self.shared_expert(x))
+        return y

@@ -150,9 +150,12 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     L = _lib()
     nbytes = L.kmi_qmm_workspace_bytes(M, K, N, group_size, bits)
     ws = _workspace(nbytes, x.device)
-    _abi.check(L.kmi_qmm(_ptr(x2), M, K, N, _ptr(w.contiguous()), _ptr(scales.contiguous()),
-                         _ptr(biases.contiguous()), DTYPE_CODE[x.dtype], group_size, bits,
-                         _ptr(y), _ptr(ws), nbytes, _stream(x)), "quantized_matmul")
+    # contiguous copies held in locals until the call returns: a temporary
+    # freed mid-call could hand its memory to the next copy
+    wc, sc, bc = w.contiguous(), scales.contiguous(), biases.contiguous()
+    _abi.check(L.kmi_qmm(_ptr(x2), M, K, N, _ptr(wc), _ptr(sc), _ptr(bc), DTYPE_CODE[x.dtype],
+                         group_size, bits, _ptr(y), _ptr(ws), nbytes, _stream(x)),
+               "quantized_matmul")
     return y
 
 
@@ -202,9 +205,83 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     L = _lib()
     nbytes = L.kmi_gather_qmm_workspace_bytes(P, M, E, K, N, group_size, bits)
     ws = _workspace(nbytes, x.device)
-    _abi.check(L.kmi_gather_qmm(_ptr(x.contiguous()), Xb, M, K, _ptr(w.contiguous()),
-                                _ptr(scales.contiguous()), _ptr(biases.contiguous()), E, N,
+    xc, wc, sc, bc = x.contiguous(), w.contiguous(), scales.contiguous(), biases.contiguous()
+    _abi.check(L.kmi_gather_qmm(_ptr(xc), Xb, M, K, _ptr(wc), _ptr(sc), _ptr(bc), E, N,
                                 _ptr(lhs), _ptr(rhs), P, DTYPE_CODE[x.dtype], group_size, bits,
                                 int(bool(sorted_indices)), _ptr(y), _ptr(ws), nbytes,
                                 _stream(x)), "gather_qmm")
     return y
+
+
+# --- MoE glue --------------------------------------------------------------------
+
+def moe_route(logits: torch.Tensor, k: int):
+    """SparseMoeBlock's router (qwen3_5.py:174-179): softmax over the last
+    axis in float32, the top ``k`` (descending; equal probabilities lower
+    expert first), renormalized in float32 and rounded to the logits' dtype.
+    Returns (inds int32 [..., k], scores [..., k])."""
+    _on_gpu(logits)
+    if logits.dtype not in DTYPE_CODE:
+        raise ValueError(f"moe_route: dtype {logits.dtype}")
+    E = logits.shape[-1]
+    lg = logits.contiguous()
+    T = lg.numel() // E if E else 0
+    inds = torch.empty(*logits.shape[:-1], k, dtype=torch.int32, device=logits.device)
+    scores = torch.empty(*logits.shape[:-1], k, dtype=logits.dtype, device=logits.device)
+    _abi.check(_lib().kmi_moe_route(_ptr(lg), DTYPE_CODE[lg.dtype], T, E, k, _ptr(inds),
+                                    _ptr(scores), _stream(lg)), "moe_route")
+    return inds, scores
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor | None = None):
+    """_SwiGLU: round(round(silu_f32(gate)) * up).  With ``up`` None,
+    ``gate`` is one stacked [..., 2I] projection: gate = [..., :I],
+    up = [..., I:]."""
+    if up is None:
+        I = gate.shape[-1] // 2
+        src = gate.contiguous()
+        g_, u_, ld = src, src[..., I:], 2 * I
+        shape = (*gate.shape[:-1], I)
+    else:
+        if gate.shape != up.shape or gate.dtype != up.dtype:
+            raise ValueError("swiglu: gate and up differ in shape or dtype")
+        g_, u_ = gate.contiguous(), up.contiguous()
+        I, ld, shape = gate.shape[-1], gate.shape[-1], tuple(gate.shape)
+    _on_gpu(g_, u_)
+    rows = math.prod(shape[:-1])
+    out = torch.empty(shape, dtype=gate.dtype, device=gate.device)
+    _abi.check(_lib().kmi_swiglu(_ptr(g_), _ptr(u_), ld, DTYPE_CODE[gate.dtype], rows, I,
+                                 _ptr(out), _stream(gate)), "swiglu")
+    return out
+
+
+def moe_combine(y: torch.Tensor, scores: torch.Tensor):
+    """(y * scores[..., None]).sum(-2) with the reference's rounding: each
+    product rounded to the dtype, the k products summed once.
+    y [..., k, H], scores [..., k] -> [..., H]."""
+    _on_gpu(y, scores)
+    if y.dtype != scores.dtype or y.shape[:-1] != scores.shape:
+        raise ValueError("moe_combine: y [..., k, H] and scores [..., k] must agree")
+    k, H = y.shape[-2], y.shape[-1]
+    T = math.prod(y.shape[:-2])
+    out = torch.empty(*y.shape[:-2], H, dtype=y.dtype, device=y.device)
+    yc, sc = y.contiguous(), scores.contiguous()
+    _abi.check(_lib().kmi_moe_combine(_ptr(yc), _ptr(sc), DTYPE_CODE[y.dtype], T, k, H,
+                                      _ptr(out), _stream(y)),
+               "moe_combine")
+    return out
+
+
+def moe_shared_add(y: torch.Tensor, gate: torch.Tensor, shared_y: torch.Tensor):
+    """y + _sigmoid(gate) * shared_y with the reference's roundings
+    (qwen3_5.py:184-187); gate [..., 1] is the shared_expert_gate logit."""
+    _on_gpu(y, gate, shared_y)
+    if y.shape != shared_y.shape or gate.shape[:-1] != y.shape[:-1] or gate.shape[-1] != 1:
+        raise ValueError("moe_shared_add: y, shared_y [..., H] and gate [..., 1] must agree")
+    H = y.shape[-1]
+    T = math.prod(y.shape[:-1])
+    out = torch.empty_like(y)
+    yc, gc, sc = y.contiguous(), gate.contiguous(), shared_y.contiguous()
+    _abi.check(_lib().kmi_moe_shared_add(_ptr(yc), _ptr(gc), _ptr(sc), DTYPE_CODE[y.dtype], T, H,
+                                         _ptr(out), _stream(y)), "moe_shared_add")
+    return out

@@ -164,3 +164,24 @@ def test_gather_qmm_moe_decode_shape(dev):
                      rhs_indices=torch.from_numpy(inds).to(dev))
     ref = O.gather_qmm(x, wq, s, b, rhs_indices=inds, out_dtype="float32")
     assert_close(to_numpy(y), ref, what="moe decode")
+
+
+def test_strided_views_are_read_as_their_values(dev):
+    """Non-contiguous w / scales / biases / x (column slices of wider
+    tensors): the ops copy them contiguous and keep every copy alive until
+    the kernel is enqueued (a freed copy can hand its memory to the next)."""
+    rng = np.random.default_rng(31)
+    N, K_, E = 96, 256, 5
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (E, N, K_), 4, 64, dev)
+    wide = lambda t: torch.cat([t, t], dim=-1)[..., :t.shape[-1]]
+    vw, vs, vb = wide(tw), wide(ts), wide(tb)
+    assert not (vw.is_contiguous() or vs.is_contiguous() or vb.is_contiguous())
+    x = bf16_normal(rng, (3, K_))
+    vx = wide(to_torch(x, dev, BF))
+    y = K.quantized_matmul(vx, vw[2], vs[2], vb[2], bits=4)
+    assert_close(to_numpy(y), O.quantized_matmul(x, wq[2], s[2], b[2], True, 64, 4, "float32"),
+                 what="qmm views")
+    inds = np.array([[4, 0], [1, 1], [3, 2]], np.int32)
+    g = K.gather_qmm(vx.reshape(3, 1, 1, K_), vw, vs, vb, rhs_indices=torch.from_numpy(inds).to(dev), bits=4)
+    ref = O.gather_qmm(x.reshape(3, 1, 1, K_), wq, s, b, rhs_indices=inds, bits=4, out_dtype="float32")
+    assert_close(to_numpy(g), ref, what="gather views")
