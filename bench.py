@@ -155,6 +155,53 @@ def bench_kv8(B, H, Hk, L, N, D, cold, calls, dev):
             "bytes": nbytes, "flops": flops}
 
 
+MOE = dict(E=128, k=8, H=2048, I=768, bits=4)
+
+
+def moe_expert_bytes(H, I, bits, gs=64):
+    per_matrix = H * I * bits // 8 + 2 * 2 * I * (H // gs)          # gate / up / down
+    return 3 * per_matrix
+
+
+def bench_moe(T, cold, calls, dev):
+    """Qwen3.5-MoE-style experts: router (softmax, top-8, renormalize) from
+    N(0, 1) logits, SwitchGLU over 4-bit g64 experts, weighted combine.
+    Bytes: every routed expert's packed gate/up/down once + x and out."""
+    import torch
+    import knurlogic_amd as KA
+    from knurlogic_amd import nn
+    E, k, H, I, bits = MOE["E"], MOE["k"], MOE["H"], MOE["I"], MOE["bits"]
+    g = torch.Generator(device=dev).manual_seed(1000 + T)
+    per = E * moe_expert_bytes(H, I, bits)
+    n = max(4, math.ceil(ROTATE_BYTES / per)) if cold else 1
+    blocks = []
+    for _ in range(n):
+        w = [(torch.randn(*s, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+             for s in ((E, I, H), (E, I, H), (E, H, I))]
+        blocks.append(nn.SparseMoeBlock(None, nn.SwitchGLU.from_float(*w, bits=bits), k))
+        del w
+    x = torch.randn(T, H, device=dev, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, device=dev, generator=g).to(torch.bfloat16)
+    inds, _ = KA.moe_route(logits, k)
+    distinct = int(torch.unique(inds).numel())
+
+    def run():
+        for i in range(calls):
+            blocks[i % n].experts(x, logits)
+
+    us = time_graph(run) / calls * 1e3
+    nbytes = distinct * moe_expert_bytes(H, I, bits) + 2 * 2 * T * H
+    flops = 2.0 * T * k * 3 * H * I
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del blocks
+    torch.cuda.empty_cache()
+    return {"op": "moe_experts", "T": T, "E": E, "top_k": k, "H": H, "I": I, "bits": bits,
+            "experts_routed": distinct, "cache": "cold" if cold else "warm", "us": round(us, 3),
+            "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2), "bound": "hbm",
+            "bytes": nbytes, "flops": flops}
+
+
 def cpu_baseline(seconds=10.0):
     """The oracle's quantized_matmul (C, OpenMP) on this host's cores, 4-bit
     M=1 [14336, 4096]: calls repeated until ~`seconds` of wall time."""
@@ -187,7 +234,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no detail table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="detail sections, comma-separated "
-                                                "(dense, kv8); default all")
+                                                "(dense, kv8, moe); default all")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the path is not sharded "
@@ -220,7 +267,11 @@ def main():
     gbs = nbytes / (us * 1e-6) / 1e9
 
     detail = []
-    only = set(args.only.split(",")) if args.only else {"dense", "kv8"}
+    only = set(args.only.split(",")) if args.only else {"dense", "kv8", "moe"}
+    if not args.quick and "moe" in only:
+        for t_ in (1, 16, 256):
+            for cold in (True, False):
+                detail.append(bench_moe(t_, cold, 50 if t_ < 256 else 20, dev))
     if not args.quick and "kv8" in only:
         for n_ in (8192, 32768):
             for l_ in (1, 4):

@@ -171,6 +171,30 @@ int kmi_moe_combine(const void* y, const void* scores, int dtype, int64_t T, int
 int kmi_moe_shared_add(const void* y, const void* gate, const void* shared_y, int dtype, int64_t T,
                        int64_t H, void* out, void* stream);
 
+/*
+ * SwitchGLU with Qwen3.5's _SwiGLU, and optionally the weighted combine, in
+ * one call: switch_layers.py:172-193 (SwitchGLU.__call__: up, gate,
+ * activation, down through gather_qmm) and qwen3_5.py:108-112,181-182.
+ *   x [T, H] bf16; inds [T, k] int32 (k <= 8); scores [T, k] bf16 or NULL;
+ *   w_gu / s_gu / b_gu: the gate and up projections stacked per expert,
+ *     [E, 2I, H*bits/32] / [E, 2I, H/group] (rows 0..I-1 gate, I..2I-1 up);
+ *   w_down / s_down / b_down: [E, H, I*bits/32] / [E, H, I/group];
+ *   out: [T, H] = round(sum_s round(y[t, s] * scores[t, s])) when scores is
+ *     given, else y [T, k, H] (SwitchGLU's own output).
+ * Every intermediate rounds where the reference rounds: gate and up outputs,
+ * silu, the activation, the down output, each weighted product.  Up to 256
+ * (token, slot) pairs run token-major (two kernels, no sort); more group
+ * rows by expert.  workspace: kmi_switch_glu_workspace_bytes.
+ */
+int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                   const void* scores, const uint32_t* w_gu, const void* s_gu, const void* b_gu,
+                   const uint32_t* w_down, const void* s_down, const void* b_down, int64_t E,
+                   int dtype, int group_size, int bits, void* out, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+size_t kmi_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k, int64_t E,
+                                      int group_size, int bits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,6 +31,8 @@ SIGNATURES = {
     "kmi_swiglu": (I, [P, P, I64, I, I64, I64, P, P]),
     "kmi_moe_combine": (I, [P, P, I, I64, I, I64, P, P]),
     "kmi_moe_shared_add": (I, [P, P, P, I, I64, I64, P, P]),
+    "kmi_switch_glu": (I, [P, I64, I64, I64, I, P, P, P, P, P, P, P, P, I64, I, I, I, P, P, SZ, P]),
+    "kmi_switch_glu_workspace_bytes": (SZ, [I64, I64, I64, I, I64, I, I]),
 }
 
 ABI_VERSION = 1

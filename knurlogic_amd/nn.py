@@ -20,7 +20,7 @@ import math
 import torch
 
 from .ops import (gather_qmm, moe_combine, moe_route, moe_shared_add, quantize,
-                  quantized_matmul, swiglu)
+                  quantized_matmul, swiglu, switch_glu)
 
 
 class Linear:
@@ -140,8 +140,30 @@ class SwitchGLU:
         q = lambda w: QuantizedSwitchLinear.from_float(w, None, group_size, bits)
         return cls(q(gate_w), q(up_w), q(down_w))
 
+    def _one_call(self, k: int) -> bool:
+        f, d = self.fused, self.down_proj
+        return (f is not None and d.bias is None and k <= 8 and f.bits == d.bits
+                and f.group_size == d.group_size and f.scales.dtype == torch.bfloat16)
+
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """x [..., H], indices [..., k] (int) -> [..., k, H]."""
+        if self._one_call(indices.shape[-1]) and x.dtype == torch.bfloat16:
+            f, d = self.fused, self.down_proj
+            return switch_glu(x, indices, f.weight, f.scales, f.biases, d.weight, d.scales, d.biases,
+                              None, f.group_size, f.bits)
+        return self.gathered(x, indices)
+
+    def combine(self, x: torch.Tensor, indices: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
+        """The experts' outputs weighted by ``scores`` and summed over the k
+        slots (SparseMoeBlock's combine, qwen3_5.py:181-182) -> [..., H]."""
+        if self._one_call(indices.shape[-1]) and x.dtype == torch.bfloat16:
+            f, d = self.fused, self.down_proj
+            return switch_glu(x, indices, f.weight, f.scales, f.biases, d.weight, d.scales, d.biases,
+                              scores, f.group_size, f.bits)
+        return moe_combine(self.gathered(x, indices), scores)
+
+    def gathered(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        """The same through separate gather_qmm calls (any layer mix)."""
         lead, H = x.shape[:-1], x.shape[-1]
         k = indices.shape[-1]
         T = math.prod(lead)
@@ -192,7 +214,7 @@ class SparseMoeBlock:
     def experts(self, x, logits):
         """The routed part from given router logits: route, experts, combine."""
         inds, scores = moe_route(logits, self.top_k)
-        return moe_combine(self.switch_mlp(x, inds), scores)
+        return self.switch_mlp.combine(x, inds, scores)
 
     def __call__(self, x):
         y = self.experts(x, self.gate(x))

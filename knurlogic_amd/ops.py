@@ -285,3 +285,43 @@ def moe_shared_add(y: torch.Tensor, gate: torch.Tensor, shared_y: torch.Tensor):
     _abi.check(_lib().kmi_moe_shared_add(_ptr(yc), _ptr(gc), _ptr(sc), DTYPE_CODE[y.dtype], T, H,
                                          _ptr(out), _stream(y)), "moe_shared_add")
     return out
+
+
+def switch_glu(x: torch.Tensor, indices: torch.Tensor, w_gu, s_gu, b_gu, w_down, s_down, b_down,
+               scores: torch.Tensor | None = None, group_size: int = 64, bits: int = 4):
+    """SwitchGLU with the _SwiGLU activation, and the weighted combine when
+    ``scores`` is given, in one library call (kmi_switch_glu).
+
+    x [..., H] bf16; indices [..., k]; the gate and up projections stacked
+    per expert (w_gu [E, 2I, H*bits/32], s_gu/b_gu [E, 2I, H/group]); down
+    [E, H, I*bits/32].  Returns [..., k, H], or [..., H] with scores."""
+    _on_gpu(x, indices, w_gu, s_gu, b_gu, w_down, s_down, b_down, scores)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("switch_glu: only bfloat16 activations are implemented")
+    lead, H = tuple(x.shape[:-1]), x.shape[-1]
+    k = indices.shape[-1]
+    if tuple(indices.shape[:-1]) != lead:
+        raise ValueError("switch_glu: indices [..., k] must match x [..., H]")
+    E, I2 = w_gu.shape[0], w_gu.shape[1]
+    I = I2 // 2
+    T = math.prod(lead)
+    xc = x.contiguous()
+    ic = indices.reshape(T, k).to(torch.int32).contiguous()
+    ts = [t.contiguous() for t in (w_gu, s_gu, b_gu, w_down, s_down, b_down)]
+    sc = None
+    if scores is not None:
+        if scores.shape != indices.shape or scores.dtype != x.dtype:
+            raise ValueError("switch_glu: scores must match indices in shape and x in dtype")
+        sc = scores.contiguous()
+        out = torch.empty(*lead, H, dtype=x.dtype, device=x.device)
+    else:
+        out = torch.empty(*lead, k, H, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out
+    L = _lib()
+    nbytes = L.kmi_switch_glu_workspace_bytes(T, H, I, k, E, group_size, bits)
+    ws = _workspace(nbytes, x.device)
+    _abi.check(L.kmi_switch_glu(_ptr(xc), T, H, I, k, _ptr(ic), _ptr(sc), *[_ptr(t) for t in ts[:3]],
+                                *[_ptr(t) for t in ts[3:]], E, DTYPE_CODE[x.dtype], group_size, bits,
+                                _ptr(out), _ptr(ws), nbytes, _stream(x)), "switch_glu")
+    return out

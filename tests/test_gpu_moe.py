@@ -95,18 +95,28 @@ def _experts(rng, E, H, I, dev, bits=4):
     return glu, (fn(mats["gate"]), fn(mats["up"]), fn(mats["down"]))
 
 
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("T,E,H,I,k", [(1, 16, 256, 128, 4), (5, 16, 256, 128, 4), (64, 16, 256, 128, 4),
-                                       (1, 128, 2048, 768, 8), (16, 128, 2048, 768, 8)])
-def test_switch_glu_matches_the_oracle(dev, T, E, H, I, k):
-    rng = np.random.default_rng(T * 7 + E)
-    glu, fns = _experts(rng, E, H, I, dev)
+                                       (100, 16, 256, 128, 4), (1, 128, 2048, 768, 8),
+                                       (16, 128, 2048, 768, 8), (40, 128, 2048, 768, 8)])
+def test_switch_glu_matches_the_oracle(dev, T, E, H, I, k, bits):
+    """One library call (token-major up to 256 (token, slot) pairs, grouped by
+    expert above), the separate gather_qmm path, and the fused combine."""
+    rng = np.random.default_rng(T * 7 + E + bits)
+    glu, fns = _experts(rng, E, H, I, dev, bits)
     assert glu.fused is not None
     x = bf16_normal(rng, (T, H))
     inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
-    got = glu(to_torch(x, dev, BF), torch.from_numpy(inds).to(dev))
+    tx, ti = to_torch(x, dev, BF), torch.from_numpy(inds).to(dev)
+    got = glu(tx, ti)
     assert got.shape == (T, k, H)
     ref = O.switch_glu(x, inds, *fns)
     assert_close(to_numpy(got), ref, what="switch_glu")
+    assert_close(to_numpy(glu.gathered(tx, ti)), ref, what="gathered")
+    _, sc = O.route(bf16_normal(rng, (T, E)), k)
+    comb = glu.combine(tx, ti, to_torch(sc, dev, BF))
+    assert comb.shape == (T, H)
+    assert_close(to_numpy(comb), O.combine(ref, sc), what="combine")
 
 
 def test_switch_glu_unstacked_gate_and_up_agree(dev):
