@@ -28,7 +28,6 @@ __device__ __forceinline__ float f64_to_f32(double v) {
 }
 
 constexpr int ROUTE_MAX_E = 1024;            // experts a wave holds (16 per lane)
-constexpr int ROUTE_PER_LANE = ROUTE_MAX_E / 64;
 
 // One wave per token.  probs = softmax(logits) in float32 (computed in
 // float64 and rounded once); the k largest probabilities in descending
@@ -36,7 +35,7 @@ constexpr int ROUTE_PER_LANE = ROUTE_MAX_E / 64;
 // probabilities come only from equal logits); scores = the selected
 // probabilities renormalized (float64, rounded to float32), then rounded to
 // the logits' dtype.
-template <class T>
+template <class T, int ROUTE_PER_LANE>
 __global__ __launch_bounds__(256) void moe_route_kernel(const void* __restrict__ logits, int64_t T_, int E,
                                                         int k, int32_t* __restrict__ inds,
                                                         void* __restrict__ scores) {
@@ -166,9 +165,21 @@ int kmi_moe_route(const void* logits, int dtype, int64_t T, int E, int k, int32_
     KMI_CHECK_ARG(logits && inds && scores, "moe_route: null pointer");
     hipStream_t st = (hipStream_t)stream;
     const unsigned grid = (unsigned)ceil_div(T, 4);
-    if (dtype == BF16) moe_route_kernel<TBF16><<<grid, 256, 0, st>>>(logits, T, E, k, inds, scores);
-    else if (dtype == F16) moe_route_kernel<TF16><<<grid, 256, 0, st>>>(logits, T, E, k, inds, scores);
-    else moe_route_kernel<TF32><<<grid, 256, 0, st>>>(logits, T, E, k, inds, scores);
+    const int per = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
+#define KMI_ROUTE(TT, PL) moe_route_kernel<TT, PL><<<grid, 256, 0, st>>>(logits, T, E, k, inds, scores)
+#define KMI_ROUTE_T(TT)                                     \
+    do {                                                    \
+        if (per == 1) KMI_ROUTE(TT, 1);                     \
+        else if (per == 2) KMI_ROUTE(TT, 2);                \
+        else if (per == 4) KMI_ROUTE(TT, 4);                \
+        else if (per == 8) KMI_ROUTE(TT, 8);                \
+        else KMI_ROUTE(TT, 16);                             \
+    } while (0)
+    if (dtype == BF16) KMI_ROUTE_T(TBF16);
+    else if (dtype == F16) KMI_ROUTE_T(TF16);
+    else KMI_ROUTE_T(TF32);
+#undef KMI_ROUTE_T
+#undef KMI_ROUTE
     KMI_CHECK_LAUNCH("moe_route");
     return OK;
 }

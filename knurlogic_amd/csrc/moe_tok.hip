@@ -290,9 +290,15 @@ __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
 
 constexpr int TOK_WV = 4;
 
-static int glu_lds(int64_t K, int bits, int gs) {
+// Weight rows per wave: 1 while a call has few workgroups' worth of rows,
+// else 4 (the staged x row is then shared by 16 rows per workgroup).
+static int tok_rpw(int64_t N, int64_t wgs_per_row_tile) {
+    return ceil_div(N, TOK_WV) * wgs_per_row_tile >= 2048 ? 4 : 1;
+}
+
+static int glu_lds(int64_t K, int bits, int gs, int rpw) {
     const int64_t CK = 128 / bits, C = K / CK;
-    return (int)((128 / bits / 8) * C * 16 + C * 4 + 2 * TOK_WV * 1 * (K / gs) * 4);
+    return (int)((128 / bits / 8) * C * 16 + C * 4 + 2 * TOK_WV * rpw * (K / gs) * 4);
 }
 
 }  // namespace kmi
@@ -305,14 +311,16 @@ namespace kmi {
 int launch_moe_glu_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
     const int64_t CK = 128 / bits, C = a.K / CK;
     const int S = (int)ceil_div(C, 64);
-    const dim3 grid((unsigned)ceil_div(a.N, TOK_WV), (unsigned)(a.T * a.k));
-    const size_t lds = (size_t)glu_lds(a.K, bits, 1 << a.gs_shift);
-#define KMI_GLU(B, SS)                                                                  \
-    if (bits == B && S == SS) {                                                         \
-        moe_glu_tok<B, 1, SS, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a);              \
+    const int rpw = tok_rpw(a.N, a.T * a.k);
+    const dim3 grid((unsigned)ceil_div(a.N, TOK_WV * rpw), (unsigned)(a.T * a.k));
+    const size_t lds = (size_t)glu_lds(a.K, bits, 1 << a.gs_shift, rpw);
+#define KMI_GLU(B, R, SS)                                                               \
+    if (bits == B && rpw == R && S == SS) {                                             \
+        moe_glu_tok<B, R, SS, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a);              \
         return OK;                                                                      \
     }
-    KMI_GLU(4, 1) KMI_GLU(4, 2) KMI_GLU(4, 4) KMI_GLU(8, 1) KMI_GLU(8, 2) KMI_GLU(8, 4) KMI_GLU(8, 8)
+    KMI_GLU(4, 1, 1) KMI_GLU(4, 1, 2) KMI_GLU(4, 1, 4) KMI_GLU(8, 1, 1) KMI_GLU(8, 1, 2) KMI_GLU(8, 1, 4)
+    KMI_GLU(8, 1, 8) KMI_GLU(4, 4, 1) KMI_GLU(4, 4, 2) KMI_GLU(8, 4, 1) KMI_GLU(8, 4, 2)
 #undef KMI_GLU
     set_error("switch_glu: no gate/up kernel for %lld chunks per row", (long long)C);
     return EINVAL_ARG;
@@ -321,18 +329,21 @@ int launch_moe_glu_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
 int launch_moe_down_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
     const int64_t CK = 128 / bits, C = a.K / CK;
     const int U = (int)ceil_div((int64_t)a.k * C, 64);
-    const dim3 grid((unsigned)ceil_div(a.N, TOK_WV), (unsigned)a.T);
+    const int rpw = U <= 4 ? tok_rpw(a.N, a.T) : 1;
+    const dim3 grid((unsigned)ceil_div(a.N, TOK_WV * rpw), (unsigned)a.T);
     const size_t lds = (size_t)a.k * ((128 / bits / 8) * C * 16 + C * 4) +
-                       (size_t)a.k * TOK_WV * (a.K >> a.gs_shift) * 4;
-#define KMI_DOWN(B, KM, UU)                                                             \
-    if (bits == B && a.k <= KM && U == UU) {                                            \
-        moe_down_tok<B, KM, UU, 1, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a);         \
+                       (size_t)a.k * TOK_WV * rpw * (a.K >> a.gs_shift) * 4;
+#define KMI_DOWN(B, KM, UU, R)                                                          \
+    if (bits == B && a.k <= KM && U == UU && rpw == R) {                                \
+        moe_down_tok<B, KM, UU, R, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a);         \
         return OK;                                                                      \
     }
-    KMI_DOWN(4, 8, 1) KMI_DOWN(4, 8, 2) KMI_DOWN(4, 8, 3) KMI_DOWN(4, 8, 4)
-    KMI_DOWN(4, 8, 6) KMI_DOWN(4, 8, 8)
-    KMI_DOWN(8, 8, 1) KMI_DOWN(8, 8, 2) KMI_DOWN(8, 8, 3) KMI_DOWN(8, 8, 4)
-    KMI_DOWN(8, 8, 6) KMI_DOWN(8, 8, 8)
+    KMI_DOWN(4, 8, 1, 1) KMI_DOWN(4, 8, 2, 1) KMI_DOWN(4, 8, 3, 1) KMI_DOWN(4, 8, 4, 1)
+    KMI_DOWN(4, 8, 6, 1) KMI_DOWN(4, 8, 8, 1)
+    KMI_DOWN(8, 8, 1, 1) KMI_DOWN(8, 8, 2, 1) KMI_DOWN(8, 8, 3, 1) KMI_DOWN(8, 8, 4, 1)
+    KMI_DOWN(8, 8, 6, 1) KMI_DOWN(8, 8, 8, 1)
+    KMI_DOWN(4, 8, 1, 4) KMI_DOWN(4, 8, 2, 4) KMI_DOWN(4, 8, 3, 4) KMI_DOWN(4, 8, 4, 4)
+    KMI_DOWN(8, 8, 1, 4) KMI_DOWN(8, 8, 2, 4) KMI_DOWN(8, 8, 3, 4) KMI_DOWN(8, 8, 4, 4)
 #undef KMI_DOWN
     set_error("switch_glu: no down kernel for k=%d, %lld chunks per row", a.k, (long long)C);
     return EINVAL_ARG;
