@@ -195,6 +195,36 @@ int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const 
 size_t kmi_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k, int64_t E,
                                       int group_size, int bits);
 
+/*
+ * VQ codebook-decode expert matmul: VQSwitchLinear, the expert layer VQ
+ * artifacts ship in their own model.py (class named at
+ * tests/engine/test_deepseek_v4_mtp.py:249,360; code layout of _pack_vq at
+ * :206-233), for 8-element vectors and byte or 16-bit indices:
+ *   What_e[o, i] = scales[e, o, i / sg] * codebook[codes[e, o, i / 8]][i % 8]
+ *   y[p, :] = x[lhs[p]] @ What_{rhs[p]}^T     (lhs NULL: x row p)
+ *   x [X, K] bf16; codes [E, N, K/8] uint8 (code_bytes 1) or uint16 (2);
+ *   codebook [kc, 8] fp16 (dim must be 8); scales fp16 [E, N] when
+ *   scale_group is 0 (one per output channel), else [E, N, K/scale_group];
+ *   y [P, N] bf16.  fp32 accumulation; x enters the dot products as fp16.
+ */
+int kmi_vq_gather_qmm(const void* x, int64_t X, int64_t K, const void* codes, int code_bytes,
+                      const void* codebook, int kc, int dim, const void* scales, int scale_group,
+                      int64_t E, int64_t N, const int32_t* lhs, const int32_t* rhs, int64_t P,
+                      int dtype, void* y, void* stream);
+
+/*
+ * The gate and up VQ projections of SwitchGLU with the _SwiGLU epilogue
+ * (switch_layers.py:172-193 over VQSwitchLinear; qwen3_5.py:108-112):
+ *   act[t*k + s, :] = round(round(silu(round(gate))) * round(up)) for the
+ *   expert inds[t, s] and the token row x[t]; x [T, H]; codes_* [E, I, H/8];
+ *   scales_* as kmi_vq_gather_qmm; act [T*k, I] bf16.  The gate and up
+ *   codebooks may be the same pointer.
+ */
+int kmi_vq_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+               const void* codes_gate, const void* scales_gate, const void* codebook_gate,
+               const void* codes_up, const void* scales_up, const void* codebook_up, int code_bytes,
+               int kc, int dim, int scale_group, int64_t E, int dtype, void* act, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

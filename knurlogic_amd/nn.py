@@ -5,6 +5,10 @@
 - ``QuantizedSwitchLinear`` / ``SwitchGLU``: mlx-lm's switch layers
   (vendored twin at src/knurlogic/engine/families/glm5/architecture/
   glm5_next/_mlx_vlm/models/switch_layers.py:24-86,156-193).
+- ``VQSwitchLinear`` / ``VQSwitchGLU``: the codebook-decode experts VQ
+  artifacts ship in their model.py (class named at tests/engine/
+  test_deepseek_v4_mtp.py:249,360), 8-element vectors, byte or 16-bit
+  indices, fp16 codebook and scales.
 - ``MLP`` / ``SparseMoeBlock``: Qwen3.5-MoE's expert block with the
   reference's rounding edits (src/knurlogic/engine/families/qwen/
   architecture/qwen3_5.py:35-40,108-118,151-192).
@@ -20,7 +24,7 @@ import math
 import torch
 
 from .ops import (gather_qmm, moe_combine, moe_route, moe_shared_add, quantize,
-                  quantized_matmul, swiglu, switch_glu)
+                  quantized_matmul, swiglu, switch_glu, vq_gather_qmm, vq_glu)
 
 
 class Linear:
@@ -188,6 +192,56 @@ class SwitchGLU:
         y = gather_qmm(act, d.weight, d.scales, d.biases, lhs_indices=pairs, rhs_indices=rhs,
                        group_size=d.group_size, bits=d.bits)                   # [P, 1, H]
         return y.reshape(*lead, k, y.shape[-1])
+
+
+class VQSwitchLinear:
+    """VQ experts: weight[e, o, i] = scales[e, o, i / scale_group] *
+    codebook[codes[e, o, i / dim]][i % dim] (scale_group 0: scales [E, N],
+    one per output channel); the call is gather_qmm's."""
+
+    def __init__(self, codes, codebook, scales, scale_group: int = 0):
+        self.codes, self.codebook, self.scales, self.scale_group = codes, codebook, scales, scale_group
+
+    @property
+    def input_dims(self):
+        return self.codes.shape[2] * self.codebook.shape[1]
+
+    @property
+    def output_dims(self):
+        return self.codes.shape[1]
+
+    @property
+    def num_experts(self):
+        return self.codes.shape[0]
+
+    def __call__(self, x, indices, sorted_indices: bool = False):
+        return vq_gather_qmm(x, self.codes, self.codebook, self.scales, rhs_indices=indices,
+                             scale_group=self.scale_group)
+
+
+class VQSwitchGLU:
+    """SwitchGLU over VQ experts with the _SwiGLU activation: the gate and up
+    projections and the activation in one kernel, then the down projection
+    (and the weighted combine)."""
+
+    def __init__(self, gate_proj: VQSwitchLinear, up_proj: VQSwitchLinear, down_proj: VQSwitchLinear):
+        self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
+
+    def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        """x [..., H], indices [..., k] -> [..., k, H]."""
+        g, u, d = self.gate_proj, self.up_proj, self.down_proj
+        act = vq_glu(x, indices, (g.codes, g.codebook, g.scales), (u.codes, u.codebook, u.scales),
+                     g.scale_group)                                           # [..., k, I]
+        lead, k = tuple(indices.shape[:-1]), indices.shape[-1]
+        P = math.prod(lead) * k
+        a2 = act.reshape(P, 1, act.shape[-1])
+        y = vq_gather_qmm(a2, d.codes, d.codebook, d.scales,
+                          lhs_indices=torch.arange(P, device=x.device, dtype=torch.int32),
+                          rhs_indices=indices.reshape(P).to(torch.int32), scale_group=d.scale_group)
+        return y.reshape(*lead, k, y.shape[-1])
+
+    def combine(self, x, indices, scores):
+        return moe_combine(self(x, indices), scores)
 
 
 class MLP:

@@ -325,3 +325,88 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, w_gu, s_gu, b_gu, w_down,
                                 *[_ptr(t) for t in ts[3:]], E, DTYPE_CODE[x.dtype], group_size, bits,
                                 _ptr(out), _ptr(ws), nbytes, _stream(x)), "switch_glu")
     return out
+
+
+# --- VQ codebook-decode experts ---------------------------------------------------
+
+_CODE_BYTES = {torch.uint8: 1, torch.uint16: 2, torch.int16: 2}
+
+
+def _vq_operands(codes, codebook, scales):
+    if codes.dtype not in _CODE_BYTES:
+        raise ValueError(f"vq: codes must be uint8 or uint16 (got {codes.dtype})")
+    if codebook.dtype != torch.float16 or scales.dtype != torch.float16:
+        raise ValueError("vq: codebook and scales must be float16")
+    if codebook.ndim != 2:
+        raise ValueError("vq: codebook [k, dim]")
+    return _CODE_BYTES[codes.dtype], codebook.shape[0], codebook.shape[1]
+
+
+def vq_gather_qmm(x: torch.Tensor, codes: torch.Tensor, codebook: torch.Tensor, scales: torch.Tensor,
+                  lhs_indices=None, rhs_indices=None, scale_group: int = 0):
+    """VQSwitchLinear's product: out[i] = x[lhs[i]] @ What[rhs[i]]^T with
+    What[e, o, j] = scales[e, o, j / scale_group] * codebook[codes[e, o, j/dim]][j % dim]
+    (scale_group 0: scales [E, N], one per output channel).  x [..., M, K];
+    codes [E, N, K/dim]; out [*broadcast(lhs, rhs), M, N]."""
+    cbytes, kc, dim = _vq_operands(codes, codebook, scales)
+    _on_gpu(x, codes, codebook, scales)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("vq_gather_qmm: only bfloat16 activations are implemented")
+    E, N = codes.shape[0], codes.shape[1]
+    M, K = x.shape[-2], x.shape[-1]
+    if codes.shape[2] * dim != K:
+        raise ValueError(f"vq_gather_qmm: codes {tuple(codes.shape)} do not cover K={K}")
+    lhs, rhs, ishape = _vq_indices(x, E, lhs_indices, rhs_indices)
+    P = lhs.numel()
+    y = torch.empty(*ishape, M, N, dtype=x.dtype, device=x.device)
+    if P == 0:
+        return y
+    # one (pair, row) per kernel row: x rows lhs*M + m, experts repeated
+    m = torch.arange(M, device=x.device, dtype=torch.int32)
+    rows = (lhs.view(-1, 1) * M + m).reshape(-1).contiguous()
+    experts = rhs.view(-1, 1).expand(P, M).reshape(-1).contiguous()
+    xc = x.reshape(-1, K).contiguous()
+    cc, cbc, sc = codes.contiguous(), codebook.contiguous(), scales.contiguous()
+    _abi.check(_lib().kmi_vq_gather_qmm(_ptr(xc), xc.shape[0], K, _ptr(cc), cbytes, _ptr(cbc), kc, dim,
+                                        _ptr(sc), scale_group, E, N, _ptr(rows), _ptr(experts), P * M,
+                                        DTYPE_CODE[x.dtype], _ptr(y), _stream(x)), "vq_gather_qmm")
+    return y
+
+
+def _vq_indices(x, E, lhs_indices, rhs_indices):
+    dev = x.device
+    xbatch = tuple(x.shape[:-2])
+    if lhs_indices is None:
+        lhs_indices = torch.arange(math.prod(xbatch), device=dev, dtype=torch.int32).reshape(xbatch)
+    if rhs_indices is None:
+        rhs_indices = torch.arange(E, device=dev, dtype=torch.int32)
+    lhs = torch.as_tensor(lhs_indices, device=dev)
+    rhs = torch.as_tensor(rhs_indices, device=dev)
+    lhs, rhs = torch.broadcast_tensors(lhs, rhs)
+    shape = tuple(lhs.shape)
+    return (lhs.reshape(-1).to(torch.int32).contiguous(), rhs.reshape(-1).to(torch.int32).contiguous(),
+            shape)
+
+
+def vq_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, scale_group: int = 0):
+    """The VQ gate and up projections of SwitchGLU with the _SwiGLU epilogue,
+    one kernel: gate / up = (codes, codebook, scales).  x [..., H],
+    indices [..., k] -> act [..., k, I]."""
+    (cg, bg, sg_), (cu, bu, su) = gate, up
+    cbytes, kc, dim = _vq_operands(cg, bg, sg_)
+    if _vq_operands(cu, bu, su) != (cbytes, kc, dim) or cu.shape != cg.shape:
+        raise ValueError("vq_glu: gate and up differ in layout")
+    _on_gpu(x, indices, cg, bg, sg_, cu, bu, su)
+    lead, H = tuple(x.shape[:-1]), x.shape[-1]
+    k = indices.shape[-1]
+    E, I = cg.shape[0], cg.shape[1]
+    T = math.prod(lead)
+    act = torch.empty(*lead, k, I, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return act
+    xc = x.reshape(T, H).contiguous()
+    ic = indices.reshape(T, k).to(torch.int32).contiguous()
+    ops = [t.contiguous() for t in (cg, sg_, bg, cu, su, bu)]
+    _abi.check(_lib().kmi_vq_glu(_ptr(xc), T, H, I, k, _ptr(ic), *[_ptr(t) for t in ops], cbytes, kc, dim,
+                                 scale_group, E, DTYPE_CODE[x.dtype], _ptr(act), _stream(x)), "vq_glu")
+    return act
