@@ -202,6 +202,71 @@ def bench_moe(T, cold, calls, dev):
             "bytes": nbytes, "flops": flops}
 
 
+def vq_expert_bytes(H, I, code_bytes):
+    codes = (2 * I * (H // 8) + H * (I // 8)) * code_bytes          # gate, up, down indices
+    return codes + 2 * (2 * I + H)                                   # fp16 per-channel scales
+
+
+def bench_vq(T, kc, cold, calls, dev):
+    """VQ experts at the Qwen3.5-MoE shape: 8-element vectors into a per-layer
+    fp16 codebook (256 x 8 with uint8 indices, or 4096 x 8 with uint16),
+    per-output-channel fp16 scales U(0.5, 1.5); router from N(0, 1) logits,
+    fused gate/up + SwiGLU, down, weighted combine.  Bytes: every routed
+    expert's indices and scales once, the codebook, x and out."""
+    import torch
+    import knurlogic_amd as KA
+    from knurlogic_amd import nn
+    E, k, H, I = MOE["E"], MOE["k"], MOE["H"], MOE["I"]
+    cb_bytes = 1 if kc <= 256 else 2
+    ct = torch.uint8 if cb_bytes == 1 else torch.uint16
+    g = torch.Generator(device=dev).manual_seed(2000 + T + kc)
+    per = E * vq_expert_bytes(H, I, cb_bytes)
+    n = max(4, math.ceil(ROTATE_BYTES / per)) if cold else 1
+    cb = (torch.randn(kc, 8, device=dev, generator=g) * 0.02).to(torch.float16)
+
+    def mat(N, K):
+        codes = torch.randint(0, kc, (E, N, K // 8), device=dev, generator=g, dtype=torch.int32).to(ct)
+        sc = (torch.rand(E, N, device=dev, generator=g) + 0.5).to(torch.float16)
+        return nn.VQSwitchLinear(codes, cb, sc)
+
+    glus = [nn.VQSwitchGLU(mat(I, H), mat(I, H), mat(H, I)) for _ in range(n)]
+    x = torch.randn(T, H, device=dev, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, device=dev, generator=g).to(torch.bfloat16)
+    inds, _ = KA.moe_route(logits, k)
+    distinct = int(torch.unique(inds).numel())
+
+    def run():
+        for i in range(calls):
+            ii, sc = KA.moe_route(logits, k)
+            glus[i % n].combine(x, ii, sc)
+
+    us = time_graph(run) / calls * 1e3
+    nbytes = distinct * vq_expert_bytes(H, I, cb_bytes) + kc * 16 + 2 * 2 * T * H
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del glus
+    torch.cuda.empty_cache()
+    return {"op": "vq_moe_experts", "T": T, "codebook": f"{kc}x8 fp16", "index_bytes": cb_bytes,
+            "experts_routed": distinct, "cache": "cold" if cold else "warm", "us": round(us, 3),
+            "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm",
+            "bytes": nbytes, "flops": 2.0 * T * k * 3 * H * I}
+
+
+HEADLINE_PROFILE = ROOT / "profiles" / "qmv_4bit_14336x4096_m1.md"
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the headline kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (scaled by a known-size copy);
+    None when the summary is absent."""
+    try:
+        for line in HEADLINE_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        return None
+    return None
+
+
 def cpu_baseline(seconds=10.0):
     """The oracle's quantized_matmul (C, OpenMP) on this host's cores, 4-bit
     M=1 [14336, 4096]: calls repeated until ~`seconds` of wall time."""
@@ -234,8 +299,21 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no detail table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="detail sections, comma-separated "
-                                                "(dense, kv8, moe); default all")
+                                                "(dense, kv8, moe, vq); default all")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 10 plain device copies of MIB MiB (the known-size kernel "
+                         "that calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    if args.copy_probe:
+        import torch
+        n = args.copy_probe << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "copies": 10}))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the path is not sharded "
                           "and no figure at several GPUs exists (bench.py --gpus 1)"}))
@@ -267,7 +345,12 @@ def main():
     gbs = nbytes / (us * 1e-6) / 1e9
 
     detail = []
-    only = set(args.only.split(",")) if args.only else {"dense", "kv8", "moe"}
+    only = set(args.only.split(",")) if args.only else {"dense", "kv8", "moe", "vq"}
+    if not args.quick and "vq" in only:
+        for kc_ in (256, 4096):
+            for t_ in (1, 16):
+                for cold in (True, False):
+                    detail.append(bench_vq(t_, kc_, cold, 50, dev))
     if not args.quick and "moe" in only:
         for t_ in (1, 16, 256):
             for cold in (True, False):
@@ -299,7 +382,9 @@ def main():
                    "us_per_layer": round(us, 3), "cache": "cold (weight sets rotated past 1 GB)",
                    "device": torch.cuda.get_device_name(dev)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": profiled_traffic(),
+                     "algorithmic_bytes": nbytes, "launch_us": round(us, 3),
+                     "traffic_source": "profiles/qmv_4bit_14336x4096_m1.md"},
         "cpu_baseline": cpu,
         "detail": detail,
     }
