@@ -141,18 +141,252 @@ __global__ __launch_bounds__(256) void qmm_kernel(
         }
 }
 
+// =============================================================================
+// qmm2: M > 128.  256 x 128 x 64 block tiles; 4 waves, each a 128 x 64 tile
+// of y (8 x 4 blocks of v_mfma_f32_16x16x32_bf16), so every 16-byte LDS read
+// feeds 4 or 8 MFMAs (44 flop per LDS byte).  The x tile (bf16, mostly L2
+// hits) is staged one k-tile ahead through registers; the packed weight tile
+// (the only HBM stream, 16 B per thread per k-tile at 4 bits) runs Q2_RING
+// k-tiles ahead in a register ring, and is dequantized once per k-tile
+// (fp32 s*q + b, rounded to bf16 by v_cvt_pk_bf16_f32) into LDS.  Rows past
+// M, columns past N and k-tiles past the split read zeros from their buffer
+// views.  When the tiles leave CUs idle, K is split: each split writes fp32
+// partials and qmm_split_reduce sums them in split order.
+// =============================================================================
+constexpr int Q2M = 256, Q2N = 128, Q2K = 64, Q2LDS = Q2K + 8;
+constexpr int Q2_RING = 4;
+
+typedef __bf16 q2_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float q2_f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+    const q2_f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, q2_bf16x2));
+}
+
+struct Qmm2Args {
+    const uint16_t* x;          // [M, K] bf16
+    const uint32_t* w;          // [N, K*bits/32]
+    const uint16_t* s;          // [N, K/gs] bf16
+    const uint16_t* b;
+    uint16_t* y;                // [M, N] bf16 (one split)
+    float* partial;             // [splits, M, N] fp32 (several splits)
+    int64_t M, N, K;
+    int kt_per_split, splits, n_tiles;
+};
+
+template <int BITS, int GS>
+__global__ __launch_bounds__(256, 1) void qmm2_kernel(Qmm2Args a) {
+    constexpr int EPW = 32 / BITS;
+    constexpr int BW = Q2K / 2 / EPW;           // packed words per thread per k-tile (4 or 8)
+    static_assert(GS >= 32, "one scale group per 32-wide half row");
+    __shared__ __align__(16) uint16_t As[2][Q2M * Q2LDS];
+    __shared__ __align__(16) uint16_t Bs[2][Q2N * Q2LDS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nt = (int)(blockIdx.x % a.n_tiles), mt = (int)(blockIdx.x / a.n_tiles);
+    const int64_t bm = (int64_t)mt * Q2M, bn = (int64_t)nt * Q2N;
+    const int nk = (int)(a.K / Q2K);
+    const int kt0 = (int)blockIdx.y * a.kt_per_split;
+    const int kt1 = kt0 + a.kt_per_split < nk ? kt0 + a.kt_per_split : nk;
+    const int64_t wpr = a.K / EPW, gpr = a.K / GS;
+
+    // A: thread chunk c = tid + 256 i -> row c / 8, 16-byte piece c % 8
+    // B: thread -> weight row tid / 2, k half tid % 2 (32 values)
+    const int brow = tid >> 1, bhalf = tid & 1;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + bm * a.K, (a.M - bm) * a.K * 2);
+    const int64_t nrows = a.N - bn;
+    const __amdgpu_buffer_rsrc_t rwt = make_rsrc(a.w + bn * wpr, nrows * wpr * 4);
+    const __amdgpu_buffer_rsrc_t rwz = make_rsrc(a.w, 0);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s + bn * gpr, nrows * gpr * 2);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b + bn * gpr, nrows * gpr * 2);
+    const uint32_t wrow_off = (uint32_t)(brow * wpr * 4 + bhalf * BW * 4);
+    const uint32_t srow_off = (uint32_t)(brow * gpr * 2);
+
+    u32x4 ra[8];
+    u32x4 rw[Q2_RING][BW / 4];
+    uint32_t rsc[Q2_RING], rbi[Q2_RING];
+
+    auto load_a = [&](int kt) {        // kt past the split: a zero-extent view, no traffic
+        const __amdgpu_buffer_rsrc_t r = kt < kt1 ? rx : rwz;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int c = tid + 256 * i;
+            const uint32_t off = (uint32_t)(((c >> 3) * a.K + (int64_t)kt * Q2K + (c & 7) * 8) * 2);
+            ra[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+        }
+    };
+    auto load_b = [&](int slot, int kt) {
+        const bool live = kt < kt1;
+        const __amdgpu_buffer_rsrc_t r = live ? rwt : rwz;
+        const uint32_t off = wrow_off + (uint32_t)kt * (Q2K / EPW) * 4u;
+#pragma unroll
+        for (int q = 0; q < BW / 4; q++)
+            rw[slot][q] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off + 16u * q), 0, AUX_NT);
+        const uint32_t g = (uint32_t)(((int64_t)kt * Q2K + 32 * bhalf) / GS);
+        rsc[slot] = __builtin_amdgcn_raw_buffer_load_b16(live ? rs : rwz, (int)(srow_off + 2u * g), 0, 0);
+        rbi[slot] = __builtin_amdgcn_raw_buffer_load_b16(live ? rb : rwz, (int)(srow_off + 2u * g), 0, 0);
+    };
+    auto store = [&](int buf, int slot) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int c = tid + 256 * i;
+            *(u32x4*)(&As[buf][(c >> 3) * Q2LDS + (c & 7) * 8]) = ra[i];
+        }
+        const float sc = bf16_to_f32((uint16_t)rsc[slot]), bi = bf16_to_f32((uint16_t)rbi[slot]);
+        uint32_t ow[16];
+#pragma unroll
+        for (int e = 0; e < 32; e += 2) {
+            const uint32_t w0 = rw[slot][(e / EPW) / 4][(e / EPW) % 4];
+            const uint32_t w1 = rw[slot][((e + 1) / EPW) / 4][((e + 1) / EPW) % 4];
+            const float q0 = (float)((w0 >> ((e % EPW) * BITS)) & ((1u << BITS) - 1u));
+            const float q1 = (float)((w1 >> (((e + 1) % EPW) * BITS)) & ((1u << BITS) - 1u));
+            ow[e / 2] = cvt_pk_bf16(__builtin_fmaf(sc, q0, bi), __builtin_fmaf(sc, q1, bi));
+        }
+        uint16_t* dst = &Bs[buf][brow * Q2LDS + 32 * bhalf];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            *(u32x4*)(dst + 8 * i) = u32x4{ow[4 * i], ow[4 * i + 1], ow[4 * i + 2], ow[4 * i + 3]};
+    };
+
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 64;
+    const int l16 = lane & 15, lk = lane >> 4;
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int r = 0; r < Q2_RING; r++) load_b(r, kt0 + r);
+    load_a(kt0);
+    store(0, 0);
+    load_b(0, kt0 + Q2_RING);
+    __syncthreads();
+
+    for (int kb = kt0; kb < kt1; kb += Q2_RING) {
+#pragma unroll
+        for (int u = 0; u < Q2_RING; u++) {
+            const int t = kb + u;
+            if (t < kt1) {
+                const int buf = (t - kt0) & 1;
+                load_a(t + 1);
+#pragma unroll
+                for (int ks = 0; ks < Q2K / 32; ks++) {
+                    u32x4 af[8], bfr[4];
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+                        af[i] = *(const u32x4*)(&As[buf][(wm + 16 * i + l16) * Q2LDS + ks * 32 + lk * 8]);
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        bfr[j] = *(const u32x4*)(&Bs[buf][(wn + 16 * j + l16) * Q2LDS + ks * 32 + lk * 8]);
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
+                }
+                const int ns = (u + 1) % Q2_RING;        // ring slot of tile t + 1
+                if (t + 1 < kt1) store(buf ^ 1, ns);
+                load_b(ns, t + 1 + Q2_RING);
+                __syncthreads();
+            }
+        }
+    }
+
+    // D of block (i, j): row 16 i + 4 lk + r, column 16 j + l16
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int64_t col = bn + wn + 16 * j + l16;
+            if (col >= a.N) continue;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int64_t row = bm + wm + 16 * i + 4 * lk + r;
+                if (row >= a.M) continue;
+                if (a.splits == 1) a.y[row * a.N + col] = f32_to_bf16(acc[i][j][r]);
+                else a.partial[((int64_t)blockIdx.y * a.M + row) * a.N + col] = acc[i][j][r];
+            }
+        }
+}
+
+__global__ __launch_bounds__(256) void qmm_split_reduce(const float* __restrict__ partial, int S,
+                                                        int64_t count, uint16_t* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    float acc = 0.f;
+    for (int s = 0; s < S; s++) acc += partial[(int64_t)s * count + i];
+    y[i] = f32_to_bf16(acc);
+}
+
+struct Qmm2Plan {
+    int n_tiles, m_tiles, splits, kt_per_split;
+    size_t ws;
+};
+
+// K splits while the tiles would fill under half of the CUs (one 110 KB
+// workgroup per CU), at least 8 k-tiles per split.
+static Qmm2Plan plan_qmm2(int64_t M, int64_t N, int64_t K) {
+    Qmm2Plan p;
+    p.n_tiles = (int)ceil_div(N, Q2N);
+    p.m_tiles = (int)ceil_div(M, Q2M);
+    const int tiles = p.n_tiles * p.m_tiles;
+    const int nk = (int)(K / Q2K);
+    int s = tiles * 2 <= 256 ? 256 / tiles : 1;
+    if (s > nk / 8) s = nk / 8 > 0 ? nk / 8 : 1;
+    p.kt_per_split = (int)ceil_div(nk, s);
+    p.splits = (int)ceil_div(nk, p.kt_per_split);
+    p.ws = p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+    return p;
+}
+
+size_t qmm_gemm_workspace(int64_t M, int64_t K, int64_t N) {
+    if (M <= 128) return 0;
+    return plan_qmm2(M, N, K).ws;
+}
+
 int qmm_gemm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
              const void* scales, const void* biases, int group_size, int bits, void* y,
-             hipStream_t st) {
+             void* workspace, size_t workspace_bytes, hipStream_t st) {
     KMI_CHECK_ARG(K % GBK == 0, "quantized_matmul: K=%lld must be a multiple of 64 for M > 16",
                   (long long)K);
     KMI_CHECK_ARG(group_size >= 32, "quantized_matmul: group_size %d", group_size);
-    dim3 grid((unsigned)ceil_div(N, GBN), (unsigned)ceil_div(M, GBM));
-    KMI_CHECK_ARG(grid.y < 65536, "quantized_matmul: M too large");
     const uint16_t* xx = (const uint16_t*)x;
     const uint16_t* ss = (const uint16_t*)scales;
     const uint16_t* bb = (const uint16_t*)biases;
     uint16_t* yy = (uint16_t*)y;
+    if (M > 128) {
+        KMI_CHECK_ARG(M * K * 2 < (1LL << 31) && N * K * bits / 8 < (1LL << 31),
+                      "quantized_matmul: x or w past 2 GiB");
+        const Qmm2Plan p = plan_qmm2(M, N, K);
+        if (p.ws > 0 && (!workspace || workspace_bytes < p.ws)) {
+            set_error("quantized_matmul: workspace of %zu bytes needed, %zu given", p.ws, workspace_bytes);
+            return EWORKSPACE;
+        }
+        Qmm2Args a = {xx, w, ss, bb, yy, (float*)workspace, M, N, K, p.kt_per_split, p.splits, p.n_tiles};
+        const dim3 grid((unsigned)(p.n_tiles * p.m_tiles), (unsigned)p.splits);
+#define KMI_QMM2(B, G) qmm2_kernel<B, G><<<grid, 256, 0, st>>>(a)
+        if (bits == 4) {
+            if (group_size == 32) KMI_QMM2(4, 32);
+            else if (group_size == 64) KMI_QMM2(4, 64);
+            else KMI_QMM2(4, 128);
+        } else {
+            if (group_size == 32) KMI_QMM2(8, 32);
+            else if (group_size == 64) KMI_QMM2(8, 64);
+            else KMI_QMM2(8, 128);
+        }
+#undef KMI_QMM2
+        KMI_CHECK_LAUNCH("qmm2");
+        if (p.splits > 1) {
+            const int64_t count = M * N;
+            qmm_split_reduce<<<(unsigned)ceil_div(count, 256), 256, 0, st>>>((const float*)workspace, p.splits,
+                                                                              count, yy);
+            KMI_CHECK_LAUNCH("qmm_split_reduce");
+        }
+        return OK;
+    }
+    dim3 grid((unsigned)ceil_div(N, GBN), (unsigned)ceil_div(M, GBM));
+    KMI_CHECK_ARG(grid.y < 65536, "quantized_matmul: M too large");
 #define KMI_QMM(B, G) qmm_kernel<B, G><<<grid, 256, 0, st>>>(xx, w, ss, bb, yy, M, N, K)
     if (bits == 4) {
         if (group_size == 32) KMI_QMM(4, 32);

@@ -349,7 +349,8 @@ static int launch_qmv(QmvKind k, const QmvArgs& a, int bits, int gs, dim3 grid, 
 
 int qmm_gemm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
              const void* scales, const void* biases, int group_size, int bits, void* y,
-             hipStream_t st);  // qmm.hip
+             void* workspace, size_t workspace_bytes, hipStream_t st);
+size_t qmm_gemm_workspace(int64_t M, int64_t K, int64_t N);  // qmm.hip
 
 static int check_common(int64_t K, int64_t N, int dtype, int gs, int bits) {
     KMI_CHECK_ARG(dtype == BF16, "quantized matmul: only bfloat16 activations are supported (got dtype %d)", dtype);
@@ -393,7 +394,7 @@ extern "C" {
 
 size_t kmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits) {
     if (M <= 0 || K <= 0 || N <= 0 || group_size <= 0 || (bits != 4 && bits != 8)) return 0;
-    if (M > QM_TILE) return 0;                                    // GEMM path
+    if (M > QM_TILE) return qmm_gemm_workspace(M, K, N);         // GEMM path (split-K partials)
     if (choose_kind(M, K, N, M, bits, group_size) != QmvKind::MFMA) return 0;   // VALU path
     MfmaPlan p = plan_mfma(K, N, 1, group_size);
     return p.S > 1 ? (size_t)p.S * M * N * sizeof(float) : 0;
@@ -410,7 +411,8 @@ int kmi_qmm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
     if (M == 0) return OK;
     KMI_CHECK_ARG(x && y, "quantized_matmul: null pointer");
     hipStream_t st = (hipStream_t)stream;
-    if (M > QM_TILE) return qmm_gemm(x, M, K, N, w, scales, biases, group_size, bits, y, st);
+    if (M > QM_TILE)
+        return qmm_gemm(x, M, K, N, w, scales, biases, group_size, bits, y, workspace, workspace_bytes, st);
     QmvArgs a = {};
     a.x = (const uint16_t*)x; a.w = w; a.s = (const uint16_t*)scales; a.b = (const uint16_t*)biases;
     a.y = (uint16_t*)y; a.K = K; a.N = N; a.rows = M; a.Mper = 1; a.Xrows = M; a.S = 1;

@@ -185,3 +185,17 @@ def test_strided_views_are_read_as_their_values(dev):
     g = K.gather_qmm(vx.reshape(3, 1, 1, K_), vw, vs, vb, rhs_indices=torch.from_numpy(inds).to(dev), bits=4)
     ref = O.gather_qmm(x.reshape(3, 1, 1, K_), wq, s, b, rhs_indices=inds, bits=4, out_dtype="float32")
     assert_close(to_numpy(g), ref, what="gather views")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,N,K_", [(129, 200, 512), (300, 200, 4096), (256, 4096, 14336 // 4),
+                                    (513, 130, 1024)])
+def test_large_m_tiles_and_split_k(dev, bits, M, N, K_):
+    """The 256 x 128 GEMM: ragged M and N edges, and K split across
+    workgroups (fp32 partials summed in split order) when tiles are few."""
+    rng = np.random.default_rng(M * 31 + N + K_ + bits)
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (N, K_), bits, 64, dev)
+    x = bf16_normal(rng, (M, K_))
+    y = K.quantized_matmul(to_torch(x, dev, BF), tw, ts, tb, bits=bits)
+    ref = O.quantized_matmul(x, wq, s, b, True, 64, bits, "float32")
+    assert_close(to_numpy(y), ref, what=f"M={M}")
