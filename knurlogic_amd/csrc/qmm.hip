@@ -176,10 +176,10 @@ struct Qmm2Args {
 };
 
 template <int BITS, int GS>
-__global__ __launch_bounds__(256, 1) void qmm2_kernel(Qmm2Args a) {
+__global__ __launch_bounds__(512, 1) void qmm2_kernel(Qmm2Args a) {
     constexpr int EPW = 32 / BITS;
-    constexpr int BW = Q2K / 2 / EPW;           // packed words per thread per k-tile (4 or 8)
-    static_assert(GS >= 32, "one scale group per 32-wide half row");
+    constexpr int BQ = Q2K / 4 / EPW;           // packed words per thread per k-tile (2 or 4)
+    static_assert(GS >= 16, "one scale group per 16-wide quarter row");
     __shared__ __align__(16) uint16_t As[2][Q2M * Q2LDS];
     __shared__ __align__(16) uint16_t Bs[2][Q2N * Q2LDS];
 
@@ -191,27 +191,27 @@ __global__ __launch_bounds__(256, 1) void qmm2_kernel(Qmm2Args a) {
     const int kt1 = kt0 + a.kt_per_split < nk ? kt0 + a.kt_per_split : nk;
     const int64_t wpr = a.K / EPW, gpr = a.K / GS;
 
-    // A: thread chunk c = tid + 256 i -> row c / 8, 16-byte piece c % 8
-    // B: thread -> weight row tid / 2, k half tid % 2 (32 values)
-    const int brow = tid >> 1, bhalf = tid & 1;
+    // A: thread chunk c = tid + 512 i -> row c / 8, 16-byte piece c % 8
+    // B: thread -> weight row tid / 4, k quarter tid % 4 (16 values)
+    const int brow = tid >> 2, bq = tid & 3;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + bm * a.K, (a.M - bm) * a.K * 2);
     const int64_t nrows = a.N - bn;
     const __amdgpu_buffer_rsrc_t rwt = make_rsrc(a.w + bn * wpr, nrows * wpr * 4);
     const __amdgpu_buffer_rsrc_t rwz = make_rsrc(a.w, 0);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s + bn * gpr, nrows * gpr * 2);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b + bn * gpr, nrows * gpr * 2);
-    const uint32_t wrow_off = (uint32_t)(brow * wpr * 4 + bhalf * BW * 4);
+    const uint32_t wrow_off = (uint32_t)(brow * wpr * 4 + bq * BQ * 4);
     const uint32_t srow_off = (uint32_t)(brow * gpr * 2);
 
-    u32x4 ra[8];
-    u32x4 rw[Q2_RING][BW / 4];
+    u32x4 ra[4];
+    uint32_t rw[Q2_RING][BQ];
     uint32_t rsc[Q2_RING], rbi[Q2_RING];
 
     auto load_a = [&](int kt) {        // kt past the split: a zero-extent view, no traffic
         const __amdgpu_buffer_rsrc_t r = kt < kt1 ? rx : rwz;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int c = tid + 256 * i;
+        for (int i = 0; i < 4; i++) {
+            const int c = tid + 512 * i;
             const uint32_t off = (uint32_t)(((c >> 3) * a.K + (int64_t)kt * Q2K + (c & 7) * 8) * 2);
             ra[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
         }
@@ -220,40 +220,43 @@ __global__ __launch_bounds__(256, 1) void qmm2_kernel(Qmm2Args a) {
         const bool live = kt < kt1;
         const __amdgpu_buffer_rsrc_t r = live ? rwt : rwz;
         const uint32_t off = wrow_off + (uint32_t)kt * (Q2K / EPW) * 4u;
-#pragma unroll
-        for (int q = 0; q < BW / 4; q++)
-            rw[slot][q] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off + 16u * q), 0, AUX_NT);
-        const uint32_t g = (uint32_t)(((int64_t)kt * Q2K + 32 * bhalf) / GS);
+        if constexpr (BQ == 2) {
+            const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, AUX_NT);
+            rw[slot][0] = v.x; rw[slot][1] = v.y;
+        } else {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_NT);
+            rw[slot][0] = v.x; rw[slot][1] = v.y; rw[slot][2] = v.z; rw[slot][3] = v.w;
+        }
+        const uint32_t g = (uint32_t)(((int64_t)kt * Q2K + 16 * bq) / GS);
         rsc[slot] = __builtin_amdgcn_raw_buffer_load_b16(live ? rs : rwz, (int)(srow_off + 2u * g), 0, 0);
         rbi[slot] = __builtin_amdgcn_raw_buffer_load_b16(live ? rb : rwz, (int)(srow_off + 2u * g), 0, 0);
     };
     auto store = [&](int buf, int slot) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int c = tid + 256 * i;
+        for (int i = 0; i < 4; i++) {
+            const int c = tid + 512 * i;
             *(u32x4*)(&As[buf][(c >> 3) * Q2LDS + (c & 7) * 8]) = ra[i];
         }
         const float sc = bf16_to_f32((uint16_t)rsc[slot]), bi = bf16_to_f32((uint16_t)rbi[slot]);
-        uint32_t ow[16];
+        uint32_t ow[8];
 #pragma unroll
-        for (int e = 0; e < 32; e += 2) {
-            const uint32_t w0 = rw[slot][(e / EPW) / 4][(e / EPW) % 4];
-            const uint32_t w1 = rw[slot][((e + 1) / EPW) / 4][((e + 1) / EPW) % 4];
+        for (int e = 0; e < 16; e += 2) {
+            const uint32_t w0 = rw[slot][e / EPW], w1 = rw[slot][(e + 1) / EPW];
             const float q0 = (float)((w0 >> ((e % EPW) * BITS)) & ((1u << BITS) - 1u));
             const float q1 = (float)((w1 >> (((e + 1) % EPW) * BITS)) & ((1u << BITS) - 1u));
             ow[e / 2] = cvt_pk_bf16(__builtin_fmaf(sc, q0, bi), __builtin_fmaf(sc, q1, bi));
         }
-        uint16_t* dst = &Bs[buf][brow * Q2LDS + 32 * bhalf];
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            *(u32x4*)(dst + 8 * i) = u32x4{ow[4 * i], ow[4 * i + 1], ow[4 * i + 2], ow[4 * i + 3]};
+        uint16_t* dst = &Bs[buf][brow * Q2LDS + 16 * bq];
+        *(u32x4*)dst = u32x4{ow[0], ow[1], ow[2], ow[3]};
+        *(u32x4*)(dst + 8) = u32x4{ow[4], ow[5], ow[6], ow[7]};
     };
 
-    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 64;
+    // 8 waves: 4 along M x 2 along N, each a 64 x 64 tile (4 x 4 MFMA blocks)
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
     const int l16 = lane & 15, lk = lane >> 4;
-    f32x4 acc[8][4];
+    f32x4 acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -273,15 +276,15 @@ __global__ __launch_bounds__(256, 1) void qmm2_kernel(Qmm2Args a) {
                 load_a(t + 1);
 #pragma unroll
                 for (int ks = 0; ks < Q2K / 32; ks++) {
-                    u32x4 af[8], bfr[4];
+                    u32x4 af[4], bfr[4];
 #pragma unroll
-                    for (int i = 0; i < 8; i++)
+                    for (int i = 0; i < 4; i++)
                         af[i] = *(const u32x4*)(&As[buf][(wm + 16 * i + l16) * Q2LDS + ks * 32 + lk * 8]);
 #pragma unroll
                     for (int j = 0; j < 4; j++)
                         bfr[j] = *(const u32x4*)(&Bs[buf][(wn + 16 * j + l16) * Q2LDS + ks * 32 + lk * 8]);
 #pragma unroll
-                    for (int i = 0; i < 8; i++)
+                    for (int i = 0; i < 4; i++)
 #pragma unroll
                         for (int j = 0; j < 4; j++) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
                 }
@@ -295,7 +298,7 @@ __global__ __launch_bounds__(256, 1) void qmm2_kernel(Qmm2Args a) {
 
     // D of block (i, j): row 16 i + 4 lk + r, column 16 j + l16
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int64_t col = bn + wn + 16 * j + l16;
@@ -365,7 +368,7 @@ int qmm_gemm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
         }
         Qmm2Args a = {xx, w, ss, bb, yy, (float*)workspace, M, N, K, p.kt_per_split, p.splits, p.n_tiles};
         const dim3 grid((unsigned)(p.n_tiles * p.m_tiles), (unsigned)p.splits);
-#define KMI_QMM2(B, G) qmm2_kernel<B, G><<<grid, 256, 0, st>>>(a)
+#define KMI_QMM2(B, G) qmm2_kernel<B, G><<<grid, 512, 0, st>>>(a)
         if (bits == 4) {
             if (group_size == 32) KMI_QMM2(4, 32);
             else if (group_size == 64) KMI_QMM2(4, 64);
