@@ -19,6 +19,11 @@ FLAGS = [
 ]
 
 
+# Per-source flags.  qgemv: MFMA results in VGPRs (the FMAs that consume them
+# each group would otherwise copy them out of AGPRs first).
+EXTRA = {"qgemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def sources():
     return sorted(SRC.glob("*.hip"))
 
@@ -41,7 +46,8 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     srcs = sources()
     objs = [objdir / (p.stem + ".o") for p in srcs]
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        errs = list(ex.map(lambda so: _run(["hipcc", *cflags, "-c", str(so[0]), "-o", str(so[1])]),
+        errs = list(ex.map(lambda so: _run(["hipcc", *cflags, *EXTRA.get(so[0].name, []), "-c", str(so[0]),
+                                            "-o", str(so[1])]),
                            zip(srcs, objs)))
     tmp = OUT.with_suffix(".so.tmp")
     errs.append(_run(["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC",

@@ -33,21 +33,32 @@ constexpr int ROUTE_MAX_E = 1024;            // experts a wave holds (16 per lan
 // float64 and rounded once); the k largest probabilities in descending
 // order, equal ones taken lower index first (softmax is monotone, so equal
 // probabilities come only from equal logits); scores = the selected
-// probabilities renormalized (float64, rounded to float32), then rounded to
-// the logits' dtype.
+// probabilities renormalized (float64, summed in selection order, rounded to
+// float32), then rounded to the logits' dtype.
+//
+// Selection is by rank, with no serial rounds: probabilities are >= 0, so
+// their float32 bits order like the values, and key = bits << 32 | ~expert
+// orders exactly as the selection does (larger p first, then lower expert)
+// with no two keys equal.  Each lane counts the wave's keys above its own
+// (broadcast LDS reads, one 64-bit compare each); rank < k is selected, at
+// slot rank.
 template <class T, int ROUTE_PER_LANE>
 __global__ __launch_bounds__(256) void moe_route_kernel(const void* __restrict__ logits, int64_t T_, int E,
                                                         int k, int32_t* __restrict__ inds,
                                                         void* __restrict__ scores) {
-    const int lane = threadIdx.x & 63;
-    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= T_) return;
+    constexpr int EP = 64 * ROUTE_PER_LANE;             // keys per wave, padded
+    __shared__ uint64_t keys[4][EP];
+    __shared__ float selp[4][64];
+    __shared__ int sele[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t t = (int64_t)blockIdx.x * 4 + w;
+    const bool live = t < T_;                            // a whole wave is live or not
     float lg[ROUTE_PER_LANE];
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < ROUTE_PER_LANE; j++) {
         const int e = lane + 64 * j;
-        lg[j] = e < E ? ld_dt<T>(logits, t * E + e) : -INFINITY;
+        lg[j] = live && e < E ? ld_dt<T>(logits, t * E + e) : -INFINITY;
         mx = fmaxf(mx, lg[j]);
     }
 #pragma unroll
@@ -62,34 +73,40 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const void* __restrict__
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
     float p[ROUTE_PER_LANE];
+    uint64_t key[ROUTE_PER_LANE];
 #pragma unroll
-    for (int j = 0; j < ROUTE_PER_LANE; j++) p[j] = lane + 64 * j < E ? f64_to_f32(ex[j] / sum) : -1.f;
-
-    double top_sum = 0.0;
-    float top_p = 0.f;       // lane s keeps the s-th selection
-    int top_e = 0;
-    for (int s = 0; s < k; s++) {
-        // this lane's best (largest p, then lowest expert)
-        float bp = -2.f;
-        int be = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < ROUTE_PER_LANE; j++)
-            if (p[j] > bp) { bp = p[j]; be = lane + 64 * j; }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float op = __shfl_xor(bp, o, 64);
-            const int oe = __shfl_xor(be, o, 64);
-            if (op > bp || (op == bp && oe < be)) { bp = op; be = oe; }
-        }
-        top_sum += (double)bp;
-        if (lane == s) { top_p = bp; top_e = be; }
-#pragma unroll
-        for (int j = 0; j < ROUTE_PER_LANE; j++)
-            if (lane + 64 * j == be) p[j] = -1.f;
+    for (int j = 0; j < ROUTE_PER_LANE; j++) {
+        const int e = lane + 64 * j;
+        p[j] = e < E ? f64_to_f32(ex[j] / sum) : 0.f;
+        // padding lanes get key 0, below every expert's key (its low word ~e > 0)
+        key[j] = e < E ? ((uint64_t)__float_as_uint(p[j]) << 32) | (uint32_t)~e : 0ull;
+        keys[w][e] = key[j];
     }
-    if (lane < k) {
-        inds[t * k + lane] = top_e;
-        st_dt<T>(scores, t * k + lane, f64_to_f32((double)top_p / top_sum));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int rank[ROUTE_PER_LANE];
+#pragma unroll
+    for (int j = 0; j < ROUTE_PER_LANE; j++) rank[j] = 0;
+    for (int i = 0; i < EP; i += 2) {
+        const uint64_t a = keys[w][i], b = keys[w][i + 1];
+#pragma unroll
+        for (int j = 0; j < ROUTE_PER_LANE; j++) rank[j] += (int)(a > key[j]) + (int)(b > key[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < ROUTE_PER_LANE; j++)
+        if (lane + 64 * j < E && rank[j] < k) {
+            selp[w][rank[j]] = p[j];
+            sele[w][rank[j]] = lane + 64 * j;
+        }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    double top_sum = 0.0;
+    for (int s2 = 0; s2 < k; s2++) top_sum += (double)selp[w][s2];
+    if (live && lane < k) {
+        inds[t * k + lane] = sele[w][lane];
+        st_dt<T>(scores, t * k + lane, f64_to_f32((double)selp[w][lane] / top_sum));
     }
 }
 

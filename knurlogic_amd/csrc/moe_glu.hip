@@ -5,45 +5,42 @@
 // architecture/qwen3_5.py:108-112,181-182).
 //
 // Up to TOK_MAX_PAIRS (token, slot) pairs run token-major (moe_tok.hip: two
-// kernels, no sort); more pairs group rows by expert (gather_qmm for the
-// gate|up and down projections, the SwiGLU and combine kernels between).
+// kernels, no sort).  More pairs are grouped by expert on the GPU once, and
+// both projections run over the same tiles (qgemv.hip), so each routed
+// expert's weights are read once per call: gate|up with the SwiGLU
+// epilogue, then down, then the weighted combine.
 #include "moe_tok.hpp"
+#include "qgemv.hpp"
 #include "../../include/knurlogic_amd.h"
 
 namespace kmi {
 
 
 
-constexpr int64_t TOK_MAX_PAIRS = 256;
-
-__global__ void pair_indices(int32_t* __restrict__ tok, int32_t* __restrict__ pair, int64_t P, int k) {
-    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p < P) {
-        tok[p] = (int32_t)(p / k);
-        pair[p] = (int32_t)p;
-    }
-}
+constexpr int64_t TOK_MAX_PAIRS = 16;
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct GluPlan {
     bool tok;
-    size_t act, y, gu, idx, g1, g2, total;
+    int tm;
+    size_t act, y, idx, total;
 };
 
-static GluPlan plan_glu(int64_t T, int64_t H, int64_t I, int k, int64_t E, int gs, int bits) {
+// rows per tile: the average routed pairs per active expert, in 16-row chunks
+static GluPlan plan_glu(int64_t T, int64_t H, int64_t I, int k, int64_t E) {
     GluPlan p = {};
     const int64_t P = T * k;
     p.tok = P <= TOK_MAX_PAIRS;
     p.act = align256((size_t)P * I * 2);
     if (!p.tok) {
+        const int64_t active = P < E ? P : E;
+        const int64_t rpt = ceil_div(P, active);
+        p.tm = rpt <= 16 ? 16 : rpt <= 32 ? 32 : 64;
         p.y = align256((size_t)P * H * 2);
-        p.gu = align256((size_t)P * 2 * I * 2);
-        p.idx = align256((size_t)P * 4 * 2);
-        p.g1 = align256(kmi_gather_qmm_workspace_bytes(P, 1, E, H, 2 * I, gs, bits));
-        p.g2 = align256(kmi_gather_qmm_workspace_bytes(P, 1, E, I, H, gs, bits));
+        p.idx = sort_index_bytes(P, E, p.tm);
     }
-    p.total = p.act + p.y + p.gu + p.idx + (p.g1 > p.g2 ? p.g1 : p.g2);
+    p.total = p.act + p.y + p.idx;
     return p;
 }
 
@@ -56,7 +53,8 @@ extern "C" {
 size_t kmi_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k, int64_t E,
                                       int group_size, int bits) {
     if (T <= 0 || H <= 0 || I <= 0 || k <= 0 || E <= 0) return 0;
-    return plan_glu(T, H, I, k, E, group_size, bits).total;
+    (void)group_size; (void)bits;
+    return plan_glu(T, H, I, k, E).total;
 }
 
 int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
@@ -80,7 +78,10 @@ int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const 
     const int epw = 32 / bits;
     KMI_CHECK_ARG(E * 2 * I * (H / epw) * 4 < (1LL << 31) && E * H * (I / epw) * 4 < (1LL << 31),
                   "switch_glu: expert weights past 2 GiB");
-    const GluPlan p = plan_glu(T, H, I, k, E, group_size, bits);
+    KMI_CHECK_ARG(E <= 4096, "switch_glu: %lld experts (at most 4096)", (long long)E);
+    KMI_CHECK_ARG(T * H * 2 < (1LL << 31) && T * k * (H > I ? H : I) * 2 < (1LL << 31),
+                  "switch_glu: activations past 2 GiB");
+    const GluPlan p = plan_glu(T, H, I, k, E);
     if (!workspace || workspace_bytes < p.total) {
         set_error("switch_glu: workspace of %zu bytes needed, %zu given", p.total, workspace_bytes);
         return EWORKSPACE;
@@ -110,24 +111,30 @@ int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const 
         KMI_CHECK_LAUNCH("moe_down_tok");
         return OK;
     }
-    // grouped by expert: gate|up gather, SwiGLU, down gather, combine
-    uint16_t* y = (uint16_t*)(ws + p.act);
-    uint16_t* gu = (uint16_t*)(ws + p.act + p.y);                       // [P, 2I]
-    int32_t* tok = (int32_t*)(ws + p.act + p.y + p.gu);
-    int32_t* pair = tok + P;
-    void* gws = ws + p.act + p.y + p.gu + p.idx;
-    const size_t gbytes = p.g1 > p.g2 ? p.g1 : p.g2;
-    pair_indices<<<(unsigned)ceil_div(P, 256), 256, 0, st>>>(tok, pair, P, k);
-    KMI_CHECK_LAUNCH("pair_indices");
-    int rc = kmi_gather_qmm(x, T, 1, H, w_gu, s_gu, b_gu, E, 2 * I, tok, inds, P, dtype, group_size,
-                            bits, 0, gu, gws, gbytes, stream);
+    // grouped by expert: one sort, gate|up + SwiGLU, down, combine
+    uint16_t* y = scores ? (uint16_t*)(ws + p.act) : (uint16_t*)out;    // [P, H]
+    SortedRows sr;
+    int rc = launch_sort_rows(inds, P, 1, (int)E, p.tm, ws + p.act + p.y, y, H, st, &sr);
     if (rc) return rc;
-    rc = kmi_swiglu(gu, gu + I, 2 * I, dtype, P, I, act, stream);
+    QgArgs g = {};
+    g.x = (const uint16_t*)x; g.xrows = T; g.w = w_gu; g.s = (const uint16_t*)s_gu;
+    g.b = (const uint16_t*)b_gu; g.E = E; g.N = I; g.K = H; g.erows = 2 * I; g.up_off = I;
+    g.y = act; g.rows = P; g.tm = p.tm; g.tiles = sr.tiles; g.sorted = sr.sorted; g.lhs = nullptr;
+    g.lhs_div = k; g.Mper = 1;
+    const QgPlan pg = plan_qgemv_unsplit(I, H, sr.max_tiles, p.tm, group_size);
+    g.S = 1; g.gps = pg.gps;
+    rc = launch_qgemv(g, pg, bits, group_size, true, sr.max_tiles, st);
     if (rc) return rc;
-    uint16_t* yd = scores ? y : (uint16_t*)out;
-    rc = kmi_gather_qmm(act, P, 1, I, w_down, s_down, b_down, E, H, pair, inds, P, dtype, group_size,
-                        bits, 0, yd, gws, gbytes, stream);
+    KMI_CHECK_LAUNCH("qgemv(gate|up)");
+    QgArgs d = {};
+    d.x = act; d.xrows = P; d.w = w_down; d.s = (const uint16_t*)s_down; d.b = (const uint16_t*)b_down;
+    d.E = E; d.N = H; d.K = I; d.erows = H; d.y = y; d.rows = P; d.tm = p.tm; d.tiles = sr.tiles;
+    d.sorted = sr.sorted; d.lhs = nullptr; d.lhs_div = 1; d.Mper = 1;
+    const QgPlan pd = plan_qgemv_unsplit(H, I, sr.max_tiles, p.tm, group_size);
+    d.S = 1; d.gps = pd.gps;
+    rc = launch_qgemv(d, pd, bits, group_size, false, sr.max_tiles, st);
     if (rc) return rc;
+    KMI_CHECK_LAUNCH("qgemv(down)");
     if (scores) return kmi_moe_combine(y, scores, dtype, T, k, H, out, stream);
     return OK;
 }

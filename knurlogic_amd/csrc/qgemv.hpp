@@ -1,0 +1,67 @@
+// Arguments and launcher of the skinny quantized matmul (qgemv.hip): up to
+// 64 activation rows per weight (dense) or per routed expert (gather).
+#pragma once
+
+#include "common.hpp"
+
+namespace kmi {
+
+struct QgArgs {
+    const uint16_t* x;          // activations, bf16 [xrows, K]
+    int64_t xrows;
+    const uint32_t* w;          // [E, erows, K*bits/32]
+    const uint16_t* s;          // [E, erows, K/gs]
+    const uint16_t* b;          // [E, erows, K/gs]
+    int64_t E, N, K;
+    int64_t erows;              // rows from one expert to the next (N; 2I for a stacked gate|up)
+    int64_t up_off;             // GLU: row of the first up row within an expert
+    uint16_t* y;                // [rows, N] bf16, when S == 1
+    float* partial;             // [S, rows, N] fp32, when S > 1
+    int64_t rows;               // rows of y
+    int S;                      // K splits (grid y)
+    int gps;                    // K chunks (256 codes) per split
+    // dense: tiles == null, tile z = rows [tm*z, tm*z + tm)
+    int tm;
+    // gather: tile z = tiles[z] = (expert, start, count) over `sorted`; x row of
+    // row id r: p = r / Mper, (lhs ? lhs[p] : p / lhs_div) * Mper + r % Mper
+    const int32_t* tiles;
+    const int32_t* sorted;
+    const int32_t* lhs;
+    int64_t lhs_div;
+    int64_t Mper;
+};
+
+// Launch shape: 64 weight rows per workgroup (16 per wave), K in chunks of
+// 256 codes, S splits of gps chunks each.
+struct QgPlan {
+    int mc;        // 16-row activation chunks per tile (1, 2 or 4)
+    int S;         // K splits
+    int gps;       // chunks per split
+};
+
+QgPlan plan_qgemv(int64_t N, int64_t K, int64_t tiles, int tile_rows, int gs);
+// the same plan with K unsplit (the SwiGLU epilogue needs whole sums)
+QgPlan plan_qgemv_unsplit(int64_t N, int64_t K, int64_t tiles, int tile_rows, int gs);
+
+// Rows grouped by expert on the GPU (qmv.hip): the index part of a workspace
+// holds sorted row ids [rows], tiles [max_tiles][3] (expert, start, count)
+// and expert offsets [E+1].
+struct SortedRows {
+    int32_t* sorted;
+    int32_t* tiles;
+    int32_t* offsets;
+    int64_t max_tiles;
+};
+
+int64_t sort_max_tiles(int64_t rows, int64_t E, int tm);
+size_t sort_index_bytes(int64_t rows, int64_t E, int tm);     // a multiple of 256
+// rows r = p*Mper + m of the P pairs, grouped by expert rhs[p] into tiles of
+// <= tm rows; rows of out-of-range experts are zeroed in y ([rows, N]) if y
+int launch_sort_rows(const int32_t* rhs, int64_t P, int64_t Mper, int E, int tm, void* index_ws,
+                     uint16_t* y, int64_t N, hipStream_t st, SortedRows* out);
+
+// glu: gate rows at 0, up rows at a.up_off, out = SwiGLU(gate, up) in bf16
+int launch_qgemv(const QgArgs& a, const QgPlan& p, int bits, int gs, bool glu, int64_t ntiles,
+                 hipStream_t st);
+
+}  // namespace kmi

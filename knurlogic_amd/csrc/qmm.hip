@@ -221,10 +221,10 @@ __global__ __launch_bounds__(512, 1) void qmm2_kernel(Qmm2Args a) {
         const __amdgpu_buffer_rsrc_t r = live ? rwt : rwz;
         const uint32_t off = wrow_off + (uint32_t)kt * (Q2K / EPW) * 4u;
         if constexpr (BQ == 2) {
-            const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, AUX_NT);
+            const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
             rw[slot][0] = v.x; rw[slot][1] = v.y;
         } else {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX_NT);
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
             rw[slot][0] = v.x; rw[slot][1] = v.y; rw[slot][2] = v.z; rw[slot][3] = v.w;
         }
         const uint32_t g = (uint32_t)(((int64_t)kt * Q2K + 16 * bq) / GS);
@@ -264,8 +264,9 @@ __global__ __launch_bounds__(512, 1) void qmm2_kernel(Qmm2Args a) {
     for (int r = 0; r < Q2_RING; r++) load_b(r, kt0 + r);
     load_a(kt0);
     store(0, 0);
-    load_b(0, kt0 + Q2_RING);
     __syncthreads();
+    load_a(kt0 + 1);
+    load_b(0, kt0 + Q2_RING);
 
     for (int kb = kt0; kb < kt1; kb += Q2_RING) {
 #pragma unroll
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(512, 1) void qmm2_kernel(Qmm2Args a) {
             const int t = kb + u;
             if (t < kt1) {
                 const int buf = (t - kt0) & 1;
-                load_a(t + 1);
+                const int ns = (u + 1) % Q2_RING;        // ring slot of tile t + 1
 #pragma unroll
                 for (int ks = 0; ks < Q2K / 32; ks++) {
                     u32x4 af[4], bfr[4];
@@ -287,11 +288,15 @@ __global__ __launch_bounds__(512, 1) void qmm2_kernel(Qmm2Args a) {
                     for (int i = 0; i < 4; i++)
 #pragma unroll
                         for (int j = 0; j < 4; j++) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
+                    // the next tile's store (its data arrived a tile ago; buf ^ 1 is free
+                    // since the last barrier) runs while these MFMAs execute
+                    if (ks == 0 && t + 1 < kt1) store(buf ^ 1, ns);
                 }
-                const int ns = (u + 1) % Q2_RING;        // ring slot of tile t + 1
-                if (t + 1 < kt1) store(buf ^ 1, ns);
-                load_b(ns, t + 1 + Q2_RING);
                 __syncthreads();
+                // x of tile t + 2 before the ring refill: waiting on it at the next
+                // store then leaves the younger ring loads in flight
+                load_a(t + 2);
+                load_b(ns, t + 1 + Q2_RING);
             }
         }
     }

@@ -100,7 +100,7 @@ def _experts(rng, E, H, I, dev, bits=4):
                                        (100, 16, 256, 128, 4), (1, 128, 2048, 768, 8),
                                        (16, 128, 2048, 768, 8), (40, 128, 2048, 768, 8)])
 def test_switch_glu_matches_the_oracle(dev, T, E, H, I, k, bits):
-    """One library call (token-major up to 256 (token, slot) pairs, grouped by
+    """One library call (token-major up to 16 (token, slot) pairs, grouped by
     expert above), the separate gather_qmm path, and the fused combine."""
     rng = np.random.default_rng(T * 7 + E + bits)
     glu, fns = _experts(rng, E, H, I, dev, bits)

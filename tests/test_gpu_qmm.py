@@ -24,7 +24,7 @@ def _weights(rng, shape, bits, group, dev):
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("group", [32, 64, 128])
-@pytest.mark.parametrize("M", [1, 3, 16, 17, 64, 200])
+@pytest.mark.parametrize("M", [1, 2, 3, 16, 17, 33, 48, 64, 200])
 def test_qmm_small(dev, bits, group, M):
     rng = np.random.default_rng(1000 * bits + group + M)
     N, K_ = 320, 512
@@ -63,18 +63,20 @@ def test_qmm_baseline_shapes(dev, bits, M, shape):
 def test_rows_are_independent_bit_for_bit(dev):
     """Row m of a call depends only on row m (the reference's padding
     contract, tests/engine/test_per_chip_rounding.py:30-41): within each
-    kernel family a row's bits do not change with the other rows."""
+    kernel family (as in mlx, where qmv and qmm differ) a row's bits do not
+    change with the number of other rows."""
     rng = np.random.default_rng(11)
     (wq, s, b), (tw, ts, tb) = _weights(rng, (256, 512), 4, 64, dev)
-    x = to_torch(bf16_normal(rng, (16, 512)), dev, BF)
-    y16 = K.quantized_matmul(x, tw, ts, tb, True, 64, 4)
-    for m in (1, 5, 9):
+    x = to_torch(bf16_normal(rng, (128, 512)), dev, BF)
+    # skinny MFMA kernel: 2..64 rows (16-, 32- and 64-row tiles)
+    y64 = K.quantized_matmul(x[:64], tw, ts, tb, True, 64, 4)
+    for m in (2, 5, 9, 16, 17, 31, 40):
         ym = K.quantized_matmul(x[:m], tw, ts, tb, True, 64, 4)
-        assert torch.equal(ym, y16[:m])
-    x64 = to_torch(bf16_normal(rng, (96, 512)), dev, BF)
-    y96 = K.quantized_matmul(x64, tw, ts, tb, True, 64, 4)
-    y40 = K.quantized_matmul(x64[:40], tw, ts, tb, True, 64, 4)
-    assert torch.equal(y40, y96[:40])
+        assert torch.equal(ym, y64[:m]), m
+    # GEMM: 65..128 rows
+    y128 = K.quantized_matmul(x, tw, ts, tb, True, 64, 4)
+    y96 = K.quantized_matmul(x[:96], tw, ts, tb, True, 64, 4)
+    assert torch.equal(y96, y128[:96])
 
 
 def test_linearity_at_full_size(dev):
@@ -133,6 +135,33 @@ def test_gather_qmm_unsorted_and_sorted(dev, T, k, bits):
                       sorted_indices=True)
     assert ys.shape == (T * k, 1, N)
     assert_close(to_numpy(ys)[np.argsort(order)].reshape(T, k, 1, N), ref, what="sorted")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,N,K_", [(16, 32, 8192), (5, 48, 16384)])
+def test_long_k_few_rows_splits_k(dev, bits, M, N, K_):
+    """Few weight rows and a long K: the skinny kernel splits K across
+    workgroups and the fp32 partials are summed in split order."""
+    rng = np.random.default_rng(M + N + bits)
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (N, K_), bits, 64, dev)
+    x = bf16_normal(rng, (M, K_))
+    y = K.quantized_matmul(to_torch(x, dev, BF), tw, ts, tb, True, 64, bits)
+    ref = O.quantized_matmul(x, wq, s, b, True, 64, bits, "float32")
+    assert_close(to_numpy(y), ref, what=f"split K M={M} K={K_}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_many_rows_per_expert(dev, bits):
+    """~100 rows per expert: 64-row tiles, several per expert, and a ragged last tile."""
+    rng = np.random.default_rng(31 + bits)
+    E, N, K_, T, k = 4, 80, 384, 200, 2
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (E, N, K_), bits, 64, dev)
+    x = bf16_normal(rng, (T, 1, 1, K_))
+    inds = rng.integers(0, E, (T, k)).astype(np.int32)
+    y = K.gather_qmm(to_torch(x, dev, BF), tw, ts, tb, rhs_indices=torch.from_numpy(inds).to(dev),
+                     bits=bits)
+    ref = O.gather_qmm(x, wq, s, b, rhs_indices=inds, bits=bits, out_dtype="float32")
+    assert_close(to_numpy(y), ref, what="many rows per expert")
 
 
 def test_gather_qmm_with_lhs_indices_and_bad_experts(dev):
