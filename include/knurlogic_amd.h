@@ -225,6 +225,26 @@ int kmi_vq_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int3
                const void* codes_up, const void* scales_up, const void* codebook_up, int code_bytes,
                int kc, int dim, int scale_group, int64_t E, int dtype, void* act, void* stream);
 
+/*
+ * VQ SwitchGLU in one call (switch_layers.py:172-193 over VQSwitchLinear,
+ * with qwen3_5.py's _SwiGLU and the SparseMoeBlock combine at
+ * qwen3_5.py:181-182): act = the gate/up projections with the SwiGLU
+ * epilogue (as kmi_vq_glu), then the down projection per (token, slot) and,
+ * when scores [T, k] bf16 is given, the weighted combine
+ *   out[t, :] = round(sum_s round(y[t, s, :] * scores[t, s]))  (out [T, H])
+ * (as kmi_moe_combine), else out = y [T*k, H].  codes_down [E, H, I/8]; all
+ * three projections share code_bytes, kc, dim and scale_group.
+ * workspace: kmi_vq_switch_glu_workspace_bytes(T, H, I, k) bytes.
+ */
+size_t kmi_vq_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k);
+int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                      const void* scores, const void* codes_gate, const void* scales_gate,
+                      const void* codebook_gate, const void* codes_up, const void* scales_up,
+                      const void* codebook_up, const void* codes_down, const void* scales_down,
+                      const void* codebook_down, int code_bytes, int kc, int dim, int scale_group,
+                      int64_t E, int dtype, void* out, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,7 +36,7 @@ static GluPlan plan_glu(int64_t T, int64_t H, int64_t I, int k, int64_t E) {
     if (!p.tok) {
         const int64_t active = P < E ? P : E;
         const int64_t rpt = ceil_div(P, active);
-        p.tm = rpt <= 16 ? 16 : rpt <= 32 ? 32 : 64;
+        p.tm = qgemv_gather_tile_rows(rpt);
         p.y = align256((size_t)P * H * 2);
         p.idx = sort_index_bytes(P, E, p.tm);
     }

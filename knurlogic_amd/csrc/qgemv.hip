@@ -355,6 +355,12 @@ QgPlan plan_qgemv(int64_t N, int64_t K, int64_t tiles, int tile_rows, int gs) {
     return p;
 }
 
+int qgemv_gather_tile_rows(int64_t avg_rows) {
+    // routed rows per expert spread around their mean (roughly binomial), so
+    // the tile covers about 1.5x the mean
+    return avg_rows <= 10 ? 16 : avg_rows <= 20 ? 32 : 64;
+}
+
 QgPlan plan_qgemv_unsplit(int64_t N, int64_t K, int64_t tiles, int tile_rows, int gs) {
     QgPlan p = plan_qgemv(N, K, tiles, tile_rows, gs);
     p.S = 1;

@@ -40,6 +40,9 @@ struct QgPlan {
 };
 
 QgPlan plan_qgemv(int64_t N, int64_t K, int64_t tiles, int tile_rows, int gs);
+// tile rows (16, 32, 64) for rows grouped by expert, from the average routed
+// rows per active expert: large enough that most experts take one tile
+int qgemv_gather_tile_rows(int64_t avg_rows);
 // the same plan with K unsplit (the SwiGLU epilogue needs whole sums)
 QgPlan plan_qgemv_unsplit(int64_t N, int64_t K, int64_t tiles, int tile_rows, int gs);
 

@@ -345,7 +345,7 @@ size_t kmi_gather_qmm_workspace_bytes(int64_t P, int64_t M, int64_t E, int64_t K
         return 0;
     const int64_t rpt = gather_rows_per_tile(P, M, E);
     const QmvKind kind = choose_kind(rpt, K, N, P * M, bits, group_size);
-    const int tm = kind == QmvKind::SKINNY ? skinny_tile_rows(rpt) : tile_rows(kind);
+    const int tm = kind == QmvKind::SKINNY ? qgemv_gather_tile_rows(rpt) : tile_rows(kind);
     size_t b = sort_index_bytes(P * M, E, tm);
     if (kind == QmvKind::SKINNY)
         b += skinny_partial_bytes(plan_qgemv(N, K, sort_max_tiles(P * M, E, tm), tm, group_size), P * M, N);
@@ -370,7 +370,7 @@ int kmi_gather_qmm(const void* x, int64_t X, int64_t M, int64_t K, const uint32_
     KMI_CHECK_ARG(x && w && scales && biases && y && lhs && rhs, "gather_qmm: null pointer");
     const int64_t rpt = gather_rows_per_tile(P, M, E);
     const QmvKind kind = choose_kind(rpt, K, N, P * M, bits, group_size);
-    const int tm = kind == QmvKind::SKINNY ? skinny_tile_rows(rpt) : tile_rows(kind);
+    const int tm = kind == QmvKind::SKINNY ? qgemv_gather_tile_rows(rpt) : tile_rows(kind);
     const size_t need = kmi_gather_qmm_workspace_bytes(P, M, E, K, N, group_size, bits);
     if (workspace == nullptr || workspace_bytes < need) {
         set_error("gather_qmm: workspace of %zu bytes needed, %zu given", need, workspace_bytes);

@@ -180,25 +180,31 @@ __global__ __launch_bounds__(256) void vq_gemv(VqArgs a) {
 }
 
 // Lanes per row and codes per lane for a row of K elements: the widest SEG in
-// {8, 4, 2} whose segments hold whole scale groups and whole 32-bit words.
-static bool vq_shape(int64_t K, int sgc, int code_bytes, int& seg, int& cps) {
+// {8, 4, 2} whose segments hold whole scale groups and whole 32-bit words,
+// widened (up to 64 lanes, a row per wave) while the grid of `rows` rows
+// would leave fewer than 1024 workgroups: shorter gather chains per lane.
+// Only for small codebooks: every workgroup stages the whole codebook, and
+// at 4096 entries (64 KB) fewer rows per workgroup cost more than they save.
+static bool vq_shape(int64_t K, int sgc, int code_bytes, int64_t rows, int kc, int& seg, int& cps) {
     const int64_t cpr = K / 8;
-    for (int s = 8; s >= 2; s >>= 1) {
-        if (cpr % s) continue;
+    auto valid = [&](int s) {
+        if (cpr % s) return false;
         const int64_t c = cpr / s;
-        if (sgc && c % sgc) continue;
-        if ((c * code_bytes) % 4) continue;
-        seg = s;
-        cps = (int)c;
-        return true;
-    }
-    return false;
+        return !(sgc && c % sgc) && (c * code_bytes) % 4 == 0;
+    };
+    seg = 0;
+    for (int s = 8; s >= 2; s >>= 1)
+        if (valid(s)) { seg = s; break; }
+    if (!seg) return false;
+    while (kc <= 256 && seg < 64 && rows / (256 / seg) < 1024 && valid(seg * 2)) seg *= 2;
+    cps = (int)(cpr / seg);
+    return true;
 }
 
 static int launch_vq(const VqArgs& a, int code_bytes, int nset, hipStream_t st) {
     const int sgc = a.sg >= a.K ? 0 : a.sg / 8;
     int seg = 0, cps = 0;
-    if (!vq_shape(a.K, sgc, code_bytes, seg, cps)) {
+    if (!vq_shape(a.K, sgc, code_bytes, a.N * a.P, a.kc, seg, cps)) {
         set_error("vq: K=%lld with scale group %d has no lane layout", (long long)a.K, a.sg);
         return EINVAL_ARG;
     }
@@ -220,41 +226,132 @@ static int launch_vq(const VqArgs& a, int code_bytes, int nset, hipStream_t st) 
         vq_gemv<CB_, SEG_, CPS_, SGC_, NS_><<<grid, 256, lds, st>>>(a);                           \
         return OK;                                                                                \
     }
-    // (index bytes, lanes per row, codes per lane, codes per scale group, row sets)
-    KMI_VQ(1, 2, 8, 8, 1) KMI_VQ(1, 2, 8, 8, 2)   /* K = 128 */
-    KMI_VQ(1, 2, 44, 0, 1) KMI_VQ(1, 2, 44, 0, 2)   /* K = 704 */
-    KMI_VQ(1, 4, 4, 0, 1) KMI_VQ(1, 4, 4, 0, 2)   /* K = 128 */
-    KMI_VQ(1, 4, 8, 8, 1) KMI_VQ(1, 4, 8, 8, 2)   /* K = 256 */
-    KMI_VQ(1, 4, 24, 8, 1) KMI_VQ(1, 4, 24, 8, 2)   /* K = 768 */
-    KMI_VQ(1, 4, 88, 8, 1) KMI_VQ(1, 4, 88, 8, 2)   /* K = 2816 */
-    KMI_VQ(1, 8, 4, 0, 1) KMI_VQ(1, 8, 4, 0, 2)   /* K = 256 */
-    KMI_VQ(1, 8, 8, 0, 1) KMI_VQ(1, 8, 8, 0, 2)   /* K = 512 */
-    KMI_VQ(1, 8, 8, 8, 1) KMI_VQ(1, 8, 8, 8, 2)   /* K = 512 */
-    KMI_VQ(1, 8, 12, 0, 1) KMI_VQ(1, 8, 12, 0, 2)   /* K = 768 */
-    KMI_VQ(1, 8, 16, 0, 1) KMI_VQ(1, 8, 16, 0, 2)   /* K = 1024 */
-    KMI_VQ(1, 8, 16, 8, 1) KMI_VQ(1, 8, 16, 8, 2)   /* K = 1024 */
-    KMI_VQ(1, 8, 32, 0, 1) KMI_VQ(1, 8, 32, 0, 2)   /* K = 2048 */
-    KMI_VQ(1, 8, 32, 8, 1) KMI_VQ(1, 8, 32, 8, 2)   /* K = 2048 */
-    KMI_VQ(1, 8, 44, 0, 1) KMI_VQ(1, 8, 44, 0, 2)   /* K = 2816 */
-    KMI_VQ(1, 8, 64, 0, 1) KMI_VQ(1, 8, 64, 0, 2)   /* K = 4096 */
-    KMI_VQ(1, 8, 64, 8, 1) KMI_VQ(1, 8, 64, 8, 2)   /* K = 4096 */
-    KMI_VQ(2, 2, 8, 8, 1) KMI_VQ(2, 2, 8, 8, 2)   /* K = 128 */
-    KMI_VQ(2, 4, 8, 8, 1) KMI_VQ(2, 4, 8, 8, 2)   /* K = 256 */
-    KMI_VQ(2, 4, 22, 0, 1) KMI_VQ(2, 4, 22, 0, 2)   /* K = 704 */
-    KMI_VQ(2, 4, 24, 8, 1) KMI_VQ(2, 4, 24, 8, 2)   /* K = 768 */
-    KMI_VQ(2, 4, 88, 8, 1) KMI_VQ(2, 4, 88, 8, 2)   /* K = 2816 */
-    KMI_VQ(2, 8, 2, 0, 1) KMI_VQ(2, 8, 2, 0, 2)   /* K = 128 */
-    KMI_VQ(2, 8, 4, 0, 1) KMI_VQ(2, 8, 4, 0, 2)   /* K = 256 */
-    KMI_VQ(2, 8, 8, 0, 1) KMI_VQ(2, 8, 8, 0, 2)   /* K = 512 */
-    KMI_VQ(2, 8, 8, 8, 1) KMI_VQ(2, 8, 8, 8, 2)   /* K = 512 */
-    KMI_VQ(2, 8, 12, 0, 1) KMI_VQ(2, 8, 12, 0, 2)   /* K = 768 */
-    KMI_VQ(2, 8, 16, 0, 1) KMI_VQ(2, 8, 16, 0, 2)   /* K = 1024 */
-    KMI_VQ(2, 8, 16, 8, 1) KMI_VQ(2, 8, 16, 8, 2)   /* K = 1024 */
-    KMI_VQ(2, 8, 32, 0, 1) KMI_VQ(2, 8, 32, 0, 2)   /* K = 2048 */
-    KMI_VQ(2, 8, 32, 8, 1) KMI_VQ(2, 8, 32, 8, 2)   /* K = 2048 */
-    KMI_VQ(2, 8, 44, 0, 1) KMI_VQ(2, 8, 44, 0, 2)   /* K = 2816 */
-    KMI_VQ(2, 8, 64, 0, 1) KMI_VQ(2, 8, 64, 0, 2)   /* K = 4096 */
-    KMI_VQ(2, 8, 64, 8, 1) KMI_VQ(2, 8, 64, 8, 2)   /* K = 4096 */
+#define KMI_VQ2(CB_, SEG_, CPS_, SGC_) KMI_VQ(CB_, SEG_, CPS_, SGC_, 1) KMI_VQ(CB_, SEG_, CPS_, SGC_, 2)
+    // (index bytes, lanes per row, codes per lane, codes per scale group)
+    KMI_VQ2(1, 2, 8, 0)   /* K = 128 */
+    KMI_VQ2(1, 4, 4, 0)   /* K = 128 */
+    KMI_VQ2(1, 2, 8, 8)   /* K = 128 */
+    KMI_VQ2(1, 2, 16, 0)   /* K = 256 */
+    KMI_VQ2(1, 4, 8, 0)   /* K = 256 */
+    KMI_VQ2(1, 8, 4, 0)   /* K = 256 */
+    KMI_VQ2(1, 2, 16, 8)   /* K = 256 */
+    KMI_VQ2(1, 4, 8, 8)   /* K = 256 */
+    KMI_VQ2(1, 2, 32, 0)   /* K = 512 */
+    KMI_VQ2(1, 4, 16, 0)   /* K = 512 */
+    KMI_VQ2(1, 8, 8, 0)   /* K = 512 */
+    KMI_VQ2(1, 16, 4, 0)   /* K = 512 */
+    KMI_VQ2(1, 2, 32, 8)   /* K = 512 */
+    KMI_VQ2(1, 4, 16, 8)   /* K = 512 */
+    KMI_VQ2(1, 8, 8, 8)   /* K = 512 */
+    KMI_VQ2(1, 2, 44, 0)   /* K = 704 */
+    KMI_VQ2(1, 2, 48, 0)   /* K = 768 */
+    KMI_VQ2(1, 4, 24, 0)   /* K = 768 */
+    KMI_VQ2(1, 8, 12, 0)   /* K = 768 */
+    KMI_VQ2(1, 2, 48, 8)   /* K = 768 */
+    KMI_VQ2(1, 4, 24, 8)   /* K = 768 */
+    KMI_VQ2(1, 2, 64, 0)   /* K = 1024 */
+    KMI_VQ2(1, 4, 32, 0)   /* K = 1024 */
+    KMI_VQ2(1, 8, 16, 0)   /* K = 1024 */
+    KMI_VQ2(1, 16, 8, 0)   /* K = 1024 */
+    KMI_VQ2(1, 32, 4, 0)   /* K = 1024 */
+    KMI_VQ2(1, 2, 64, 8)   /* K = 1024 */
+    KMI_VQ2(1, 4, 32, 8)   /* K = 1024 */
+    KMI_VQ2(1, 8, 16, 8)   /* K = 1024 */
+    KMI_VQ2(1, 16, 8, 8)   /* K = 1024 */
+    KMI_VQ2(1, 2, 128, 0)   /* K = 2048 */
+    KMI_VQ2(1, 4, 64, 0)   /* K = 2048 */
+    KMI_VQ2(1, 8, 32, 0)   /* K = 2048 */
+    KMI_VQ2(1, 16, 16, 0)   /* K = 2048 */
+    KMI_VQ2(1, 32, 8, 0)   /* K = 2048 */
+    KMI_VQ2(1, 64, 4, 0)   /* K = 2048 */
+    KMI_VQ2(1, 2, 128, 8)   /* K = 2048 */
+    KMI_VQ2(1, 4, 64, 8)   /* K = 2048 */
+    KMI_VQ2(1, 8, 32, 8)   /* K = 2048 */
+    KMI_VQ2(1, 16, 16, 8)   /* K = 2048 */
+    KMI_VQ2(1, 32, 8, 8)   /* K = 2048 */
+    KMI_VQ2(1, 2, 176, 0)   /* K = 2816 */
+    KMI_VQ2(1, 4, 88, 0)   /* K = 2816 */
+    KMI_VQ2(1, 8, 44, 0)   /* K = 2816 */
+    KMI_VQ2(1, 2, 176, 8)   /* K = 2816 */
+    KMI_VQ2(1, 4, 88, 8)   /* K = 2816 */
+    KMI_VQ2(1, 2, 256, 0)   /* K = 4096 */
+    KMI_VQ2(1, 4, 128, 0)   /* K = 4096 */
+    KMI_VQ2(1, 8, 64, 0)   /* K = 4096 */
+    KMI_VQ2(1, 16, 32, 0)   /* K = 4096 */
+    KMI_VQ2(1, 32, 16, 0)   /* K = 4096 */
+    KMI_VQ2(1, 64, 8, 0)   /* K = 4096 */
+    KMI_VQ2(1, 2, 256, 8)   /* K = 4096 */
+    KMI_VQ2(1, 4, 128, 8)   /* K = 4096 */
+    KMI_VQ2(1, 8, 64, 8)   /* K = 4096 */
+    KMI_VQ2(1, 16, 32, 8)   /* K = 4096 */
+    KMI_VQ2(1, 32, 16, 8)   /* K = 4096 */
+    KMI_VQ2(1, 64, 8, 8)   /* K = 4096 */
+    KMI_VQ2(2, 2, 8, 0)   /* K = 128 */
+    KMI_VQ2(2, 4, 4, 0)   /* K = 128 */
+    KMI_VQ2(2, 8, 2, 0)   /* K = 128 */
+    KMI_VQ2(2, 2, 8, 8)   /* K = 128 */
+    KMI_VQ2(2, 2, 16, 0)   /* K = 256 */
+    KMI_VQ2(2, 4, 8, 0)   /* K = 256 */
+    KMI_VQ2(2, 8, 4, 0)   /* K = 256 */
+    KMI_VQ2(2, 16, 2, 0)   /* K = 256 */
+    KMI_VQ2(2, 2, 16, 8)   /* K = 256 */
+    KMI_VQ2(2, 4, 8, 8)   /* K = 256 */
+    KMI_VQ2(2, 2, 32, 0)   /* K = 512 */
+    KMI_VQ2(2, 4, 16, 0)   /* K = 512 */
+    KMI_VQ2(2, 8, 8, 0)   /* K = 512 */
+    KMI_VQ2(2, 16, 4, 0)   /* K = 512 */
+    KMI_VQ2(2, 32, 2, 0)   /* K = 512 */
+    KMI_VQ2(2, 2, 32, 8)   /* K = 512 */
+    KMI_VQ2(2, 4, 16, 8)   /* K = 512 */
+    KMI_VQ2(2, 8, 8, 8)   /* K = 512 */
+    KMI_VQ2(2, 2, 44, 0)   /* K = 704 */
+    KMI_VQ2(2, 4, 22, 0)   /* K = 704 */
+    KMI_VQ2(2, 2, 48, 0)   /* K = 768 */
+    KMI_VQ2(2, 4, 24, 0)   /* K = 768 */
+    KMI_VQ2(2, 8, 12, 0)   /* K = 768 */
+    KMI_VQ2(2, 16, 6, 0)   /* K = 768 */
+    KMI_VQ2(2, 2, 48, 8)   /* K = 768 */
+    KMI_VQ2(2, 4, 24, 8)   /* K = 768 */
+    KMI_VQ2(2, 2, 64, 0)   /* K = 1024 */
+    KMI_VQ2(2, 4, 32, 0)   /* K = 1024 */
+    KMI_VQ2(2, 8, 16, 0)   /* K = 1024 */
+    KMI_VQ2(2, 16, 8, 0)   /* K = 1024 */
+    KMI_VQ2(2, 32, 4, 0)   /* K = 1024 */
+    KMI_VQ2(2, 64, 2, 0)   /* K = 1024 */
+    KMI_VQ2(2, 2, 64, 8)   /* K = 1024 */
+    KMI_VQ2(2, 4, 32, 8)   /* K = 1024 */
+    KMI_VQ2(2, 8, 16, 8)   /* K = 1024 */
+    KMI_VQ2(2, 16, 8, 8)   /* K = 1024 */
+    KMI_VQ2(2, 2, 128, 0)   /* K = 2048 */
+    KMI_VQ2(2, 4, 64, 0)   /* K = 2048 */
+    KMI_VQ2(2, 8, 32, 0)   /* K = 2048 */
+    KMI_VQ2(2, 16, 16, 0)   /* K = 2048 */
+    KMI_VQ2(2, 32, 8, 0)   /* K = 2048 */
+    KMI_VQ2(2, 64, 4, 0)   /* K = 2048 */
+    KMI_VQ2(2, 2, 128, 8)   /* K = 2048 */
+    KMI_VQ2(2, 4, 64, 8)   /* K = 2048 */
+    KMI_VQ2(2, 8, 32, 8)   /* K = 2048 */
+    KMI_VQ2(2, 16, 16, 8)   /* K = 2048 */
+    KMI_VQ2(2, 32, 8, 8)   /* K = 2048 */
+    KMI_VQ2(2, 2, 176, 0)   /* K = 2816 */
+    KMI_VQ2(2, 4, 88, 0)   /* K = 2816 */
+    KMI_VQ2(2, 8, 44, 0)   /* K = 2816 */
+    KMI_VQ2(2, 16, 22, 0)   /* K = 2816 */
+    KMI_VQ2(2, 2, 176, 8)   /* K = 2816 */
+    KMI_VQ2(2, 4, 88, 8)   /* K = 2816 */
+    KMI_VQ2(2, 2, 256, 0)   /* K = 4096 */
+    KMI_VQ2(2, 4, 128, 0)   /* K = 4096 */
+    KMI_VQ2(2, 8, 64, 0)   /* K = 4096 */
+    KMI_VQ2(2, 16, 32, 0)   /* K = 4096 */
+    KMI_VQ2(2, 32, 16, 0)   /* K = 4096 */
+    KMI_VQ2(2, 64, 8, 0)   /* K = 4096 */
+    KMI_VQ2(2, 2, 256, 8)   /* K = 4096 */
+    KMI_VQ2(2, 4, 128, 8)   /* K = 4096 */
+    KMI_VQ2(2, 8, 64, 8)   /* K = 4096 */
+    KMI_VQ2(2, 16, 32, 8)   /* K = 4096 */
+    KMI_VQ2(2, 32, 16, 8)   /* K = 4096 */
+    KMI_VQ2(2, 64, 8, 8)   /* K = 4096 */
+#undef KMI_VQ2
 #undef KMI_VQ
     set_error("vq: no kernel for K=%lld (%d lanes x %d codes, scale group %d)", (long long)a.K, seg, cps, a.sg);
     return EINVAL_ARG;
@@ -321,6 +418,59 @@ int kmi_vq_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int3
     rc = launch_vq(a, code_bytes, 2, (hipStream_t)stream);
     if (rc) return rc;
     KMI_CHECK_LAUNCH("vq_gemv(glu)");
+    return OK;
+}
+
+size_t kmi_vq_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k) {
+    if (T <= 0 || H <= 0 || I <= 0 || k <= 0) return 0;
+    const size_t act = ((size_t)T * k * I * 2 + 255) & ~(size_t)255;
+    return act + (size_t)T * k * H * 2;          // act, then y for the combine
+}
+
+int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                      const void* scores, const void* codes_gate, const void* scales_gate,
+                      const void* codebook_gate, const void* codes_up, const void* scales_up,
+                      const void* codebook_up, const void* codes_down, const void* scales_down,
+                      const void* codebook_down, int code_bytes, int kc, int dim, int scale_group,
+                      int64_t E, int dtype, void* out, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+    clear_error();
+    int rc = vq_check(dtype, code_bytes, kc, dim, scale_group, H, I, E);
+    if (rc) return rc;
+    rc = vq_check(dtype, code_bytes, kc, dim, scale_group, I, H, E);
+    if (rc) return rc;
+    KMI_CHECK_ARG(T >= 0 && k >= 1 && k <= 64, "vq_switch_glu: bad sizes");
+    if (T == 0) return OK;
+    KMI_CHECK_ARG(x && inds && codes_gate && scales_gate && codebook_gate && codes_up && scales_up &&
+                  codebook_up && codes_down && scales_down && codebook_down && out,
+                  "vq_switch_glu: null pointer");
+    const size_t need = kmi_vq_switch_glu_workspace_bytes(T, H, I, k);
+    if (!workspace || workspace_bytes < need) {
+        set_error("vq_switch_glu: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+        return EWORKSPACE;
+    }
+    uint16_t* act = (uint16_t*)workspace;
+    hipStream_t st = (hipStream_t)stream;
+    VqArgs g = {};
+    g.x = (const uint16_t*)x; g.lhs = nullptr; g.lhs_div = k; g.rhs = inds; g.P = T * k; g.X = T;
+    g.codes0 = codes_gate; g.sc0 = (const uint16_t*)scales_gate; g.cb0 = (const uint16_t*)codebook_gate;
+    g.codes1 = codes_up; g.sc1 = (const uint16_t*)scales_up; g.cb1 = (const uint16_t*)codebook_up;
+    g.kc = kc; g.y = act; g.E = E; g.N = I; g.K = H; g.erows = I;
+    g.sg = scale_group ? scale_group : (int)H;
+    rc = launch_vq(g, code_bytes, 2, st);
+    if (rc) return rc;
+    KMI_CHECK_LAUNCH("vq_gemv(glu)");
+    uint16_t* y = scores ? act + (((size_t)T * k * I + 127) & ~(size_t)127) : (uint16_t*)out;
+    VqArgs d = {};
+    d.x = act; d.lhs = nullptr; d.lhs_div = 1; d.rhs = inds; d.P = T * k; d.X = T * k;
+    d.codes0 = codes_down; d.sc0 = (const uint16_t*)scales_down; d.cb0 = (const uint16_t*)codebook_down;
+    d.codes1 = nullptr; d.sc1 = nullptr; d.cb1 = d.cb0; d.kc = kc;
+    d.y = y; d.E = E; d.N = H; d.K = I; d.erows = H;
+    d.sg = scale_group ? scale_group : (int)I;
+    rc = launch_vq(d, code_bytes, 1, st);
+    if (rc) return rc;
+    KMI_CHECK_LAUNCH("vq_gemv(down)");
+    if (scores) return kmi_moe_combine(y, scores, dtype, T, k, H, out, stream);
     return OK;
 }
 

@@ -24,7 +24,7 @@ import math
 import torch
 
 from .ops import (gather_qmm, moe_combine, moe_route, moe_shared_add, quantize,
-                  quantized_matmul, swiglu, switch_glu, vq_gather_qmm, vq_glu)
+                  quantized_matmul, swiglu, switch_glu, vq_gather_qmm, vq_glu, vq_switch_glu)
 
 
 class Linear:
@@ -227,8 +227,21 @@ class VQSwitchGLU:
     def __init__(self, gate_proj: VQSwitchLinear, up_proj: VQSwitchLinear, down_proj: VQSwitchLinear):
         self.gate_proj, self.up_proj, self.down_proj = gate_proj, up_proj, down_proj
 
+    def _mats(self):
+        return tuple((m.codes, m.codebook, m.scales) for m in (self.gate_proj, self.up_proj, self.down_proj))
+
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
-        """x [..., H], indices [..., k] -> [..., k, H]."""
+        """x [..., H], indices [..., k] -> [..., k, H]: one library call."""
+        return vq_switch_glu(x, indices, *self._mats(), self.gate_proj.scale_group)
+
+    def combine(self, x, indices, scores):
+        """(self(x, indices) * scores[..., None]).sum(-2) with the reference's
+        roundings, in the same library call."""
+        return vq_switch_glu(x, indices, *self._mats(), self.gate_proj.scale_group, scores=scores)
+
+    def separate(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+        """The same through the separate ops: vq_glu, then vq_gather_qmm over
+        the (token, slot) rows."""
         g, u, d = self.gate_proj, self.up_proj, self.down_proj
         act = vq_glu(x, indices, (g.codes, g.codebook, g.scales), (u.codes, u.codebook, u.scales),
                      g.scale_group)                                           # [..., k, I]
@@ -239,9 +252,6 @@ class VQSwitchGLU:
                           lhs_indices=torch.arange(P, device=x.device, dtype=torch.int32),
                           rhs_indices=indices.reshape(P).to(torch.int32), scale_group=d.scale_group)
         return y.reshape(*lead, k, y.shape[-1])
-
-    def combine(self, x, indices, scores):
-        return moe_combine(self(x, indices), scores)
 
 
 class MLP:

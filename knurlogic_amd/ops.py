@@ -410,3 +410,45 @@ def vq_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, scale_group: int = 
     _abi.check(_lib().kmi_vq_glu(_ptr(xc), T, H, I, k, _ptr(ic), *[_ptr(t) for t in ops], cbytes, kc, dim,
                                  scale_group, E, DTYPE_CODE[x.dtype], _ptr(act), _stream(x)), "vq_glu")
     return act
+
+
+
+def vq_switch_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, down, scale_group: int = 0,
+                  scores: torch.Tensor | None = None):
+    """SwitchGLU over VQ experts in one library call: gate/up with the
+    _SwiGLU epilogue, down, and (with scores [..., k]) the weighted combine.
+    gate / up / down = (codes, codebook, scales).  x [..., H], indices
+    [..., k] -> [..., k, H], or [..., H] with scores."""
+    (cg, bg, sg_), (cu, bu, su), (cd, bd, sd) = gate, up, down
+    cbytes, kc, dim = _vq_operands(cg, bg, sg_)
+    if (_vq_operands(cu, bu, su) != (cbytes, kc, dim) or _vq_operands(cd, bd, sd) != (cbytes, kc, dim)
+            or cu.shape != cg.shape):
+        raise ValueError("vq_switch_glu: gate, up and down differ in layout")
+    _on_gpu(x, indices, cg, bg, sg_, cu, bu, su, cd, bd, sd)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("vq_switch_glu: only bfloat16 activations are implemented")
+    lead, H = tuple(x.shape[:-1]), x.shape[-1]
+    k = indices.shape[-1]
+    E, I = cg.shape[0], cg.shape[1]
+    if cd.shape[0] != E or cd.shape[1] != H or cd.shape[2] * dim != I:
+        raise ValueError(f"vq_switch_glu: down codes {tuple(cd.shape)} do not match [E, H, I/dim]")
+    T = math.prod(lead)
+    if scores is not None:
+        if scores.dtype != x.dtype or tuple(scores.shape) != tuple(indices.shape):
+            raise ValueError("vq_switch_glu: scores must match indices and the dtype of x")
+        out = torch.empty(*lead, H, dtype=x.dtype, device=x.device)
+    else:
+        out = torch.empty(*lead, k, H, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out
+    xc = x.reshape(T, H).contiguous()
+    ic = indices.reshape(T, k).to(torch.int32).contiguous()
+    scc = scores.reshape(T, k).contiguous() if scores is not None else None
+    ops = [t.contiguous() for t in (cg, sg_, bg, cu, su, bu, cd, sd, bd)]
+    nbytes = _lib().kmi_vq_switch_glu_workspace_bytes(T, H, I, k)
+    ws = _workspace(nbytes, x.device)
+    _abi.check(_lib().kmi_vq_switch_glu(_ptr(xc), T, H, I, k, _ptr(ic), _ptr(scc) if scc is not None else None,
+                                        *[_ptr(t) for t in ops], cbytes, kc, dim, scale_group, E,
+                                        DTYPE_CODE[x.dtype], _ptr(out), _ptr(ws), nbytes, _stream(x)),
+               "vq_switch_glu")
+    return out

@@ -89,5 +89,30 @@ def test_vq_switch_glu_matches_the_oracle(dev, kc, scale_group, T, E, H, I, k):
     got = glu(tx, ti)
     assert got.shape == (T, k, H)
     assert_close(to_numpy(got), ref, what="vq switch_glu")
+    sep = glu.separate(tx, ti)
+    assert torch.equal(sep, got), "one call and the separate ops differ"
     _, sc = O.route(bf16_normal(rng, (T, E)), k)
-    assert_close(to_numpy(glu.combine(tx, ti, to_torch(sc, dev, BF))), O.combine(ref, sc), what="combine")
+    comb = glu.combine(tx, ti, to_torch(sc, dev, BF))
+    assert comb.shape == (T, H)
+    assert_close(to_numpy(comb), O.combine(ref, sc), what="combine")
+    # the one-call combine is the combine op applied to the same y, bit for bit
+    assert torch.equal(comb, K.moe_combine(got, to_torch(sc, dev, BF)))
+
+
+def test_vq_switch_glu_bad_expert_and_errors(dev):
+    """An out-of-range expert contributes nothing (its y row is 0, its
+    combine term 0); mismatched scores are refused."""
+    rng = np.random.default_rng(41)
+    E, H, I, T, k = 6, 256, 128, 3, 2
+    (hg, gg), (hu, gu), (hd, gd) = [_vq(rng, E, n, kd, 256, 0, dev) for n, kd in ((I, H), (I, H), (H, I))]
+    glu = nn.VQSwitchGLU(*(nn.VQSwitchLinear(*g) for g in (gg, gu, gd)))
+    x = bf16_normal(rng, (T, H))
+    inds = np.array([[0, 9], [2, 3], [-1, 5]], np.int32)
+    tx, ti = to_torch(x, dev, BF), torch.from_numpy(inds).to(dev)
+    y = to_numpy(glu(tx, ti))
+    assert (y[0, 1] == 0).all() and (y[2, 0] == 0).all()
+    sc = O.round_to(rng.uniform(0.1, 0.5, (T, k)).astype(np.float32), "bfloat16")
+    comb = to_numpy(glu.combine(tx, ti, to_torch(sc, dev, BF)))
+    assert_close(comb, O.combine(y, sc), what="combine with bad experts")
+    with pytest.raises(ValueError):
+        K.vq_switch_glu(tx, ti, gg, gu, gd, scores=torch.zeros(T, k + 1, dtype=BF, device=dev))
