@@ -13,6 +13,8 @@
 #include "qgemv.hpp"
 #include "../../include/knurlogic_amd.h"
 
+#include <cstdlib>
+
 namespace kmi {
 // y[r, n] = bf16(sum_s partial[s, r, n]), slices summed in order.  Rows of
 // pairs with an out-of-range expert (gather) are left alone here: the sort
@@ -163,61 +165,52 @@ int launch_sort_rows(const int32_t* rhs, int64_t P, int64_t Mper, int E, int tm,
 #define KMI_SKINNY_MIN_ROWS 2
 #endif
 
-enum class QmvKind { VALU1, VALU2, VALU4, SKINNY };
+enum class QmvKind { VALU1, SKINNY };
 
-static int tile_rows(QmvKind k) {
-    switch (k) {
-        case QmvKind::VALU1: return 1;
-        case QmvKind::VALU2: return 2;
-        case QmvKind::VALU4: return 4;
-        default: return 16;
-    }
+static int tile_rows(QmvKind k) { return k == QmvKind::VALU1 ? 1 : 16; }
+
+// LDS of the VALU kernel: the tile's x row as fp16 (2 bytes per k) and a
+// 16-byte {scale, correction, sum} record per 16-byte weight chunk.
+static size_t valu_lds(int64_t K, int bits) {
+    return (size_t)K * 2 + (size_t)(K / (128 / bits)) * 16;
 }
 
-static size_t valu_lds(int64_t K, int bits, int mt, int gs, const ValuShape& v) {
-    const int64_t CK = 128 / bits;
-    return (size_t)mt * (K + 8) * 2 + (size_t)mt * (K / CK) * 4 +
-           (size_t)v.WV * v.RPW * (K / gs) * 4;
+static int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
 }
 
-// Launch shape of the VALU kernel.  S: chunk slots per lane, all of K up to
-// 8 slots (one load batch).  RPW: weight rows per wave, so the grid's waves
-// over all tiles stay within what 256 CUs hold at once yet fill them.  WV:
-// waves per workgroup, so the weight bytes a workgroup streams are at least
-// 4x the x bytes it stages into LDS (x is read from L2 once per workgroup).
-static ValuShape valu_shape(int64_t N, int64_t K, int bits, int64_t tiles, int mt) {
+// Launch shape of the VALU kernel.  S: 16-byte chunk slots per lane, all of
+// K up to 8 slots (one load batch).  RPW: weight rows per wave, as many as
+// keep S * RPW <= 8 loads in registers while the grid still has >= 4096
+// waves (4 per SIMD) to spread over the chip.  WV: waves per workgroup,
+// which amortizes the x staging over WV * RPW rows.  KMI_QMV_RPW and
+// KMI_QMV_WV override the choice (tuning).
+static ValuShape valu_shape(int64_t N, int64_t K, int bits, int64_t tiles) {
     const int64_t C = K / (128 / bits);
     const int64_t slots = ceil_div(C, 64);
     ValuShape v;
     v.S = slots <= 1 ? 1 : slots <= 2 ? 2 : slots <= 4 ? 4 : 8;
     const int64_t T = tiles > 0 ? tiles : 1;
     v.RPW = 1;
-    if (mt == 1) {
-        if (v.S <= 4 && N * T / 2 >= 4096) v.RPW = 2;
-        if (v.S <= 2 && N * T / 4 >= 4096) v.RPW = 4;
-    }
-    const int64_t rows_target = (int64_t)16 * mt * 4 / bits;   // 16*mt at 4 bits, 8*mt at 8 bits
-    const int64_t wv = ceil_div(rows_target, v.RPW);
-    v.WV = wv <= 4 ? 4 : wv <= 8 ? 8 : 16;
+    if (v.S <= 4 && N * T / 2 >= 4096) v.RPW = 2;
+    if (v.S <= 2 && N * T / 4 >= 4096) v.RPW = 4;
+    const int rpw = env_int("KMI_QMV_RPW", 0);
+    if (rpw == 1 || (rpw == 2 && v.S <= 4) || (rpw == 4 && v.S <= 2)) v.RPW = rpw;
+    v.WV = 8;
+    const int wv = env_int("KMI_QMV_WV", 0);
+    if (wv == 4 || wv == 8) v.WV = wv;
     // no more waves per workgroup than the rows need
     while (v.WV > 4 && (int64_t)(v.WV / 2) * v.RPW >= N) v.WV /= 2;
     v.groups = ceil_div(N, (int64_t)v.WV * v.RPW);
     return v;
 }
 
-// Kernel choice by rows per tile: the VALU GEMV below KMI_SKINNY_MIN_ROWS
-// rows while its LDS (x rows of the tile, their chunk sums, the workgroup's
-// scales/biases) fits 64 KB at the shape it would launch with, else qgemv.
-static QmvKind choose_kind(int64_t rows_per_tile, int64_t K, int64_t N, int64_t total_rows, int bits,
-                           int gs) {
-    const size_t cap = 64 * 1024;
-    const QmvKind kinds[3] = {QmvKind::VALU1, QmvKind::VALU2, QmvKind::VALU4};
-    const int mts[3] = {1, 2, 4};
-    for (int i = 0; i < 3; i++) {
-        if (rows_per_tile > mts[i] || rows_per_tile >= KMI_SKINNY_MIN_ROWS) continue;
-        const ValuShape v = valu_shape(N, K, bits, ceil_div(total_rows, mts[i]), mts[i]);
-        if (valu_lds(K, bits, mts[i], gs, v) <= cap) return kinds[i];
-    }
+// Kernel choice by rows per tile: the VALU GEMV for one row per tile while
+// its LDS fits 64 KB, else qgemv (MFMA).
+static QmvKind choose_kind(int64_t rows_per_tile, int64_t K, int bits) {
+    if (rows_per_tile < KMI_SKINNY_MIN_ROWS && rows_per_tile <= 1 && valu_lds(K, bits) <= 64 * 1024)
+        return QmvKind::VALU1;
     return QmvKind::SKINNY;
 }
 
@@ -225,9 +218,9 @@ static int skinny_tile_rows(int64_t rows_per_tile) {
     return rows_per_tile <= 16 ? 16 : rows_per_tile <= 32 ? 32 : 64;
 }
 
-static int launch_valu(QmvKind k, const QmvArgs& a, int bits, dim3 grid, size_t lds, hipStream_t st,
+static int launch_valu(const QmvArgs& a, int bits, dim3 grid, size_t lds, hipStream_t st,
                        const ValuShape& v) {
-    if (!launch_qmv_valu(bits, tile_rows(k), v, a, grid, lds, st)) {
+    if (!launch_qmv_valu(bits, v, a, grid, lds, st)) {
         set_error("qmv: no kernel for shape S=%d RPW=%d WV=%d", v.S, v.RPW, v.WV);
         return EINVAL_ARG;
     }
@@ -292,7 +285,7 @@ extern "C" {
 size_t kmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits) {
     if (M <= 0 || K <= 0 || N <= 0 || group_size <= 0 || (bits != 4 && bits != 8)) return 0;
     if (M > SKINNY_MAX_M) return qmm_gemm_workspace(M, K, N);       // GEMM path (split-K partials)
-    if (choose_kind(M, K, N, M, bits, group_size) != QmvKind::SKINNY) return 0;   // VALU path
+    if (choose_kind(M, K, bits) != QmvKind::SKINNY) return 0;   // VALU path
     const int tm = skinny_tile_rows(M);
     return skinny_partial_bytes(plan_qgemv(N, K, ceil_div(M, tm), tm, group_size), M, N);
 }
@@ -312,7 +305,7 @@ int kmi_qmm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
     hipStream_t st = (hipStream_t)stream;
     if (M > SKINNY_MAX_M)
         return qmm_gemm(x, M, K, N, w, scales, biases, group_size, bits, y, workspace, workspace_bytes, st);
-    const QmvKind kind = choose_kind(M, K, N, M, bits, group_size);
+    const QmvKind kind = choose_kind(M, K, bits);
     if (kind != QmvKind::SKINNY) {
         QmvArgs a = {};
         a.x = (const uint16_t*)x; a.w = w; a.s = (const uint16_t*)scales; a.b = (const uint16_t*)biases;
@@ -320,9 +313,9 @@ int kmi_qmm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
         a.gs_shift = group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
         const int tm = tile_rows(kind);
         a.tile_m = tm;
-        const ValuShape v = valu_shape(N, K, bits, ceil_div(M, tm), tm);
+        const ValuShape v = valu_shape(N, K, bits, ceil_div(M, tm));
         dim3 grid((unsigned)v.groups, 1, (unsigned)ceil_div(M, tm));
-        return launch_valu(kind, a, bits, grid, valu_lds(K, bits, tm, group_size, v), st, v);
+        return launch_valu(a, bits, grid, valu_lds(K, bits), st, v);
     }
     const int tm = skinny_tile_rows(M);
     const int64_t ntiles = ceil_div(M, tm);
@@ -344,7 +337,7 @@ size_t kmi_gather_qmm_workspace_bytes(int64_t P, int64_t M, int64_t E, int64_t K
     if (P <= 0 || M <= 0 || E <= 0 || K <= 0 || N <= 0 || group_size <= 0 || (bits != 4 && bits != 8))
         return 0;
     const int64_t rpt = gather_rows_per_tile(P, M, E);
-    const QmvKind kind = choose_kind(rpt, K, N, P * M, bits, group_size);
+    const QmvKind kind = choose_kind(rpt, K, bits);
     const int tm = kind == QmvKind::SKINNY ? qgemv_gather_tile_rows(rpt) : tile_rows(kind);
     size_t b = sort_index_bytes(P * M, E, tm);
     if (kind == QmvKind::SKINNY)
@@ -369,7 +362,7 @@ int kmi_gather_qmm(const void* x, int64_t X, int64_t M, int64_t K, const uint32_
     if (P == 0) return OK;
     KMI_CHECK_ARG(x && w && scales && biases && y && lhs && rhs, "gather_qmm: null pointer");
     const int64_t rpt = gather_rows_per_tile(P, M, E);
-    const QmvKind kind = choose_kind(rpt, K, N, P * M, bits, group_size);
+    const QmvKind kind = choose_kind(rpt, K, bits);
     const int tm = kind == QmvKind::SKINNY ? qgemv_gather_tile_rows(rpt) : tile_rows(kind);
     const size_t need = kmi_gather_qmm_workspace_bytes(P, M, E, K, N, group_size, bits);
     if (workspace == nullptr || workspace_bytes < need) {
@@ -388,9 +381,9 @@ int kmi_gather_qmm(const void* x, int64_t X, int64_t M, int64_t K, const uint32_
         a.y = (uint16_t*)y; a.K = K; a.N = N; a.rows = rows; a.S = 1; a.tile_m = tm;
         a.gs_shift = group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
         a.tiles = sr.tiles; a.sorted = sr.sorted; a.lhs = lhs; a.Mper = M; a.Xrows = X * M;
-        const ValuShape v = valu_shape(N, K, bits, ceil_div(rows, tm), tm);
+        const ValuShape v = valu_shape(N, K, bits, ceil_div(rows, tm));
         dim3 grid((unsigned)v.groups, 1, (unsigned)sr.max_tiles);
-        return launch_valu(kind, a, bits, grid, valu_lds(K, bits, tm, group_size, v), st, v);
+        return launch_valu(a, bits, grid, valu_lds(K, bits), st, v);
     }
     const QgPlan p = plan_qgemv(N, K, sr.max_tiles, tm, group_size);
     QgArgs a = {};

@@ -123,9 +123,9 @@ struct ValuShape {
     int64_t groups;   // workgroups along N
 };
 
-// Launches qmv_valu_kernel<bits, mt, v.RPW, v.S, v.WV>; returns false for
-// a shape that has no instantiation.
-bool launch_qmv_valu(int bits, int mt, const ValuShape& v, const QmvArgs& a, dim3 grid,
-                     size_t lds, hipStream_t st);
+// Launches qmv_valu_kernel<bits, v.RPW, v.S, v.WV>; returns false for a
+// shape that has no instantiation.
+bool launch_qmv_valu(int bits, const ValuShape& v, const QmvArgs& a, dim3 grid, size_t lds,
+                     hipStream_t st);
 
 }  // namespace kmi

@@ -1,225 +1,318 @@
-// Decode-shape quantized GEMV on the VALU (M <= 4 activation rows per
-// tile), templated on the launch shape; the host side (qmv.hip) picks the
-// shape.  See qmv.hip for the arithmetic.
+// Decode-shape quantized GEMV on the VALU: one activation row per tile (the
+// dense M = 1 call, or one routed row per tile of gather_qmm).  The host side
+// (qmv.hip) picks the launch shape.
 //
-// Decode shapes are latency-bound unless the whole weight stream is in
-// flight at once, so each wave issues every load of its rows (S 16-byte
-// chunk slots per lane per row: all of K when K fits) right after the small
-// L2-resident x and scale/bias loads, and the grid is sized so all waves are
-// resident together.  Loads are consumed in issue order, so the math of the
-// first chunks overlaps the arrival of the later ones.  All global reads are
-// buffer loads: 32-bit offsets (one VGPR per address) and hardware range
-// checks (reads past a buffer return 0) instead of clamps or branches --
-// a guarded load becomes a branch whose join waits for the load.
+// The work is HBM-bound only if the decode math stays well under the weight
+// stream, so the inner loop is built around the fewest VALU operations per
+// packed word:
+//
+//   * codes become fp16 "1024 + q" with one v_and_or_b32 per pair: a low
+//     nibble (or a byte) lands in the low mantissa bits of 0x6400 = 1024.0,
+//     and a high nibble is left in place, giving 1024 + 16 q, which is also
+//     exact (fp16 has 10 mantissa bits).  A 4-bit word costs 1 shift + 4
+//     and-or + 4 v_dot2_f32_f16 for 8 weights; an 8-bit word 2 v_perm_b32 +
+//     2 v_dot2 for 4 weights.
+//   * x is staged in LDS as fp16 with a power-of-two scale per 16-byte chunk
+//     of weights (the chunk's largest |x| maps to [2^14, 2^15)), so every
+//     bf16 value converts exactly and nothing overflows; the scale, the
+//     chunk's x sum and the magic correction 1024 * (sum of x under low
+//     codes + sum under high codes / 16) sit beside it in fp32.
+//   * per chunk and row:  y += s * (mult * (A_lo + A_hi / 16) - corr) + b * X,
+//     which is  s * sum(q x) + b * sum(x)  over the chunk (a chunk lies in
+//     one quantization group).
+//
+// Every load of a wave is issued up front, the x piece first (it gates the
+// LDS staging and the barrier; loads complete in issue order), then each
+// chunk's weights, scale and bias in the order the loop consumes them.  All
+// global reads are raw buffer loads: 32-bit offsets, and an offset past the
+// buffer reads 0 with no traffic, which is how absent rows and chunks are
+// expressed (no clamps, no branches around loads).
 #include "qmv_common.hpp"
 
 namespace kmi {
 
-template <int BITS, int MT, int RPW, int S, int WV>
+namespace {
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// A constant kept in a VGPR.  Held in a register (not an instruction
+// literal), a mask-and-or pair folds into one v_and_or_b32.
+__device__ __forceinline__ uint32_t vconst(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+__device__ __forceinline__ float fdot2(uint32_t x, uint32_t w, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), __builtin_bit_cast(f16x2_t, w), c, false);
+}
+
+__device__ __forceinline__ uint32_t pk_f16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false)));
+}
+
+constexpr uint32_t NONE = 0x80000000u;   // an offset past every buffer: reads 0
+
+}  // namespace
+
+// GATHER: tiles come from the expert sort (tile z = one routed row); else
+// tile z is row z of a dense x, and no pointer-dependent branch delays the
+// first loads (each scalar round trip to the kernel arguments costs the
+// first wave of a CU most of a microsecond).
+template <int BITS, int RPW, int S, int WV, bool GATHER>
 __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
     constexpr int NT = 64 * WV;                   // threads per workgroup
     constexpr int CK = 128 / BITS;                // k per 16-byte chunk: 32 or 16
-    constexpr int XV = CK / 8;                    // 16-byte x loads per chunk
-    constexpr int SR = 4;                         // scale/bias pairs per thread held in registers
-    constexpr int ROWS = WV * RPW;                // weight rows per workgroup
+    constexpr int XV = CK / 8;                    // 8-element x pieces per chunk: 4 or 2
+    constexpr int XV_SHIFT = XV == 4 ? 2 : 1;
     extern __shared__ __align__(16) unsigned char smem[];
 
     Tile t;
-    if (!resolve_tile(a, t)) return;
+    if constexpr (GATHER) {
+        if (!resolve_tile(a, t)) return;
+    } else {
+        t.expert = 0;
+        t.start = blockIdx.z;
+        t.count = 1;
+    }
     const int C = (int)(a.K / CK);                // chunks per row
     const int NB = (C + 64 * S - 1) / (64 * S);   // load batches per row
     const int wpr = (int)(a.K / (32 / BITS));     // packed words per row
     const int gpr = (int)(a.K >> a.gs_shift);     // groups per row
-    const int xstride = (int)a.K + 8;             // bf16 per LDS x row
-    // x row m in LDS: [piece v8 < XV][chunk c < C] 16-byte slots, so the 64
-    // lanes of one ds_read_b128 hit 64 consecutive slots
-    uint16_t* xs = (uint16_t*)smem;                                                      // [MT][xstride]
-    float* xc = (float*)(smem + (size_t)MT * xstride * 2);                               // [MT][C]
-    uint32_t* sbl = (uint32_t*)(smem + (size_t)MT * xstride * 2 + (size_t)MT * C * 4);  // [ROWS][gpr]
+    const int P = (int)(a.K >> 3);                // x pieces per row
+    u32x4* xs = (u32x4*)smem;                                  // [XV][C] fp16 pieces
+    float4* xm = (float4*)(smem + (size_t)XV * C * 16);        // [C] {mult, corr, sum, -}
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int nwg = (int)blockIdx.x * ROWS;
-    const int n0 = nwg + wave * RPW;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar offsets
+    const int n0 = (int)blockIdx.x * (WV * RPW) + wave * RPW;
     const int64_t eoff = (int64_t)t.expert * a.N;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + eoff * wpr, a.N * (int64_t)wpr * 4);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s + eoff * gpr, a.N * (int64_t)gpr * 2);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b + eoff * gpr, a.N * (int64_t)gpr * 2);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.Xrows * a.K * 2);
-    const int nx = (int)t.count * C;              // x chunks of the tile
-    const int nsb = ROWS * gpr;                   // scale/bias pairs of the workgroup
 
-    // byte offset of x chunk (m, c); rows that do not exist get an offset
-    // past every buffer, which reads as zeros
-    constexpr uint32_t NONE = 0x80000000u;
-    auto x_off = [&](int m, int c) -> uint32_t {
-        const int64_t xrow = x_row_of(a, t.start + m);
-        return (xrow >= 0 && xrow < a.Xrows) ? (uint32_t)((xrow * a.K + (int64_t)c * CK) * 2) : NONE;
-    };
-    auto stage_x = [&](int idx, const u32x4* v) {
-        const int m = idx / C, c = idx - m * C;
-        float sum = 0.f;
+    const int64_t xrow = GATHER ? x_row_of(a, t.start) : t.start;
+    const bool xok = xrow >= 0 && xrow < a.Xrows;
+    // Load offsets: lane-only VGPRs shared by every load of a stream, with
+    // the wave-uniform part (x row, weight row, slot) in the scalar offset
+    // operand, so issuing a wave's loads costs almost no VALU work (with
+    // several waves per SIMD, prologue instructions delay the last wave's
+    // loads).  NONE marks a lane with nothing to read.
+    const uint32_t xso = xok ? (uint32_t)(xrow * a.K * 2) : 0u;
+    auto xvo = [&](int p) -> uint32_t { return (xok && p < P) ? (uint32_t)p * 16u : NONE; };
+
+    // Piece p of the row (x[8p .. 8p+8)) -> LDS.  Every lane of the wave runs
+    // this (the quad reductions read neighbours); only in-row pieces store.
+    auto stage = [&](int p, u32x4 raw) {
+        float f[8];
 #pragma unroll
-        for (int v8 = 0; v8 < XV; v8++)
-            *(u32x4*)(xs + m * xstride + (v8 * C + c) * 8) = permute8<BITS>(v[v8], sum);
-        xc[m * C + c] = sum;
-    };
-    auto sb_pair = [&](int idx) -> uint32_t {      // (scale | bias << 16) of pair idx
-        const int rl = idx / gpr, g = idx - rl * gpr;
-        const int off = (int)(((uint32_t)(nwg + rl) * (uint32_t)gpr + (uint32_t)g) * 2u);
-        const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
-        const uint32_t bv = __builtin_amdgcn_raw_buffer_load_b16(rb, off, 0, 0);
-        return sv | (bv << 16);
+        for (int i = 0; i < 4; i++) {
+            f[2 * i] = __uint_as_float(raw[i] << 16);
+            f[2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
+        }
+        float am = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) am = fmaxf(am, fabsf(f[i]));
+        am = dpp_max<0xb1>(am);                           // quad_perm [1,0,3,2]
+        if constexpr (XV == 4) am = dpp_max<0x4e>(am);    // quad_perm [2,3,0,1]
+        int e = (int)((__float_as_uint(am) >> 23) & 0xffu);
+        e = e < 15 ? 15 : e;
+        const float mult = __uint_as_float((uint32_t)(e - 14) << 23);   // 2^(e-141)
+        const float inv = __uint_as_float((uint32_t)(268 - e) << 23);   // 2^(141-e)
+        u32x4 o;
+        float lo, hi = 0.f;
+        if constexpr (BITS == 4) {
+            // dword i pairs (x_i, x_{i+4}): the codes one and-or places there
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = pk_f16(f[i] * inv, f[i + 4] * inv);
+            lo = (f[0] + f[2]) + (f[4] + f[6]);           // under low nibbles
+            hi = (f[1] + f[3]) + (f[5] + f[7]);           // under high nibbles
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = pk_f16(f[2 * i] * inv, f[2 * i + 1] * inv);
+            lo = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+        }
+        lo = dpp_add<0xb1, 0xf>(lo);
+        if constexpr (XV == 4) lo = dpp_add<0x4e, 0xf>(lo);
+        if constexpr (BITS == 4) {
+            hi = dpp_add<0xb1, 0xf>(hi);
+            hi = dpp_add<0x4e, 0xf>(hi);
+        }
+        if (p < P) {
+            const int c = p >> XV_SHIFT, v = p & (XV - 1);
+            xs[v * C + c] = o;
+            if (v == 0) {
+                const float corr = BITS == 4 ? 1024.f * __builtin_fmaf(hi, 0.0625f, lo) : 1024.f * lo;
+                xm[c] = make_float4(mult, corr, lo + hi, 0.f);
+            }
+        }
     };
 
-    // (0) what will not fit in registers (many x rows, wide groups): plain
-    // loops, before any weight load is issued so their waits drain nothing
-    for (int idx = tid + NT; idx < nx; idx += NT) {
-        const uint32_t off = x_off(idx / C, idx % C);
-        u32x4 v[XV];
-#pragma unroll
-        for (int v8 = 0; v8 < XV; v8++)
-            v[v8] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(off + 16u * v8), 0, 0);
-        stage_x(idx, v);
+    // (0) pieces beyond two per thread (long rows): staged before any
+    // weight load is issued, so their waits drain nothing
+    if (P > 2 * NT) {
+        for (int p = tid + 2 * NT; p - (tid & 3) < P; p += NT) {
+            const u32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(p), (int)xso, 0);
+            stage(p, raw);
+        }
     }
-    for (int idx = tid + NT * SR; idx < nsb; idx += NT) sbl[idx] = sb_pair(idx);
 
-    // (1) this thread's x chunk and (2) scale/bias pairs
-    u32x4 xr[XV];
-    {
-        const uint32_t off = tid < nx ? x_off(tid / C, tid % C) : NONE;
+    // (1) this thread's first two pieces, then every load of batch 0
+    const u32x4 xr0 = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(tid), (int)xso, 0);
+    const u32x4 xr1 = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(tid + NT), (int)xso, 0);
+
+    // slots (64 chunks) with every lane in the row, and the partial one
+    const int full = C >> 6;
+    const bool in_tail = lane < (C & 63);
+    const uint32_t vw = (uint32_t)lane * 16u;
+    const uint32_t vg = (uint32_t)((lane * CK) >> a.gs_shift) * 2u;
+    const uint32_t vwt = in_tail ? vw : NONE, vgt = in_tail ? vg : NONE;
+    // rows past N (only in the last wave of the grid) re-read row N-1; their
+    // results are never stored
+    uint32_t wrow[RPW], srow[RPW];
 #pragma unroll
-        for (int v8 = 0; v8 < XV; v8++)
-            xr[v8] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(off + 16u * v8), 0, 0);
+    for (int r = 0; r < RPW; r++) {
+        const uint32_t row = (uint32_t)(n0 + r < a.N ? n0 + r : a.N - 1);
+        wrow[r] = row * (uint32_t)wpr * 4u;
+        srow[r] = row * (uint32_t)gpr * 2u;
     }
-    uint32_t sr[SR];
-#pragma unroll
-    for (int j = 0; j < SR; j++) sr[j] = sb_pair(tid + NT * j);
 
-    // (3) every weight load of this wave's rows for the first batch
     u32x4 W[S][RPW];
+    uint32_t SC[S][RPW], BI[S][RPW];
+    // The small scale/bias loads go first: each chunk-row then waits only
+    // for its own weights (the barrier keeps the compiler from moving them
+    // behind the weight loads).
     auto load = [&](int nb) {
 #pragma unroll
         for (int u = 0; u < S; u++) {
-            const int c = lane + 64 * (nb * S + u);
+            const int su = nb * S + u;
+            const uint32_t vo = su < full ? vg : su == full ? vgt : NONE;
+            const uint32_t so = (uint32_t)(((64 * su * CK) >> a.gs_shift) * 2);
+#pragma unroll
+            for (int r = 0; r < RPW; r++) {
+                SC[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)vo, (int)(srow[r] + so), 0);
+                BI[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)vo, (int)(srow[r] + so), 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < S; u++) {
+            const int su = nb * S + u;
+            const uint32_t vo = su < full ? vw : su == full ? vwt : NONE;
 #pragma unroll
             for (int r = 0; r < RPW; r++)
-                W[u][r] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rw, (int)(((uint32_t)(n0 + r) * (uint32_t)wpr + (uint32_t)c * 4u) * 4u), 0, AUX_NT);
+                W[u][r] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)vo, (int)(wrow[r] + (uint32_t)su * 1024u),
+                                                                AUX_NT);
         }
     };
     load(0);
 
-    // (4) x and scales/biases -> LDS
-    if (tid < nx) stage_x(tid, xr);
-#pragma unroll
-    for (int j = 0; j < SR; j++)
-        if (tid + NT * j < nsb) sbl[tid + NT * j] = sr[j];
+    // (2) x -> LDS
+    stage(tid, xr0);
+    if (P > NT) stage(tid + NT, xr1);
     lds_barrier();
 
-    float acc[RPW][MT];
+    const uint32_t MLO = vconst(0x000F000Fu), MHI = vconst(0x00F000F0u), E16 = vconst(0x64006400u);
+    float acc[RPW];
 #pragma unroll
-    for (int r = 0; r < RPW; r++)
-#pragma unroll
-        for (int m = 0; m < MT; m++) acc[r][m] = 0.f;
+    for (int r = 0; r < RPW; r++) acc[r] = 0.f;
 
     for (int nb = 0; nb < NB; nb++) {
         if (nb > 0) load(nb);
 #pragma unroll
         for (int u = 0; u < S; u++) {
-            const int c = lane + 64 * (nb * S + u);
-            if (c >= C) continue;
-            const int g = (c * CK) >> a.gs_shift;
+            const int cbase = 64 * (nb * S + u);
+            if (cbase >= C) break;                    // wave-uniform
+            const int c = lane + cbase;
+            const bool cok = c < C;
+            const int cc = cok ? c : 0;
+            u32x4 xv[XV];
 #pragma unroll
-            for (int m = 0; m < MT; m++) {
-                if (m >= t.count) continue;
-                const uint16_t* xp = xs + m * xstride + c * 8;
-                u32x4 xv[XV];
+            for (int v = 0; v < XV; v++) xv[v] = xs[v * C + cc];
+            const float4 m = xm[cc];
 #pragma unroll
-                for (int v8 = 0; v8 < XV; v8++) xv[v8] = *(const u32x4*)(xp + v8 * C * 8);
-                const float X = xc[m * C + c];
+            for (int r = 0; r < RPW; r++) {
+                float A = 0.f, B = 0.f;
+                if constexpr (BITS == 4) {
 #pragma unroll
-                for (int r = 0; r < RPW; r++) {
-                    float A0 = 0.f, A1 = 0.f;
-                    if constexpr (BITS == 4) {
-#pragma unroll
-                        for (int wd = 0; wd < 4; wd++) {
-                            const u32x4 q = nibbles_to_bf16_magic(W[u][r][wd]);
-                            A0 = dot2(xv[wd][0], q[0], A0);
-                            A1 = dot2(xv[wd][1], q[1], A1);
-                            A0 = dot2(xv[wd][2], q[2], A0);
-                            A1 = dot2(xv[wd][3], q[3], A1);
-                        }
-                    } else {
-#pragma unroll
-                        for (int wd = 0; wd < 4; wd++) {
-                            const uint32_t word = W[u][r][wd];
-                            A0 = dot2(xv[wd >> 1][(wd & 1) * 2], bytes_to_bf16x2(word, 0), A0);
-                            A1 = dot2(xv[wd >> 1][(wd & 1) * 2 + 1], bytes_to_bf16x2(word, 2), A1);
-                        }
+                    for (int wd = 0; wd < 4; wd++) {
+                        const uint32_t w = W[u][r][wd], w8 = w >> 8;
+                        A = fdot2(xv[wd][0], (w & MLO) | E16, A);
+                        B = fdot2(xv[wd][1], (w & MHI) | E16, B);
+                        A = fdot2(xv[wd][2], (w8 & MLO) | E16, A);
+                        B = fdot2(xv[wd][3], (w8 & MHI) | E16, B);
                     }
-                    const uint32_t sbv = sbl[(wave * RPW + r) * gpr + g];
-                    const float sc = bf16_to_f32((uint16_t)(sbv & 0xffffu));
-                    const float bi = bf16_to_f32((uint16_t)(sbv >> 16));
-                    const float bb = (BITS == 4) ? __builtin_fmaf(-128.f, sc, bi) : bi;
-                    acc[r][m] = __builtin_fmaf(sc, A0 + A1, __builtin_fmaf(bb, X, acc[r][m]));
+                    A = __builtin_fmaf(B, 0.0625f, A);
+                } else {
+#pragma unroll
+                    for (int wd = 0; wd < 4; wd++) {
+                        const uint32_t w = W[u][r][wd];
+                        A = fdot2(xv[wd >> 1][(wd & 1) * 2], __builtin_amdgcn_perm(E16, w, 0x05010500u), A);
+                        B = fdot2(xv[wd >> 1][(wd & 1) * 2 + 1], __builtin_amdgcn_perm(E16, w, 0x05030502u), B);
+                    }
+                    A += B;
                 }
+                const float sv = __uint_as_float(SC[u][r] << 16), bv = __uint_as_float(BI[u][r] << 16);
+                const float q = __builtin_fmaf(m.x, A, -m.y);
+                const float nv = __builtin_fmaf(sv, q, __builtin_fmaf(bv, m.z, acc[r]));
+                acc[r] = cok ? nv : acc[r];
             }
         }
     }
 
+    const int64_t yrow = GATHER ? y_row_of(a, t.start) : t.start;
 #pragma unroll
-    for (int r = 0; r < RPW; r++)
-#pragma unroll
-        for (int m = 0; m < MT; m++) {
-            if (m >= t.count) continue;
-            const float v = wave_sum(acc[r][m]);
-            if (lane == 0 && n0 + r < a.N) a.y[y_row_of(a, t.start + m) * a.N + n0 + r] = f32_to_bf16(v);
-        }
+    for (int r = 0; r < RPW; r++) {
+        const float v = wave_sum(acc[r]);
+        if (lane == 0 && n0 + r < a.N) a.y[yrow * a.N + n0 + r] = f32_to_bf16(v);
+    }
 }
 
-template <int BITS, int MT, int RPW, int S>
+template <int BITS, int RPW, int S>
 static bool launch_wv(const ValuShape& v, const QmvArgs& a, dim3 grid, size_t lds, hipStream_t st) {
-    if (v.WV == 4) qmv_valu_kernel<BITS, MT, RPW, S, 4><<<grid, 256, lds, st>>>(a);
-    else if (v.WV == 8) qmv_valu_kernel<BITS, MT, RPW, S, 8><<<grid, 512, lds, st>>>(a);
-    else if (v.WV == 16) qmv_valu_kernel<BITS, MT, RPW, S, 16><<<grid, 1024, lds, st>>>(a);
-    else return false;
+    const bool g = a.tiles != nullptr;
+    if (v.WV == 4) {
+        if (g) qmv_valu_kernel<BITS, RPW, S, 4, true><<<grid, 256, lds, st>>>(a);
+        else qmv_valu_kernel<BITS, RPW, S, 4, false><<<grid, 256, lds, st>>>(a);
+    } else if (v.WV == 8) {
+        if (g) qmv_valu_kernel<BITS, RPW, S, 8, true><<<grid, 512, lds, st>>>(a);
+        else qmv_valu_kernel<BITS, RPW, S, 8, false><<<grid, 512, lds, st>>>(a);
+    } else {
+        return false;
+    }
     return true;
 }
 
-template <int BITS, int MT>
+template <int BITS>
 static bool launch_shape(const ValuShape& v, const QmvArgs& a, dim3 grid, size_t lds, hipStream_t st) {
     if (v.RPW == 1) {
-        if (v.S == 1) return launch_wv<BITS, MT, 1, 1>(v, a, grid, lds, st);
-        if (v.S == 2) return launch_wv<BITS, MT, 1, 2>(v, a, grid, lds, st);
-        if (v.S == 4) return launch_wv<BITS, MT, 1, 4>(v, a, grid, lds, st);
-        if (v.S == 8) return launch_wv<BITS, MT, 1, 8>(v, a, grid, lds, st);
+        if (v.S == 1) return launch_wv<BITS, 1, 1>(v, a, grid, lds, st);
+        if (v.S == 2) return launch_wv<BITS, 1, 2>(v, a, grid, lds, st);
+        if (v.S == 4) return launch_wv<BITS, 1, 4>(v, a, grid, lds, st);
+        if (v.S == 8) return launch_wv<BITS, 1, 8>(v, a, grid, lds, st);
     }
-    if constexpr (MT == 1) {
-        if (v.RPW == 2) {
-            if (v.S == 1) return launch_wv<BITS, MT, 2, 1>(v, a, grid, lds, st);
-            if (v.S == 2) return launch_wv<BITS, MT, 2, 2>(v, a, grid, lds, st);
-            if (v.S == 4) return launch_wv<BITS, MT, 2, 4>(v, a, grid, lds, st);
-        }
-        if (v.RPW == 4) {
-            if (v.S == 1) return launch_wv<BITS, MT, 4, 1>(v, a, grid, lds, st);
-            if (v.S == 2) return launch_wv<BITS, MT, 4, 2>(v, a, grid, lds, st);
-        }
+    if (v.RPW == 2) {
+        if (v.S == 1) return launch_wv<BITS, 2, 1>(v, a, grid, lds, st);
+        if (v.S == 2) return launch_wv<BITS, 2, 2>(v, a, grid, lds, st);
+        if (v.S == 4) return launch_wv<BITS, 2, 4>(v, a, grid, lds, st);
+    }
+    if (v.RPW == 4) {
+        if (v.S == 1) return launch_wv<BITS, 4, 1>(v, a, grid, lds, st);
+        if (v.S == 2) return launch_wv<BITS, 4, 2>(v, a, grid, lds, st);
     }
     return false;
 }
 
-bool launch_qmv_valu(int bits, int mt, const ValuShape& v, const QmvArgs& a, dim3 grid,
-                     size_t lds, hipStream_t st) {
-    if (bits == 4) {
-        if (mt == 1) return launch_shape<4, 1>(v, a, grid, lds, st);
-        if (mt == 2) return launch_shape<4, 2>(v, a, grid, lds, st);
-        if (mt == 4) return launch_shape<4, 4>(v, a, grid, lds, st);
-    } else if (bits == 8) {
-        if (mt == 1) return launch_shape<8, 1>(v, a, grid, lds, st);
-        if (mt == 2) return launch_shape<8, 2>(v, a, grid, lds, st);
-        if (mt == 4) return launch_shape<8, 4>(v, a, grid, lds, st);
-    }
+bool launch_qmv_valu(int bits, const ValuShape& v, const QmvArgs& a, dim3 grid, size_t lds,
+                     hipStream_t st) {
+    if (bits == 4) return launch_shape<4>(v, a, grid, lds, st);
+    if (bits == 8) return launch_shape<8>(v, a, grid, lds, st);
     return false;
 }
 
