@@ -20,6 +20,8 @@
 // x is converted to fp16 for the dot products: exact for activations of
 // normal fp16 range (|x| < 65504; tiny values lose precision below 6e-5).
 #include "common.hpp"
+#include "qgemv.hpp"
+#include "vq_mfma.hpp"
 #include "../../include/knurlogic_amd.h"
 
 namespace kmi {
@@ -421,10 +423,14 @@ int kmi_vq_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int3
     return OK;
 }
 
+// Workspace: act [T*k, I], y [T*k, H] for the combine, then the expert sort
+// of the MFMA path (sized for up to 4096 experts).
+static size_t vq_act_bytes(int64_t T, int64_t I, int k) { return ((size_t)T * k * I * 2 + 255) & ~(size_t)255; }
+static size_t vq_y_bytes(int64_t T, int64_t H, int k) { return ((size_t)T * k * H * 2 + 255) & ~(size_t)255; }
+
 size_t kmi_vq_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k) {
     if (T <= 0 || H <= 0 || I <= 0 || k <= 0) return 0;
-    const size_t act = ((size_t)T * k * I * 2 + 255) & ~(size_t)255;
-    return act + (size_t)T * k * H * 2;          // act, then y for the combine
+    return vq_act_bytes(T, I, k) + vq_y_bytes(T, H, k) + sort_index_bytes(T * k, 4096, VQM_TILE_ROWS);
 }
 
 int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
@@ -451,25 +457,68 @@ int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, con
     }
     uint16_t* act = (uint16_t*)workspace;
     hipStream_t st = (hipStream_t)stream;
-    VqArgs g = {};
-    g.x = (const uint16_t*)x; g.lhs = nullptr; g.lhs_div = k; g.rhs = inds; g.P = T * k; g.X = T;
-    g.codes0 = codes_gate; g.sc0 = (const uint16_t*)scales_gate; g.cb0 = (const uint16_t*)codebook_gate;
-    g.codes1 = codes_up; g.sc1 = (const uint16_t*)scales_up; g.cb1 = (const uint16_t*)codebook_up;
-    g.kc = kc; g.y = act; g.E = E; g.N = I; g.K = H; g.erows = I;
-    g.sg = scale_group ? scale_group : (int)H;
-    rc = launch_vq(g, code_bytes, 2, st);
-    if (rc) return rc;
-    KMI_CHECK_LAUNCH("vq_gemv(glu)");
-    uint16_t* y = scores ? act + (((size_t)T * k * I + 127) & ~(size_t)127) : (uint16_t*)out;
-    VqArgs d = {};
-    d.x = act; d.lhs = nullptr; d.lhs_div = 1; d.rhs = inds; d.P = T * k; d.X = T * k;
-    d.codes0 = codes_down; d.sc0 = (const uint16_t*)scales_down; d.cb0 = (const uint16_t*)codebook_down;
-    d.codes1 = nullptr; d.sc1 = nullptr; d.cb1 = d.cb0; d.kc = kc;
-    d.y = y; d.E = E; d.N = H; d.K = I; d.erows = H;
-    d.sg = scale_group ? scale_group : (int)I;
-    rc = launch_vq(d, code_bytes, 1, st);
-    if (rc) return rc;
-    KMI_CHECK_LAUNCH("vq_gemv(down)");
+    const int64_t P = T * k;
+    const bool two_cb = codebook_up != codebook_gate;
+    // Each projection runs expert-major on MFMA where that kernel covers it
+    // (per-channel scales, K a multiple of 128), else per pair on the VALU.
+    const bool sortable = scale_group == 0 && E <= 4096 && P < (1LL << 24);
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+    const bool m_glu = sortable && vq_mfma_supported(H, code_bytes, kc, two_cb) && al16(codes_gate) &&
+                       al16(codes_up);
+    const bool m_down = sortable && vq_mfma_supported(I, code_bytes, kc, false) && al16(codes_down);
+    uint16_t* y = scores ? (uint16_t*)((char*)workspace + vq_act_bytes(T, I, k)) : (uint16_t*)out;
+    // one token: its k pairs are their own tiles (pair mode), no sort
+    const bool pair_mode = T == 1;
+    const int tile_rows = pair_mode ? 1 : (int)(P < VQM_TILE_ROWS ? P : VQM_TILE_ROWS);
+    SortedRows sr = {};
+    if ((m_glu || m_down) && !pair_mode) {
+        void* index_ws = (char*)workspace + vq_act_bytes(T, I, k) + vq_y_bytes(T, H, k);
+        // the sort zeroes y's rows of out-of-range experts (no tile holds them)
+        rc = launch_sort_rows(inds, P, 1, (int)E, VQM_TILE_ROWS, index_ws, m_down ? y : nullptr, H, st, &sr);
+        if (rc) return rc;
+    }
+    if (m_glu) {
+        VqmArgs g = {};
+        g.x = (const uint16_t*)x; g.X = T; g.lhs_magic = k > 1 ? (uint32_t)((0x100000000ULL + k - 1) / k) : 0u;
+        g.tiles = pair_mode ? nullptr : sr.tiles; g.sorted = sr.sorted; g.rhs = inds; g.E = E;
+        g.codes0 = codes_gate; g.sc0 = (const uint16_t*)scales_gate; g.cb0 = (const uint16_t*)codebook_gate;
+        g.codes1 = codes_up; g.sc1 = (const uint16_t*)scales_up; g.cb1 = (const uint16_t*)codebook_up;
+        g.kc = kc; g.y = act; g.N = I; g.K = H; g.erows = I; g.tile_rows = tile_rows;
+        rc = launch_vq_mfma(g, code_bytes, 2, pair_mode ? P : sr.max_tiles, st);
+        if (rc) return rc;
+        KMI_CHECK_LAUNCH("vq_mfma(glu)");
+    } else {
+        VqArgs g = {};
+        g.x = (const uint16_t*)x; g.lhs = nullptr; g.lhs_div = k; g.rhs = inds; g.P = P; g.X = T;
+        g.codes0 = codes_gate; g.sc0 = (const uint16_t*)scales_gate; g.cb0 = (const uint16_t*)codebook_gate;
+        g.codes1 = codes_up; g.sc1 = (const uint16_t*)scales_up; g.cb1 = (const uint16_t*)codebook_up;
+        g.kc = kc; g.y = act; g.E = E; g.N = I; g.K = H; g.erows = I;
+        g.sg = scale_group ? scale_group : (int)H;
+        rc = launch_vq(g, code_bytes, 2, st);
+        if (rc) return rc;
+        KMI_CHECK_LAUNCH("vq_gemv(glu)");
+    }
+    if (m_down) {
+        VqmArgs d = {};
+        d.x = act; d.X = P; d.lhs_magic = 0;
+        d.tiles = pair_mode ? nullptr : sr.tiles; d.sorted = sr.sorted; d.rhs = inds; d.E = E;
+        d.codes0 = codes_down; d.sc0 = (const uint16_t*)scales_down; d.cb0 = (const uint16_t*)codebook_down;
+        d.codes1 = nullptr; d.sc1 = nullptr; d.cb1 = d.cb0;
+        d.kc = kc; d.y = y; d.N = H; d.K = I; d.erows = H; d.tile_rows = tile_rows;
+        rc = launch_vq_mfma(d, code_bytes, 1, pair_mode ? P : sr.max_tiles, st);
+        if (rc) return rc;
+        KMI_CHECK_LAUNCH("vq_mfma(down)");
+    } else {
+        VqArgs d = {};
+        d.x = act; d.lhs = nullptr; d.lhs_div = 1; d.rhs = inds; d.P = P; d.X = P;
+        d.codes0 = codes_down; d.sc0 = (const uint16_t*)scales_down; d.cb0 = (const uint16_t*)codebook_down;
+        d.codes1 = nullptr; d.sc1 = nullptr; d.cb1 = d.cb0; d.kc = kc;
+        d.y = y; d.E = E; d.N = H; d.K = I; d.erows = H;
+        d.sg = scale_group ? scale_group : (int)I;
+        rc = launch_vq(d, code_bytes, 1, st);
+        if (rc) return rc;
+        KMI_CHECK_LAUNCH("vq_gemv(down)");
+    }
     if (scores) return kmi_moe_combine(y, scores, dtype, T, k, H, out, stream);
     return OK;
 }

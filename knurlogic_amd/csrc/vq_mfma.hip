@@ -1,0 +1,325 @@
+// VQ expert matmul on MFMA for gfx950, expert-major: the (token, expert)
+// pairs are grouped by expert on the GPU (the gather sort of qmv.hip), and a
+// tile of up to 16 rows routed to one expert shares every code gather.
+//
+//   What[o, i] = scale[o] * codebook[codes[o, i / 8]][i % 8]   (per channel)
+//   y[r, o]    = x[r] . What_e[o]   for the rows r of the tile
+//
+// v_mfma_f32_16x16x32_f16 takes, per lane, 8 fp16 values along k of one
+// row of B: exactly one 8-element codebook vector.  So lane (n = l % 16,
+// q = l / 16) gathers codebook[code] from LDS straight into its B operand
+// (no decode arithmetic) for weight row n, and A holds the tile's x rows
+// (fp16 in LDS) at the same k-run.  Lane q of a row owns the q-th quarter
+// of the row's codes, loaded contiguously; MFMA step kb takes code
+// q * CPR/4 + kb from every lane (any order of k works with one scale per
+// row).  One code per lane per MFMA: a 4-wave workgroup streams 256 codes
+// per step.
+//
+// Scales apply to the fp32 sums; each projection's result is rounded to
+// bf16, and two row sets (gate, up) end in Qwen3.5's _SwiGLU with the same
+// roundings as the VALU kernel in vq.hip.
+//
+// x is converted to fp16 (exact for |x| < 65504; tiny values lose precision
+// below 6e-5), as in vq.hip.
+#include "common.hpp"
+#include "vq_mfma.hpp"
+
+namespace kmi {
+
+namespace {
+
+typedef _Float16 vqm_f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 vqm_f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vqm_f16x8, a),
+                                                   __builtin_bit_cast(vqm_f16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float vqm_bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+__device__ __forceinline__ float vqm_f32_kept(double v) {
+    float f = (float)v;
+    asm volatile("" : "+v"(f));
+    return f;
+}
+
+// 8 bf16 -> 8 fp16
+__device__ __forceinline__ u32x4 bf16x8_to_f16x8(u32x4 v) {
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const vqm_f16x2 h = {(_Float16)__uint_as_float(v[q] << 16), (_Float16)__uint_as_float(v[q] & 0xffff0000u)};
+        o[q] = __builtin_bit_cast(uint32_t, h);
+    }
+    return o;
+}
+
+constexpr uint32_t NONE = 0x80000000u;      // an offset past every buffer: reads 0
+constexpr int WG = 256;                     // 4 waves
+constexpr int TM = VQM_TILE_ROWS;           // tile rows (MFMA M)
+
+}  // namespace
+
+// CB: index bytes (1, 2); NSET: row sets (2: gate, up + SwiGLU); LW: 32-bit
+// words of codes per lane; KS: waves sharing a 16-row group, each over
+// 1/KS of K (partials summed in LDS), so small grids still fill the chip.
+template <int CB, int NSET, int LW, int KS>
+__global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
+    constexpr int CPL = LW * 4 / CB;                 // codes per lane
+    constexpr int RW = 64 / KS;                      // weight rows per workgroup
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    // tile: (expert, first sorted row, rows) from the sort, or in pair mode
+    // (no tiles) pair blockIdx.y alone, its expert straight from rhs
+    int e, start, count;
+    if (a.tiles) {
+        const int32_t* tp = a.tiles + 3 * (int64_t)blockIdx.y;
+        count = tp[2];
+        if (count <= 0 || count > a.tile_rows) return;   // a tile never exceeds the staged rows
+        e = tp[0];
+        start = tp[1];
+    } else {
+        start = (int)blockIdx.y;
+        count = 1;
+        e = a.rhs[start];
+    }
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rg = wave / KS, kp = wave % KS;        // row group, K part
+    const int n = lane & 15, q = lane >> 4;
+    const int row = (int)blockIdx.x * RW + rg * 16 + n;
+    const int K = (int)a.K, CPR = K / 8;
+
+    if (e < 0 || e >= a.E) {                         // pair mode: an out-of-range expert gives 0
+        if (kp == 0 && q == 0 && row < a.N) a.y[(int64_t)start * a.N + row] = 0;
+        return;
+    }
+
+    const int xstride = K * 2 + 16;                  // bytes per staged x row (padded: rows on distinct banks)
+    const bool two_cb = NSET == 2 && a.cb1 != a.cb0;
+    const int ncb = a.kc * (two_cb ? 2 : 1);         // codebook pieces (16 B each)
+    unsigned char* cbl0 = smem;
+    unsigned char* cbl1 = smem + (two_cb ? (size_t)a.kc * 16 : 0);
+    unsigned char* xs = smem + (size_t)ncb * 16;
+    f32x4* red = (f32x4*)(xs + (size_t)a.tile_rows * xstride);   // [4 waves][NSET][64], KS > 1
+
+    // Sorted row ids of the tile, by scalar loads (tracked apart from the
+    // vector loads, so waiting for them drains nothing of the code stream;
+    // the sort kernel wrote `sorted` before this launch, and a constant
+    // address-space view makes uniform reads scalar).  x row = row id /
+    // lhs_div, by multiply-high with the host's magic (exact for the row
+    // ids the host admits).
+    typedef const __attribute__((address_space(4))) int32_t* cint_p;
+    const cint_p srt = (cint_p)(a.tiles ? a.sorted + start : nullptr);
+    auto rowid = [&](int m) -> uint32_t { return a.tiles ? (uint32_t)srt[m] : (uint32_t)start; };
+    auto xrow_of = [&](int m) -> int {
+        const uint32_t r = rowid(m);
+        return a.lhs_magic ? (int)__umulhi(r, a.lhs_magic) : (int)r;
+    };
+
+    // ---- staging: codebook entries (16 B) and the tile's x rows (8 bf16 ->
+    // 8 fp16 per piece).  The first codebook pieces and x rows 0 and 1 are
+    // loaded into registers ahead of the code stream (loads complete in
+    // issue order); anything more is staged before the stream is issued.
+    const __amdgpu_buffer_rsrc_t rcb0 = make_rsrc(a.cb0, (int64_t)a.kc * 16);
+    const __amdgpu_buffer_rsrc_t rcb1 = make_rsrc(a.cb1, (int64_t)a.kc * 16);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.X * a.K * 2);
+    auto cb_load = [&](int p) -> u32x4 {
+        const bool second = p >= a.kc;
+        const uint32_t off = p < ncb ? (uint32_t)(p - (second ? a.kc : 0)) * 16u : NONE;
+        return __builtin_amdgcn_raw_buffer_load_b128(second ? rcb1 : rcb0, (int)off, 0, 0);
+    };
+    auto cb_store = [&](int p, u32x4 v) {
+        if (p < ncb) *(u32x4*)(cbl0 + (size_t)p * 16) = v;     // cbl1 follows cbl0 directly
+    };
+    auto x_load = [&](int xr, int k8) -> u32x4 {
+        const uint32_t off = (xr >= 0 && xr < a.X && k8 < CPR) ? (uint32_t)(((int64_t)xr * K + k8 * 8) * 2) : NONE;
+        return __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+    };
+    auto x_store = [&](int m, int k8, u32x4 v) {
+        if (k8 < CPR) *(u32x4*)(xs + (size_t)m * xstride + k8 * 16) = bf16x8_to_f16x8(v);
+    };
+    for (int p = tid + 2 * WG; p < ncb; p += WG) cb_store(p, cb_load(p));
+    for (int m = 0; m < count; m++) {
+        const int xr = xrow_of(m);
+        for (int k8 = tid + (m < 2 ? WG : 0); k8 < CPR; k8 += WG) x_store(m, k8, x_load(xr, k8));
+    }
+    const int xr0 = xrow_of(0), xr1 = count > 1 ? xrow_of(1) : -1;
+    const u32x4 c0 = cb_load(tid), c1 = cb_load(tid + WG);
+    const u32x4 x0 = x_load(xr0, tid), x1 = x_load(xr1, tid);
+
+    // ---- this lane's codes and row scale (the HBM stream)
+    const int crow = row < a.N ? row : (int)a.N - 1;           // rows past N re-read row N-1, never stored
+    const int64_t ebase = (int64_t)e * a.erows;
+    const int cfirst = kp * (CPR / KS) + q * CPL;              // this lane's first code of its row
+    uint32_t cw[NSET][LW];
+    float scl[NSET];
+#pragma unroll
+    for (int s = 0; s < NSET; s++) {
+        const char* cb = (const char*)(s ? a.codes1 : a.codes0) + ebase * CPR * CB;
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(cb, a.N * CPR * CB);
+        const uint32_t lo = (uint32_t)((crow * CPR + cfirst) * CB);
+        if constexpr (LW % 4 == 0) {
+#pragma unroll
+            for (int i = 0; i < LW; i += 4) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rc, (int)(lo + i * 4), 0, AUX_NT);
+                cw[s][i] = v.x; cw[s][i + 1] = v.y; cw[s][i + 2] = v.z; cw[s][i + 3] = v.w;
+            }
+        } else if constexpr (LW % 2 == 0) {
+#pragma unroll
+            for (int i = 0; i < LW; i += 2) {
+                const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(lo + i * 4), 0, AUX_NT);
+                cw[s][i] = v.x; cw[s][i + 1] = v.y;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < LW; i++) cw[s][i] = __builtin_amdgcn_raw_buffer_load_b32(rc, (int)(lo + i * 4), 0, AUX_NT);
+        }
+        const __amdgpu_buffer_rsrc_t rsc = make_rsrc((s ? a.sc1 : a.sc0) + ebase, a.N * 2);
+        scl[s] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rsc, crow * 2, 0, 0));
+    }
+
+    // ---- staging -> LDS
+    cb_store(tid, c0);
+    cb_store(tid + WG, c1);
+    x_store(0, tid, x0);
+    if (count > 1) x_store(1, tid, x1);
+    lds_barrier();
+
+    // ---- MFMA over the lane's codes
+    f32x4 acc[NSET];
+#pragma unroll
+    for (int s = 0; s < NSET; s++) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int mrow = n < count ? n : count - 1;                 // A rows past the tile repeat a real row
+    const unsigned char* xa = xs + (size_t)mrow * xstride + (size_t)cfirst * 16;
+#pragma unroll
+    for (int kb = 0; kb < CPL; kb++) {
+        const u32x4 av = *(const u32x4*)(xa + kb * 16);
+#pragma unroll
+        for (int s = 0; s < NSET; s++) {
+            uint32_t code;
+            if constexpr (CB == 1) code = (cw[s][kb >> 2] >> (8 * (kb & 3))) & 0xffu;
+            else code = (cw[s][kb >> 1] >> (16 * (kb & 1))) & 0xffffu;
+            code = code < (uint32_t)a.kc ? code : (uint32_t)(a.kc - 1);
+            const u32x4 bv = *(const u32x4*)((s ? cbl1 : cbl0) + code * 16);
+            acc[s] = mfma_f16(av, bv, acc[s]);
+        }
+    }
+
+    // ---- K parts of a row group summed in LDS, in part order
+    if constexpr (KS > 1) {
+#pragma unroll
+        for (int s = 0; s < NSET; s++) red[(wave * NSET + s) * 64 + lane] = acc[s];
+        lds_barrier();
+        if (kp != 0) return;
+#pragma unroll
+        for (int s = 0; s < NSET; s++) {
+            f32x4 t = red[(wave * NSET + s) * 64 + lane];
+#pragma unroll
+            for (int j = 1; j < KS; j++) t += red[((wave + j) * NSET + s) * 64 + lane];
+            acc[s] = t;
+        }
+    }
+
+    // ---- epilogue: lane holds D[m = 4q + i][n]
+    if (row < a.N) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 4 * q + i;
+            if (m >= count) continue;
+            float out = vqm_bf16r(scl[0] * acc[0][i]);
+            if constexpr (NSET == 2) {     // round(round(silu_f32(gate)) * up)
+                const float up = vqm_bf16r(scl[1] * acc[1][i]);
+                const double g = (double)out;
+                out = vqm_bf16r(vqm_f32_kept(g / (1.0 + exp(-g)))) * up;
+            }
+            const int64_t r = a.tiles ? a.sorted[start + m] : start;
+            a.y[r * a.N + row] = f32_to_bf16(out);
+        }
+    }
+}
+
+size_t vq_mfma_lds(int64_t K, int kc, bool two_cb, int tile_rows, int nset, int ks) {
+    return (size_t)kc * 16 * (two_cb ? 2 : 1) + (size_t)tile_rows * (K * 2 + 16) +
+           (ks > 1 ? (size_t)4 * nset * 64 * 16 : 0);
+}
+
+// code words per lane at K split KS, or 0 if the lanes' code runs are not
+// whole 32-bit words
+static int vq_lw(int64_t K, int code_bytes, int ks) {
+    const int64_t b = K * code_bytes;
+    return b % (128 * ks) ? 0 : (int)(b / (128 * ks));
+}
+
+#define KMI_VQM_SHAPES(X)                                                          \
+    X(1, 4, 1) X(1, 2, 2) X(1, 1, 4)          /* K = 512, u8 */                     \
+    X(1, 6, 1) X(1, 3, 2)                     /* K = 768 */                         \
+    X(1, 8, 1) X(1, 4, 2) X(1, 2, 4)          /* K = 1024 */                        \
+    X(1, 12, 1) X(1, 6, 2) X(1, 3, 4)         /* K = 1536 */                        \
+    X(1, 16, 1) X(1, 8, 2) X(1, 4, 4)         /* K = 2048 */                        \
+    X(1, 22, 1) X(1, 11, 2)                   /* K = 2816 */                        \
+    X(1, 32, 1) X(1, 16, 2) X(1, 8, 4)        /* K = 4096 */                        \
+    X(2, 8, 1) X(2, 4, 2) X(2, 2, 4)          /* K = 512, u16 */                    \
+    X(2, 12, 1) X(2, 6, 2) X(2, 3, 4)         /* K = 768 */                         \
+    X(2, 16, 1) X(2, 8, 2) X(2, 4, 4)         /* K = 1024 */                        \
+    X(2, 24, 1) X(2, 12, 2) X(2, 6, 4)        /* K = 1536 */                        \
+    X(2, 32, 1) X(2, 16, 2) X(2, 8, 4)        /* K = 2048 */                        \
+    X(2, 22, 2) X(2, 11, 4)                   /* K = 2816 */                        \
+    X(2, 32, 2) X(2, 16, 4)                   /* K = 4096 */
+
+static bool vq_has_kernel(int code_bytes, int lw, int ks) {
+#define KMI_VQM_HAS(CB_, LW_, KS_) if (code_bytes == CB_ && lw == LW_ && ks == KS_) return true;
+    KMI_VQM_SHAPES(KMI_VQM_HAS)
+#undef KMI_VQM_HAS
+    return false;
+}
+
+bool vq_mfma_supported(int64_t K, int code_bytes, int kc, bool two_cb) {
+    if (K % 128) return false;
+    bool any = false;
+    for (int ks = 1; ks <= 4; ks *= 2) any = any || vq_has_kernel(code_bytes, vq_lw(K, code_bytes, ks), ks);
+    return any && vq_mfma_lds(K, kc, two_cb, TM, 2, 4) <= 160 * 1024;
+}
+
+int launch_vq_mfma(const VqmArgs& a, int code_bytes, int nset, int64_t ntiles, hipStream_t st) {
+    const bool two_cb = nset == 2 && a.cb1 != a.cb0;
+    if (a.tile_rows < 1 || a.tile_rows > TM || (!a.tiles && a.tile_rows != 1)) {
+        set_error("vq_mfma: tile rows %d", a.tile_rows);
+        return EINVAL_ARG;
+    }
+    // widest K split (up to 4) that the grid needs to reach ~512 workgroups
+    const int64_t base = ceil_div(a.N, 64) * ntiles;
+    int ks = 0;
+    for (int c = 1; c <= 4; c *= 2) {
+        if (!vq_has_kernel(code_bytes, vq_lw(a.K, code_bytes, c), c)) continue;
+        if (ks == 0 || base * ks < 512) ks = c;
+    }
+    if (ks == 0) {
+        set_error("vq_mfma: no kernel for K=%lld, %d-byte codes", (long long)a.K, code_bytes);
+        return EINVAL_ARG;
+    }
+    const int lw = vq_lw(a.K, code_bytes, ks);
+    const size_t lds = vq_mfma_lds(a.K, a.kc, two_cb, a.tile_rows, nset, ks);
+    const dim3 grid((unsigned)ceil_div(a.N, 64 / ks), (unsigned)ntiles);
+#define KMI_VQM_ONE(CB_, NS_, LW_, KS_)                                                          \
+    if (code_bytes == CB_ && nset == NS_ && lw == LW_ && ks == KS_) {                            \
+        static bool attr = false;                                                                \
+        if (!attr) {                                                                             \
+            (void)hipFuncSetAttribute((const void*)vq_mfma<CB_, NS_, LW_, KS_>,                  \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);   \
+            attr = true;                                                                         \
+        }                                                                                        \
+        vq_mfma<CB_, NS_, LW_, KS_><<<grid, WG, lds, st>>>(a);                                   \
+        return OK;                                                                               \
+    }
+#define KMI_VQM_LAUNCH(CB_, LW_, KS_) KMI_VQM_ONE(CB_, 1, LW_, KS_) KMI_VQM_ONE(CB_, 2, LW_, KS_)
+    KMI_VQM_SHAPES(KMI_VQM_LAUNCH)
+#undef KMI_VQM_LAUNCH
+#undef KMI_VQM_ONE
+    set_error("vq_mfma: no kernel for K=%lld, %d-byte codes", (long long)a.K, code_bytes);
+    return EINVAL_ARG;
+}
+
+}  // namespace kmi

@@ -1,0 +1,37 @@
+// Arguments and launcher of the MFMA VQ expert matmul (vq_mfma.hip).
+#pragma once
+
+#include "common.hpp"
+
+namespace kmi {
+
+constexpr int VQM_TILE_ROWS = 16;   // rows (tokens or pairs) per expert tile
+
+struct VqmArgs {
+    const uint16_t* x;          // bf16 [X, K]
+    int64_t X;
+    uint32_t lhs_magic;         // x row = umulhi(row id, lhs_magic); 0: x row = row id
+    const int32_t* tiles;       // [ntiles][3] (expert, start, count <= 16) over `sorted`; null:
+                                // pair mode, tile z = row id z alone with expert rhs[z]
+    const int32_t* sorted;      // row ids grouped by expert
+    const int32_t* rhs;         // pair mode: expert per row id
+    int64_t E;
+    const void* codes0;         // [E, erows, K/8] (u8 or u16)
+    const uint16_t* sc0;        // [E, erows] fp16, one scale per output row
+    const uint16_t* cb0;        // [kc, 8] fp16
+    const void* codes1;         // second row set (GLU: the up rows), or null
+    const uint16_t* sc1;
+    const uint16_t* cb1;
+    int kc;
+    uint16_t* y;                // [row ids, N] bf16
+    int64_t N, K, erows;
+    int tile_rows;              // largest tile count the launch stages (<= 16): sizes the LDS
+};
+
+size_t vq_mfma_lds(int64_t K, int kc, bool two_cb, int tile_rows, int nset, int ks);
+// K, index width, codebook size that the MFMA path covers (per-channel scales)
+bool vq_mfma_supported(int64_t K, int code_bytes, int kc, bool two_cb);
+// ntiles: grid rows (tiles of the sort, or the row ids in pair mode)
+int launch_vq_mfma(const VqmArgs& a, int code_bytes, int nset, int64_t ntiles, hipStream_t st);
+
+}  // namespace kmi
