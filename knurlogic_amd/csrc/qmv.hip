@@ -197,7 +197,10 @@ static ValuShape valu_shape(int64_t N, int64_t K, int bits, int64_t tiles) {
     if (v.S <= 2 && N * T / 4 >= 4096) v.RPW = 4;
     const int rpw = env_int("KMI_QMV_RPW", 0);
     if (rpw == 1 || (rpw == 2 && v.S <= 4) || (rpw == 4 && v.S <= 2)) v.RPW = rpw;
-    v.WV = 8;
+    // 4 waves while each thread stages at most two x pieces (K <= 4096):
+    // smaller workgroups start sooner; longer rows need 8 waves to keep the
+    // staging ahead of the weight stream short
+    v.WV = K <= 4096 ? 4 : 8;
     const int wv = env_int("KMI_QMV_WV", 0);
     if (wv == 4 || wv == 8) v.WV = wv;
     // no more waves per workgroup than the rows need

@@ -430,7 +430,7 @@ static size_t vq_y_bytes(int64_t T, int64_t H, int k) { return ((size_t)T * k * 
 
 size_t kmi_vq_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k) {
     if (T <= 0 || H <= 0 || I <= 0 || k <= 0) return 0;
-    return vq_act_bytes(T, I, k) + vq_y_bytes(T, H, k) + sort_index_bytes(T * k, 4096, VQM_TILE_ROWS);
+    return vq_act_bytes(T, I, k) + vq_y_bytes(T, H, k) + sort_index_bytes(T * k, 4096, 1);   // any tile size
 }
 
 int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
@@ -469,12 +469,18 @@ int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, con
     uint16_t* y = scores ? (uint16_t*)((char*)workspace + vq_act_bytes(T, I, k)) : (uint16_t*)out;
     // one token: its k pairs are their own tiles (pair mode), no sort
     const bool pair_mode = T == 1;
-    const int tile_rows = pair_mode ? 1 : (int)(P < VQM_TILE_ROWS ? P : VQM_TILE_ROWS);
+    // Tile rows: LDS holds a tile's x rows, sized for the largest tile, so
+    // few routed rows per expert take 8-row tiles (more workgroups fit a
+    // CU); the sort cuts every expert's rows into tiles of at most this.
+    const int64_t avg = ceil_div(P, E < P ? E : P);
+    int tile_rows = avg <= 4 ? 8 : VQM_TILE_ROWS;
+    if (tile_rows > P) tile_rows = (int)P;
+    if (pair_mode) tile_rows = 1;
     SortedRows sr = {};
     if ((m_glu || m_down) && !pair_mode) {
         void* index_ws = (char*)workspace + vq_act_bytes(T, I, k) + vq_y_bytes(T, H, k);
         // the sort zeroes y's rows of out-of-range experts (no tile holds them)
-        rc = launch_sort_rows(inds, P, 1, (int)E, VQM_TILE_ROWS, index_ws, m_down ? y : nullptr, H, st, &sr);
+        rc = launch_sort_rows(inds, P, 1, (int)E, tile_rows, index_ws, m_down ? y : nullptr, H, st, &sr);
         if (rc) return rc;
     }
     if (m_glu) {
