@@ -14,10 +14,10 @@
 //                 together), then either the weighted combine
 //                 round(sum_s round(y * score)) (qwen3_5.py:181-182) or
 //                 y itself.
-// Both stream packed 16-byte chunks with raw buffer loads and use the
-// factorized dequant of the decode GEMV: per group, s * sum(q x) +
-// (b - 128 s or b) * sum(x), the 4-bit nibbles unpacked to bf16 "128 + q"
-// and dotted with v_dot2_f32_bf16.
+// Both stream packed 16-byte chunks with raw buffer loads and decode them as
+// the decode GEMV does (qmv_common.hpp): codes as fp16 "1024 + q" against x
+// staged as fp16 with a power-of-two scale per chunk, v_dot2_f32_f16, and per
+// chunk s * sum(q x) + b * sum(x) in fp32.
 #include "qmv_common.hpp"
 #include "moe_tok.hpp"
 #include "../../include/knurlogic_amd.h"
@@ -33,67 +33,31 @@ __device__ __forceinline__ float f64_to_f32_kept(double v) {
     return f;
 }
 
-// Stage one x row (K bf16) into LDS as [piece][chunk] 16-byte slots with the
-// 4-bit unpack permutation, and its per-chunk sums.
-template <int BITS>
-__device__ __forceinline__ void stage_row(uint16_t* xs, float* xc, const u32x4* v, int c, int C) {
-    constexpr int XV = (128 / BITS) / 8;
-    float sum = 0.f;
-#pragma unroll
-    for (int v8 = 0; v8 < XV; v8++) *(u32x4*)(xs + (v8 * C + c) * 8) = permute8<BITS>(v[v8], sum);
-    xc[c] = sum;
-}
-
-// Partial dot product of one 16-byte weight chunk with the staged x chunk.
-template <int BITS>
-__device__ __forceinline__ float chunk_dot(const u32x4& W, const u32x4* xv) {
-    float A0 = 0.f, A1 = 0.f;
-    if constexpr (BITS == 4) {
-#pragma unroll
-        for (int wd = 0; wd < 4; wd++) {
-            const u32x4 q = nibbles_to_bf16_magic(W[wd]);
-            A0 = dot2(xv[wd][0], q[0], A0);
-            A1 = dot2(xv[wd][1], q[1], A1);
-            A0 = dot2(xv[wd][2], q[2], A0);
-            A1 = dot2(xv[wd][3], q[3], A1);
-        }
-    } else {
-#pragma unroll
-        for (int wd = 0; wd < 4; wd++) {
-            A0 = dot2(xv[wd >> 1][(wd & 1) * 2], bytes_to_bf16x2(W[wd], 0), A0);
-            A1 = dot2(xv[wd >> 1][(wd & 1) * 2 + 1], bytes_to_bf16x2(W[wd], 2), A1);
-        }
-    }
-    return A0 + A1;
-}
-
-// acc += s * dot + b' * xsum  (b' = b - 128 s for the 4-bit "128 + q" unpack)
-template <int BITS>
-__device__ __forceinline__ float apply_group(float acc, float dot, float xsum, uint32_t sb) {
-    const float sc = bf16_to_f32((uint16_t)(sb & 0xffffu));
-    const float bi = bf16_to_f32((uint16_t)(sb >> 16));
-    const float bb = (BITS == 4) ? __builtin_fmaf(-128.f, sc, bi) : bi;
-    return __builtin_fmaf(sc, dot, __builtin_fmaf(bb, xsum, acc));
-}
-
 // ---- gate + up + SwiGLU -----------------------------------------------------
-// grid (ceil(N / (WV*RPW)), T*k); K = H.  S 16-byte chunks per lane per row.
+// grid (ceil(N / (WV*RPW)), T*k); K = H.  The decode GEMV's streaming scheme
+// (qmv_valu.hip) over two row sets: x (one token row) staged as fp16 with a
+// power-of-two scale per chunk, codes decoded as fp16 "1024 + q", every load
+// of a wave issued up front with the wave-uniform part of its offset in the
+// scalar operand, each chunk-row's scale and bias loaded per lane ahead of
+// its weights.  S 16-byte chunk slots per lane per row (all of K).
 template <int BITS, int RPW, int S, int WV>
 __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
-    constexpr int CK = 128 / BITS, XV = CK / 8, ROWS = WV * RPW;
+    constexpr int NT = 64 * WV, CK = 128 / BITS, XV = CK / 8, ROWS = WV * RPW;
+    constexpr uint32_t NONE = QV_NONE;
     extern __shared__ __align__(16) unsigned char smem[];
     const int C = (int)(a.K / CK);
     const int wpr = (int)(a.K / (32 / BITS));
     const int gpr = (int)(a.K >> a.gs_shift);
-    uint16_t* xs = (uint16_t*)smem;                                        // [XV][C] 16-byte slots
-    float* xc = (float*)(smem + (size_t)XV * C * 16);                      // [C]
-    uint32_t* sbl = (uint32_t*)(xc + C);                                   // [2][ROWS][gpr]
+    const int P = (int)(a.K >> 3);                   // x pieces of the row
+    u32x4* xs = (u32x4*)smem;                                  // [XV][C] fp16 pieces
+    float4* xm = (float4*)(smem + (size_t)XV * C * 16);        // [C] {scale, correction, sum}
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int p = blockIdx.y;
     const int64_t t = p / a.k;
     const int e = a.inds[p];
-    const int nwg = (int)blockIdx.x * ROWS, n0 = nwg + wave * RPW;
+    const int n0 = (int)blockIdx.x * ROWS + wave * RPW;
     const bool ok_e = e >= 0 && e < a.E;
     const int64_t eoff = (int64_t)(ok_e ? e : 0) * a.erows;
     const int64_t wbytes = ok_e ? a.N * (int64_t)wpr * 4 : 0, sbytes = ok_e ? a.N * (int64_t)gpr * 2 : 0;
@@ -104,61 +68,82 @@ __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
     const __amdgpu_buffer_rsrc_t rs1 = make_rsrc(a.s1 + eoff * gpr, sbytes);
     const __amdgpu_buffer_rsrc_t rb1 = make_rsrc(a.b1 + eoff * gpr, sbytes);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + t * a.K, a.K * 2);
+    auto xvo = [&](int q) -> uint32_t { return q < P ? (uint32_t)q * 16u : NONE; };
 
-    // x chunks first (one per thread for C <= 64*WV), then every weight load
-    const int NT = 64 * WV;
-    u32x4 xr[XV];
+    // (0) x pieces beyond two per thread (long rows), before any weight load
+    if (P > 2 * NT) {
+        for (int q = tid + 2 * NT; q - (tid & 3) < P; q += NT)
+            stage_x16<BITS>(q, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(q), 0, 0), P, C, xs, xm);
+    }
+    // (1) this thread's x pieces, then scales/biases and weights of both sets
+    const u32x4 xr0 = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(tid), 0, 0);
+    const u32x4 xr1 = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(tid + NT), 0, 0);
+    const int full = C >> 6;
+    const bool in_tail = lane < (C & 63);
+    const uint32_t vw = (uint32_t)lane * 16u;
+    const uint32_t vg = (uint32_t)((lane * CK) >> a.gs_shift) * 2u;
+    const uint32_t vwt = in_tail ? vw : NONE, vgt = in_tail ? vg : NONE;
+    uint32_t wrow[RPW], srow[RPW];
 #pragma unroll
-    for (int v8 = 0; v8 < XV; v8++)
-        xr[v8] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)((tid * CK + v8 * 8) * 2), 0, 0);
+    for (int r = 0; r < RPW; r++) {           // rows past N re-read row N-1 (never stored)
+        const uint32_t row = (uint32_t)(n0 + r < a.N ? n0 + r : a.N - 1);
+        wrow[r] = row * (uint32_t)wpr * 4u;
+        srow[r] = row * (uint32_t)gpr * 2u;
+    }
     u32x4 W0[S][RPW], W1[S][RPW];
+    uint32_t S0[S][RPW], B0[S][RPW], S1[S][RPW], B1[S][RPW];
 #pragma unroll
     for (int u = 0; u < S; u++) {
-        const int c = lane + 64 * u;
+        const uint32_t vo = u < full ? vg : u == full ? vgt : NONE;
+        const uint32_t so = (uint32_t)(((64 * u * CK) >> a.gs_shift) * 2);
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            const int off = (int)(((uint32_t)(n0 + r) * (uint32_t)wpr + (uint32_t)c * 4u) * 4u);
-            W0[u][r] = __builtin_amdgcn_raw_buffer_load_b128(rw0, off, 0, AUX_NT);
-            W1[u][r] = __builtin_amdgcn_raw_buffer_load_b128(rw1, off, 0, AUX_NT);
+            S0[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs0, (int)vo, (int)(srow[r] + so), 0);
+            B0[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb0, (int)vo, (int)(srow[r] + so), 0);
+            S1[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs1, (int)vo, (int)(srow[r] + so), 0);
+            B1[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb1, (int)vo, (int)(srow[r] + so), 0);
         }
     }
-    // scales / biases of both row sets -> LDS (rows past N read 0)
-    for (int idx = tid; idx < ROWS * gpr; idx += NT) {
-        const int rl = idx / gpr, g = idx - rl * gpr;
-        const int off = (int)(((uint32_t)(nwg + rl) * (uint32_t)gpr + (uint32_t)g) * 2u);
-        sbl[idx] = __builtin_amdgcn_raw_buffer_load_b16(rs0, off, 0, 0) |
-                   ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb0, off, 0, 0) << 16);
-        sbl[ROWS * gpr + idx] = __builtin_amdgcn_raw_buffer_load_b16(rs1, off, 0, 0) |
-                                ((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rb1, off, 0, 0) << 16);
-    }
-    if (tid < C) stage_row<BITS>(xs, xc, xr, tid, C);
-    for (int c = tid + NT; c < C; c += NT) {           // wide rows: the rest of x
-        u32x4 v[XV];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int v8 = 0; v8 < XV; v8++)
-            v[v8] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)((c * CK + v8 * 8) * 2), 0, 0);
-        stage_row<BITS>(xs, xc, v, c, C);
+    for (int u = 0; u < S; u++) {
+        const uint32_t vo = u < full ? vw : u == full ? vwt : NONE;
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            W0[u][r] = __builtin_amdgcn_raw_buffer_load_b128(rw0, (int)vo, (int)(wrow[r] + (uint32_t)u * 1024u), AUX_NT);
+            W1[u][r] = __builtin_amdgcn_raw_buffer_load_b128(rw1, (int)vo, (int)(wrow[r] + (uint32_t)u * 1024u), AUX_NT);
+        }
     }
+
+    // (2) x -> LDS
+    stage_x16<BITS>(tid, xr0, P, C, xs, xm);
+    if (P > NT) stage_x16<BITS>(tid + NT, xr1, P, C, xs, xm);
     lds_barrier();
 
+    const Magic16 mk = magic16();
     float acc0[RPW], acc1[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; r++) acc0[r] = acc1[r] = 0.f;
 #pragma unroll
     for (int u = 0; u < S; u++) {
+        if (64 * u >= C) break;                       // wave-uniform
         const int c = lane + 64 * u;
-        if (c >= C) continue;
-        const int g = (c * CK) >> a.gs_shift;
+        const bool cok = c < C;
+        const int cc = cok ? c : 0;
         u32x4 xv[XV];
 #pragma unroll
-        for (int v8 = 0; v8 < XV; v8++) xv[v8] = *(const u32x4*)(xs + (v8 * C + c) * 8);
-        const float X = xc[c];
+        for (int v = 0; v < XV; v++) xv[v] = xs[v * C + cc];
+        const float4 m = xm[cc];
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            const int rl = wave * RPW + r;
-            acc0[r] = apply_group<BITS>(acc0[r], chunk_dot<BITS>(W0[u][r], xv), X, sbl[rl * gpr + g]);
-            acc1[r] = apply_group<BITS>(acc1[r], chunk_dot<BITS>(W1[u][r], xv), X,
-                                        sbl[(ROWS + rl) * gpr + g]);
+            const float q0 = chunk_qx<BITS>(W0[u][r], xv, m, mk);
+            const float q1 = chunk_qx<BITS>(W1[u][r], xv, m, mk);
+            const float g0 = __builtin_fmaf(__uint_as_float(S0[u][r] << 16), q0,
+                                            __builtin_fmaf(__uint_as_float(B0[u][r] << 16), m.z, acc0[r]));
+            const float g1 = __builtin_fmaf(__uint_as_float(S1[u][r] << 16), q1,
+                                            __builtin_fmaf(__uint_as_float(B1[u][r] << 16), m.z, acc1[r]));
+            acc0[r] = cok ? g0 : acc0[r];
+            acc1[r] = cok ? g1 : acc1[r];
         }
     }
 #pragma unroll
@@ -174,96 +159,133 @@ __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
 }
 
 // ---- down projection + combine ----------------------------------------------
-// grid (ceil(N / (WV*RPW)), T); K = I.  Lane items (slot, chunk): U per lane.
+// grid (ceil(N / (WV*RPW)), T); K = I.  All k slots of token t in one
+// workgroup: their act rows staged once (fp16, as in the gate/up kernel),
+// lanes spread over (slot, chunk) items (U per lane) so short rows keep every
+// lane busy and all k experts' loads are in flight together.  The item's
+// expert differs per lane, so the expert part of an offset is per lane and
+// the row part (wave-uniform) is in the scalar operand.
 template <int BITS, int KMAX, int U, int RPW, int WV>
 __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
-    constexpr int CK = 128 / BITS, XV = CK / 8, ROWS = WV * RPW;
+    constexpr int NT = 64 * WV, CK = 128 / BITS, XV = CK / 8;
+    constexpr int XREG = 4;                          // x pieces per thread held in registers
+    constexpr uint32_t NONE = QV_NONE;
     extern __shared__ __align__(16) unsigned char smem[];
     const int C = (int)(a.K / CK);
     const int k = a.k;
     const int wpr = (int)(a.K / (32 / BITS));
     const int gpr = (int)(a.K >> a.gs_shift);
-    uint16_t* xs = (uint16_t*)smem;                                        // [k][XV][C] slots
-    float* xc = (float*)(smem + (size_t)k * XV * C * 16);                  // [k][C]
-    uint32_t* sbl = (uint32_t*)(xc + k * C);                               // [k][ROWS][gpr]
+    const int P = (int)(a.K >> 3);                   // x pieces per slot row
+    const size_t slot_bytes = (size_t)XV * C * 16 + (size_t)C * 16;
+    auto xs_of = [&](int s) { return (u32x4*)(smem + s * slot_bytes); };
+    auto xm_of = [&](int s) { return (float4*)(smem + s * slot_bytes + (size_t)XV * C * 16); };
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int NT = 64 * WV;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t t = blockIdx.y;
-    const int nwg = (int)blockIdx.x * ROWS, n0 = nwg + wave * RPW;
-    const int64_t wexp = a.N * (int64_t)wpr;                                // words per expert
-    const int64_t gexp = a.N * (int64_t)gpr;
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w0, a.E * wexp * 4);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s0, a.E * gexp * 2);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b0, a.E * gexp * 2);
+    const int n0 = (int)blockIdx.x * (WV * RPW) + wave * RPW;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w0, a.E * a.N * (int64_t)wpr * 4);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s0, a.E * a.N * (int64_t)gpr * 2);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b0, a.E * a.N * (int64_t)gpr * 2);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + t * k * a.K, (int64_t)k * a.K * 2);
 
-    int ex[KMAX];                      // experts of the k slots (an invalid one reads zeros)
-#pragma unroll
-    for (int s = 0; s < KMAX; s++) {
-        const int e = s < k ? a.inds[t * k + s] : -1;
-        ex[s] = (e >= 0 && e < a.E) ? e : -1;
-    }
-    auto ebase = [&](int s) -> uint32_t {  // expert word base, or past the buffer
-        return ex[s] >= 0 ? (uint32_t)(ex[s] * wexp) : 0x20000000u;
+    // x pieces q = tid + NT j of the k slot rows: slot q / P, piece q % P
+    // (P is a multiple of 4, so a chunk's pieces stay in one lane quad)
+    auto xq = [&](int q, int& sl, int& pc) {
+        sl = q / P;
+        pc = q - sl * P;
+        if (sl >= k) { sl = 0; pc = P; }              // past the slots: stage nothing
     };
+    for (int q = tid + XREG * NT; q - (tid & 3) < k * P; q += NT) {
+        int sl, pc;
+        xq(q, sl, pc);
+        const uint32_t o = pc < P ? (uint32_t)((sl * a.K + pc * 8) * 2) : NONE;
+        stage_x16<BITS>(pc, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)o, 0, 0), P, C, xs_of(sl), xm_of(sl));
+    }
+    u32x4 xr[XREG];
+#pragma unroll
+    for (int j = 0; j < XREG; j++) {
+        int sl, pc;
+        xq(tid + j * NT, sl, pc);
+        const uint32_t o = pc < P ? (uint32_t)((sl * a.K + pc * 8) * 2) : NONE;
+        xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)o, 0, 0);
+    }
 
-    // this lane's items: i = lane + 64 u -> slot i / C, chunk i % C
-    u32x4 W[U][RPW];
-    int sl[U];
+    // this lane's items i = lane + 64 u: slot i / C, chunk i % C; per-lane
+    // expert offsets, rows in the scalar offset
+    // the k experts by scalar loads (the sort-free caller wrote inds before
+    // this launch; uniform reads of a constant address-space view are scalar
+    // and do not wait behind the vector loads), then each lane's by select
+    typedef const __attribute__((address_space(4))) int32_t* cint_p;
+    const cint_p ic = (cint_p)(a.inds + t * k);
+    int ex[KMAX];
+#pragma unroll
+    for (int s = 0; s < KMAX; s++) ex[s] = s < k ? ic[s] : -1;
+    int isl[U];
+    uint32_t vwo[U], vso[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const int i = lane + 64 * u;
-        const int s = i / C, c = i - (i / C) * C;
-        sl[u] = i < k * C ? s : -1;
-        uint32_t eb = 0x20000000u;
-#pragma unroll
-        for (int q = 0; q < KMAX; q++)
-            if (q == s) eb = ebase(q);
-        if (sl[u] < 0) eb = 0x20000000u;
-#pragma unroll
-        for (int r = 0; r < RPW; r++)
-            W[u][r] = __builtin_amdgcn_raw_buffer_load_b128(
-                rw, (int)((eb + (uint32_t)(n0 + r) * (uint32_t)wpr + (uint32_t)c * 4u) * 4u), 0, AUX_NT);
-    }
-    // x rows of the k slots, scales / biases -> LDS
-    for (int idx = tid; idx < k * C; idx += NT) {
-        const int s = idx / C, c = idx - s * C;
-        u32x4 v[XV];
-#pragma unroll
-        for (int v8 = 0; v8 < XV; v8++)
-            v[v8] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(((int64_t)s * a.K + c * CK + v8 * 8) * 2), 0, 0);
-        stage_row<BITS>(xs + (size_t)s * XV * C * 8, xc + s * C, v, c, C);
-    }
-    for (int idx = tid; idx < k * ROWS * gpr; idx += NT) {
-        const int s = idx / (ROWS * gpr), rem = idx - s * ROWS * gpr;
-        const int rl = rem / gpr, g = rem - rl * gpr;
+        const int sidx = i / C, c = i - sidx * C;
         int e = -1;
 #pragma unroll
-        for (int q = 0; q < KMAX; q++)
-            if (q == s) e = ex[q];
-        const uint32_t off = e >= 0 ? (uint32_t)((e * gexp + (int64_t)(nwg + rl) * gpr + g) * 2) : 0x40000000u;
-        const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)off, 0, 0);
-        const uint32_t bv = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)off, 0, 0);
-        sbl[idx] = (nwg + rl < a.N) ? (sv | (bv << 16)) : 0u;
+        for (int s = 0; s < KMAX; s++) e = sidx == s ? ex[s] : e;
+        const bool ok = sidx < k && e >= 0 && e < a.E;
+        isl[u] = sidx < k ? sidx : -1;
+        vwo[u] = ok ? (uint32_t)((((int64_t)e * a.N) * wpr + (int64_t)c * 4) * 4) : NONE;
+        vso[u] = ok ? (uint32_t)((((int64_t)e * a.N) * gpr + ((c * CK) >> a.gs_shift)) * 2) : NONE;
+    }
+    uint32_t wrow[RPW], srow[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {           // rows past N re-read row N-1 (never stored)
+        const uint32_t row = (uint32_t)(n0 + r < a.N ? n0 + r : a.N - 1);
+        wrow[r] = row * (uint32_t)wpr * 4u;
+        srow[r] = row * (uint32_t)gpr * 2u;
+    }
+    u32x4 W[U][RPW];
+    uint32_t SC[U][RPW], BI[U][RPW];
+#pragma unroll
+    for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            SC[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)vso[u], (int)srow[r], 0);
+            BI[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)vso[u], (int)srow[r], 0);
+        }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int r = 0; r < RPW; r++)
+            W[u][r] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)vwo[u], (int)wrow[r], AUX_NT);
+
+    // x -> LDS
+#pragma unroll
+    for (int j = 0; j < XREG; j++) {
+        if (j * NT >= k * P) break;                   // wave-uniform
+        int sl, pc;
+        xq(tid + j * NT, sl, pc);
+        stage_x16<BITS>(pc, xr[j], P, C, xs_of(sl), xm_of(sl));
     }
     lds_barrier();
 
+    const Magic16 mk = magic16();
     float acc[U][RPW];
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const int i = lane + 64 * u;
-        const int s = sl[u] < 0 ? 0 : sl[u], c = i - (i / C) * C;
+        const int sl = isl[u] < 0 ? 0 : isl[u];
+        const int c = isl[u] < 0 ? 0 : i - sl * C;
+        const u32x4* xsp = xs_of(sl);
         u32x4 xv[XV];
 #pragma unroll
-        for (int v8 = 0; v8 < XV; v8++) xv[v8] = *(const u32x4*)(xs + ((size_t)s * XV * C + v8 * C + c) * 8);
-        const float X = xc[s * C + c];
-        const int g = (c * CK) >> a.gs_shift;
+        for (int v = 0; v < XV; v++) xv[v] = xsp[v * C + c];
+        const float4 m = xm_of(sl)[c];
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            const float v = apply_group<BITS>(0.f, chunk_dot<BITS>(W[u][r], xv), X,
-                                              sbl[(s * ROWS + wave * RPW + r) * gpr + g]);
-            acc[u][r] = sl[u] < 0 ? 0.f : v;
+            const float q = chunk_qx<BITS>(W[u][r], xv, m, mk);
+            const float v = __builtin_fmaf(__uint_as_float(SC[u][r] << 16), q,
+                                           __uint_as_float(BI[u][r] << 16) * m.z);
+            acc[u][r] = isl[u] < 0 ? 0.f : v;
         }
     }
     // per slot: sum this lane's items of the slot, then over the wave
@@ -275,7 +297,7 @@ __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
             if (s >= k) break;
             float v = 0.f;
 #pragma unroll
-            for (int u = 0; u < U; u++) v += sl[u] == s ? acc[u][r] : 0.f;
+            for (int u = 0; u < U; u++) v += isl[u] == s ? acc[u][r] : 0.f;
             const float y = bf16r(wave_sum(v));
             if (a.scores) {
                 comb += (double)bf16r(y * bf16_to_f32(a.scores[t * k + s]));
@@ -290,16 +312,7 @@ __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
 
 constexpr int TOK_WV = 4;
 
-// Weight rows per wave: 1 while a call has few workgroups' worth of rows,
-// else 4 (the staged x row is then shared by 16 rows per workgroup).
-static int tok_rpw(int64_t N, int64_t wgs_per_row_tile) {
-    return ceil_div(N, TOK_WV) * wgs_per_row_tile >= 2048 ? 4 : 1;
-}
 
-static int glu_lds(int64_t K, int bits, int gs, int rpw) {
-    const int64_t CK = 128 / bits, C = K / CK;
-    return (int)((128 / bits / 8) * C * 16 + C * 4 + 2 * TOK_WV * rpw * (K / gs) * 4);
-}
 
 }  // namespace kmi
 
@@ -310,17 +323,27 @@ namespace kmi {
 
 int launch_moe_glu_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
     const int64_t CK = 128 / bits, C = a.K / CK;
-    const int S = (int)ceil_div(C, 64);
-    const int rpw = tok_rpw(a.N, a.T * a.k);
-    const dim3 grid((unsigned)ceil_div(a.N, TOK_WV * rpw), (unsigned)(a.T * a.k));
-    const size_t lds = (size_t)glu_lds(a.K, bits, 1 << a.gs_shift, rpw);
-#define KMI_GLU(B, R, SS)                                                               \
-    if (bits == B && rpw == R && S == SS) {                                             \
-        moe_glu_tok<B, R, SS, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a);              \
+    const int64_t slots = ceil_div(C, 64);
+    const int S = slots <= 1 ? 1 : slots <= 2 ? 2 : slots <= 4 ? 4 : 0;
+    if (S == 0) {
+        set_error("switch_glu: no gate/up kernel for %lld chunks per row", (long long)C);
+        return EINVAL_ARG;
+    }
+    // rows per wave: as many as keep >= 2048 waves (2 per SIMD) in the grid,
+    // within 8 chunk-rows of loads per set
+    const int64_t pairs = a.T * a.k;
+    int rpw = 1;
+    if (S <= 4 && a.N * pairs / 2 >= 2048) rpw = 2;
+    if (S <= 2 && a.N * pairs / 4 >= 2048) rpw = 4;
+    const dim3 grid((unsigned)ceil_div(a.N, TOK_WV * rpw), (unsigned)pairs);
+    const size_t lds = (size_t)a.K * 2 + (size_t)C * 16;
+#define KMI_GLU(R, SS)                                                                  \
+    if (rpw == R && S == SS) {                                                          \
+        if (bits == 4) moe_glu_tok<4, R, SS, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a); \
+        else moe_glu_tok<8, R, SS, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a);           \
         return OK;                                                                      \
     }
-    KMI_GLU(4, 1, 1) KMI_GLU(4, 1, 2) KMI_GLU(4, 1, 4) KMI_GLU(8, 1, 1) KMI_GLU(8, 1, 2) KMI_GLU(8, 1, 4)
-    KMI_GLU(8, 1, 8) KMI_GLU(4, 4, 1) KMI_GLU(4, 4, 2) KMI_GLU(8, 4, 1) KMI_GLU(8, 4, 2)
+    KMI_GLU(1, 1) KMI_GLU(1, 2) KMI_GLU(1, 4) KMI_GLU(2, 1) KMI_GLU(2, 2) KMI_GLU(2, 4) KMI_GLU(4, 1) KMI_GLU(4, 2)
 #undef KMI_GLU
     set_error("switch_glu: no gate/up kernel for %lld chunks per row", (long long)C);
     return EINVAL_ARG;
@@ -329,21 +352,22 @@ int launch_moe_glu_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
 int launch_moe_down_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
     const int64_t CK = 128 / bits, C = a.K / CK;
     const int U = (int)ceil_div((int64_t)a.k * C, 64);
-    const int rpw = U <= 4 ? tok_rpw(a.N, a.T) : 1;
+    // two rows per wave while the grid keeps >= 2048 waves
+    const int rpw = U <= 4 && a.N * a.T / 2 >= 2048 ? 2 : 1;
     const dim3 grid((unsigned)ceil_div(a.N, TOK_WV * rpw), (unsigned)a.T);
-    const size_t lds = (size_t)a.k * ((128 / bits / 8) * C * 16 + C * 4) +
-                       (size_t)a.k * TOK_WV * rpw * (a.K >> a.gs_shift) * 4;
-#define KMI_DOWN(B, KM, UU, R)                                                          \
-    if (bits == B && a.k <= KM && U == UU && rpw == R) {                                \
-        moe_down_tok<B, KM, UU, R, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a);         \
+    const size_t lds = (size_t)a.k * ((size_t)a.K * 2 + (size_t)C * 16);
+    if (a.E * a.N * (a.K * bits / 8) >= (1LL << 31)) {
+        set_error("switch_glu: down experts past 2 GiB");
+        return EINVAL_ARG;
+    }
+#define KMI_DOWN(KM, UU, R)                                                             \
+    if (a.k <= KM && U == UU && rpw == R) {                                             \
+        if (bits == 4) moe_down_tok<4, KM, UU, R, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a); \
+        else moe_down_tok<8, KM, UU, R, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a);            \
         return OK;                                                                      \
     }
-    KMI_DOWN(4, 8, 1, 1) KMI_DOWN(4, 8, 2, 1) KMI_DOWN(4, 8, 3, 1) KMI_DOWN(4, 8, 4, 1)
-    KMI_DOWN(4, 8, 6, 1) KMI_DOWN(4, 8, 8, 1)
-    KMI_DOWN(8, 8, 1, 1) KMI_DOWN(8, 8, 2, 1) KMI_DOWN(8, 8, 3, 1) KMI_DOWN(8, 8, 4, 1)
-    KMI_DOWN(8, 8, 6, 1) KMI_DOWN(8, 8, 8, 1)
-    KMI_DOWN(4, 8, 1, 4) KMI_DOWN(4, 8, 2, 4) KMI_DOWN(4, 8, 3, 4) KMI_DOWN(4, 8, 4, 4)
-    KMI_DOWN(8, 8, 1, 4) KMI_DOWN(8, 8, 2, 4) KMI_DOWN(8, 8, 3, 4) KMI_DOWN(8, 8, 4, 4)
+    KMI_DOWN(8, 1, 1) KMI_DOWN(8, 2, 1) KMI_DOWN(8, 3, 1) KMI_DOWN(8, 4, 1) KMI_DOWN(8, 6, 1) KMI_DOWN(8, 8, 1)
+    KMI_DOWN(8, 1, 2) KMI_DOWN(8, 2, 2) KMI_DOWN(8, 3, 2) KMI_DOWN(8, 4, 2)
 #undef KMI_DOWN
     set_error("switch_glu: no down kernel for k=%d, %lld chunks per row", a.k, (long long)C);
     return EINVAL_ARG;

@@ -116,6 +116,124 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 
+// ---- fp16 "1024 + q" decode shared by the VALU decode kernels -------------
+// A code becomes fp16 1024 + q with one v_and_or_b32 per pair: a low nibble
+// (or a byte) lands in the low mantissa bits of 0x6400 = 1024.0, and a high
+// nibble is left in place as 1024 + 16 q, also exact (fp16 has 10 mantissa
+// bits).  x is staged as fp16 with a power-of-two scale per 16-byte weight
+// chunk (the chunk's largest |x| maps to [2^14, 2^15)), exact for every bf16
+// value, with the chunk's {scale, correction, sum} beside it, so that
+//   chunk_qx = scale * (A_lo + A_hi / 16) - correction = sum(q x) over the chunk.
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// A constant kept in a VGPR.  Held in a register (not an instruction
+// literal), a mask-and-or pair folds into one v_and_or_b32.
+__device__ __forceinline__ uint32_t vconst(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+__device__ __forceinline__ float fdot2_f16(uint32_t x, uint32_t w, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), __builtin_bit_cast(f16x2_t, w), c, false);
+}
+
+__device__ __forceinline__ uint32_t pk_f16(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false)));
+}
+
+constexpr uint32_t QV_NONE = 0x80000000u;   // a buffer offset past every buffer: reads 0
+
+// Piece p (x[8p .. 8p+8)) of a row -> xs [XV][C] 16-byte fp16 slots and the
+// chunk record xm [C] = {scale, correction, sum}.  Every lane of the wave runs
+// this (the quad reductions read neighbours); only pieces p < P store.
+template <int BITS>
+__device__ __forceinline__ void stage_x16(int p, u32x4 raw, int P, int C, u32x4* xs, float4* xm) {
+    constexpr int XV = (128 / BITS) / 8;            // pieces per chunk: 4 or 2
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f[2 * i] = __uint_as_float(raw[i] << 16);
+        f[2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
+    }
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) am = fmaxf(am, fabsf(f[i]));
+    am = dpp_max<0xb1>(am);                           // quad_perm [1,0,3,2]
+    if constexpr (XV == 4) am = dpp_max<0x4e>(am);    // quad_perm [2,3,0,1]
+    int e = (int)((__float_as_uint(am) >> 23) & 0xffu);
+    e = e < 15 ? 15 : e;
+    const float mult = __uint_as_float((uint32_t)(e - 14) << 23);   // 2^(e-141)
+    const float inv = __uint_as_float((uint32_t)(268 - e) << 23);   // 2^(141-e)
+    u32x4 o;
+    float lo, hi = 0.f;
+    if constexpr (BITS == 4) {
+        // dword i pairs (x_i, x_{i+4}): the codes one and-or places there
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = pk_f16(f[i] * inv, f[i + 4] * inv);
+        lo = (f[0] + f[2]) + (f[4] + f[6]);           // under low nibbles
+        hi = (f[1] + f[3]) + (f[5] + f[7]);           // under high nibbles
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = pk_f16(f[2 * i] * inv, f[2 * i + 1] * inv);
+        lo = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+    }
+    lo = dpp_add<0xb1, 0xf>(lo);
+    if constexpr (XV == 4) lo = dpp_add<0x4e, 0xf>(lo);
+    if constexpr (BITS == 4) {
+        hi = dpp_add<0xb1, 0xf>(hi);
+        hi = dpp_add<0x4e, 0xf>(hi);
+    }
+    if (p < P) {
+        const int c = p / XV, v = p % XV;
+        xs[v * C + c] = o;
+        if (v == 0) {
+            const float corr = BITS == 4 ? 1024.f * __builtin_fmaf(hi, 0.0625f, lo) : 1024.f * lo;
+            xm[c] = make_float4(mult, corr, lo + hi, 0.f);
+        }
+    }
+}
+
+// The masks and the 1024.0 pair held in VGPRs (see vconst).
+struct Magic16 {
+    uint32_t mlo, mhi, e16;
+};
+__device__ __forceinline__ Magic16 magic16() {
+    return Magic16{vconst(0x000F000Fu), vconst(0x00F000F0u), vconst(0x64006400u)};
+}
+
+// sum(q x) over one 16-byte chunk of codes W against its staged x pieces xv
+// and record m (see stage_x16).
+template <int BITS>
+__device__ __forceinline__ float chunk_qx(const u32x4& W, const u32x4* xv, const float4& m, const Magic16& k) {
+    float A = 0.f, B = 0.f;
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int wd = 0; wd < 4; wd++) {
+            const uint32_t w = W[wd], w8 = w >> 8;
+            A = fdot2_f16(xv[wd][0], (w & k.mlo) | k.e16, A);
+            B = fdot2_f16(xv[wd][1], (w & k.mhi) | k.e16, B);
+            A = fdot2_f16(xv[wd][2], (w8 & k.mlo) | k.e16, A);
+            B = fdot2_f16(xv[wd][3], (w8 & k.mhi) | k.e16, B);
+        }
+        A = __builtin_fmaf(B, 0.0625f, A);
+    } else {
+#pragma unroll
+        for (int wd = 0; wd < 4; wd++) {
+            const uint32_t w = W[wd];
+            A = fdot2_f16(xv[wd >> 1][(wd & 1) * 2], __builtin_amdgcn_perm(k.e16, w, 0x05010500u), A);
+            B = fdot2_f16(xv[wd >> 1][(wd & 1) * 2 + 1], __builtin_amdgcn_perm(k.e16, w, 0x05030502u), B);
+        }
+        A += B;
+    }
+    return __builtin_fmaf(m.x, A, -m.y);
+}
+
 // Launch shape of the VALU kernel (qmv_valu.hip): S 16-byte chunk slots per
 // lane, RPW weight rows per wave, WV waves per workgroup.
 struct ValuShape {

@@ -32,31 +32,7 @@
 namespace kmi {
 
 namespace {
-
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-
-// A constant kept in a VGPR.  Held in a register (not an instruction
-// literal), a mask-and-or pair folds into one v_and_or_b32.
-__device__ __forceinline__ uint32_t vconst(uint32_t v) {
-    asm volatile("" : "+v"(v));
-    return v;
-}
-
-__device__ __forceinline__ float fdot2(uint32_t x, uint32_t w, float c) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), __builtin_bit_cast(f16x2_t, w), c, false);
-}
-
-__device__ __forceinline__ uint32_t pk_f16(float lo, float hi) {
-    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_max(float v) {
-    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false)));
-}
-
-constexpr uint32_t NONE = 0x80000000u;   // an offset past every buffer: reads 0
-
+constexpr uint32_t NONE = QV_NONE;
 }  // namespace
 
 // GATHER: tiles come from the expert sort (tile z = one routed row); else
@@ -68,7 +44,6 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
     constexpr int NT = 64 * WV;                   // threads per workgroup
     constexpr int CK = 128 / BITS;                // k per 16-byte chunk: 32 or 16
     constexpr int XV = CK / 8;                    // 8-element x pieces per chunk: 4 or 2
-    constexpr int XV_SHIFT = XV == 4 ? 2 : 1;
     extern __shared__ __align__(16) unsigned char smem[];
 
     Tile t;
@@ -107,52 +82,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
     const uint32_t xso = xok ? (uint32_t)(xrow * a.K * 2) : 0u;
     auto xvo = [&](int p) -> uint32_t { return (xok && p < P) ? (uint32_t)p * 16u : NONE; };
 
-    // Piece p of the row (x[8p .. 8p+8)) -> LDS.  Every lane of the wave runs
-    // this (the quad reductions read neighbours); only in-row pieces store.
-    auto stage = [&](int p, u32x4 raw) {
-        float f[8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            f[2 * i] = __uint_as_float(raw[i] << 16);
-            f[2 * i + 1] = __uint_as_float(raw[i] & 0xffff0000u);
-        }
-        float am = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) am = fmaxf(am, fabsf(f[i]));
-        am = dpp_max<0xb1>(am);                           // quad_perm [1,0,3,2]
-        if constexpr (XV == 4) am = dpp_max<0x4e>(am);    // quad_perm [2,3,0,1]
-        int e = (int)((__float_as_uint(am) >> 23) & 0xffu);
-        e = e < 15 ? 15 : e;
-        const float mult = __uint_as_float((uint32_t)(e - 14) << 23);   // 2^(e-141)
-        const float inv = __uint_as_float((uint32_t)(268 - e) << 23);   // 2^(141-e)
-        u32x4 o;
-        float lo, hi = 0.f;
-        if constexpr (BITS == 4) {
-            // dword i pairs (x_i, x_{i+4}): the codes one and-or places there
-#pragma unroll
-            for (int i = 0; i < 4; i++) o[i] = pk_f16(f[i] * inv, f[i + 4] * inv);
-            lo = (f[0] + f[2]) + (f[4] + f[6]);           // under low nibbles
-            hi = (f[1] + f[3]) + (f[5] + f[7]);           // under high nibbles
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++) o[i] = pk_f16(f[2 * i] * inv, f[2 * i + 1] * inv);
-            lo = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
-        }
-        lo = dpp_add<0xb1, 0xf>(lo);
-        if constexpr (XV == 4) lo = dpp_add<0x4e, 0xf>(lo);
-        if constexpr (BITS == 4) {
-            hi = dpp_add<0xb1, 0xf>(hi);
-            hi = dpp_add<0x4e, 0xf>(hi);
-        }
-        if (p < P) {
-            const int c = p >> XV_SHIFT, v = p & (XV - 1);
-            xs[v * C + c] = o;
-            if (v == 0) {
-                const float corr = BITS == 4 ? 1024.f * __builtin_fmaf(hi, 0.0625f, lo) : 1024.f * lo;
-                xm[c] = make_float4(mult, corr, lo + hi, 0.f);
-            }
-        }
-    };
+    auto stage = [&](int p, u32x4 raw) { stage_x16<BITS>(p, raw, P, C, xs, xm); };
 
     // (0) pieces beyond two per thread (long rows): staged before any
     // weight load is issued, so their waits drain nothing
@@ -218,7 +148,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
     if (P > NT) stage(tid + NT, xr1);
     lds_barrier();
 
-    const uint32_t MLO = vconst(0x000F000Fu), MHI = vconst(0x00F000F0u), E16 = vconst(0x64006400u);
+    const Magic16 mk = magic16();
     float acc[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; r++) acc[r] = 0.f;
@@ -238,28 +168,8 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
             const float4 m = xm[cc];
 #pragma unroll
             for (int r = 0; r < RPW; r++) {
-                float A = 0.f, B = 0.f;
-                if constexpr (BITS == 4) {
-#pragma unroll
-                    for (int wd = 0; wd < 4; wd++) {
-                        const uint32_t w = W[u][r][wd], w8 = w >> 8;
-                        A = fdot2(xv[wd][0], (w & MLO) | E16, A);
-                        B = fdot2(xv[wd][1], (w & MHI) | E16, B);
-                        A = fdot2(xv[wd][2], (w8 & MLO) | E16, A);
-                        B = fdot2(xv[wd][3], (w8 & MHI) | E16, B);
-                    }
-                    A = __builtin_fmaf(B, 0.0625f, A);
-                } else {
-#pragma unroll
-                    for (int wd = 0; wd < 4; wd++) {
-                        const uint32_t w = W[u][r][wd];
-                        A = fdot2(xv[wd >> 1][(wd & 1) * 2], __builtin_amdgcn_perm(E16, w, 0x05010500u), A);
-                        B = fdot2(xv[wd >> 1][(wd & 1) * 2 + 1], __builtin_amdgcn_perm(E16, w, 0x05030502u), B);
-                    }
-                    A += B;
-                }
+                const float q = chunk_qx<BITS>(W[u][r], xv, m, mk);
                 const float sv = __uint_as_float(SC[u][r] << 16), bv = __uint_as_float(BI[u][r] << 16);
-                const float q = __builtin_fmaf(m.x, A, -m.y);
                 const float nv = __builtin_fmaf(sv, q, __builtin_fmaf(bv, m.z, acc[r]));
                 acc[r] = cok ? nv : acc[r];
             }
