@@ -141,30 +141,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(
         }
 }
 
-// =============================================================================
-// qmm2: M > 128.  256 x 128 x 64 block tiles; 4 waves, each a 128 x 64 tile
-// of y (8 x 4 blocks of v_mfma_f32_16x16x32_bf16), so every 16-byte LDS read
-// feeds 4 or 8 MFMAs (44 flop per LDS byte).  The x tile (bf16, mostly L2
-// hits) is staged one k-tile ahead through registers; the packed weight tile
-// (the only HBM stream, 16 B per thread per k-tile at 4 bits) runs Q2_RING
-// k-tiles ahead in a register ring, and is dequantized once per k-tile
-// (fp32 s*q + b, rounded to bf16 by v_cvt_pk_bf16_f32) into LDS.  Rows past
-// M, columns past N and k-tiles past the split read zeros from their buffer
-// views.  When the tiles leave CUs idle, K is split: each split writes fp32
-// partials and qmm_split_reduce sums them in split order.
-// =============================================================================
-constexpr int Q2M = 256, Q2N = 128, Q2K = 64, Q2LDS = Q2K + 8;
-constexpr int Q2_RING = 4;
-
-typedef __bf16 q2_bf16x2 __attribute__((ext_vector_type(2)));
-typedef float q2_f32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
-    const q2_f32x2 v = {lo, hi};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, q2_bf16x2));
-}
-
-struct Qmm2Args {
+struct QgemmArgs {
     const uint16_t* x;          // [M, K] bf16
     const uint32_t* w;          // [N, K*bits/32]
     const uint16_t* s;          // [N, K/gs] bf16
@@ -175,147 +152,231 @@ struct Qmm2Args {
     int kt_per_split, splits, n_tiles;
 };
 
-template <int BITS, int GS>
-__global__ __launch_bounds__(512, 1) void qmm2_kernel(Qmm2Args a) {
-    constexpr int EPW = 32 / BITS;
-    constexpr int BQ = Q2K / 4 / EPW;           // packed words per thread per k-tile (2 or 4)
-    static_assert(GS >= 16, "one scale group per 16-wide quarter row");
-    __shared__ __align__(16) uint16_t As[2][Q2M * Q2LDS];
-    __shared__ __align__(16) uint16_t Bs[2][Q2N * Q2LDS];
+// =============================================================================
+// qmm5: M > 128.  Block tile 256 (M) x 128 (N) x 64 (K); 8 waves (two per
+// SIMD) as 4 (M) x 2 (N), each a 64 x 64 tile of y as 2 x 2 blocks of
+// v_mfma_f32_32x32x16_bf16 (64 fp32 accumulators per lane).
+//   - x and the dequantized weights are staged through LDS (two buffers),
+//     both loaded with 8 lanes per 128-byte row segment.  The weight tile is
+//     dequantized once per workgroup (fp32 s*q + b, one bf16 rounding: 16
+//     values per thread).
+//   - k order: in a k-tile, lane half h reads k in [32h, 32h + 32) and MFMA
+//     step s the 8 values 32h + 8s .. +8 of it, for x and w alike (the
+//     contraction is unchanged).
+//   - Per k-tile a wave reads all 16 of its fragments, then runs 16 MFMAs
+//     with tile t+1's dequantization and LDS stores between them; x and
+//     weights run Q5_RING k-tiles ahead in register rings (x mostly comes
+//     from L2 or the last-level cache, whose latency one tile does not
+//     cover).
+//   - Global load offsets: the lane part is fixed, the k-tile part is the
+//     scalar offset (past the split: 2^31, which reads 0).
+//   - Workgroups are numbered so that the m-tiles of one n-tile share an
+//     XCD (and its L2).  Rows past M, columns past N and k-tiles past the
+//     split read zeros from their buffer views.  When the tiles leave CUs
+//     idle, K is split: each split writes fp32 partials and
+//     qmm_split_reduce sums them in split order.
+// Measured limits on gfx950 that shaped it: a 32x32x16 MFMA occupies the
+// matrix core 32 cycles, and stays hidden only while a wave issues about 4
+// other instructions per MFMA (an instruction takes ~4.5 cycles to issue),
+// so instruction count per MFMA is the budget; LDS serves ~190-210 B/clk per
+// CU; loads with one row per lane run at a quarter of the rate of loads with
+// 8 lanes per 128-byte row.
+// =============================================================================
+constexpr int Q5M = 256, Q5N = 128, Q5K = 64, Q5LDS = Q5K + 8;
+constexpr int Q5_RING = 4;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nt = (int)(blockIdx.x % a.n_tiles), mt = (int)(blockIdx.x / a.n_tiles);
-    const int64_t bm = (int64_t)mt * Q2M, bn = (int64_t)nt * Q2N;
-    const int nk = (int)(a.K / Q2K);
+typedef __bf16 q5_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float q5_f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {   // v_cvt_pk_bf16_f32
+    const q5_f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, q5_bf16x2));
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// 8 consecutive weights (packed: 4-bit in one word, 8-bit in two) dequantized
+// to 4 bf16 pairs.
+template <int BITS>
+__device__ __forceinline__ u32x4 q5_dequant8(uint32_t w0, uint32_t w1, float sc, float bi) {
+    u32x4 o;
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            o[j] = cvt_pk_bf16(__builtin_fmaf(sc, (float)((w0 >> (8 * j)) & 15u), bi),
+                               __builtin_fmaf(sc, (float)((w0 >> (8 * j + 4)) & 15u), bi));
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            o[j] = cvt_pk_bf16(__builtin_fmaf(sc, (float)((w0 >> (16 * j)) & 255u), bi),
+                               __builtin_fmaf(sc, (float)((w0 >> (16 * j + 8)) & 255u), bi));
+            o[2 + j] = cvt_pk_bf16(__builtin_fmaf(sc, (float)((w1 >> (16 * j)) & 255u), bi),
+                                   __builtin_fmaf(sc, (float)((w1 >> (16 * j + 8)) & 255u), bi));
+        }
+    }
+    return o;
+}
+
+template <int BITS, int GS>
+__global__ __launch_bounds__(512, 1) void qmm5_kernel(QgemmArgs a) {
+    constexpr int EPW = 32 / BITS;
+    constexpr int TB = Q5K * BITS / 8;           // bytes of a weight row per k-tile
+    constexpr int QB = 16 * BITS / 8;            // bytes of a thread's 16 weights (8 or 16)
+    constexpr uint32_t DEAD = 0x80000000u;       // scalar offset past every extent
+    __shared__ __align__(16) uint16_t As[2][Q5M * Q5LDS];
+    __shared__ __align__(16) uint16_t Bs[2][Q5N * Q5LDS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31, h = lane >> 5;
+    // ids grp*8*mtn + 8*mt + x -> n-tile 8 grp + x, m-tile mt (XCD = id % 8)
+    const int mtn = (int)((a.M + Q5M - 1) / Q5M);
+    const int id = (int)blockIdx.x, grp = id / (8 * mtn), rem = id % (8 * mtn);
+    const int gw = a.n_tiles - 8 * grp < 8 ? a.n_tiles - 8 * grp : 8;
+    const int mt = rem / gw, nt = 8 * grp + rem % gw;
+    const int64_t bm = (int64_t)mt * Q5M, bn = (int64_t)nt * Q5N;
+    const int nk = (int)(a.K / Q5K);
     const int kt0 = (int)blockIdx.y * a.kt_per_split;
     const int kt1 = kt0 + a.kt_per_split < nk ? kt0 + a.kt_per_split : nk;
     const int64_t wpr = a.K / EPW, gpr = a.K / GS;
 
-    // A: thread chunk c = tid + 512 i -> row c / 8, 16-byte piece c % 8
-    // B: thread -> weight row tid / 4, k quarter tid % 4 (16 values)
-    const int brow = tid >> 2, bq = tid & 3;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + bm * a.K, (a.M - bm) * a.K * 2);
     const int64_t nrows = a.N - bn;
-    const __amdgpu_buffer_rsrc_t rwt = make_rsrc(a.w + bn * wpr, nrows * wpr * 4);
-    const __amdgpu_buffer_rsrc_t rwz = make_rsrc(a.w, 0);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + bn * wpr, nrows * wpr * 4);
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s + bn * gpr, nrows * gpr * 2);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b + bn * gpr, nrows * gpr * 2);
-    const uint32_t wrow_off = (uint32_t)(brow * wpr * 4 + bq * BQ * 4);
-    const uint32_t srow_off = (uint32_t)(brow * gpr * 2);
 
-    u32x4 ra[4];
-    uint32_t rw[Q2_RING][BQ];
-    uint32_t rsc[Q2_RING], rbi[Q2_RING];
-
-    auto load_a = [&](int kt) {        // kt past the split: a zero-extent view, no traffic
-        const __amdgpu_buffer_rsrc_t r = kt < kt1 ? rx : rwz;
+    // x: chunk c = tid + 512 i -> row c / 8, 16-byte piece c % 8
+    uint32_t xoff[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + 512 * i;
-            const uint32_t off = (uint32_t)(((c >> 3) * a.K + (int64_t)kt * Q2K + (c & 7) * 8) * 2);
-            ra[i] = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-        }
+    for (int i = 0; i < 4; i++) {
+        const int c = tid + 512 * i;
+        xoff[i] = (uint32_t)(((c >> 3) * a.K + (c & 7) * 8) * 2);
+    }
+    // weights: thread -> row tid / 4, quarter q = tid % 4 (16 weights)
+    const int brow = tid >> 2, bq = tid & 3;
+    const uint32_t woff = (uint32_t)(brow * wpr * 4 + bq * QB);
+    const uint32_t soff = (uint32_t)(brow * gpr * 2 + 2 * ((16 * bq) / GS));
+
+    u32x4 ra[Q5_RING][4];                         // x ring
+    uint32_t rwv[Q5_RING][QB / 4];                // weight ring
+    uint32_t rsc[Q5_RING], rbi[Q5_RING];
+
+    auto load_x = [&](int slot, int kt) {
+        const uint32_t so = kt < kt1 ? (uint32_t)kt * (Q5K * 2) : DEAD;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            ra[slot][i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xoff[i], (int)so, 0);
     };
-    auto load_b = [&](int slot, int kt) {
+    auto load_w = [&](int slot, int kt) {
         const bool live = kt < kt1;
-        const __amdgpu_buffer_rsrc_t r = live ? rwt : rwz;
-        const uint32_t off = wrow_off + (uint32_t)kt * (Q2K / EPW) * 4u;
-        if constexpr (BQ == 2) {
-            const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
-            rw[slot][0] = v.x; rw[slot][1] = v.y;
+        const uint32_t so = live ? (uint32_t)kt * TB : DEAD;
+        if constexpr (QB == 8) {
+            const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)woff, (int)so, 0);
+            rwv[slot][0] = v.x; rwv[slot][1] = v.y;
         } else {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-            rw[slot][0] = v.x; rw[slot][1] = v.y; rw[slot][2] = v.z; rw[slot][3] = v.w;
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff, (int)so, 0);
+            rwv[slot][0] = v.x; rwv[slot][1] = v.y; rwv[slot][2] = v.z; rwv[slot][3] = v.w;
         }
-        const uint32_t g = (uint32_t)(((int64_t)kt * Q2K + 16 * bq) / GS);
-        rsc[slot] = __builtin_amdgcn_raw_buffer_load_b16(live ? rs : rwz, (int)(srow_off + 2u * g), 0, 0);
-        rbi[slot] = __builtin_amdgcn_raw_buffer_load_b16(live ? rb : rwz, (int)(srow_off + 2u * g), 0, 0);
+        const uint32_t sg = live ? (uint32_t)(2 * (((int64_t)kt * Q5K) / GS)) : DEAD;
+        rsc[slot] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff, (int)sg, 0);
+        rbi[slot] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)soff, (int)sg, 0);
     };
-    auto store = [&](int buf, int slot) {
+    auto store_x = [&](int buf, int slot) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int c = tid + 512 * i;
-            *(u32x4*)(&As[buf][(c >> 3) * Q2LDS + (c & 7) * 8]) = ra[i];
+            *(u32x4*)(&As[buf][(c >> 3) * Q5LDS + (c & 7) * 8]) = ra[slot][i];
         }
+    };
+    auto store_w = [&](int buf, int slot) {
         const float sc = bf16_to_f32((uint16_t)rsc[slot]), bi = bf16_to_f32((uint16_t)rbi[slot]);
-        uint32_t ow[8];
-#pragma unroll
-        for (int e = 0; e < 16; e += 2) {
-            const uint32_t w0 = rw[slot][e / EPW], w1 = rw[slot][(e + 1) / EPW];
-            const float q0 = (float)((w0 >> ((e % EPW) * BITS)) & ((1u << BITS) - 1u));
-            const float q1 = (float)((w1 >> (((e + 1) % EPW) * BITS)) & ((1u << BITS) - 1u));
-            ow[e / 2] = cvt_pk_bf16(__builtin_fmaf(sc, q0, bi), __builtin_fmaf(sc, q1, bi));
+        uint16_t* dst = &Bs[buf][brow * Q5LDS + 16 * bq];
+        if constexpr (BITS == 4) {
+            *(u32x4*)dst = q5_dequant8<4>(rwv[slot][0], 0u, sc, bi);
+            *(u32x4*)(dst + 8) = q5_dequant8<4>(rwv[slot][1], 0u, sc, bi);
+        } else {
+            *(u32x4*)dst = q5_dequant8<8>(rwv[slot][0], rwv[slot][1], sc, bi);
+            *(u32x4*)(dst + 8) = q5_dequant8<8>(rwv[slot][2], rwv[slot][3], sc, bi);
         }
-        uint16_t* dst = &Bs[buf][brow * Q2LDS + 16 * bq];
-        *(u32x4*)dst = u32x4{ow[0], ow[1], ow[2], ow[3]};
-        *(u32x4*)(dst + 8) = u32x4{ow[4], ow[5], ow[6], ow[7]};
     };
 
-    // 8 waves: 4 along M x 2 along N, each a 64 x 64 tile (4 x 4 MFMA blocks)
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    const int l16 = lane & 15, lk = lane >> 4;
-    f32x4 acc[4][4];
+    f32x16 acc[2][2];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
 #pragma unroll
-    for (int r = 0; r < Q2_RING; r++) load_b(r, kt0 + r);
-    load_a(kt0);
-    store(0, 0);
+    for (int r = 0; r < Q5_RING; r++) {
+        load_x(r, kt0 + r);
+        load_w(r, kt0 + r);
+    }
+    store_x(0, 0);
+    store_w(0, 0);
+    load_x(0, kt0 + Q5_RING);
+    load_w(0, kt0 + Q5_RING);
     __syncthreads();
-    load_a(kt0 + 1);
-    load_b(0, kt0 + Q2_RING);
 
-    for (int kb = kt0; kb < kt1; kb += Q2_RING) {
+    for (int kb = kt0; kb < kt1; kb += Q5_RING) {
 #pragma unroll
-        for (int u = 0; u < Q2_RING; u++) {
+        for (int u = 0; u < Q5_RING; u++) {
             const int t = kb + u;
             if (t < kt1) {
                 const int buf = (t - kt0) & 1;
-                const int ns = (u + 1) % Q2_RING;        // ring slot of tile t + 1
+                const int ns = (u + 1) % Q5_RING;        // ring slot of tile t + 1
+                u32x4 af[4][2], bf[4][2];
 #pragma unroll
-                for (int ks = 0; ks < Q2K / 32; ks++) {
-                    u32x4 af[4], bfr[4];
+                for (int s = 0; s < 4; s++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        af[i] = *(const u32x4*)(&As[buf][(wm + 16 * i + l16) * Q2LDS + ks * 32 + lk * 8]);
+                    for (int i = 0; i < 2; i++) {
+                        af[s][i] = *(const u32x4*)(&As[buf][(wm + 32 * i + l32) * Q5LDS + 32 * h + 8 * s]);
+                        bf[s][i] = *(const u32x4*)(&Bs[buf][(wn + 32 * i + l32) * Q5LDS + 32 * h + 8 * s]);
+                    }
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        bfr[j] = *(const u32x4*)(&Bs[buf][(wn + 16 * j + l16) * Q2LDS + ks * 32 + lk * 8]);
+                for (int s = 0; s < 4; s++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
+                    for (int i = 0; i < 2; i++)
 #pragma unroll
-                        for (int j = 0; j < 4; j++) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
-                    // the next tile's store (its data arrived a tile ago; buf ^ 1 is free
-                    // since the last barrier) runs while these MFMAs execute
-                    if (ks == 0 && t + 1 < kt1) store(buf ^ 1, ns);
+                        for (int j = 0; j < 2; j++) acc[i][j] = mfma32x32x16(af[s][i], bf[s][j], acc[i][j]);
+                // tile t+1 into the other buffers (past the split: zeros, harmless),
+                // then its ring slot refilled, all between the MFMAs
+                store_w(buf ^ 1, ns);
+                store_x(buf ^ 1, ns);
+                load_x(ns, t + 1 + Q5_RING);
+                load_w(ns, t + 1 + Q5_RING);
+                __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);      // LDS reads
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
+                    if (i >= 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
                 }
                 __syncthreads();
-                // x of tile t + 2 before the ring refill: waiting on it at the next
-                // store then leaves the younger ring loads in flight
-                load_a(t + 2);
-                load_b(ns, t + 1 + Q2_RING);
             }
         }
     }
 
-    // D of block (i, j): row 16 i + 4 lk + r, column 16 j + l16
+    // D of block (i, j): row 32 i + 8 (r / 4) + 4 h + r % 4, column 32 j + l32.
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int j = 0; j < 2; j++) {
+        const int64_t col = bn + wn + 32 * j + l32;
+        if (col >= a.N) continue;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int64_t col = bn + wn + 16 * j + l16;
-            if (col >= a.N) continue;
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int64_t row = bm + wm + 16 * i + 4 * lk + r;
+            for (int r = 0; r < 16; r++) {
+                const int64_t row = bm + wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
                 if (row >= a.M) continue;
                 if (a.splits == 1) a.y[row * a.N + col] = f32_to_bf16(acc[i][j][r]);
                 else a.partial[((int64_t)blockIdx.y * a.M + row) * a.N + col] = acc[i][j][r];
             }
-        }
+    }
 }
 
 __global__ __launch_bounds__(256) void qmm_split_reduce(const float* __restrict__ partial, int S,
@@ -327,19 +388,19 @@ __global__ __launch_bounds__(256) void qmm_split_reduce(const float* __restrict_
     y[i] = f32_to_bf16(acc);
 }
 
-struct Qmm2Plan {
+struct QgemmPlan {
     int n_tiles, m_tiles, splits, kt_per_split;
     size_t ws;
 };
 
-// K splits while the tiles would fill under half of the CUs (one 110 KB
-// workgroup per CU), at least 8 k-tiles per split.
-static Qmm2Plan plan_qmm2(int64_t M, int64_t N, int64_t K) {
-    Qmm2Plan p;
-    p.n_tiles = (int)ceil_div(N, Q2N);
-    p.m_tiles = (int)ceil_div(M, Q2M);
+// K splits while the tiles would fill under half of the CUs (one workgroup
+// per CU), at least 8 k-tiles per split.
+static QgemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
+    QgemmPlan p;
+    p.n_tiles = (int)ceil_div(N, Q5N);
+    p.m_tiles = (int)ceil_div(M, Q5M);
     const int tiles = p.n_tiles * p.m_tiles;
-    const int nk = (int)(K / Q2K);
+    const int nk = (int)(K / Q5K);
     int s = tiles * 2 <= 256 ? 256 / tiles : 1;
     if (s > nk / 8) s = nk / 8 > 0 ? nk / 8 : 1;
     p.kt_per_split = (int)ceil_div(nk, s);
@@ -350,7 +411,7 @@ static Qmm2Plan plan_qmm2(int64_t M, int64_t N, int64_t K) {
 
 size_t qmm_gemm_workspace(int64_t M, int64_t K, int64_t N) {
     if (M <= 128) return 0;
-    return plan_qmm2(M, N, K).ws;
+    return plan_gemm(M, N, K).ws;
 }
 
 int qmm_gemm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
@@ -366,25 +427,25 @@ int qmm_gemm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
     if (M > 128) {
         KMI_CHECK_ARG(M * K * 2 < (1LL << 31) && N * K * bits / 8 < (1LL << 31),
                       "quantized_matmul: x or w past 2 GiB");
-        const Qmm2Plan p = plan_qmm2(M, N, K);
+        const QgemmPlan p = plan_gemm(M, N, K);
         if (p.ws > 0 && (!workspace || workspace_bytes < p.ws)) {
             set_error("quantized_matmul: workspace of %zu bytes needed, %zu given", p.ws, workspace_bytes);
             return EWORKSPACE;
         }
-        Qmm2Args a = {xx, w, ss, bb, yy, (float*)workspace, M, N, K, p.kt_per_split, p.splits, p.n_tiles};
+        QgemmArgs a = {xx, w, ss, bb, yy, (float*)workspace, M, N, K, p.kt_per_split, p.splits, p.n_tiles};
         const dim3 grid((unsigned)(p.n_tiles * p.m_tiles), (unsigned)p.splits);
-#define KMI_QMM2(B, G) qmm2_kernel<B, G><<<grid, 512, 0, st>>>(a)
+#define KMI_QMM5(B, G) qmm5_kernel<B, G><<<grid, 512, 0, st>>>(a)
         if (bits == 4) {
-            if (group_size == 32) KMI_QMM2(4, 32);
-            else if (group_size == 64) KMI_QMM2(4, 64);
-            else KMI_QMM2(4, 128);
+            if (group_size == 32) KMI_QMM5(4, 32);
+            else if (group_size == 64) KMI_QMM5(4, 64);
+            else KMI_QMM5(4, 128);
         } else {
-            if (group_size == 32) KMI_QMM2(8, 32);
-            else if (group_size == 64) KMI_QMM2(8, 64);
-            else KMI_QMM2(8, 128);
+            if (group_size == 32) KMI_QMM5(8, 32);
+            else if (group_size == 64) KMI_QMM5(8, 64);
+            else KMI_QMM5(8, 128);
         }
-#undef KMI_QMM2
-        KMI_CHECK_LAUNCH("qmm2");
+#undef KMI_QMM5
+        KMI_CHECK_LAUNCH("qmm5");
         if (p.splits > 1) {
             const int64_t count = M * N;
             qmm_split_reduce<<<(unsigned)ceil_div(count, 256), 256, 0, st>>>((const float*)workspace, p.splits,

@@ -163,3 +163,30 @@ def test_the_decode_workload(dev, N, L):
     """4 sequences, 32 query heads over 4 KV heads, head dim 128, 8-bit
     group-64 K/V; 1 query token, or 4 under a causal mask (MTP verify)."""
     _check(*_case(dev, 4, 32, 4, L, N, 128, seed=N + L), "causal" if L > 1 else None)
+
+
+
+def test_graph_replays_match_the_eager_call(dev):
+    """decode_sdpa captured in a HIP graph after a warm call on the capturing
+    stream; several replays, with eager work and synchronisation between
+    them, each equal to the eager result."""
+    host, gpu = _case(dev, 2, 16, 2, 1, 6000, 128, seed=31)
+    tq, tK, tV = gpu
+    scale = 128 ** -0.5
+    eager = kvattn.decode_sdpa(tq, tK, tV, scale, None, 64, 8)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        kvattn.decode_sdpa(tq, tK, tV, scale, None, 64, 8)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = kvattn.decode_sdpa(tq, tK, tV, scale, None, 64, 8)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        again = kvattn.decode_sdpa(tq, tK, tV, scale, None, 64, 8)
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)
+    del g
