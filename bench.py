@@ -155,6 +155,39 @@ def bench_kv8(B, H, Hk, L, N, D, cold, calls, dev):
             "bytes": nbytes, "flops": flops}
 
 
+def bench_kv_append(B, Hk, S, D, bits, calls, dev):
+    """Quantize-on-append into a quantized KV cache (kvcache.QuantKVCache's
+    update_and_fetch): S new K and V rows of B x Hk heads quantized along D
+    (group 64) straight into slab slots, one kmi_kv_quantize_append launch
+    each; slots rotate through a 1 GB slab set so every write is cold.
+    Bytes: K and V rows read (bf16) + packed words, scales and biases
+    written."""
+    import torch
+    from knurlogic_amd import kvcache
+    g = torch.Generator(device=dev).manual_seed(3000 + S)
+    per_slot = B * Hk * (D * bits // 8 + (D // 64) * 4) * 2
+    slots = max(S, (ROTATE_BYTES // per_slot) // S * S)
+    k_parts = kvcache._alloc(B, Hk, slots, D, bits, 64, torch.bfloat16, dev)
+    v_parts = kvcache._alloc(B, Hk, slots, D, bits, 64, torch.bfloat16, dev)
+    xs = [torch.randn(B, Hk, S, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(2)]
+    n_pos = slots // S
+
+    def run():
+        for i in range(calls):
+            pos = (i % n_pos) * S
+            kvcache.append_quantized(k_parts, xs[0], pos, 64, bits)
+            kvcache.append_quantized(v_parts, xs[1], pos, 64, bits)
+
+    us = time_graph(run) / calls * 1e3
+    nbytes = 2 * B * Hk * S * D * 2 + S * per_slot
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del k_parts, v_parts
+    torch.cuda.empty_cache()
+    return {"op": "kv_append", "B": B, "Hk": Hk, "S": S, "D": D, "bits": bits, "cache": "cold",
+            "us": round(us, 3), "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+            "bound": "hbm", "bytes": nbytes}
+
+
 MOE = dict(E=128, k=8, H=2048, I=768, bits=4)
 
 
@@ -299,7 +332,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no detail table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="detail sections, comma-separated "
-                                                "(dense, kv8, moe, vq); default all")
+                                                "(dense, kv8, kvcache, moe, vq); default all")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 10 plain device copies of MIB MiB (the known-size kernel "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -345,7 +378,7 @@ def main():
     gbs = nbytes / (us * 1e-6) / 1e9
 
     detail = []
-    only = set(args.only.split(",")) if args.only else {"dense", "kv8", "moe", "vq"}
+    only = set(args.only.split(",")) if args.only else {"dense", "kv8", "kvcache", "moe", "vq"}
     if not args.quick and "vq" in only:
         for kc_ in (256, 4096):
             for t_ in (1, 16):
@@ -360,6 +393,9 @@ def main():
             for l_ in (1, 4):
                 for cold in (True, False):
                     detail.append(bench_kv8(4, 32, 4, l_, n_, 128, cold, 50, dev))
+    if not args.quick and "kvcache" in only:
+        for s_ in (1, 512):
+            detail.append(bench_kv_append(4, 4, s_, 128, 8, 200 if s_ == 1 else 50, dev))
     if not args.quick and "dense" in only:
         for b_ in (4, 8):
             for shape in ((14336, 4096), (4096, 14336)):

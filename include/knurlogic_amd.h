@@ -46,7 +46,7 @@ int kmi_abi_version(void);
  * at src/knurlogic/engine/kvquant.py:46-47 (KV append) and
  * src/knurlogic/engine/families/glm5/architecture/glm5_next/_mlx_vlm/models/
  * switch_layers.py:38-48 (weights).
- *   w       [rows, cols] of `dtype`
+ *   w       [rows, cols] of `dtype`, 16-byte aligned
  *   wq      [rows, cols*bits/32] uint32 out
  *   scales, biases [rows, cols/group_size] of `dtype` out
  * bits in {2, 4, 8}; group_size in {32, 64, 128}.
@@ -54,6 +54,23 @@ int kmi_abi_version(void);
 int kmi_quantize_affine(const void* w, int dtype, int64_t rows, int64_t cols,
                         int group_size, int bits, uint32_t* wq, void* scales,
                         void* biases, void* stream);
+
+/*
+ * Quantize-on-append for a quantized KV cache: the reference's
+ * QuantKVCache / BatchQuantKVCache.update_and_fetch writes
+ * mx.quantize(keys) into slab slots prev .. prev+S
+ * (src/knurlogic/engine/kvquant.py:136-155,214-234).  x [B, H, S, D]
+ * contiguous (dtype), 16-byte aligned, quantized along D in groups of
+ * group_size (the same arithmetic as kmi_quantize_affine, bit for bit),
+ * written to slots
+ * n = pos .. pos+S-1 of a cache triple: wq u32 [B, H, capacity, D*bits/32],
+ * scales / biases [B, H, capacity, D/group_size] (dtype), each possibly a
+ * strided view with a contiguous last axis.  strides[6]: element strides
+ * (b, h, n) of wq, then (b, h, n) shared by scales and biases.
+ */
+int kmi_kv_quantize_append(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                           int group_size, int bits, uint32_t* wq, void* scales, void* biases,
+                           const int64_t* strides, int64_t pos, int64_t capacity, void* stream);
 
 /*
  * mx.dequantize(wq, scales, biases, group_size, bits, mode="affine",

@@ -1,8 +1,8 @@
 // Affine group quantize / dequantize (mx.quantize / mx.dequantize, mode
-// "affine") for gfx950.  One thread per group: a group is at most 128
-// elements, read with 16-byte loads; both ops are bandwidth-trivial next to
-// the matmuls (weights are quantized offline; the KV cache quantizes one
-// new token per layer per step).
+// "affine") for gfx950, and the KV cache's quantize-on-append.  Quantize:
+// GS/8 lanes per group, 8 elements per lane in one 16-byte load, the group's
+// min / max exchanged by lane shuffles.  Dequantize: one thread per packed
+// word.  All are HBM-bound element passes.
 #include "common.hpp"
 #include "../../include/knurlogic_amd.h"
 
@@ -22,23 +22,58 @@ void set_error(const char* fmt, ...) {
 
 void clear_error() { g_err[0] = 0; }
 
-// mlx's affine quantizer for one group (restated; the oracle's
-// orc_quantize_affine follows the same steps in the same float32 order).
-template <typename T, int BITS>
-__global__ __launch_bounds__(256) void quantize_kernel(
-    const typename T::storage* __restrict__ w, int64_t n_groups, int group,
-    uint32_t* __restrict__ wq, typename T::storage* __restrict__ scales,
-    typename T::storage* __restrict__ biases) {
-    const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gi >= n_groups) return;
-    const typename T::storage* wg = w + gi * group;
-    const float n_bins = (float)((1u << BITS) - 1u);
-    float w_max = -INFINITY, w_min = INFINITY;
-    for (int i = 0; i < group; i++) {
-        float v = T::load(wg[i]);
-        w_max = fmaxf(w_max, v);
-        w_min = fminf(w_min, v);
+// mlx's affine quantizer (restated; the oracle's orc_quantize_affine follows
+// the same steps in the same float32 order), one group per GS/8 consecutive
+// lanes: each lane loads 8 consecutive elements (one 16-byte load for 16-bit
+// types), min / max are exchanged across the group's lanes, every lane
+// derives the same scale and bias and quantizes its own 8 elements.  Where
+// the packed words and scales go: contiguous (quantize), or KV-cache slab
+// slots (append).
+struct QuantDst {
+    uint32_t* wq;
+    void* scales;
+    void* biases;
+    int64_t wst[3], sst[3];     // append: element strides (b, h, n) of wq and of scales / biases
+    int64_t pos, H, S;          // append: first slot, heads, new rows per head
+    int kv;                     // 0: contiguous [groups] layout, 1: slab slots
+};
+
+template <typename T, int BITS, int GS>
+__global__ __launch_bounds__(256) void quantize_kernel(const typename T::storage* __restrict__ w,
+                                                       int64_t n_groups, int64_t D, QuantDst d) {
+    constexpr int LPG = GS / 8;                  // lanes per group
+    constexpr int EPW = 32 / BITS;
+    using St = typename T::storage;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t gi = t / LPG;
+    const int sub = (int)(t % LPG);
+    const bool live = gi < n_groups;             // whole groups are live or not (LPG divides 64)
+    float v[8];
+    const St* src = w + (live ? gi : 0) * GS + sub * 8;
+    if constexpr (sizeof(St) == 2) {
+        const u32x4 r = *(const u32x4*)src;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[2 * e] = T::load((St)(r[e] & 0xffffu));
+            v[2 * e + 1] = T::load((St)(r[e] >> 16));
+        }
+    } else {
+        const float4 r0 = *(const float4*)src, r1 = *(const float4*)(src + 4);
+        v[0] = r0.x; v[1] = r0.y; v[2] = r0.z; v[3] = r0.w;
+        v[4] = r1.x; v[5] = r1.y; v[6] = r1.z; v[7] = r1.w;
     }
+    float w_max = -INFINITY, w_min = INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        w_max = fmaxf(w_max, v[e]);
+        w_min = fminf(w_min, v[e]);
+    }
+#pragma unroll
+    for (int o = 1; o < LPG; o <<= 1) {
+        w_max = fmaxf(w_max, __shfl_xor(w_max, o, 64));
+        w_min = fminf(w_min, __shfl_xor(w_min, o, 64));
+    }
+    const float n_bins = (float)((1u << BITS) - 1u);
     const bool neg_edge = fabsf(w_min) > fabsf(w_max);
     float scale = fmaxf((w_max - w_min) / n_bins, 1e-7f);
     scale = neg_edge ? scale : -scale;
@@ -49,20 +84,43 @@ __global__ __launch_bounds__(256) void quantize_kernel(
         scale = edge / q0;
         bias = edge;
     }
-    constexpr int EPW = 32 / BITS;
-    uint32_t* qg = wq + gi * (group / EPW);
-    for (int wi = 0; wi < group / EPW; wi++) {
-        uint32_t word = 0;
+    uint32_t bitsv = 0;                          // this lane's 8 codes (8 * BITS bits, low first)
+    uint32_t hi = 0;                             // codes 4..7 at 8 bits
 #pragma unroll
-        for (int e = 0; e < EPW; e++) {
-            float q = rintf((T::load(wg[wi * EPW + e]) - bias) / scale);
-            q = fminf(fmaxf(q, 0.0f), n_bins);
-            word |= ((uint32_t)q) << (e * BITS);
-        }
-        qg[wi] = word;
+    for (int e = 0; e < 8; e++) {
+        float q = rintf((v[e] - bias) / scale);
+        q = fminf(fmaxf(q, 0.0f), n_bins);
+        const uint32_t c = (uint32_t)q;
+        if (BITS == 8 && e >= 4) hi |= c << ((e - 4) * 8);
+        else bitsv |= c << (e * BITS);
     }
-    scales[gi] = T::store(scale);
-    biases[gi] = T::store(bias);
+    if (!live) return;
+    // destination of this group's words and of its scale / bias
+    int64_t wo, so;
+    if (d.kv) {
+        const int64_t gpr = D / GS;
+        const int64_t r = gi / gpr, gs = gi % gpr;
+        const int64_t s = r % d.S, bh = r / d.S, h = bh % d.H, b = bh / d.H;
+        const int64_t n = d.pos + s;
+        wo = b * d.wst[0] + h * d.wst[1] + n * d.wst[2] + gs * (GS / EPW);
+        so = b * d.sst[0] + h * d.sst[1] + n * d.sst[2] + gs;
+    } else {
+        wo = gi * (GS / EPW);
+        so = gi;
+    }
+    if constexpr (BITS == 8) {
+        d.wq[wo + 2 * sub] = bitsv;              // word strides need only be 4-byte multiples
+        d.wq[wo + 2 * sub + 1] = hi;
+    } else if constexpr (BITS == 4) {
+        d.wq[wo + sub] = bitsv;
+    } else {                                     // 2 bits: two lanes per word
+        const uint32_t other = __shfl_xor(bitsv, 1, 64);
+        if ((sub & 1) == 0) d.wq[wo + sub / 2] = bitsv | (other << 16);
+    }
+    if (sub == 0) {
+        ((St*)d.scales)[so] = T::store(scale);
+        ((St*)d.biases)[so] = T::store(bias);
+    }
 }
 
 // out = T(T(s*q) + b) (rounding 0) or T(fma(s, q, b)) (rounding 1); one
@@ -94,17 +152,23 @@ __global__ __launch_bounds__(256) void dequantize_kernel(
     }
 }
 
-template <typename T>
-static void launch_quantize(const void* w, int64_t n_groups, int group, int bits,
-                            uint32_t* wq, void* s, void* b, hipStream_t st) {
-    dim3 grid((unsigned)ceil_div(n_groups, 256));
+template <typename T, int BITS>
+static void launch_quantize_b(const void* w, int64_t n_groups, int group, int64_t D, const QuantDst& d,
+                              hipStream_t st) {
     using S = typename T::storage;
-    if (bits == 4)
-        quantize_kernel<T, 4><<<grid, 256, 0, st>>>((const S*)w, n_groups, group, wq, (S*)s, (S*)b);
-    else if (bits == 8)
-        quantize_kernel<T, 8><<<grid, 256, 0, st>>>((const S*)w, n_groups, group, wq, (S*)s, (S*)b);
-    else
-        quantize_kernel<T, 2><<<grid, 256, 0, st>>>((const S*)w, n_groups, group, wq, (S*)s, (S*)b);
+    const int64_t threads = n_groups * (group / 8);
+    dim3 grid((unsigned)ceil_div(threads, 256));
+    if (group == 32) quantize_kernel<T, BITS, 32><<<grid, 256, 0, st>>>((const S*)w, n_groups, D, d);
+    else if (group == 64) quantize_kernel<T, BITS, 64><<<grid, 256, 0, st>>>((const S*)w, n_groups, D, d);
+    else quantize_kernel<T, BITS, 128><<<grid, 256, 0, st>>>((const S*)w, n_groups, D, d);
+}
+
+template <typename T>
+static void launch_quantize(const void* w, int64_t n_groups, int group, int bits, int64_t D,
+                            const QuantDst& d, hipStream_t st) {
+    if (bits == 4) launch_quantize_b<T, 4>(w, n_groups, group, D, d, st);
+    else if (bits == 8) launch_quantize_b<T, 8>(w, n_groups, group, D, d, st);
+    else launch_quantize_b<T, 2>(w, n_groups, group, D, d, st);
 }
 
 template <typename TS, typename TO>
@@ -145,11 +209,47 @@ int kmi_quantize_affine(const void* w, int dtype, int64_t rows, int64_t cols,
     KMI_CHECK_ARG(dtype >= BF16 && dtype <= F32, "quantize: bad dtype %d", dtype);
     const int64_t n_groups = rows * (cols / group_size);
     if (n_groups == 0) return OK;
+    KMI_CHECK_ARG(((uintptr_t)w & 15) == 0, "quantize: w must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
-    if (dtype == BF16) launch_quantize<TBF16>(w, n_groups, group_size, bits, wq, scales, biases, st);
-    else if (dtype == F16) launch_quantize<TF16>(w, n_groups, group_size, bits, wq, scales, biases, st);
-    else launch_quantize<TF32>(w, n_groups, group_size, bits, wq, scales, biases, st);
+    QuantDst d = {};
+    d.wq = wq; d.scales = scales; d.biases = biases; d.kv = 0;
+    if (dtype == BF16) launch_quantize<TBF16>(w, n_groups, group_size, bits, cols, d, st);
+    else if (dtype == F16) launch_quantize<TF16>(w, n_groups, group_size, bits, cols, d, st);
+    else launch_quantize<TF32>(w, n_groups, group_size, bits, cols, d, st);
     KMI_CHECK_LAUNCH("quantize");
+    return OK;
+}
+
+int kmi_kv_quantize_append(const void* x, int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                           int group_size, int bits, uint32_t* wq, void* scales, void* biases,
+                           const int64_t* strides, int64_t pos, int64_t capacity, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(x && wq && scales && biases && strides, "kv_quantize_append: null pointer");
+    KMI_CHECK_ARG(bits == 2 || bits == 4 || bits == 8, "kv_quantize_append: bits %d not in {2,4,8}", bits);
+    KMI_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
+                  "kv_quantize_append: group_size %d not in {32,64,128}", group_size);
+    KMI_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && D > 0 && D % group_size == 0,
+                  "kv_quantize_append: head dim %lld is not a multiple of the group %d", (long long)D,
+                  group_size);
+    KMI_CHECK_ARG(dtype >= BF16 && dtype <= F32, "kv_quantize_append: bad dtype %d", dtype);
+    KMI_CHECK_ARG(pos >= 0 && pos + S <= capacity,
+                  "kv_quantize_append: slots %lld..%lld past the slab capacity %lld", (long long)pos,
+                  (long long)(pos + S), (long long)capacity);
+    QuantDst d = {};
+    d.wq = wq; d.scales = scales; d.biases = biases; d.pos = pos; d.H = H; d.S = S; d.kv = 1;
+    for (int i = 0; i < 3; i++) {
+        KMI_CHECK_ARG(strides[i] >= 0 && strides[3 + i] >= 0, "kv_quantize_append: negative stride");
+        d.wst[i] = strides[i];
+        d.sst[i] = strides[3 + i];
+    }
+    const int64_t n_groups = B * H * S * (D / group_size);
+    if (n_groups == 0) return OK;
+    KMI_CHECK_ARG(((uintptr_t)x & 15) == 0, "kv_quantize_append: x must be 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == BF16) launch_quantize<TBF16>(x, n_groups, group_size, bits, D, d, st);
+    else if (dtype == F16) launch_quantize<TF16>(x, n_groups, group_size, bits, D, d, st);
+    else launch_quantize<TF32>(x, n_groups, group_size, bits, D, d, st);
+    KMI_CHECK_LAUNCH("kv_quantize_append");
     return OK;
 }
 

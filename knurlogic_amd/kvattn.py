@@ -189,7 +189,8 @@ def sdpa(queries, keys, values, cache, scale, mask, sinks=None):
             return decode_sdpa(queries, K, V, scale, mask, g, 8, same_layout=True)
     if sinks is not None:
         raise ValueError("sdpa: attention sinks are not implemented")
-    return _dense_sdpa(queries, keys, values, scale, mask)
+    from .kvcache import materialize          # a quantized cache's lazily dequantized K / V
+    return _dense_sdpa(queries, materialize(keys), materialize(values), scale, mask)
 
 
 def _dense_sdpa(q, k, v, scale, mask):

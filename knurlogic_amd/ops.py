@@ -54,6 +54,13 @@ def _workspace(nbytes: int, device) -> torch.Tensor | None:
     return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
 
 
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    """t contiguous at a 16-byte aligned address (the quantize kernels read
+    8 elements per lane as one 16-byte load)."""
+    t = t.contiguous()
+    return t.clone() if t.data_ptr() % 16 else t
+
+
 def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4,
              mode: str = "affine"):
     """``mx.quantize``: (wq uint32 [..., K*bits/32], scales, biases
@@ -65,7 +72,7 @@ def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4,
     if w.ndim < 1 or w.shape[-1] % group_size or (w.shape[-1] * bits) % 32:
         raise ValueError(f"quantize: the last axis ({w.shape[-1] if w.ndim else None}) "
                          f"must be a multiple of the group size {group_size}")
-    w = w.contiguous()
+    w = _aligned16(w)
     cols = w.shape[-1]
     rows = w.numel() // cols if cols else 0
     lead = tuple(w.shape[:-1])
