@@ -155,6 +155,46 @@ def bench_kv8(B, H, Hk, L, N, D, cold, calls, dev):
             "bytes": nbytes, "flops": flops}
 
 
+def bench_qsdpa(B, H, Hk, L, N, D, bits, calls, dev):
+    """mlx-lm's quantized attention (kvattn.quantized_sdpa: two
+    kmi_qmm_batched products around kmi_masked_softmax) over quantized K/V
+    of N keys, causal inside the L-token block; K/V sets rotated past 1 GB.
+    Bytes: the packed K and V with their scales and biases, q in and out
+    (the scores / probabilities round trip through L2 is not counted)."""
+    import torch
+    import knurlogic_amd as KA
+    from knurlogic_amd import kvattn
+    g = torch.Generator(device=dev).manual_seed(7000 + N + L)
+    per = B * Hk * N * 2 * (D * bits // 8 + (D // 64) * 4)
+    n = max(4, math.ceil(ROTATE_BYTES / per))
+    sets = []
+    for _ in range(n):
+        trip = []
+        for _kv in range(2):
+            t = torch.randn(B * Hk * N, D, device=dev, generator=g).to(torch.bfloat16)
+            wq, s, b = KA.quantize(t, group_size=64, bits=bits)
+            del t
+            trip.append((wq.view(B, Hk, N, -1), s.view(B, Hk, N, -1), b.view(B, Hk, N, -1)))
+        sets.append(tuple(trip))
+    q = torch.randn(B, H, L, D, device=dev, generator=g).to(torch.bfloat16)
+    mask = "causal" if L > 1 else None
+    scale = D ** -0.5
+
+    def run():
+        for i in range(calls):
+            K, V = sets[i % n]
+            kvattn.quantized_sdpa(q, K, V, scale, mask, 64, bits)
+
+    us = time_graph(run) / calls * 1e3
+    nbytes = per + 4 * B * H * L * D
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del sets
+    torch.cuda.empty_cache()
+    return {"op": "quantized_sdpa", "B": B, "H": H, "Hk": Hk, "L": L, "N": N, "D": D, "bits": bits,
+            "cache": "cold", "us": round(us, 3), "GBps": round(gbs, 1),
+            "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm", "bytes": nbytes}
+
+
 def bench_kv_append(B, Hk, S, D, bits, calls, dev):
     """Quantize-on-append into a quantized KV cache (kvcache.QuantKVCache's
     update_and_fetch): S new K and V rows of B x Hk heads quantized along D
@@ -332,7 +372,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no detail table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="detail sections, comma-separated "
-                                                "(dense, kv8, kvcache, moe, vq); default all")
+                                                "(dense, kv8, kvcache, qsdpa, moe, vq); default all")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 10 plain device copies of MIB MiB (the known-size kernel "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -378,7 +418,7 @@ def main():
     gbs = nbytes / (us * 1e-6) / 1e9
 
     detail = []
-    only = set(args.only.split(",")) if args.only else {"dense", "kv8", "kvcache", "moe", "vq"}
+    only = set(args.only.split(",")) if args.only else {"dense", "kv8", "kvcache", "qsdpa", "moe", "vq"}
     if not args.quick and "vq" in only:
         for kc_ in (256, 4096):
             for t_ in (1, 16):
@@ -396,6 +436,10 @@ def main():
     if not args.quick and "kvcache" in only:
         for s_ in (1, 512):
             detail.append(bench_kv_append(4, 4, s_, 128, 8, 200 if s_ == 1 else 50, dev))
+    if not args.quick and "qsdpa" in only:
+        for n_ in (8192, 32768):
+            for l_ in (1, 4):
+                detail.append(bench_qsdpa(4, 32, 4, l_, n_, 128, 8, 30, dev))
     if not args.quick and "dense" in only:
         for b_ in (4, 8):
             for shape in ((14336, 4096), (4096, 14336)):

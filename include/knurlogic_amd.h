@@ -149,6 +149,54 @@ int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
 size_t kmi_kv8_workspace_bytes(int B, int H, int Hk, int L, int N, int D);
 
 /*
+ * mx.quantized_matmul with a batched weight, transpose=True or False: the
+ * products of mlx-lm's quantized scaled-dot-product attention
+ * (src/knurlogic/engine/families/glm5/architecture/glm5_next/_mlx_vlm/
+ * models/base.py:281-297: scores = q K^T, transpose=True; out = P V,
+ * transpose=False) and of QuantizedMultiLinear (.../_mlx_vlm/models/
+ * mla.py:80-87; transpose=False at .../glm5_next/language.py:760).
+ *   for every batch index b (nd <= 4 dimensions of batch_shape):
+ *     transpose=1: y[b] = x[b] @ What[b]^T, What[b] [N, K], groups along K
+ *     transpose=0: y[b] = x[b] @ What[b],   What[b] [K, N], groups along N
+ *   x[b] [M, K] bf16, optionally staged as bf16(x * x_scale) (x_scale = 1:
+ *   unchanged), y contiguous [batch..., M, N] bf16.
+ * Strides are in elements (x, scales / biases) or words (w): *_strides[d]
+ * for batch dimension d (0 broadcasts), then *_strides[nd] between rows.
+ * x rows and batch strides are multiples of 8 elements from a 16-byte
+ * aligned base, and each row is read in 16-byte units: the elements up to
+ * the next multiple of 8 past K must be readable memory (their values are
+ * ignored).  With transpose=1 the weight rows are 16-byte aligned.
+ * The weight tile is dequantized to bf16 operands (as mlx's tiled qmm),
+ * fp32 accumulation.  `workspace` (kmi_qmm_batched_workspace_bytes) holds
+ * split-K partials; it may be NULL when that size is 0.
+ */
+size_t kmi_qmm_batched_workspace_bytes(int nd, const int64_t* batch_shape, int64_t M, int64_t K, int64_t N);
+int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, const int64_t* w_strides,
+                    const void* scales, const void* biases, const int64_t* s_strides, int nd,
+                    const int64_t* batch_shape, int64_t M, int64_t K, int64_t N, int transpose, int dtype,
+                    int group_size, int bits, float x_scale, void* y, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* mask kinds of kmi_masked_softmax */
+#define KMI_MASK_NONE 0
+#define KMI_MASK_BOOL 1   /* uint8, nonzero = visible; hidden scores become finfo(bf16).min */
+#define KMI_MASK_ADD 2    /* bf16 added to the scores (rounded to bf16) */
+#define KMI_MASK_CAUSAL 3 /* key j hidden from query row l of L when j > N - L + l */
+
+/*
+ * The step between mlx-lm's two quantized attention products
+ * (.../_mlx_vlm/models/base.py:285-295): mask, then
+ * mx.softmax(scores, precise=True) -- max, exp and sum in fp32, the
+ * probabilities rounded to bf16.  Rows of x [R, N] (row stride ldx) are
+ * indexed by row_dims[4] (row = ((i0*d1 + i1)*d2 + i2)*d3 + i3, d3 the query
+ * length L); mask_strides[4] are the mask's element strides over those four
+ * dimensions (0 broadcasts), its last axis contiguous.  out may alias x.
+ */
+int kmi_masked_softmax(const void* x, int64_t ldx, int dtype, const int64_t* row_dims, int64_t N,
+                       const void* mask, int mask_kind, const int64_t* mask_strides, void* out, int64_t ldo,
+                       void* stream);
+
+/*
  * The MoE router of Qwen3.5-MoE's SparseMoeBlock
  * (src/knurlogic/engine/families/qwen/architecture/qwen3_5.py:174-179):
  * probs = softmax(logits) in float32; the top k in descending order (equal

@@ -7,8 +7,11 @@ one HIP kernel over the packed K/V (kmi_kv8_decode) instead of
 dequantizing the cache; ``supports`` (:213-238) is the routing rule;
 ``sdpa`` (:301-320) is the dispatch a model's attention calls, which takes
 the kernel when handed exactly the keys the quantized cache just returned
-and otherwise falls back to dequantize + scaled-dot-product attention (both
-on the GPU); ``STATS`` counts hits and misses (:25-53).
+and otherwise falls back as mlx-lm's base dispatch does: a cache with a
+``bits`` attribute (mlx-lm's own quantized cache) through
+``quantized_sdpa``, the two quantized products of
+.../_mlx_vlm/models/base.py:260-302, else dequantize + scaled-dot-product
+attention (all on the GPU); ``STATS`` counts hits and misses (:25-53).
 
 A query row whose every key is masked returns 0 here (the reference
 kernel's rule, :11-12), where a plain softmax would give NaN.
@@ -21,7 +24,7 @@ import math
 import torch
 
 from . import _abi
-from .ops import DTYPE_CODE, _on_gpu, _ptr, _stream, dequantize
+from .ops import DTYPE_CODE, _on_gpu, _ptr, _stream, dequantize, qmm_batched
 
 logger = logging.getLogger(__name__)
 
@@ -170,6 +173,103 @@ def dequant_sdpa(q, K, V, scale: float, mask=None, group: int = 64, bits: int = 
     return o.to(q.dtype)
 
 
+#: KMI_MASK_* of include/knurlogic_amd.h
+MASK_NONE, MASK_BOOL, MASK_ADD, MASK_CAUSAL = 0, 1, 2, 3
+
+
+def align_mask(mask, ndim: int):
+    """mlx-lm's align_attention_mask_to_scores (.../_mlx_vlm/models/
+    base.py:242-257): size-1 axes inserted just before the last two until
+    the mask has the scores' rank, so a (B, 1, L, N) batch mask does not
+    alias B with the KV heads of (B, Hk, rep, L, N) scores."""
+    if mask is None or isinstance(mask, str):
+        return mask
+    while mask.dim() < ndim:
+        mask = mask.unsqueeze(max(mask.dim() - 2, 0))
+    return mask
+
+
+def masked_softmax(scores, mask=None, out=None):
+    """The step between mlx-lm's two quantized attention products
+    (base.py:285-295) on bf16 scores [..., L, N] (kmi_masked_softmax): a
+    bool mask hides scores with finfo(bf16).min, a bf16 mask is added,
+    "causal" hides key j from query row l when j > N - L + l; then
+    softmax(precise=True), probabilities rounded to bf16.  ``out`` may be a
+    row-padded view of the same shape."""
+    if scores.dtype != torch.bfloat16 or scores.stride(-1) != 1 or scores.dim() < 2 or scores.dim() > 5:
+        raise ValueError("masked_softmax: bf16 scores [..., L, N] with a contiguous last axis")
+    _on_gpu(scores)
+    lead = tuple(scores.shape[:-1])
+    N = scores.shape[-1]
+    if out is None:
+        out = torch.empty_like(scores)
+    rows = scores.reshape(-1, N) if scores.is_contiguous() else None
+    if rows is None or out.stride(-1) != 1:
+        raise ValueError("masked_softmax: scores must be contiguous, out's last axis contiguous")
+    ldo = out.stride(-2)
+    if any(out.stride(d) != out.shape[d + 1] * out.stride(d + 1) for d in range(out.dim() - 2)):
+        raise ValueError("masked_softmax: out must be a row-padded contiguous block")
+    dims = [1] * (4 - len(lead)) + list(lead)
+    kind, mt, mstr = MASK_NONE, None, [0, 0, 0, 0]
+    if isinstance(mask, str):
+        if mask != "causal":
+            raise ValueError(f"masked_softmax: mask {mask!r}")
+        kind = MASK_CAUSAL
+    elif mask is not None:
+        _on_gpu(mask)
+        if mask.dtype == torch.bool:
+            kind = MASK_BOOL
+        elif mask.dtype == torch.bfloat16:
+            kind = MASK_ADD
+        else:
+            raise ValueError(f"masked_softmax: an additive mask must be bf16 like the scores (got {mask.dtype})")
+        m = align_mask(mask, scores.dim())
+        try:
+            m = m.expand(*scores.shape)
+        except RuntimeError as e:
+            raise ValueError(f"masked_softmax: mask {tuple(mask.shape)} does not broadcast to "
+                             f"scores {tuple(scores.shape)}") from e
+        if m.stride(-1) != 1:
+            m = m.contiguous()
+        mt = m.view(torch.uint8) if kind == MASK_BOOL else m
+        mstr = [0] * (4 - len(lead)) + [m.stride(d) for d in range(len(lead))]
+    dt = torch.tensor(dims, dtype=torch.int64)
+    ms = torch.tensor(mstr, dtype=torch.int64)
+    _abi.check(_abi.load().kmi_masked_softmax(
+        _ptr(scores), N, DTYPE_CODE[scores.dtype], dt.data_ptr(), N, _ptr(mt), kind, ms.data_ptr(),
+        _ptr(out), ldo, _stream(scores)), "masked_softmax")
+    return out
+
+
+def quantized_sdpa(queries, q_keys, q_values, scale: float, mask=None, group_size: int = 64,
+                   bits: int = 8):
+    """mlx-lm's quantized_scaled_dot_product_attention (.../_mlx_vlm/
+    models/base.py:260-302) over quantized K/V triples (packed, scales,
+    biases) of shape (B, Hk, N, *): q scaled (rounded to bf16), scores =
+    quantized_matmul(q, K, transpose=True) in bf16, masked, softmax(precise)
+    in bf16, out = quantized_matmul(p, V, transpose=False).  GQA query heads
+    share their KV head's triple (broadcast, never copied).  Three HIP
+    launches (four when the keys are split across workgroups)."""
+    B, Hq, L, D = queries.shape
+    Hk = q_keys[0].shape[-3]
+    if Hq % Hk:
+        raise ValueError(f"quantized_sdpa: {Hq} query heads over {Hk} KV heads")
+    rep = Hq // Hk
+    q = queries
+    Kt, Vt = tuple(q_keys), tuple(q_values)
+    if rep > 1:
+        q = q.reshape(B, Hk, rep, L, D)
+        Kt = tuple(t.unsqueeze(-3) for t in Kt)
+        Vt = tuple(t.unsqueeze(-3) for t in Vt)
+    scores = qmm_batched(q, *Kt, transpose=True, group_size=group_size, bits=bits, x_scale=float(scale))
+    N = scores.shape[-1]
+    Np = -(-N // 8) * 8
+    pbuf = torch.empty(*scores.shape[:-1], Np, dtype=scores.dtype, device=scores.device)
+    p = masked_softmax(scores, mask, out=pbuf[..., :N])
+    out = qmm_batched(p, *Vt, transpose=False, group_size=group_size, bits=bits)
+    return out.reshape(B, Hq, L, -1) if rep > 1 else out
+
+
 def sdpa(queries, keys, values, cache, scale, mask, sinks=None):
     """The dispatch a model's attention calls (kvattn.sdpa): the 8-bit
     kernel when ``cache`` just handed back exactly these keys for a short
@@ -187,6 +287,12 @@ def sdpa(queries, keys, values, cache, scale, mask, sinks=None):
         else:
             count(True)
             return decode_sdpa(queries, K, V, scale, mask, g, 8, same_layout=True)
+    if hasattr(cache, "bits"):
+        # mlx-lm's own quantized cache (a `bits` attribute): its fetch hands
+        # back the triples, attention goes through the two quantized products
+        if sinks is not None:
+            raise ValueError("Quantized SDPA does not support attention sinks.")
+        return quantized_sdpa(queries, keys, values, scale, mask, cache.group_size, cache.bits)
     if sinks is not None:
         raise ValueError("sdpa: attention sinks are not implemented")
     from .kvcache import materialize          # a quantized cache's lazily dequantized K / V

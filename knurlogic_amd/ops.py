@@ -141,13 +141,15 @@ def _check_affine_operands(x, w, scales, biases, group_size, bits, what):
 def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                      biases: torch.Tensor | None = None, transpose: bool = True,
                      group_size: int = 64, bits: int = 4, mode: str = "affine"):
-    """``mx.quantized_matmul``: x [..., K] @ What^T with What [N, K]
-    (transpose=True), fp32 accumulation, the result in x's dtype."""
+    """``mx.quantized_matmul``: x [..., M, K] @ What^T with What [..., N, K]
+    (transpose=True) or x @ What with What [..., K, N] (transpose=False,
+    groups along N), fp32 accumulation, the result in x's dtype.  A 2-D
+    What with transpose=True is the dense projection (kmi_qmm); a batched
+    What (leading dimensions broadcast against x's) or transpose=False runs
+    kmi_qmm_batched."""
     _check_mode(mode)
-    if not transpose:
-        raise ValueError("quantized_matmul: transpose=False is not implemented")
-    if w.ndim != 2:
-        raise ValueError("quantized_matmul: w must be 2-D (use gather_qmm for experts)")
+    if not transpose or w.ndim != 2:
+        return qmm_batched(x, w, scales, biases, transpose, group_size, bits)
     _check_affine_operands(x, w, scales, biases, group_size, bits, "quantized_matmul")
     K = x.shape[-1]
     N = w.shape[0]
@@ -164,6 +166,112 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                          group_size, bits, _ptr(y), _ptr(ws), nbytes, _stream(x)),
                "quantized_matmul")
     return y
+
+
+def _aligned_rows(x: torch.Tensor) -> torch.Tensor:
+    """x with a contiguous last axis, rows and batch strides multiples of 8
+    elements from a 16-byte aligned base, and readable memory up to the
+    next multiple of 8 past the last row (kmi_qmm_batched reads rows in
+    16-byte units); a zero-padded copy otherwise."""
+    K = x.shape[-1]
+    Kp = -(-K // 8) * 8
+    ok = x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and \
+        all(st % 8 == 0 for d, st in enumerate(x.stride()[:-1]) if x.shape[d] > 1)
+    if ok and Kp != K:
+        last = x.storage_offset() + sum((n - 1) * st for n, st in zip(x.shape, x.stride()))
+        ok = last + (Kp - K) < x.untyped_storage().nbytes() // x.element_size()
+    if ok:
+        return x
+    xp = torch.zeros(*x.shape[:-1], Kp, dtype=x.dtype, device=x.device)
+    xp[..., :K] = x
+    return xp[..., :K]
+
+
+def _fold(shape, strides, M, xr):
+    """Batch dimensions of (x, w, scales) strides: drop size-1 dimensions,
+    fold trailing dimensions that only x walks (w broadcast, x rows
+    consecutive) into M, merge dimensions contiguous in all three."""
+    dims = [(n, list(st)) for n, st in zip(shape, strides) if n != 1]
+    while dims and dims[-1][1][1] == 0 and dims[-1][1][2] == 0 and dims[-1][1][0] == M * xr:
+        M *= dims.pop()[0]
+    merged = []
+    for n, st in dims:
+        if merged and all(merged[-1][1][i] == n * st[i] for i in range(3)):
+            merged[-1] = (merged[-1][0] * n, st)
+        else:
+            merged.append((n, st))
+    return merged, M
+
+
+def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 64,
+                bits: int = 4, x_scale: float = 1.0):
+    """mx.quantized_matmul with batch dimensions on w (broadcast against
+    x's) in either orientation; ``x_scale`` != 1 multiplies x by it first,
+    rounded to x's dtype (mlx-lm's ``queries *= scale``)."""
+    what = "quantized_matmul"
+    if biases is None:
+        raise ValueError(f"{what}: affine mode needs biases")
+    _on_gpu(x, w, scales, biases)
+    if x.dtype != torch.bfloat16 or scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
+        raise ValueError(f"{what}: only bfloat16 activations, scales and biases are implemented")
+    if w.dtype not in (torch.uint32, torch.int32) or w.ndim < 2:
+        raise ValueError(f"{what}: w must be packed uint32 with at least 2 dimensions")
+    if bits not in (4, 8) or group_size not in (32, 64, 128):
+        raise ValueError(f"{what}: bits {bits} / group {group_size} not implemented (4, 8 / 32, 64, 128)")
+    vec = x.ndim == 1
+    if vec:
+        x = x[None]
+    K = x.shape[-1]
+    if transpose:
+        N, Kw, grouped = w.shape[-2], w.shape[-1] * 32 // bits, K
+    else:
+        N, Kw = w.shape[-1] * 32 // bits, w.shape[-2]
+        grouped = N
+    if Kw != K:
+        raise ValueError(f"{what}: x has {K} features but w holds {Kw} (transpose={transpose})")
+    if scales.shape != biases.shape or scales.shape[:-1] != w.shape[:-1] \
+            or scales.shape[-1] * group_size != grouped:
+        raise ValueError(f"{what}: scales {tuple(scales.shape)} / biases {tuple(biases.shape)} "
+                         f"do not match w {tuple(w.shape)} at group {group_size}")
+    M = x.shape[-2]
+    try:
+        batch = torch.broadcast_shapes(tuple(x.shape[:-2]), tuple(w.shape[:-2]))
+    except RuntimeError as e:
+        raise ValueError(f"{what}: batch shapes {tuple(x.shape[:-2])} and {tuple(w.shape[:-2])} "
+                         "do not broadcast") from e
+    y = torch.empty(*batch, M, N, dtype=x.dtype, device=x.device)
+    if y.numel() == 0:
+        return y[0] if vec else y
+    x = _aligned_rows(x)
+    if w.stride(-1) != 1 or (transpose and (w.data_ptr() % 16 or any(
+            st % 4 for d, st in enumerate(w.stride()[:-1]) if w.shape[d] > 1))):
+        w = w.contiguous()
+        if w.data_ptr() % 16:
+            w = w.clone()
+    if scales.stride() != biases.stride() or scales.stride(-1) != 1:
+        scales, biases = scales.contiguous(), biases.contiguous()
+    xe = x.expand(*batch, M, K)
+    we = w.expand(*batch, *w.shape[-2:])
+    se = scales.expand(*batch, *scales.shape[-2:])
+    be = biases.expand(*batch, *biases.shape[-2:])
+    nb = len(batch)
+    dims, Mf = _fold(batch, [(xe.stride(d), we.stride(d), se.stride(d)) for d in range(nb)],
+                     M, xe.stride(-2))
+    if len(dims) > 4:
+        raise ValueError(f"{what}: more than 4 batch dimensions after merging ({len(dims)})")
+    nd = len(dims)
+    shape = torch.tensor([n for n, _ in dims] or [1], dtype=torch.int64)
+    xs = torch.tensor([st[0] for _, st in dims] + [xe.stride(-2)], dtype=torch.int64)
+    ws_ = torch.tensor([st[1] for _, st in dims] + [we.stride(-2)], dtype=torch.int64)
+    ss = torch.tensor([st[2] for _, st in dims] + [se.stride(-2)], dtype=torch.int64)
+    L = _lib()
+    nbytes = L.kmi_qmm_batched_workspace_bytes(nd, shape.data_ptr(), Mf, K, N)
+    ws = _workspace(nbytes, x.device)
+    _abi.check(L.kmi_qmm_batched(
+        _ptr(xe), xs.data_ptr(), _ptr(we), ws_.data_ptr(), _ptr(se), _ptr(be), ss.data_ptr(), nd,
+        shape.data_ptr(), Mf, K, N, int(bool(transpose)), DTYPE_CODE[x.dtype], group_size, bits,
+        float(x_scale), _ptr(y), _ptr(ws), nbytes, _stream(x)), what)
+    return y[0] if vec else y
 
 
 def _flat_indices(x, w, lhs_indices, rhs_indices):

@@ -26,6 +26,12 @@ sites, and pinned as follows (each function's docstring names its pins):
 * quantized_matmul / gather_qmm -- float64 brute force through an
   independently written numpy dequantize, linearity and row independence,
   and the reference's 2e-3 bar (tests/engine/test_deepseek_v4_bf16.py:247-270).
+  The batched form (both orientations, broadcast batches) -- on-grid
+  weights packed independently of the oracle, against a dense float64
+  product.
+* quantized attention (mlx-lm's base.py:260-302) -- float64 attention
+  (``sdpa_numpy_f64``) within the bf16 roundings the path makes, and the
+  exact uniform softmax of a fully hidden row.
 * router / SwiGLU / combine / shared expert -- the reference's golden
   ``qwen_reference.npz`` key ``qwen3_5_moe/bf16/0.mlp`` (HF transformers'
   bf16 block, bit for bit), committed as tests/golden/qwen35_moe_block.npz.
@@ -234,6 +240,85 @@ def gather_qmm(x, wq, scales, biases, lhs_indices=None, rhs_indices=None,
                              group_size, bits, "float32")
         out[sel] = y.reshape(sel.size, M, N)
     return round_to(out, out_dtype).reshape(*ishape, M, N)
+
+
+def quantized_matmul_batched(x, wq, scales, biases, transpose: bool = True,
+                             group_size: int = 64, bits: int = 4,
+                             out_dtype: str = "bfloat16"):
+    """mx.quantized_matmul with batch dimensions on w, broadcast against
+    x's (numpy broadcasting of x [..., M, K] and w [..., R, C]); each batch
+    entry is the 2-D ``quantized_matmul`` above (exact product rounded once).
+    The products of mlx-lm's quantized attention
+    (.../_mlx_vlm/models/base.py:281-297) and of QuantizedMultiLinear
+    (.../_mlx_vlm/models/mla.py:80-87).  Pinned by on-grid weights packed
+    independently (tests/test_oracle.py)."""
+    x = _f32(x)
+    wq = np.asarray(wq, np.uint32)
+    s, b = _f32(scales), _f32(biases)
+    M, K = x.shape[-2], x.shape[-1]
+    batch = np.broadcast_shapes(x.shape[:-2], wq.shape[:-2])
+    xb = np.broadcast_to(x, batch + (M, K)).reshape(-1, M, K)
+    wb = np.broadcast_to(wq, batch + wq.shape[-2:]).reshape(-1, *wq.shape[-2:])
+    sb = np.broadcast_to(s, batch + s.shape[-2:]).reshape(-1, *s.shape[-2:])
+    bb = np.broadcast_to(b, batch + b.shape[-2:]).reshape(-1, *b.shape[-2:])
+    N = wq.shape[-2] if transpose else wq.shape[-1] * 32 // bits
+    out = np.zeros((xb.shape[0], M, N), np.float32)
+    for i in range(xb.shape[0]):
+        out[i] = quantized_matmul(xb[i], wb[i], sb[i], bb[i], transpose, group_size, bits,
+                                  "float32", nthreads=1)
+    return round_to(out, out_dtype).reshape(*batch, M, N)
+
+
+#: mx.finfo(mx.bfloat16).min, what a hidden score becomes
+BF16_LOWEST = -3.3895313892515355e38
+
+
+def align_mask(mask, ndim: int):
+    """align_attention_mask_to_scores (.../_mlx_vlm/models/base.py:242-257):
+    size-1 axes inserted before the last two until the ranks match."""
+    m = np.asarray(mask)
+    while m.ndim < ndim:
+        m = np.expand_dims(m, max(m.ndim - 2, 0))
+    return m
+
+
+def quantized_sdpa(q, K, V, scale: float, mask=None, group_size: int = 64, bits: int = 8):
+    """mlx-lm's quantized_scaled_dot_product_attention
+    (.../_mlx_vlm/models/base.py:260-302) in bfloat16: q *= scale (rounded),
+    scores = quantized_matmul(q, K, transpose=True) (rounded), a bool mask
+    puts finfo(bf16).min where it is False, an additive mask is added
+    (rounded), "causal" keeps key j for query l of L when j <= N - L + l;
+    softmax(precise=True) in float32, probabilities rounded; out =
+    quantized_matmul(p, V, transpose=False) (rounded).  q [B, Hq, L, D]; K,
+    V = (packed, scales, biases) of [B, Hk, N, *].  Pinned against
+    ``sdpa_numpy_f64`` and by the uniform softmax of a fully hidden row
+    (tests/test_oracle.py)."""
+    q = _f32(q)
+    B, Hq, L, D = q.shape
+    Hk = np.asarray(K[0]).shape[-3]
+    rep = Hq // Hk
+    qs = bf16_round(q * np.float32(scale))
+    Ke, Ve = tuple(K), tuple(V)
+    if rep > 1:
+        qs = qs.reshape(B, Hk, rep, L, D)
+        Ke = tuple(np.expand_dims(np.asarray(t), -3) for t in Ke)
+        Ve = tuple(np.expand_dims(np.asarray(t), -3) for t in Ve)
+    scores = quantized_matmul_batched(qs, *Ke, True, group_size, bits, "bfloat16")
+    N = scores.shape[-1]
+    if mask is not None:
+        if isinstance(mask, str):
+            m = np.arange(N - L, N)[:, None] >= np.arange(N)[None]
+        else:
+            m = align_mask(mask, scores.ndim)
+        if m.dtype == bool:
+            scores = np.where(m, scores, np.float32(BF16_LOWEST)).astype(np.float32)
+        else:
+            scores = bf16_round((scores + _f32(m)).astype(np.float32))
+    mx = scores.max(axis=-1, keepdims=True)
+    e = np.exp((scores - mx).astype(np.float32))
+    p = bf16_round((e / e.sum(axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32))
+    out = quantized_matmul_batched(p, *Ve, False, group_size, bits, "bfloat16")
+    return out.reshape(B, Hq, L, -1)
 
 
 # --- the Qwen3.5-MoE router, SwiGLU and SwitchGLU ----------------------------

@@ -258,6 +258,98 @@ def test_causal_rows_see_their_own_prefix():
     assert O.mask_rows("causal", 2, 1, 6) is None
 
 
+# --- batched quantized_matmul and mlx-lm's quantized attention -----------------
+
+def _on_grid(rng, lead, R, C, group, bits):
+    """Packed words, scales, biases and the dense float64 weight they encode,
+    built from random codes with numpy bit operations (independent of the
+    oracle's packing and dequantize).  The weight is [..., R, C] quantized
+    along C in groups of `group`."""
+    q = rng.integers(0, 1 << bits, size=lead + (R, C), dtype=np.uint64)
+    epw = 32 // bits
+    words = np.zeros(lead + (R, C // epw), np.uint64)
+    for i in range(epw):
+        words |= q[..., i::epw] << np.uint64(bits * i)
+    s = bf16_normal(rng, lead + (R, C // group), 0.01)
+    b = bf16_normal(rng, lead + (R, C // group), 0.05)
+    dense = np.repeat(s.astype(np.float64), group, -1) * q.astype(np.float64) + \
+        np.repeat(b.astype(np.float64), group, -1)
+    return words.astype(np.uint32), s, b, dense
+
+
+@pytest.mark.parametrize("transpose", [True, False])
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 32), (4, 128)])
+def test_batched_qmm_on_grid_weights_equals_the_dense_product(transpose, bits, group):
+    """A transposed operand, a group read along the wrong axis or a batch
+    entry paired with the wrong weight all fail this."""
+    rng = np.random.default_rng(11)
+    M, K, N = 3, 256, 128
+    R, C = (N, K) if transpose else (K, N)
+    wq, s, b, dense = _on_grid(rng, (1, 3), R, C, group, bits)
+    x = bf16_normal(rng, (2, 1, M, K))
+    got = O.quantized_matmul_batched(x, wq, s, b, transpose, group, bits, "float32")
+    wmat = np.swapaxes(dense, -1, -2) if transpose else dense
+    ref = np.matmul(x.astype(np.float64), wmat)
+    assert got.shape == (2, 3, M, N)
+    assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+
+
+def _qsdpa_case(rng, B, Hq, Hk, L, N, D, bits=8):
+    q = bf16_normal(rng, (B, Hq, L, D))
+    k = bf16_normal(rng, (B, Hk, N, D))
+    v = bf16_normal(rng, (B, Hk, N, D))
+    return q, O.quantize(k, 64, bits), O.quantize(v, 64, bits)
+
+
+@pytest.mark.parametrize("mask", [None, "causal", "bool", "additive"])
+def test_quantized_sdpa_matches_float64_attention(mask):
+    """Within the bf16 roundings of q*scale, the scores and the
+    probabilities (relative 2^-8 each), the result is float64 attention
+    over the dequantized cache.  A transposed V product or the scale
+    applied twice fails by far more."""
+    rng = np.random.default_rng(12)
+    B, Hq, Hk, L, N, D = 2, 8, 2, 3, 96, 128
+    q, K, V = _qsdpa_case(rng, B, Hq, Hk, L, N, D)
+    kd, vd = O.dequantize_numpy_f64(*K, 64, 8), O.dequantize_numpy_f64(*V, 64, 8)
+    scale = D ** -0.5
+    ref_mask, m = mask, mask
+    if mask == "bool":
+        m = rng.random((B, 1, L, N)) > 0.3
+        ref_mask = m
+    elif mask == "additive":
+        m = O.bf16_round(rng.standard_normal((B, 1, L, N)).astype(np.float32))
+        ref_mask = None
+    qs = O.bf16_round(q * np.float32(scale)).astype(np.float64)
+    if mask == "additive":
+        s = np.einsum("bhld,bhnd->bhln", qs.reshape(B, Hk, Hq // Hk, L, D).reshape(B, Hq, L, D),
+                      np.repeat(kd, Hq // Hk, axis=1)) + m
+        p = np.exp(s - s.max(-1, keepdims=True))
+        ref = np.einsum("bhln,bhnd->bhld", p / p.sum(-1, keepdims=True), np.repeat(vd, Hq // Hk, axis=1))
+    else:
+        ref = O.sdpa_numpy_f64(qs, kd, vd, 1.0, ref_mask)
+    got = O.quantized_sdpa(q, K, V, scale, m, 64, 8)
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err < 2e-2, err
+
+
+def test_quantized_sdpa_hidden_row_is_the_plain_mean_of_v():
+    """A row whose every key is hidden scores finfo(bf16).min everywhere, so
+    its softmax is uniform: with N a power of two the probabilities 1/N are
+    exact in bf16 and the row is the mean of the dequantized V, rounded once
+    (not 0, the 8-bit kernel's rule)."""
+    rng = np.random.default_rng(13)
+    B, Hq, Hk, L, N, D = 1, 4, 2, 2, 64, 64
+    q, K, V = _qsdpa_case(rng, B, Hq, Hk, L, N, D, bits=4)
+    m = np.ones((B, 1, L, N), bool)
+    m[0, 0, 1, :] = False
+    got = O.quantized_sdpa(q, K, V, 0.125, m, 64, 4)
+    vd = O.dequantize_numpy_f64(*V, 64, 4)
+    mean = vd.mean(axis=2)                                  # [B, Hk, D]
+    want = O.bf16_round(mean.astype(np.float32))
+    for h in range(Hq):
+        assert np.array_equal(got[0, h, 1], want[0, h // 2])
+
+
 # --- VQ decode matmul ----------------------------------------------------------------
 
 @pytest.mark.parametrize("code_dtype,kc", [(np.uint8, 256), (np.uint16, 4096)])
