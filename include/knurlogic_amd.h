@@ -159,7 +159,8 @@ size_t kmi_kv8_workspace_bytes(int B, int H, int Hk, int L, int N, int D);
  *     transpose=1: y[b] = x[b] @ What[b]^T, What[b] [N, K], groups along K
  *     transpose=0: y[b] = x[b] @ What[b],   What[b] [K, N], groups along N
  *   x[b] [M, K] bf16, optionally staged as bf16(x * x_scale) (x_scale = 1:
- *   unchanged), y contiguous [batch..., M, N] bf16.
+ *   unchanged), y [batch..., M, N] bf16 with row stride ldy >= N (rows
+ *   otherwise contiguous).
  * Strides are in elements (x, scales / biases) or words (w): *_strides[d]
  * for batch dimension d (0 broadcasts), then *_strides[nd] between rows.
  * x rows and batch strides are multiples of 8 elements from a 16-byte
@@ -174,7 +175,7 @@ size_t kmi_qmm_batched_workspace_bytes(int nd, const int64_t* batch_shape, int64
 int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, const int64_t* w_strides,
                     const void* scales, const void* biases, const int64_t* s_strides, int nd,
                     const int64_t* batch_shape, int64_t M, int64_t K, int64_t N, int transpose, int dtype,
-                    int group_size, int bits, float x_scale, void* y, void* workspace,
+                    int group_size, int bits, float x_scale, void* y, int64_t ldy, void* workspace,
                     size_t workspace_bytes, void* stream);
 
 /* mask kinds of kmi_masked_softmax */
@@ -190,7 +191,9 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
  * probabilities rounded to bf16.  Rows of x [R, N] (row stride ldx) are
  * indexed by row_dims[4] (row = ((i0*d1 + i1)*d2 + i2)*d3 + i3, d3 the query
  * length L); mask_strides[4] are the mask's element strides over those four
- * dimensions (0 broadcasts), its last axis contiguous.  out may alias x.
+ * dimensions (0 broadcasts), its last axis contiguous.  Rows of x and out
+ * are 16-byte aligned and padded to a multiple of 8 elements (ldx, ldo >=
+ * N rounded up to 8); out's padding is written with zeros.  out may alias x.
  */
 int kmi_masked_softmax(const void* x, int64_t ldx, int dtype, const int64_t* row_dims, int64_t N,
                        const void* mask, int mask_kind, const int64_t* mask_strides, void* out, int64_t ldo,

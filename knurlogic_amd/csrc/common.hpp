@@ -91,6 +91,15 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> two bf16 (round to nearest even) in one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+    const f32x2_t v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 // 16x16x32 bf16 MFMA, fp32 accumulate (gfx950).  Lane l holds A[m = l%16]
 // [k-run l/16], B[k-run l/16][n = l%16]; D[m = 4*(l/16)+i][n = l%16] in
 // item i.  A and B share the k-run mapping, so any permutation of k

@@ -185,13 +185,6 @@ struct QgemmArgs {
 constexpr int Q5M = 256, Q5N = 128, Q5K = 64, Q5LDS = Q5K + 8;
 constexpr int Q5_RING = 4;
 
-typedef __bf16 q5_bf16x2 __attribute__((ext_vector_type(2)));
-typedef float q5_f32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {   // v_cvt_pk_bf16_f32
-    const q5_f32x2 v = {lo, hi};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, q5_bf16x2));
-}
 
 __device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);

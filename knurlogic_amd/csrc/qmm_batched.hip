@@ -37,10 +37,11 @@ struct QbArgs {
     const uint32_t* w;
     const uint16_t* s;
     const uint16_t* b;
-    uint16_t* y;                 // [P, M, N] bf16, when S == 1
+    uint16_t* y;                 // [P, M, ldy] bf16, when S == 1
     float* partial;              // [S, P, M, N] fp32, when S > 1
     int64_t M, K, N;
     int64_t xr, wr, sr;          // row strides: x in elements, w in words, scales / biases in elements
+    int64_t ldy;                 // row stride of y (elements)
     int nd;
     int64_t shape[QB_MAXD], xs[QB_MAXD], ws[QB_MAXD], ss[QB_MAXD];
     int64_t P;                   // batch entries (product of shape)
@@ -49,15 +50,12 @@ struct QbArgs {
     float x_scale;
 };
 
-__device__ __forceinline__ uint32_t qb_pack(float lo, float hi) {
-    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
-}
+__device__ __forceinline__ uint32_t qb_pack(float lo, float hi) { return cvt_pk_bf16(lo, hi); }
 
 // two fp32 values -> their bf16 hi parts and lo = bf16(v - hi), packed
 __device__ __forceinline__ void qb_split(float v0, float v1, uint32_t& hi, uint32_t& lo) {
-    const uint16_t h0 = f32_to_bf16(v0), h1 = f32_to_bf16(v1);
-    hi = (uint32_t)h0 | ((uint32_t)h1 << 16);
-    lo = qb_pack(v0 - bf16_to_f32(h0), v1 - bf16_to_f32(h1));
+    hi = cvt_pk_bf16(v0, v1);
+    lo = cvt_pk_bf16(v0 - __uint_as_float(hi << 16), v1 - __uint_as_float(hi & 0xffff0000u));
 }
 
 __device__ __forceinline__ float qb_code(uint32_t word, int i, int bits) {
@@ -66,9 +64,11 @@ __device__ __forceinline__ float qb_code(uint32_t word, int i, int bits) {
 
 template <int BITS, int GS, bool TRANS>
 __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
-    __shared__ __align__(16) uint16_t As[2][QB_T * QB_LD];
-    __shared__ __align__(16) uint16_t Bh[2][QB_T * QB_LD];     // hi parts of the dequantized weight
-    __shared__ __align__(16) uint16_t Bl[2][QB_T * QB_LD];     // lo parts
+    // one LDS stage (27 KB: five workgroups per CU); the next k-tile's
+    // global loads are in flight in registers while this one is multiplied
+    __shared__ __align__(16) uint16_t As[QB_T * QB_LD];
+    __shared__ __align__(16) uint16_t Bh[QB_T * QB_LD];     // hi parts of the dequantized weight
+    __shared__ __align__(16) uint16_t Bl[QB_T * QB_LD];     // lo parts
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
         }
     };
 
-    auto store = [&](int64_t kt, int buf) {
+    auto store = [&](int64_t kt) {
         // x: zero the elements past K of a run that straddles it, apply the scale
         const int64_t k0 = kt * QB_T + 16 * xc;
 #pragma unroll
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
                                    bf16_to_f32((uint16_t)(u >> 16)) * a.x_scale);
                 }
             }
-            *(u32x4*)&As[buf][xrow * QB_LD + 16 * xc + 8 * h] = v;
+            *(u32x4*)&As[xrow * QB_LD + 16 * xc + 8 * h] = v;
         }
         if constexpr (TRANS) {
             const float sc = bf16_to_f32((uint16_t)rsv[0]), bi = bf16_to_f32((uint16_t)rbv[0]);
@@ -189,8 +189,8 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
                 const float v1 = __builtin_fmaf(sc, qb_code(rwv[(i + 1) / CPW], (i + 1) % CPW, BITS), bi);
                 qb_split(v0, v1, oh[i / 2], ol[i / 2]);
             }
-            u32x4* dh = (u32x4*)&Bh[buf][xrow * QB_LD + 16 * xc];
-            u32x4* dl = (u32x4*)&Bl[buf][xrow * QB_LD + 16 * xc];
+            u32x4* dh = (u32x4*)&Bh[xrow * QB_LD + 16 * xc];
+            u32x4* dl = (u32x4*)&Bl[xrow * QB_LD + 16 * xc];
             dh[0] = u32x4{oh[0], oh[1], oh[2], oh[3]};
             dh[1] = u32x4{oh[4], oh[5], oh[6], oh[7]};
             dl[0] = u32x4{ol[0], ol[1], ol[2], ol[3]};
@@ -208,8 +208,8 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
                 uint32_t h0, l0, h1, l1;
                 qb_split(v[0][c], v[1][c], h0, l0);
                 qb_split(v[2][c], v[3][c], h1, l1);
-                *(u32x2*)&Bh[buf][(4 * nq + c) * QB_LD + 4 * kq] = u32x2{h0, h1};
-                *(u32x2*)&Bl[buf][(4 * nq + c) * QB_LD + 4 * kq] = u32x2{l0, l1};
+                *(u32x2*)&Bh[(4 * nq + c) * QB_LD + 4 * kq] = u32x2{h0, h1};
+                *(u32x2*)&Bl[(4 * nq + c) * QB_LD + 4 * kq] = u32x2{l0, l1};
             }
         }
     };
@@ -221,15 +221,15 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
         for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int fr = lane & 15, fk = 8 * (lane >> 4);
-    auto compute = [&](int buf) {
+    auto compute = [&]() {
 #pragma unroll
         for (int kk = 0; kk < QB_T; kk += 32) {
             u32x4 A[2], H[2], Lo[2];
 #pragma unroll
             for (int i = 0; i < 2; i++) {
-                A[i] = *(const u32x4*)&As[buf][(32 * wm + 16 * i + fr) * QB_LD + kk + fk];
-                H[i] = *(const u32x4*)&Bh[buf][(32 * wn + 16 * i + fr) * QB_LD + kk + fk];
-                Lo[i] = *(const u32x4*)&Bl[buf][(32 * wn + 16 * i + fr) * QB_LD + kk + fk];
+                A[i] = *(const u32x4*)&As[(32 * wm + 16 * i + fr) * QB_LD + kk + fk];
+                H[i] = *(const u32x4*)&Bh[(32 * wn + 16 * i + fr) * QB_LD + kk + fk];
+                Lo[i] = *(const u32x4*)&Bl[(32 * wn + 16 * i + fr) * QB_LD + kk + fk];
             }
 #pragma unroll
             for (int i = 0; i < 2; i++)
@@ -241,18 +241,14 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
         }
     };
 
-    if (kt0 < kt1) {
-        issue(kt0);
-        store(kt0, 0);
-        __syncthreads();
-        for (int64_t kt = kt0; kt < kt1; kt++) {
-            const int buf = (int)((kt - kt0) & 1);
-            const bool more = kt + 1 < kt1;
-            if (more) issue(kt + 1);
-            compute(buf);
-            if (more) store(kt + 1, buf ^ 1);
-            __syncthreads();
-        }
+    // LDS-only barriers: the loads of the next k-tile stay in flight
+    if (kt0 < kt1) issue(kt0);
+    for (int64_t kt = kt0; kt < kt1; kt++) {
+        store(kt);
+        lds_barrier();
+        if (kt + 1 < kt1) issue(kt + 1);
+        compute();
+        lds_barrier();
     }
 
 #pragma unroll
@@ -266,7 +262,7 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
                 const int64_t m = (int64_t)mt * QB_T + 32 * wm + 16 * i + 4 * (lane >> 4) + e;
                 if (m >= M) continue;
                 if (a.S == 1)
-                    a.y[(p * M + m) * N + n] = f32_to_bf16(acc[i][j][e]);
+                    a.y[(p * M + m) * a.ldy + n] = f32_to_bf16(acc[i][j][e]);
                 else
                     a.partial[(((int64_t)split * a.P + p) * M + m) * N + n] = acc[i][j][e];
             }
@@ -275,12 +271,20 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
 
 // y = bf16(sum over the S splits, in split order)
 __global__ __launch_bounds__(256) void qmm_batched_reduce(const float* __restrict__ partial, int S,
-                                                          int64_t count, uint16_t* __restrict__ y) {
+                                                          int64_t count, int64_t N, int64_t ldy,
+                                                          uint16_t* __restrict__ y) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
+    // the S loads are issued together, then summed in split order
+    float v[8];
     float s = 0.f;
-    for (int k = 0; k < S; k++) s += partial[k * count + i];
-    y[i] = f32_to_bf16(s);
+    for (int k0 = 0; k0 < S; k0 += 8) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = k0 + k < S ? partial[(k0 + k) * count + i] : 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) s += v[k];
+    }
+    y[(i / N) * ldy + i % N] = f32_to_bf16(s);
 }
 
 // ---- masked softmax --------------------------------------------------------------
@@ -304,19 +308,6 @@ struct SmArgs {
 
 constexpr float BF16_LOWEST = -3.38953139e38f;      // finfo(bfloat16).min
 
-__device__ __forceinline__ float sm_value(const SmArgs& a, const uint16_t* xr, const uint8_t* mb,
-                                          const uint16_t* ma, int64_t j, int64_t vis) {
-    float v = bf16_to_f32(xr[j]);
-    if (a.kind == KMI_MASK_BOOL) {
-        if (!mb[j]) v = BF16_LOWEST;
-    } else if (a.kind == KMI_MASK_ADD) {
-        v = bf16_to_f32(f32_to_bf16(v + bf16_to_f32(ma[j])));
-    } else if (a.kind == KMI_MASK_CAUSAL) {
-        if (j > vis) v = BF16_LOWEST;
-    }
-    return v;
-}
-
 __device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -333,6 +324,59 @@ __device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) 
     return r;
 }
 
+constexpr uint32_t BF16_NEG_INF = 0xff80u;
+
+// Eight scores from j0 on, masked: hidden -> finfo(bf16).min, additive mask
+// added and rounded, past the row -> -inf (adds nothing to the sum).
+__device__ __forceinline__ u32x4 sm_chunk(const SmArgs& a, const uint16_t* xr, const uint8_t* mb,
+                                          const uint16_t* ma, int64_t j0, int64_t vis) {
+    u32x4 v = *(const u32x4*)(xr + j0);
+    if (a.kind == KMI_MASK_NONE && j0 + 8 <= a.N) return v;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int64_t j = j0 + e;
+        uint32_t h = (v[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        if (j >= a.N) {
+            h = BF16_NEG_INF;
+        } else if (a.kind == KMI_MASK_BOOL) {
+            if (!mb[j]) h = f32_to_bf16(BF16_LOWEST);
+        } else if (a.kind == KMI_MASK_ADD) {
+            h = f32_to_bf16(bf16_to_f32((uint16_t)h) + bf16_to_f32(ma[j]));
+        } else if (a.kind == KMI_MASK_CAUSAL) {
+            if (j > vis) h = f32_to_bf16(BF16_LOWEST);
+        }
+        v[e >> 1] = (e & 1) ? ((v[e >> 1] & 0x0000ffffu) | (h << 16)) : ((v[e >> 1] & 0xffff0000u) | h);
+    }
+    return v;
+}
+
+__device__ __forceinline__ float sm_max8(u32x4 v, float m) {
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        m = fmaxf(m, fmaxf(__uint_as_float(v[e] << 16), __uint_as_float(v[e] & 0xffff0000u)));
+    return m;
+}
+
+__device__ __forceinline__ float sm_sum8(u32x4 v, float mx, float s) {
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        s += expf(__uint_as_float(v[e] << 16) - mx) + expf(__uint_as_float(v[e] & 0xffff0000u) - mx);
+    return s;
+}
+
+__device__ __forceinline__ u32x4 sm_prob8(u32x4 v, float mx, float sum) {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        o[e] = qb_pack(expf(__uint_as_float(v[e] << 16) - mx) / sum,
+                       expf(__uint_as_float(v[e] & 0xffff0000u) - mx) / sum);
+    return o;
+}
+
+// One workgroup per row, 8 scores per 16-byte load.  CH > 0: the row stays
+// in registers (CH chunks of 8 per thread, N <= 2048 CH); CH == 0: any N,
+// three passes over the row.
+template <int CH>
 __global__ __launch_bounds__(256) void masked_softmax_kernel(SmArgs a) {
     __shared__ float red[4];
     const int64_t r = blockIdx.x;
@@ -345,16 +389,36 @@ __global__ __launch_bounds__(256) void masked_softmax_kernel(SmArgs a) {
     const uint8_t* mb = a.kind == KMI_MASK_BOOL ? (const uint8_t*)a.mask + moff : nullptr;
     const uint16_t* ma = a.kind == KMI_MASK_ADD ? (const uint16_t*)a.mask + moff : nullptr;
     const int64_t vis = a.N - a.dims[3] + i3;              // causal: last visible key
-    const int64_t N = a.N;
+    const int64_t nch = (a.N + 7) / 8;
+    const int t = threadIdx.x;
 
-    float mx = -INFINITY;
-    for (int64_t j = threadIdx.x; j < N; j += 256) mx = fmaxf(mx, sm_value(a, xr, mb, ma, j, vis));
-    mx = block_reduce(mx, true, red);
-    float sum = 0.f;
-    for (int64_t j = threadIdx.x; j < N; j += 256) sum += expf(sm_value(a, xr, mb, ma, j, vis) - mx);
-    sum = block_reduce(sum, false, red);
-    for (int64_t j = threadIdx.x; j < N; j += 256)
-        orow[j] = f32_to_bf16(expf(sm_value(a, xr, mb, ma, j, vis) - mx) / sum);
+    float mx = -INFINITY, sum = 0.f;
+    if constexpr (CH > 0) {
+        u32x4 v[CH];
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int64_t j = t + 256 * c;
+            v[c] = j < nch ? sm_chunk(a, xr, mb, ma, 8 * j, vis)
+                           : u32x4{0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u};
+            mx = sm_max8(v[c], mx);
+        }
+        mx = block_reduce(mx, true, red);
+#pragma unroll
+        for (int c = 0; c < CH; c++) sum = sm_sum8(v[c], mx, sum);
+        sum = block_reduce(sum, false, red);
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int64_t j = t + 256 * c;
+            if (j < nch) *(u32x4*)(orow + 8 * j) = sm_prob8(v[c], mx, sum);
+        }
+    } else {
+        for (int64_t j = t; j < nch; j += 256) mx = sm_max8(sm_chunk(a, xr, mb, ma, 8 * j, vis), mx);
+        mx = block_reduce(mx, true, red);
+        for (int64_t j = t; j < nch; j += 256) sum = sm_sum8(sm_chunk(a, xr, mb, ma, 8 * j, vis), mx, sum);
+        sum = block_reduce(sum, false, red);
+        for (int64_t j = t; j < nch; j += 256)
+            *(u32x4*)(orow + 8 * j) = sm_prob8(sm_chunk(a, xr, mb, ma, 8 * j, vis), mx, sum);
+    }
 }
 
 // ---- host side ------------------------------------------------------------------
@@ -371,10 +435,10 @@ static QbPlan plan_batched(int64_t P, int64_t M, int64_t K, int64_t N) {
     q.ntiles = ceil_div(N, QB_T);
     const int64_t kt_all = ceil_div(K, QB_T);
     const int64_t tiles = q.mtiles * q.ntiles * P;
-    // split K while the grid is short of two workgroups per CU and each
+    // split K while the grid is short of four workgroups per CU and each
     // split keeps at least 4 k-tiles
     int64_t S = 1;
-    while (tiles * S < 512 && kt_all / (S * 2) >= 4) S *= 2;
+    while (tiles * S < 1024 && kt_all / (S * 2) >= 4) S *= 2;
     const int64_t kts = ceil_div(kt_all, S);
     q.kts = (int)kts;
     q.S = (int)ceil_div(kt_all, kts);
@@ -425,7 +489,7 @@ size_t kmi_qmm_batched_workspace_bytes(int nd, const int64_t* batch_shape, int64
 int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, const int64_t* w_strides,
                     const void* scales, const void* biases, const int64_t* s_strides, int nd,
                     const int64_t* batch_shape, int64_t M, int64_t K, int64_t N, int transpose, int dtype,
-                    int group_size, int bits, float x_scale, void* y, void* workspace,
+                    int group_size, int bits, float x_scale, void* y, int64_t ldy, void* workspace,
                     size_t workspace_bytes, void* stream) {
     clear_error();
     KMI_CHECK_ARG(dtype == BF16, "quantized_matmul (batched): only bfloat16 is supported (got dtype %d)", dtype);
@@ -467,6 +531,7 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
         for (int d = 0; d < nd; d++) al = al && w_strides[d] % 4 == 0;
         KMI_CHECK_ARG(al, "quantized_matmul (batched): weight rows must be 16-byte aligned");
     }
+    KMI_CHECK_ARG(ldy >= N, "quantized_matmul (batched): output row stride %lld < N", (long long)ldy);
     const QbPlan q = plan_batched(P, M, K, N);
     KMI_CHECK_ARG(q.mtiles * q.S < 65536 && P < 65536 && q.ntiles < (1LL << 31),
                   "quantized_matmul (batched): grid too large (M=%lld, batch %lld)", (long long)M, (long long)P);
@@ -478,7 +543,7 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
     QbArgs a = {};
     a.x = (const uint16_t*)x; a.w = w; a.s = (const uint16_t*)scales; a.b = (const uint16_t*)biases;
     a.y = (uint16_t*)y; a.partial = (float*)workspace;
-    a.M = M; a.K = K; a.N = N; a.xr = xr; a.wr = wr; a.sr = sr;
+    a.M = M; a.K = K; a.N = N; a.xr = xr; a.wr = wr; a.sr = sr; a.ldy = ldy;
     a.nd = nd;
     for (int d = 0; d < nd; d++) {
         a.shape[d] = batch_shape[d];
@@ -497,7 +562,7 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
     if (q.S > 1) {
         const int64_t count = P * M * N;
         qmm_batched_reduce<<<(unsigned)ceil_div(count, 256), 256, 0, st>>>((const float*)workspace, q.S, count,
-                                                                          (uint16_t*)y);
+                                                                          N, ldy, (uint16_t*)y);
         KMI_CHECK_LAUNCH("quantized_matmul (batched) reduce");
     }
     return OK;
@@ -518,6 +583,11 @@ int kmi_masked_softmax(const void* x, int64_t ldx, int dtype, const int64_t* row
     }
     if (R == 0 || N == 0) return OK;
     KMI_CHECK_ARG(x && out, "masked_softmax: null pointer");
+    const int64_t Np = (N + 7) & ~7LL;
+    KMI_CHECK_ARG(ldx % 8 == 0 && ldo % 8 == 0 && ldx >= Np && ldo >= Np && ((uintptr_t)x & 15) == 0 &&
+                      ((uintptr_t)out & 15) == 0,
+                  "masked_softmax: rows must be 16-byte aligned and padded to a multiple of 8 (N=%lld, "
+                  "ldx=%lld, ldo=%lld)", (long long)N, (long long)ldx, (long long)ldo);
     KMI_CHECK_ARG(R < (1LL << 31), "masked_softmax: %lld rows", (long long)R);
     SmArgs a = {};
     a.x = (const uint16_t*)x; a.ldx = ldx; a.out = (uint16_t*)out; a.ldo = ldo; a.N = N;
@@ -530,7 +600,14 @@ int kmi_masked_softmax(const void* x, int64_t ldx, int dtype, const int64_t* row
             a.ms[d] = mask_strides[d];
         }
     }
-    masked_softmax_kernel<<<(unsigned)R, 256, 0, (hipStream_t)stream>>>(a);
+    const int64_t per_thread = ceil_div(ceil_div(N, 8), 256);
+    hipStream_t st = (hipStream_t)stream;
+    if (per_thread <= 1) masked_softmax_kernel<1><<<(unsigned)R, 256, 0, st>>>(a);
+    else if (per_thread <= 2) masked_softmax_kernel<2><<<(unsigned)R, 256, 0, st>>>(a);
+    else if (per_thread <= 4) masked_softmax_kernel<4><<<(unsigned)R, 256, 0, st>>>(a);
+    else if (per_thread <= 8) masked_softmax_kernel<8><<<(unsigned)R, 256, 0, st>>>(a);
+    else if (per_thread <= 16) masked_softmax_kernel<16><<<(unsigned)R, 256, 0, st>>>(a);
+    else masked_softmax_kernel<0><<<(unsigned)R, 256, 0, st>>>(a);
     KMI_CHECK_LAUNCH("masked_softmax");
     return OK;
 }

@@ -24,7 +24,7 @@ import math
 import torch
 
 from . import _abi
-from .ops import DTYPE_CODE, _on_gpu, _ptr, _stream, dequantize, qmm_batched
+from .ops import DTYPE_CODE, _on_gpu, _ptr, _stream, dequantize, padded_rows, qmm_batched, row_padded
 
 logger = logging.getLogger(__name__)
 
@@ -194,21 +194,22 @@ def masked_softmax(scores, mask=None, out=None):
     (base.py:285-295) on bf16 scores [..., L, N] (kmi_masked_softmax): a
     bool mask hides scores with finfo(bf16).min, a bf16 mask is added,
     "causal" hides key j from query row l when j > N - L + l; then
-    softmax(precise=True), probabilities rounded to bf16.  ``out`` may be a
-    row-padded view of the same shape."""
-    if scores.dtype != torch.bfloat16 or scores.stride(-1) != 1 or scores.dim() < 2 or scores.dim() > 5:
-        raise ValueError("masked_softmax: bf16 scores [..., L, N] with a contiguous last axis")
+    softmax(precise=True), probabilities rounded to bf16.  The kernel reads
+    and writes rows padded to 8 elements (``ops.padded_rows``); other
+    layouts are copied.  ``out`` may be ``scores`` itself."""
+    if scores.dtype != torch.bfloat16 or scores.dim() < 2 or scores.dim() > 5:
+        raise ValueError("masked_softmax: bf16 scores [..., L, N] of 2 to 5 dimensions")
     _on_gpu(scores)
+    if not row_padded(scores):
+        src = padded_rows(tuple(scores.shape), scores.dtype, scores.device)
+        src.copy_(scores)
+        scores = src
+    if out is None:
+        out = padded_rows(tuple(scores.shape), scores.dtype, scores.device)
+    elif not row_padded(out) or tuple(out.shape) != tuple(scores.shape) or out.dtype != scores.dtype:
+        raise ValueError("masked_softmax: out must be a row-padded bf16 tensor of the scores' shape")
     lead = tuple(scores.shape[:-1])
     N = scores.shape[-1]
-    if out is None:
-        out = torch.empty_like(scores)
-    rows = scores.reshape(-1, N) if scores.is_contiguous() else None
-    if rows is None or out.stride(-1) != 1:
-        raise ValueError("masked_softmax: scores must be contiguous, out's last axis contiguous")
-    ldo = out.stride(-2)
-    if any(out.stride(d) != out.shape[d + 1] * out.stride(d + 1) for d in range(out.dim() - 2)):
-        raise ValueError("masked_softmax: out must be a row-padded contiguous block")
     dims = [1] * (4 - len(lead)) + list(lead)
     kind, mt, mstr = MASK_NONE, None, [0, 0, 0, 0]
     if isinstance(mask, str):
@@ -236,8 +237,8 @@ def masked_softmax(scores, mask=None, out=None):
     dt = torch.tensor(dims, dtype=torch.int64)
     ms = torch.tensor(mstr, dtype=torch.int64)
     _abi.check(_abi.load().kmi_masked_softmax(
-        _ptr(scores), N, DTYPE_CODE[scores.dtype], dt.data_ptr(), N, _ptr(mt), kind, ms.data_ptr(),
-        _ptr(out), ldo, _stream(scores)), "masked_softmax")
+        _ptr(scores), scores.stride(-2), DTYPE_CODE[scores.dtype], dt.data_ptr(), N, _ptr(mt), kind,
+        ms.data_ptr(), _ptr(out), out.stride(-2), _stream(scores)), "masked_softmax")
     return out
 
 
@@ -261,11 +262,12 @@ def quantized_sdpa(queries, q_keys, q_values, scale: float, mask=None, group_siz
         q = q.reshape(B, Hk, rep, L, D)
         Kt = tuple(t.unsqueeze(-3) for t in Kt)
         Vt = tuple(t.unsqueeze(-3) for t in Vt)
-    scores = qmm_batched(q, *Kt, transpose=True, group_size=group_size, bits=bits, x_scale=float(scale))
-    N = scores.shape[-1]
-    Np = -(-N // 8) * 8
-    pbuf = torch.empty(*scores.shape[:-1], Np, dtype=scores.dtype, device=scores.device)
-    p = masked_softmax(scores, mask, out=pbuf[..., :N])
+    N = Kt[0].shape[-2]
+    # scores, then probabilities in place, in rows padded to 8 elements
+    buf = padded_rows(tuple(q.shape[:-1]) + (N,), q.dtype, q.device)
+    scores = qmm_batched(q, *Kt, transpose=True, group_size=group_size, bits=bits, x_scale=float(scale),
+                         out=buf)
+    p = masked_softmax(scores, mask, out=scores)
     out = qmm_batched(p, *Vt, transpose=False, group_size=group_size, bits=bits)
     return out.reshape(B, Hq, L, -1) if rep > 1 else out
 

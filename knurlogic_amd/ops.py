@@ -203,11 +203,37 @@ def _fold(shape, strides, M, xr):
     return merged, M
 
 
+def padded_rows(shape, dtype, device) -> torch.Tensor:
+    """An empty [..., N] tensor whose rows start 16 bytes apart at a
+    multiple of 8 elements (a view into [..., N rounded up to 8])."""
+    N = shape[-1]
+    Np = -(-N // 8) * 8
+    return torch.empty(*shape[:-1], Np, dtype=dtype, device=device)[..., :N]
+
+
+def row_padded(t: torch.Tensor) -> bool:
+    """Whether t [..., N] has 16-byte aligned rows of a multiple of 8
+    elements, readable up to N rounded to 8, and rows otherwise contiguous."""
+    if t.dim() < 2 or t.stride(-1) != 1 or t.data_ptr() % 16:
+        return False
+    N = t.shape[-1]
+    Np = -(-N // 8) * 8
+    ld = t.stride(-2)
+    if ld % 8 or ld < Np:
+        return False
+    if any(t.stride(d) != t.shape[d + 1] * t.stride(d + 1) for d in range(t.dim() - 2)):
+        return False
+    last = t.storage_offset() + sum((n - 1) * st for n, st in zip(t.shape, t.stride()))
+    return last + (Np - N) < t.untyped_storage().nbytes() // t.element_size()
+
+
 def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 64,
-                bits: int = 4, x_scale: float = 1.0):
+                bits: int = 4, x_scale: float = 1.0, out=None):
     """mx.quantized_matmul with batch dimensions on w (broadcast against
     x's) in either orientation; ``x_scale`` != 1 multiplies x by it first,
-    rounded to x's dtype (mlx-lm's ``queries *= scale``)."""
+    rounded to x's dtype (mlx-lm's ``queries *= scale``).  ``out``: a
+    [batch..., M, N] bf16 tensor with rows otherwise contiguous (a row
+    padding is allowed) to write into."""
     what = "quantized_matmul"
     if biases is None:
         raise ValueError(f"{what}: affine mode needs biases")
@@ -239,7 +265,14 @@ def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 
     except RuntimeError as e:
         raise ValueError(f"{what}: batch shapes {tuple(x.shape[:-2])} and {tuple(w.shape[:-2])} "
                          "do not broadcast") from e
-    y = torch.empty(*batch, M, N, dtype=x.dtype, device=x.device)
+    if out is not None:
+        _on_gpu(out)
+        if tuple(out.shape) != tuple(batch) + (M, N) or out.dtype != x.dtype or out.stride(-1) != 1 or any(
+                out.stride(d) != out.shape[d + 1] * out.stride(d + 1) for d in range(out.dim() - 2)):
+            raise ValueError(f"{what}: out must be a row-padded {tuple(batch) + (M, N)} {x.dtype} tensor")
+        y = out
+    else:
+        y = torch.empty(*batch, M, N, dtype=x.dtype, device=x.device)
     if y.numel() == 0:
         return y[0] if vec else y
     x = _aligned_rows(x)
@@ -270,7 +303,7 @@ def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 
     _abi.check(L.kmi_qmm_batched(
         _ptr(xe), xs.data_ptr(), _ptr(we), ws_.data_ptr(), _ptr(se), _ptr(be), ss.data_ptr(), nd,
         shape.data_ptr(), Mf, K, N, int(bool(transpose)), DTYPE_CODE[x.dtype], group_size, bits,
-        float(x_scale), _ptr(y), _ptr(ws), nbytes, _stream(x)), what)
+        float(x_scale), _ptr(y), y.stride(-2), _ptr(ws), nbytes, _stream(x)), what)
     return y[0] if vec else y
 
 
