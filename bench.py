@@ -324,6 +324,55 @@ def bench_vq(T, kc, cold, calls, dev):
             "bytes": nbytes, "flops": 2.0 * T * k * 3 * H * I}
 
 
+def bench_vq_packed(T, calls, dev, dim=4, kc=2048, group=64):
+    """VQ experts in the artifacts' packed layout at the Qwen3.5-MoE shape:
+    11-bit fields (2048-entry codebook) of dim-4 vectors, per-group fp16
+    scales (64 inputs); router, gate/up + SwiGLU (one launch), down, weighted
+    combine.  Expert sets rotated past 1 GB.  Bytes: every routed expert's
+    packed words and scales once, the codebook, x and out."""
+    import torch
+    import knurlogic_amd as KA
+    from knurlogic_amd import nn
+    E, k, H, I = MOE["E"], MOE["k"], MOE["H"], MOE["I"]
+    bits = (kc - 1).bit_length()
+
+    def mat_bytes(N, K):
+        return N * ((K // dim + 31) // 32 * bits * 4 + K // group * 2)
+
+    per_e = 2 * mat_bytes(I, H) + mat_bytes(H, I)
+    n = max(4, math.ceil(ROTATE_BYTES / (E * per_e)))
+    g = torch.Generator(device=dev).manual_seed(5000 + T)
+    cb = (torch.randn(kc, dim, device=dev, generator=g) * 0.3).to(torch.float16)
+
+    def mat(N, K):
+        W = (K // dim + 31) // 32 * bits
+        codes = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, N, W), device=dev, generator=g,
+                              dtype=torch.int32).view(torch.uint32)
+        sc = (torch.rand(E, N, K // group, device=dev, generator=g) + 0.5).to(torch.float16)
+        return nn.VQSwitchLinear(codes, cb, sc, scale_group=group, pack_bits=bits, in_features=K)
+
+    glus = [nn.VQSwitchGLU(mat(I, H), mat(I, H), mat(H, I)) for _ in range(n)]
+    x = torch.randn(T, H, device=dev, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, device=dev, generator=g).to(torch.bfloat16)
+    inds, _ = KA.moe_route(logits, k)
+    distinct = int(torch.unique(inds).numel())
+
+    def run():
+        for i in range(calls):
+            ii, sc = KA.moe_route(logits, k)
+            glus[i % n].combine(x, ii, sc)
+
+    us = time_graph(run) / calls * 1e3
+    nbytes = distinct * per_e + kc * dim * 2 + 2 * 2 * T * H
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del glus
+    torch.cuda.empty_cache()
+    return {"op": "vq_packed_moe_experts", "T": T, "codebook": f"{kc}x{dim} fp16", "field_bits": bits,
+            "experts_routed": distinct, "cache": "cold", "us": round(us, 3), "GBps": round(gbs, 1),
+            "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm", "bytes": nbytes,
+            "flops": 2.0 * T * k * 3 * H * I}
+
+
 HEADLINE_PROFILE = ROOT / "profiles" / "qmv_4bit_14336x4096_m1.md"
 
 
@@ -424,6 +473,9 @@ def main():
             for t_ in (1, 16):
                 for cold in (True, False):
                     detail.append(bench_vq(t_, kc_, cold, 50, dev))
+    if not args.quick and "vq" in only:
+        for t_ in (1, 16):
+            detail.append(bench_vq_packed(t_, 50, dev))
     if not args.quick and "moe" in only:
         for t_ in (1, 16, 256):
             for cold in (True, False):

@@ -305,6 +305,41 @@ int kmi_vq_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int3
  * workspace: kmi_vq_switch_glu_workspace_bytes(T, H, I, k) bytes.
  */
 size_t kmi_vq_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k);
+/*
+ * VQSwitchLinear over the bit-packed on-disk code layout of the VQ
+ * artifacts (src/knurlogic/engine/families/deepseek/heads/deepseek_v4.py:
+ * 36-44,95-129; shipped as K = 2048 entries of dim 2-4 in 11-bit fields,
+ * tests/engine/test_deepseek_v4_mtp.py:206-233):
+ *   What_e[o, i] = scales[e, o, i / group] * codebook[field(e, o, i / dim)][i % dim]
+ *   y[r, :] = x[rows[r]] @ What_{experts[r]}^T      (r < R; rows NULL: x row r / rows_div)
+ *   codes [E, N, W] uint32, W = ceil(K / dim / 32) * pack_bits: field j of a
+ *   row at bits [j*pack_bits, (j+1)*pack_bits) of the row's words read as
+ *   one little-endian bit stream; pack_bits in 8..12 or 16; codebook
+ *   [kc, dim] fp16 (dim 2, 4 or 8); scales [E, N, K / group] fp16 with
+ *   group >= 32 and group / dim a power of two; x [X, K] bf16, y [R, N] bf16.
+ * fp32 accumulation; x enters the dot products as fp16.  The field order
+ * within the words is not fixed by the reference tree (its runtime is not
+ * vendored): LSB first, as mlx packs sub-byte fields.
+ */
+int kmi_vq_packed_gather_qmm(const void* x, int64_t X, int64_t K, const uint32_t* codes, int pack_bits,
+                             const void* codebook, int kc, int dim, const void* scales, int group, int64_t E,
+                             int64_t N, const int32_t* rows, int64_t rows_div, const int32_t* experts, int64_t R,
+                             int dtype, void* y, void* stream);
+
+/*
+ * The gate and up projections of a packed VQ SwitchGLU with Qwen3.5's
+ * _SwiGLU (qwen3_5.py:108-112) in one launch: act[r, :] =
+ * round(round(silu(round(x[rows[r]] @ Gate_e^T))) * round(x[rows[r]] @ Up_e^T)),
+ * e = experts[r] (rows NULL: x row r / rows_div, e.g. k slots per token);
+ * codes / scales / codebooks as kmi_vq_packed_gather_qmm,
+ * gate and up [E, I, *] over H inputs; act [R, I] bf16.
+ */
+int kmi_vq_packed_glu(const void* x, int64_t X, int64_t H, int64_t I, const uint32_t* codes_gate,
+                      const void* scales_gate, const void* codebook_gate, const uint32_t* codes_up,
+                      const void* scales_up, const void* codebook_up, int pack_bits, int kc, int dim, int group,
+                      int64_t E, const int32_t* rows, int64_t rows_div, const int32_t* experts, int64_t R,
+                      int dtype, void* act, void* stream);
+
 int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
                       const void* scores, const void* codes_gate, const void* scales_gate,
                       const void* codebook_gate, const void* codes_up, const void* scales_up,

@@ -32,6 +32,8 @@ SIGNATURES = {
                             SZ, P]),
     "kmi_qmm_batched_workspace_bytes": (SZ, [I, P, I64, I64, I64]),
     "kmi_masked_softmax": (I, [P, I64, I, P, I64, P, I, P, P, I64, P]),
+    "kmi_vq_packed_gather_qmm": (I, [P, I64, I64, P, I, P, I, I, P, I, I64, I64, P, I64, P, I64, I, P, P]),
+    "kmi_vq_packed_glu": (I, [P, I64, I64, I64, P, P, P, P, P, P, I, I, I, I, I64, P, I64, P, I64, I, P, P]),
     "kmi_moe_route": (I, [P, I, I64, I, I, P, P, P]),
     "kmi_swiglu": (I, [P, P, I64, I, I64, I64, P, P]),
     "kmi_moe_combine": (I, [P, P, I, I64, I, I64, P, P]),

@@ -1,0 +1,317 @@
+// VQ expert matmul over the bit-packed on-disk code layout, for gfx950.
+// The VQ artifacts' routed experts store, per output row, the codebook
+// indices of the row's dim-element vectors as ceil(log2 K)-bit fields
+// packed into uint32 words, ceil(in/dim/32) * bits words per row
+// (src/knurlogic/engine/families/deepseek/heads/deepseek_v4.py:36-44,
+// 95-129; the shipped geometry is K = 2048 entries of dim 2-4 at 11 bits,
+// tests/engine/test_deepseek_v4_mtp.py:206-233), with fp16 scales per group
+// of `group` inputs:
+//   What[o, i] = scales[o, i / group] * codebook[code(o, i / dim)][i % dim]
+//   y[r, o]    = x[rows[r]] . What_{experts[r]}[o]
+// Field j of a row occupies bits [j*PB, j*PB + PB) of the row's words read
+// as one little-endian bit stream (LSB first), so each run of 32 fields is
+// exactly PB whole words.
+//
+// One lane decodes one 32-field block at a time: it loads the block's PB
+// words, extracts the fields with funnel shifts at compile-time offsets,
+// gathers each field's codebook vector from LDS (fp16, the whole codebook
+// staged per workgroup) and dots it with the matching x values (staged in
+// LDS as fp16, read by every row at the same address) by v_dot2_f32_f16.
+// SEG lanes share a row and take its blocks round-robin; their partial
+// sums meet by cross-lane shuffles.  Scale groups are summed in fp32 and
+// scaled once per group.  With two row sets (gate and up) the epilogue is
+// Qwen3.5's _SwiGLU with its roundings.
+#include "common.hpp"
+#include "../../include/knurlogic_amd.h"
+
+namespace kmi {
+
+typedef _Float16 vp_f16x2 __attribute__((ext_vector_type(2)));
+
+struct VpArgs {
+    const uint16_t* x;          // bf16 [X, K]
+    int64_t X;
+    const int32_t* rows;        // [R] x row of each output row set, or null: x row r / rows_div
+    int64_t rows_div;
+    const int32_t* experts;     // [R] expert of each
+    int64_t R;
+    const uint32_t* codes[2];   // [E, N, W] packed fields (set 1: the up rows, GLU only)
+    const uint16_t* sc[2];      // [E, N, K / group] fp16
+    const uint16_t* cb[2];      // [kc, dim] fp16
+    int nset;
+    int kc;
+    int64_t E, N, K, W;         // W: words per row
+    int group;
+    uint16_t* y;                // [R, N] bf16
+};
+
+__device__ __forceinline__ float vp_dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(vp_f16x2, a), __builtin_bit_cast(vp_f16x2, b), acc, false);
+}
+
+template <int DIM>
+__device__ __forceinline__ float vp_dot(const uint16_t* cbe, const uint16_t* xe, float acc) {
+    if constexpr (DIM == 2) {
+        return vp_dot2(*(const uint32_t*)cbe, *(const uint32_t*)xe, acc);
+    } else if constexpr (DIM == 4) {
+        const u32x2 c = *(const u32x2*)cbe, v = *(const u32x2*)xe;
+        return vp_dot2(c.y, v.y, vp_dot2(c.x, v.x, acc));
+    } else {
+        const u32x4 c = *(const u32x4*)cbe, v = *(const u32x4*)xe;
+        acc = vp_dot2(c.x, v.x, acc);
+        acc = vp_dot2(c.y, v.y, acc);
+        acc = vp_dot2(c.z, v.z, acc);
+        return vp_dot2(c.w, v.w, acc);
+    }
+}
+
+// field j (0..31) of a block of PB words
+template <int PB>
+__device__ __forceinline__ uint32_t vp_field(const uint32_t* w, int j) {
+    const int off = j * PB, q = off >> 5, sh = off & 31;
+    uint32_t v;
+    if (sh + PB <= 32) v = w[q] >> sh;
+    else v = __builtin_amdgcn_alignbit(w[q + 1], w[q], (uint32_t)sh);
+    return v & ((1u << PB) - 1u);
+}
+
+__device__ __forceinline__ float vp_bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+__device__ __forceinline__ float vp_f32_kept(double v) {
+    float f = (float)v;
+    asm volatile("" : "+v"(f));
+    return f;
+}
+
+// PB bits per field, DIM elements per code vector, GPB scale groups per
+// 32-field block (1: a block lies inside one group), SEG lanes per row.
+template <int PB, int DIM, int GPB, int SEG>
+__global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
+    constexpr int RPWG = 256 / SEG;
+    constexpr int FPG = 32 / GPB;                    // fields per group within a block (GPB > 1)
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int64_t r = blockIdx.y;
+    const int e = a.experts[r];
+    const bool ok_e = e >= 0 && e < a.E;
+    const int64_t xrow = a.rows ? (int64_t)a.rows[r] : r / a.rows_div;
+    const bool ok_x = xrow >= 0 && xrow < a.X;
+    const bool two_cb = a.nset == 2 && a.cb[1] != a.cb[0];
+    const int64_t nsub = a.K / DIM;                  // fields per row
+    const int64_t Kp = (nsub + 31) / 32 * 32 * DIM;  // x staged to whole blocks (zeros past K)
+    uint16_t* cbl0 = (uint16_t*)smem;
+    uint16_t* cbl1 = two_cb ? cbl0 + (size_t)a.kc * DIM : cbl0;
+    uint16_t* xl = cbl0 + (size_t)a.kc * DIM * (two_cb ? 2 : 1);
+
+    // codebook(s) and the x row (fp16) -> LDS
+    for (int s = 0; s < (two_cb ? 2 : 1); s++) {
+        uint16_t* dst = s ? cbl1 : cbl0;
+        const __amdgpu_buffer_rsrc_t rcb = make_rsrc(a.cb[s], (int64_t)a.kc * DIM * 2);
+        for (int i = tid; i < a.kc * DIM / 2; i += 256)
+            *(uint32_t*)(dst + 2 * i) = __builtin_amdgcn_raw_buffer_load_b32(rcb, i * 4, 0, 0);
+    }
+    {
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (ok_x ? xrow : 0) * a.K, ok_x ? a.K * 2 : 0);
+        for (int i = tid; i < (int)(Kp / 2); i += 256) {
+            const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(rx, i * 4, 0, 0);
+            const vp_f16x2 h = {(_Float16)bf16_to_f32((uint16_t)(v & 0xffffu)),
+                                (_Float16)bf16_to_f32((uint16_t)(v >> 16))};
+            *(uint32_t*)(xl + 2 * i) = __builtin_bit_cast(uint32_t, h);
+        }
+    }
+    __syncthreads();
+
+    const int64_t row = (int64_t)blockIdx.x * RPWG + tid / SEG;
+    const int seg = tid % SEG;
+    const int64_t nblk = (nsub + 31) / 32;
+    const int64_t gpr = a.K / a.group;                // scale groups per row
+    const int64_t fpg = a.group / DIM;                // fields per group
+    const int64_t erow = (int64_t)(ok_e ? e : 0) * a.N + (row < a.N ? row : 0);
+    float res[2] = {0.f, 0.f};
+    for (int s = 0; s < a.nset; s++) {
+        const uint16_t* cbl = s ? cbl1 : cbl0;
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.codes[s] + erow * a.W, (ok_e && row < a.N) ? a.W * 4 : 0);
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sc[s] + erow * gpr, (ok_e && row < a.N) ? gpr * 2 : 0);
+        float tot = 0.f;
+        for (int64_t b = seg; b < nblk; b += SEG) {
+            uint32_t w[PB + 1];
+#pragma unroll
+            for (int q = 0; q < PB; q++)
+                w[q] = __builtin_amdgcn_raw_buffer_load_b32(rc, (int)((b * PB + q) * 4), 0, AUX_NT);
+            w[PB] = 0;
+            float sv[GPB];
+#pragma unroll
+            for (int g = 0; g < GPB; g++) {
+                const int64_t gi = (b * 32 + g * FPG) / fpg;
+                sv[g] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rs, (int)(gi * 2), 0, 0));
+            }
+            const int64_t f0 = b * 32;
+            const int nvalid = (int)(nsub - f0 < 32 ? nsub - f0 : 32);
+            float acc[GPB];
+#pragma unroll
+            for (int g = 0; g < GPB; g++) acc[g] = 0.f;
+#pragma unroll
+            for (int j = 0; j < 32; j++) {
+                uint32_t c = vp_field<PB>(w, j);
+                c = c < (uint32_t)a.kc ? c : (uint32_t)(a.kc - 1);
+                const float d = vp_dot<DIM>(cbl + c * DIM, xl + (f0 + j) * DIM, 0.f);
+                acc[j / FPG] += j < nvalid ? d : 0.f;
+            }
+#pragma unroll
+            for (int g = 0; g < GPB; g++) tot = __builtin_fmaf(sv[g], acc[g], tot);
+        }
+#pragma unroll
+        for (int o = SEG / 2; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
+        res[s] = vp_bf16r(tot);
+    }
+    if (seg == 0 && row < a.N) {
+        float out = res[0];
+        if (a.nset == 2) {           // round(round(silu_f32(gate)) * up)
+            const double g = (double)res[0];
+            out = vp_bf16r(vp_f32_kept(g / (1.0 + exp(-g)))) * res[1];
+        }
+        a.y[r * a.N + row] = (ok_e && ok_x) ? f32_to_bf16(out) : (uint16_t)0;
+    }
+}
+
+// Lanes per row: the blocks of a row rounded down to a power of two, at
+// most 16 (fewer lanes per row, each with more blocks, measured slower: a
+// lane's blocks are a serial chain of loads and codebook gathers).
+static int vp_seg(int64_t nblk) {
+    int s = 1;
+    while (s < 16 && s * 2 <= nblk) s *= 2;
+    return s;
+}
+
+template <int PB, int DIM, int GPB>
+static int launch_vp3(const VpArgs& a, int seg, size_t lds, hipStream_t st) {
+#define KMI_VP_SEG(S_)                                                                                  \
+    if (seg == S_) {                                                                                    \
+        static bool attr = false;                                                                       \
+        if (!attr) {                                                                                    \
+            (void)hipFuncSetAttribute((const void*)vq_packed_gemv<PB, DIM, GPB, S_>,                    \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);          \
+            attr = true;                                                                                \
+        }                                                                                               \
+        const dim3 grid((unsigned)ceil_div(a.N, 256 / S_), (unsigned)a.R);                              \
+        vq_packed_gemv<PB, DIM, GPB, S_><<<grid, 256, lds, st>>>(a);                                    \
+        return OK;                                                                                      \
+    }
+    KMI_VP_SEG(1) KMI_VP_SEG(2) KMI_VP_SEG(4) KMI_VP_SEG(8) KMI_VP_SEG(16)
+#undef KMI_VP_SEG
+    return EINVAL_ARG;
+}
+
+template <int PB>
+static int launch_vp_pb(const VpArgs& a, int dim, int gpb, int seg, size_t lds, hipStream_t st) {
+    if (dim == 2 && gpb == 1) return launch_vp3<PB, 2, 1>(a, seg, lds, st);
+    if (dim == 2 && gpb == 2) return launch_vp3<PB, 2, 2>(a, seg, lds, st);
+    if (dim == 4 && gpb == 1) return launch_vp3<PB, 4, 1>(a, seg, lds, st);
+    if (dim == 4 && gpb == 2) return launch_vp3<PB, 4, 2>(a, seg, lds, st);
+    if (dim == 4 && gpb == 4) return launch_vp3<PB, 4, 4>(a, seg, lds, st);
+    if (dim == 8 && gpb == 2) return launch_vp3<PB, 8, 2>(a, seg, lds, st);
+    if (dim == 8 && gpb == 4) return launch_vp3<PB, 8, 4>(a, seg, lds, st);
+    if (dim == 8 && gpb == 8) return launch_vp3<PB, 8, 8>(a, seg, lds, st);
+    if (dim == 8 && gpb == 1) return launch_vp3<PB, 8, 1>(a, seg, lds, st);
+    return EINVAL_ARG;
+}
+
+static int vp_check(int dtype, int pack_bits, int kc, int dim, int group, int64_t K, int64_t N, int64_t E) {
+    KMI_CHECK_ARG(dtype == BF16, "vq (packed): only bfloat16 activations are implemented");
+    KMI_CHECK_ARG(pack_bits == 8 || pack_bits == 9 || pack_bits == 10 || pack_bits == 11 || pack_bits == 12 ||
+                      pack_bits == 16,
+                  "vq (packed): %d-bit fields (8-12 and 16 are implemented)", pack_bits);
+    KMI_CHECK_ARG(dim == 2 || dim == 4 || dim == 8, "vq (packed): vector length %d (2, 4, 8)", dim);
+    KMI_CHECK_ARG(kc >= 1 && kc <= (1 << pack_bits), "vq (packed): %d codebook entries for %d-bit fields", kc,
+                  pack_bits);
+    KMI_CHECK_ARG(K > 0 && N > 0 && E > 0 && K % dim == 0, "vq (packed): K=%lld is not a multiple of dim %d",
+                  (long long)K, dim);
+    KMI_CHECK_ARG(group > 0 && K % group == 0 && group % dim == 0,
+                  "vq (packed): scale group %d must divide K=%lld and be a multiple of dim %d", group,
+                  (long long)K, dim);
+    const int fpg = group / dim;
+    KMI_CHECK_ARG((fpg & (fpg - 1)) == 0 && group >= 32,
+                  "vq (packed): scale group %d (at least 32 inputs, a power of two fields) is not implemented",
+                  group);
+    const int64_t W = (K / dim + 31) / 32 * pack_bits;
+    KMI_CHECK_ARG(E * N * W * 4 < (1LL << 31) && (size_t)kc * dim * 2 * 2 + (size_t)(K + 256) * 2 <= 160 * 1024,
+                  "vq (packed): codes past 2 GiB or codebook + x past the LDS");
+    return OK;
+}
+
+static int run_vp(VpArgs& a, int pack_bits, int dim, hipStream_t st) {
+    const int64_t nsub = a.K / dim, nblk = (nsub + 31) / 32;
+    const int fpg = a.group / dim;
+    const int gpb = fpg >= 32 ? 1 : 32 / fpg;
+    const int seg = vp_seg(nblk);
+    const bool two_cb = a.nset == 2 && a.cb[1] != a.cb[0];
+    const size_t lds = (size_t)a.kc * dim * 2 * (two_cb ? 2 : 1) + (size_t)nblk * 32 * dim * 2;
+    int rc;
+    switch (pack_bits) {
+        case 8: rc = launch_vp_pb<8>(a, dim, gpb, seg, lds, st); break;
+        case 9: rc = launch_vp_pb<9>(a, dim, gpb, seg, lds, st); break;
+        case 10: rc = launch_vp_pb<10>(a, dim, gpb, seg, lds, st); break;
+        case 11: rc = launch_vp_pb<11>(a, dim, gpb, seg, lds, st); break;
+        case 12: rc = launch_vp_pb<12>(a, dim, gpb, seg, lds, st); break;
+        default: rc = launch_vp_pb<16>(a, dim, gpb, seg, lds, st); break;
+    }
+    if (rc) {
+        set_error("vq (packed): no kernel for %d-bit fields, dim %d, %d groups per block", pack_bits, dim, gpb);
+        return rc;
+    }
+    KMI_CHECK_LAUNCH("vq_packed_gemv");
+    return OK;
+}
+
+}  // namespace kmi
+
+using namespace kmi;
+
+extern "C" {
+
+int kmi_vq_packed_gather_qmm(const void* x, int64_t X, int64_t K, const uint32_t* codes, int pack_bits,
+                             const void* codebook, int kc, int dim, const void* scales, int group, int64_t E,
+                             int64_t N, const int32_t* rows, int64_t rows_div, const int32_t* experts, int64_t R,
+                             int dtype, void* y, void* stream) {
+    clear_error();
+    int rc = vp_check(dtype, pack_bits, kc, dim, group, K, N, E);
+    if (rc) return rc;
+    KMI_CHECK_ARG(R >= 0 && X >= 1 && R < 65536, "vq_packed_gather_qmm: %lld output rows (at most 65535)",
+                  (long long)R);
+    if (R == 0) return OK;
+    KMI_CHECK_ARG(x && codes && codebook && scales && experts && y && (rows || rows_div >= 1),
+                  "vq_packed_gather_qmm: null pointer");
+    VpArgs a = {};
+    a.x = (const uint16_t*)x; a.X = X; a.rows = rows; a.rows_div = rows_div; a.experts = experts; a.R = R;
+    a.codes[0] = a.codes[1] = codes;
+    a.sc[0] = a.sc[1] = (const uint16_t*)scales;
+    a.cb[0] = a.cb[1] = (const uint16_t*)codebook;
+    a.nset = 1; a.kc = kc; a.E = E; a.N = N; a.K = K; a.W = (K / dim + 31) / 32 * pack_bits; a.group = group;
+    a.y = (uint16_t*)y;
+    return run_vp(a, pack_bits, dim, (hipStream_t)stream);
+}
+
+int kmi_vq_packed_glu(const void* x, int64_t X, int64_t H, int64_t I, const uint32_t* codes_gate,
+                      const void* scales_gate, const void* codebook_gate, const uint32_t* codes_up,
+                      const void* scales_up, const void* codebook_up, int pack_bits, int kc, int dim, int group,
+                      int64_t E, const int32_t* rows, int64_t rows_div, const int32_t* experts, int64_t R,
+                      int dtype, void* act, void* stream) {
+    clear_error();
+    int rc = vp_check(dtype, pack_bits, kc, dim, group, H, I, E);
+    if (rc) return rc;
+    KMI_CHECK_ARG(R >= 0 && X >= 1 && R < 65536, "vq_packed_glu: %lld output rows (at most 65535)", (long long)R);
+    if (R == 0) return OK;
+    KMI_CHECK_ARG(x && codes_gate && scales_gate && codebook_gate && codes_up && scales_up && codebook_up &&
+                      experts && act && (rows || rows_div >= 1),
+                  "vq_packed_glu: null pointer");
+    VpArgs a = {};
+    a.x = (const uint16_t*)x; a.X = X; a.rows = rows; a.rows_div = rows_div; a.experts = experts; a.R = R;
+    a.codes[0] = codes_gate; a.codes[1] = codes_up;
+    a.sc[0] = (const uint16_t*)scales_gate; a.sc[1] = (const uint16_t*)scales_up;
+    a.cb[0] = (const uint16_t*)codebook_gate; a.cb[1] = (const uint16_t*)codebook_up;
+    a.nset = 2; a.kc = kc; a.E = E; a.N = I; a.K = H; a.W = (H / dim + 31) / 32 * pack_bits; a.group = group;
+    a.y = (uint16_t*)act;
+    return run_vp(a, pack_bits, dim, (hipStream_t)stream);
+}
+
+}  // extern "C"

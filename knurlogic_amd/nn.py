@@ -7,8 +7,9 @@
   glm5_next/_mlx_vlm/models/switch_layers.py:24-86,156-193).
 - ``VQSwitchLinear`` / ``VQSwitchGLU``: the codebook-decode experts VQ
   artifacts ship in their model.py (class named at tests/engine/
-  test_deepseek_v4_mtp.py:249,360), 8-element vectors, byte or 16-bit
-  indices, fp16 codebook and scales.
+  test_deepseek_v4_mtp.py:249,360): 8-element vectors with byte or 16-bit
+  indices, or the on-disk packed layout (2-8-element vectors, 8-12 or
+  16-bit fields), fp16 codebook and scales.
 - ``MLP`` / ``SparseMoeBlock``: Qwen3.5-MoE's expert block with the
   reference's rounding edits (src/knurlogic/engine/families/qwen/
   architecture/qwen3_5.py:35-40,108-118,151-192).
@@ -24,7 +25,8 @@ import math
 import torch
 
 from .ops import (gather_qmm, moe_combine, moe_route, moe_shared_add, quantize,
-                  quantized_matmul, swiglu, switch_glu, vq_gather_qmm, vq_glu, vq_switch_glu)
+                  quantized_matmul, swiglu, switch_glu, vq_gather_qmm, vq_glu, vq_packed_gather_qmm,
+                  vq_packed_glu, vq_switch_glu)
 
 
 class Linear:
@@ -197,13 +199,28 @@ class SwitchGLU:
 class VQSwitchLinear:
     """VQ experts: weight[e, o, i] = scales[e, o, i / scale_group] *
     codebook[codes[e, o, i / dim]][i % dim] (scale_group 0: scales [E, N],
-    one per output channel); the call is gather_qmm's."""
+    one per output channel); the call is gather_qmm's.  ``pack_bits`` > 0:
+    codes are the artifacts' packed layout, uint32 [E, N, ceil(in/dim/32) *
+    pack_bits] of pack_bits-bit fields, with per-group scales
+    (``scale_group`` inputs each), as the bundled runtime's class takes them
+    (.../heads/deepseek_v4.py:126-129)."""
 
-    def __init__(self, codes, codebook, scales, scale_group: int = 0):
+    def __init__(self, codes, codebook, scales, scale_group: int = 0, pack_bits: int = 0,
+                 in_features: int | None = None):
         self.codes, self.codebook, self.scales, self.scale_group = codes, codebook, scales, scale_group
+        self.pack_bits = int(pack_bits)
+        if self.pack_bits and not scale_group:
+            raise ValueError("VQSwitchLinear: packed codes carry per-group scales (scale_group > 0)")
+        self.in_features = in_features
+
+    @property
+    def group_size(self):
+        return self.scale_group
 
     @property
     def input_dims(self):
+        if self.pack_bits:
+            return self.in_features or self.scales.shape[2] * self.scale_group
         return self.codes.shape[2] * self.codebook.shape[1]
 
     @property
@@ -215,6 +232,9 @@ class VQSwitchLinear:
         return self.codes.shape[0]
 
     def __call__(self, x, indices, sorted_indices: bool = False):
+        if self.pack_bits:
+            return vq_packed_gather_qmm(x, self.codes, self.codebook, self.scales, self.pack_bits,
+                                        self.scale_group, rhs_indices=indices)
         return vq_gather_qmm(x, self.codes, self.codebook, self.scales, rhs_indices=indices,
                              scale_group=self.scale_group)
 
@@ -230,14 +250,35 @@ class VQSwitchGLU:
     def _mats(self):
         return tuple((m.codes, m.codebook, m.scales) for m in (self.gate_proj, self.up_proj, self.down_proj))
 
+    def _packed(self):
+        return self.gate_proj.pack_bits or self.up_proj.pack_bits or self.down_proj.pack_bits
+
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
-        """x [..., H], indices [..., k] -> [..., k, H]: one library call."""
+        """x [..., H], indices [..., k] -> [..., k, H]: one library call
+        (two for the packed layout: gate/up + SwiGLU, then down)."""
+        if self._packed():
+            return self._packed_call(x, indices)
         return vq_switch_glu(x, indices, *self._mats(), self.gate_proj.scale_group)
 
     def combine(self, x, indices, scores):
         """(self(x, indices) * scores[..., None]).sum(-2) with the reference's
         roundings, in the same library call."""
+        if self._packed():
+            return moe_combine(self._packed_call(x, indices), scores)
         return vq_switch_glu(x, indices, *self._mats(), self.gate_proj.scale_group, scores=scores)
+
+    def _packed_call(self, x, indices):
+        g, u, d = self.gate_proj, self.up_proj, self.down_proj
+        if not (g.pack_bits == u.pack_bits == d.pack_bits) or g.scale_group != u.scale_group:
+            raise ValueError("VQSwitchGLU: gate, up and down must share the packed layout")
+        act = vq_packed_glu(x, indices, (g.codes, g.codebook, g.scales), (u.codes, u.codebook, u.scales),
+                            g.pack_bits, g.scale_group)                          # [..., k, I]
+        lead, k = tuple(indices.shape[:-1]), indices.shape[-1]
+        P = math.prod(lead) * k
+        y = vq_packed_gather_qmm(act.reshape(P, 1, act.shape[-1]), d.codes, d.codebook, d.scales,
+                                 d.pack_bits, d.scale_group, rhs_indices=indices.reshape(P),
+                                 rows_are_pairs=True)
+        return y.reshape(*lead, k, y.shape[-1])
 
     def separate(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """The same through the separate ops: vq_glu, then vq_gather_qmm over

@@ -521,6 +521,98 @@ def vq_gather_qmm(x: torch.Tensor, codes: torch.Tensor, codebook: torch.Tensor, 
     return y
 
 
+def _vq_packed_operands(codes, codebook, scales, pack_bits, group, K, what):
+    if codes.dtype not in (torch.uint32, torch.int32) or codes.ndim != 3:
+        raise ValueError(f"{what}: packed codes must be uint32 [E, N, W]")
+    if codebook.dtype != torch.float16 or scales.dtype != torch.float16 or codebook.ndim != 2:
+        raise ValueError(f"{what}: codebook [k, dim] and scales must be float16")
+    kc, dim = codebook.shape
+    if K % dim or K % group:
+        raise ValueError(f"{what}: K={K} is not a multiple of dim {dim} and group {group}")
+    W = (K // dim + 31) // 32 * pack_bits
+    if codes.shape[2] != W:
+        raise ValueError(f"{what}: codes rows are {codes.shape[2]} wide; K={K} at dim {dim} is {W} "
+                         f"packed {pack_bits}-bit words")
+    if tuple(scales.shape) != (codes.shape[0], codes.shape[1], K // group):
+        raise ValueError(f"{what}: scales {tuple(scales.shape)} do not match codes {tuple(codes.shape)} "
+                         f"at group {group}")
+    return kc, dim
+
+
+def vq_packed_gather_qmm(x: torch.Tensor, codes: torch.Tensor, codebook: torch.Tensor, scales: torch.Tensor,
+                         pack_bits: int, group: int, lhs_indices=None, rhs_indices=None,
+                         rows_are_pairs: bool = False):
+    """VQSwitchLinear's product over the bit-packed code layout of the VQ
+    artifacts (kmi_vq_packed_gather_qmm): What[e, o, i] =
+    scales[e, o, i / group] * codebook[field(e, o, i / dim)][i % dim],
+    fields of ``pack_bits`` bits; out[i] = x[lhs[i]] @ What[rhs[i]]^T.
+    ``rows_are_pairs``: the caller guarantees lhs[i] == i (x holds one row
+    per pair), so no row list is built."""
+    _on_gpu(x, codes, codebook, scales)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("vq_packed_gather_qmm: only bfloat16 activations are implemented")
+    M, K = x.shape[-2], x.shape[-1]
+    kc, dim = _vq_packed_operands(codes, codebook, scales, pack_bits, group, K, "vq_packed_gather_qmm")
+    E, N = codes.shape[0], codes.shape[1]
+    xc = x.reshape(-1, K).contiguous()
+    if rows_are_pairs:
+        # one x row per pair (x row p): the expert list is all the kernel needs
+        rhs = torch.as_tensor(rhs_indices, device=x.device).reshape(-1)
+        rhs = (rhs if rhs.dtype == torch.int32 else rhs.to(torch.int32)).contiguous()
+        P, ishape = rhs.numel(), (rhs.numel(),)
+        if M != 1 or xc.shape[0] != P:
+            raise ValueError("vq_packed_gather_qmm: rows_are_pairs takes x [P, 1, K] with P = len(rhs)")
+    else:
+        lhs, rhs, ishape = _vq_indices(x, E, lhs_indices, rhs_indices)
+        P = lhs.numel()
+    y = torch.empty(*ishape, M, N, dtype=x.dtype, device=x.device)
+    if P == 0:
+        return y
+    cc, cbc, sc = codes.contiguous(), codebook.contiguous(), scales.contiguous()
+    if rows_are_pairs:
+        rows, div, experts = None, 1, rhs
+    else:
+        m = torch.arange(M, device=x.device, dtype=torch.int32)
+        rows = (lhs.view(-1, 1) * M + m).reshape(-1).contiguous()
+        div = 1
+        experts = rhs.view(-1, 1).expand(P, M).reshape(-1).contiguous()
+    _abi.check(_lib().kmi_vq_packed_gather_qmm(
+        _ptr(xc), xc.shape[0], K, _ptr(cc), pack_bits, _ptr(cbc), kc, dim, _ptr(sc), group, E, N,
+        _ptr(rows), div, _ptr(experts), P * M, DTYPE_CODE[x.dtype], _ptr(y), _stream(x)), "vq_packed_gather_qmm")
+    return y
+
+
+def vq_packed_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, pack_bits: int, group: int):
+    """SwitchGLU's gate and up products over packed VQ experts with
+    _SwiGLU, one launch (kmi_vq_packed_glu): x [..., H], indices [..., k]
+    -> act [..., k, I]; gate / up = (codes, codebook, scales)."""
+    _on_gpu(x, indices, *gate, *up)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("vq_packed_glu: only bfloat16 activations are implemented")
+    H = x.shape[-1]
+    kc, dim = _vq_packed_operands(gate[0], gate[1], gate[2], pack_bits, group, H, "vq_packed_glu")
+    _vq_packed_operands(up[0], up[1], up[2], pack_bits, group, H, "vq_packed_glu")
+    if up[0].shape != gate[0].shape or up[1].shape != gate[1].shape:
+        raise ValueError("vq_packed_glu: gate and up differ in shape")
+    E, I = gate[0].shape[0], gate[0].shape[1]
+    lead, k = tuple(indices.shape[:-1]), indices.shape[-1]
+    T = math.prod(lead)
+    if tuple(x.shape[:-1]) != lead:
+        raise ValueError("vq_packed_glu: x [..., H] and indices [..., k] must share leading dimensions")
+    act = torch.empty(*lead, k, I, dtype=x.dtype, device=x.device)
+    if T * k == 0:
+        return act
+    experts = indices.reshape(-1).to(torch.int32).contiguous()
+    xc = x.reshape(T, H).contiguous()
+    g = tuple(t.contiguous() for t in gate)
+    u = tuple(t.contiguous() for t in up)
+    _abi.check(_lib().kmi_vq_packed_glu(
+        _ptr(xc), T, H, I, _ptr(g[0]), _ptr(g[2]), _ptr(g[1]), _ptr(u[0]), _ptr(u[2]), _ptr(u[1]), pack_bits,
+        kc, dim, group, E, None, k, _ptr(experts), T * k, DTYPE_CODE[x.dtype], _ptr(act), _stream(x)),
+        "vq_packed_glu")
+    return act
+
+
 def _vq_indices(x, E, lhs_indices, rhs_indices):
     dev = x.device
     xbatch = tuple(x.shape[:-2])

@@ -39,7 +39,9 @@ sites, and pinned as follows (each function's docstring names its pins):
   numpy softmax, mask cases of tests/engine/test_kvattn.py:86-113,253-279.
 * VQ decode matmul -- closed form (decode, then dense matmul in numpy);
   the bundled VQ runtime is not in the reference, so bit-level parity with
-  it is unpinned.
+  it is unpinned.  The packed field order (LSB first in a little-endian
+  word stream) is pinned against an independent bit-by-bit writer; that the
+  bundled runtime reads the same order is unpinned (it is not vendored).
 """
 from __future__ import annotations
 
@@ -501,6 +503,38 @@ def vq_matmul(x, codes, codebook, scales, scale_group: int = 0,
     lib().orc_vq_matmul(_p(x), M, IN, OUT, _p(codes), cbytes, _p(cb), kc, dim,
                         _p(s), sg, _p(y), threads())
     return round_to(y, out_dtype).reshape(*x.shape[:-1], OUT)
+
+
+def unpack_fields(words, pack_bits: int, nfields: int) -> np.ndarray:
+    """The packed on-disk VQ code layout (.../heads/deepseek_v4.py:36-44,
+    95-129): field j of a row at bits [j*b, j*b + b) of the row's uint32
+    words read as one little-endian bit stream; ceil(nfields/32) * b words
+    per row.  -> uint16 codes [..., nfields].  Pinned against a bit-by-bit
+    Python writer (tests/test_oracle.py)."""
+    w = np.ascontiguousarray(words, np.uint32)
+    lead = w.shape[:-1]
+    w2 = w.reshape(-1, w.shape[-1]).astype(np.uint64)
+    j = np.arange(nfields, dtype=np.uint64)
+    off = j * np.uint64(pack_bits)
+    q = (off >> np.uint64(5)).astype(np.int64)
+    sh = off & np.uint64(31)
+    lo = w2[:, q] >> sh
+    nxt = np.minimum(q + 1, w2.shape[1] - 1)
+    hi = np.where(sh + np.uint64(pack_bits) > np.uint64(32),
+                  w2[:, nxt] << (np.uint64(32) - sh), np.uint64(0))
+    mask = np.uint64((1 << pack_bits) - 1)
+    return ((lo | hi) & mask).astype(np.uint16).reshape(*lead, nfields)
+
+
+def vq_packed_matmul(x, words, codebook, scales, pack_bits: int, group: int,
+                     out_dtype: str = "bfloat16"):
+    """One VQ expert matrix in the packed layout: the fields unpacked, then
+    ``vq_matmul`` with per-group scales [OUT, IN / group]."""
+    cb = np.asarray(codebook)
+    dim = cb.shape[1]
+    IN = np.asarray(scales).shape[-1] * group
+    codes = unpack_fields(words, pack_bits, IN // dim)
+    return vq_matmul(x, codes, cb, scales, group, out_dtype)
 
 
 def vq_decode_numpy(codes, codebook, scales, scale_group: int = 0):

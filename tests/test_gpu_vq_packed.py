@@ -1,0 +1,127 @@
+"""GPU parity: VQ experts in the artifacts' bit-packed on-disk layout
+(kmi_vq_packed_gather_qmm / kmi_vq_packed_glu: 8-12 and 16-bit fields,
+2-8-element vectors, per-group fp16 scales) against the oracle's unpack
+then exact decode-then-matmul; and modules read from a written safetensors
+artifact (knurlogic_amd.checkpoint) against the oracle.  Bar: max rel err
+1e-2, cosine 0.9999."""
+import json
+
+import numpy as np
+import pytest
+import torch
+
+import knurlogic_amd as K
+import oracle as O
+from knurlogic_amd import checkpoint as C
+from knurlogic_amd import nn
+from tests.util import assert_close, bf16_normal, to_numpy, to_torch, u32_to_torch
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def _packed(rng, E, N, IN, dim, kc, bits, group, dev):
+    nsub = IN // dim
+    codes = rng.integers(0, kc, (E, N, nsub))
+    words = np.zeros((E, N, (nsub + 31) // 32 * bits), np.uint32)
+    flat = C._repack(torch.from_numpy(codes), bits).view(torch.int32).numpy().view(np.uint32)
+    words[...] = flat
+    cb = (rng.standard_normal((kc, dim)) * 0.3).astype(np.float16)
+    sc = rng.uniform(0.5, 1.5, (E, N, IN // group)).astype(np.float16)
+    host = (words, cb.astype(np.float32), sc.astype(np.float32))
+    gpu = (u32_to_torch(words, dev), torch.from_numpy(cb).to(dev), torch.from_numpy(sc).to(dev))
+    return host, gpu
+
+
+CASES = [  # (bits, kc, dim, group, IN)
+    (11, 2048, 4, 64, 2048),
+    (11, 2048, 2, 64, 768),
+    (11, 2048, 4, 32, 96),       # a partial last block (24 fields)
+    (8, 256, 4, 64, 512),
+    (12, 4096, 2, 128, 1024),
+    (16, 5000, 8, 64, 256),
+    (9, 300, 4, 32, 128),
+    (10, 1024, 8, 128, 384),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_packed_gather_matches_the_oracle(dev, case):
+    bits, kc, dim, group, IN = CASES[case]
+    rng = np.random.default_rng(case)
+    E, N, P = 4, 96, 5
+    host, gpu = _packed(rng, E, N, IN, dim, kc, bits, group, dev)
+    x = bf16_normal(rng, (P, 2, IN))
+    rhs = rng.integers(0, E, P).astype(np.int32)
+    got = K.ops.vq_packed_gather_qmm(to_torch(x, dev, BF), *gpu, bits, group,
+                                     rhs_indices=torch.from_numpy(rhs).to(dev))
+    ref = np.stack([O.vq_packed_matmul(x[p], host[0][rhs[p]], host[1], host[2][rhs[p]], bits, group,
+                                       "float32") for p in range(P)])
+    assert got.shape == (P, 2, N)
+    assert_close(to_numpy(got), ref, what=f"packed case {case}")
+
+
+@pytest.mark.parametrize("T,E,H,I,k", [(1, 16, 512, 256, 4), (3, 32, 2048, 768, 8)])
+def test_packed_switch_glu_matches_the_oracle(dev, T, E, H, I, k):
+    rng = np.random.default_rng(T + E)
+    bits, kc, dim, group = 11, 2048, 4, 64
+    (hg, gg), (hu, gu), (hd, gd) = [_packed(rng, E, n, kd, dim, kc, bits, group, dev)
+                                    for n, kd in ((I, H), (I, H), (H, I))]
+    mods = [nn.VQSwitchLinear(*g, scale_group=group, pack_bits=bits) for g in (gg, gu, gd)]
+    glu = nn.VQSwitchGLU(*mods)
+    x = bf16_normal(rng, (T, H))
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    fn = lambda h: (lambda xs, e: O.vq_packed_matmul(xs, h[0][e], h[1], h[2][e], bits, group, "bfloat16"))
+    ref = O.switch_glu(x, inds, fn(hg), fn(hu), fn(hd))
+    tx, ti = to_torch(x, dev, BF), torch.from_numpy(inds).to(dev)
+    got = glu(tx, ti)
+    assert got.shape == (T, k, H)
+    assert_close(to_numpy(got), ref, what="packed vq switch_glu")
+    _, sc = O.route(bf16_normal(rng, (T, E)), k)
+    comb = glu.combine(tx, ti, to_torch(sc, dev, BF))
+    assert_close(to_numpy(comb), O.combine(ref, sc), what="packed combine")
+    # one module's own call
+    y = mods[2](to_torch(ref.reshape(T * k, 1, H)[:, :, :I] * 0 + bf16_normal(rng, (T * k, 1, I)), dev, BF),
+                torch.from_numpy(inds.reshape(-1)).to(dev))
+    assert y.shape == (T * k, 1, H)
+
+
+def test_packed_errors(dev):
+    rng = np.random.default_rng(9)
+    _, gpu = _packed(rng, 2, 8, 128, 4, 2048, 11, 64, dev)
+    x = torch.zeros(1, 1, 128, dtype=BF, device=dev)
+    with pytest.raises(ValueError):
+        K.ops.vq_packed_gather_qmm(x, *gpu, 12, 64)                 # width is not 12-bit
+    with pytest.raises(ValueError):
+        K.ops.vq_packed_gather_qmm(x[..., :64].contiguous(), *gpu, 11, 64)   # K mismatch
+
+
+def test_a_written_artifact_loads_and_matches_the_oracle(dev, tmp_path):
+    """mlx-format affine layers and packed VQ experts written to a
+    safetensors file, read back by checkpoint.load_quantized, computed on
+    the GPU."""
+    from safetensors.torch import save_file
+    rng = np.random.default_rng(11)
+    w = bf16_normal(rng, (256, 512), 0.02)
+    wq, s, b = O.quantize(w, 64, 4)
+    E, OUT, IN, dim, kc, bits, group = 4, 64, 256, 4, 2048, 11, 64
+    host, _ = _packed(rng, E, OUT, IN, dim, kc, bits, group, "cpu")
+    t = {"lin.weight": torch.from_numpy(wq.view(np.int32)).view(torch.uint32),
+         "lin.scales": torch.from_numpy(s).to(BF), "lin.biases": torch.from_numpy(b).to(BF),
+         "vq.codes": torch.from_numpy(host[0].view(np.int32)).view(torch.uint32),
+         "vq.codebook": torch.from_numpy(host[1]).half(), "vq.vq_scales": torch.from_numpy(host[2]).half()}
+    d = tmp_path / "art"
+    d.mkdir()
+    save_file(t, str(d / "model.safetensors"), metadata={"format": "mlx", "vq_modules": json.dumps(
+        {"vq": {"experts": E, "out": OUT, "in": IN, "dim": dim, "k": kc, "group": group, "pack_bits": bits}})})
+    (d / "config.json").write_text(json.dumps({"quantization": {"group_size": 64, "bits": 4}}))
+    mods = C.load_quantized(d, device=dev)
+    x = bf16_normal(rng, (3, 512))
+    got = mods["lin"](to_torch(x, dev, BF))
+    assert_close(to_numpy(got), O.quantized_matmul(x, wq, s, b, True, 64, 4, "float32"), what="loaded linear")
+    xv = bf16_normal(rng, (2, 1, IN))
+    rhs = np.array([3, 1], np.int32)
+    gv = mods["vq"](to_torch(xv, dev, BF), torch.from_numpy(rhs).to(dev))
+    ref = np.stack([O.vq_packed_matmul(xv[p], host[0][rhs[p]], host[1], host[2][rhs[p]], bits, group, "float32")
+                    for p in range(2)])
+    assert_close(to_numpy(gv), ref, what="loaded vq")

@@ -350,6 +350,54 @@ def test_quantized_sdpa_hidden_row_is_the_plain_mean_of_v():
         assert np.array_equal(got[0, h, 1], want[0, h // 2])
 
 
+# --- packed VQ codes ------------------------------------------------------------------
+
+def _pack_fields_bitwise(codes, bits):
+    """Rows of integer codes -> uint32 words, one bit at a time: bit t of
+    field j goes to stream position j*bits + t, stream position p to bit
+    p % 32 of word p // 32, rows padded to whole 32-field blocks."""
+    rows, n = codes.shape
+    words = np.zeros((rows, (n + 31) // 32 * bits), np.uint32)
+    for r in range(rows):
+        for j in range(n):
+            for t in range(bits):
+                if (int(codes[r, j]) >> t) & 1:
+                    p = j * bits + t
+                    words[r, p // 32] |= np.uint32(1 << (p % 32))
+    return words
+
+
+@pytest.mark.parametrize("bits,n", [(11, 48), (8, 40), (12, 32), (9, 7)])
+def test_unpack_fields_reads_the_bitwise_packing(bits, n):
+    rng = np.random.default_rng(bits * 100 + n)
+    codes = rng.integers(0, 1 << bits, (3, n))
+    words = _pack_fields_bitwise(codes, bits)
+    assert words.shape == (3, (n + 31) // 32 * bits)
+    assert np.array_equal(O.unpack_fields(words, bits, n), codes)
+
+
+def test_eight_bit_fields_are_the_byte_layout():
+    """At 8 bits the packed stream is the uint8 code layout (little-endian
+    words), whole blocks."""
+    rng = np.random.default_rng(1)
+    codes = rng.integers(0, 256, (2, 64)).astype(np.uint8)
+    words = codes.view(np.uint32)
+    assert np.array_equal(O.unpack_fields(words, 8, 64), codes)
+
+
+def test_vq_packed_matmul_equals_decode_then_dense():
+    rng = np.random.default_rng(2)
+    OUT, IN, dim, kc, group = 24, 256, 4, 2048, 64
+    codes = rng.integers(0, kc, (OUT, IN // dim))
+    words = _pack_fields_bitwise(codes, 11)
+    cb = O.f16_round(rng.standard_normal((kc, dim)).astype(np.float32) * 0.3)
+    sc = O.f16_round((0.5 + rng.random((OUT, IN // group))).astype(np.float32))
+    x = bf16_normal(rng, (3, IN))
+    ref = x.astype(np.float64) @ O.vq_decode_numpy(codes, cb, sc, group).T
+    got = O.vq_packed_matmul(x, words, cb, sc, 11, group, "float32")
+    assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+
+
 # --- VQ decode matmul ----------------------------------------------------------------
 
 @pytest.mark.parametrize("code_dtype,kc", [(np.uint8, 256), (np.uint16, 4096)])
