@@ -99,6 +99,10 @@ __global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
     const bool two_cb = a.nset == 2 && a.cb[1] != a.cb[0];
     const int64_t nsub = a.K / DIM;                  // fields per row
     const int64_t Kp = (nsub + 31) / 32 * 32 * DIM;  // x staged to whole blocks (zeros past K)
+    // x in LDS: block b's 32 vectors at b * XBS elements, one vector of
+    // padding per block, so the lanes of a row (one block each) read
+    // different banks (a block is a multiple of 256 bytes otherwise)
+    constexpr int XBS = 33 * DIM;
     uint16_t* cbl0 = (uint16_t*)smem;
     uint16_t* cbl1 = two_cb ? cbl0 + (size_t)a.kc * DIM : cbl0;
     uint16_t* xl = cbl0 + (size_t)a.kc * DIM * (two_cb ? 2 : 1);
@@ -116,7 +120,8 @@ __global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
             const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(rx, i * 4, 0, 0);
             const vp_f16x2 h = {(_Float16)bf16_to_f32((uint16_t)(v & 0xffffu)),
                                 (_Float16)bf16_to_f32((uint16_t)(v >> 16))};
-            *(uint32_t*)(xl + 2 * i) = __builtin_bit_cast(uint32_t, h);
+            const int e = 2 * i, blk = e / (32 * DIM);
+            *(uint32_t*)(xl + blk * XBS + (e - blk * 32 * DIM)) = __builtin_bit_cast(uint32_t, h);
         }
     }
     __syncthreads();
@@ -147,15 +152,25 @@ __global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
             }
             const int64_t f0 = b * 32;
             const int nvalid = (int)(nsub - f0 < 32 ? nsub - f0 : 32);
+            const uint16_t* xb = xl + b * XBS;
             float acc[GPB];
 #pragma unroll
             for (int g = 0; g < GPB; g++) acc[g] = 0.f;
+            if (nvalid == 32) {
 #pragma unroll
-            for (int j = 0; j < 32; j++) {
-                uint32_t c = vp_field<PB>(w, j);
-                c = c < (uint32_t)a.kc ? c : (uint32_t)(a.kc - 1);
-                const float d = vp_dot<DIM>(cbl + c * DIM, xl + (f0 + j) * DIM, 0.f);
-                acc[j / FPG] += j < nvalid ? d : 0.f;
+                for (int j = 0; j < 32; j++) {
+                    uint32_t c = vp_field<PB>(w, j);
+                    c = c < (uint32_t)a.kc ? c : (uint32_t)(a.kc - 1);
+                    acc[j / FPG] = vp_dot<DIM>(cbl + c * DIM, xb + j * DIM, acc[j / FPG]);
+                }
+            } else {                 // the last, partial block of a row
+#pragma unroll
+                for (int j = 0; j < 32; j++) {
+                    uint32_t c = vp_field<PB>(w, j);
+                    c = c < (uint32_t)a.kc ? c : (uint32_t)(a.kc - 1);
+                    const float d = vp_dot<DIM>(cbl + c * DIM, xb + j * DIM, 0.f);
+                    acc[j / FPG] += j < nvalid ? d : 0.f;
+                }
             }
 #pragma unroll
             for (int g = 0; g < GPB; g++) tot = __builtin_fmaf(sv[g], acc[g], tot);
@@ -234,7 +249,8 @@ static int vp_check(int dtype, int pack_bits, int kc, int dim, int group, int64_
                   "vq (packed): scale group %d (at least 32 inputs, a power of two fields) is not implemented",
                   group);
     const int64_t W = (K / dim + 31) / 32 * pack_bits;
-    KMI_CHECK_ARG(E * N * W * 4 < (1LL << 31) && (size_t)kc * dim * 2 * 2 + (size_t)(K + 256) * 2 <= 160 * 1024,
+    KMI_CHECK_ARG(E * N * W * 4 < (1LL << 31) &&
+                      (size_t)kc * dim * 2 * 2 + (size_t)(W / pack_bits) * 33 * dim * 2 <= 160 * 1024,
                   "vq (packed): codes past 2 GiB or codebook + x past the LDS");
     return OK;
 }
@@ -245,7 +261,7 @@ static int run_vp(VpArgs& a, int pack_bits, int dim, hipStream_t st) {
     const int gpb = fpg >= 32 ? 1 : 32 / fpg;
     const int seg = vp_seg(nblk);
     const bool two_cb = a.nset == 2 && a.cb[1] != a.cb[0];
-    const size_t lds = (size_t)a.kc * dim * 2 * (two_cb ? 2 : 1) + (size_t)nblk * 32 * dim * 2;
+    const size_t lds = (size_t)a.kc * dim * 2 * (two_cb ? 2 : 1) + (size_t)nblk * 33 * dim * 2;
     int rc;
     switch (pack_bits) {
         case 8: rc = launch_vp_pb<8>(a, dim, gpb, seg, lds, st); break;
