@@ -166,7 +166,9 @@ size_t kmi_kv8_workspace_bytes(int B, int H, int Hk, int L, int N, int D);
  * x rows and batch strides are multiples of 8 elements from a 16-byte
  * aligned base, and each row is read in 16-byte units: the elements up to
  * the next multiple of 8 past K must be readable memory (their values are
- * ignored).  With transpose=1 the weight rows are 16-byte aligned.
+ * ignored).  With transpose=1 and 4 or 8 bits the weight rows are 16-byte
+ * aligned.  bits: 2, 3, 4, 5, 6 or 8 (3, 5 and 6-bit codes are read from the
+ * row's little-endian bit stream, mlx's packing of those widths).
  * The weight tile is dequantized to bf16 operands (as mlx's tiled qmm),
  * fp32 accumulation.  `workspace` (kmi_qmm_batched_workspace_bytes) holds
  * split-K partials; it may be NULL when that size is 0.

@@ -42,7 +42,6 @@ template <typename T, int BITS, int GS>
 __global__ __launch_bounds__(256) void quantize_kernel(const typename T::storage* __restrict__ w,
                                                        int64_t n_groups, int64_t D, QuantDst d) {
     constexpr int LPG = GS / 8;                  // lanes per group
-    constexpr int EPW = 32 / BITS;
     using St = typename T::storage;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t gi = t / LPG;
@@ -84,15 +83,12 @@ __global__ __launch_bounds__(256) void quantize_kernel(const typename T::storage
         scale = edge / q0;
         bias = edge;
     }
-    uint32_t bitsv = 0;                          // this lane's 8 codes (8 * BITS bits, low first)
-    uint32_t hi = 0;                             // codes 4..7 at 8 bits
+    uint64_t bitsv = 0;                          // this lane's 8 codes (8 * BITS bits, low first)
 #pragma unroll
     for (int e = 0; e < 8; e++) {
         float q = rintf((v[e] - bias) / scale);
         q = fminf(fmaxf(q, 0.0f), n_bins);
-        const uint32_t c = (uint32_t)q;
-        if (BITS == 8 && e >= 4) hi |= c << ((e - 4) * 8);
-        else bitsv |= c << (e * BITS);
+        bitsv |= (uint64_t)q << (e * BITS);
     }
     if (!live) return;
     // destination of this group's words and of its scale / bias
@@ -102,20 +98,24 @@ __global__ __launch_bounds__(256) void quantize_kernel(const typename T::storage
         const int64_t r = gi / gpr, gs = gi % gpr;
         const int64_t s = r % d.S, bh = r / d.S, h = bh % d.H, b = bh / d.H;
         const int64_t n = d.pos + s;
-        wo = b * d.wst[0] + h * d.wst[1] + n * d.wst[2] + gs * (GS / EPW);
+        wo = b * d.wst[0] + h * d.wst[1] + n * d.wst[2] + gs * (GS * BITS / 32);
         so = b * d.sst[0] + h * d.sst[1] + n * d.sst[2] + gs;
     } else {
-        wo = gi * (GS / EPW);
+        wo = gi * (GS * BITS / 32);
         so = gi;
     }
     if constexpr (BITS == 8) {
-        d.wq[wo + 2 * sub] = bitsv;              // word strides need only be 4-byte multiples
-        d.wq[wo + 2 * sub + 1] = hi;
+        d.wq[wo + 2 * sub] = (uint32_t)bitsv;    // word strides need only be 4-byte multiples
+        d.wq[wo + 2 * sub + 1] = (uint32_t)(bitsv >> 32);
     } else if constexpr (BITS == 4) {
-        d.wq[wo + sub] = bitsv;
-    } else {                                     // 2 bits: two lanes per word
-        const uint32_t other = __shfl_xor(bitsv, 1, 64);
-        if ((sub & 1) == 0) d.wq[wo + sub / 2] = bitsv | (other << 16);
+        d.wq[wo + sub] = (uint32_t)bitsv;
+    } else if constexpr (BITS == 2) {            // two lanes per word
+        const uint32_t other = __shfl_xor((uint32_t)bitsv, 1, 64);
+        if ((sub & 1) == 0) d.wq[wo + sub / 2] = (uint32_t)bitsv | (other << 16);
+    } else {                                     // 3, 5, 6 bits: BITS whole bytes per lane
+        unsigned char* dst = (unsigned char*)(d.wq + wo) + sub * BITS;
+#pragma unroll
+        for (int i = 0; i < BITS; i++) dst[i] = (unsigned char)(bitsv >> (8 * i));
     }
     if (sub == 0) {
         ((St*)d.scales)[so] = T::store(scale);
@@ -152,6 +152,32 @@ __global__ __launch_bounds__(256) void dequantize_kernel(
     }
 }
 
+// 3, 5 and 6 bits: one thread per 8 elements (BITS whole bytes of the
+// row's bit stream).
+template <typename TS, typename TO, int BITS>
+__global__ __launch_bounds__(256) void dequantize_bytes_kernel(
+    const uint32_t* __restrict__ wq, const typename TS::storage* __restrict__ scales,
+    const typename TS::storage* __restrict__ biases, int64_t n_units, int group,
+    int rounding, typename TO::storage* __restrict__ out) {
+    const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= n_units) return;
+    const unsigned char* src = (const unsigned char*)wq + u * BITS;
+    uint64_t v = 0;
+#pragma unroll
+    for (int i = 0; i < BITS; i++) v |= (uint64_t)src[i] << (8 * i);
+    const int64_t e0 = u * 8;
+    const int64_t g = e0 / group;
+    const float s = TS::load(scales[g]);
+    const float b = TS::load(biases[g]);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float q = (float)((v >> (BITS * e)) & ((1u << BITS) - 1u));
+        const float r = rounding == 0 ? TO::round(__fadd_rn(TO::round(__fmul_rn(s, q)), b))
+                                      : TO::round(__builtin_fmaf(s, q, b));
+        out[e0 + e] = TO::store(r);
+    }
+}
+
 template <typename T, int BITS>
 static void launch_quantize_b(const void* w, int64_t n_groups, int group, int64_t D, const QuantDst& d,
                               hipStream_t st) {
@@ -168,6 +194,9 @@ static void launch_quantize(const void* w, int64_t n_groups, int group, int bits
                             const QuantDst& d, hipStream_t st) {
     if (bits == 4) launch_quantize_b<T, 4>(w, n_groups, group, D, d, st);
     else if (bits == 8) launch_quantize_b<T, 8>(w, n_groups, group, D, d, st);
+    else if (bits == 3) launch_quantize_b<T, 3>(w, n_groups, group, D, d, st);
+    else if (bits == 5) launch_quantize_b<T, 5>(w, n_groups, group, D, d, st);
+    else if (bits == 6) launch_quantize_b<T, 6>(w, n_groups, group, D, d, st);
     else launch_quantize_b<T, 2>(w, n_groups, group, D, d, st);
 }
 
@@ -178,6 +207,15 @@ static void launch_dequantize(const uint32_t* wq, const void* s, const void* b,
     dim3 grid((unsigned)ceil_div(n_words, 256));
     using SS = typename TS::storage;
     using SO = typename TO::storage;
+    if (32 % bits) {                   // n_words counts 8-element units here
+        if (bits == 3)
+            dequantize_bytes_kernel<TS, TO, 3><<<grid, 256, 0, st>>>(wq, (const SS*)s, (const SS*)b, n_words, group, rounding, (SO*)out);
+        else if (bits == 5)
+            dequantize_bytes_kernel<TS, TO, 5><<<grid, 256, 0, st>>>(wq, (const SS*)s, (const SS*)b, n_words, group, rounding, (SO*)out);
+        else
+            dequantize_bytes_kernel<TS, TO, 6><<<grid, 256, 0, st>>>(wq, (const SS*)s, (const SS*)b, n_words, group, rounding, (SO*)out);
+        return;
+    }
     if (bits == 4)
         dequantize_kernel<TS, TO, 4><<<grid, 256, 0, st>>>(wq, (const SS*)s, (const SS*)b, n_words, group, rounding, (SO*)out);
     else if (bits == 8)
@@ -201,7 +239,7 @@ int kmi_quantize_affine(const void* w, int dtype, int64_t rows, int64_t cols,
                         void* biases, void* stream) {
     clear_error();
     KMI_CHECK_ARG(w && wq && scales && biases, "quantize: null pointer");
-    KMI_CHECK_ARG(bits == 2 || bits == 4 || bits == 8, "quantize: bits %d not in {2,4,8}", bits);
+    KMI_CHECK_ARG(bits >= 2 && bits <= 8 && bits != 7, "quantize: bits %d not in {2,3,4,5,6,8}", bits);
     KMI_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
                   "quantize: group_size %d not in {32,64,128}", group_size);
     KMI_CHECK_ARG(rows >= 0 && cols > 0 && cols % group_size == 0,
@@ -225,7 +263,8 @@ int kmi_kv_quantize_append(const void* x, int dtype, int64_t B, int64_t H, int64
                            const int64_t* strides, int64_t pos, int64_t capacity, void* stream) {
     clear_error();
     KMI_CHECK_ARG(x && wq && scales && biases && strides, "kv_quantize_append: null pointer");
-    KMI_CHECK_ARG(bits == 2 || bits == 4 || bits == 8, "kv_quantize_append: bits %d not in {2,4,8}", bits);
+    KMI_CHECK_ARG(bits >= 2 && bits <= 8 && bits != 7, "kv_quantize_append: bits %d not in {2,3,4,5,6,8}",
+                  bits);
     KMI_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
                   "kv_quantize_append: group_size %d not in {32,64,128}", group_size);
     KMI_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && D > 0 && D % group_size == 0,
@@ -258,14 +297,15 @@ int kmi_dequantize_affine(const uint32_t* wq, const void* scales, const void* bi
                           int bits, void* out, int out_dtype, int rounding, void* stream) {
     clear_error();
     KMI_CHECK_ARG(wq && scales && biases && out, "dequantize: null pointer (affine needs biases)");
-    KMI_CHECK_ARG(bits == 2 || bits == 4 || bits == 8, "dequantize: bits %d not in {2,4,8}", bits);
+    KMI_CHECK_ARG(bits >= 2 && bits <= 8 && bits != 7, "dequantize: bits %d not in {2,3,4,5,6,8}", bits);
     KMI_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
                   "dequantize: group_size %d not in {32,64,128}", group_size);
     KMI_CHECK_ARG(rows >= 0 && cols > 0 && cols % group_size == 0, "dequantize: bad shape");
     KMI_CHECK_ARG(rounding == 0 || rounding == 1, "dequantize: rounding %d not in {0,1}", rounding);
     KMI_CHECK_ARG(scale_dtype >= BF16 && scale_dtype <= F32 && out_dtype >= BF16 && out_dtype <= F32,
                   "dequantize: bad dtype");
-    const int64_t n_words = rows * cols * bits / 32;
+    // packed words, or 8-element units for the widths that do not divide 32
+    const int64_t n_words = 32 % bits ? rows * cols / 8 : rows * cols * bits / 32;
     if (n_words == 0) return OK;
     hipStream_t st = (hipStream_t)stream;
 #define KMI_DQ(TS, TO) launch_dequantize<TS, TO>(wq, scales, biases, n_words, group_size, bits, rounding, out, st)

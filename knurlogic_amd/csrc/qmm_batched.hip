@@ -111,7 +111,14 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
     const int kq = tid >> 4, nq = tid & 15;
     const int64_t n_t = nt * QB_T + xrow;
 
-    constexpr int WV = TRANS ? BITS / 2 : 4;      // staged words (TRANS: 16 codes; else 4 rows x 4 codes)
+    // staged words: TRANS 16 codes (4 / 8 bits: the words themselves; other
+    // widths: four words from the one holding the run's first bit), else 4
+    // rows x 4 codes (one word per row, or two for the other widths)
+    constexpr bool WORD_ALIGNED = BITS == 4 || BITS == 8;
+    constexpr int WV = TRANS ? (BITS == 8 ? 4 : BITS == 4 ? 2 : 4) : (WORD_ALIGNED ? 4 : 8);
+    // other widths: the bit offset of a thread's run within its first word
+    // is the same on every k-tile / row (tiles hold 64 codes)
+    const uint32_t wsh = TRANS ? (uint32_t)((16 * xc * BITS) & 31) : (uint32_t)((4 * nq * BITS) & 31);
     u32x4 rxv[2];
     uint32_t rwv[WV];
     uint32_t rsv[TRANS ? 1 : 4], rbv[TRANS ? 1 : 4];
@@ -130,9 +137,15 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
             if constexpr (BITS == 8) {
                 const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)woff, 0, 0);
                 rwv[0] = v.x; rwv[1] = v.y; rwv[2] = v.z; rwv[3] = v.w;
-            } else {
+            } else if constexpr (BITS == 4) {
                 const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rw, (int)woff, 0, 0);
                 rwv[0] = v.x; rwv[1] = v.y;
+            } else {
+                // words past the row's end belong to the next row or read
+                // as zeros past the range; their bits are never used
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    rwv[q] = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? (int)(woff + 4 * q) : (int)QB_DEAD, 0, 0);
             }
             const uint32_t soff = ok ? (uint32_t)((n_t * a.sr + k0 / GS) * 2) : QB_DEAD;
             rsv[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff, 0, 0);
@@ -146,9 +159,13 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
                 if constexpr (BITS == 8) {
                     const uint32_t woff = ok ? (uint32_t)((k * a.wr + n / 4) * 4) : QB_DEAD;
                     rwv[j] = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)woff, 0, 0);
-                } else {
+                } else if constexpr (BITS == 4) {
                     const uint32_t woff = ok ? (uint32_t)(k * a.wr * 4 + n / 2) : QB_DEAD;
                     rwv[j] = __builtin_amdgcn_raw_buffer_load_b16(rw, (int)woff, 0, 0);
+                } else {
+                    const uint32_t woff = ok ? (uint32_t)((k * a.wr + n * BITS / 32) * 4) : QB_DEAD;
+                    rwv[2 * j] = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)woff, 0, 0);
+                    rwv[2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? (int)(woff + 4) : (int)QB_DEAD, 0, 0);
                 }
                 const uint32_t soff = ok ? (uint32_t)((k * a.sr + n / GS) * 2) : QB_DEAD;
                 rsv[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff, 0, 0);
@@ -181,14 +198,28 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
         }
         if constexpr (TRANS) {
             const float sc = bf16_to_f32((uint16_t)rsv[0]), bi = bf16_to_f32((uint16_t)rbv[0]);
-            constexpr int CPW = 32 / BITS;
+            float q[16];
+            if constexpr (WORD_ALIGNED) {
+                constexpr int CPW = 32 / BITS;
+#pragma unroll
+                for (int i = 0; i < 16; i++) q[i] = qb_code(rwv[i / CPW], i % CPW, BITS);
+            } else {
+                // the run's bit stream shifted to bit 0, then fields at i * BITS
+                const uint32_t r0 = __builtin_amdgcn_alignbit(rwv[1], rwv[0], wsh);
+                const uint32_t r1 = __builtin_amdgcn_alignbit(rwv[2], rwv[1], wsh);
+                const uint32_t r2 = __builtin_amdgcn_alignbit(rwv[3], rwv[2], wsh);
+                const uint32_t r[3] = {r0, r1, r2};
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int o = i * BITS, w = o >> 5, sh = o & 31;
+                    const uint32_t f = sh + BITS <= 32 ? r[w] >> sh : __builtin_amdgcn_alignbit(r[w + 1], r[w], sh);
+                    q[i] = (float)(f & ((1u << BITS) - 1u));
+                }
+            }
             uint32_t oh[8], ol[8];
 #pragma unroll
-            for (int i = 0; i < 16; i += 2) {
-                const float v0 = __builtin_fmaf(sc, qb_code(rwv[i / CPW], i % CPW, BITS), bi);
-                const float v1 = __builtin_fmaf(sc, qb_code(rwv[(i + 1) / CPW], (i + 1) % CPW, BITS), bi);
-                qb_split(v0, v1, oh[i / 2], ol[i / 2]);
-            }
+            for (int i = 0; i < 16; i += 2)
+                qb_split(__builtin_fmaf(sc, q[i], bi), __builtin_fmaf(sc, q[i + 1], bi), oh[i / 2], ol[i / 2]);
             u32x4* dh = (u32x4*)&Bh[xrow * QB_LD + 16 * xc];
             u32x4* dl = (u32x4*)&Bl[xrow * QB_LD + 16 * xc];
             dh[0] = u32x4{oh[0], oh[1], oh[2], oh[3]};
@@ -201,7 +232,16 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
             for (int j = 0; j < 4; j++) {
                 const float sc = bf16_to_f32((uint16_t)rsv[j]), bi = bf16_to_f32((uint16_t)rbv[j]);
 #pragma unroll
-                for (int c = 0; c < 4; c++) v[j][c] = __builtin_fmaf(sc, qb_code(rwv[j], c, BITS), bi);
+                for (int c = 0; c < 4; c++) {
+                    float q;
+                    if constexpr (WORD_ALIGNED) {
+                        q = qb_code(rwv[j], c, BITS);
+                    } else {
+                        const uint32_t r = __builtin_amdgcn_alignbit(rwv[2 * j + 1], rwv[2 * j], wsh);
+                        q = (float)((r >> (c * BITS)) & ((1u << BITS) - 1u));
+                    }
+                    v[j][c] = __builtin_fmaf(sc, q, bi);
+                }
             }
 #pragma unroll
             for (int c = 0; c < 4; c++) {
@@ -457,13 +497,15 @@ static void launch_qb(const QbArgs& a, dim3 grid, hipStream_t st) {
 #define KMI_QB_CASE(B_, G_, T_) \
     if (bits == B_ && gs == G_ && trans == T_) { launch_qb<B_, G_, T_>(a, grid, st); return OK; }
 #define KMI_QB_G(B_, T_) KMI_QB_CASE(B_, 32, T_) KMI_QB_CASE(B_, 64, T_) KMI_QB_CASE(B_, 128, T_)
+#define KMI_QB_B(B_) KMI_QB_G(B_, true) KMI_QB_G(B_, false)
 
 static int launch_batched(const QbArgs& a, int bits, int gs, bool trans, dim3 grid, hipStream_t st) {
-    KMI_QB_G(4, true) KMI_QB_G(8, true) KMI_QB_G(4, false) KMI_QB_G(8, false)
+    KMI_QB_B(4) KMI_QB_B(8) KMI_QB_B(2) KMI_QB_B(3) KMI_QB_B(5) KMI_QB_B(6)
     set_error("quantized_matmul (batched): no kernel for bits=%d gs=%d", bits, gs);
     return EINVAL_ARG;
 }
 
+#undef KMI_QB_B
 #undef KMI_QB_G
 #undef KMI_QB_CASE
 
@@ -493,7 +535,8 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
                     size_t workspace_bytes, void* stream) {
     clear_error();
     KMI_CHECK_ARG(dtype == BF16, "quantized_matmul (batched): only bfloat16 is supported (got dtype %d)", dtype);
-    KMI_CHECK_ARG(bits == 4 || bits == 8, "quantized_matmul (batched): bits %d not in {4, 8}", bits);
+    KMI_CHECK_ARG(bits >= 2 && bits <= 8 && bits != 7, "quantized_matmul (batched): bits %d not in {2,3,4,5,6,8}",
+                  bits);
     KMI_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
                   "quantized_matmul (batched): group_size %d not in {32, 64, 128}", group_size);
     KMI_CHECK_ARG(nd >= 0 && nd <= QB_MAXD, "quantized_matmul (batched): %d batch dimensions (at most %d)",
@@ -525,7 +568,7 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
     KMI_CHECK_ARG(((M - 1) * xr + ((K + 7) & ~7LL)) * 2 < (1LL << 31) && ((wrows - 1) * wr + wrow_words) * 4 < (1LL << 31) &&
                       ((wrows - 1) * sr + grouped / group_size) * 2 < (1LL << 31),
                   "quantized_matmul (batched): one batch entry exceeds 2 GB");
-    if (transpose) {
+    if (transpose && (bits == 4 || bits == 8)) {
         // 16-byte (8-bit) / 8-byte (4-bit) weight loads along a row
         bool al = ((uintptr_t)w & 15) == 0 && wr % 4 == 0;
         for (int d = 0; d < nd; d++) al = al && w_strides[d] % 4 == 0;

@@ -106,8 +106,8 @@ def append_quantized(parts, x: torch.Tensor, pos: int, group: int, bits: int) ->
     triple ``parts`` (kmi_kv_quantize_append: one launch)."""
     wq, sc, bi = parts
     _on_gpu(x, wq, sc, bi)
-    if bits not in (2, 4, 8):
-        raise ValueError(f"KV cache: {bits}-bit storage is not implemented on the GPU (8, 4)")
+    if bits not in (2, 3, 4, 5, 6, 8):
+        raise ValueError(f"KV cache: {bits}-bit storage is not implemented (2, 3, 4, 5, 6, 8)")
     if x.dtype not in DTYPE_CODE or sc.dtype != x.dtype or bi.dtype != x.dtype:
         raise ValueError("KV cache: keys/values and the stored scales must share a float dtype")
     if sc.stride(-1) != 1 or wq.stride(-1) != 1 or sc.stride() != bi.stride():

@@ -144,11 +144,11 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     """``mx.quantized_matmul``: x [..., M, K] @ What^T with What [..., N, K]
     (transpose=True) or x @ What with What [..., K, N] (transpose=False,
     groups along N), fp32 accumulation, the result in x's dtype.  A 2-D
-    What with transpose=True is the dense projection (kmi_qmm); a batched
-    What (leading dimensions broadcast against x's) or transpose=False runs
-    kmi_qmm_batched."""
+    What at 4 or 8 bits with transpose=True is the dense projection
+    (kmi_qmm); a batched What (leading dimensions broadcast against x's),
+    transpose=False or the 2, 3, 5 and 6-bit widths run kmi_qmm_batched."""
     _check_mode(mode)
-    if not transpose or w.ndim != 2:
+    if not transpose or w.ndim != 2 or bits not in (4, 8):
         return qmm_batched(x, w, scales, biases, transpose, group_size, bits)
     _check_affine_operands(x, w, scales, biases, group_size, bits, "quantized_matmul")
     K = x.shape[-1]
@@ -242,8 +242,9 @@ def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 
         raise ValueError(f"{what}: only bfloat16 activations, scales and biases are implemented")
     if w.dtype not in (torch.uint32, torch.int32) or w.ndim < 2:
         raise ValueError(f"{what}: w must be packed uint32 with at least 2 dimensions")
-    if bits not in (4, 8) or group_size not in (32, 64, 128):
-        raise ValueError(f"{what}: bits {bits} / group {group_size} not implemented (4, 8 / 32, 64, 128)")
+    if bits not in (2, 3, 4, 5, 6, 8) or group_size not in (32, 64, 128):
+        raise ValueError(f"{what}: bits {bits} / group {group_size} not implemented "
+                         "(2, 3, 4, 5, 6, 8 / 32, 64, 128)")
     vec = x.ndim == 1
     if vec:
         x = x[None]
@@ -276,7 +277,7 @@ def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 
     if y.numel() == 0:
         return y[0] if vec else y
     x = _aligned_rows(x)
-    if w.stride(-1) != 1 or (transpose and (w.data_ptr() % 16 or any(
+    if w.stride(-1) != 1 or (transpose and bits in (4, 8) and (w.data_ptr() % 16 or any(
             st % 4 for d, st in enumerate(w.stride()[:-1]) if w.shape[d] > 1))):
         w = w.contiguous()
         if w.data_ptr() % 16:

@@ -141,7 +141,7 @@ def quantize(w, group_size: int = 64, bits: int = 4, dtype: str = "bfloat16"):
     w = _f32(w)
     shp = w.shape
     cols = shp[-1]
-    if cols % group_size or (cols * bits) % 32 or bits not in (2, 4, 8):
+    if cols % group_size or (cols * bits) % 32 or bits not in (2, 3, 4, 5, 6, 8):
         raise ValueError("last axis must divide by the group and pack in 32 bits")
     rows = int(np.prod(shp[:-1], dtype=np.int64))
     wq = np.zeros((rows, cols * bits // 32), np.uint32)
@@ -173,8 +173,12 @@ def dequantize(wq, scales, biases, group_size: int = 64, bits: int = 4,
 
 def unpack_numpy(wq, bits: int) -> np.ndarray:
     """The integer codes of packed words, written independently of the C
-    oracle (vectorised shifts) -- the cross-check of the packing order."""
+    oracle (vectorised shifts) -- the cross-check of the packing order.
+    Widths that do not divide 32 read the row's little-endian bit stream
+    (``unpack_fields``)."""
     wq = np.asarray(wq, np.uint32)
+    if 32 % bits:
+        return unpack_fields(wq, bits, wq.shape[-1] * 32 // bits)
     epw = 32 / bits
     epw = int(epw)
     shifts = (np.arange(epw, dtype=np.uint32) * bits)

@@ -33,9 +33,25 @@
 /* ------------------------------------------------------------------------ */
 
 static inline uint32_t unpack_q(const uint32_t* row, int64_t j, int bits) {
-    const int epw = 32 / bits;
-    const uint32_t mask = (bits == 32) ? 0xffffffffu : ((1u << bits) - 1u);
-    return (row[j / epw] >> ((j % epw) * bits)) & mask;
+    /* element j at bits [j*bits, j*bits + bits) of the row read as one
+       little-endian bit stream; for bits dividing 32 this is word
+       j / (32/bits), shift (j % (32/bits)) * bits.  mlx packs its 3, 5 and
+       6-bit modes into bytes in the same stream order. */
+    const int64_t off = j * bits;
+    const int64_t q = off >> 5;
+    const int sh = (int)(off & 31);
+    const uint32_t mask = (1u << bits) - 1u;
+    uint64_t v = row[q] >> sh;
+    if (sh + bits > 32) v |= (uint64_t)row[q + 1] << (32 - sh);
+    return (uint32_t)v & mask;
+}
+
+static inline void pack_q(uint32_t* row, int64_t j, int bits, uint32_t q) {
+    const int64_t off = j * bits;
+    const int64_t w = off >> 5;
+    const int sh = (int)(off & 31);
+    row[w] |= q << sh;
+    if (sh + bits > 32) row[w + 1] |= q >> (32 - sh);
 }
 
 /*
@@ -60,8 +76,7 @@ void orc_quantize_affine(const float* w, int64_t rows, int64_t cols, int group,
                          int bits, uint32_t* wq, float* scales, float* biases) {
     const float n_bins = (float)((1u << bits) - 1u);
     const float eps = 1e-7f;
-    const int epw = 32 / bits;
-    const int64_t wpr = cols / epw;
+    const int64_t wpr = cols * bits / 32;
     const int64_t gpr = cols / group;
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; r++) {
@@ -88,8 +103,7 @@ void orc_quantize_affine(const float* w, int64_t rows, int64_t cols, int group,
             for (int i = 0; i < group; i++) {
                 float q = rintf((wg[i] - bias) / scale);
                 q = fminf(fmaxf(q, 0.0f), n_bins);
-                int64_t j = g * group + i;
-                qr[j / epw] |= ((uint32_t)q) << ((j % epw) * bits);
+                pack_q(qr, g * group + i, bits, (uint32_t)q);
             }
             scales[r * gpr + g] = scale;
             biases[r * gpr + g] = bias;
@@ -150,8 +164,7 @@ void orc_dequantize_affine(const uint32_t* wq, const float* scales,
                            const float* biases, int64_t rows, int64_t cols,
                            int group, int bits, int dtype, int rounding,
                            float* out) {
-    const int epw = 32 / bits;
-    const int64_t wpr = cols / epw;
+    const int64_t wpr = cols * bits / 32;
     const int64_t gpr = cols / group;
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; r++) {
@@ -183,14 +196,13 @@ void orc_dequantize_affine(const uint32_t* wq, const float* scales,
 void orc_qmm(const float* x, int64_t M, int64_t K, int64_t N,
              const uint32_t* wq, const float* scales, const float* biases,
              int group, int bits, int transpose, float* y, int nthreads) {
-    const int epw = 32 / bits;
 #ifdef _OPENMP
     if (nthreads > 0) omp_set_num_threads(nthreads);
 #else
     (void)nthreads;
 #endif
     if (transpose) {
-        const int64_t wpr = K / epw, gpr = K / group;
+        const int64_t wpr = K * bits / 32, gpr = K / group;
 #pragma omp parallel
         {
             double* wrow = (double*)malloc(sizeof(double) * (size_t)K);
@@ -212,7 +224,7 @@ void orc_qmm(const float* x, int64_t M, int64_t K, int64_t N,
             free(wrow);
         }
     } else {
-        const int64_t wpr = N / epw, gpr = N / group;
+        const int64_t wpr = N * bits / 32, gpr = N / group;
 #pragma omp parallel
         {
             double* acc = (double*)malloc(sizeof(double) * (size_t)N);
@@ -256,8 +268,7 @@ void orc_kv8_decode(const float* q, int64_t B, int64_t H, int64_t L, int64_t D,
                     const uint32_t* vw, const float* vs, const float* vb,
                     int64_t Hk, int64_t N, int group, int bits, float scale,
                     const uint8_t* mask, float* out, int nthreads) {
-    const int epw = 32 / bits;
-    const int64_t wpr = D / epw, gpr = D / group;
+    const int64_t wpr = D * bits / 32, gpr = D / group;
     const int64_t rep = H / Hk;
 #ifdef _OPENMP
     if (nthreads > 0) omp_set_num_threads(nthreads);

@@ -19,7 +19,7 @@ def _values(rng, shape, std, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
-@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("group", [32, 64, 128])
 def test_quantize_is_bit_exact(dev, dtype, bits, group):
     rng = np.random.default_rng(100 + bits + group)
@@ -44,7 +44,7 @@ def test_quantize_edge_cases(dev):
 
 
 @pytest.mark.parametrize("rounding", [K.ROUND_OP_BY_OP, K.ROUND_FUSED])
-@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("out", ["bfloat16", "float16", "float32"])
 def test_dequantize_is_bit_exact(dev, rounding, bits, out):
     rng = np.random.default_rng(200 + bits)

@@ -29,7 +29,7 @@ def _bits(t):
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
-@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("bits", [8, 6, 4])
 def test_append_writes_the_oracle_quantization_into_the_slots(dev, dtype, bits):
     c = KC.QuantKVCache(bits)
     chunks = [_kv((2, 4, n, 128), n, dev, DT[dtype]) for n in (3, 1, 300, 1)]
@@ -114,7 +114,34 @@ def test_batched_rows_hold_the_oracle_quantization(dev):
 
 
 def test_append_refuses_what_it_cannot_store(dev):
-    c = KC.QuantKVCache(6)
+    c = KC.QuantKVCache(7)
     x = _kv((1, 1, 2, 64), 0, dev)
     with pytest.raises(ValueError):
         c.update_and_fetch(x, x)
+
+
+def test_a_six_bit_cache_stores_fetches_and_attends_through_the_fallback(dev):
+    """6-bit K/V (the reference's kvquant.BITS): codes straddle words in
+    the row's bit stream; a fetch is within four 8-bit steps of what went
+    in, and attention takes dequantize + sdpa (the decode kernel is
+    8-bit only), matching float64 attention over the dequantized cache."""
+    c = KC.QuantKVCache(6)
+    c.kv8_kernel = True
+    k, v = _kv((1, 2, 50, 128), 1, dev), _kv((1, 2, 50, 128), 2, dev)
+    kk, vv = c.update_and_fetch(k, v)
+    wq, s, b = O.quantize(k.float().cpu().numpy(), 64, 6, "bfloat16")
+    assert np.array_equal(c.keys[0][:, :, :50].cpu().view(torch.int32).numpy(), wq.view(np.int32))
+    assert (KC.materialize(kk).float() - k.float()).abs().max().item() < 0.2
+    assert c.kv8_fetch is None
+    q = _kv((1, 8, 1, 128), 3, dev)
+    kvattn.reset()
+    out = kvattn.sdpa(q, kk, vv, c, 128 ** -0.5, None)
+    Kd = O.dequantize_numpy_f64(*(t.cpu().view(torch.int32).numpy().view(np.uint32) if t.dtype == torch.uint32
+                                  else t.float().cpu().numpy() for t in (c.keys[0][:, :, :50], c.keys[1][:, :, :50],
+                                                                        c.keys[2][:, :, :50])), 64, 6)
+    Vd = O.dequantize_numpy_f64(*(t.cpu().view(torch.int32).numpy().view(np.uint32) if t.dtype == torch.uint32
+                                  else t.float().cpu().numpy() for t in (c.values[0][:, :, :50],
+                                                                        c.values[1][:, :, :50],
+                                                                        c.values[2][:, :, :50])), 64, 6)
+    ref = O.sdpa_numpy_f64(q.float().cpu().numpy() * 128 ** -0.5, Kd, Vd, 1.0)
+    assert_close(to_numpy(out), ref, what="6-bit fallback attention")

@@ -1,9 +1,11 @@
 """GPU: the batched quantized matmul (kmi_qmm_batched, both orientations)
 and mlx-lm's quantized scaled-dot-product attention built on it
 (kvattn.quantized_sdpa, after .../_mlx_vlm/models/base.py:260-302), against
-the oracle.  The kernel dequantizes weight tiles to bf16 operands, as mlx's
-tiled qmm does, where the oracle keeps them exact, so the products meet the
-float bar (max rel err <= 1e-2, cosine >= 0.9999), not bit equality."""
+the oracle.  The kernel dequantizes weight tiles in fp32 and feeds them to
+the matrix cores as two bf16 parts (hi + lo, exact to 2^-17) where the
+oracle keeps them exact, so the products meet the float bar (max rel err
+<= 1e-2, cosine >= 0.9999), not bit equality.  All of mlx's affine widths
+(2, 3, 4, 5, 6, 8 bits) are covered."""
 import numpy as np
 import pytest
 import torch
@@ -33,7 +35,8 @@ CASES = [
 
 
 @pytest.mark.parametrize("transpose", [True, False])
-@pytest.mark.parametrize("bits,group", [(4, 64), (8, 64), (4, 32), (8, 128)])
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 64), (4, 32), (8, 128), (2, 64), (3, 32), (5, 64),
+                                        (6, 128)])
 @pytest.mark.parametrize("case", range(len(CASES)))
 def test_batched_qmm_matches_the_oracle(dev, transpose, bits, group, case):
     xb, wb, M, K, N = CASES[case]
@@ -59,6 +62,19 @@ def test_transpose_false_over_long_and_ragged_reductions(dev, K):
     ref = O.quantized_matmul_batched(x, wq, s, b, False, 64, 8, "float32")
     got = ops.quantized_matmul(to_torch(x, dev, torch.bfloat16), tw, ts, tb, False, 64, 8)
     assert_close(to_numpy(got), ref, what=f"K={K}")
+
+
+@pytest.mark.parametrize("bits", [2, 3, 5, 6])
+def test_dense_projection_at_the_other_widths(dev, bits):
+    """A 2-D weight at 2, 3, 5 or 6 bits (mlx's other affine widths) through
+    quantized_matmul, decode and prefill row counts."""
+    rng = np.random.default_rng(bits)
+    (wq, s, b), (tw, ts, tb) = _quantized(rng, (320, 512), 64, bits, dev)
+    for M in (1, 70):
+        x = bf16_normal(rng, (M, 512))
+        got = ops.quantized_matmul(to_torch(x, dev, torch.bfloat16), tw, ts, tb, True, 64, bits)
+        ref = O.quantized_matmul(x, wq, s, b, True, 64, bits, "float32")
+        assert_close(to_numpy(got), ref, what=f"{bits}-bit M={M}")
 
 
 def test_strided_slab_views_are_read_in_place(dev):

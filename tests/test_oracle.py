@@ -91,7 +91,7 @@ def test_quantize_all_zero_group():
     assert (wq == 0).all() and b[0, 0] == 0.0 and s[0, 0] == O.bf16_round(np.float32(-1e-7))
 
 
-@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("group", [32, 64, 128])
 def test_quantize_invariants(bits, group):
     rng = np.random.default_rng(bits * 1000 + group)
@@ -118,6 +118,39 @@ def test_quantize_invariants(bits, group):
     idx = np.argmax(g == edge[..., None], axis=-1)
     qe = np.take_along_axis(q.reshape(64, -1, group), idx[..., None], -1)[..., 0]
     assert (qe == 0).all()
+
+
+@pytest.mark.parametrize("bits", [3, 5, 6])
+def test_odd_widths_pack_as_one_bit_stream(bits):
+    """3, 5 and 6-bit codes sit back to back in the row's little-endian
+    bit stream (a code may straddle two words): the codes unpacked by the
+    bitwise reader re-pack, bit by bit, into exactly the quantizer's words."""
+    rng = np.random.default_rng(bits)
+    w = bf16_normal(rng, (3, 96), 0.02)
+    wq, s, b = O.quantize(w, 32, bits)
+    assert wq.shape == (3, 96 * bits // 32)
+    q = O.unpack_fields(wq, bits, 96)
+    words = np.zeros_like(wq)
+    for r in range(3):
+        for j in range(96):
+            for t in range(bits):
+                if (int(q[r, j]) >> t) & 1:
+                    p = j * bits + t
+                    words[r, p // 32] |= np.uint32(1 << (p % 32))
+    assert np.array_equal(words, wq)
+    # and the C dequantize reads the same codes
+    deq = O.dequantize(wq, s, b, 32, bits, dtype="float32", rounding=O.ROUND_FUSED)
+    ref = np.repeat(s, 32, -1) * q.astype(np.float32) + np.repeat(b, 32, -1)
+    assert np.abs(deq - ref).max() <= 1e-6 * np.abs(ref).max()
+
+
+def test_six_bit_round_trip_is_within_the_eight_bit_bar_times_four():
+    """The reference offers 6-bit KV (kvquant.py:22); its step is four times
+    the 8-bit one, so a fetch of N(0,1) stays within 4 x 0.05."""
+    rng = np.random.default_rng(2)
+    x = bf16_normal(rng, (2, 40, 64))
+    wq, s, b = O.quantize(x, 64, 6)
+    assert np.abs(O.dequantize(wq, s, b, 64, 6) - x).max() < 0.2
 
 
 def test_eight_bit_round_trip_is_within_the_references_bar():
