@@ -73,6 +73,17 @@ int kmi_kv_quantize_append(const void* x, int dtype, int64_t B, int64_t H, int64
                            const int64_t* strides, int64_t pos, int64_t capacity, void* stream);
 
 /*
+ * mx.dequantize(w, scales, mode="mxfp4" | "mxfp8") over [rows, cols]: element
+ * codes E2M1 (mode 1, 4 bits) or E4M3 (mode 2, 8 bits) packed as mlx packs
+ * 4 / 8-bit codes, times 2^(e - 127) for the uint8 E8M0 scale e of each group
+ * of 32 (scales [rows, cols/32]) -- the scaled modes the reference's loader
+ * maps layers without biases to (src/knurlogic/engine/model/packed.py:20,
+ * load_model.py:153-173).  out in out_dtype.
+ */
+int kmi_dequantize_mx(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t cols, int mode,
+                      void* out, int out_dtype, void* stream);
+
+/*
  * mx.dequantize(wq, scales, biases, group_size, bits, mode="affine",
  * dtype=out_dtype), as called at src/knurlogic/engine/kvquant.py:50-51.
  *   rounding 0: out = T(T(scale*q) + bias)  (op-by-op, the default)
@@ -169,16 +180,25 @@ size_t kmi_kv8_workspace_bytes(int B, int H, int Hk, int L, int N, int D);
  * ignored).  With transpose=1 and 4 or 8 bits the weight rows are 16-byte
  * aligned.  bits: 2, 3, 4, 5, 6 or 8 (3, 5 and 6-bit codes are read from the
  * row's little-endian bit stream, mlx's packing of those widths).
- * The weight tile is dequantized to bf16 operands (as mlx's tiled qmm),
- * fp32 accumulation.  `workspace` (kmi_qmm_batched_workspace_bytes) holds
+ * mode: 0 affine; 1 mxfp4 (E2M1 codes, bits 4); 2 mxfp8 (E4M3 codes, bits
+ * 8) -- both with one E8M0 uint8 scale per 32 elements and no biases
+ * (biases may be NULL), the modes of load_model.py:153-173.
+ * Gather form (mx.gather_qmm, one batch dimension of P pairs): widx[p] picks
+ * the weight / scales of pair p among nw stacked ones (w_strides[0] /
+ * s_strides[0] apart), xidx[p] (or p) its x entry among nx (x_strides[0]
+ * apart); an index out of range gives a zero output.  Both NULL: the strided
+ * batch form (nw, nx unused).
+ * The weight tile is dequantized in fp32 and fed to the MFMAs as two bf16
+ * parts (exact to 2^-17), fp32 accumulation.  `workspace` (kmi_qmm_batched_workspace_bytes) holds
  * split-K partials; it may be NULL when that size is 0.
  */
 size_t kmi_qmm_batched_workspace_bytes(int nd, const int64_t* batch_shape, int64_t M, int64_t K, int64_t N);
 int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, const int64_t* w_strides,
                     const void* scales, const void* biases, const int64_t* s_strides, int nd,
                     const int64_t* batch_shape, int64_t M, int64_t K, int64_t N, int transpose, int dtype,
-                    int group_size, int bits, float x_scale, void* y, int64_t ldy, void* workspace,
-                    size_t workspace_bytes, void* stream);
+                    int group_size, int bits, int mode, const int32_t* widx, const int32_t* xidx, int64_t nw,
+                    int64_t nx, float x_scale, void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                    void* stream);
 
 /* mask kinds of kmi_masked_softmax */
 #define KMI_MASK_NONE 0

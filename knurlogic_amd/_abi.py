@@ -28,8 +28,9 @@ SIGNATURES = {
     "kmi_kv8_decode": (I, [P, I, I, I, I, I, P, P, P, P, P, P, P, I, I, I, I,
                            ctypes.c_float, P, I, P, P, SZ, P]),
     "kmi_kv8_workspace_bytes": (SZ, [I, I, I, I, I, I]),
-    "kmi_qmm_batched": (I, [P, P, P, P, P, P, P, I, P, I64, I64, I64, I, I, I, I, ctypes.c_float, P, I64, P,
-                            SZ, P]),
+    "kmi_dequantize_mx": (I, [P, P, I64, I64, I, P, I, P]),
+    "kmi_qmm_batched": (I, [P, P, P, P, P, P, P, I, P, I64, I64, I64, I, I, I, I, I, P, P, I64, I64,
+                            ctypes.c_float, P, I64, P, SZ, P]),
     "kmi_qmm_batched_workspace_bytes": (SZ, [I, P, I64, I64, I64]),
     "kmi_masked_softmax": (I, [P, I64, I, P, I64, P, I, P, P, I64, P]),
     "kmi_vq_packed_gather_qmm": (I, [P, I64, I64, P, I, P, I, I, P, I, I64, I64, P, I64, P, I64, I, P, P]),

@@ -18,8 +18,8 @@ and the VQ artifacts' expert tensors, read into this package's modules.
   ``vq_modules`` metadata (``experts/out/in/dim/k/group/pack_bits``,
   tests/engine/test_deepseek_v4_mtp.py:206-233).
 
-Only the affine mode is implemented here; an mxfp4 / mxfp8 layer raises
-``ValueError`` naming its mode.  Files are read with safetensors (no code
+The affine, mxfp4 and mxfp8 modes are built; another mode (nvfp4, ...)
+raises ``ValueError`` naming it.  Files are read with safetensors (no code
 executes from a file); tensors are moved to the requested device.
 """
 from __future__ import annotations
@@ -198,15 +198,19 @@ def build(weights: dict, path: str, in_dims: int | None = None, quant: dict | No
             raise ValueError(f"{path}: packed, but neither a module shape nor the config's quantization "
                              "block gives its input size")
     r = recipe(weights, path, in_dims, quant, prefix)
-    if r["mode"] != "affine":
-        raise ValueError(f"{path}: mode {r['mode']!r} is not implemented (affine only)")
+    if r["mode"] not in ("affine", "mxfp4", "mxfp8"):
+        raise ValueError(f"{path}: mode {r['mode']!r} is not implemented (affine, mxfp4, mxfp8)")
     w = _u32(weights[f"{path}.weight"]).to(device)
     s = weights[f"{path}.scales"].to(device)
-    b = weights[f"{path}.biases"].to(device=device, dtype=s.dtype)
+    if r["mode"] == "affine":
+        b = weights[f"{path}.biases"].to(device=device, dtype=s.dtype)
+        act = s.dtype
+    else:
+        b, act = None, torch.bfloat16                      # uint8 E8M0 scales, no biases
     bias = weights.get(f"{path}.bias")
-    bias = bias.to(device=device, dtype=s.dtype) if bias is not None else None
+    bias = bias.to(device=device, dtype=act) if bias is not None else None
     cls = QuantizedLinear if w.dim() == 2 else QuantizedSwitchLinear
-    return cls(w, s, b, bias, group_size=r["group_size"], bits=r["bits"])
+    return cls(w, s, b, bias, group_size=r["group_size"], bits=r["bits"], mode=r["mode"])
 
 
 def load_quantized(model_path=None, files=None, shapes: dict | None = None, device="cuda") -> dict:

@@ -178,6 +178,41 @@ __global__ __launch_bounds__(256) void dequantize_bytes_kernel(
     }
 }
 
+// mx.dequantize(mode="mxfp4" / "mxfp8"): E2M1 / E4M3 elements times the
+// E8M0 scale (2^(e - 127)) of their group of 32; one thread per packed word.
+__device__ __forceinline__ float mx_e8m0(uint32_t e) {
+    if (e == 255u) return __uint_as_float(0x7fc00000u);
+    return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
+}
+
+__device__ __forceinline__ float mx_elem(uint32_t c, int mode) {
+    if (mode == 1) {                              // E2M1
+        const uint32_t e = (c >> 1) & 3u, m = c & 1u;
+        const float mag = e ? __uint_as_float(((e + 126u) << 23) | (m << 22)) : (m ? 0.5f : 0.0f);
+        return (c & 8u) ? -mag : mag;
+    }
+    const uint32_t e = (c >> 3) & 15u, m = c & 7u;  // E4M3
+    float mag;
+    if (e == 15u && m == 7u) mag = __uint_as_float(0x7fc00000u);
+    else if (e == 0u) mag = (float)m * 0.001953125f;
+    else mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+    return (c & 0x80u) ? -mag : mag;
+}
+
+template <typename TO>
+__global__ __launch_bounds__(256) void dequantize_mx_kernel(const uint32_t* __restrict__ wq,
+                                                            const uint8_t* __restrict__ scales, int64_t n_words,
+                                                            int mode, typename TO::storage* __restrict__ out) {
+    const int64_t wi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (wi >= n_words) return;
+    const int bits = mode == 1 ? 4 : 8, epw = 32 / bits;
+    const int64_t e0 = wi * epw;
+    const float s = mx_e8m0(scales[e0 / 32]);
+    const uint32_t w = wq[wi];
+    for (int e = 0; e < epw; e++)
+        out[e0 + e] = TO::store(mx_elem((w >> (bits * e)) & ((1u << bits) - 1u), mode) * s);
+}
+
 template <typename T, int BITS>
 static void launch_quantize_b(const void* w, int64_t n_groups, int group, int64_t D, const QuantDst& d,
                               hipStream_t st) {
@@ -289,6 +324,25 @@ int kmi_kv_quantize_append(const void* x, int dtype, int64_t B, int64_t H, int64
     else if (dtype == F16) launch_quantize<TF16>(x, n_groups, group_size, bits, D, d, st);
     else launch_quantize<TF32>(x, n_groups, group_size, bits, D, d, st);
     KMI_CHECK_LAUNCH("kv_quantize_append");
+    return OK;
+}
+
+int kmi_dequantize_mx(const uint32_t* wq, const uint8_t* scales, int64_t rows, int64_t cols, int mode,
+                      void* out, int out_dtype, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(wq && scales && out, "dequantize (mx): null pointer");
+    KMI_CHECK_ARG(mode == 1 || mode == 2, "dequantize (mx): mode %d (1 mxfp4, 2 mxfp8)", mode);
+    KMI_CHECK_ARG(rows >= 0 && cols > 0 && cols % 32 == 0, "dequantize (mx): cols %lld not a multiple of 32",
+                  (long long)cols);
+    KMI_CHECK_ARG(out_dtype >= BF16 && out_dtype <= F32, "dequantize (mx): bad dtype");
+    const int64_t n_words = rows * cols * (mode == 1 ? 4 : 8) / 32;
+    if (n_words == 0) return OK;
+    const dim3 grid((unsigned)ceil_div(n_words, 256));
+    hipStream_t st = (hipStream_t)stream;
+    if (out_dtype == BF16) dequantize_mx_kernel<TBF16><<<grid, 256, 0, st>>>(wq, scales, n_words, mode, (uint16_t*)out);
+    else if (out_dtype == F16) dequantize_mx_kernel<TF16><<<grid, 256, 0, st>>>(wq, scales, n_words, mode, (uint16_t*)out);
+    else dequantize_mx_kernel<TF32><<<grid, 256, 0, st>>>(wq, scales, n_words, mode, (float*)out);
+    KMI_CHECK_LAUNCH("dequantize (mx)");
     return OK;
 }
 

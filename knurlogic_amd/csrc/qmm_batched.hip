@@ -48,7 +48,44 @@ struct QbArgs {
     int mtiles, S, kts;          // row tiles, K splits, k-tiles per split
     int scale_x;                 // 1: x is staged as bf16(x * x_scale)
     float x_scale;
+    // gather form (one batch dimension of P pairs): the weight of pair p is
+    // entry widx[p] of nw stacked ones (ws[0] / ss[0] apart; out of range:
+    // a zero output), its x entry xidx[p] (xs[0] apart)
+    const int32_t* widx;
+    const int32_t* xidx;
+    int64_t nw, nx;              // stacked weights / x entries (indices past them: zero rows)
 };
+
+// OCP microscaling element and scale encodings (mxfp4: E2M1 elements,
+// mxfp8: E4M3, both with an E8M0 power-of-two scale per 32 elements), built
+// from their bit fields; every value is exact in fp32 (and in bf16).
+__device__ __forceinline__ float qb_e8m0(uint32_t e) {
+    if (e == 255u) return __uint_as_float(0x7fc00000u);
+    return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);     // 2^(e - 127)
+}
+
+__device__ __forceinline__ float qb_e2m1(uint32_t c) {
+    const uint32_t e = (c >> 1) & 3u, m = c & 1u;
+    const float mag = e ? __uint_as_float(((e + 126u) << 23) | (m << 22)) : (m ? 0.5f : 0.0f);
+    return (c & 8u) ? -mag : mag;
+}
+
+__device__ __forceinline__ float qb_e4m3(uint32_t c) {
+    const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+    float mag;
+    if (e == 15u && m == 7u) mag = __uint_as_float(0x7fc00000u);
+    else if (e == 0u) mag = (float)m * 0.001953125f;                         // m * 2^-9
+    else mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+    return (c & 0x80u) ? -mag : mag;
+}
+
+// MODE 0 affine (integer code), 1 mxfp4, 2 mxfp8: the element value of a code
+template <int MODE>
+__device__ __forceinline__ float qb_elem(uint32_t c) {
+    if constexpr (MODE == 1) return qb_e2m1(c);
+    else if constexpr (MODE == 2) return qb_e4m3(c);
+    else return (float)c;
+}
 
 __device__ __forceinline__ uint32_t qb_pack(float lo, float hi) { return cvt_pk_bf16(lo, hi); }
 
@@ -58,11 +95,11 @@ __device__ __forceinline__ void qb_split(float v0, float v1, uint32_t& hi, uint3
     lo = cvt_pk_bf16(v0 - __uint_as_float(hi << 16), v1 - __uint_as_float(hi & 0xffff0000u));
 }
 
-__device__ __forceinline__ float qb_code(uint32_t word, int i, int bits) {
-    return (float)((word >> (bits * i)) & ((1u << bits) - 1u));
+__device__ __forceinline__ uint32_t qb_code(uint32_t word, int i, int bits) {
+    return (word >> (bits * i)) & ((1u << bits) - 1u);
 }
 
-template <int BITS, int GS, bool TRANS>
+template <int BITS, int GS, bool TRANS, int MODE>
 __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
     // one LDS stage (27 KB: five workgroups per CU); the next k-tile's
     // global loads are in flight in registers while this one is multiplied
@@ -80,12 +117,23 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
 
     // this batch entry's matrices
     int64_t xo = 0, wo = 0, so = 0, rem = p;
-    for (int d = a.nd - 1; d >= 0; d--) {
-        const int64_t i = rem % a.shape[d];
-        rem /= a.shape[d];
-        xo += i * a.xs[d];
-        wo += i * a.ws[d];
-        so += i * a.ss[d];
+    bool w_ok = true, x_ok = true;
+    if (a.widx) {
+        const int64_t e = a.widx[p];
+        w_ok = e >= 0 && e < a.nw;
+        wo = (w_ok ? e : 0) * a.ws[0];
+        so = (w_ok ? e : 0) * a.ss[0];
+        const int64_t xi = a.xidx ? (int64_t)a.xidx[p] : p;
+        x_ok = xi >= 0 && xi < a.nx;
+        xo = (x_ok ? xi : 0) * a.xs[0];
+    } else {
+        for (int d = a.nd - 1; d >= 0; d--) {
+            const int64_t i = rem % a.shape[d];
+            rem /= a.shape[d];
+            xo += i * a.xs[d];
+            wo += i * a.ws[d];
+            so += i * a.ss[d];
+        }
     }
     const int64_t wrow_words = (TRANS ? K : N) * BITS / 32;
     const int64_t wrows = TRANS ? N : K;
@@ -93,10 +141,14 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
     // x rows are read in whole 16-byte runs (a run that crosses the end of
     // the range reads as zeros entirely), so the range ends at the last
     // row's padding to 8 elements; elements past K are zeroed on staging
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + xo, ((M - 1) * a.xr + ((K + 7) & ~7LL)) * 2);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + wo, ((wrows - 1) * a.wr + wrow_words) * 4);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s + so, ((wrows - 1) * a.sr + srow) * 2);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b + so, ((wrows - 1) * a.sr + srow) * 2);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + xo, x_ok ? ((M - 1) * a.xr + ((K + 7) & ~7LL)) * 2 : 0);
+    // scales: bf16 (affine) or one E8M0 byte (mx modes); mx modes have no biases
+    constexpr int SB = MODE ? 1 : 2;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + wo, w_ok ? ((wrows - 1) * a.wr + wrow_words) * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc((const char*)a.s + so * SB, w_ok ? ((wrows - 1) * a.sr + srow) * SB : 0);
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(MODE ? (const void*)a.s : (const void*)(a.b + so), (w_ok && !MODE) ? ((wrows - 1) * a.sr + srow) * 2 : 0);
 
     const int64_t kt_all = (K + QB_T - 1) / QB_T;
     const int64_t kt0 = (int64_t)split * a.kts;
@@ -147,9 +199,14 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
                 for (int q = 0; q < 4; q++)
                     rwv[q] = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? (int)(woff + 4 * q) : (int)QB_DEAD, 0, 0);
             }
-            const uint32_t soff = ok ? (uint32_t)((n_t * a.sr + k0 / GS) * 2) : QB_DEAD;
-            rsv[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff, 0, 0);
-            rbv[0] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)soff, 0, 0);
+            const uint32_t soff = ok ? (uint32_t)((n_t * a.sr + k0 / GS) * SB) : QB_DEAD;
+            if constexpr (MODE) {
+                rsv[0] = __builtin_amdgcn_raw_buffer_load_b8(rs, (int)soff, 0, 0);
+                rbv[0] = 0;
+            } else {
+                rsv[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff, 0, 0);
+                rbv[0] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)soff, 0, 0);
+            }
         } else {
             const int64_t n = nt * QB_T + 4 * nq;
 #pragma unroll
@@ -167,9 +224,14 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
                     rwv[2 * j] = __builtin_amdgcn_raw_buffer_load_b32(rw, (int)woff, 0, 0);
                     rwv[2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? (int)(woff + 4) : (int)QB_DEAD, 0, 0);
                 }
-                const uint32_t soff = ok ? (uint32_t)((k * a.sr + n / GS) * 2) : QB_DEAD;
-                rsv[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff, 0, 0);
-                rbv[j] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)soff, 0, 0);
+                const uint32_t soff = ok ? (uint32_t)((k * a.sr + n / GS) * SB) : QB_DEAD;
+                if constexpr (MODE) {
+                    rsv[j] = __builtin_amdgcn_raw_buffer_load_b8(rs, (int)soff, 0, 0);
+                    rbv[j] = 0;
+                } else {
+                    rsv[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff, 0, 0);
+                    rbv[j] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)soff, 0, 0);
+                }
             }
         }
     };
@@ -197,12 +259,13 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
             *(u32x4*)&As[xrow * QB_LD + 16 * xc + 8 * h] = v;
         }
         if constexpr (TRANS) {
-            const float sc = bf16_to_f32((uint16_t)rsv[0]), bi = bf16_to_f32((uint16_t)rbv[0]);
+            const float sc = MODE ? qb_e8m0(rsv[0] & 0xffu) : bf16_to_f32((uint16_t)rsv[0]);
+            const float bi = MODE ? 0.0f : bf16_to_f32((uint16_t)rbv[0]);
             float q[16];
             if constexpr (WORD_ALIGNED) {
                 constexpr int CPW = 32 / BITS;
 #pragma unroll
-                for (int i = 0; i < 16; i++) q[i] = qb_code(rwv[i / CPW], i % CPW, BITS);
+                for (int i = 0; i < 16; i++) q[i] = qb_elem<MODE>(qb_code(rwv[i / CPW], i % CPW, BITS));
             } else {
                 // the run's bit stream shifted to bit 0, then fields at i * BITS
                 const uint32_t r0 = __builtin_amdgcn_alignbit(rwv[1], rwv[0], wsh);
@@ -230,12 +293,13 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
             float v[4][4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float sc = bf16_to_f32((uint16_t)rsv[j]), bi = bf16_to_f32((uint16_t)rbv[j]);
+                const float sc = MODE ? qb_e8m0(rsv[j] & 0xffu) : bf16_to_f32((uint16_t)rsv[j]);
+                const float bi = MODE ? 0.0f : bf16_to_f32((uint16_t)rbv[j]);
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
                     float q;
                     if constexpr (WORD_ALIGNED) {
-                        q = qb_code(rwv[j], c, BITS);
+                        q = qb_elem<MODE>(qb_code(rwv[j], c, BITS));
                     } else {
                         const uint32_t r = __builtin_amdgcn_alignbit(rwv[2 * j + 1], rwv[2 * j], wsh);
                         q = (float)((r >> (c * BITS)) & ((1u << BITS) - 1u));
@@ -489,18 +553,22 @@ static size_t batched_partial_bytes(const QbPlan& q, int64_t M, int64_t N) {
     return q.S > 1 ? (size_t)q.S * q.P * M * N * 4 : 0;
 }
 
-template <int B_, int G_, bool T_>
+template <int B_, int G_, bool T_, int M_>
 static void launch_qb(const QbArgs& a, dim3 grid, hipStream_t st) {
-    qmm_batched_kernel<B_, G_, T_><<<grid, 256, 0, st>>>(a);
+    qmm_batched_kernel<B_, G_, T_, M_><<<grid, 256, 0, st>>>(a);
 }
 
 #define KMI_QB_CASE(B_, G_, T_) \
-    if (bits == B_ && gs == G_ && trans == T_) { launch_qb<B_, G_, T_>(a, grid, st); return OK; }
+    if (mode == 0 && bits == B_ && gs == G_ && trans == T_) { launch_qb<B_, G_, T_, 0>(a, grid, st); return OK; }
 #define KMI_QB_G(B_, T_) KMI_QB_CASE(B_, 32, T_) KMI_QB_CASE(B_, 64, T_) KMI_QB_CASE(B_, 128, T_)
 #define KMI_QB_B(B_) KMI_QB_G(B_, true) KMI_QB_G(B_, false)
 
-static int launch_batched(const QbArgs& a, int bits, int gs, bool trans, dim3 grid, hipStream_t st) {
+static int launch_batched(const QbArgs& a, int mode, int bits, int gs, bool trans, dim3 grid, hipStream_t st) {
     KMI_QB_B(4) KMI_QB_B(8) KMI_QB_B(2) KMI_QB_B(3) KMI_QB_B(5) KMI_QB_B(6)
+    if (mode == 1 && trans) { launch_qb<4, 32, true, 1>(a, grid, st); return OK; }
+    if (mode == 1 && !trans) { launch_qb<4, 32, false, 1>(a, grid, st); return OK; }
+    if (mode == 2 && trans) { launch_qb<8, 32, true, 2>(a, grid, st); return OK; }
+    if (mode == 2 && !trans) { launch_qb<8, 32, false, 2>(a, grid, st); return OK; }
     set_error("quantized_matmul (batched): no kernel for bits=%d gs=%d", bits, gs);
     return EINVAL_ARG;
 }
@@ -531,10 +599,17 @@ size_t kmi_qmm_batched_workspace_bytes(int nd, const int64_t* batch_shape, int64
 int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, const int64_t* w_strides,
                     const void* scales, const void* biases, const int64_t* s_strides, int nd,
                     const int64_t* batch_shape, int64_t M, int64_t K, int64_t N, int transpose, int dtype,
-                    int group_size, int bits, float x_scale, void* y, int64_t ldy, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+                    int group_size, int bits, int mode, const int32_t* widx, const int32_t* xidx, int64_t nw,
+                    int64_t nx, float x_scale, void* y, int64_t ldy, void* workspace, size_t workspace_bytes,
+                    void* stream) {
     clear_error();
     KMI_CHECK_ARG(dtype == BF16, "quantized_matmul (batched): only bfloat16 is supported (got dtype %d)", dtype);
+    KMI_CHECK_ARG(mode == 0 || (mode == 1 && bits == 4 && group_size == 32) ||
+                      (mode == 2 && bits == 8 && group_size == 32),
+                  "quantized_matmul (batched): mode %d with %d bits / group %d (mxfp4: 4 / 32, mxfp8: 8 / 32)",
+                  mode, bits, group_size);
+    KMI_CHECK_ARG(!(widx || xidx) || (widx && nd == 1 && nw >= 1 && nx >= 1),
+                  "quantized_matmul (batched): the gather form takes widx, one batch dimension, nw, nx >= 1");
     KMI_CHECK_ARG(bits >= 2 && bits <= 8 && bits != 7, "quantized_matmul (batched): bits %d not in {2,3,4,5,6,8}",
                   bits);
     KMI_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
@@ -554,7 +629,7 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
                       "quantized_matmul (batched): negative batch size or stride (dimension %d)", d);
     const int64_t P = batch_count(nd, batch_shape);
     if (M == 0 || P == 0) return OK;
-    KMI_CHECK_ARG(x && w && scales && biases && y, "quantized_matmul (batched): null pointer");
+    KMI_CHECK_ARG(x && w && scales && (biases || mode) && y, "quantized_matmul (batched): null pointer");
     const int64_t xr = x_strides[nd], wr = w_strides[nd], sr = s_strides[nd];
     const int64_t wrow_words = grouped * bits / 32, wrows = transpose ? N : K;
     KMI_CHECK_ARG(xr >= K && xr % 8 == 0 && ((uintptr_t)x & 15) == 0,
@@ -566,7 +641,7 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
                       (long long)x_strides[d]);
     // 32-bit buffer offsets within one batch entry
     KMI_CHECK_ARG(((M - 1) * xr + ((K + 7) & ~7LL)) * 2 < (1LL << 31) && ((wrows - 1) * wr + wrow_words) * 4 < (1LL << 31) &&
-                      ((wrows - 1) * sr + grouped / group_size) * 2 < (1LL << 31),
+                      ((wrows - 1) * sr + grouped / group_size) * (mode ? 1 : 2) < (1LL << 31),
                   "quantized_matmul (batched): one batch entry exceeds 2 GB");
     if (transpose && (bits == 4 || bits == 8)) {
         // 16-byte (8-bit) / 8-byte (4-bit) weight loads along a row
@@ -597,9 +672,10 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
     a.P = P; a.mtiles = (int)q.mtiles; a.S = q.S; a.kts = q.kts;
     a.scale_x = x_scale != 1.0f;
     a.x_scale = x_scale;
+    a.widx = widx; a.xidx = xidx; a.nw = nw; a.nx = nx;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)q.ntiles, (unsigned)(q.mtiles * q.S), (unsigned)P);
-    int rc = launch_batched(a, bits, group_size, transpose != 0, grid, st);
+    int rc = launch_batched(a, mode, bits, group_size, transpose != 0, grid, st);
     if (rc) return rc;
     KMI_CHECK_LAUNCH("quantized_matmul (batched)");
     if (q.S > 1) {

@@ -43,9 +43,26 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
-def _check_mode(mode: str):
-    if mode != "affine":
-        raise ValueError(f"mode {mode!r}: only 'affine' is implemented")
+#: quantization modes: affine, and the scaled (microscaling) ones the
+#: reference's loader maps bias-less layers to (packed.py:20)
+MODE_CODE = {"affine": 0, "mxfp4": 1, "mxfp8": 2}
+_MX_BITS = {"mxfp4": 4, "mxfp8": 8}
+
+
+def _check_mode(mode: str, allow_mx: bool = False):
+    if mode == "affine" or (allow_mx and mode in _MX_BITS):
+        return
+    raise ValueError(f"mode {mode!r}: {'affine, mxfp4 and mxfp8 are' if allow_mx else 'only affine is'} "
+                     "implemented here")
+
+
+def _check_mx(what, scales, biases, group_size, bits, mode):
+    if biases is not None:
+        raise ValueError(f"{what}: {mode} has no biases")
+    if scales.dtype != torch.uint8:
+        raise ValueError(f"{what}: {mode} scales are uint8 E8M0 exponents (got {scales.dtype})")
+    if group_size != 32 or bits != _MX_BITS[mode]:
+        raise ValueError(f"{what}: {mode} takes group_size 32 and {_MX_BITS[mode]} bits")
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor | None:
@@ -90,8 +107,23 @@ def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | Non
                group_size: int = 64, bits: int = 4, mode: str = "affine",
                dtype: torch.dtype | None = None, rounding: int = ROUND_OP_BY_OP):
     """``mx.dequantize``: scale * q + bias in ``dtype`` (default: scales'
-    dtype).  ``rounding`` picks the storage rounding order."""
-    _check_mode(mode)
+    dtype).  ``rounding`` picks the storage rounding order.  mxfp4 / mxfp8:
+    element * 2^(scale - 127), uint8 E8M0 scales, no biases (default dtype
+    bfloat16)."""
+    _check_mode(mode, allow_mx=True)
+    if mode != "affine":
+        _check_mx("dequantize", scales, biases, group_size, bits, mode)
+        _on_gpu(w, scales)
+        out_dtype = dtype or torch.bfloat16
+        cols = w.shape[-1] * 32 // bits
+        if scales.shape[:-1] != w.shape[:-1] or scales.shape[-1] * 32 != cols:
+            raise ValueError(f"dequantize: shapes {tuple(w.shape)}, scales {tuple(scales.shape)} ({mode})")
+        wc, sc = w.contiguous(), scales.contiguous()
+        rows = wc.numel() // wc.shape[-1] if wc.shape[-1] else 0
+        out = torch.empty(*w.shape[:-1], cols, dtype=out_dtype, device=w.device)
+        _abi.check(_lib().kmi_dequantize_mx(_ptr(wc), _ptr(sc), rows, cols, MODE_CODE[mode], _ptr(out),
+                                            DTYPE_CODE[out_dtype], _stream(w)), "dequantize")
+        return out
     if biases is None:
         raise ValueError("dequantize: affine mode needs biases")
     _on_gpu(w, scales, biases)
@@ -147,9 +179,9 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     What at 4 or 8 bits with transpose=True is the dense projection
     (kmi_qmm); a batched What (leading dimensions broadcast against x's),
     transpose=False or the 2, 3, 5 and 6-bit widths run kmi_qmm_batched."""
-    _check_mode(mode)
-    if not transpose or w.ndim != 2 or bits not in (4, 8):
-        return qmm_batched(x, w, scales, biases, transpose, group_size, bits)
+    _check_mode(mode, allow_mx=True)
+    if not transpose or w.ndim != 2 or bits not in (4, 8) or mode != "affine":
+        return qmm_batched(x, w, scales, biases, transpose, group_size, bits, mode=mode)
     _check_affine_operands(x, w, scales, biases, group_size, bits, "quantized_matmul")
     K = x.shape[-1]
     N = w.shape[0]
@@ -228,18 +260,26 @@ def row_padded(t: torch.Tensor) -> bool:
 
 
 def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 64,
-                bits: int = 4, x_scale: float = 1.0, out=None):
+                bits: int = 4, x_scale: float = 1.0, out=None, mode: str = "affine"):
     """mx.quantized_matmul with batch dimensions on w (broadcast against
     x's) in either orientation; ``x_scale`` != 1 multiplies x by it first,
     rounded to x's dtype (mlx-lm's ``queries *= scale``).  ``out``: a
     [batch..., M, N] bf16 tensor with rows otherwise contiguous (a row
-    padding is allowed) to write into."""
+    padding is allowed) to write into.  ``mode`` mxfp4 / mxfp8: uint8 E8M0
+    scales, no biases."""
     what = "quantized_matmul"
-    if biases is None:
-        raise ValueError(f"{what}: affine mode needs biases")
-    _on_gpu(x, w, scales, biases)
-    if x.dtype != torch.bfloat16 or scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
-        raise ValueError(f"{what}: only bfloat16 activations, scales and biases are implemented")
+    _check_mode(mode, allow_mx=True)
+    if mode != "affine":
+        _check_mx(what, scales, biases, group_size, bits, mode)
+        _on_gpu(x, w, scales)
+        if x.dtype != torch.bfloat16:
+            raise ValueError(f"{what}: only bfloat16 activations are implemented")
+    else:
+        if biases is None:
+            raise ValueError(f"{what}: affine mode needs biases")
+        _on_gpu(x, w, scales, biases)
+        if x.dtype != torch.bfloat16 or scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
+            raise ValueError(f"{what}: only bfloat16 activations, scales and biases are implemented")
     if w.dtype not in (torch.uint32, torch.int32) or w.ndim < 2:
         raise ValueError(f"{what}: w must be packed uint32 with at least 2 dimensions")
     if bits not in (2, 3, 4, 5, 6, 8) or group_size not in (32, 64, 128):
@@ -256,9 +296,10 @@ def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 
         grouped = N
     if Kw != K:
         raise ValueError(f"{what}: x has {K} features but w holds {Kw} (transpose={transpose})")
-    if scales.shape != biases.shape or scales.shape[:-1] != w.shape[:-1] \
+    if (biases is not None and scales.shape != biases.shape) or scales.shape[:-1] != w.shape[:-1] \
             or scales.shape[-1] * group_size != grouped:
-        raise ValueError(f"{what}: scales {tuple(scales.shape)} / biases {tuple(biases.shape)} "
+        raise ValueError(f"{what}: scales {tuple(scales.shape)} / biases "
+                         f"{None if biases is None else tuple(biases.shape)} "
                          f"do not match w {tuple(w.shape)} at group {group_size}")
     M = x.shape[-2]
     try:
@@ -282,12 +323,13 @@ def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 
         w = w.contiguous()
         if w.data_ptr() % 16:
             w = w.clone()
-    if scales.stride() != biases.stride() or scales.stride(-1) != 1:
-        scales, biases = scales.contiguous(), biases.contiguous()
+    if (biases is not None and scales.stride() != biases.stride()) or scales.stride(-1) != 1:
+        scales = scales.contiguous()
+        biases = biases.contiguous() if biases is not None else None
     xe = x.expand(*batch, M, K)
     we = w.expand(*batch, *w.shape[-2:])
     se = scales.expand(*batch, *scales.shape[-2:])
-    be = biases.expand(*batch, *biases.shape[-2:])
+    be = biases.expand(*batch, *biases.shape[-2:]) if biases is not None else None
     nb = len(batch)
     dims, Mf = _fold(batch, [(xe.stride(d), we.stride(d), se.stride(d)) for d in range(nb)],
                      M, xe.stride(-2))
@@ -304,8 +346,44 @@ def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 
     _abi.check(L.kmi_qmm_batched(
         _ptr(xe), xs.data_ptr(), _ptr(we), ws_.data_ptr(), _ptr(se), _ptr(be), ss.data_ptr(), nd,
         shape.data_ptr(), Mf, K, N, int(bool(transpose)), DTYPE_CODE[x.dtype], group_size, bits,
-        float(x_scale), _ptr(y), y.stride(-2), _ptr(ws), nbytes, _stream(x)), what)
+        MODE_CODE[mode], None, None, 0, 0, float(x_scale), _ptr(y), y.stride(-2), _ptr(ws), nbytes, _stream(x)),
+        what)
     return y[0] if vec else y
+
+
+def _gather_batched(x, w, scales, lhs, rhs, ishape, transpose, group_size, bits, mode):
+    """mx.gather_qmm in the scaled modes: kmi_qmm_batched's gather form, one
+    batch entry per (lhs, rhs) pair."""
+    what = "gather_qmm"
+    M, K = x.shape[-2], x.shape[-1]
+    E = math.prod(w.shape[:-2])
+    wc = w.reshape(E, *w.shape[-2:]).contiguous()
+    sc = scales.reshape(E, *scales.shape[-2:]).contiguous()
+    if transpose:
+        N, Kw = wc.shape[1], wc.shape[2] * 32 // bits
+    else:
+        N, Kw = wc.shape[2] * 32 // bits, wc.shape[1]
+    if Kw != K or sc.shape[-1] * group_size != (K if transpose else N):
+        raise ValueError(f"{what}: x has {K} features; w {tuple(w.shape)}, scales {tuple(scales.shape)}")
+    xb = _aligned_rows(x.reshape(-1, M, K))
+    P = lhs.numel()
+    y = torch.empty(P, M, N, dtype=x.dtype, device=x.device)
+    if P == 0:
+        return y.reshape(*ishape, M, N)
+    if transpose and (wc.data_ptr() % 16 or wc.stride(1) % 4 or wc.stride(0) % 4):
+        raise ValueError(f"{what}: weight rows must be 16-byte aligned")
+    shape = torch.tensor([P], dtype=torch.int64)
+    xs = torch.tensor([xb.stride(0), xb.stride(1)], dtype=torch.int64)
+    ws_ = torch.tensor([wc.stride(0), wc.stride(1)], dtype=torch.int64)
+    ss = torch.tensor([sc.stride(0), sc.stride(1)], dtype=torch.int64)
+    L = _lib()
+    nbytes = L.kmi_qmm_batched_workspace_bytes(1, shape.data_ptr(), M, K, N)
+    ws = _workspace(nbytes, x.device)
+    _abi.check(L.kmi_qmm_batched(
+        _ptr(xb), xs.data_ptr(), _ptr(wc), ws_.data_ptr(), _ptr(sc), None, ss.data_ptr(), 1, shape.data_ptr(),
+        M, K, N, int(bool(transpose)), DTYPE_CODE[x.dtype], group_size, bits, MODE_CODE[mode], _ptr(rhs),
+        _ptr(lhs), E, xb.shape[0], 1.0, _ptr(y), N, _ptr(ws), nbytes, _stream(x)), what)
+    return y.reshape(*ishape, M, N)
 
 
 def _flat_indices(x, w, lhs_indices, rhs_indices):
@@ -335,12 +413,21 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     """``mx.gather_qmm``: out[i] = x[lhs[i]] @ What[rhs[i]]^T for x
     [..., M, K] and w [..., N, K*bits/32]; out [*broadcast(lhs, rhs), M, N].
     Rows are grouped by expert on the GPU whatever ``sorted_indices`` says,
-    so each routed expert's weights are read once."""
-    _check_mode(mode)
-    if not transpose:
-        raise ValueError("gather_qmm: transpose=False is not implemented")
+    so each routed expert's weights are read once.  The mxfp4 / mxfp8
+    modes (uint8 E8M0 scales, no biases) run the batched kernel's gather
+    form, either orientation."""
+    _check_mode(mode, allow_mx=True)
     if x.ndim < 2 or w.ndim < 3:
         raise ValueError("gather_qmm: x needs [..., M, K] and w [..., N, K*bits/32]")
+    if mode != "affine":
+        _check_mx("gather_qmm", scales, biases, group_size, bits, mode)
+        _on_gpu(x, w, scales)
+        if x.dtype != torch.bfloat16:
+            raise ValueError("gather_qmm: only bfloat16 activations are implemented")
+        lhs, rhs, ishape = _flat_indices(x, w, lhs_indices, rhs_indices)
+        return _gather_batched(x, w, scales, lhs, rhs, ishape, transpose, group_size, bits, mode)
+    if not transpose:
+        raise ValueError("gather_qmm: transpose=False is not implemented for the affine mode")
     _check_affine_operands(x, w, scales, biases, group_size, bits, "gather_qmm")
     M, K = x.shape[-2], x.shape[-1]
     N = w.shape[-2]

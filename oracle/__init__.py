@@ -29,6 +29,9 @@ sites, and pinned as follows (each function's docstring names its pins):
   The batched form (both orientations, broadcast batches) -- on-grid
   weights packed independently of the oracle, against a dense float64
   product.
+* mxfp4 / mxfp8 -- the OCP MX element and scale encodings, pinned by the
+  spec's known answers (E2M1 table, E4M3 extremes and NaN, E8M0 powers of
+  two).  How mlx orders the packed codes is its 4 / 8-bit affine order.
 * quantized attention (mlx-lm's base.py:260-302) -- float64 attention
   (``sdpa_numpy_f64``) within the bf16 roundings the path makes, and the
   exact uniform softmax of a fully hidden row.
@@ -325,6 +328,52 @@ def quantized_sdpa(q, K, V, scale: float, mask=None, group_size: int = 64, bits:
     p = bf16_round((e / e.sum(axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32))
     out = quantized_matmul_batched(p, *Ve, False, group_size, bits, "bfloat16")
     return out.reshape(B, Hq, L, -1)
+
+
+# --- the scaled (microscaling) modes -------------------------------------------
+
+#: OCP MX FP4 (E2M1) magnitudes of codes 0..7 (the spec's table); bit 3 is the sign
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def e4m3(codes) -> np.ndarray:
+    """OCP MX FP8 E4M3 (bias 7, no infinities, S.1111.111 = NaN) -> float64."""
+    c = np.asarray(codes, np.int64)
+    s = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 15
+    m = (c & 7).astype(np.float64)
+    v = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    v = np.where((e == 15) & (m == 7), np.nan, v)
+    return s * v
+
+
+def e8m0(scales) -> np.ndarray:
+    """OCP MX E8M0 scale: 2^(e - 127); 255 is NaN."""
+    e = np.asarray(scales, np.int64)
+    return np.where(e == 255, np.nan, np.exp2(e - 127.0))
+
+
+def mx_dequantize(wq, scales, mode: str) -> np.ndarray:
+    """mx.dequantize(mode="mxfp4" | "mxfp8") in float64: codes packed as mlx
+    packs 4 / 8-bit codes (``unpack_numpy``), one uint8 E8M0 scale per 32.
+    The scaled modes of the reference's loader (engine/model/packed.py:20,
+    load_model.py:153-173).  Pinned by the spec's known answers."""
+    bits = 4 if mode == "mxfp4" else 8
+    q = unpack_numpy(wq, bits).astype(np.int64)
+    if mode == "mxfp4":
+        v = np.where(q & 8, -1.0, 1.0) * E2M1[q & 7]
+    else:
+        v = e4m3(q)
+    return v * np.repeat(e8m0(scales), 32, axis=-1)
+
+
+def mx_quantized_matmul(x, wq, scales, mode: str, transpose: bool = True,
+                        out_dtype: str = "bfloat16"):
+    """mx.quantized_matmul(mode=mxfp4 | mxfp8) for a 2-D weight: the exact
+    product in float64, rounded once."""
+    w = mx_dequantize(wq, scales, mode)
+    y = np.asarray(x, np.float64) @ (w.T if transpose else w)
+    return round_to(y.astype(np.float32), out_dtype)
 
 
 # --- the Qwen3.5-MoE router, SwiGLU and SwitchGLU ----------------------------

@@ -116,7 +116,7 @@ def test_load_quantized_builds_each_layer_from_its_tensors(tmp_path):
     assert mods["lin"].bits == 4
 
 
-def test_a_declared_vq_entry_must_match_and_mx_modes_are_named(tmp_path):
+def test_a_declared_vq_entry_must_match_and_modes_are_read_off_the_tensors(tmp_path):
     g = torch.Generator().manual_seed(1)
     t = {"vq.codes": torch.zeros(2, 8, 22, dtype=torch.int32).view(torch.uint32),
          "vq.codebook": torch.randn(2048, 4, generator=g).half(),
@@ -133,9 +133,12 @@ def test_a_declared_vq_entry_must_match_and_mx_modes_are_named(tmp_path):
     from safetensors.torch import save_file
     save_file(t2, str(d2 / "model.safetensors"))
     (d2 / "config.json").write_text(json.dumps({"quantization": {"group_size": 32, "bits": 4,
-                                                                 "mode": "mxfp4"}}))
-    with pytest.raises(ValueError, match="mxfp4"):
+                                                                 "mode": "nvfp4"}}))
+    with pytest.raises(ValueError, match="nvfp4"):
         C.load_quantized(d2, device="cpu")
+    (d2 / "config.json").write_text(json.dumps({"quantization": {"group_size": 32, "bits": 4}}))
+    m = C.load_quantized(d2, device="cpu")["l"]
+    assert (m.mode, m.bits, m.group_size, m.biases) == ("mxfp4", 4, 32, None)
 
 
 def test_unpacked_short_vectors_are_repacked_exactly():

@@ -1,0 +1,124 @@
+"""GPU parity: the scaled modes mxfp4 / mxfp8 (E2M1 / E4M3 elements, one
+uint8 E8M0 scale per 32, no biases) -- dequantize, quantized_matmul (dense,
+batched, either orientation) and gather_qmm / QuantizedSwitchLinear --
+against the oracle's spec decoding, on the reference's own mxfp4 experts
+(tests/golden/deepseek_v4_tiny_mxfp4_experts.npz) and on random codes.
+Every mx value is exact in bf16, so dequantize is bit-exact; products meet
+max rel err 1e-2, cosine 0.9999."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import knurlogic_amd as K
+import oracle as O
+from knurlogic_amd import checkpoint as C
+from knurlogic_amd import nn
+from tests.util import assert_close, bf16_normal, to_numpy, to_torch, u32_to_torch
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def _fixture(dev):
+    z = np.load(GOLD / "deepseek_v4_tiny_mxfp4_experts.npz")
+    host = {p: (z[p + "__weight"], z[p + "__scales"]) for p in ("gate_proj", "up_proj", "down_proj")}
+    gpu = {p: (u32_to_torch(w, dev), torch.from_numpy(s).to(dev)) for p, (w, s) in host.items()}
+    return host, gpu
+
+
+def _random_mx(rng, shape_rows, cols, mode, dev):
+    bits = 4 if mode == "mxfp4" else 8
+    wq = rng.integers(0, 2 ** 32, shape_rows + (cols * bits // 32,), dtype=np.uint64).astype(np.uint32)
+    if mode == "mxfp8":
+        b = wq.view(np.uint8)
+        b[(b & 0x7F) == 0x7F] = 0x3F               # no NaN codes
+    sc = rng.integers(118, 124, shape_rows + (cols // 32,)).astype(np.uint8)
+    return (wq, sc), (u32_to_torch(wq, dev), torch.from_numpy(sc).to(dev))
+
+
+@pytest.mark.parametrize("out", [torch.bfloat16, torch.float32])
+def test_dequantize_the_references_mxfp4_experts_bit_exact(dev, out):
+    host, gpu = _fixture(dev)
+    for p in host:
+        got = K.dequantize(*gpu[p], None, 32, 4, mode="mxfp4", dtype=out)
+        assert np.array_equal(to_numpy(got), O.mx_dequantize(*host[p], "mxfp4").astype(np.float32))
+
+
+def test_dequantize_mxfp8_bit_exact(dev):
+    rng = np.random.default_rng(1)
+    h, g = _random_mx(rng, (8, 16), 128, "mxfp8", dev)
+    got = K.dequantize(*g, None, 32, 8, mode="mxfp8", dtype=torch.float32)
+    assert np.array_equal(to_numpy(got), O.mx_dequantize(*h, "mxfp8").astype(np.float32))
+
+
+def test_switch_layers_on_the_references_mxfp4_experts(dev):
+    """QuantizedSwitchLinear(mode="mxfp4") over the fixture's experts: the
+    gather of each token's routed experts, gate / up / down."""
+    host, gpu = _fixture(dev)
+    rng = np.random.default_rng(2)
+    T, k = 5, 2
+    inds = np.stack([rng.choice(4, k, replace=False) for _ in range(T)]).astype(np.int32)
+    x = bf16_normal(rng, (T, 1, 1, 64))
+    for p, K_in in (("gate_proj", 64), ("up_proj", 64)):
+        lin = nn.QuantizedSwitchLinear(*gpu[p], None, None, 32, 4, "mxfp4")
+        got = lin(to_torch(x, dev, BF), torch.from_numpy(inds).to(dev))         # [T, 1, k, 1, N]
+        w, s = host[p]
+        ref = np.stack([[O.mx_quantized_matmul(x[t, 0], w[e], s[e], "mxfp4", True, "float32")
+                         for e in inds[t]] for t in range(T)])
+        assert_close(to_numpy(got).reshape(ref.shape), ref, what=p)
+    act = bf16_normal(rng, (T, k, 1, 32))
+    down = nn.QuantizedSwitchLinear(*gpu["down_proj"], None, None, 32, 4, "mxfp4")
+    got = down(to_torch(act, dev, BF), torch.from_numpy(inds).to(dev))
+    w, s = host["down_proj"]
+    ref = np.stack([[O.mx_quantized_matmul(act[t, j], w[inds[t, j]], s[inds[t, j]], "mxfp4", True, "float32")
+                     for j in range(k)] for t in range(T)])
+    assert_close(to_numpy(got).reshape(ref.shape), ref, what="down")
+
+
+@pytest.mark.parametrize("mode", ["mxfp4", "mxfp8"])
+@pytest.mark.parametrize("transpose", [True, False])
+@pytest.mark.parametrize("M", [1, 70])
+def test_quantized_matmul_mx(dev, mode, transpose, M):
+    rng = np.random.default_rng(M + (mode == "mxfp8"))
+    K_, N = 256, 192
+    h, g = _random_mx(rng, (N,) if transpose else (K_,), K_ if transpose else N, mode, dev)
+    x = bf16_normal(rng, (M, K_))
+    got = K.quantized_matmul(to_torch(x, dev, BF), *g[:1], g[1], None, transpose, 32, 4 if mode == "mxfp4" else 8,
+                             mode)
+    ref = O.mx_quantized_matmul(x, *h, mode, transpose, "float32")
+    assert_close(to_numpy(got), ref, what=f"{mode} transpose={transpose} M={M}")
+
+
+def test_gather_with_a_bad_expert_gives_a_zero_row(dev):
+    host, gpu = _fixture(dev)
+    x = to_torch(bf16_normal(np.random.default_rng(3), (2, 1, 64)), dev, BF)
+    rhs = torch.tensor([1, 7], dtype=torch.int32, device=dev)
+    y = K.gather_qmm(x, *gpu["gate_proj"], None, rhs_indices=rhs, group_size=32, bits=4, mode="mxfp4")
+    assert y.shape == (2, 1, 32) and not y[1].any() and y[0].abs().sum() > 0
+
+
+def test_mx_checkpoint_layers_load_and_run(dev, tmp_path):
+    """The fixture's experts written as an mlx-format file (no biases, no
+    config): the loader reads them as mxfp4 off the tensors."""
+    from safetensors.torch import save_file
+    host, _ = _fixture("cpu")
+    t = {}
+    for p, (w, s) in host.items():
+        t[f"switch_mlp.{p}.weight"] = torch.from_numpy(w.view(np.int32)).view(torch.uint32)
+        t[f"switch_mlp.{p}.scales"] = torch.from_numpy(s)
+    d = tmp_path / "art"
+    d.mkdir()
+    save_file(t, str(d / "model.safetensors"), metadata={"format": "mlx"})
+    shapes = {"switch_mlp.gate_proj": (4, 32, 64), "switch_mlp.up_proj": (4, 32, 64),
+              "switch_mlp.down_proj": (4, 64, 32)}
+    mods = C.load_quantized(d, shapes=shapes, device=dev)
+    g = mods["switch_mlp.gate_proj"]
+    assert (g.mode, g.bits, g.group_size) == ("mxfp4", 4, 32)
+    x = bf16_normal(np.random.default_rng(4), (1, 1, 64))
+    got = g(to_torch(x, dev, BF), torch.tensor([2], dtype=torch.int32, device=dev))
+    w, s = host["gate_proj"]
+    assert_close(to_numpy(got).reshape(-1), O.mx_quantized_matmul(x[0], w[2], s[2], "mxfp4", True,
+                                                                  "float32").reshape(-1), what="loaded mxfp4")

@@ -383,6 +383,37 @@ def test_quantized_sdpa_hidden_row_is_the_plain_mean_of_v():
         assert np.array_equal(got[0, h, 1], want[0, h // 2])
 
 
+# --- mxfp4 / mxfp8 ------------------------------------------------------------------
+
+def test_mx_element_encodings_are_the_ocp_spec():
+    """Known answers of the OCP Microscaling spec: the E2M1 values, E4M3's
+    largest normal (S.1111.110 = 448), smallest normal (2^-6) and
+    subnormal (2^-9), its NaN, and E8M0 = 2^(e - 127)."""
+    q = np.arange(16, dtype=np.uint32)
+    word = np.zeros((1, 2), np.uint32)
+    for j in range(16):
+        word[0, j // 8] |= np.uint32(int(q[j]) << (4 * (j % 8)))
+    v = O.mx_dequantize(np.tile(word, (1, 2)), np.array([[127]], np.uint8), "mxfp4")[0, :16]
+    assert v.tolist() == [0, .5, 1, 1.5, 2, 3, 4, 6, -0.0, -.5, -1, -1.5, -2, -3, -4, -6]
+    assert O.e4m3([0x7E, 0x08, 0x01, 0xFE, 0x38])[:5].tolist() == [448.0, 2.0 ** -6, 2.0 ** -9, -448.0, 1.0]
+    assert np.isnan(O.e4m3([0x7F])[0]) and np.isnan(O.e4m3([0xFF])[0])
+    assert O.e8m0([127, 128, 0]).tolist() == [1.0, 2.0, 2.0 ** -127] and np.isnan(O.e8m0([255])[0])
+
+
+def test_mx_matmul_equals_the_decoded_product():
+    rng = np.random.default_rng(5)
+    for mode, bits in (("mxfp4", 4), ("mxfp8", 8)):
+        wq = rng.integers(0, 2 ** 32, (16, 64 * bits // 32), dtype=np.uint64).astype(np.uint32)
+        if mode == "mxfp8":                      # no NaN codes
+            b = wq.view(np.uint8)
+            b[(b & 0x7F) == 0x7F] = 0
+        sc = rng.integers(120, 134, (16, 2)).astype(np.uint8)
+        x = bf16_normal(rng, (3, 64))
+        ref = x.astype(np.float64) @ O.mx_dequantize(wq, sc, mode).T
+        got = O.mx_quantized_matmul(x, wq, sc, mode, True, "float32")
+        assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+
+
 # --- packed VQ codes ------------------------------------------------------------------
 
 def _pack_fields_bitwise(codes, bits):
@@ -448,3 +479,18 @@ def test_vq_matmul_equals_decode_then_dense(code_dtype, kc):
     o, i = 3, 17
     assert np.isclose(O.vq_decode_numpy(codes, cb, sc)[o, i],
                       sc[o] * cb[codes[o, i // dim], i % dim])
+
+
+def test_the_references_mxfp4_experts_decode_as_the_spec_quantizes():
+    """The reference's tiny DeepSeek-V4 checkpoint (mlx-format, mxfp4
+    experts; tests/golden/make_mxfp4_fixture.py): per the OCP scheme each
+    group's shared exponent is floor(log2 max|w|) - 2, so its largest
+    element magnitude is 4 or 6 (codes 6, 7), and all values are finite."""
+    z = np.load(GOLD / "deepseek_v4_tiny_mxfp4_experts.npz")
+    for p in ("gate_proj", "up_proj", "down_proj"):
+        w, s = z[p + "__weight"], z[p + "__scales"]
+        v = O.mx_dequantize(w, s, "mxfp4")
+        assert np.isfinite(v).all()
+        elem = v / np.repeat(O.e8m0(s), 32, axis=-1)
+        gmax = np.abs(elem).reshape(*elem.shape[:-1], -1, 32).max(-1)
+        assert set(np.unique(gmax).tolist()) <= {4.0, 6.0}
