@@ -99,16 +99,22 @@ __device__ __forceinline__ uint32_t qb_code(uint32_t word, int i, int bits) {
     return (word >> (bits * i)) & ((1u << bits) - 1u);
 }
 
-template <int BITS, int GS, bool TRANS, int MODE>
+// MB: 16-row blocks per output tile (1, 2 or 4): a tile is 16 MB rows x 64
+// columns; the four waves cover it as WM x WN, each IM x JN MFMA blocks
+// (few activation rows -- attention's GQA heads x queries -- take narrow
+// tiles, so no MFMA or LDS work goes to rows that do not exist).
+template <int BITS, int GS, bool TRANS, int MODE, int MB>
 __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
+    constexpr int BM = 16 * MB;
+    constexpr int WM = MB == 1 ? 1 : 2, WN = 4 / WM, IM = MB / WM, JN = 4 / WN;
     // one LDS stage (27 KB: five workgroups per CU); the next k-tile's
     // global loads are in flight in registers while this one is multiplied
-    __shared__ __align__(16) uint16_t As[QB_T * QB_LD];
+    __shared__ __align__(16) uint16_t As[BM * QB_LD];
     __shared__ __align__(16) uint16_t Bh[QB_T * QB_LD];     // hi parts of the dequantized weight
     __shared__ __align__(16) uint16_t Bl[QB_T * QB_LD];     // lo parts
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
 
     const int64_t p = blockIdx.z;
     const int mt = (int)(blockIdx.y % a.mtiles), split = (int)(blockIdx.y / a.mtiles);
@@ -157,7 +163,8 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
 
     // staging coordinates: x row xrow, k run [16 xc, 16 xc + 16) of the tile
     const int xrow = tid >> 2, xc = tid & 3;
-    const int64_t m_x = (int64_t)mt * QB_T + xrow;
+    const int64_t m_x = (int64_t)mt * BM + xrow;
+    const bool x_row = xrow < BM;                 // this thread stages x (whole waves)
     // weight: TRANS -- row n = wrow_t of the tile, codes [16 xc, +16) of k;
     //         !TRANS -- rows k = 4 kq .. 4 kq + 3, columns n = 4 nq .. 4 nq + 3
     const int kq = tid >> 4, nq = tid & 15;
@@ -180,8 +187,8 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int64_t k = k0 + 8 * h;
-            const uint32_t off = (m_x < M && k < K) ? (uint32_t)((m_x * a.xr + k) * 2) : QB_DEAD;
-            rxv[h] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+            const uint32_t off = (x_row && m_x < M && k < K) ? (uint32_t)((m_x * a.xr + k) * 2) : QB_DEAD;
+            rxv[h] = x_row ? __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0) : u32x4{0u, 0u, 0u, 0u};
         }
         if constexpr (TRANS) {
             const bool ok = n_t < N && k0 < K;
@@ -256,7 +263,7 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
                                    bf16_to_f32((uint16_t)(u >> 16)) * a.x_scale);
                 }
             }
-            *(u32x4*)&As[xrow * QB_LD + 16 * xc + 8 * h] = v;
+            if (x_row) *(u32x4*)&As[xrow * QB_LD + 16 * xc + 8 * h] = v;
         }
         if constexpr (TRANS) {
             const float sc = MODE ? qb_e8m0(rsv[0] & 0xffu) : bf16_to_f32((uint16_t)rsv[0]);
@@ -318,27 +325,29 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
         }
     };
 
-    f32x4 acc[2][2];
+    f32x4 acc[IM][JN];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < IM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < JN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int fr = lane & 15, fk = 8 * (lane >> 4);
     auto compute = [&]() {
 #pragma unroll
         for (int kk = 0; kk < QB_T; kk += 32) {
-            u32x4 A[2], H[2], Lo[2];
+            u32x4 A[IM], H[JN], Lo[JN];
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                A[i] = *(const u32x4*)&As[(32 * wm + 16 * i + fr) * QB_LD + kk + fk];
-                H[i] = *(const u32x4*)&Bh[(32 * wn + 16 * i + fr) * QB_LD + kk + fk];
-                Lo[i] = *(const u32x4*)&Bl[(32 * wn + 16 * i + fr) * QB_LD + kk + fk];
+            for (int i = 0; i < IM; i++)
+                A[i] = *(const u32x4*)&As[(16 * IM * wm + 16 * i + fr) * QB_LD + kk + fk];
+#pragma unroll
+            for (int j = 0; j < JN; j++) {
+                H[j] = *(const u32x4*)&Bh[(16 * JN * wn + 16 * j + fr) * QB_LD + kk + fk];
+                Lo[j] = *(const u32x4*)&Bl[(16 * JN * wn + 16 * j + fr) * QB_LD + kk + fk];
             }
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < IM; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
+                for (int j = 0; j < JN; j++) {
                     acc[i][j] = mfma16x16x32(A[i], Lo[j], acc[i][j]);
                     acc[i][j] = mfma16x16x32(A[i], H[j], acc[i][j]);
                 }
@@ -356,14 +365,14 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
     }
 
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < IM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int64_t n = nt * QB_T + 32 * wn + 16 * j + fr;
+        for (int j = 0; j < JN; j++) {
+            const int64_t n = nt * QB_T + 16 * JN * wn + 16 * j + fr;
             if (n >= N) continue;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int64_t m = (int64_t)mt * QB_T + 32 * wm + 16 * i + 4 * (lane >> 4) + e;
+                const int64_t m = (int64_t)mt * BM + 16 * IM * wm + 16 * i + 4 * (lane >> 4) + e;
                 if (m >= M) continue;
                 if (a.S == 1)
                     a.y[(p * M + m) * a.ldy + n] = f32_to_bf16(acc[i][j][e]);
@@ -529,16 +538,20 @@ __global__ __launch_bounds__(256) void masked_softmax_kernel(SmArgs a) {
 
 struct QbPlan {
     int64_t P, mtiles, ntiles;
-    int S, kts;
+    int S, kts, mb;
 };
 
-static QbPlan plan_batched(int64_t P, int64_t M, int64_t K, int64_t N) {
+// narrow: whether 32-row tiles exist for the width (4 and 8 bits)
+static QbPlan plan_batched(int64_t P, int64_t M, int64_t K, int64_t N, bool narrow = true) {
     QbPlan q;
     q.P = P;
-    q.mtiles = ceil_div(M, QB_T);
+    q.mb = M <= 16 ? 1 : (M <= 32 && narrow) ? 2 : 4;
+    q.mtiles = ceil_div(M, 16 * q.mb);
     q.ntiles = ceil_div(N, QB_T);
     const int64_t kt_all = ceil_div(K, QB_T);
-    const int64_t tiles = q.mtiles * q.ntiles * P;
+    // the K split depends on 64-row tiles only (so the workspace size does
+    // not depend on the tile shape)
+    const int64_t tiles = ceil_div(M, QB_T) * q.ntiles * P;
     // split K while the grid is short of four workgroups per CU and each
     // split keeps at least 4 k-tiles
     int64_t S = 1;
@@ -554,21 +567,24 @@ static size_t batched_partial_bytes(const QbPlan& q, int64_t M, int64_t N) {
 }
 
 template <int B_, int G_, bool T_, int M_>
-static void launch_qb(const QbArgs& a, dim3 grid, hipStream_t st) {
-    qmm_batched_kernel<B_, G_, T_, M_><<<grid, 256, 0, st>>>(a);
+static void launch_qb(const QbArgs& a, int mb, dim3 grid, hipStream_t st) {
+    if (mb == 1) qmm_batched_kernel<B_, G_, T_, M_, 1><<<grid, 256, 0, st>>>(a);
+    else if (mb == 2 && (B_ == 4 || B_ == 8)) qmm_batched_kernel<B_, G_, T_, M_, (B_ == 4 || B_ == 8) ? 2 : 4><<<grid, 256, 0, st>>>(a);
+    else qmm_batched_kernel<B_, G_, T_, M_, 4><<<grid, 256, 0, st>>>(a);
 }
 
 #define KMI_QB_CASE(B_, G_, T_) \
-    if (mode == 0 && bits == B_ && gs == G_ && trans == T_) { launch_qb<B_, G_, T_, 0>(a, grid, st); return OK; }
+    if (mode == 0 && bits == B_ && gs == G_ && trans == T_) { launch_qb<B_, G_, T_, 0>(a, mb, grid, st); return OK; }
 #define KMI_QB_G(B_, T_) KMI_QB_CASE(B_, 32, T_) KMI_QB_CASE(B_, 64, T_) KMI_QB_CASE(B_, 128, T_)
 #define KMI_QB_B(B_) KMI_QB_G(B_, true) KMI_QB_G(B_, false)
 
-static int launch_batched(const QbArgs& a, int mode, int bits, int gs, bool trans, dim3 grid, hipStream_t st) {
+static int launch_batched(const QbArgs& a, int mode, int bits, int gs, bool trans, int mb, dim3 grid,
+                          hipStream_t st) {
     KMI_QB_B(4) KMI_QB_B(8) KMI_QB_B(2) KMI_QB_B(3) KMI_QB_B(5) KMI_QB_B(6)
-    if (mode == 1 && trans) { launch_qb<4, 32, true, 1>(a, grid, st); return OK; }
-    if (mode == 1 && !trans) { launch_qb<4, 32, false, 1>(a, grid, st); return OK; }
-    if (mode == 2 && trans) { launch_qb<8, 32, true, 2>(a, grid, st); return OK; }
-    if (mode == 2 && !trans) { launch_qb<8, 32, false, 2>(a, grid, st); return OK; }
+    if (mode == 1 && trans) { launch_qb<4, 32, true, 1>(a, mb, grid, st); return OK; }
+    if (mode == 1 && !trans) { launch_qb<4, 32, false, 1>(a, mb, grid, st); return OK; }
+    if (mode == 2 && trans) { launch_qb<8, 32, true, 2>(a, mb, grid, st); return OK; }
+    if (mode == 2 && !trans) { launch_qb<8, 32, false, 2>(a, mb, grid, st); return OK; }
     set_error("quantized_matmul (batched): no kernel for bits=%d gs=%d", bits, gs);
     return EINVAL_ARG;
 }
@@ -650,7 +666,7 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
         KMI_CHECK_ARG(al, "quantized_matmul (batched): weight rows must be 16-byte aligned");
     }
     KMI_CHECK_ARG(ldy >= N, "quantized_matmul (batched): output row stride %lld < N", (long long)ldy);
-    const QbPlan q = plan_batched(P, M, K, N);
+    const QbPlan q = plan_batched(P, M, K, N, bits == 4 || bits == 8);
     KMI_CHECK_ARG(q.mtiles * q.S < 65536 && P < 65536 && q.ntiles < (1LL << 31),
                   "quantized_matmul (batched): grid too large (M=%lld, batch %lld)", (long long)M, (long long)P);
     const size_t need = batched_partial_bytes(q, M, N);
@@ -675,7 +691,7 @@ int kmi_qmm_batched(const void* x, const int64_t* x_strides, const uint32_t* w, 
     a.widx = widx; a.xidx = xidx; a.nw = nw; a.nx = nx;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)q.ntiles, (unsigned)(q.mtiles * q.S), (unsigned)P);
-    int rc = launch_batched(a, mode, bits, group_size, transpose != 0, grid, st);
+    int rc = launch_batched(a, mode, bits, group_size, transpose != 0, q.mb, grid, st);
     if (rc) return rc;
     KMI_CHECK_LAUNCH("quantized_matmul (batched)");
     if (q.S > 1) {
