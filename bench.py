@@ -373,6 +373,56 @@ def bench_vq_packed(T, calls, dev, dim=4, kc=2048, group=64):
             "flops": 2.0 * T * k * 3 * H * I}
 
 
+def bench_mx_moe(T, calls, dev, mode="mxfp4"):
+    """MoE experts stored mxfp4 (E2M1 codes, E8M0 scales per 32 inputs, the
+    routed-expert format of DeepSeek-V4 checkpoints) at the Qwen3.5-MoE
+    shape: router, gate and up (gather_qmm each), SwiGLU, down, weighted
+    combine.  Expert sets rotated past 1 GB.  Bytes: every routed expert's
+    codes and scales once, x and out."""
+    import torch
+    import knurlogic_amd as KA
+    from knurlogic_amd import nn
+    E, k, H, I = MOE["E"], MOE["k"], MOE["H"], MOE["I"]
+    bits = 4 if mode == "mxfp4" else 8
+
+    def mat_bytes(N, K):
+        return N * (K * bits // 8 + K // 32)
+
+    per_e = 2 * mat_bytes(I, H) + mat_bytes(H, I)
+    n = max(4, math.ceil(ROTATE_BYTES / (E * per_e)))
+    g = torch.Generator(device=dev).manual_seed(6000 + T)
+
+    def mat(N, K):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, N, K * bits // 32), device=dev, generator=g,
+                          dtype=torch.int32).view(torch.uint32)
+        sc = torch.randint(118, 124, (E, N, K // 32), device=dev, generator=g, dtype=torch.int32).to(torch.uint8)
+        return nn.QuantizedSwitchLinear(w, sc, None, None, 32, bits, mode)
+
+    sets = [(mat(I, H), mat(I, H), mat(H, I)) for _ in range(n)]
+    x = torch.randn(T, H, device=dev, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, device=dev, generator=g).to(torch.bfloat16)
+    inds, _ = KA.moe_route(logits, k)
+    distinct = int(torch.unique(inds).numel())
+    xe = x[:, None, None, :]
+
+    def run():
+        for i in range(calls):
+            gp, up, dn = sets[i % n]
+            ii, sc = KA.moe_route(logits, k)
+            act = KA.swiglu(gp(xe, ii), up(xe, ii))                     # [T, k, 1, I]
+            y = dn(act, ii)                                              # [T, k, 1, H]
+            KA.moe_combine(y.reshape(T, k, H), sc)
+
+    us = time_graph(run) / calls * 1e3
+    nbytes = distinct * per_e + 2 * 2 * T * H
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del sets
+    torch.cuda.empty_cache()
+    return {"op": f"{mode}_moe_experts", "T": T, "experts_routed": distinct, "cache": "cold",
+            "us": round(us, 3), "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+            "bound": "hbm", "bytes": nbytes, "flops": 2.0 * T * k * 3 * H * I}
+
+
 HEADLINE_PROFILE = ROOT / "profiles" / "qmv_4bit_14336x4096_m1.md"
 
 
@@ -476,6 +526,9 @@ def main():
     if not args.quick and "vq" in only:
         for t_ in (1, 16):
             detail.append(bench_vq_packed(t_, 50, dev))
+    if not args.quick and "moe" in only:
+        for t_ in (1, 16):
+            detail.append(bench_mx_moe(t_, 30, dev))
     if not args.quick and "moe" in only:
         for t_ in (1, 16, 256):
             for cold in (True, False):
