@@ -111,7 +111,9 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
     // global loads are in flight in registers while this one is multiplied
     __shared__ __align__(16) uint16_t As[BM * QB_LD];
     __shared__ __align__(16) uint16_t Bh[QB_T * QB_LD];     // hi parts of the dequantized weight
-    __shared__ __align__(16) uint16_t Bl[QB_T * QB_LD];     // lo parts
+    // lo parts (the mx modes' values are exact in bf16: no lo part)
+    constexpr bool LO = MODE == 0;
+    __shared__ __align__(16) uint16_t Bl[LO ? QB_T * QB_LD : 8];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
@@ -291,11 +293,13 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
             for (int i = 0; i < 16; i += 2)
                 qb_split(__builtin_fmaf(sc, q[i], bi), __builtin_fmaf(sc, q[i + 1], bi), oh[i / 2], ol[i / 2]);
             u32x4* dh = (u32x4*)&Bh[xrow * QB_LD + 16 * xc];
-            u32x4* dl = (u32x4*)&Bl[xrow * QB_LD + 16 * xc];
             dh[0] = u32x4{oh[0], oh[1], oh[2], oh[3]};
             dh[1] = u32x4{oh[4], oh[5], oh[6], oh[7]};
-            dl[0] = u32x4{ol[0], ol[1], ol[2], ol[3]};
-            dl[1] = u32x4{ol[4], ol[5], ol[6], ol[7]};
+            if constexpr (LO) {
+                u32x4* dl = (u32x4*)&Bl[xrow * QB_LD + 16 * xc];
+                dl[0] = u32x4{ol[0], ol[1], ol[2], ol[3]};
+                dl[1] = u32x4{ol[4], ol[5], ol[6], ol[7]};
+            }
         } else {
             float v[4][4];
 #pragma unroll
@@ -320,7 +324,7 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
                 qb_split(v[0][c], v[1][c], h0, l0);
                 qb_split(v[2][c], v[3][c], h1, l1);
                 *(u32x2*)&Bh[(4 * nq + c) * QB_LD + 4 * kq] = u32x2{h0, h1};
-                *(u32x2*)&Bl[(4 * nq + c) * QB_LD + 4 * kq] = u32x2{l0, l1};
+                if constexpr (LO) *(u32x2*)&Bl[(4 * nq + c) * QB_LD + 4 * kq] = u32x2{l0, l1};
             }
         }
     };
@@ -342,13 +346,13 @@ __global__ __launch_bounds__(256) void qmm_batched_kernel(QbArgs a) {
 #pragma unroll
             for (int j = 0; j < JN; j++) {
                 H[j] = *(const u32x4*)&Bh[(16 * JN * wn + 16 * j + fr) * QB_LD + kk + fk];
-                Lo[j] = *(const u32x4*)&Bl[(16 * JN * wn + 16 * j + fr) * QB_LD + kk + fk];
+                if constexpr (LO) Lo[j] = *(const u32x4*)&Bl[(16 * JN * wn + 16 * j + fr) * QB_LD + kk + fk];
             }
 #pragma unroll
             for (int i = 0; i < IM; i++)
 #pragma unroll
                 for (int j = 0; j < JN; j++) {
-                    acc[i][j] = mfma16x16x32(A[i], Lo[j], acc[i][j]);
+                    if constexpr (LO) acc[i][j] = mfma16x16x32(A[i], Lo[j], acc[i][j]);
                     acc[i][j] = mfma16x16x32(A[i], H[j], acc[i][j]);
                 }
         }

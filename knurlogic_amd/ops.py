@@ -386,12 +386,40 @@ def _gather_batched(x, w, scales, lhs, rhs, ishape, transpose, group_size, bits,
     return y.reshape(*ishape, M, N)
 
 
+#: the default lhs of a gather (every batch element of x, broadcast against
+#: rhs), kept per shape: built once instead of on every call
+_DEFAULT_LHS: dict = {}
+
+
+def _default_lhs(xbatch, shape, dev):
+    key = (xbatch, shape, str(dev))
+    t = _DEFAULT_LHS.get(key)
+    if t is None:
+        base = torch.arange(math.prod(xbatch), device=dev, dtype=torch.int32).reshape(xbatch)
+        t = torch.broadcast_to(base, shape).reshape(-1).contiguous()
+        if len(_DEFAULT_LHS) > 64:
+            _DEFAULT_LHS.clear()
+        _DEFAULT_LHS[key] = t
+    return t
+
+
 def _flat_indices(x, w, lhs_indices, rhs_indices):
     """mx.gather_qmm's index semantics: lhs defaults to every batch element
     of x, rhs to every batch element of w; the two broadcast together."""
     dev = x.device
     xbatch = tuple(x.shape[:-2])
     wbatch = tuple(w.shape[:-2])
+    if lhs_indices is None and rhs_indices is not None:
+        rhs = torch.as_tensor(rhs_indices, device=dev)
+        if rhs.dtype.is_floating_point:
+            raise ValueError("gather_qmm: indices must be integers")
+        try:
+            shape = tuple(torch.broadcast_shapes(xbatch, tuple(rhs.shape)))
+        except RuntimeError as e:
+            raise ValueError(f"gather_qmm: x batch {xbatch} and indices {tuple(rhs.shape)} do not broadcast") from e
+        rhs = torch.broadcast_to(rhs, shape).reshape(-1)
+        rhs = (rhs if rhs.dtype == torch.int32 else rhs.to(torch.int32)).contiguous()
+        return _default_lhs(xbatch, shape, dev), rhs, shape
     if lhs_indices is None:
         lhs_indices = torch.arange(math.prod(xbatch), device=dev, dtype=torch.int32).reshape(xbatch)
     if rhs_indices is None:
