@@ -150,6 +150,20 @@ def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | Non
     return out
 
 
+def _check_affine_operands_t(x, w, scales, biases, group_size, bits, what):
+    """The affine operand rules for a weight stored [..., K, N*bits/32]
+    (transpose=False: groups along N)."""
+    if biases is None:
+        raise ValueError(f"{what}: affine mode needs biases")
+    _on_gpu(x, w, scales, biases)
+    if x.dtype != torch.bfloat16 or scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
+        raise ValueError(f"{what}: only bfloat16 activations, scales and biases are implemented")
+    if w.shape[-2] != x.shape[-1] or scales.shape != biases.shape or scales.shape[:-1] != w.shape[:-1] \
+            or scales.shape[-1] * group_size != w.shape[-1] * 32 // bits:
+        raise ValueError(f"{what}: w {tuple(w.shape)} / scales {tuple(scales.shape)} do not take x "
+                         f"{tuple(x.shape)} with transpose=False at group {group_size}")
+
+
 def _check_affine_operands(x, w, scales, biases, group_size, bits, what):
     if biases is None:
         raise ValueError(f"{what}: affine mode needs biases")
@@ -351,14 +365,15 @@ def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 
     return y[0] if vec else y
 
 
-def _gather_batched(x, w, scales, lhs, rhs, ishape, transpose, group_size, bits, mode):
-    """mx.gather_qmm in the scaled modes: kmi_qmm_batched's gather form, one
-    batch entry per (lhs, rhs) pair."""
+def _gather_batched(x, w, scales, lhs, rhs, ishape, transpose, group_size, bits, mode, biases=None):
+    """mx.gather_qmm through kmi_qmm_batched's gather form, one batch entry
+    per (lhs, rhs) pair: the scaled modes, and transpose=False."""
     what = "gather_qmm"
     M, K = x.shape[-2], x.shape[-1]
     E = math.prod(w.shape[:-2])
     wc = w.reshape(E, *w.shape[-2:]).contiguous()
     sc = scales.reshape(E, *scales.shape[-2:]).contiguous()
+    bc = biases.reshape(E, *biases.shape[-2:]).contiguous() if biases is not None else None
     if transpose:
         N, Kw = wc.shape[1], wc.shape[2] * 32 // bits
     else:
@@ -380,7 +395,7 @@ def _gather_batched(x, w, scales, lhs, rhs, ishape, transpose, group_size, bits,
     nbytes = L.kmi_qmm_batched_workspace_bytes(1, shape.data_ptr(), M, K, N)
     ws = _workspace(nbytes, x.device)
     _abi.check(L.kmi_qmm_batched(
-        _ptr(xb), xs.data_ptr(), _ptr(wc), ws_.data_ptr(), _ptr(sc), None, ss.data_ptr(), 1, shape.data_ptr(),
+        _ptr(xb), xs.data_ptr(), _ptr(wc), ws_.data_ptr(), _ptr(sc), _ptr(bc), ss.data_ptr(), 1, shape.data_ptr(),
         M, K, N, int(bool(transpose)), DTYPE_CODE[x.dtype], group_size, bits, MODE_CODE[mode], _ptr(rhs),
         _ptr(lhs), E, xb.shape[0], 1.0, _ptr(y), N, _ptr(ws), nbytes, _stream(x)), what)
     return y.reshape(*ishape, M, N)
@@ -455,7 +470,9 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
         lhs, rhs, ishape = _flat_indices(x, w, lhs_indices, rhs_indices)
         return _gather_batched(x, w, scales, lhs, rhs, ishape, transpose, group_size, bits, mode)
     if not transpose:
-        raise ValueError("gather_qmm: transpose=False is not implemented for the affine mode")
+        _check_affine_operands_t(x, w, scales, biases, group_size, bits, "gather_qmm")
+        lhs, rhs, ishape = _flat_indices(x, w, lhs_indices, rhs_indices)
+        return _gather_batched(x, w, scales, lhs, rhs, ishape, False, group_size, bits, mode, biases)
     _check_affine_operands(x, w, scales, biases, group_size, bits, "gather_qmm")
     M, K = x.shape[-2], x.shape[-1]
     N = w.shape[-2]

@@ -77,6 +77,22 @@ def test_dense_projection_at_the_other_widths(dev, bits):
         assert_close(to_numpy(got), ref, what=f"{bits}-bit M={M}")
 
 
+def test_gather_qmm_transpose_false(dev):
+    """mx.gather_qmm with transpose=False (What[e] [K, N], groups along N):
+    each pair's x rows times its expert's weight."""
+    rng = np.random.default_rng(31)
+    E, K, N, P, M = 5, 256, 192, 7, 3
+    (wq, s, b), (tw, ts, tb) = _quantized(rng, (E, K, N), 64, 4, dev)
+    x = bf16_normal(rng, (P, M, K))
+    rhs = rng.integers(0, E, P).astype(np.int32)
+    got = ops.gather_qmm(to_torch(x, dev, torch.bfloat16), tw, ts, tb, rhs_indices=torch.from_numpy(rhs).to(dev),
+                         transpose=False, group_size=64, bits=4)
+    ref = np.stack([O.quantized_matmul(x[p], wq[rhs[p]], s[rhs[p]], b[rhs[p]], False, 64, 4, "float32")
+                    for p in range(P)])
+    assert got.shape == (P, M, N)
+    assert_close(to_numpy(got), ref, what="gather transpose=False")
+
+
 def test_strided_slab_views_are_read_in_place(dev):
     """K/V slabs are views into a larger capacity: the batch and row strides
     are passed through, nothing is copied."""
