@@ -59,3 +59,35 @@ def test_ops_refuse_cpu_tensors():
         K.quantize(torch.zeros(4, 64, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="affine"):
         K.quantize(torch.zeros(4, 64, dtype=torch.bfloat16), mode="mxfp4")
+
+
+def test_new_entries_refuse_bad_arguments_on_the_host():
+    """The batched matmul, masked softmax, packed VQ, mx dequantize and KV
+    append entries check their arguments before touching the GPU (fake
+    non-null pointers are never dereferenced)."""
+    import ctypes
+    from knurlogic_amd import _abi
+    L = _abi.load()
+    i64 = lambda *v: (ctypes.c_int64 * len(v))(*v)
+    st = i64(0, 64)
+    # mxfp4 requires 4 bits and groups of 32
+    rc = L.kmi_qmm_batched(16, st, 16, st, 16, None, st, 0, None, 1, 64, 64, 1, 0, 64, 4, 1, None, None, 0, 0,
+                           1.0, 16, 64, None, 0, None)
+    assert rc == -1 and b"mxfp4" in L.kmi_last_error()
+    # 7-bit codes do not exist in mlx
+    rc = L.kmi_qmm_batched(16, st, 16, st, 16, 16, st, 0, None, 1, 64, 64, 1, 0, 64, 7, 0, None, None, 0, 0,
+                           1.0, 16, 64, None, 0, None)
+    assert rc == -1 and b"bits 7" in L.kmi_last_error()
+    # rows of the softmax must be padded to 8 elements
+    dims = i64(1, 1, 1, 2)
+    rc = L.kmi_masked_softmax(16, 5, 0, dims, 5, None, 0, None, 16, 5, None)
+    assert rc == -1 and b"padded" in L.kmi_last_error()
+    # packed VQ: 13-bit fields are not built
+    rc = L.kmi_vq_packed_gather_qmm(16, 1, 128, 16, 13, 16, 4096, 4, 16, 64, 2, 8, None, 1, 16, 1, 0, 16, None)
+    assert rc == -1 and b"13-bit" in L.kmi_last_error()
+    # mx dequantize: mode 3 does not exist
+    rc = L.kmi_dequantize_mx(16, 16, 1, 64, 3, 16, 0, None)
+    assert rc == -1 and b"mode 3" in L.kmi_last_error()
+    # KV append past the slab's capacity
+    rc = L.kmi_kv_quantize_append(16, 0, 1, 1, 4, 64, 64, 8, 16, 16, 16, i64(0, 0, 0, 0, 0, 0), 254, 256, None)
+    assert rc == -1 and b"capacity" in L.kmi_last_error()
