@@ -198,8 +198,9 @@ def bench_qsdpa(B, H, Hk, L, N, D, bits, calls, dev):
 def bench_kv_append(B, Hk, S, D, bits, calls, dev):
     """Quantize-on-append into a quantized KV cache (kvcache.QuantKVCache's
     update_and_fetch): S new K and V rows of B x Hk heads quantized along D
-    (group 64) straight into slab slots, one kmi_kv_quantize_append launch
-    each; slots rotate through a 1 GB slab set so every write is cold.
+    (group 64) straight into slab slots, K and V in one
+    kmi_kv_quantize_append_kv launch; slots rotate through a 1 GB slab set
+    so every write is cold.
     Bytes: K and V rows read (bf16) + packed words, scales and biases
     written."""
     import torch
@@ -215,8 +216,7 @@ def bench_kv_append(B, Hk, S, D, bits, calls, dev):
     def run():
         for i in range(calls):
             pos = (i % n_pos) * S
-            kvcache.append_quantized(k_parts, xs[0], pos, 64, bits)
-            kvcache.append_quantized(v_parts, xs[1], pos, 64, bits)
+            kvcache.append_kv(k_parts, v_parts, xs[0], xs[1], pos, 64, bits)
 
     us = time_graph(run) / calls * 1e3
     nbytes = 2 * B * Hk * S * D * 2 + S * per_slot

@@ -73,6 +73,18 @@ int kmi_kv_quantize_append(const void* x, int dtype, int64_t B, int64_t H, int64
                            const int64_t* strides, int64_t pos, int64_t capacity, void* stream);
 
 /*
+ * Keys and values of one update_and_fetch in one launch (the two
+ * mx.quantize writes of kvquant.py:153-156): as kmi_kv_quantize_append for
+ * k [B, H, S, Dk] into the K triple and v [B, H, S, Dv] into the V triple,
+ * same dtype, group and bits; each triple with its own strides[6].
+ */
+int kmi_kv_quantize_append_kv(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t S,
+                              int64_t Dk, int64_t Dv, int group_size, int bits, uint32_t* k_wq, void* k_scales,
+                              void* k_biases, const int64_t* k_strides, uint32_t* v_wq, void* v_scales,
+                              void* v_biases, const int64_t* v_strides, int64_t pos, int64_t capacity,
+                              void* stream);
+
+/*
  * mx.dequantize(w, scales, mode="mxfp4" | "mxfp8") over [rows, cols]: element
  * codes E2M1 (mode 1, 4 bits) or E4M3 (mode 2, 8 bits) packed as mlx packs
  * 4 / 8-bit codes, times 2^(e - 127) for the uint8 E8M0 scale e of each group

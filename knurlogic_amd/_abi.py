@@ -19,6 +19,7 @@ SIGNATURES = {
     "kmi_abi_version": (I, []),
     "kmi_quantize_affine": (I, [P, I, I64, I64, I, I, P, P, P, P]),
     "kmi_kv_quantize_append": (I, [P, I, I64, I64, I64, I64, I, I, P, P, P, P, I64, I64, P]),
+    "kmi_kv_quantize_append_kv": (I, [P, P, I, I64, I64, I64, I64, I64, I, I, P, P, P, P, P, P, P, P, I64, I64, P]),
     "kmi_dequantize_affine": (I, [P, P, P, I, I64, I64, I, I, P, I, I, P]),
     "kmi_qmm": (I, [P, I64, I64, I64, P, P, P, I, I, I, P, P, SZ, P]),
     "kmi_qmm_workspace_bytes": (SZ, [I64, I64, I64, I, I]),

@@ -39,8 +39,8 @@ struct QuantDst {
 };
 
 template <typename T, int BITS, int GS>
-__global__ __launch_bounds__(256) void quantize_kernel(const typename T::storage* __restrict__ w,
-                                                       int64_t n_groups, int64_t D, QuantDst d) {
+__device__ __forceinline__ void quantize_body(const typename T::storage* __restrict__ w, int64_t n_groups,
+                                              int64_t D, const QuantDst& d) {
     constexpr int LPG = GS / 8;                  // lanes per group
     using St = typename T::storage;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -152,6 +152,22 @@ __global__ __launch_bounds__(256) void dequantize_kernel(
     }
 }
 
+template <typename T, int BITS, int GS>
+__global__ __launch_bounds__(256) void quantize_kernel(const typename T::storage* __restrict__ w,
+                                                       int64_t n_groups, int64_t D, QuantDst d) {
+    quantize_body<T, BITS, GS>(w, n_groups, D, d);
+}
+
+// K and V of one KV-cache append in one launch: grid y picks the tensor.
+template <typename T, int BITS, int GS>
+__global__ __launch_bounds__(256) void quantize_kv_kernel(const typename T::storage* __restrict__ k, int64_t nk,
+                                                          int64_t Dk, QuantDst dk,
+                                                          const typename T::storage* __restrict__ v, int64_t nv,
+                                                          int64_t Dv, QuantDst dv) {
+    if (blockIdx.y == 0) quantize_body<T, BITS, GS>(k, nk, Dk, dk);
+    else quantize_body<T, BITS, GS>(v, nv, Dv, dv);
+}
+
 // 3, 5 and 6 bits: one thread per 8 elements (BITS whole bytes of the
 // row's bit stream).
 template <typename TS, typename TO, int BITS>
@@ -222,6 +238,30 @@ static void launch_quantize_b(const void* w, int64_t n_groups, int group, int64_
     if (group == 32) quantize_kernel<T, BITS, 32><<<grid, 256, 0, st>>>((const S*)w, n_groups, D, d);
     else if (group == 64) quantize_kernel<T, BITS, 64><<<grid, 256, 0, st>>>((const S*)w, n_groups, D, d);
     else quantize_kernel<T, BITS, 128><<<grid, 256, 0, st>>>((const S*)w, n_groups, D, d);
+}
+
+template <typename T, int BITS>
+static void launch_quantize_kv_b(const void* k, int64_t nk, int64_t Dk, const QuantDst& dk, const void* v,
+                                 int64_t nv, int64_t Dv, const QuantDst& dv, int group, hipStream_t st) {
+    using S = typename T::storage;
+    const int64_t n = nk > nv ? nk : nv;
+    dim3 grid((unsigned)ceil_div(n * (group / 8), 256), 2);
+#define KMI_QKV(G_) quantize_kv_kernel<T, BITS, G_><<<grid, 256, 0, st>>>((const S*)k, nk, Dk, dk, (const S*)v, nv, Dv, dv)
+    if (group == 32) KMI_QKV(32);
+    else if (group == 64) KMI_QKV(64);
+    else KMI_QKV(128);
+#undef KMI_QKV
+}
+
+template <typename T>
+static void launch_quantize_kv(const void* k, int64_t nk, int64_t Dk, const QuantDst& dk, const void* v,
+                               int64_t nv, int64_t Dv, const QuantDst& dv, int group, int bits, hipStream_t st) {
+    if (bits == 4) launch_quantize_kv_b<T, 4>(k, nk, Dk, dk, v, nv, Dv, dv, group, st);
+    else if (bits == 8) launch_quantize_kv_b<T, 8>(k, nk, Dk, dk, v, nv, Dv, dv, group, st);
+    else if (bits == 3) launch_quantize_kv_b<T, 3>(k, nk, Dk, dk, v, nv, Dv, dv, group, st);
+    else if (bits == 5) launch_quantize_kv_b<T, 5>(k, nk, Dk, dk, v, nv, Dv, dv, group, st);
+    else if (bits == 6) launch_quantize_kv_b<T, 6>(k, nk, Dk, dk, v, nv, Dv, dv, group, st);
+    else launch_quantize_kv_b<T, 2>(k, nk, Dk, dk, v, nv, Dv, dv, group, st);
 }
 
 template <typename T>
@@ -323,6 +363,49 @@ int kmi_kv_quantize_append(const void* x, int dtype, int64_t B, int64_t H, int64
     if (dtype == BF16) launch_quantize<TBF16>(x, n_groups, group_size, bits, D, d, st);
     else if (dtype == F16) launch_quantize<TF16>(x, n_groups, group_size, bits, D, d, st);
     else launch_quantize<TF32>(x, n_groups, group_size, bits, D, d, st);
+    KMI_CHECK_LAUNCH("kv_quantize_append");
+    return OK;
+}
+
+int kmi_kv_quantize_append_kv(const void* k, const void* v, int dtype, int64_t B, int64_t H, int64_t S,
+                              int64_t Dk, int64_t Dv, int group_size, int bits, uint32_t* k_wq, void* k_scales,
+                              void* k_biases, const int64_t* k_strides, uint32_t* v_wq, void* v_scales,
+                              void* v_biases, const int64_t* v_strides, int64_t pos, int64_t capacity,
+                              void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(k && v && k_wq && k_scales && k_biases && k_strides && v_wq && v_scales && v_biases && v_strides,
+                  "kv_quantize_append: null pointer");
+    KMI_CHECK_ARG(bits >= 2 && bits <= 8 && bits != 7, "kv_quantize_append: bits %d not in {2,3,4,5,6,8}",
+                  bits);
+    KMI_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
+                  "kv_quantize_append: group_size %d not in {32,64,128}", group_size);
+    KMI_CHECK_ARG(B >= 0 && H >= 0 && S >= 0 && Dk > 0 && Dv > 0 && Dk % group_size == 0 && Dv % group_size == 0,
+                  "kv_quantize_append: head dims %lld / %lld are not multiples of the group %d", (long long)Dk,
+                  (long long)Dv, group_size);
+    KMI_CHECK_ARG(dtype >= BF16 && dtype <= F32, "kv_quantize_append: bad dtype %d", dtype);
+    KMI_CHECK_ARG(pos >= 0 && pos + S <= capacity,
+                  "kv_quantize_append: slots %lld..%lld past the slab capacity %lld", (long long)pos,
+                  (long long)(pos + S), (long long)capacity);
+    QuantDst dk = {}, dv = {};
+    dk.wq = k_wq; dk.scales = k_scales; dk.biases = k_biases;
+    dv.wq = v_wq; dv.scales = v_scales; dv.biases = v_biases;
+    for (QuantDst* d : {&dk, &dv}) {
+        d->pos = pos; d->H = H; d->S = S; d->kv = 1;
+    }
+    for (int i = 0; i < 3; i++) {
+        KMI_CHECK_ARG(k_strides[i] >= 0 && k_strides[3 + i] >= 0 && v_strides[i] >= 0 && v_strides[3 + i] >= 0,
+                      "kv_quantize_append: negative stride");
+        dk.wst[i] = k_strides[i]; dk.sst[i] = k_strides[3 + i];
+        dv.wst[i] = v_strides[i]; dv.sst[i] = v_strides[3 + i];
+    }
+    const int64_t nk = B * H * S * (Dk / group_size), nv = B * H * S * (Dv / group_size);
+    if (nk == 0) return OK;
+    KMI_CHECK_ARG(((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0,
+                  "kv_quantize_append: keys and values must be 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == BF16) launch_quantize_kv<TBF16>(k, nk, Dk, dk, v, nv, Dv, dv, group_size, bits, st);
+    else if (dtype == F16) launch_quantize_kv<TF16>(k, nk, Dk, dk, v, nv, Dv, dv, group_size, bits, st);
+    else launch_quantize_kv<TF32>(k, nk, Dk, dk, v, nv, Dv, dv, group_size, bits, st);
     KMI_CHECK_LAUNCH("kv_quantize_append");
     return OK;
 }

@@ -121,6 +121,38 @@ def append_quantized(parts, x: torch.Tensor, pos: int, group: int, bits: int) ->
         strides.data_ptr(), int(pos), wq.shape[2], _stream(x)), "kv_quantize_append")
 
 
+def _check_slab(parts, x, bits):
+    wq, sc, bi = parts
+    _on_gpu(x, wq, sc, bi)
+    if bits not in (2, 3, 4, 5, 6, 8):
+        raise ValueError(f"KV cache: {bits}-bit storage is not implemented (2, 3, 4, 5, 6, 8)")
+    if x.dtype not in DTYPE_CODE or sc.dtype != x.dtype or bi.dtype != x.dtype:
+        raise ValueError("KV cache: keys/values and the stored scales must share a float dtype")
+    if sc.stride(-1) != 1 or wq.stride(-1) != 1 or sc.stride() != bi.stride():
+        raise ValueError("KV cache: the slab's last axis must be contiguous, scales laid out like biases")
+    return [wq.stride(0), wq.stride(1), wq.stride(2), sc.stride(0), sc.stride(1), sc.stride(2)]
+
+
+def append_kv(kparts, vparts, keys: torch.Tensor, values: torch.Tensor, pos: int, group: int,
+              bits: int) -> None:
+    """Both appends of one update_and_fetch (keys into ``kparts``, values
+    into ``vparts``, slots pos .. pos+S-1) in one launch
+    (kmi_kv_quantize_append_kv)."""
+    ks = _check_slab(kparts, keys, bits)
+    vs = _check_slab(vparts, values, bits)
+    if keys.dtype != values.dtype or keys.shape[:3] != values.shape[:3]:
+        raise ValueError("KV cache: keys and values must share dtype and [B, H, S]")
+    B, H, S, Dk = keys.shape
+    Dv = values.shape[3]
+    kc, vc = _aligned16(keys), _aligned16(values)
+    st = torch.tensor(ks + vs, dtype=torch.int64)
+    _abi.check(_abi.load().kmi_kv_quantize_append_kv(
+        _ptr(kc), _ptr(vc), DTYPE_CODE[keys.dtype], B, H, S, Dk, Dv, group, bits,
+        _ptr(kparts[0]), _ptr(kparts[1]), _ptr(kparts[2]), st.data_ptr(),
+        _ptr(vparts[0]), _ptr(vparts[1]), _ptr(vparts[2]), st.data_ptr() + 6 * 8,
+        int(pos), kparts[0].shape[2], _stream(keys)), "kv_quantize_append")
+
+
 class LazyDequant:
     """K or V as ``update_and_fetch`` hands it back: the quantized slab
     view, dequantized (``mx.dequantize(...).astype(dtype)``) the first time
@@ -281,8 +313,7 @@ class QuantKVCache:
         prev = self.offset
         _grow(self, prev, B, H, S, Dk, Dv, keys.dtype, keys.device)
         self.offset += S
-        append_quantized(self.keys, keys, prev, self.group, self.kv_bits)
-        append_quantized(self.values, values, prev, self.group, self.kv_bits)
+        append_kv(self.keys, self.values, keys, values, prev, self.group, self.kv_bits)
         return _fetch(self, self.offset, S, keys.dtype, values.dtype)
 
     def size(self) -> int:
@@ -374,8 +405,7 @@ class BatchQuantKVCache:
         _grow(self, prev, B, H, S, Dk, Dv, keys.dtype, keys.device)
         self.offset = self.offset + S
         self._idx += S
-        append_quantized(self.keys, keys, prev, self.group, self.kv_bits)
-        append_quantized(self.values, values, prev, self.group, self.kv_bits)
+        append_kv(self.keys, self.values, keys, values, prev, self.group, self.kv_bits)
         return _fetch(self, self._idx, S, keys.dtype, values.dtype)
 
     def size(self) -> int:

@@ -24,9 +24,15 @@ def _cpu_append(parts, x, pos, group, bits):
     bi[:, :, pos:pos + S] = torch.from_numpy(b).to(bi.dtype)
 
 
+def _cpu_append_kv(kparts, vparts, keys, values, pos, group, bits):
+    _cpu_append(kparts, keys, pos, group, bits)
+    _cpu_append(vparts, values, pos, group, bits)
+
+
 @pytest.fixture(autouse=True)
 def cpu_append(monkeypatch):
     monkeypatch.setattr(KC, "append_quantized", _cpu_append)
+    monkeypatch.setattr(KC, "append_kv", _cpu_append_kv)
 
 
 def _kv(shape, seed):
