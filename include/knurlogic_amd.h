@@ -49,7 +49,9 @@ int kmi_abi_version(void);
  *   w       [rows, cols] of `dtype`, 16-byte aligned
  *   wq      [rows, cols*bits/32] uint32 out
  *   scales, biases [rows, cols/group_size] of `dtype` out
- * bits in {2, 4, 8}; group_size in {32, 64, 128}.
+ * bits in {2, 3, 4, 5, 6, 8} (3, 5 and 6-bit codes back to back in the row's
+ * little-endian bit stream, mlx's packing of those widths); group_size in
+ * {32, 64, 128}.
  */
 int kmi_quantize_affine(const void* w, int dtype, int64_t rows, int64_t cols,
                         int group_size, int bits, uint32_t* wq, void* scales,
@@ -100,6 +102,7 @@ int kmi_dequantize_mx(const uint32_t* wq, const uint8_t* scales, int64_t rows, i
  * dtype=out_dtype), as called at src/knurlogic/engine/kvquant.py:50-51.
  *   rounding 0: out = T(T(scale*q) + bias)  (op-by-op, the default)
  *   rounding 1: out = T(fma(scale, q, bias))
+ * bits in {2, 3, 4, 5, 6, 8}, codes packed as kmi_quantize_affine writes them.
  */
 int kmi_dequantize_affine(const uint32_t* wq, const void* scales, const void* biases,
                           int scale_dtype, int64_t rows, int64_t cols, int group_size,
