@@ -87,6 +87,19 @@ int kmi_kv_quantize_append_kv(const void* k, const void* v, int dtype, int64_t B
                               void* stream);
 
 /*
+ * mx.quantize(w, group_size=32, mode="mxfp4" | "mxfp8") over [rows, cols]:
+ * per group of 32 the OCP shared exponent X = floor(log2 max|w|) - emax
+ * (emax 2 for E2M1, 8 for E4M3) stored as the E8M0 byte X + 127 (an
+ * all-zero group: 0), elements w / 2^X rounded to the nearest code (ties to
+ * even) and saturated, the sign of w kept on every code (-0 included) --
+ * the rule the reference's mxfp4 checkpoint re-quantizes to bit for bit
+ * (tests/support/goldens/deepseek_v4_tiny).  wq [rows, cols*bits/32],
+ * scales uint8 [rows, cols/32].
+ */
+int kmi_quantize_mx(const void* w, int dtype, int64_t rows, int64_t cols, int mode, uint32_t* wq,
+                    uint8_t* scales, void* stream);
+
+/*
  * mx.dequantize(w, scales, mode="mxfp4" | "mxfp8") over [rows, cols]: element
  * codes E2M1 (mode 1, 4 bits) or E4M3 (mode 2, 8 bits) packed as mlx packs
  * 4 / 8-bit codes, times 2^(e - 127) for the uint8 E8M0 scale e of each group

@@ -30,6 +30,7 @@ SIGNATURES = {
                            ctypes.c_float, P, I, P, P, SZ, P]),
     "kmi_kv8_workspace_bytes": (SZ, [I, I, I, I, I, I]),
     "kmi_dequantize_mx": (I, [P, P, I64, I64, I, P, I, P]),
+    "kmi_quantize_mx": (I, [P, I, I64, I64, I, P, P, P]),
     "kmi_qmm_batched": (I, [P, P, P, P, P, P, P, I, P, I64, I64, I64, I, I, I, I, I, P, P, I64, I64,
                             ctypes.c_float, P, I64, P, SZ, P]),
     "kmi_qmm_batched_workspace_bytes": (SZ, [I, P, I64, I64, I64]),

@@ -215,6 +215,60 @@ __device__ __forceinline__ float mx_elem(uint32_t c, int mode) {
     return (c & 0x80u) ? -mag : mag;
 }
 
+// mx.quantize(mode="mxfp4" / "mxfp8"), one thread per group of 32: the
+// OCP shared exponent X = floor(log2 max|w|) - emax (2 for E2M1, 8 for
+// E4M3) as E8M0 byte X + 127 (an all-zero group: 0), elements w / 2^X to
+// the nearest code (rintf: ties to the even code, the codes of a binade
+// being consecutive), saturated, the input's sign kept (negative zeros too).
+__device__ __forceinline__ uint32_t mx_code(float v, int mode) {
+    const uint32_t sign = __float_as_uint(v) >> 31;
+    const float a = fabsf(v);
+    uint32_t c;
+    if (mode == 1) {                                       // E2M1: emin 0, 1 mantissa bit, max 6 = code 7
+        if (a >= 6.0f) c = 7;
+        else if (a < 1.0f) c = (uint32_t)rintf(a * 2.0f);  // 0, 0.5, 1.0 (code 2)
+        else {
+            const int e = (int)((__float_as_uint(a) >> 23) & 0xff) - 127;
+            c = (uint32_t)(((e + 1) << 1) + (int)rintf((a * __uint_as_float((uint32_t)(127 - e) << 23) - 1.0f) * 2.0f));
+        }
+        return c > 7 ? 7 | (sign << 3) : c | (sign << 3);
+    }
+    if (a >= 448.0f) c = 0x7e;                             // E4M3: max 448 = 0x7e
+    else if (a < 0.015625f) c = (uint32_t)rintf(a * 512.0f);   // subnormals m * 2^-9 (code 8 = 2^-6)
+    else {
+        const int e = (int)((__float_as_uint(a) >> 23) & 0xff) - 127;
+        c = (uint32_t)(((e + 7) << 3) + (int)rintf((a * __uint_as_float((uint32_t)(127 - e) << 23) - 1.0f) * 8.0f));
+    }
+    if (c > 0x7e) c = 0x7e;
+    return c | (sign << 7);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void quantize_mx_kernel(const typename T::storage* __restrict__ w, int64_t n_groups,
+                                                          int mode, uint32_t* __restrict__ wq,
+                                                          uint8_t* __restrict__ scales) {
+    const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gi >= n_groups) return;
+    const typename T::storage* src = w + gi * 32;
+    float amax = 0.f;
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(T::load(src[i])));
+    const int emax = mode == 1 ? 2 : 8;
+    int eb = 0;
+    if (amax > 0.f) {
+        const int e = (int)((__float_as_uint(amax) >> 23) & 0xff);     // biased exponent (normal range)
+        eb = e == 0 ? 0 : e - emax;                                     // X + 127, X = floor(log2 amax) - emax
+        eb = eb < 0 ? 0 : eb > 254 ? 254 : eb;
+    }
+    const float inv = eb >= 1 ? __uint_as_float((uint32_t)(254 - eb) << 23) : __uint_as_float(0x7f000000u);
+    const int bits = mode == 1 ? 4 : 8, epw = 32 / bits;
+    for (int wd = 0; wd < 32 / epw; wd++) {
+        uint32_t word = 0;
+        for (int e = 0; e < epw; e++) word |= mx_code(T::load(src[wd * epw + e]) * inv, mode) << (bits * e);
+        wq[gi * (32 / epw) + wd] = word;
+    }
+    scales[gi] = (uint8_t)eb;
+}
+
 template <typename TO>
 __global__ __launch_bounds__(256) void dequantize_mx_kernel(const uint32_t* __restrict__ wq,
                                                             const uint8_t* __restrict__ scales, int64_t n_words,
@@ -407,6 +461,25 @@ int kmi_kv_quantize_append_kv(const void* k, const void* v, int dtype, int64_t B
     else if (dtype == F16) launch_quantize_kv<TF16>(k, nk, Dk, dk, v, nv, Dv, dv, group_size, bits, st);
     else launch_quantize_kv<TF32>(k, nk, Dk, dk, v, nv, Dv, dv, group_size, bits, st);
     KMI_CHECK_LAUNCH("kv_quantize_append");
+    return OK;
+}
+
+int kmi_quantize_mx(const void* w, int dtype, int64_t rows, int64_t cols, int mode, uint32_t* wq,
+                    uint8_t* scales, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(w && wq && scales, "quantize (mx): null pointer");
+    KMI_CHECK_ARG(mode == 1 || mode == 2, "quantize (mx): mode %d (1 mxfp4, 2 mxfp8)", mode);
+    KMI_CHECK_ARG(rows >= 0 && cols > 0 && cols % 32 == 0, "quantize (mx): cols %lld not a multiple of 32",
+                  (long long)cols);
+    KMI_CHECK_ARG(dtype >= BF16 && dtype <= F32, "quantize (mx): bad dtype %d", dtype);
+    const int64_t n_groups = rows * cols / 32;
+    if (n_groups == 0) return OK;
+    const dim3 grid((unsigned)ceil_div(n_groups, 256));
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == BF16) quantize_mx_kernel<TBF16><<<grid, 256, 0, st>>>((const uint16_t*)w, n_groups, mode, wq, scales);
+    else if (dtype == F16) quantize_mx_kernel<TF16><<<grid, 256, 0, st>>>((const uint16_t*)w, n_groups, mode, wq, scales);
+    else quantize_mx_kernel<TF32><<<grid, 256, 0, st>>>((const float*)w, n_groups, mode, wq, scales);
+    KMI_CHECK_LAUNCH("quantize (mx)");
     return OK;
 }
 

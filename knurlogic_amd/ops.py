@@ -81,8 +81,22 @@ def _aligned16(t: torch.Tensor) -> torch.Tensor:
 def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4,
              mode: str = "affine"):
     """``mx.quantize``: (wq uint32 [..., K*bits/32], scales, biases
-    [..., K/group_size]) in w's dtype, groups along the last axis."""
-    _check_mode(mode)
+    [..., K/group_size]) in w's dtype, groups along the last axis.  mxfp4 /
+    mxfp8: (wq, scales uint8 E8M0), group 32 (mlx returns no biases)."""
+    _check_mode(mode, allow_mx=True)
+    if mode != "affine":
+        _on_gpu(w)
+        if w.dtype not in DTYPE_CODE or w.ndim < 1 or w.shape[-1] % 32:
+            raise ValueError(f"quantize: {mode} needs a float tensor whose last axis is a multiple of 32")
+        bits_mx = _MX_BITS[mode]
+        wc = w.contiguous()
+        cols = wc.shape[-1]
+        rows = wc.numel() // cols if cols else 0
+        wq = torch.empty(*wc.shape[:-1], cols * bits_mx // 32, dtype=torch.uint32, device=w.device)
+        sc = torch.empty(*wc.shape[:-1], cols // 32, dtype=torch.uint8, device=w.device)
+        _abi.check(_lib().kmi_quantize_mx(_ptr(wc), DTYPE_CODE[w.dtype], rows, cols, MODE_CODE[mode], _ptr(wq),
+                                          _ptr(sc), _stream(w)), "quantize")
+        return wq, sc
     _on_gpu(w)
     if w.dtype not in DTYPE_CODE:
         raise ValueError(f"quantize: dtype {w.dtype} not in bf16/fp16/fp32")

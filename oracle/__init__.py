@@ -367,6 +367,49 @@ def mx_dequantize(wq, scales, mode: str) -> np.ndarray:
     return v * np.repeat(e8m0(scales), 32, axis=-1)
 
 
+def mx_quantize(w, mode: str):
+    """mx.quantize(w, group_size=32, mode="mxfp4" | "mxfp8") per the OCP MX
+    scheme: per group of 32, X = floor(log2 max|w|) - emax (emax 2 for E2M1,
+    8 for E4M3), E8M0 byte X + 127 (clamped to 0..254; an all-zero group
+    takes 0), elements w / 2^X rounded to nearest (ties to the even code)
+    and saturated to the largest finite element, the input's sign kept
+    (negative zeros included).  -> (wq uint32, scales uint8).  Pinned by the reference's mxfp4 checkpoint: re-quantizing its
+    decoded values gives back its codes and scales."""
+    w = np.asarray(w, np.float64)
+    rows = w.reshape(-1, w.shape[-1])
+    G = rows.shape[1] // 32
+    g = rows.reshape(rows.shape[0], G, 32)
+    amax = np.abs(g).max(-1)
+    emax, bits = (2, 4) if mode == "mxfp4" else (8, 8)
+    with np.errstate(divide="ignore"):
+        X = np.floor(np.log2(np.where(amax > 0, amax, 1.0))) - emax
+    e = np.clip(np.where(amax > 0, X + 127, 0), 0, 254).astype(np.int64)
+    v = g / np.exp2(e - 127.0)[..., None]
+    if mode == "mxfp4":
+        grid = E2M1
+    else:
+        grid = e4m3(np.arange(127))                 # codes 0..126: every finite magnitude
+    mag = np.abs(v)
+    # nearest grid value, ties to the even code; past the top: the top code
+    idx = np.searchsorted(grid, mag)                 # first grid value >= mag
+    idx = np.clip(idx, 1, len(grid) - 1)
+    lo, hi = grid[idx - 1], grid[idx]
+    pick_hi = (mag - lo > hi - mag) | ((mag - lo == hi - mag) & (idx % 2 == 0))
+    code = np.where(pick_hi, idx, idx - 1)
+    code = np.where(mag >= grid[-1], len(grid) - 1, code)
+    # the input's sign is kept on every code, zero included (-0 is code 8 /
+    # 0x80): the reference's checkpoint holds such negative zeros
+    code = code | np.where(np.signbit(v), 8 if mode == "mxfp4" else 0x80, 0)
+    codes = code.reshape(rows.shape[0], -1).astype(np.uint32)
+    epw = 32 // bits
+    q = codes.reshape(rows.shape[0], -1, epw)
+    words = np.zeros(q.shape[:2], np.uint32)
+    for i in range(epw):
+        words |= q[..., i] << np.uint32(bits * i)
+    tail = w.shape[:-1]
+    return words.reshape(*tail, -1), e.astype(np.uint8).reshape(*tail, -1)
+
+
 def mx_quantized_matmul(x, wq, scales, mode: str, transpose: bool = True,
                         out_dtype: str = "bfloat16"):
     """mx.quantized_matmul(mode=mxfp4 | mxfp8) for a 2-D weight: the exact

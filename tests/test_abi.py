@@ -57,8 +57,8 @@ def test_ops_refuse_cpu_tensors():
     import knurlogic_amd as K
     with pytest.raises(ValueError, match="GPU memory"):
         K.quantize(torch.zeros(4, 64, dtype=torch.bfloat16))
-    with pytest.raises(ValueError, match="affine"):
-        K.quantize(torch.zeros(4, 64, dtype=torch.bfloat16), mode="mxfp4")
+    with pytest.raises(ValueError, match="affine, mxfp4 and mxfp8"):
+        K.quantize(torch.zeros(4, 64, dtype=torch.bfloat16), mode="nvfp4")
 
 
 def test_new_entries_refuse_bad_arguments_on_the_host():

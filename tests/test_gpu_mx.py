@@ -122,3 +122,28 @@ def test_mx_checkpoint_layers_load_and_run(dev, tmp_path):
     w, s = host["gate_proj"]
     assert_close(to_numpy(got).reshape(-1), O.mx_quantized_matmul(x[0], w[2], s[2], "mxfp4", True,
                                                                   "float32").reshape(-1), what="loaded mxfp4")
+
+
+@pytest.mark.parametrize("mode", ["mxfp4", "mxfp8"])
+def test_quantize_mx_bit_exact(dev, mode):
+    """mx.quantize on the GPU equals the oracle's OCP rule, code for code
+    (signs of zeros included), bf16 and fp32 inputs."""
+    rng = np.random.default_rng(7 if mode == "mxfp4" else 8)
+    w = bf16_normal(rng, (48, 256), 0.05)
+    w[0, :32] = 0.0
+    w[1, :32] = -0.0
+    w[2, 5] = 1e4                                    # saturates
+    for dt in (torch.bfloat16, torch.float32):
+        wq, sc = K.quantize(to_torch(w, dev, dt), group_size=32, bits=4 if mode == "mxfp4" else 8, mode=mode)
+        rq, rs = O.mx_quantize(w, mode)
+        assert np.array_equal(sc.cpu().numpy(), rs)
+        assert np.array_equal(wq.view(torch.int32).cpu().numpy().view(np.uint32), rq)
+
+
+def test_quantize_mx_gives_the_references_checkpoint_back(dev):
+    host, gpu = _fixture(dev)
+    for p, (w, s) in host.items():
+        d = to_torch(O.mx_dequantize(w, s, "mxfp4").astype(np.float32), dev, torch.float32)
+        wq, sc = K.quantize(d, group_size=32, bits=4, mode="mxfp4")
+        assert np.array_equal(sc.cpu().numpy(), s)
+        assert np.array_equal(wq.view(torch.int32).cpu().numpy().view(np.uint32), w)

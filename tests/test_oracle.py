@@ -494,3 +494,30 @@ def test_the_references_mxfp4_experts_decode_as_the_spec_quantizes():
         elem = v / np.repeat(O.e8m0(s), 32, axis=-1)
         gmax = np.abs(elem).reshape(*elem.shape[:-1], -1, 32).max(-1)
         assert set(np.unique(gmax).tolist()) <= {4.0, 6.0}
+
+
+def test_requantizing_the_references_mxfp4_experts_gives_them_back():
+    """mx_quantize of the fixture's decoded values reproduces its codes and
+    E8M0 scales exactly: the floor(log2 amax) - 2 exponent, RNE to E2M1 and
+    the packing order all agree with the checkpoint (a ceil-based scale
+    would move every group whose max element is 4 or 6 to another code)."""
+    z = np.load(GOLD / "deepseek_v4_tiny_mxfp4_experts.npz")
+    for p in ("gate_proj", "up_proj", "down_proj"):
+        w, s = z[p + "__weight"], z[p + "__scales"]
+        wq2, s2 = O.mx_quantize(O.mx_dequantize(w, s, "mxfp4"), "mxfp4")
+        assert np.array_equal(s2, s) and np.array_equal(wq2, w)
+
+
+def test_mx_quantize_round_trip_and_saturation():
+    rng = np.random.default_rng(9)
+    w = rng.standard_normal((4, 64)) * 0.05
+    w[0, :32] = 0.0                                   # an all-zero group
+    for mode in ("mxfp4", "mxfp8"):
+        wq, s = O.mx_quantize(w, mode)
+        back = O.mx_dequantize(wq, s, mode)
+        assert s[0, 0] == 0 and not back[0, :32].any()
+        # worst case in element units: saturation of [6, 8) to 6 (E2M1) or of
+        # [448, 512) to 448 (E4M3), which bounds the rounding error as well
+        worst = 2.0 if mode == "mxfp4" else 64.0
+        scale = np.repeat(O.e8m0(s), 32, -1)
+        assert (np.abs(back - w) <= scale * worst + 1e-12).all()
