@@ -98,7 +98,8 @@ def _experts(rng, E, H, I, dev, bits=4):
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("T,E,H,I,k", [(1, 16, 256, 128, 4), (5, 16, 256, 128, 4), (64, 16, 256, 128, 4),
                                        (100, 16, 256, 128, 4), (1, 128, 2048, 768, 8),
-                                       (16, 128, 2048, 768, 8), (40, 128, 2048, 768, 8)])
+                                       (16, 128, 2048, 768, 8), (40, 128, 2048, 768, 8),
+                                       (256, 128, 2048, 768, 8)])
 def test_switch_glu_matches_the_oracle(dev, T, E, H, I, k, bits):
     """One library call (token-major up to 16 (token, slot) pairs, grouped by
     expert above), the separate gather_qmm path, and the fused combine."""
@@ -134,7 +135,7 @@ def test_switch_glu_unstacked_gate_and_up_agree(dev):
     assert_close(to_numpy(glu(tx, ti)), ref, what="separate")
 
 
-@pytest.mark.parametrize("T", [1, 16])
+@pytest.mark.parametrize("T", [1, 16, 256])
 def test_sparse_moe_block_matches_the_oracle(dev, T):
     """Router from given logits, SwitchGLU, combine and the sigmoid-gated
     quantized shared expert, at the Qwen3.5-MoE shapes."""

@@ -60,6 +60,25 @@ def test_qmm_baseline_shapes(dev, bits, M, shape):
     assert np.isfinite(y).all()
 
 
+def test_qmm_decode_4096_square_every_column(dev):
+    """The single-layer decode workload: 4-bit g64 W [4096, 4096] ~ N(0, 0.02)
+    quantized on the GPU, x [1, 4096] ~ N(0, 1) bf16, every output column
+    against the oracle's matmul over the oracle's own quantization (the GPU
+    quantization is checked bit for bit on the way)."""
+    rng = np.random.default_rng(20251)
+    w = bf16_normal(rng, (4096, 4096), 0.02)
+    x = bf16_normal(rng, (1, 4096))
+    wq, s, b = K.quantize(to_torch(w, dev, BF), group_size=64, bits=4)
+    rq, rs, rb = O.quantize(w, 64, 4)
+    np.testing.assert_array_equal(wq.view(torch.int32).cpu().numpy().view(np.uint32), rq)
+    np.testing.assert_array_equal(to_numpy(s), rs)
+    np.testing.assert_array_equal(to_numpy(b), rb)
+    y = to_numpy(K.quantized_matmul(to_torch(x, dev, BF), wq, s, b, True, 64, 4))
+    ref = O.quantized_matmul(x, rq, rs, rb, True, 64, 4, "float32")
+    assert y.shape == (1, 4096)
+    assert_close(y, ref, what="[4096, 4096] M=1")
+
+
 def test_rows_are_independent_bit_for_bit(dev):
     """Row m of a call depends only on row m (the reference's padding
     contract, tests/engine/test_per_chip_rounding.py:30-41): within each
