@@ -140,6 +140,24 @@ int kmi_qmm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
 size_t kmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits);
 
 /*
+ * kmi_qmm without a workspace argument, allocating nothing: no counterpart
+ * in the reference.  It is for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops that forbid hipMalloc).  The
+ * same kernels as kmi_qmm, with the split-K partials in a device array of
+ * KMI_QMM_SCRATCH_BYTES that the library holds on every GPU it runs on
+ * until the process ends (its address is looked up once per device, on the
+ * first call with that device current).  Shapes whose partials need more
+ * (kmi_qmm_workspace_bytes > KMI_QMM_SCRATCH_BYTES) are refused with -1.
+ * The caller still allocates x and y.  All calls on one GPU share its
+ * array: calls that overlap on one GPU (two streams or threads) race.
+ */
+#define KMI_QMM_SCRATCH_BYTES (32u << 20)
+size_t kmi_qmm_noalloc_scratch_bytes(void);
+int kmi_qmm_noalloc(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
+                    const void* scales, const void* biases, int dtype, int group_size,
+                    int bits, void* y, void* stream);
+
+/*
  * mx.gather_qmm(x, w, scales, biases, lhs_indices, rhs_indices,
  * transpose=True, group_size, bits, sorted_indices) -- QuantizedSwitchLinear's
  * op (src/knurlogic/engine/families/glm5/architecture/glm5_next/_mlx_vlm/

@@ -91,3 +91,24 @@ def test_new_entries_refuse_bad_arguments_on_the_host():
     # KV append past the slab's capacity
     rc = L.kmi_kv_quantize_append(16, 0, 1, 1, 4, 64, 64, 8, 16, 16, 16, i64(0, 0, 0, 0, 0, 0), 254, 256, None)
     assert rc == -1 and b"capacity" in L.kmi_last_error()
+
+
+def test_noalloc_scratch_covers_every_planned_qmm():
+    """kmi_qmm_noalloc's scratch array (KMI_QMM_SCRATCH_BYTES) holds the
+    split-K partials of every shape kmi_qmm plans: the GEMM keeps
+    splits x tiles <= 256 (tiles of 256 x 128 outputs) and the skinny kernel
+    fewer than 1024 split workgroups of 64 x 64 outputs, so the partials never
+    pass 32 MiB.  Swept here on the host (workspace queries only)."""
+    import re
+    from knurlogic_amd import _abi
+    L = _abi.load()
+    cap = L.kmi_qmm_noalloc_scratch_bytes()
+    hdr = (ROOT / "include" / "knurlogic_amd.h").read_text()
+    assert cap == eval(re.search(r"#define KMI_QMM_SCRATCH_BYTES \((\d+)u << (\d+)\)", hdr).expand(r"\1 << \2"))
+    worst = 0
+    for M in (1, 2, 5, 16, 17, 33, 64, 65, 128, 129, 200, 256, 300, 384, 512, 640, 1000, 1024, 2048, 4096):
+        for K in (64, 512, 1024, 2048, 4096, 8192, 14336, 28672):
+            for N in (64, 100, 768, 2048, 4096, 6144, 8192, 14336, 28672):
+                for bits in (4, 8):
+                    worst = max(worst, L.kmi_qmm_workspace_bytes(M, K, N, 64, bits))
+    assert worst == cap      # reached (M = 512, K = 14336, N = 4096) and never passed
