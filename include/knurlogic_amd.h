@@ -91,10 +91,13 @@ int kmi_kv_quantize_append_kv(const void* k, const void* v, int dtype, int64_t B
  * per group of 32 the OCP shared exponent X = floor(log2 max|w|) - emax
  * (emax 2 for E2M1, 8 for E4M3) stored as the E8M0 byte X + 127 (an
  * all-zero group: 0), elements w / 2^X rounded to the nearest code (ties to
- * even) and saturated, the sign of w kept on every code (-0 included) --
- * the rule the reference's mxfp4 checkpoint re-quantizes to bit for bit
- * (tests/support/goldens/deepseek_v4_tiny).  wq [rows, cols*bits/32],
- * scales uint8 [rows, cols/32].
+ * even) and saturated, the sign of w kept on every code (-0 included):
+ * the OCP MX v1.0 conversion.  mlx's own quantizer is not in the
+ * reference tree, so its tie, saturation and zero-sign behaviour is not
+ * pinned; the reference's mxfp4 checkpoint
+ * (tests/support/goldens/deepseek_v4_tiny) re-quantizes to itself, which
+ * checks the shared exponent only.  wq [rows, cols*bits/32], scales uint8
+ * [rows, cols/32].
  */
 int kmi_quantize_mx(const void* w, int dtype, int64_t rows, int64_t cols, int mode, uint32_t* wq,
                     uint8_t* scales, void* stream);

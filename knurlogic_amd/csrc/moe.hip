@@ -29,12 +29,15 @@ __device__ __forceinline__ float f64_to_f32(double v) {
 
 constexpr int ROUTE_MAX_E = 1024;            // experts a wave holds (16 per lane)
 
-// One wave per token.  probs = softmax(logits) in float32 (computed in
-// float64 and rounded once); the k largest probabilities in descending
-// order, equal ones taken lower index first (softmax is monotone, so equal
-// probabilities come only from equal logits); scores = the selected
-// probabilities renormalized (float64, summed in selection order, rounded to
-// float32), then rounded to the logits' dtype.
+// One wave per token.  probs = softmax(logits) in float32, one rounding per
+// step as mlx's CPU softmax takes them (max m; e = exp(x - m); n = sum e;
+// r = 1 / n; p = e * r), with exp correctly rounded (evaluated in float64)
+// and the sum exact before its one rounding; the k largest probabilities in
+// descending order, equal ones taken lower index first; scores = p / t with
+// t the float32 sum of the k selected (again exact, then rounded), rounded
+// to the logits' dtype.  Quotients and products of two floats are formed in
+// float64 and rounded once, which gives the correctly rounded float32
+// result (53 >= 2 * 24 + 2 bits).
 //
 // Selection is by rank, with no serial rounds: probabilities are >= 0, so
 // their float32 bits order like the values, and key = bits << 32 | ~expert
@@ -63,21 +66,23 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const void* __restrict__
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    double ex[ROUTE_PER_LANE];
+    float ex[ROUTE_PER_LANE];
     double sum = 0.0;
 #pragma unroll
     for (int j = 0; j < ROUTE_PER_LANE; j++) {
-        ex[j] = lane + 64 * j < E ? exp((double)lg[j] - (double)mx) : 0.0;
-        sum += ex[j];
+        const float d = lg[j] - mx;                      // float32 subtraction, as mlx's kernel
+        ex[j] = lane + 64 * j < E ? f64_to_f32(exp((double)d)) : 0.f;
+        sum += (double)ex[j];
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    const float rn = f64_to_f32(1.0 / (double)f64_to_f32(sum));
     float p[ROUTE_PER_LANE];
     uint64_t key[ROUTE_PER_LANE];
 #pragma unroll
     for (int j = 0; j < ROUTE_PER_LANE; j++) {
         const int e = lane + 64 * j;
-        p[j] = e < E ? f64_to_f32(ex[j] / sum) : 0.f;
+        p[j] = e < E ? f64_to_f32((double)ex[j] * (double)rn) : 0.f;
         // padding lanes get key 0, below every expert's key (its low word ~e > 0)
         key[j] = e < E ? ((uint64_t)__float_as_uint(p[j]) << 32) | (uint32_t)~e : 0ull;
         keys[w][e] = key[j];
@@ -104,9 +109,10 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const void* __restrict__
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     double top_sum = 0.0;
     for (int s2 = 0; s2 < k; s2++) top_sum += (double)selp[w][s2];
+    const double tsum = (double)f64_to_f32(top_sum);
     if (live && lane < k) {
         inds[t * k + lane] = sele[w][lane];
-        st_dt<T>(scores, t * k + lane, f64_to_f32((double)selp[w][lane] / top_sum));
+        st_dt<T>(scores, t * k + lane, f64_to_f32((double)selp[w][lane] / tsum));
     }
 }
 

@@ -5,26 +5,34 @@ Mirrors the reference's src/knurlogic/engine/kvattn.py: ``decode_sdpa``
 biases) triples -- q pre-scaled, softmax over the keys a row may see -- with
 one HIP kernel over the packed K/V (kmi_kv8_decode) instead of
 dequantizing the cache; ``supports`` (:213-238) is the routing rule;
-``sdpa`` (:301-320) is the dispatch a model's attention calls, which takes
-the kernel when handed exactly the keys the quantized cache just returned
-and otherwise falls back as mlx-lm's base dispatch does: a cache with a
-``bits`` attribute (mlx-lm's own quantized cache) through
-``quantized_sdpa``, the two quantized products of
-.../_mlx_vlm/models/base.py:260-302, else dequantize + scaled-dot-product
-attention (all on the GPU); ``STATS`` counts hits and misses (:25-53).
+``sdpa`` (:301-320) is the dispatch a model's attention calls once
+``patch_model`` (:323-339) has rebound it; ``STATS`` counts hits and misses
+(:25-53); ``ENV`` / ``enabled`` (:69-75) switch the kernel.
 
-A query row whose every key is masked returns 0 here (the reference
-kernel's rule, :11-12), where a plain softmax would give NaN.
+Off the kernel, ``sdpa`` never computes attention in torch:
+  * quantized K/V -- a cache with a ``bits`` attribute (mlx-lm's own), or
+    the ``LazyDequant`` views this library's caches return (6 / 4-bit
+    caches, queries longer than the kernel takes, masks it does not take)
+    -- go through ``quantized_sdpa``, mlx-lm's quantized attention
+    (.../_mlx_vlm/models/base.py:260-302) over the packed triples: three
+    HIP launches, no dequantized copy of the cache;
+  * dense K/V go to the model's own attention function, the one
+    ``patch_model`` found and replaced (the reference likewise hands them
+    to mlx-lm's base function).
+
+A query row whose every key is masked returns 0 in the kernel (the
+reference kernel's rule, :11-12), where a plain softmax would give NaN.
 """
 from __future__ import annotations
 
 import logging
-import math
+import os
+import sys
 
 import torch
 
 from . import _abi
-from .ops import DTYPE_CODE, _on_gpu, _ptr, _stream, dequantize, padded_rows, qmm_batched, row_padded
+from .ops import DTYPE_CODE, _on_gpu, _ptr, _stream, padded_rows, qmm_batched, row_padded
 
 logger = logging.getLogger(__name__)
 
@@ -34,6 +42,20 @@ _LOGGED: set = set()
 
 #: query rows per KV head (GQA ratio x query length) the kernel takes
 MAX_ROWS = 64
+
+#: the kernel's on/off switch, the reference's knob (engine/kvattn.py:69):
+#: unset or any other value is on
+ENV = "KNURLOGIC_KV_KERNEL"
+_OFF = ("0", "off", "false", "no", "disable", "disabled")
+
+#: the model's own attention function that patch_model replaced: dense K/V
+#: go back to it
+_BASE: dict = {"fn": None}
+
+
+def enabled() -> bool:
+    """Whether the 8-bit decode kernel may be used (``ENV`` not off)."""
+    return os.environ.get(ENV, "").strip().lower() not in _OFF
 
 
 def reset(on: bool = True) -> None:
@@ -145,34 +167,6 @@ def decode_sdpa(q, K, V, scale: float, mask=None, group: int = 64, bits: int = 8
     return out
 
 
-def dequant_sdpa(q, K, V, scale: float, mask=None, group: int = 64, bits: int = 8):
-    """The fallback the reference takes off the kernel: dequantize the cache
-    (on the GPU) and run scaled-dot-product attention in float32, rows that
-    see no key returning 0."""
-    kd = dequantize(*K, group_size=group, bits=bits, dtype=torch.float32)
-    vd = dequantize(*V, group_size=group, bits=bits, dtype=torch.float32)
-    B, H, L, D = q.shape
-    Hk, N = kd.shape[1], kd.shape[2]
-    rep = H // Hk
-    qf = q.float() * scale
-    kd = kd.repeat_interleave(rep, dim=1)
-    vd = vd.repeat_interleave(rep, dim=1)
-    s = qf @ kd.transpose(-1, -2)
-    if isinstance(mask, str):
-        if L > 1:
-            rows = torch.arange(N - L, N, device=q.device)[:, None]
-            s = s.masked_fill(~(rows >= torch.arange(N, device=q.device)[None]), -math.inf)
-    elif mask is not None:
-        mm = mask if mask.dim() == 4 else mask.reshape((1,) * (4 - mask.dim()) + tuple(mask.shape))
-        s = s.masked_fill(~mm.to(torch.bool), -math.inf)
-    mx = s.amax(dim=-1, keepdim=True)
-    ok = torch.isfinite(mx)
-    p = torch.where(ok, torch.exp(s - torch.where(ok, mx, torch.zeros_like(mx))), torch.zeros_like(s))
-    den = p.sum(-1, keepdim=True)
-    o = (p @ vd) / torch.where(den > 0, den, torch.ones_like(den))
-    return o.to(q.dtype)
-
-
 #: KMI_MASK_* of include/knurlogic_amd.h
 MASK_NONE, MASK_BOOL, MASK_ADD, MASK_CAUSAL = 0, 1, 2, 3
 
@@ -246,7 +240,8 @@ def quantized_sdpa(queries, q_keys, q_values, scale: float, mask=None, group_siz
                    bits: int = 8):
     """mlx-lm's quantized_scaled_dot_product_attention (.../_mlx_vlm/
     models/base.py:260-302) over quantized K/V triples (packed, scales,
-    biases) of shape (B, Hk, N, *): q scaled (rounded to bf16), scores =
+    biases) of shape (B, Hk, N, *): q scaled by the scale rounded to q's
+    dtype (mlx casts the scalar), the product rounded to bf16, scores =
     quantized_matmul(q, K, transpose=True) in bf16, masked, softmax(precise)
     in bf16, out = quantized_matmul(p, V, transpose=False).  GQA query heads
     share their KV head's triple (broadcast, never copied).  Three HIP
@@ -265,18 +260,30 @@ def quantized_sdpa(queries, q_keys, q_values, scale: float, mask=None, group_siz
     N = Kt[0].shape[-2]
     # scores, then probabilities in place, in rows padded to 8 elements
     buf = padded_rows(tuple(q.shape[:-1]) + (N,), q.dtype, q.device)
-    scores = qmm_batched(q, *Kt, transpose=True, group_size=group_size, bits=bits, x_scale=float(scale),
+    # `queries *= scale` in mlx casts the Python scalar to the queries' dtype
+    # first: q * bf16(scale), rounded to bf16 as x is staged
+    qscale = float(torch.tensor(float(scale), dtype=torch.float32).to(q.dtype))
+    scores = qmm_batched(q, *Kt, transpose=True, group_size=group_size, bits=bits, x_scale=qscale,
                          out=buf)
     p = masked_softmax(scores, mask, out=scores)
     out = qmm_batched(p, *Vt, transpose=False, group_size=group_size, bits=bits)
     return out.reshape(B, Hq, L, -1) if rep > 1 else out
 
 
+def _packed(kv):
+    """(triple, group, bits) of a quantized cache's LazyDequant view, else None."""
+    from .kvcache import LazyDequant
+    if isinstance(kv, LazyDequant):
+        return kv.parts, kv.group, kv.bits
+    return None
+
+
 def sdpa(queries, keys, values, cache, scale, mask, sinks=None):
     """The dispatch a model's attention calls (kvattn.sdpa): the 8-bit
     kernel when ``cache`` just handed back exactly these keys for a short
-    query (its ``kv8_fetch``), else dequantize + sdpa over ``keys``/
-    ``values`` as given (dense tensors, or the quantized triples)."""
+    query (its ``kv8_fetch``); otherwise quantized K/V through
+    ``quantized_sdpa`` on their packed triples, and dense K/V through the
+    model's own attention function (recorded by ``patch_model``)."""
     hit = getattr(cache, "kv8_fetch", None)
     if hit is not None:
         cache.kv8_fetch = None
@@ -295,23 +302,43 @@ def sdpa(queries, keys, values, cache, scale, mask, sinks=None):
         if sinks is not None:
             raise ValueError("Quantized SDPA does not support attention sinks.")
         return quantized_sdpa(queries, keys, values, scale, mask, cache.group_size, cache.bits)
-    if sinks is not None:
-        raise ValueError("sdpa: attention sinks are not implemented")
-    from .kvcache import materialize          # a quantized cache's lazily dequantized K / V
-    return _dense_sdpa(queries, materialize(keys), materialize(values), scale, mask)
+    pk, pv = _packed(keys), _packed(values)
+    mask_ok = mask is None or isinstance(mask, str) or mask.dtype in (torch.bool, torch.bfloat16)
+    if (pk is not None and pv is not None and sinks is None and queries.dtype == torch.bfloat16
+            and pk[1:] == pv[1:] and mask_ok):
+        return quantized_sdpa(queries, pk[0], pv[0], scale, mask, pk[1], pk[2])
+    base = _BASE["fn"]
+    if base is None:
+        raise ValueError("kvattn.sdpa: dense (or fp16 / fp32) attention runs in the model's own "
+                         "scaled_dot_product_attention, which patch_model records; call patch_model first")
+    return base(queries, keys, values, cache=cache, scale=scale, mask=mask, sinks=sinks)
 
 
-def _dense_sdpa(q, k, v, scale, mask):
-    B, H, L, D = q.shape
-    rep = H // k.shape[1]
-    kf = k.float().repeat_interleave(rep, dim=1)
-    vf = v.float().repeat_interleave(rep, dim=1)
-    s = (q.float() * scale) @ kf.transpose(-1, -2)
-    N = kf.shape[2]
-    if isinstance(mask, str):
-        if L > 1:
-            rows = torch.arange(N - L, N, device=q.device)[:, None]
-            s = s.masked_fill(~(rows >= torch.arange(N, device=q.device)[None]), -math.inf)
-    elif mask is not None:
-        s = s.masked_fill(~mask.to(torch.bool), -math.inf) if mask.dtype == torch.bool else s + mask
-    return torch.softmax(s, dim=-1).nan_to_num(0.0).matmul(vf).to(q.dtype)
+def _model_modules(model):
+    if hasattr(model, "named_modules"):
+        return [m for _, m in model.named_modules()]
+    return [model]
+
+
+def patch_model(model) -> int:
+    """Rebind ``scaled_dot_product_attention`` to ``sdpa`` in every Python
+    module that defines one of the model's (sub)module classes, where it
+    is the model's original attention function (the first one met, which
+    is kept as the base for dense K/V) or already ``sdpa``.  Idempotent;
+    harmless for unquantized caches.  Returns how many modules."""
+    names = sorted({type(m).__module__ for m in _model_modules(model)} | {type(model).__module__})
+    base, n = _BASE["fn"], 0
+    for name in names:
+        mod = sys.modules.get(name)
+        f = getattr(mod, "scaled_dot_product_attention", None)
+        if f is None:
+            continue
+        if f is not sdpa:
+            if base is None:
+                base = f
+            if f is not base:
+                continue
+            mod.scaled_dot_product_attention = sdpa
+        n += 1
+    _BASE["fn"] = base
+    return n

@@ -1,22 +1,28 @@
-"""Quantized KV caches on MI355X: the reference's engine/kvquant.py
-(``QuantKVCache`` :117-188, ``BatchQuantKVCache`` :191-398, ``parse_bits`` /
-``group_for`` / ``_group`` :26-57) over torch tensors.
+"""Quantized KV caches on MI355X, with the interface of the reference's
+engine/kvquant.py: ``QuantKVCache`` (one sequence, :117-188),
+``BatchQuantKVCache`` (left-padded rows, :191-369), ``parse_bits`` /
+``group_for`` (:25-42), ``mark_kernel`` (:455-460) and the ``state`` tuples
+that from_state round-trips.
 
-Each of K and V is stored as the affine-quantized triple (packed uint32,
-scales, biases in the keys' dtype) in slabs grown 256 slots at a time.
-``update_and_fetch`` quantizes the new keys / values on the GPU straight
-into their slab slots (one ``kmi_kv_quantize_append`` launch each, the
-``mx.quantize`` arithmetic bit for bit) and returns K and V as
-``LazyDequant`` views: they become dequantized tensors the first time they
-are used as tensors, so a decode step that takes the 8-bit kernel
-(``kvattn.sdpa`` through the cache's ``kv8_fetch``) never dequantizes the
-cache -- what mlx's lazy arrays give the reference.
+Storage.  A cache owns one ``_Slabs``: the keys and the values, each an
+affine triple (packed uint32 [B, H, capacity, D*bits/32], scales and biases
+[B, H, capacity, D/group] in the keys' dtype).  Slots [0, used) hold tokens;
+capacity grows by whole 256-slot steps.  An append quantizes the new K and V
+rows on the GPU straight into their slots (``kmi_kv_quantize_append_kv``,
+the ``mx.quantize`` arithmetic bit for bit, one launch), after checking
+that the rows fit the slabs they are written into.
 
-The batched cache follows the row bookkeeping of mlx-lm's ``BatchKVCache``
-(left-padded rows, one offset per row, a shared write index ``_idx``),
-which the reference class extends; offsets and paddings are host int64
-tensors.  Neither class has a ``bits`` attribute (it is ``kv_bits``), as
-in the reference.
+Fetch.  ``update_and_fetch`` hands back K and V as ``LazyDequant`` views of
+the filled slots: they dequantize (on the GPU) only when something uses
+them as tensors.  For a short query with the 8-bit kernel on, the cache
+also leaves ``kv8_fetch = (K returned, K triple, V triple, group)`` for
+``kvattn.sdpa``, which then reads the packed slots directly.
+
+Row bookkeeping of the batched cache follows mlx-lm's BatchKVCache: every
+row ends at the shared write index ``_idx``; row b's tokens start at
+``left_padding[b]``; ``offset[b]`` is its token count (negative while only
+padding has been declared).  Offsets and paddings are host int64 tensors.
+Neither class has a ``bits`` attribute (it is ``kv_bits``).
 """
 from __future__ import annotations
 
@@ -26,131 +32,210 @@ from . import _abi
 from .ops import DTYPE_CODE, _aligned16, _on_gpu, _ptr, _stream, dequantize
 
 #: bits a person can ask for; None (or "bf16") is the unquantized cache.
-#: The GPU quantizer and the decode kernel take 8 and 4 (6 raises).
 BITS = (8, 6, 4)
 
-#: query lengths up to this hand their packed K/V to the 8-bit decode
-#: kernel (the reference's KERNEL_MAX_QUERY: decode steps only)
-KERNEL_MAX_QUERY = 1
+#: queries of up to this many tokens per sequence hand their packed K/V to
+#: the 8-bit decode kernel.  Measured on MI355X (B 4, 32 query / 4 KV heads,
+#: D 128): at L = 4 (an MTP verify) the kernel takes 23.6 us at 8k keys and
+#: 46.7 us at 32k, against 46.5 / 130 us for the packed-triple attention
+#: that serves the other cases.
+KERNEL_MAX_QUERY = 4
+
+#: slots added at a time
+STEP = 256
+
+_OFF_WORDS = ("", "bf16", "16", "none", "off")
 
 
 def parse_bits(v) -> int | None:
-    """'bf16'/''/None/16 -> None; '8'/'6'/'4' -> int.  Anything else raises."""
+    """A KV precision as a person writes it: None, "" / "bf16" / "16" /
+    "none" / "off" mean the unquantized cache (None); "8", "6", "4" (or the
+    ints) the stored width.  Anything else is a ValueError."""
     if v is None:
         return None
-    s = str(v).strip().lower()
-    if s in ("", "bf16", "16", "none", "off"):
+    text = str(v).strip().lower()
+    if text in _OFF_WORDS:
         return None
-    b = int(s)
-    if b not in BITS:
+    bits = int(text)
+    if bits not in BITS:
         raise ValueError(f"KV bits {v!r}: bf16, 8, 6 or 4")
-    return b
+    return bits
 
 
 def group_for(dim: int) -> int:
-    for g in (64, 32):
-        if dim % g == 0:
-            return g
+    """The quantization group of a head dim: 64 if it divides, else 32."""
+    if dim % 64 == 0:
+        return 64
+    if dim % 32 == 0:
+        return 32
     raise ValueError(f"head dim {dim} is not a multiple of 32: its K/V "
                      f"cannot be quantized in groups")
 
 
 def _group(dk: int, dv: int) -> int:
-    """One group size for K and V: 64 when both allow it, else 32."""
-    group_for(dk), group_for(dv)
-    return 64 if not (dk % 64 or dv % 64) else 32
+    """The one group K and V share: the smaller of their own groups."""
+    return min(group_for(dk), group_for(dv))
 
 
-# Structural ops on the packed words (cat, index, pad, gather, zeros) run
-# on int32 views: torch implements few kernels for uint32.
-def _i32(p: torch.Tensor) -> torch.Tensor:
-    return p.view(torch.int32) if p.dtype == torch.uint32 else p
+def _steps(n: int) -> int:
+    return -(-n // STEP) * STEP
 
 
-def _as(p: torch.Tensor, like_dtype) -> torch.Tensor:
-    return p.view(torch.uint32) if like_dtype == torch.uint32 else p
+# torch has few uint32 kernels (cat, index, pad, gather, roll): structural
+# moves of the packed words go through an int32 view of the same bytes.
+def _as_i32(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.int32) if t.dtype == torch.uint32 else t
 
 
-def _map(parts, fn):
-    return tuple(_as(fn(_i32(p)), p.dtype) for p in parts)
+def _like(t: torch.Tensor, ref: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.uint32) if ref.dtype == torch.uint32 else t
 
 
-def _alloc(B, H, L, dim, bits, g, dtype, device):
-    return (torch.zeros(B, H, L, dim * bits // 32, dtype=torch.int32, device=device).view(torch.uint32),
-            torch.zeros(B, H, L, dim // g, dtype=dtype, device=device),
-            torch.zeros(B, H, L, dim // g, dtype=dtype, device=device))
+def _triple_zeros(B, H, cap, dim, bits, group, dtype, device):
+    packed = torch.zeros(B, H, cap, dim * bits // 32, dtype=torch.int32, device=device).view(torch.uint32)
+    return (packed, torch.zeros(B, H, cap, dim // group, dtype=dtype, device=device),
+            torch.zeros(B, H, cap, dim // group, dtype=dtype, device=device))
 
 
-def _slice(parts, a, b):
-    return tuple(p[..., a:b, :] for p in parts)
+# the bench and the tests allocate bare triples with this
+_alloc = _triple_zeros
 
 
-def _parts(v):
-    return None if v is None else tuple(v)
-
-
-def _sliced(parts, n):
-    return None if parts is None else _slice(parts, 0, n)
-
-
-def _cat(xs, ys, dim=2):
-    return tuple(_as(torch.cat([_i32(x), _i32(y)], dim=dim), x.dtype) for x, y in zip(xs, ys))
-
-
-def _nbytes(parts) -> int:
-    return sum(p.numel() * p.element_size() for p in parts) if parts is not None else 0
+def _slab_strides(parts, x: torch.Tensor, bits: int, group: int, what: str):
+    """Check that x [B, H, S, D] can be written into the triple ``parts``
+    (the kernel only sees strides and a capacity, so a slab of another
+    batch, head count or width must be refused here), and return the six
+    element strides the launcher takes."""
+    wq, sc, bi = parts
+    if bits not in (2, 3, 4, 5, 6, 8):
+        raise ValueError(f"KV cache: {bits}-bit storage is not implemented (2, 3, 4, 5, 6, 8)")
+    if x.dtype not in DTYPE_CODE or sc.dtype != x.dtype or bi.dtype != x.dtype:
+        raise ValueError("KV cache: keys/values and the stored scales must share a float dtype")
+    if x.dim() != 4 or wq.dim() != 4 or sc.dim() != 4 or bi.dim() != 4:
+        raise ValueError(f"KV cache: {what} and its slab must be [B, H, slots, *]")
+    B, H, _, D = x.shape
+    if D % group or (D * bits) % 32:
+        raise ValueError(f"KV cache: {what} head dim {D} does not pack at {bits} bits in groups of {group}")
+    want_w = (B, H, wq.shape[2], D * bits // 32)
+    want_s = (B, H, wq.shape[2], D // group)
+    if tuple(wq.shape) != want_w or tuple(sc.shape) != want_s or tuple(bi.shape) != want_s:
+        raise ValueError(f"KV cache: {what} {tuple(x.shape)} does not fit its slab (packed "
+                         f"{tuple(wq.shape)}, scales {tuple(sc.shape)}, biases {tuple(bi.shape)})")
+    if wq.stride(-1) != 1 or sc.stride(-1) != 1 or sc.stride() != bi.stride():
+        raise ValueError("KV cache: the slab's last axis must be contiguous, scales laid out like biases")
+    return [wq.stride(0), wq.stride(1), wq.stride(2), sc.stride(0), sc.stride(1), sc.stride(2)]
 
 
 def append_quantized(parts, x: torch.Tensor, pos: int, group: int, bits: int) -> None:
     """Quantize x [B, H, S, D] along D into slots pos .. pos+S-1 of the
     triple ``parts`` (kmi_kv_quantize_append: one launch)."""
-    wq, sc, bi = parts
-    _on_gpu(x, wq, sc, bi)
-    if bits not in (2, 3, 4, 5, 6, 8):
-        raise ValueError(f"KV cache: {bits}-bit storage is not implemented (2, 3, 4, 5, 6, 8)")
-    if x.dtype not in DTYPE_CODE or sc.dtype != x.dtype or bi.dtype != x.dtype:
-        raise ValueError("KV cache: keys/values and the stored scales must share a float dtype")
-    if sc.stride(-1) != 1 or wq.stride(-1) != 1 or sc.stride() != bi.stride():
-        raise ValueError("KV cache: the slab's last axis must be contiguous, scales laid out like biases")
+    strides = torch.tensor(_slab_strides(parts, x, bits, group, "x"), dtype=torch.int64)
+    _on_gpu(x, *parts)
     B, H, S, D = x.shape
-    xc = _aligned16(x)
-    strides = torch.tensor([wq.stride(0), wq.stride(1), wq.stride(2),
-                            sc.stride(0), sc.stride(1), sc.stride(2)], dtype=torch.int64)
-    _abi.check(_abi.load().kmi_kv_quantize_append(
-        _ptr(xc), DTYPE_CODE[x.dtype], B, H, S, D, group, bits, _ptr(wq), _ptr(sc), _ptr(bi),
-        strides.data_ptr(), int(pos), wq.shape[2], _stream(x)), "kv_quantize_append")
-
-
-def _check_slab(parts, x, bits):
     wq, sc, bi = parts
-    _on_gpu(x, wq, sc, bi)
-    if bits not in (2, 3, 4, 5, 6, 8):
-        raise ValueError(f"KV cache: {bits}-bit storage is not implemented (2, 3, 4, 5, 6, 8)")
-    if x.dtype not in DTYPE_CODE or sc.dtype != x.dtype or bi.dtype != x.dtype:
-        raise ValueError("KV cache: keys/values and the stored scales must share a float dtype")
-    if sc.stride(-1) != 1 or wq.stride(-1) != 1 or sc.stride() != bi.stride():
-        raise ValueError("KV cache: the slab's last axis must be contiguous, scales laid out like biases")
-    return [wq.stride(0), wq.stride(1), wq.stride(2), sc.stride(0), sc.stride(1), sc.stride(2)]
+    _abi.check(_abi.load().kmi_kv_quantize_append(
+        _ptr(_aligned16(x)), DTYPE_CODE[x.dtype], B, H, S, D, group, bits, _ptr(wq), _ptr(sc), _ptr(bi),
+        strides.data_ptr(), int(pos), wq.shape[2], _stream(x)), "kv_quantize_append")
 
 
 def append_kv(kparts, vparts, keys: torch.Tensor, values: torch.Tensor, pos: int, group: int,
               bits: int) -> None:
-    """Both appends of one update_and_fetch (keys into ``kparts``, values
-    into ``vparts``, slots pos .. pos+S-1) in one launch
+    """Both appends of one update (keys into ``kparts``, values into
+    ``vparts``, slots pos .. pos+S-1) in one launch
     (kmi_kv_quantize_append_kv)."""
-    ks = _check_slab(kparts, keys, bits)
-    vs = _check_slab(vparts, values, bits)
+    st = _slab_strides(kparts, keys, bits, group, "keys") + _slab_strides(vparts, values, bits, group, "values")
     if keys.dtype != values.dtype or keys.shape[:3] != values.shape[:3]:
         raise ValueError("KV cache: keys and values must share dtype and [B, H, S]")
+    if kparts[0].shape[2] != vparts[0].shape[2]:
+        raise ValueError("KV cache: the key and value slabs must hold the same number of slots")
+    _on_gpu(keys, values, *kparts, *vparts)
     B, H, S, Dk = keys.shape
-    Dv = values.shape[3]
+    strides = torch.tensor(st, dtype=torch.int64)
     kc, vc = _aligned16(keys), _aligned16(values)
-    st = torch.tensor(ks + vs, dtype=torch.int64)
     _abi.check(_abi.load().kmi_kv_quantize_append_kv(
-        _ptr(kc), _ptr(vc), DTYPE_CODE[keys.dtype], B, H, S, Dk, Dv, group, bits,
-        _ptr(kparts[0]), _ptr(kparts[1]), _ptr(kparts[2]), st.data_ptr(),
-        _ptr(vparts[0]), _ptr(vparts[1]), _ptr(vparts[2]), st.data_ptr() + 6 * 8,
+        _ptr(kc), _ptr(vc), DTYPE_CODE[keys.dtype], B, H, S, Dk, values.shape[3], group, bits,
+        _ptr(kparts[0]), _ptr(kparts[1]), _ptr(kparts[2]), strides.data_ptr(),
+        _ptr(vparts[0]), _ptr(vparts[1]), _ptr(vparts[2]), strides.data_ptr() + 6 * 8,
         int(pos), kparts[0].shape[2], _stream(keys)), "kv_quantize_append")
+
+
+class _Slabs:
+    """The stored keys and values of one cache: two triples of shape
+    [B, H, capacity, *].  Every structural operation returns new slabs."""
+
+    __slots__ = ("k", "v")
+
+    def __init__(self, k, v):
+        self.k, self.v = tuple(k), tuple(v)
+
+    @classmethod
+    def empty(cls, B, H, cap, dims, bits, group, dtype, device) -> "_Slabs":
+        return cls(_triple_zeros(B, H, cap, dims[0], bits, group, dtype, device),
+                   _triple_zeros(B, H, cap, dims[1], bits, group, dtype, device))
+
+    @property
+    def tensors(self):
+        return self.k + self.v
+
+    @property
+    def capacity(self) -> int:
+        return self.k[0].shape[2]
+
+    @property
+    def rows(self) -> int:
+        return self.k[0].shape[0]
+
+    def _map(self, fn) -> "_Slabs":
+        out = [_like(fn(_as_i32(t)), t) for t in self.tensors]
+        return _Slabs(out[:3], out[3:])
+
+    def window(self, lo: int, hi: int):
+        """(K triple, V triple) views of slots lo .. hi-1."""
+        return (tuple(t[:, :, lo:hi] for t in self.k), tuple(t[:, :, lo:hi] for t in self.v))
+
+    def grown(self, keep: int, cap: int) -> "_Slabs":
+        """New slabs of ``cap`` slots whose first ``keep`` are these."""
+        def grow(t):
+            g = t.new_zeros(*t.shape[:2], cap, t.shape[3])
+            g[:, :, :keep] = t[:, :, :keep]
+            return g
+        return self._map(grow)
+
+    def take_rows(self, idx: torch.Tensor) -> "_Slabs":
+        return self._map(lambda t: t[idx.to(t.device)])
+
+    def drop_front(self, m: int) -> "_Slabs":
+        return self._map(lambda t: t[:, :, m:])
+
+    def roll_rows(self, shifts: torch.Tensor) -> "_Slabs":
+        """Row b rolled right by shifts[b] slots (wrapping)."""
+        n = self.capacity
+        src = (torch.arange(n)[None, :] - shifts[:, None]) % n          # [B, n]: slot s takes src[b, s]
+
+        def roll(t):
+            i = src.to(t.device)[:, None, :, None].expand(t.shape[0], t.shape[1], n, t.shape[3])
+            return torch.gather(t, 2, i)
+        return self._map(roll)
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in self.tensors)
+
+
+def _stack_rows(parts: list, cap: int, like: _Slabs) -> _Slabs:
+    """Slabs of sum(rows) rows and ``cap`` slots: each (slabs, shift, n) in
+    ``parts`` contributes its rows with slots 0 .. n-1 placed at shift .. ,
+    everything else zero."""
+    B = sum(s.rows for s, _, _ in parts)
+    out = []
+    for j, ref in enumerate(like.tensors):
+        dst = _as_i32(ref).new_zeros(B, ref.shape[1], cap, ref.shape[3])
+        r = 0
+        for s, shift, n in parts:
+            src = _as_i32(s.tensors[j])
+            dst[r:r + s.rows, :, shift:shift + n] = src[:, :, :n]
+            r += s.rows
+        out.append(_like(dst, ref))
+    return _Slabs(out[:3], out[3:])
 
 
 class LazyDequant:
@@ -158,7 +243,7 @@ class LazyDequant:
     view, dequantized (``mx.dequantize(...).astype(dtype)``) the first time
     it is used as a tensor -- by any torch function, operator or tensor
     attribute.  ``shape``, ``dtype``, ``device`` and ``ndim`` need no
-    dequantization."""
+    dequantization; ``parts`` / ``group`` / ``bits`` are the packed triple."""
 
     __slots__ = ("parts", "group", "bits", "_dtype", "_t")
 
@@ -253,77 +338,93 @@ def _materialized(obj):
     return obj
 
 
-def _fetch(c, n, S, kdt, vdt):
-    """What ``update_and_fetch`` returns (K, V over slots 0 .. n-1, lazily
-    dequantized) and, for a short 8-bit query with the kernel on, what
-    ``kvattn.sdpa`` needs (the reference's _fetch, kvquant.py:89-104)."""
-    g, bits = c.group, c.kv_bits
-    K, V = _slice(c.keys, 0, n), _slice(c.values, 0, n)
-    k, v = LazyDequant(K, g, bits, kdt), LazyDequant(V, g, bits, vdt)
-    if getattr(c, "kv8_fetch", None) is not None:
-        # handed out last step and never taken: its attention did not go
-        # through kvattn.sdpa
-        from . import kvattn
-        kvattn.count(False, "the attention never asked for it")
-    c.kv8_fetch = None
-    if c.kv8_kernel and bits == 8 and S <= KERNEL_MAX_QUERY:
-        c.kv8_fetch = (k, K, V, g)
-    return k, v
+class _QuantStore:
+    """What both caches share: the slabs, their metadata and the update."""
+
+    step = STEP
+    slabs = None
+    #: hand the packed K/V to the 8-bit decode kernel (kvattn.sdpa); per
+    #: cache, set by kvattn.install's make_cache and carried by merge /
+    #: extract / extend
+    kv8_kernel = False
+    kv8_fetch = None
+
+    def _init_store(self, kv_bits) -> None:
+        self.slabs = None
+        self.kv_bits = int(kv_bits)
+        self.group = None
+        self.dims = None               # (key head dim, value head dim)
+
+    # the triples as attributes (the reference's `keys` / `values`)
+    @property
+    def keys(self):
+        return None if self.slabs is None else self.slabs.k
+
+    @property
+    def values(self):
+        return None if self.slabs is None else self.slabs.v
+
+    def _set_parts(self, k, v) -> None:
+        self.slabs = None if k is None else _Slabs(k, v)
+
+    def _append(self, keys: torch.Tensor, values: torch.Tensor, at: int):
+        """Write S new tokens at slot ``at`` (growing the slabs first when
+        they are full) and return what update_and_fetch returns."""
+        B, H, S, Dk = keys.shape
+        if self.group is None:
+            self.dims = (Dk, values.shape[3])
+            self.group = _group(*self.dims)
+        if self.slabs is None:
+            self.slabs = _Slabs.empty(B, H, _steps(S), self.dims, self.kv_bits, self.group, keys.dtype,
+                                      keys.device)
+        elif at + S > self.slabs.capacity:
+            self.slabs = self.slabs.grown(at, at + _steps(S))
+        append_kv(self.slabs.k, self.slabs.v, keys, values, at, self.group, self.kv_bits)
+        return self._fetch(at + S, S, keys.dtype, values.dtype)
+
+    def _fetch(self, used: int, S: int, kdt, vdt):
+        K, V = self.slabs.window(0, used)
+        k = LazyDequant(K, self.group, self.kv_bits, kdt)
+        v = LazyDequant(V, self.group, self.kv_bits, vdt)
+        if self.kv8_fetch is not None:
+            # left by the previous step and never picked up: that step's
+            # attention did not go through kvattn.sdpa
+            from . import kvattn
+            kvattn.count(False, "the attention never asked for it")
+        hand = self.kv8_kernel and self.kv_bits == 8 and S <= KERNEL_MAX_QUERY
+        self.kv8_fetch = (k, K, V, self.group) if hand else None
+        return k, v
+
+    def is_trimmable(self) -> bool:
+        return True
+
+    def empty(self) -> bool:
+        return self.slabs is None
+
+    def to_quantized(self, *a, **k):
+        raise TypeError("already quantized")
+
+    @property
+    def nbytes(self) -> int:
+        return 0 if self.slabs is None else self.slabs.nbytes()
 
 
-def _grow(c, prev, B, H, S, Dk, Dv, dtype, device):
-    """Room for S more slots after ``prev``: a new slab rounded up to 256
-    slots, appended to the kept prefix (kvquant.py:143-151)."""
-    g, bits = c.group, c.kv_bits
-    if c.keys is None or prev + S > c.keys[0].shape[2]:
-        n = (c.step + S - 1) // c.step * c.step
-        nk = _alloc(B, H, n, Dk, bits, g, dtype, device)
-        nv = _alloc(B, H, n, Dv, bits, g, dtype, device)
-        if c.keys is None:
-            c.keys, c.values = nk, nv
-        else:
-            c.keys = _cat(_slice(c.keys, 0, prev), nk)
-            c.values = _cat(_slice(c.values, 0, prev), nv)
-
-
-class QuantKVCache:
+class QuantKVCache(_QuantStore):
     """One sequence's attention cache, stored quantized.  ``keys`` /
     ``values`` are (packed, scales, biases) triples [B, H, slots, *];
     ``update_and_fetch`` returns K/V of the dtype it was given."""
 
-    step = 256
-    #: this cache hands its packed K/V to the 8-bit decode kernel
-    #: (kvattn.sdpa); per cache, carried by merge / extract / extend
-    kv8_kernel = False
-    kv8_fetch = None
-
     def __init__(self, kv_bits: int = 8):
-        self.keys = self.values = None
+        self._init_store(kv_bits)
         self.offset = 0
-        self.kv_bits = int(kv_bits)
-        self.group = None
-        self.dims = None               # (k head dim, v head dim)
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
-        B, H, S, Dk = keys.shape
-        Dv = values.shape[3]
-        if self.group is None:
-            self.group = _group(Dk, Dv)
-            self.dims = (Dk, Dv)
-        prev = self.offset
-        _grow(self, prev, B, H, S, Dk, Dv, keys.dtype, keys.device)
-        self.offset += S
-        append_kv(self.keys, self.values, keys, values, prev, self.group, self.kv_bits)
-        return _fetch(self, self.offset, S, keys.dtype, values.dtype)
+        at = self.offset
+        self.offset += keys.shape[2]
+        return self._append(keys, values, at)
 
     def size(self) -> int:
         return self.offset
-
-    def empty(self) -> bool:
-        return self.keys is None
-
-    def is_trimmable(self) -> bool:
-        return True
 
     def trim(self, n: int) -> int:
         n = min(self.offset, n)
@@ -332,90 +433,42 @@ class QuantKVCache:
 
     @property
     def state(self):
-        return (_sliced(self.keys, self.offset), _sliced(self.values, self.offset), self.offset,
-                self.kv_bits, self.group or 0, bool(self.kv8_kernel))
+        K, V = (None, None) if self.slabs is None else self.slabs.window(0, self.offset)
+        return K, V, self.offset, self.kv_bits, self.group or 0, bool(self.kv8_kernel)
 
     @state.setter
     def state(self, v):
-        k, vv, self.offset, bits, g, kernel = v
-        self.keys, self.values = _parts(k), _parts(vv)
-        self.kv_bits, self.group = int(bits), (int(g) or None)
-        self.kv8_kernel = bool(kernel)
-        if self.keys is not None and self.dims is None:
-            self.dims = (self.keys[0].shape[3] * 32 // self.kv_bits,
-                         self.values[0].shape[3] * 32 // self.kv_bits)
-
-    def to_quantized(self, *a, **k):
-        raise TypeError("already quantized")
+        k, vv, offset, bits, group, kernel = v
+        self._set_parts(k, vv)
+        self.offset, self.kv_bits = offset, int(bits)
+        self.group, self.kv8_kernel = int(group) or None, bool(kernel)
+        self.dims = None if k is None else (k[0].shape[3] * 32 // self.kv_bits,
+                                            vv[0].shape[3] * 32 // self.kv_bits)
 
     @classmethod
     def merge(cls, caches):
         return BatchQuantKVCache.merge(caches)
 
-    @property
-    def nbytes(self) -> int:
-        return _nbytes(self.keys) + _nbytes(self.values)
 
-
-def _carry(out, caches):
-    """``out`` takes the kernel setting of the caches it was built from."""
-    out.kv8_kernel = any(getattr(c, "kv8_kernel", False) for c in caches)
-    return out
-
-
-def _roll_rows(p: torch.Tensor, shifts: torch.Tensor) -> torch.Tensor:
-    """Each batch row b of p rolled by shifts[b] along the slot axis
-    (mlx-lm's dynamic_roll on axis 2)."""
-    n = p.shape[2]
-    idx = (torch.arange(n)[None, :] - shifts[:, None]) % n              # [B, n]
-    idx = idx.to(p.device)[:, None, :, None].expand(p.shape[0], p.shape[1], n, p.shape[3])
-    return _as(torch.gather(_i32(p), 2, idx), p.dtype)
-
-
-class BatchQuantKVCache:
-    """Left-padded rows (one offset per row, a shared write index
-    ``_idx``), stored quantized: the reference's BatchQuantKVCache over
-    mlx-lm's BatchKVCache row bookkeeping."""
-
-    step = 256
-    kv8_kernel = False
-    kv8_fetch = None
+class BatchQuantKVCache(_QuantStore):
+    """Left-padded rows sharing one write index ``_idx`` (mlx-lm's
+    BatchKVCache bookkeeping), stored quantized."""
 
     def __init__(self, left_padding, kv_bits: int = 8):
-        self.keys = self.values = None
-        self.left_padding = torch.as_tensor(list(left_padding), dtype=torch.int64)
-        self.offset = -self.left_padding.clone()
+        self._init_store(kv_bits)
+        self.left_padding = torch.tensor([int(p) for p in left_padding], dtype=torch.int64)
+        self.offset = -self.left_padding
         self._idx = 0
         self._right_padding = None
-        self.kv_bits = int(kv_bits)
-        self.group = None
-        self.dims = None
-
-    def _meta_from(self, o) -> None:
-        if self.group is None and getattr(o, "group", None) is not None:
-            self.group, self.dims = o.group, o.dims
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
-        B, H, S, Dk = keys.shape
-        Dv = values.shape[3]
-        if self.group is None:
-            self.group = _group(Dk, Dv)
-            self.dims = (Dk, Dv)
-        prev = self._idx
-        _grow(self, prev, B, H, S, Dk, Dv, keys.dtype, keys.device)
-        self.offset = self.offset + S
+        at, S = self._idx, keys.shape[2]
         self._idx += S
-        append_kv(self.keys, self.values, keys, values, prev, self.group, self.kv_bits)
-        return _fetch(self, self._idx, S, keys.dtype, values.dtype)
+        self.offset = self.offset + S
+        return self._append(keys, values, at)
 
     def size(self) -> int:
         return self._idx
-
-    def empty(self) -> bool:
-        return self.keys is None
-
-    def is_trimmable(self) -> bool:
-        return True
 
     def trim(self, n: int) -> int:
         n = min(self._idx, n)
@@ -424,157 +477,199 @@ class BatchQuantKVCache:
         return n
 
     def prepare(self, *, left_padding=None, lengths=None, right_padding=None):
-        """Rows right-padded in the next update are rolled back into place
-        by ``finalize`` (mlx-lm's prepare; only right_padding is kept)."""
+        """Declare more left padding (empty cache only), or right padding of
+        the next update, which ``finalize`` rolls back into place."""
         if left_padding is not None:
-            if self.keys is not None:
+            if self.slabs is not None:
                 raise ValueError("left padding can only be added to an empty cache")
-            lp = torch.as_tensor(list(left_padding), dtype=torch.int64)
-            self.left_padding = self.left_padding + lp
-            self.offset = self.offset - lp
+            extra = torch.tensor([int(p) for p in left_padding], dtype=torch.int64)
+            self.left_padding = self.left_padding + extra
+            self.offset = self.offset - extra
         if right_padding is not None and max(right_padding) > 0:
-            self._right_padding = torch.as_tensor(list(right_padding), dtype=torch.int64)
+            self._right_padding = torch.tensor([int(p) for p in right_padding], dtype=torch.int64)
 
     def finalize(self):
-        if self._right_padding is not None:
-            pad = self._right_padding
-            self.keys = tuple(_roll_rows(p, pad) for p in self.keys)
-            self.values = tuple(_roll_rows(p, pad) for p in self.values)
-            self.offset = self.offset - pad
-            self.left_padding = self.left_padding + pad
-            self._right_padding = None
+        pad, self._right_padding = self._right_padding, None
+        if pad is None:
+            return
+        self.slabs = self.slabs.roll_rows(pad)
+        self.offset = self.offset - pad
+        self.left_padding = self.left_padding + pad
 
     def make_mask(self, L: int, device=None) -> torch.Tensor:
-        """bool [B, 1, L, _idx + L]: what each of the next L query rows may
-        see once they are appended -- its own row's keys from its left
-        padding on, causal inside the new block."""
-        N = self._idx + L
-        n = torch.arange(N)[None, None, :]
-        rows = self._idx + torch.arange(L)[None, :, None]
-        m = (n >= self.left_padding[:, None, None]) & (n <= rows)
+        """bool [B, 1, L, _idx + L]: query row l of the next L tokens sees
+        its own row's slots from the row's left padding up to itself."""
+        n = torch.arange(self._idx + L)
+        first = self.left_padding[:, None, None]                       # [B, 1, 1]
+        last = (self._idx + torch.arange(L))[None, :, None]             # [1, L, 1]
+        m = (n[None, None, :] >= first) & (n[None, None, :] <= last)
         return m[:, None].to(device if device is not None else "cpu")
 
     @property
     def state(self):
+        K, V = (None, None) if self.slabs is None else self.slabs.window(0, self._idx)
         dk, dv = self.dims or (0, 0)
-        return (_sliced(self.keys, self._idx), _sliced(self.values, self._idx), self.offset,
-                self.left_padding, self._idx, self.kv_bits, self.group or 0, dk, dv,
+        return (K, V, self.offset, self.left_padding, self._idx, self.kv_bits, self.group or 0, dk, dv,
                 bool(self.kv8_kernel))
 
     @state.setter
     def state(self, v):
-        (k, vv, self.offset, self.left_padding, self._idx, bits, g, dk, dv, kernel) = v
-        self.keys, self.values = _parts(k), _parts(vv)
-        self.kv_bits, self.group = int(bits) or 8, (int(g) or None)
+        k, vv, self.offset, self.left_padding, self._idx, bits, group, dk, dv, kernel = v
+        self._set_parts(k, vv)
+        self.kv_bits, self.group = int(bits) or 8, int(group) or None
         self.dims = (int(dk), int(dv)) if dk else None
         self.kv8_kernel = bool(kernel)
-        if not hasattr(self, "_right_padding"):
-            self._right_padding = None
+        self._right_padding = getattr(self, "_right_padding", None)
 
     def filter(self, batch_indices):
-        bi = torch.as_tensor(batch_indices, dtype=torch.int64)
-        if self.keys is not None:
-            sel = bi.to(self.keys[0].device)
-            self.keys = _map(self.keys, lambda p: p[sel])
-            self.values = _map(self.values, lambda p: p[sel])
-        self.offset = self.offset[bi]
-        self.left_padding = self.left_padding[bi]
-        m = int(self.left_padding.min().item())
-        if m > 0:
-            if self.keys is not None:
-                self.keys = _slice(self.keys, m, None)
-                self.values = _slice(self.values, m, None)
-            self._idx -= m
-            self.left_padding = self.left_padding - m
-
-    def _empty_parts(self, B, H, dt, device):
-        Dk, Dv = self.dims
-        g, bits = self.group, self.kv_bits
-        return (_alloc(B, H, 0, Dk, bits, g, dt, device), _alloc(B, H, 0, Dv, bits, g, dt, device))
+        """Keep the rows ``batch_indices``, then drop the slots every kept
+        row has as padding."""
+        keep = torch.as_tensor(batch_indices, dtype=torch.int64)
+        self.offset, self.left_padding = self.offset[keep], self.left_padding[keep]
+        if self.slabs is not None:
+            self.slabs = self.slabs.take_rows(keep)
+        common = int(self.left_padding.min())
+        if common > 0:
+            if self.slabs is not None:
+                self.slabs = self.slabs.drop_front(common)
+            self._idx -= common
+            self.left_padding = self.left_padding - common
 
     def extend(self, other):
-        if self.keys is None and other.keys is None:
-            self.left_padding = torch.cat([self.left_padding, other.left_padding])
-            self.offset = torch.cat([self.offset, other.offset])
-            return
-        self._meta_from(other)
+        """Append ``other``'s rows: both caches' rows are shifted right so
+        they end at the larger write index."""
         self.kv8_kernel = self.kv8_kernel or other.kv8_kernel
-        other._meta_from(self)
-        src = self if self.keys is not None else other
-        H, dt, dev = src.keys[0].shape[1], src.keys[1].dtype, src.keys[0].device
-        max_idx = max(self._idx, other._idx)
-        size = max(c.keys[0].shape[2] for c in (self, other) if c.keys is not None)
-
-        def pad(c):
-            if c.keys is None:
-                k, v = c._empty_parts(c.offset.shape[0], H, dt, dev)
-            else:
-                k, v = c.keys, c.values
-            left = max_idx - c._idx
-            right = size - k[0].shape[2] - left
-            if right < 0:
-                k, v = _slice(k, 0, right), _slice(v, 0, right)
-                right = 0
-            if left or right:
-                k = _map(k, lambda p: torch.nn.functional.pad(p, (0, 0, left, right)))
-                v = _map(v, lambda p: torch.nn.functional.pad(p, (0, 0, left, right)))
-            return k, v, c.offset, c.left_padding + left
-
-        (k1, v1, o1, l1), (k2, v2, o2, l2) = pad(self), pad(other)
-        self.keys = _cat(k1, k2, dim=0)
-        self.values = _cat(v1, v2, dim=0)
-        self.offset = torch.cat([o1, o2])
-        self.left_padding = torch.cat([l1, l2])
-        self._idx = max_idx
+        for a, b in ((self, other), (other, self)):
+            if a.group is None and b.group is not None:
+                a.group, a.dims = b.group, b.dims
+        idx = max(self._idx, other._idx)
+        shifts = (idx - self._idx, idx - other._idx)
+        held = [c for c in (self, other) if c.slabs is not None]
+        if held:
+            like = held[0].slabs
+            cap = max([idx] + [c.slabs.capacity for c in held])
+            parts = []
+            for c, sh in zip((self, other), shifts):
+                s = c.slabs
+                if s is None:
+                    s = _Slabs.empty(c.offset.shape[0], like.k[0].shape[1], 0, c.dims, c.kv_bits, c.group,
+                                     like.k[1].dtype, like.k[0].device)
+                parts.append((s, sh, c._idx))
+            self.slabs = _stack_rows(parts, cap, like)
+        self.left_padding = torch.cat([self.left_padding + shifts[0], other.left_padding + shifts[1]])
+        self.offset = torch.cat([self.offset, other.offset])
+        self._idx = idx
 
     def extract(self, idx: int) -> QuantKVCache:
+        """Row ``idx`` as a single-sequence cache holding only its tokens."""
         c = QuantKVCache(self.kv_bits)
-        c.kv8_kernel = self.kv8_kernel
-        c.group, c.dims = self.group, self.dims
-        pad = int(self.left_padding[idx].item())
-        if self.keys is not None:
-            c.keys = _map(self.keys, lambda p: p[idx:idx + 1, :, pad:self._idx].contiguous())
-            c.values = _map(self.values, lambda p: p[idx:idx + 1, :, pad:self._idx].contiguous())
-            c.offset = c.keys[0].shape[2]
+        c.kv8_kernel, c.group, c.dims = self.kv8_kernel, self.group, self.dims
+        if self.slabs is not None:
+            lo = int(self.left_padding[idx])
+            k, v = self.slabs.window(lo, self._idx)
+            c.slabs = _Slabs([t[idx:idx + 1].contiguous() for t in k], [t[idx:idx + 1].contiguous() for t in v])
+            c.offset = self._idx - lo
         return c
 
     @classmethod
     def merge(cls, caches):
-        bits = next(c.kv_bits for c in caches)
+        """One batched cache of the given single-sequence caches, each row
+        right-aligned at the longest one's length."""
+        caches = list(caches)
+        bits = caches[0].kv_bits
         lengths = [c.size() for c in caches]
-        L = max(lengths)
-        if L == 0:
-            return _carry(cls([0] * len(caches), bits), caches)
-        first = next(c for c in caches if c.keys is not None)
-        pad = [L - n for n in lengths]
-        B = len(caches)
-        H = first.keys[0].shape[1]
-        dev = first.keys[0].device
-        keys = _map(first.keys, lambda p: torch.zeros(B, H, L, p.shape[3], dtype=p.dtype, device=dev))
-        values = _map(first.values, lambda p: torch.zeros(B, H, L, p.shape[3], dtype=p.dtype, device=dev))
-        for i, (p, c) in enumerate(zip(pad, caches)):
-            if c.keys is None:
-                continue
-            for dst, src in ((keys, c.keys), (values, c.values)):
-                for d, s in zip(dst, src):
-                    _i32(d)[i:i + 1, :, p:p + c.offset] = _i32(s)[..., :c.offset, :]
-        out = _carry(cls(pad, bits), caches)
+        longest = max(lengths)
+        out = cls([longest - n for n in lengths], bits)
+        out.kv8_kernel = any(getattr(c, "kv8_kernel", False) for c in caches)
+        if longest == 0:
+            return out
+        first = next(c for c in caches if c.slabs is not None)
         out.group, out.dims = first.group, first.dims
-        out.keys, out.values = keys, values
-        out.offset = out.offset + L
-        out._idx = L
+        parts = []
+        for c, n in zip(caches, lengths):
+            s = c.slabs if c.slabs is not None else _Slabs.empty(
+                1, first.slabs.k[0].shape[1], 0, first.dims, bits, first.group, first.slabs.k[1].dtype,
+                first.slabs.k[0].device)
+            parts.append((s, longest - n, n))
+        out.slabs = _stack_rows(parts, longest, first.slabs)
+        out.offset = out.offset + longest
+        out._idx = longest
         return out
-
-    @property
-    def nbytes(self) -> int:
-        return _nbytes(self.keys) + _nbytes(self.values)
 
 
 def mark_kernel(caches) -> None:
-    """Let the quantized caches in ``caches`` hand their packed K/V to the
-    8-bit decode kernel (the reference's mark_kernel, kvquant.py:452-460)."""
+    """Let the quantized caches in ``caches`` (and inside cache lists) hand
+    their packed K/V to the 8-bit decode kernel."""
     for c in caches:
-        if isinstance(c, (QuantKVCache, BatchQuantKVCache)):
+        if isinstance(c, _QuantStore):
             c.kv8_kernel = True
-        elif isinstance(getattr(c, "caches", None), (tuple, list)):
-            mark_kernel(c.caches)
+        else:
+            inner = getattr(c, "caches", None)
+            if isinstance(inner, (tuple, list)):
+                mark_kernel(inner)
+
+
+def _plain_empty(c) -> bool:
+    """An unquantized, still-empty cache of the kind a model's make_cache
+    builds: a class named KVCache (mlx-lm's, or a port's) holding no keys."""
+    return type(c).__name__ == "KVCache" and getattr(c, "keys", None) is None
+
+
+def quantize_cache_list(caches, bits: int, table=None):
+    """(new list, how many were quantized): each empty plain ``KVCache``
+    becomes a ``QuantKVCache(bits)``; a cache whose class is a key of
+    ``table`` ({class: factory(bits)}, a family's own attention caches)
+    becomes what its factory builds; a cache list (a ``caches`` tuple or
+    list) is rebuilt from its converted members.  Everything else -- caches
+    already holding tokens, recurrent state -- passes through."""
+    table = table or {}
+    count = 0
+
+    def convert(c):
+        nonlocal count
+        make = table.get(type(c))
+        if make is not None and getattr(c, "keys", None) is None:
+            count += 1
+            return make(bits)
+        if _plain_empty(c):
+            count += 1
+            return QuantKVCache(bits)
+        inner = getattr(c, "caches", None)
+        if isinstance(inner, (tuple, list)):
+            return type(c)(*(convert(m) for m in inner))
+        return c
+
+    return [convert(c) for c in caches], count
+
+
+def install(model, bits, table=None) -> int:
+    """Wrap ``model.make_cache`` so every new cache list stores attention
+    K/V at ``bits`` (8, 6 or 4), and rebind the model's attention modules
+    to ``kvattn.sdpa``.  At 8 bits with the kernel enabled (``kvattn.ENV``)
+    the new caches hand their packed K/V to the decode kernel;
+    ``model.kv8_kernel`` records whether.  Returns how many caches
+    of a probe list are quantized (0: none of this model's caches can be,
+    and nothing is wrapped)."""
+    bits = parse_bits(bits)
+    if bits is None:
+        return 0
+    build = model.make_cache
+    _, n = quantize_cache_list(build(), bits, table)
+    if n == 0:
+        return 0
+    from . import kvattn
+    # attention goes through kvattn.sdpa at every width (the packed-triple
+    # path serves what the kernel does not take); the kernel needs 8 bits
+    patched = kvattn.patch_model(model)
+    kernel = bits == 8 and kvattn.enabled() and patched > 0
+    kvattn.reset(kernel)
+    model.kv8_kernel = kernel
+
+    def make_cache():
+        caches = quantize_cache_list(build(), bits, table)[0]
+        if kernel:
+            mark_kernel(caches)
+        return caches
+
+    model.make_cache = make_cache
+    return n

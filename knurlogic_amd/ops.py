@@ -65,6 +65,15 @@ def _check_mx(what, scales, biases, group_size, bits, mode):
         raise ValueError(f"{what}: {mode} takes group_size 32 and {_MX_BITS[mode]} bits")
 
 
+def _resolve(group_size, bits, mode: str):
+    """mlx's mode-dependent defaults for an omitted group_size / bits: affine
+    64 and 4, mxfp4 32 and 4, mxfp8 32 and 8."""
+    if mode in _MX_BITS:
+        return (32 if group_size is None else int(group_size),
+                _MX_BITS[mode] if bits is None else int(bits))
+    return 64 if group_size is None else int(group_size), 4 if bits is None else int(bits)
+
+
 def _workspace(nbytes: int, device) -> torch.Tensor | None:
     if nbytes == 0:
         return None
@@ -78,13 +87,19 @@ def _aligned16(t: torch.Tensor) -> torch.Tensor:
     return t.clone() if t.data_ptr() % 16 else t
 
 
-def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4,
+def quantize(w: torch.Tensor, group_size: int | None = None, bits: int | None = None,
              mode: str = "affine"):
     """``mx.quantize``: (wq uint32 [..., K*bits/32], scales, biases
-    [..., K/group_size]) in w's dtype, groups along the last axis.  mxfp4 /
-    mxfp8: (wq, scales uint8 E8M0), group 32 (mlx returns no biases)."""
+    [..., K/group_size]) in w's dtype, groups along the last axis (omitted
+    group_size / bits: 64 and 4).  mxfp4 / mxfp8: (wq, scales uint8 E8M0),
+    group 32 and 4 / 8 bits, which are also the only values taken (mlx
+    returns no biases)."""
     _check_mode(mode, allow_mx=True)
+    group_size, bits = _resolve(group_size, bits, mode)
     if mode != "affine":
+        if group_size != 32 or bits != _MX_BITS[mode]:
+            raise ValueError(f"quantize: {mode} takes group_size 32 and {_MX_BITS[mode]} bits "
+                             f"(got {group_size} and {bits})")
         _on_gpu(w)
         if w.dtype not in DTYPE_CODE or w.ndim < 1 or w.shape[-1] % 32:
             raise ValueError(f"quantize: {mode} needs a float tensor whose last axis is a multiple of 32")
@@ -118,13 +133,14 @@ def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4,
 
 
 def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor | None = None,
-               group_size: int = 64, bits: int = 4, mode: str = "affine",
+               group_size: int | None = None, bits: int | None = None, mode: str = "affine",
                dtype: torch.dtype | None = None, rounding: int = ROUND_OP_BY_OP):
     """``mx.dequantize``: scale * q + bias in ``dtype`` (default: scales'
     dtype).  ``rounding`` picks the storage rounding order.  mxfp4 / mxfp8:
     element * 2^(scale - 127), uint8 E8M0 scales, no biases (default dtype
-    bfloat16)."""
+    bfloat16).  Omitted group_size / bits take mlx's defaults for the mode."""
     _check_mode(mode, allow_mx=True)
+    group_size, bits = _resolve(group_size, bits, mode)
     if mode != "affine":
         _check_mx("dequantize", scales, biases, group_size, bits, mode)
         _on_gpu(w, scales)
@@ -200,14 +216,16 @@ def _check_affine_operands(x, w, scales, biases, group_size, bits, what):
 
 def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                      biases: torch.Tensor | None = None, transpose: bool = True,
-                     group_size: int = 64, bits: int = 4, mode: str = "affine"):
+                     group_size: int | None = None, bits: int | None = None, mode: str = "affine"):
     """``mx.quantized_matmul``: x [..., M, K] @ What^T with What [..., N, K]
     (transpose=True) or x @ What with What [..., K, N] (transpose=False,
     groups along N), fp32 accumulation, the result in x's dtype.  A 2-D
     What at 4 or 8 bits with transpose=True is the dense projection
     (kmi_qmm); a batched What (leading dimensions broadcast against x's),
-    transpose=False or the 2, 3, 5 and 6-bit widths run kmi_qmm_batched."""
+    transpose=False or the 2, 3, 5 and 6-bit widths run kmi_qmm_batched.
+    Omitted group_size / bits take mlx's defaults for the mode."""
     _check_mode(mode, allow_mx=True)
+    group_size, bits = _resolve(group_size, bits, mode)
     if not transpose or w.ndim != 2 or bits not in (4, 8) or mode != "affine":
         return qmm_batched(x, w, scales, biases, transpose, group_size, bits, mode=mode)
     _check_affine_operands(x, w, scales, biases, group_size, bits, "quantized_matmul")
@@ -287,8 +305,8 @@ def row_padded(t: torch.Tensor) -> bool:
     return last + (Np - N) < t.untyped_storage().nbytes() // t.element_size()
 
 
-def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 64,
-                bits: int = 4, x_scale: float = 1.0, out=None, mode: str = "affine"):
+def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int | None = None,
+                bits: int | None = None, x_scale: float = 1.0, out=None, mode: str = "affine"):
     """mx.quantized_matmul with batch dimensions on w (broadcast against
     x's) in either orientation; ``x_scale`` != 1 multiplies x by it first,
     rounded to x's dtype (mlx-lm's ``queries *= scale``).  ``out``: a
@@ -297,6 +315,7 @@ def qmm_batched(x, w, scales, biases, transpose: bool = True, group_size: int = 
     scales, no biases."""
     what = "quantized_matmul"
     _check_mode(mode, allow_mx=True)
+    group_size, bits = _resolve(group_size, bits, mode)
     if mode != "affine":
         _check_mx(what, scales, biases, group_size, bits, mode)
         _on_gpu(x, w, scales)
@@ -465,7 +484,7 @@ def _flat_indices(x, w, lhs_indices, rhs_indices):
 
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                biases: torch.Tensor | None = None, lhs_indices=None, rhs_indices=None,
-               transpose: bool = True, group_size: int = 64, bits: int = 4,
+               transpose: bool = True, group_size: int | None = None, bits: int | None = None,
                mode: str = "affine", sorted_indices: bool = False):
     """``mx.gather_qmm``: out[i] = x[lhs[i]] @ What[rhs[i]]^T for x
     [..., M, K] and w [..., N, K*bits/32]; out [*broadcast(lhs, rhs), M, N].
@@ -474,6 +493,7 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     modes (uint8 E8M0 scales, no biases) run the batched kernel's gather
     form, either orientation."""
     _check_mode(mode, allow_mx=True)
+    group_size, bits = _resolve(group_size, bits, mode)
     if x.ndim < 2 or w.ndim < 3:
         raise ValueError("gather_qmm: x needs [..., M, K] and w [..., N, K*bits/32]")
     if mode != "affine":

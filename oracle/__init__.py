@@ -32,6 +32,9 @@ sites, and pinned as follows (each function's docstring names its pins):
 * mxfp4 / mxfp8 -- the OCP MX element and scale encodings, pinned by the
   spec's known answers (E2M1 table, E4M3 extremes and NaN, E8M0 powers of
   two).  How mlx orders the packed codes is its 4 / 8-bit affine order.
+  mx quantize follows the OCP conversion rule (shared exponent, ties to
+  even, saturation, the sign of zero kept): parity with mlx's quantizer
+  is unpinned; hand-computed codes check the rule as stated.
 * quantized attention (mlx-lm's base.py:260-302) -- float64 attention
   (``sdpa_numpy_f64``) within the bf16 roundings the path makes, and the
   exact uniform softmax of a fully hidden row.
@@ -306,7 +309,8 @@ def quantized_sdpa(q, K, V, scale: float, mask=None, group_size: int = 64, bits:
     B, Hq, L, D = q.shape
     Hk = np.asarray(K[0]).shape[-3]
     rep = Hq // Hk
-    qs = bf16_round(q * np.float32(scale))
+    # mlx casts the Python scalar to the queries' dtype before `queries *= scale`
+    qs = bf16_round(q * bf16_round(np.float32(scale)))
     Ke, Ve = tuple(K), tuple(V)
     if rep > 1:
         qs = qs.reshape(B, Hk, rep, L, D)
@@ -373,8 +377,14 @@ def mx_quantize(w, mode: str):
     8 for E4M3), E8M0 byte X + 127 (clamped to 0..254; an all-zero group
     takes 0), elements w / 2^X rounded to nearest (ties to the even code)
     and saturated to the largest finite element, the input's sign kept
-    (negative zeros included).  -> (wq uint32, scales uint8).  Pinned by the reference's mxfp4 checkpoint: re-quantizing its
-    decoded values gives back its codes and scales."""
+    (negative zeros included).  -> (wq uint32, scales uint8).
+
+    Parity unpinned: this is the OCP MX v1.0 conversion, and mlx's own
+    quantizer is not in the reference tree.  The reference's mxfp4
+    checkpoint holds random codes under random scales, all on the grid, so
+    re-quantizing it checks only the shared exponent of groups whose
+    largest code is 4 or 6 -- not ties, saturation or the sign of zero;
+    those are checked against hand-computed codes (tests/test_oracle.py)."""
     w = np.asarray(w, np.float64)
     rows = w.reshape(-1, w.shape[-1])
     G = rows.shape[1] // 32
@@ -423,18 +433,34 @@ def mx_quantized_matmul(x, wq, scales, mode: str, transpose: bool = True,
 
 def route(logits, k: int, out_dtype: str = "bfloat16"):
     """SparseMoeBlock's router (src/knurlogic/engine/families/qwen/
-    architecture/qwen3_5.py:174-179): softmax of the logits in float32,
-    top-k, renormalize in float32, round to the logits' dtype.  The top-k
-    set is order-free (argpartition); ties go to the lower expert index.
+    architecture/qwen3_5.py:174-179): ``probs = mx.softmax(logits.astype(
+    float32))``, top-k, ``scores / scores.sum()`` in float32, rounded to the
+    logits' dtype.
+
+    The softmax follows mlx 0.32.3's CPU kernel for a float32 row
+    (mlx/backend/cpu/softmax.cpp, ``softmax<float, float>``), one float32
+    rounding per step: m = max(x); e_i = exp(x_i - m); n = sum(e); r = 1/n
+    (the normaliser is inverted once); p_i = e_i * r.  The renormalisation
+    is two float32 array ops: t = sum of the k selected p, score = p / t.
+    Two parts are fixed here where mlx's own code cannot be matched bit for
+    bit without it: exp is the correctly rounded float32 exp (mlx uses its
+    SIMD polynomial, within a few ulp), and both sums are the exact sum
+    rounded once to float32 (mlx adds in SIMD-lane order).  Differences of
+    an ulp or two in float32 only reach the rounded scores at a bf16 / fp16
+    rounding boundary.  The top-k set is order-free (argpartition); ties go
+    to the lower expert index.
     Returns (inds [T, k] int32 in descending-probability order, scores)."""
-    lg = np.asarray(logits, np.float64)
-    p = np.exp(lg - lg.max(axis=-1, keepdims=True))
-    p = (p / p.sum(axis=-1, keepdims=True)).astype(np.float32)
+    x = np.asarray(logits, np.float32)
+    m = x.max(axis=-1, keepdims=True)
+    e = np.exp((x - m).astype(np.float64)).astype(np.float32)
+    n = e.astype(np.float64).sum(axis=-1, keepdims=True).astype(np.float32)
+    r = np.float32(1.0) / n
+    p = e * r
     # stable descending order: larger prob first, lower index on ties
     order = np.argsort(-p, axis=-1, kind="stable")[..., :k]
-    top = np.take_along_axis(p, order, axis=-1).astype(np.float64)
-    scores = top / top.sum(axis=-1, keepdims=True)
-    return order.astype(np.int32), round_to(scores.astype(np.float32), out_dtype)
+    top = np.take_along_axis(p, order, axis=-1)
+    t = top.astype(np.float64).sum(axis=-1, keepdims=True).astype(np.float32)
+    return order.astype(np.int32), round_to(top / t, out_dtype)
 
 
 def silu_rounded(g, dtype: str = "bfloat16"):

@@ -59,6 +59,11 @@ def test_ops_refuse_cpu_tensors():
         K.quantize(torch.zeros(4, 64, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="affine, mxfp4 and mxfp8"):
         K.quantize(torch.zeros(4, 64, dtype=torch.bfloat16), mode="nvfp4")
+    # the mx modes take group 32 and their own width, as mlx requires
+    with pytest.raises(ValueError, match="mxfp8 takes group_size 32 and 8 bits"):
+        K.quantize(torch.zeros(4, 64, dtype=torch.bfloat16), bits=4, mode="mxfp8")
+    with pytest.raises(ValueError, match="mxfp4 takes group_size 32"):
+        K.quantize(torch.zeros(4, 64, dtype=torch.bfloat16), group_size=64, mode="mxfp4")
 
 
 def test_new_entries_refuse_bad_arguments_on_the_host():

@@ -31,6 +31,32 @@ def test_quantize_is_bit_exact(dev, dtype, bits, group):
     assert np.array_equal(to_numpy(s), rs) and np.array_equal(to_numpy(b), rb)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
+def test_quantize_rounds_ties_to_even(dev, dtype):
+    """mlx's CPU quantizer takes std::rint of (w - bias) / scale: group
+    [0, 15, 6.5, 4.5, ...] has scale -1 and bias 15, so 6.5 and 4.5 sit on
+    ties (8.5, 10.5) and get codes 8 and 10 (half away from zero: 9, 11)."""
+    w = np.zeros((1, 64), np.float32)
+    w[0, 1], w[0, 2], w[0, 3] = 15.0, 6.5, 4.5
+    w[0, 4:] = np.arange(60) % 16
+    wq, s, b = K.quantize(to_torch(w, dev, DT[dtype]), group_size=64, bits=4)
+    q = O.unpack_numpy(u32_to_numpy(wq), 4)[0]
+    assert q[2] == 8 and q[3] == 10
+    assert to_numpy(s)[0, 0] == -1.0 and to_numpy(b)[0, 0] == 15.0
+    assert np.array_equal(u32_to_numpy(wq), O.quantize(w, 64, 4, dtype)[0])
+
+
+def test_dequantize_takes_the_op_by_op_rounding_by_default(dev):
+    """mx.dequantize on a CPU stream is a multiply then an add in the
+    scales' dtype: s = 1 + 2^-7, q = 3, b = -3 gives bf16(bf16(3.0234375)
+    - 3) = 0.03125, where one rounding of s*q + b would give 0.0234375."""
+    words = torch.tensor([[3, 0, 0, 0, 0, 0, 0, 0]], dtype=torch.int32, device=dev).view(torch.uint32)
+    sc = torch.tensor([[1.0078125]], dtype=torch.bfloat16, device=dev)
+    bi = torch.tensor([[-3.0]], dtype=torch.bfloat16, device=dev)
+    assert to_numpy(K.dequantize(words, sc, bi, 64, 4))[0, 0] == 0.03125
+    assert to_numpy(K.dequantize(words, sc, bi, 64, 4, rounding=1))[0, 0] == 0.0234375
+
+
 def test_quantize_edge_cases(dev):
     # constant groups, all-zero groups, ties and a 3-D tensor
     w = np.zeros((2, 3, 128), np.float32)

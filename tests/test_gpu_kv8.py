@@ -72,8 +72,10 @@ def test_other_group_sizes(dev, g):
 def test_a_group_narrower_than_a_lane_run_falls_back(dev):
     (q, K, V, g), (tq, tK, tV) = _case(dev, 1, 8, 2, 1, 64, 256, g=32)
     assert not kvattn.supports(tq, tK, tV, 8, g)
-    got = kvattn.dequant_sdpa(tq, tK, tV, 256 ** -0.5, None, g, 8)
-    assert_close(to_numpy(got), O.kv8_decode(q, K, V, 256 ** -0.5, None, g, 8, "float32"), what="fallback")
+    # the fallback: mlx-lm's quantized attention over the packed triples
+    got = kvattn.quantized_sdpa(tq, tK, tV, 256 ** -0.5, None, g, 8)
+    assert_close(to_numpy(got), O.quantized_sdpa(q, K, V, 256 ** -0.5, None, g, 8), what="fallback")
+    assert_close(to_numpy(got), O.kv8_decode(q, K, V, 256 ** -0.5, None, g, 8, "float32"), what="vs kernel semantics")
 
 
 def test_many_blocks_per_head(dev):
@@ -129,13 +131,15 @@ def test_unsupported_shapes_are_refused_and_fall_back(dev):
     assert not kvattn.supports(tq, tK, tV, 8, g, per_head)
     (_, _, _, _), (q9, K9, V9) = _case(dev, 1, 32, 1, 3, 64, 128)
     assert not kvattn.supports(q9, K9, V9, 8, 64)               # 96 rows per KV head
-    # the fallback (dequantize + sdpa on the GPU) computes the same attention
-    got = kvattn.dequant_sdpa(tq, tK, tV, 128 ** -0.5, None, g, 8)
+    # the fallback (the packed-triple attention on the GPU) computes the same attention
+    got = kvattn.quantized_sdpa(tq, tK, tV, 128 ** -0.5, None, g, 8)
     ref = O.kv8_decode(q, K, V, 128 ** -0.5, None, g, 8, "float32")
     assert_close(to_numpy(got), ref, what="fallback")
 
 
-def test_sdpa_dispatch_counts_hits_and_misses(dev):
+def test_sdpa_dispatch_counts_hits_and_misses(dev, monkeypatch):
+    from tests.toy_attention import scaled_dot_product_attention as model_attention
+    monkeypatch.setattr(kvattn, "_BASE", {"fn": model_attention})    # what patch_model records
     (q, K, V, g), (tq, tK, tV) = _case(dev, 1, 8, 2, 1, 100, 128)
 
     class Cache:
@@ -155,6 +159,7 @@ def test_sdpa_dispatch_counts_hits_and_misses(dev):
     c.kv8_fetch = (kd, tK, tV, g)
     out2 = kvattn.sdpa(tq, kd * 2, vd, c, 128 ** -0.5, None)
     assert kvattn.STATS["misses"] == 1 and out2.shape == tq.shape
+    assert torch.equal(out2, model_attention(tq, kd * 2, vd, scale=128 ** -0.5))   # dense: the model's own
 
 
 @pytest.mark.parametrize("N", [8192, 32768])

@@ -79,7 +79,7 @@ def test_a_decode_step_takes_the_kernel_from_the_cache(dev):
     V = O.quantize(allk * 0.5, 64, 8, "bfloat16")
     ref = O.kv8_decode(q.float().cpu().numpy(), K, V, D ** -0.5, None, 64, 8, "float32")
     assert_close(to_numpy(out), ref, what="kv8 through the cache")
-    # the same step without the kernel: dequantize + sdpa over the lazy K/V
+    # the same step without the kernel: attention over the cache's packed triples
     c2 = KC.QuantKVCache(8)
     k2, v2 = c2.update_and_fetch(torch.cat([prompt, step], 2)[:1], (torch.cat([prompt, step], 2) * 0.5)[:1])
     out2 = kvattn.sdpa(q[:1], k2, v2, c2, D ** -0.5, None)
@@ -123,8 +123,9 @@ def test_append_refuses_what_it_cannot_store(dev):
 def test_a_six_bit_cache_stores_fetches_and_attends_through_the_fallback(dev):
     """6-bit K/V (the reference's kvquant.BITS): codes straddle words in
     the row's bit stream; a fetch is within four 8-bit steps of what went
-    in, and attention takes dequantize + sdpa (the decode kernel is
-    8-bit only), matching float64 attention over the dequantized cache."""
+    in, and attention takes the packed-triple path (the decode kernel is
+    8-bit only), within the bar of float64 attention over the dequantized
+    cache."""
     c = KC.QuantKVCache(6)
     c.kv8_kernel = True
     k, v = _kv((1, 2, 50, 128), 1, dev), _kv((1, 2, 50, 128), 2, dev)

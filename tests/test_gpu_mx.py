@@ -132,11 +132,50 @@ def test_quantize_mx_bit_exact(dev, mode):
     w = bf16_normal(rng, (48, 256), 0.05)
     w[0, :32] = 0.0
     w[1, :32] = -0.0
-    w[2, 5] = 1e4                                    # saturates
+    w[2, 5] = 1e4                                    # a group 2^11 times larger than the rest
     for dt in (torch.bfloat16, torch.float32):
         wq, sc = K.quantize(to_torch(w, dev, dt), group_size=32, bits=4 if mode == "mxfp4" else 8, mode=mode)
         rq, rs = O.mx_quantize(w, mode)
         assert np.array_equal(sc.cpu().numpy(), rs)
+        assert np.array_equal(wq.view(torch.int32).cpu().numpy().view(np.uint32), rq)
+
+
+# One group of 32 per mode, scale byte 127 (X = 0), and the codes worked out
+# by hand from the OCP rule: ties to the even code, saturation to the
+# largest finite element, the sign kept on zero.
+MX_HAND = {
+    # E2M1 codes 0..7 = 0, .5, 1, 1.5, 2, 3, 4, 6; bit 3 is the sign
+    "mxfp4": [(7.5, 7), (6.5, 7), (0.25, 0), (0.75, 2), (1.25, 2), (1.75, 4), (2.5, 4), (3.5, 6), (5.0, 6),
+              (-0.25, 8), (-2.5, 12), (0.3, 1), (-0.0, 8), (0.0, 0)],
+    # E4M3: 1.0 = 0x38, 1.125 = 0x39, 1.25 = 0x3A, 288 = 0x79, 320 = 0x7A, 448 = 0x7E, 2^-9 = 0x01
+    "mxfp8": [(480.0, 0x7E), (460.0, 0x7E), (1.0625, 0x38), (1.1875, 0x3A), (2.0 ** -10, 0x00),
+              (3 * 2.0 ** -10, 0x02), (-1.0625, 0xB8), (-0.0, 0x80), (0.0, 0x00), (300.0, 0x79),
+              (304.0, 0x7A)],
+}
+
+
+def mx_hand_group(mode):
+    vals, codes = zip(*MX_HAND[mode])
+    w = np.zeros((1, 32), np.float32)
+    w[0, :len(vals)] = vals
+    c = np.zeros(32, np.uint32)
+    c[:len(codes)] = codes
+    return w, c
+
+
+@pytest.mark.parametrize("mode", ["mxfp4", "mxfp8"])
+def test_quantize_mx_ties_saturation_and_signed_zeros(dev, mode):
+    """Off-grid values, exact ties, values past the largest element and
+    signed zeros: the GPU's codes equal the hand-computed ones (and the
+    oracle's), scale byte 127."""
+    w, want = mx_hand_group(mode)
+    bits = 4 if mode == "mxfp4" else 8
+    for dt in (torch.bfloat16, torch.float32):
+        wq, sc = K.quantize(to_torch(w, dev, dt), mode=mode)
+        assert sc.cpu().numpy().tolist() == [[127]]
+        got = O.unpack_numpy(wq.view(torch.int32).cpu().numpy().view(np.uint32), bits)[0]
+        assert got.tolist() == want.tolist()
+        rq, rs = O.mx_quantize(w, mode)
         assert np.array_equal(wq.view(torch.int32).cpu().numpy().view(np.uint32), rq)
 
 

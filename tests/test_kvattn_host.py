@@ -1,0 +1,108 @@
+"""kvattn.patch_model / enabled and kvcache.install on the CPU (no kernel
+calls): which modules get rebound, which caches get quantized, and that
+dense K/V go back to the model's own attention function -- the reference's
+engine/kvattn.py:323-339 and engine/kvquant.py:390-452."""
+import importlib
+import sys
+
+import pytest
+import torch
+
+from knurlogic_amd import kvattn
+from knurlogic_amd import kvcache as KC
+
+
+@pytest.fixture
+def toy(monkeypatch):
+    """A fresh toy model module (its attention function unpatched)."""
+    sys.modules.pop("tests.toy_attention", None)
+    mod = importlib.import_module("tests.toy_attention")
+    monkeypatch.setattr(kvattn, "_BASE", {"fn": None})
+    monkeypatch.delenv(kvattn.ENV, raising=False)
+    yield mod
+    sys.modules.pop("tests.toy_attention", None)
+
+
+def test_patch_model_rebinds_the_models_attention_and_keeps_it_as_the_base(toy):
+    orig = toy.scaled_dot_product_attention
+    model = toy.Model()
+    assert kvattn.patch_model(model) == 1
+    assert toy.scaled_dot_product_attention is kvattn.sdpa
+    assert kvattn._BASE["fn"] is orig
+    assert kvattn.patch_model(model) == 1                    # idempotent
+    assert kvattn._BASE["fn"] is orig
+
+
+def test_dense_kv_go_back_to_the_models_own_attention(toy):
+    model = toy.Model(layers=1)
+    x = torch.randn(1, 7, 256)
+    want = toy.run(model, x, 5)
+    kvattn.patch_model(model)
+    got = toy.run(model, x, 5)                                # plain caches: every call is dense
+    assert torch.equal(got, want)
+
+
+def test_dense_kv_without_patch_model_is_an_error(toy):
+    q = torch.zeros(1, 2, 1, 128)
+    with pytest.raises(ValueError, match="patch_model"):
+        kvattn.sdpa(q, q, q, None, 1.0, None)
+
+
+def test_enabled_follows_the_switch(monkeypatch):
+    monkeypatch.delenv(kvattn.ENV, raising=False)
+    assert kvattn.enabled()
+    for off in ("off", "0", "False"):
+        monkeypatch.setenv(kvattn.ENV, off)
+        assert not kvattn.enabled()
+    monkeypatch.setenv(kvattn.ENV, "on")
+    assert kvattn.enabled()
+
+
+def test_install_quantizes_plain_caches_and_marks_the_kernel(toy, monkeypatch):
+    model = toy.Model()
+    assert KC.install(model, 8) == 2
+    assert model.kv8_kernel is True and toy.scaled_dot_product_attention is kvattn.sdpa
+    caches = model.make_cache()
+    assert all(type(c) is KC.QuantKVCache and c.kv_bits == 8 and c.kv8_kernel for c in caches)
+    # the switch off: quantized caches, no kernel
+    other = toy.Model()
+    monkeypatch.setenv(kvattn.ENV, "off")
+    assert KC.install(other, 8) == 2 and other.kv8_kernel is False
+    assert not any(c.kv8_kernel for c in other.make_cache())
+    # 4 bits: quantized, never the 8-bit kernel
+    four = toy.Model()
+    monkeypatch.delenv(kvattn.ENV)
+    assert KC.install(four, "4") == 2 and four.kv8_kernel is False
+    assert all(c.kv_bits == 4 and not c.kv8_kernel for c in four.make_cache())
+    # bf16: nothing to do
+    plain = toy.Model()
+    assert KC.install(plain, "bf16") == 0 and not hasattr(plain, "kv8_kernel")
+
+
+def test_quantize_cache_list_recurses_and_leaves_the_rest():
+    class KVCache:
+        keys = None
+
+    class Recurrent:
+        keys = None
+
+    class CacheList:
+        def __init__(self, *caches):
+            self.caches = caches
+
+    class Family:
+        keys = None
+
+    filled = KVCache()
+    filled.keys = torch.zeros(1)
+    made = []
+    out, n = KC.quantize_cache_list(
+        [KVCache(), Recurrent(), CacheList(KVCache(), Recurrent()), filled, Family()], 6,
+        {Family: lambda bits: made.append(bits) or KC.BatchQuantKVCache([0], bits)})
+    assert n == 3 and made == [6]
+    assert type(out[0]) is KC.QuantKVCache and out[0].kv_bits == 6
+    assert type(out[1]) is Recurrent
+    assert type(out[2]) is CacheList and type(out[2].caches[0]) is KC.QuantKVCache
+    assert type(out[2].caches[1]) is Recurrent
+    assert out[3] is filled
+    assert type(out[4]) is KC.BatchQuantKVCache

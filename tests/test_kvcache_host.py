@@ -29,6 +29,9 @@ def _cpu_append_kv(kparts, vparts, keys, values, pos, group, bits):
     _cpu_append(vparts, values, pos, group, bits)
 
 
+REAL_APPEND_KV = KC.append_kv
+
+
 @pytest.fixture(autouse=True)
 def cpu_append(monkeypatch):
     monkeypatch.setattr(KC, "append_quantized", _cpu_append)
@@ -171,3 +174,24 @@ def test_state_round_trips():
     d.state = c.state
     assert d.offset == 7 and d.group == 32 and d.kv8_kernel and d.dims == (32, 32)
     assert torch.equal(d.keys[0].view(torch.int32), c.keys[0][:, :, :7].view(torch.int32))
+
+
+@pytest.mark.parametrize("what", ["batch", "heads", "width", "scales", "capacity"])
+def test_an_append_that_does_not_fit_its_slab_is_refused(what):
+    """The append kernel sees only strides and a capacity, so rows of
+    another batch, head count or head dim (a cache reused at another batch,
+    a state restored from another model) must be refused on the host rather
+    than written past the slab."""
+    k = _kv((2, 4, 3, 64), 0)
+    kp = KC._alloc(2, 4, 256, 64, 8, 64, BF, "cpu")
+    vp = KC._alloc(2, 4, 256, 64, 8, 64, BF, "cpu")
+    bad = {"batch": lambda: KC._alloc(3, 4, 256, 64, 8, 64, BF, "cpu"),
+           "heads": lambda: KC._alloc(2, 2, 256, 64, 8, 64, BF, "cpu"),
+           "width": lambda: KC._alloc(2, 4, 256, 128, 8, 64, BF, "cpu"),
+           "scales": lambda: (kp[0], kp[1][..., :0], kp[2][..., :0]),
+           "capacity": lambda: KC._alloc(2, 4, 512, 64, 8, 64, BF, "cpu")}[what]()
+    match = "same number of slots" if what == "capacity" else "does not fit its slab"
+    with pytest.raises(ValueError, match=match):
+        REAL_APPEND_KV(kp, bad, k, k, 0, 64, 8)         # the real append, not the CPU stand-in
+    with pytest.raises(ValueError, match="GPU memory"):
+        REAL_APPEND_KV(kp, vp, k, k, 0, 64, 8)          # a fitting slab only fails for being on the CPU

@@ -86,6 +86,22 @@ def test_quantize_known_answer_min_edge_positive_scale():
     assert np.array_equal(O.unpack_numpy(wq, 4)[0], (w[0] + 15).astype(np.uint32))
 
 
+def test_quantize_ties_round_to_even():
+    """mlx's CPU quantizer (mlx/backend/cpu/quantized.cpp, ``quantize``) forms
+    each code as std::rint((w - bias) / scale), which rounds a tie to the
+    even integer.  Group [0, 15, 6.5, 4.5, ...]: scale -1, bias 15, so
+    6.5 -> rint(8.5) = 8 and 4.5 -> rint(10.5) = 10 (half away from zero
+    would give 9 and 11); dequantized 7 and 5."""
+    w = np.zeros((1, 64), np.float32)
+    w[0, 1], w[0, 2], w[0, 3] = 15.0, 6.5, 4.5
+    w[0, 4:] = np.arange(60) % 16
+    wq, s, b = O.quantize(w, 64, 4)
+    assert s[0, 0] == -1.0 and b[0, 0] == 15.0
+    q = O.unpack_numpy(wq, 4)[0]
+    assert q[2] == 8 and q[3] == 10
+    assert O.dequantize(wq, s, b, 64, 4)[0, 2] == 7.0
+
+
 def test_quantize_all_zero_group():
     wq, s, b = O.quantize(np.zeros((1, 64), np.float32), 64, 8)
     assert (wq == 0).all() and b[0, 0] == 0.0 and s[0, 0] == O.bf16_round(np.float32(-1e-7))
@@ -252,6 +268,50 @@ def test_route_known_answer_and_ties():
     assert np.allclose(scores[0], e / e.sum(), rtol=1e-6)
     inds, _ = O.route(np.zeros((1, 5), np.float32), 3)
     assert list(inds[0]) == [0, 1, 2]
+
+
+def test_route_uniform_rows_by_hand():
+    """Equal logits: e = 1, n = E, r = float32(1/E), p = r.  E = 3, k = 2:
+    r = 0x3EAAAAAB, t = 2r exactly, scores = r / 2r = 0.5; experts 0, 1
+    (ties to the lower index).  A hidden expert (-inf) gets e = 0 and is
+    never chosen ahead of a visible one."""
+    inds, scores = O.route(np.zeros((1, 3), np.float32), 2, "float32")
+    assert list(inds[0]) == [0, 1] and list(scores[0]) == [0.5, 0.5]
+    inds, scores = O.route(np.array([[-np.inf, 0.0, -np.inf, 0.0, 0.0]], np.float32), 3, "float32")
+    assert list(inds[0]) == [1, 3, 4]
+    assert scores[0, 0].view(np.uint32) == 0x3EAAAAAB          # float32(1/3): r / (3r rounded)
+    assert scores.sum() == np.float32(1.0)
+
+
+def test_route_agrees_with_an_independent_fp32_router():
+    """HF transformers' Qwen MoE router on torch's CPU kernels (softmax in
+    float32, top-k, p / sum(p) in float32, cast to bf16) -- the
+    implementation the reference's golden was made with -- computes the
+    same float32 op sequence as mlx (softmax with one reciprocal of the
+    normaliser).  Over 20000 rows of 128 bf16 logits the oracle picks the
+    same top-8 set everywhere and the same bf16 scores, bit for bit, in all
+    but a handful of boundary cases (one bf16 ulp apart, where torch's SIMD
+    exp lands an ulp away from the correctly rounded one)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(0)
+    lg = O.bf16_round(rng.standard_normal((20000, 128)).astype(np.float32))
+    p = torch.softmax(torch.from_numpy(lg), -1)
+    top, ind = p.topk(8, -1)
+    ref = (top / top.sum(-1, keepdim=True)).to(torch.bfloat16).float().numpy()
+    ind = ind.numpy()
+    inds, scores = O.route(lg, 8)
+    # torch picks freely among equal probabilities at the 8th place (equal
+    # bf16 logits); everywhere else the sets must agree
+    p9 = np.sort(p.numpy(), -1)[:, ::-1][:, 7:9]
+    clear = p9[:, 0] > p9[:, 1]
+    assert clear.mean() > 0.9
+    assert (np.sort(inds, -1) == np.sort(ind, -1))[clear].all()
+    # compare each expert's score (torch orders equal probabilities freely)
+    got = np.take_along_axis(scores, np.argsort(inds, -1), -1)[clear]
+    want = np.take_along_axis(ref, np.argsort(ind, -1), -1)[clear]
+    diff = got != want
+    assert diff.mean() < 1e-4, diff.mean()
+    assert np.all(np.abs(got - want)[diff] <= np.abs(want[diff]) * 2 ** -7)
 
 
 # --- KV8 decode attention ---------------------------------------------------------
@@ -521,3 +581,15 @@ def test_mx_quantize_round_trip_and_saturation():
         worst = 2.0 if mode == "mxfp4" else 64.0
         scale = np.repeat(O.e8m0(s), 32, -1)
         assert (np.abs(back - w) <= scale * worst + 1e-12).all()
+
+
+@pytest.mark.parametrize("mode", ["mxfp4", "mxfp8"])
+def test_mx_quantize_hand_computed_ties_and_saturation(mode):
+    """The OCP conversion worked out by hand for one group (scale byte 127):
+    ties to the even code, saturation to the largest finite element, the
+    sign of zero kept (the table is shared with the GPU test)."""
+    from tests.test_gpu_mx import mx_hand_group
+    w, want = mx_hand_group(mode)
+    wq, sc = O.mx_quantize(w, mode)
+    assert sc.tolist() == [[127]]
+    assert O.unpack_numpy(wq, 4 if mode == "mxfp4" else 8)[0].tolist() == want.tolist()
