@@ -271,6 +271,29 @@ int kmi_masked_softmax(const void* x, int64_t ldx, int dtype, const int64_t* row
                        void* stream);
 
 /*
+ * mlx's nn.Linear for the layers a quantized model keeps unquantized: the
+ * Qwen3.5-MoE router gate and shared-expert gate (qwen3_5.py:173-174,186,
+ * self.gate(x) / self.shared_expert_gate(x)):
+ *   y[M, N] = x[M, K] @ w[N, K]^T            (bias NULL), or
+ *   y[M, N] = addmm(bias, x, w^T)            (one rounding of acc + bias[n])
+ * fp32 accumulation, y rounded to `dtype` (bfloat16 or float16); x, w, bias
+ * and y share it.  K % 8 == 0, x and w contiguous and 16-byte aligned.
+ */
+int kmi_linear(const void* x, int64_t M, int64_t K, const void* w, int64_t N, const void* bias, int dtype,
+               void* y, void* stream);
+
+/*
+ * The bias of nn.QuantizedLinear / QuantizedSwitchLinear, added to the
+ * rounded product as its own op (switch_layers.py:82-85:
+ * x + expand_dims(bias[indices], -2)):
+ *   y[r, n] = round(y[r, n] + bias[e, n]),  e = idx[r / rows_per_index]
+ * (idx NULL: e = 0; bias [E, N]); rows with e outside [0, E) are left alone.
+ * y [rows, N] in place, bfloat16 or float16.
+ */
+int kmi_add_bias(void* y, int64_t rows, int64_t N, const void* bias, const int32_t* idx, int64_t rows_per_index,
+                 int64_t E, int dtype, void* stream);
+
+/*
  * The MoE router of Qwen3.5-MoE's SparseMoeBlock
  * (src/knurlogic/engine/families/qwen/architecture/qwen3_5.py:174-179):
  * probs = softmax(logits) in float32; the top k in descending order (equal

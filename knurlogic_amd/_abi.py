@@ -39,6 +39,8 @@ SIGNATURES = {
     "kmi_masked_softmax": (I, [P, I64, I, P, I64, P, I, P, P, I64, P]),
     "kmi_vq_packed_gather_qmm": (I, [P, I64, I64, P, I, P, I, I, P, I, I64, I64, P, I64, P, I64, I, P, P]),
     "kmi_vq_packed_glu": (I, [P, I64, I64, I64, P, P, P, P, P, P, I, I, I, I, I64, P, I64, P, I64, I, P, P]),
+    "kmi_linear": (I, [P, I64, I64, P, I64, P, I, P, P]),
+    "kmi_add_bias": (I, [P, I64, I64, P, P, I64, I64, I, P]),
     "kmi_moe_route": (I, [P, I, I64, I, I, P, P, P]),
     "kmi_swiglu": (I, [P, P, I64, I, I64, I64, P, P]),
     "kmi_moe_combine": (I, [P, P, I, I64, I, I64, P, P]),

@@ -15,8 +15,8 @@
   architecture/qwen3_5.py:35-40,108-118,151-192).
 
 Tensors live in GPU memory (torch); every product and every elementwise
-step with a rounding rule runs in the HIP library.  A dense (unquantized)
-router or shared-expert gate goes through torch's GEMM.
+step runs in the HIP library -- the dense (unquantized) router and
+shared-expert gate too (``Linear``, kmi_linear).
 """
 from __future__ import annotations
 
@@ -24,21 +24,21 @@ import math
 
 import torch
 
-from .ops import (gather_qmm, moe_combine, moe_route, moe_shared_add, quantize,
+from .ops import (add_bias, gather_qmm, linear, moe_combine, moe_route, moe_shared_add, quantize,
                   quantized_matmul, swiglu, switch_glu, vq_gather_qmm, vq_glu, vq_packed_gather_qmm,
                   vq_packed_glu, vq_switch_glu)
 
 
 class Linear:
-    """A dense linear layer y = x @ w^T (+ bias), the library GEMM of the
-    activation dtype (a router or gate the loader left unquantized)."""
+    """mlx's nn.Linear for a layer the loader left unquantized (the router,
+    the shared-expert gate): x @ w^T, or addmm(bias, x, w^T), through
+    kmi_linear."""
 
     def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None = None):
         self.weight, self.bias = weight, bias
 
     def __call__(self, x):
-        y = x @ self.weight.t()
-        return y + self.bias if self.bias is not None else y
+        return linear(x, self.weight, self.bias)
 
 
 class QuantizedLinear:
@@ -64,7 +64,7 @@ class QuantizedLinear:
     def __call__(self, x):
         y = quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
                              group_size=self.group_size, bits=self.bits, mode=self.mode)
-        return y + self.bias if self.bias is not None else y
+        return add_bias(y, self.bias) if self.bias is not None else y
 
 
 class QuantizedSwitchLinear:
@@ -98,7 +98,7 @@ class QuantizedSwitchLinear:
                        transpose=True, group_size=self.group_size, bits=self.bits,
                        mode=self.mode, sorted_indices=sorted_indices)
         if self.bias is not None:
-            y = y + self.bias[indices.long()].unsqueeze(-2)
+            y = add_bias(y, self.bias, indices)
         return y
 
 

@@ -570,6 +570,57 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor | None = None):
     return out
 
 
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None):
+    """mlx's nn.Linear: x [..., K] @ weight[N, K]^T, or addmm(bias, x,
+    weight^T) with one rounding of the fp32 sum plus the bias
+    (kmi_linear).  bfloat16 or float16, shared by x, weight and bias."""
+    _on_gpu(x, weight)
+    if x.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != x.dtype:
+        raise ValueError(f"linear: x and weight must share bfloat16 or float16 (got {x.dtype}, {weight.dtype})")
+    if weight.dim() != 2 or x.shape[-1] != weight.shape[1]:
+        raise ValueError(f"linear: x {tuple(x.shape)} and weight {tuple(weight.shape)} do not match")
+    N, K = weight.shape
+    if K % 8:
+        raise ValueError(f"linear: K={K} must be a multiple of 8")
+    if bias is not None:
+        _on_gpu(bias)
+        if bias.shape != (N,) or bias.dtype != x.dtype:
+            raise ValueError(f"linear: bias must be [{N}] of {x.dtype}")
+        bias = bias.contiguous()
+    xc, wc = _aligned16(x), _aligned16(weight)
+    M = xc.numel() // K if K else 0
+    y = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=x.device)
+    _abi.check(_lib().kmi_linear(_ptr(xc), M, K, _ptr(wc), N, _ptr(bias), DTYPE_CODE[x.dtype], _ptr(y),
+                                 _stream(x)), "linear")
+    return y
+
+
+def add_bias(y: torch.Tensor, bias: torch.Tensor, indices: torch.Tensor | None = None) -> torch.Tensor:
+    """y + bias as its own rounded op (nn.QuantizedLinear's bias), or, with
+    ``indices`` [...] of experts, y[..., M, N] + bias[indices][..., None, :]
+    (QuantizedSwitchLinear's, switch_layers.py:82-85).  Returns a new
+    tensor (kmi_add_bias on a copy of y)."""
+    _on_gpu(y, bias)
+    if y.dtype not in (torch.bfloat16, torch.float16) or bias.dtype != y.dtype:
+        raise ValueError("add_bias: y and bias must share bfloat16 or float16")
+    N = y.shape[-1]
+    out = y.contiguous().clone()
+    if indices is None:
+        if bias.shape != (N,):
+            raise ValueError(f"add_bias: bias must be [{N}]")
+        idx, per, E = None, 1, 1
+    else:
+        _on_gpu(indices)
+        if bias.dim() != 2 or bias.shape[1] != N or tuple(y.shape[:-2]) != tuple(indices.shape):
+            raise ValueError("add_bias: y [..., M, N], indices [...] and bias [E, N] must agree")
+        idx, per, E = indices.reshape(-1).to(torch.int32).contiguous(), y.shape[-2], bias.shape[0]
+    rows = out.numel() // N
+    bc = bias.contiguous()
+    _abi.check(_lib().kmi_add_bias(_ptr(out), rows, N, _ptr(bc), _ptr(idx), per, E, DTYPE_CODE[y.dtype],
+                                   _stream(y)), "add_bias")
+    return out
+
+
 def moe_combine(y: torch.Tensor, scores: torch.Tensor):
     """(y * scores[..., None]).sum(-2) with the reference's rounding: each
     product rounded to the dtype, the k products summed once.
