@@ -358,6 +358,22 @@ size_t kmi_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k, in
                                       int group_size, int bits);
 
 /*
+ * SparseMoeBlock's routed experts from the router logits, in one call
+ * (qwen3_5.py:174-182): the router of kmi_moe_route (softmax in float32,
+ * top-k, renormalized scores in bf16), then kmi_switch_glu with the
+ * weighted combine.  logits [T, E] bf16; inds [T, k] int32 and scores
+ * [T, k] bf16 are written (the routing, as kmi_moe_route gives it bit for
+ * bit); out [T, H] bf16; the weights as kmi_switch_glu takes them.  At
+ * decode sizes (T * k <= 16, E <= 256) the gate/up kernel routes its own
+ * token, so the call is two kernel launches; otherwise it routes first.
+ * k <= 8, E <= 1024.  workspace: kmi_switch_glu_workspace_bytes.
+ */
+int kmi_moe_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k, int64_t E,
+                    const uint32_t* w_gu, const void* s_gu, const void* b_gu, const uint32_t* w_down,
+                    const void* s_down, const void* b_down, int dtype, int group_size, int bits, void* out,
+                    int32_t* inds, void* scores, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * VQ codebook-decode expert matmul: VQSwitchLinear, the expert layer VQ
  * artifacts ship in their own model.py (class named at
  * tests/engine/test_deepseek_v4_mtp.py:249,360; code layout of _pack_vq at

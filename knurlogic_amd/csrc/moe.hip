@@ -5,6 +5,7 @@
 // (src/knurlogic/engine/families/qwen/architecture/qwen3_5.py:35-40,108-112,
 // 170-192), each rounding step where the reference rounds.
 #include "common.hpp"
+#include "route.hpp"
 #include "../../include/knurlogic_amd.h"
 
 namespace kmi {
@@ -27,92 +28,18 @@ __device__ __forceinline__ float f64_to_f32(double v) {
     return f;
 }
 
-constexpr int ROUTE_MAX_E = 1024;            // experts a wave holds (16 per lane)
-
-// One wave per token.  probs = softmax(logits) in float32, one rounding per
-// step as mlx's CPU softmax takes them (max m; e = exp(x - m); n = sum e;
-// r = 1 / n; p = e * r), with exp correctly rounded (evaluated in float64)
-// and the sum exact before its one rounding; the k largest probabilities in
-// descending order, equal ones taken lower index first; scores = p / t with
-// t the float32 sum of the k selected (again exact, then rounded), rounded
-// to the logits' dtype.  Quotients and products of two floats are formed in
-// float64 and rounded once, which gives the correctly rounded float32
-// result (53 >= 2 * 24 + 2 bits).
-//
-// Selection is by rank, with no serial rounds: probabilities are >= 0, so
-// their float32 bits order like the values, and key = bits << 32 | ~expert
-// orders exactly as the selection does (larger p first, then lower expert)
-// with no two keys equal.  Each lane counts the wave's keys above its own
-// (broadcast LDS reads, one 64-bit compare each); rank < k is selected, at
-// slot rank.
-template <class T, int ROUTE_PER_LANE>
-__global__ __launch_bounds__(256) void moe_route_kernel(const void* __restrict__ logits, int64_t T_, int E,
-                                                        int k, int32_t* __restrict__ inds,
-                                                        void* __restrict__ scores) {
-    constexpr int EP = 64 * ROUTE_PER_LANE;             // keys per wave, padded
-    __shared__ uint64_t keys[4][EP];
-    __shared__ float selp[4][64];
-    __shared__ int sele[4][64];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int64_t t = (int64_t)blockIdx.x * 4 + w;
-    const bool live = t < T_;                            // a whole wave is live or not
-    float lg[ROUTE_PER_LANE];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < ROUTE_PER_LANE; j++) {
-        const int e = lane + 64 * j;
-        lg[j] = live && e < E ? ld_dt<T>(logits, t * E + e) : -INFINITY;
-        mx = fmaxf(mx, lg[j]);
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    float ex[ROUTE_PER_LANE];
-    double sum = 0.0;
-#pragma unroll
-    for (int j = 0; j < ROUTE_PER_LANE; j++) {
-        const float d = lg[j] - mx;                      // float32 subtraction, as mlx's kernel
-        ex[j] = lane + 64 * j < E ? f64_to_f32(exp((double)d)) : 0.f;
-        sum += (double)ex[j];
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
-    const float rn = f64_to_f32(1.0 / (double)f64_to_f32(sum));
-    float p[ROUTE_PER_LANE];
-    uint64_t key[ROUTE_PER_LANE];
-#pragma unroll
-    for (int j = 0; j < ROUTE_PER_LANE; j++) {
-        const int e = lane + 64 * j;
-        p[j] = e < E ? f64_to_f32((double)ex[j] * (double)rn) : 0.f;
-        // padding lanes get key 0, below every expert's key (its low word ~e > 0)
-        key[j] = e < E ? ((uint64_t)__float_as_uint(p[j]) << 32) | (uint32_t)~e : 0ull;
-        keys[w][e] = key[j];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    int rank[ROUTE_PER_LANE];
-#pragma unroll
-    for (int j = 0; j < ROUTE_PER_LANE; j++) rank[j] = 0;
-    for (int i = 0; i < EP; i += 2) {
-        const uint64_t a = keys[w][i], b = keys[w][i + 1];
-#pragma unroll
-        for (int j = 0; j < ROUTE_PER_LANE; j++) rank[j] += (int)(a > key[j]) + (int)(b > key[j]);
-    }
-#pragma unroll
-    for (int j = 0; j < ROUTE_PER_LANE; j++)
-        if (lane + 64 * j < E && rank[j] < k) {
-            selp[w][rank[j]] = p[j];
-            sele[w][rank[j]] = lane + 64 * j;
-        }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    double top_sum = 0.0;
-    for (int s2 = 0; s2 < k; s2++) top_sum += (double)selp[w][s2];
-    const double tsum = (double)f64_to_f32(top_sum);
-    if (live && lane < k) {
-        inds[t * k + lane] = sele[w][lane];
-        st_dt<T>(scores, t * k + lane, f64_to_f32((double)selp[w][lane] / tsum));
+// One workgroup per token: the router of route.hpp, then the k experts and
+// their scores stored.
+template <class T, int PER>
+__global__ __launch_bounds__(ROUTE_THREADS) void moe_route_kernel(const void* __restrict__ logits, int E, int k,
+                                                                  int32_t* __restrict__ inds,
+                                                                  void* __restrict__ scores) {
+    __shared__ RouteLds sm;
+    const int64_t t = blockIdx.x;
+    route_token<T, PER>((const typename T::storage*)logits + t * E, E, k, sm);
+    if ((int)threadIdx.x < k) {
+        inds[t * k + threadIdx.x] = sm.sel_e[threadIdx.x];
+        st_dt<T>(scores, t * k + threadIdx.x, sm.sel_p[threadIdx.x]);
     }
 }
 
@@ -183,25 +110,20 @@ int kmi_moe_route(const void* logits, int dtype, int64_t T, int E, int k, int32_
     clear_error();
     KMI_CHECK_ARG(dtype >= BF16 && dtype <= F32, "moe_route: bad dtype %d", dtype);
     KMI_CHECK_ARG(T >= 0 && E >= 1 && E <= ROUTE_MAX_E, "moe_route: %d experts (1..%d)", E, ROUTE_MAX_E);
-    KMI_CHECK_ARG(k >= 1 && k <= E && k <= 64, "moe_route: top-%d of %d experts", k, E);
+    KMI_CHECK_ARG(k >= 1 && k <= E && k <= ROUTE_MAX_K, "moe_route: top-%d of %d experts", k, E);
     if (T == 0) return OK;
     KMI_CHECK_ARG(logits && inds && scores, "moe_route: null pointer");
+    KMI_CHECK_ARG(T < 0x7fffffffLL, "moe_route: T=%lld", (long long)T);
     hipStream_t st = (hipStream_t)stream;
-    const unsigned grid = (unsigned)ceil_div(T, 4);
-    const int per = E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16;
-#define KMI_ROUTE(TT, PL) moe_route_kernel<TT, PL><<<grid, 256, 0, st>>>(logits, T, E, k, inds, scores)
-#define KMI_ROUTE_T(TT)                                     \
-    do {                                                    \
-        if (per == 1) KMI_ROUTE(TT, 1);                     \
-        else if (per == 2) KMI_ROUTE(TT, 2);                \
-        else if (per == 4) KMI_ROUTE(TT, 4);                \
-        else if (per == 8) KMI_ROUTE(TT, 8);                \
-        else KMI_ROUTE(TT, 16);                             \
-    } while (0)
-    if (dtype == BF16) KMI_ROUTE_T(TBF16);
-    else if (dtype == F16) KMI_ROUTE_T(TF16);
-    else KMI_ROUTE_T(TF32);
-#undef KMI_ROUTE_T
+    const unsigned grid = (unsigned)T;
+    const int per = E <= ROUTE_THREADS ? 1 : E <= 2 * ROUTE_THREADS ? 2 : 4;
+#define KMI_ROUTE(TT)                                                                                   \
+    if (per == 1) moe_route_kernel<TT, 1><<<grid, ROUTE_THREADS, 0, st>>>(logits, E, k, inds, scores);      \
+    else if (per == 2) moe_route_kernel<TT, 2><<<grid, ROUTE_THREADS, 0, st>>>(logits, E, k, inds, scores); \
+    else moe_route_kernel<TT, 4><<<grid, ROUTE_THREADS, 0, st>>>(logits, E, k, inds, scores);
+    if (dtype == BF16) { KMI_ROUTE(TBF16) }
+    else if (dtype == F16) { KMI_ROUTE(TF16) }
+    else { KMI_ROUTE(TF32) }
 #undef KMI_ROUTE
     KMI_CHECK_LAUNCH("moe_route");
     return OK;

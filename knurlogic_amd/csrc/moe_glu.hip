@@ -11,6 +11,7 @@
 // epilogue, then down, then the weighted combine.
 #include "moe_tok.hpp"
 #include "qgemv.hpp"
+#include "route.hpp"
 #include "../../include/knurlogic_amd.h"
 
 namespace kmi {
@@ -57,12 +58,17 @@ size_t kmi_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k, in
     return plan_glu(T, H, I, k, E).total;
 }
 
-int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
-                   const void* scores, const uint32_t* w_gu, const void* s_gu, const void* b_gu,
-                   const uint32_t* w_down, const void* s_down, const void* b_down,
-                   int64_t E, int dtype, int group_size, int bits, void* out, void* workspace,
-                   size_t workspace_bytes, void* stream) {
-    clear_error();
+}  // extern "C"
+
+// SwitchGLU + combine; with route_logits (token-major only) the gate/up
+// kernel routes each token itself and writes route_inds / route_scores,
+// which the down kernel then reads as inds / scores.
+static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                           const void* scores, const uint32_t* w_gu, const void* s_gu, const void* b_gu,
+                           const uint32_t* w_down, const void* s_down, const void* b_down,
+                           int64_t E, int dtype, int group_size, int bits, void* out, void* workspace,
+                           size_t workspace_bytes, void* stream, const void* route_logits,
+                           int32_t* route_inds, void* route_scores) {
     KMI_CHECK_ARG(dtype == BF16, "switch_glu: only bfloat16 activations are implemented");
     KMI_CHECK_ARG(bits == 4 || bits == 8, "switch_glu: bits=%d (4 or 8)", bits);
     KMI_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
@@ -94,6 +100,9 @@ int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const 
     const int64_t wpr_h = H / epw, gpr_h = H / group_size;
     if (p.tok) {
         MoeTokArgs g = {};
+        g.logits = (const uint16_t*)route_logits;
+        g.inds_out = route_inds;
+        g.scores_out = (uint16_t*)route_scores;
         g.x = (const uint16_t*)x;
         g.w0 = w_gu; g.s0 = (const uint16_t*)s_gu; g.b0 = (const uint16_t*)b_gu;
         g.w1 = w_gu + I * wpr_h; g.s1 = (const uint16_t*)s_gu + I * gpr_h; g.b1 = (const uint16_t*)b_gu + I * gpr_h;
@@ -137,6 +146,38 @@ int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const 
     KMI_CHECK_LAUNCH("qgemv(down)");
     if (scores) return kmi_moe_combine(y, scores, dtype, T, k, H, out, stream);
     return OK;
+}
+
+extern "C" {
+
+int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                   const void* scores, const uint32_t* w_gu, const void* s_gu, const void* b_gu,
+                   const uint32_t* w_down, const void* s_down, const void* b_down,
+                   int64_t E, int dtype, int group_size, int bits, void* out, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+    clear_error();
+    return switch_glu_impl(x, T, H, I, k, inds, scores, w_gu, s_gu, b_gu, w_down, s_down, b_down, E, dtype,
+                           group_size, bits, out, workspace, workspace_bytes, stream, nullptr, nullptr, nullptr);
+}
+
+int kmi_moe_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k, int64_t E,
+                    const uint32_t* w_gu, const void* s_gu, const void* b_gu, const uint32_t* w_down,
+                    const void* s_down, const void* b_down, int dtype, int group_size, int bits, void* out,
+                    int32_t* inds, void* scores, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(dtype == BF16, "moe_experts: only bfloat16 activations and logits are implemented");
+    KMI_CHECK_ARG(E >= 1 && E <= ROUTE_MAX_E && k >= 1 && k <= 8 && k <= E,
+                  "moe_experts: top-%d of %lld experts (k <= 8, E <= %d)", k, (long long)E, ROUTE_MAX_E);
+    if (T == 0) return OK;
+    KMI_CHECK_ARG(logits && inds && scores, "moe_experts: null pointer");
+    const GluPlan p = plan_glu(T, H, I, k, E);
+    if (p.tok && E <= ROUTE_THREADS)   // decode sizes: the gate/up kernel routes its own token
+        return switch_glu_impl(x, T, H, I, k, inds, scores, w_gu, s_gu, b_gu, w_down, s_down, b_down, E, dtype,
+                               group_size, bits, out, workspace, workspace_bytes, stream, logits, inds, scores);
+    int rc = kmi_moe_route(logits, dtype, T, (int)E, k, inds, scores, stream);
+    if (rc) return rc;
+    return switch_glu_impl(x, T, H, I, k, inds, scores, w_gu, s_gu, b_gu, w_down, s_down, b_down, E, dtype,
+                           group_size, bits, out, workspace, workspace_bytes, stream, nullptr, nullptr, nullptr);
 }
 
 }  // extern "C"

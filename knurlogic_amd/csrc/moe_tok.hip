@@ -20,6 +20,9 @@
 // chunk s * sum(q x) + b * sum(x) in fp32.
 #include "qmv_common.hpp"
 #include "moe_tok.hpp"
+#include "route.hpp"
+
+#include <cstdlib>
 #include "../../include/knurlogic_amd.h"
 
 namespace kmi {
@@ -40,7 +43,10 @@ __device__ __forceinline__ float f64_to_f32_kept(double v) {
 // of a wave issued up front with the wave-uniform part of its offset in the
 // scalar operand, each chunk-row's scale and bias loaded per lane ahead of
 // its weights.  S 16-byte chunk slots per lane per row (all of K).
-template <int BITS, int RPW, int S, int WV>
+// ROUTE: the pair's expert comes from routing its token's logits in the
+// workgroup (route.hpp, the router kernel's arithmetic), after the x loads
+// are issued; workgroup 0 of each pair writes the expert and its score.
+template <int BITS, int RPW, int S, int WV, bool ROUTE>
 __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
     constexpr int NT = 64 * WV, CK = 128 / BITS, XV = CK / 8, ROWS = WV * RPW;
     constexpr uint32_t NONE = QV_NONE;
@@ -56,7 +62,25 @@ __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int p = blockIdx.y;
     const int64_t t = p / a.k;
-    const int e = a.inds[p];
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + t * a.K, a.K * 2);
+    auto xvo = [&](int q) -> uint32_t { return q < P ? (uint32_t)q * 16u : NONE; };
+    // x pieces first: independent of the expert, in flight during the routing
+    const u32x4 xr0 = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(tid), 0, 0);
+    const u32x4 xr1 = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(tid + NT), 0, 0);
+    int e;
+    if constexpr (ROUTE) {
+        static_assert(NT == ROUTE_THREADS, "the in-kernel router takes 256 threads");
+        __shared__ RouteLds rsm;
+        route_token<TBF16, 1>(a.logits + t * a.E, (int)a.E, a.k, rsm);      // E <= 256
+        const int s = p - (int)t * a.k;
+        e = __builtin_amdgcn_readfirstlane(rsm.sel_e[s]);
+        if (blockIdx.x == 0 && tid == 0) {
+            a.inds_out[p] = e;
+            a.scores_out[p] = f32_to_bf16(rsm.sel_p[s]);
+        }
+    } else {
+        e = a.inds[p];
+    }
     const int n0 = (int)blockIdx.x * ROWS + wave * RPW;
     const bool ok_e = e >= 0 && e < a.E;
     const int64_t eoff = (int64_t)(ok_e ? e : 0) * a.erows;
@@ -67,17 +91,13 @@ __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
     const __amdgpu_buffer_rsrc_t rb0 = make_rsrc(a.b0 + eoff * gpr, sbytes);
     const __amdgpu_buffer_rsrc_t rs1 = make_rsrc(a.s1 + eoff * gpr, sbytes);
     const __amdgpu_buffer_rsrc_t rb1 = make_rsrc(a.b1 + eoff * gpr, sbytes);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + t * a.K, a.K * 2);
-    auto xvo = [&](int q) -> uint32_t { return q < P ? (uint32_t)q * 16u : NONE; };
 
     // (0) x pieces beyond two per thread (long rows), before any weight load
     if (P > 2 * NT) {
         for (int q = tid + 2 * NT; q - (tid & 3) < P; q += NT)
             stage_x16<BITS>(q, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(q), 0, 0), P, C, xs, xm);
     }
-    // (1) this thread's x pieces, then scales/biases and weights of both sets
-    const u32x4 xr0 = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(tid), 0, 0);
-    const u32x4 xr1 = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(tid + NT), 0, 0);
+    // (1) scales/biases and weights of both sets
     const int full = C >> 6;
     const bool in_tail = lane < (C & 63);
     const uint32_t vw = (uint32_t)lane * 16u;
@@ -337,14 +357,17 @@ int launch_moe_glu_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
     if (S <= 2 && a.N * pairs / 4 >= 2048) rpw = 4;
     const dim3 grid((unsigned)ceil_div(a.N, TOK_WV * rpw), (unsigned)pairs);
     const size_t lds = (size_t)a.K * 2 + (size_t)C * 16;
+#define KMI_GLU_R(R, SS, RT)                                                                \
+    if (bits == 4) moe_glu_tok<4, R, SS, TOK_WV, RT><<<grid, 64 * TOK_WV, lds, st>>>(a);    \
+    else moe_glu_tok<8, R, SS, TOK_WV, RT><<<grid, 64 * TOK_WV, lds, st>>>(a);
 #define KMI_GLU(R, SS)                                                                  \
     if (rpw == R && S == SS) {                                                          \
-        if (bits == 4) moe_glu_tok<4, R, SS, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a); \
-        else moe_glu_tok<8, R, SS, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a);           \
+        if (a.logits) { KMI_GLU_R(R, SS, true) } else { KMI_GLU_R(R, SS, false) }       \
         return OK;                                                                      \
     }
     KMI_GLU(1, 1) KMI_GLU(1, 2) KMI_GLU(1, 4) KMI_GLU(2, 1) KMI_GLU(2, 2) KMI_GLU(2, 4) KMI_GLU(4, 1) KMI_GLU(4, 2)
 #undef KMI_GLU
+#undef KMI_GLU_R
     set_error("switch_glu: no gate/up kernel for %lld chunks per row", (long long)C);
     return EINVAL_ARG;
 }
@@ -352,8 +375,11 @@ int launch_moe_glu_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
 int launch_moe_down_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
     const int64_t CK = 128 / bits, C = a.K / CK;
     const int U = (int)ceil_div((int64_t)a.k * C, 64);
-    // two rows per wave while the grid keeps >= 2048 waves
-    const int rpw = U <= 4 && a.N * a.T / 2 >= 2048 ? 2 : 1;
+    // two rows per wave while the grid keeps >= 2048 waves (KMI_DOWN_RPW
+    // overrides: tuning)
+    int rpw = U <= 4 && a.N * a.T / 2 >= 2048 ? 2 : 1;
+    const char* ov = getenv("KMI_DOWN_RPW");
+    if (ov && *ov) rpw = atoi(ov) == 2 && U <= 4 ? 2 : 1;
     const dim3 grid((unsigned)ceil_div(a.N, TOK_WV * rpw), (unsigned)a.T);
     const size_t lds = (size_t)a.k * ((size_t)a.K * 2 + (size_t)C * 16);
     if (a.E * a.N * (a.K * bits / 8) >= (1LL << 31)) {

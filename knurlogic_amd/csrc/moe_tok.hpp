@@ -14,7 +14,10 @@ struct MoeTokArgs {
     const uint32_t* w1;         // gate/up: up rows (same layout as the gate rows)
     const uint16_t* s1;
     const uint16_t* b1;
-    const int32_t* inds;        // [T, k]
+    const int32_t* inds;        // [T, k] (gate/up: unused when logits are given)
+    const uint16_t* logits;     // gate/up only: [T, E] bf16 router logits, routed in the kernel, or null
+    int32_t* inds_out;          // with logits: [T, k] experts written (for the down kernel and the caller)
+    uint16_t* scores_out;       // with logits: [T, k] bf16 scores written
     const uint16_t* scores;     // [T, k] bf16, or null (down: write y, no combine)
     uint16_t* out;              // gate/up: act [T*k, N]; down: [T, N] or y [T*k, N]
     int64_t E, N, K, T;

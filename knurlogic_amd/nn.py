@@ -24,7 +24,7 @@ import math
 
 import torch
 
-from .ops import (add_bias, gather_qmm, linear, moe_combine, moe_route, moe_shared_add, quantize,
+from .ops import (add_bias, gather_qmm, linear, moe_combine, moe_experts, moe_route, moe_shared_add, quantize,
                   quantized_matmul, swiglu, switch_glu, vq_gather_qmm, vq_glu, vq_packed_gather_qmm,
                   vq_packed_glu, vq_switch_glu)
 
@@ -317,9 +317,18 @@ class SparseMoeBlock:
         self.norm_topk_prob = True
 
     def experts(self, x, logits):
-        """The routed part from given router logits: route, experts, combine."""
+        """The routed part from given router logits: route, experts, combine
+        (one library call when the experts take it: the gate/up kernel then
+        routes each token itself at decode sizes)."""
+        sm = self.switch_mlp
+        if (isinstance(sm, SwitchGLU) and sm._one_call(self.top_k) and x.dtype == torch.bfloat16
+                and logits.dtype == torch.bfloat16 and logits.shape[-1] <= 1024):
+            f, d = sm.fused, sm.down_proj
+            out, _, _ = moe_experts(x, logits, self.top_k, f.weight, f.scales, f.biases, d.weight, d.scales,
+                                    d.biases, f.group_size, f.bits)
+            return out
         inds, scores = moe_route(logits, self.top_k)
-        return self.switch_mlp.combine(x, inds, scores)
+        return sm.combine(x, inds, scores)
 
     def __call__(self, x):
         y = self.experts(x, self.gate(x))

@@ -693,6 +693,37 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, w_gu, s_gu, b_gu, w_down,
     return out
 
 
+def moe_experts(x: torch.Tensor, logits: torch.Tensor, k: int, w_gu, s_gu, b_gu, w_down, s_down, b_down,
+                group_size: int = 64, bits: int = 4):
+    """SparseMoeBlock's routed part from its router logits in one library
+    call (kmi_moe_experts): route (as ``moe_route``), SwitchGLU, weighted
+    combine.  x [..., H] and logits [..., E] bf16.  Returns (out [..., H],
+    inds [..., k] int32, scores [..., k])."""
+    _on_gpu(x, logits, w_gu, s_gu, b_gu, w_down, s_down, b_down)
+    if x.dtype != torch.bfloat16 or logits.dtype != torch.bfloat16:
+        raise ValueError("moe_experts: bfloat16 activations and logits only")
+    lead, H = tuple(x.shape[:-1]), x.shape[-1]
+    if tuple(logits.shape[:-1]) != lead:
+        raise ValueError("moe_experts: logits [..., E] must match x [..., H]")
+    E = logits.shape[-1]
+    I = w_gu.shape[1] // 2
+    T = math.prod(lead)
+    out = torch.empty(*lead, H, dtype=x.dtype, device=x.device)
+    inds = torch.empty(*lead, k, dtype=torch.int32, device=x.device)
+    scores = torch.empty(*lead, k, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out, inds, scores
+    xc, lc = x.contiguous(), logits.contiguous()
+    ts = [t.contiguous() for t in (w_gu, s_gu, b_gu, w_down, s_down, b_down)]
+    L = _lib()
+    nbytes = L.kmi_switch_glu_workspace_bytes(T, H, I, k, E, group_size, bits)
+    ws = _workspace(nbytes, x.device)
+    _abi.check(L.kmi_moe_experts(_ptr(xc), _ptr(lc), T, H, I, k, E, *[_ptr(t) for t in ts], DTYPE_CODE[x.dtype],
+                                 group_size, bits, _ptr(out), _ptr(inds), _ptr(scores), _ptr(ws), nbytes,
+                                 _stream(x)), "moe_experts")
+    return out, inds, scores
+
+
 # --- VQ codebook-decode experts ---------------------------------------------------
 
 _CODE_BYTES = {torch.uint8: 1, torch.uint16: 2, torch.int16: 2}

@@ -164,3 +164,30 @@ def test_sparse_moe_block_matches_the_oracle(dev, T):
     assert_close(to_numpy(got), ref, what="moe block")
     # the routed part alone, from the same logits
     assert_close(to_numpy(block.experts(to_torch(x, dev, BF), tl)), y, what="experts")
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 16])
+def test_moe_experts_routes_in_the_kernel_like_the_router(dev, T):
+    """kmi_moe_experts (one call from the router logits): at decode sizes
+    the gate/up kernel routes each token itself.  The experts and scores
+    equal kmi_moe_route's bit for bit, the output equals route + SwitchGLU
+    bit for bit, and both match the oracle (the matmul bar)."""
+    rng = np.random.default_rng(300 + T)
+    E, H, I, k = 128, 2048, 768, 8
+    glu, fns = _experts(rng, E, H, I, dev)
+    x = bf16_normal(rng, (T, H))
+    logits = bf16_normal(rng, (T, E))
+    tx, tl = to_torch(x, dev, BF), to_torch(logits, dev, BF)
+    f, d = glu.fused, glu.down_proj
+    out, inds, scores = K.moe_experts(tx, tl, k, f.weight, f.scales, f.biases, d.weight, d.scales, d.biases)
+    ri, rs = K.moe_route(tl, k)
+    assert torch.equal(inds, ri) and torch.equal(scores, rs)
+    oi, os_ = O.route(logits, k)
+    np.testing.assert_array_equal(inds.cpu().numpy(), oi)
+    _bits_equal(to_numpy(scores), os_)
+    assert torch.equal(out, glu.combine(tx, ri, rs))
+    ref = O.combine(O.switch_glu(x, oi, *fns), os_)
+    assert_close(to_numpy(out), ref, what=f"moe_experts T={T}")
+    # and the block's routed part takes this call
+    block = nn.SparseMoeBlock(None, glu, k)
+    assert torch.equal(block.experts(tx, tl), out)
