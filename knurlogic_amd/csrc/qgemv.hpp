@@ -67,4 +67,10 @@ int launch_sort_rows(const int32_t* rhs, int64_t P, int64_t Mper, int E, int tm,
 int launch_qgemv(const QgArgs& a, const QgPlan& p, int bits, int gs, bool glu, int64_t ntiles,
                  hipStream_t st);
 
+// Dense calls of 1..16 rows with direct-to-LDS staging (qgemv_dl.hip):
+// 4 or 8 bits, groups of 32 or 64, K a multiple of 256.
+bool qgemv_dl_supported(int64_t M, int64_t K, int bits, int gs);
+QgPlan plan_qgemv_dl(int64_t N, int64_t K);
+int launch_qgemv_dl(const QgArgs& a, const QgPlan& p, int bits, int gs, hipStream_t st);
+
 }  // namespace kmi

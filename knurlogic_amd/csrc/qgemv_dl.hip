@@ -1,0 +1,283 @@
+// Dense quantized matmul for 2..16 activation rows on gfx950, with the
+// weight, x and scale/bias tiles staged by direct-to-LDS buffer loads
+// (buffer_load_dwordx4 ... lds): the decode / MTP-verify shapes of
+// mx.quantized_matmul (nn.QuantizedLinear, src/knurlogic/engine/model/
+// load_model.py:124-144; the 9..31-row calls of engine/matmul_padding.py:
+// 94-105 included).
+//
+//   y[m, n] = sum_g ( s[n, g] * P[m, n, g] + b[n, g] * X[m, g] )
+//   P[m, n, g] = sum_{k in g} x[m, k] q[n, k],   X[m, g] = sum_{k in g} x[m, k]
+//
+// A workgroup owns 64 weight rows (16 per wave: the n of
+// v_mfma_f32_16x16x32_bf16) and walks its share of K in chunks of 256 codes
+// through NS LDS stages, NS - 1 chunks in flight: the loads write LDS
+// directly, so the depth costs no registers, and the wait for a chunk is an
+// explicit vmcnt (the DMA loads return nothing to registers) followed by a
+// barrier.  The DMA writes a wave's 64 lanes as one contiguous 1 KB block, so
+// the bank-conflict swizzles are applied on the global side: lane slot s of
+// a weight or x row holds the row's 16-byte piece s ^ (row & 7), and weight
+// blocks are padded by 16 bytes.  x is staged in its natural k order, so
+// 4-bit codes are decoded in natural order too (two v_perm_b32 + four
+// fp8 -> bf16 conversions per 8 codes, exact).  Per chunk every LDS read is
+// issued first, then the groups' independent MFMA chains, then the
+// per-group scale / bias FMAs.
+#include "qgemv.hpp"
+#include "../../include/knurlogic_amd.h"
+
+#define KMI_LDSP(p) ((__attribute__((address_space(3))) void*)(p))
+
+namespace kmi {
+
+namespace {
+
+constexpr int DL_KC = 256;                // codes per chunk
+constexpr int DL_ROWS = 64;               // weight rows per workgroup
+constexpr int DL_NS = 4;                  // LDS stages
+constexpr int DL_WBLK_BYTES = 1024 + 16;  // one DMA block of weight rows, padded
+constexpr uint32_t DL_NONE = 0x80000000u; // an offset past every buffer: reads 0
+
+// 8 codes (code i at bits 4i) -> 8 exact bf16 in natural order: a byte q in
+// 0..15 read as fp8 e4m3 is q * 2^-9, and the conversion's scale 2^9 is exact
+__device__ __forceinline__ u32x4 nib8_natural(uint32_t w) {
+    const uint32_t lo = w & 0x0F0F0F0Fu;            // codes 0, 2, 4, 6
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;     // codes 1, 3, 5, 7
+    const uint32_t a = __builtin_amdgcn_perm(hi, lo, 0x05010400u);   // [c0, c1, c2, c3]
+    const uint32_t b = __builtin_amdgcn_perm(hi, lo, 0x07030602u);   // [c4, c5, c6, c7]
+    u32x4 r;
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(a, 512.f, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(a, 512.f, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(b, 512.f, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(b, 512.f, true));
+    return r;
+}
+
+template <int N_>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N_ >= 0 && N_ < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_) : "memory");
+}
+
+// One DMA load: lane i's `size` bytes at voff + soff land at lds + i * size.
+// (Device functions, not the builtin itself inside the kernel template's
+// lambda: there the builtin stops hipcc emitting the host launch stubs.)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff,
+                                      int aux) {
+    if (aux) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KMI_LDSP(lds), 16, voff, soff, 0, AUX_NT);
+    else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KMI_LDSP(lds), 16, voff, soff, 0, 0);
+}
+
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KMI_LDSP(lds), 4, voff, soff, 0, 0);
+}
+
+template <int BITS, int GS>
+struct DlShape {
+    static constexpr int RB = DL_KC * BITS / 8;          // weight bytes per row per chunk
+    static constexpr int RPI = 1024 / RB;                // weight rows per DMA block
+    static constexpr int WBLK = DL_ROWS / RPI;           // weight blocks per chunk
+    static constexpr int PPR = RB / 16;                  // 16-byte pieces per weight row
+    static constexpr int W_BYTES = WBLK * DL_WBLK_BYTES;
+    static constexpr int XI = 8;                         // x blocks per chunk: 2 rows of 512 bytes each
+    static constexpr int X_BYTES = 16 * DL_KC * 2;
+    static constexpr int GPC = DL_KC / GS;               // groups per chunk
+    static constexpr int DPR = GPC / 2;                  // scale dwords per row per chunk
+    static constexpr int SBI = 2 * DPR;                  // scale + bias blocks per chunk
+    static constexpr int SB_BYTES = 2 * DL_ROWS * GPC * 2;
+    static constexpr int STAGE = W_BYTES + X_BYTES + SB_BYTES;
+    static constexpr int PER_WAVE = WBLK / 4 + XI / 4 + SBI / 4;   // DMA loads per wave per chunk
+    static constexpr int GB = GS * BITS / 8;             // bytes per row per group
+    static constexpr int LB = GB / 4;                    // bytes of a group per lane (k run)
+    static constexpr int NT = GS / 32;                   // MFMAs per group
+    static_assert(WBLK % 4 == 0 && XI % 4 == 0 && SBI % 4 == 0, "every wave issues the same loads");
+    static_assert(LB == 4 || LB == 8 || LB == 16, "lane run of 4, 8 or 16 bytes");
+};
+
+}  // namespace
+
+template <int BITS, int GS>
+__global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
+    using S_ = DlShape<BITS, GS>;
+    constexpr int RB = S_::RB, RPI = S_::RPI, WBLK = S_::WBLK, PPR = S_::PPR, W_BYTES = S_::W_BYTES;
+    constexpr int X_BYTES = S_::X_BYTES, GPC = S_::GPC, DPR = S_::DPR, SBI = S_::SBI, STAGE = S_::STAGE;
+    constexpr int GB = S_::GB, LB = S_::LB, NT = S_::NT;
+    constexpr int PER_WAVE = S_::PER_WAVE;
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t n0 = (int64_t)blockIdx.x * DL_ROWS;
+    const int64_t K = a.K, G = K / GS, M = a.rows;
+    const uint32_t rowbytes = (uint32_t)(K * BITS / 8);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, a.N * (int64_t)rowbytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s, a.N * G * 2);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b, a.N * G * 2);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, M * K * 2);
+    const int chunks = (int)(K / DL_KC);
+    const int c0 = (int)blockIdx.y * a.gps;
+    const int nc = chunks - c0 < a.gps ? chunks - c0 : a.gps;
+
+    // per-lane parts of the DMA offsets (rows past N / past M read zeros)
+    uint32_t wv[WBLK / 4];
+#pragma unroll
+    for (int j = 0; j < WBLK / 4; j++) {
+        const int r = (wave + 4 * j) * RPI + lane / PPR, slot = lane % PPR;
+        wv[j] = n0 + r < a.N ? (uint32_t)(n0 + r) * rowbytes + 16u * (uint32_t)(slot ^ (r & 7)) : DL_NONE;
+    }
+    uint32_t xv[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int m = 2 * (wave + 4 * j) + lane / 32, slot = lane % 32;
+        xv[j] = m < M ? (uint32_t)(m * K * 2) + 16u * (uint32_t)(slot ^ (m & 7)) : DL_NONE;
+    }
+    uint32_t sbv[SBI / 4];
+    int sbo[SBI / 4], sbw[SBI / 4];
+#pragma unroll
+    for (int j = 0; j < SBI / 4; j++) {
+        const int q = wave + 4 * j, which = q / DPR, d = q % DPR;
+        const int row = d * (DL_ROWS / DPR) + lane / DPR;
+        sbv[j] = n0 + row < a.N ? (uint32_t)((n0 + row) * G * 2) + 4u * (uint32_t)(lane % DPR) : DL_NONE;
+        sbo[j] = which * (DL_ROWS * GPC * 2) + d * 256;
+        sbw[j] = which;
+    }
+
+    // chunk i of this split into stage i % NS; past the split's chunks every
+    // load reads zeros into a stage that is never read again
+    auto issue = [&](int i) {
+        const bool live = i < nc;
+        const uint32_t c = (uint32_t)(c0 + (live ? i : 0));
+        unsigned char* base = smem + (i % DL_NS) * STAGE;
+#pragma unroll
+        for (int j = 0; j < WBLK / 4; j++)
+            dma16(rw, base + (wave + 4 * j) * DL_WBLK_BYTES, live ? wv[j] : DL_NONE, c * RB, 1);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            dma16(rx, base + W_BYTES + (wave + 4 * j) * 1024, live ? xv[j] : DL_NONE, c * (DL_KC * 2), 0);
+#pragma unroll
+        for (int j = 0; j < SBI / 4; j++)
+            dma4(sbw[j] ? rb : rs, base + W_BYTES + X_BYTES + sbo[j], live ? sbv[j] : DL_NONE, c * (GPC * 2));
+    };
+#pragma unroll
+    for (int i = 0; i < DL_NS - 1; i++) issue(i);
+
+    const int nl = lane & 15, j4 = lane >> 4;
+    const int wr = wave * 16 + nl;                       // this lane's weight row in the tile
+    const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < nc; i++) {
+        wait_vmcnt<PER_WAVE * (DL_NS - 2)>();            // this wave's loads of chunk i are in LDS
+        __builtin_amdgcn_s_barrier();                    // and every wave's
+        const unsigned char* base = smem + (i % DL_NS) * STAGE;
+        const unsigned char* wl = base + (wr / RPI) * DL_WBLK_BYTES + (wr % RPI) * RB;
+        const unsigned char* xl = base + W_BYTES + nl * (DL_KC * 2);
+        const uint16_t* sl = (const uint16_t*)(base + W_BYTES + X_BYTES);
+#pragma unroll
+        for (int h = 0; h < GPC; h += 4) {
+            constexpr int GH = GPC < 4 ? GPC : 4;
+            u32x4 wd[GH];
+            u32x4 A[GH][NT];
+            float sc[GH], bi[GH];
+#pragma unroll
+            for (int g = 0; g < GH; g++) {
+                const int gi = h + g;
+                const int off = gi * GB + j4 * LB;
+                const unsigned char* p = wl + 16 * ((off / 16) ^ (wr & 7)) + off % 16;
+                if constexpr (LB == 4) wd[g] = u32x4{*(const uint32_t*)p, 0u, 0u, 0u};
+                else if constexpr (LB == 8) {
+                    const u32x2 t = *(const u32x2*)p;
+                    wd[g] = u32x4{t.x, t.y, 0u, 0u};
+                } else wd[g] = *(const u32x4*)p;
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const int xp = gi * (GS / 8) + j4 * (GS / 32) + t;
+                    A[g][t] = *(const u32x4*)(xl + 16 * (xp ^ (nl & 7)));
+                }
+                sc[g] = bf16_to_f32(sl[wr * GPC + gi]);
+                bi[g] = bf16_to_f32(sl[DL_ROWS * GPC + wr * GPC + gi]);
+            }
+            f32x4 P[GH], X[GH];
+#pragma unroll
+            for (int g = 0; g < GH; g++) {
+                P[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+                X[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+#pragma unroll
+                for (int g = 0; g < GH; g++) {
+                    u32x4 B;
+                    if constexpr (BITS == 4) B = nib8_natural(wd[g][t]);
+                    else B = u32x4{bytes_to_bf16x2(wd[g][2 * t], 0), bytes_to_bf16x2(wd[g][2 * t], 2),
+                                   bytes_to_bf16x2(wd[g][2 * t + 1], 0), bytes_to_bf16x2(wd[g][2 * t + 1], 2)};
+                    X[g] = mfma16x16x32(A[g][t], ones, X[g]);
+                    P[g] = mfma16x16x32(A[g][t], B, P[g]);
+                }
+#pragma unroll
+            for (int g = 0; g < GH; g++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    acc[e] = __builtin_fmaf(sc[g], P[g][e], __builtin_fmaf(bi[g], X[g][e], acc[e]));
+        }
+        issue(i + DL_NS - 1);
+    }
+    wait_vmcnt<0>();                                     // no LDS write may land after the workgroup ends
+
+    // D of the MFMA: item e is x row 4 * j4 + e, column nl (weight row wr)
+    const int64_t n = n0 + wr;
+    if (n < a.N) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int64_t m = 4 * j4 + e;
+            if (m < M) {
+                if (a.S == 1) a.y[m * a.N + n] = f32_to_bf16(acc[e]);
+                else a.partial[((int64_t)blockIdx.y * M + m) * a.N + n] = acc[e];
+            }
+        }
+    }
+}
+
+namespace {
+
+template <int BITS, int GS>
+int launch_dl(const QgArgs& a, dim3 grid, hipStream_t st) {
+    constexpr size_t lds = (size_t)DL_NS * DlShape<BITS, GS>::STAGE;
+    static_assert(lds <= 160 * 1024, "qgemv_dl stages exceed the LDS");
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void*)qgemv_dl_kernel<BITS, GS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds);
+        attr = true;
+    }
+    qgemv_dl_kernel<BITS, GS><<<grid, 256, lds, st>>>(a);
+    return OK;
+}
+
+}  // namespace
+
+bool qgemv_dl_supported(int64_t M, int64_t K, int bits, int gs) {
+    return M >= 1 && M <= 16 && K % DL_KC == 0 && (bits == 4 || bits == 8) && (gs == 32 || gs == 64);
+}
+
+// K splits so the grid reaches about one workgroup per CU, each split
+// keeping at least 4 chunks
+QgPlan plan_qgemv_dl(int64_t N, int64_t K) {
+    const int64_t tiles = ceil_div(N, DL_ROWS), chunks = K / DL_KC;
+    int64_t S = 1;
+    while (tiles * S * 2 <= 256 && chunks / (S * 2) >= 4) S *= 2;
+    QgPlan p = {};
+    p.gps = (int)ceil_div(chunks, S);
+    p.S = (int)ceil_div(chunks, p.gps);     // no split without chunks
+    p.mc = 1;
+    return p;
+}
+
+int launch_qgemv_dl(const QgArgs& a, const QgPlan& p, int bits, int gs, hipStream_t st) {
+    const dim3 grid((unsigned)ceil_div(a.N, DL_ROWS), (unsigned)p.S);
+    if (bits == 4 && gs == 64) return launch_dl<4, 64>(a, grid, st);
+    if (bits == 4 && gs == 32) return launch_dl<4, 32>(a, grid, st);
+    if (bits == 8 && gs == 64) return launch_dl<8, 64>(a, grid, st);
+    if (bits == 8 && gs == 32) return launch_dl<8, 32>(a, grid, st);
+    set_error("quantized_matmul: no direct-to-LDS kernel for %d bits, group %d", bits, gs);
+    return EINVAL_ARG;
+}
+
+}  // namespace kmi

@@ -258,11 +258,11 @@ static size_t skinny_partial_bytes(const QgPlan& p, int64_t rows, int64_t N) {
 
 // qgemv launch plus the in-order reduction of K-split partials
 static int run_skinny(QgArgs& a, const QgPlan& p, int bits, int gs, int64_t ntiles, void* partial,
-                      const int32_t* rhs, int64_t Mper, hipStream_t st) {
+                      const int32_t* rhs, int64_t Mper, bool dl, hipStream_t st) {
     a.S = p.S; a.gps = p.gps; a.partial = (float*)partial;
-    int rc = launch_qgemv(a, p, bits, gs, false, ntiles, st);
+    int rc = dl ? launch_qgemv_dl(a, p, bits, gs, st) : launch_qgemv(a, p, bits, gs, false, ntiles, st);
     if (rc) return rc;
-    KMI_CHECK_LAUNCH("qgemv");
+    KMI_CHECK_LAUNCH(dl ? "qgemv_dl" : "qgemv");
     if (p.S > 1) {
         const int64_t count = a.rows * a.N;
         qmv_reduce<<<(unsigned)ceil_div(count, 256), 256, 0, st>>>(a.partial, p.S, count, a.N, rhs, Mper,
@@ -270,6 +270,19 @@ static int run_skinny(QgArgs& a, const QgPlan& p, int bits, int gs, int64_t ntil
         KMI_CHECK_LAUNCH("qmv_reduce");
     }
     return OK;
+}
+
+// Dense 2..16-row calls take the direct-to-LDS kernel where it has a
+// variant (KMI_QGEMV_DL=0 keeps them on qgemv, for comparisons)
+static bool use_dl(int64_t M, int64_t K, int bits, int gs) {
+    static const int on = env_int("KMI_QGEMV_DL", 1);
+    return on != 0 && qgemv_dl_supported(M, K, bits, gs);
+}
+
+static QgPlan dense_skinny_plan(int64_t M, int64_t K, int64_t N, int bits, int gs) {
+    if (use_dl(M, K, bits, gs)) return plan_qgemv_dl(N, K);
+    const int tm = skinny_tile_rows(M);
+    return plan_qgemv(N, K, ceil_div(M, tm), tm, gs);
 }
 
 // rows per tile for gather: average routed rows per active expert
@@ -289,8 +302,7 @@ size_t kmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, 
     if (M <= 0 || K <= 0 || N <= 0 || group_size <= 0 || (bits != 4 && bits != 8)) return 0;
     if (M > SKINNY_MAX_M) return qmm_gemm_workspace(M, K, N);       // GEMM path (split-K partials)
     if (choose_kind(M, K, bits) != QmvKind::SKINNY) return 0;   // VALU path
-    const int tm = skinny_tile_rows(M);
-    return skinny_partial_bytes(plan_qgemv(N, K, ceil_div(M, tm), tm, group_size), M, N);
+    return skinny_partial_bytes(dense_skinny_plan(M, K, N, bits, group_size), M, N);
 }
 
 int kmi_qmm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
@@ -322,7 +334,8 @@ int kmi_qmm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
     }
     const int tm = skinny_tile_rows(M);
     const int64_t ntiles = ceil_div(M, tm);
-    const QgPlan p = plan_qgemv(N, K, ntiles, tm, group_size);
+    const bool dl = use_dl(M, K, bits, group_size);
+    const QgPlan p = dense_skinny_plan(M, K, N, bits, group_size);
     const size_t need = skinny_partial_bytes(p, M, N);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
         set_error("quantized_matmul: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
@@ -332,7 +345,7 @@ int kmi_qmm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
     a.x = (const uint16_t*)x; a.xrows = M; a.w = w; a.s = (const uint16_t*)scales;
     a.b = (const uint16_t*)biases; a.E = 1; a.N = N; a.K = K; a.erows = N; a.y = (uint16_t*)y;
     a.rows = M; a.tm = tm; a.lhs_div = 1; a.Mper = 1;
-    return run_skinny(a, p, bits, group_size, ntiles, workspace, nullptr, 1, st);
+    return run_skinny(a, p, bits, group_size, ntiles, workspace, nullptr, 1, dl, st);
 }
 
 size_t kmi_gather_qmm_workspace_bytes(int64_t P, int64_t M, int64_t E, int64_t K,
@@ -394,7 +407,7 @@ int kmi_gather_qmm(const void* x, int64_t X, int64_t M, int64_t K, const uint32_
     a.b = (const uint16_t*)biases; a.E = E; a.N = N; a.K = K; a.erows = N; a.y = (uint16_t*)y;
     a.rows = rows; a.tm = tm; a.tiles = sr.tiles; a.sorted = sr.sorted; a.lhs = lhs; a.lhs_div = 1;
     a.Mper = M;
-    return run_skinny(a, p, bits, group_size, sr.max_tiles, partial, rhs, M, st);
+    return run_skinny(a, p, bits, group_size, sr.max_tiles, partial, rhs, M, false, st);
 }
 
 }  // extern "C"

@@ -87,9 +87,15 @@ def test_rows_are_independent_bit_for_bit(dev):
     rng = np.random.default_rng(11)
     (wq, s, b), (tw, ts, tb) = _weights(rng, (256, 512), 4, 64, dev)
     x = to_torch(bf16_normal(rng, (128, 512)), dev, BF)
-    # skinny MFMA kernel: 2..64 rows (16-, 32- and 64-row tiles)
+    # direct-to-LDS MFMA kernel: 2..16 rows
+    y16 = K.quantized_matmul(x[:16], tw, ts, tb, True, 64, 4)
+    for m in (2, 5, 9, 15):
+        ym = K.quantized_matmul(x[:m], tw, ts, tb, True, 64, 4)
+        assert torch.equal(ym, y16[:m]), m
+    # skinny MFMA kernel: 17..64 rows (32- and 64-row tiles); the padded
+    # 9..31-row calls of the reference land here as 32-row calls
     y64 = K.quantized_matmul(x[:64], tw, ts, tb, True, 64, 4)
-    for m in (2, 5, 9, 16, 17, 31, 40):
+    for m in (17, 31, 32, 40):
         ym = K.quantized_matmul(x[:m], tw, ts, tb, True, 64, 4)
         assert torch.equal(ym, y64[:m]), m
     # GEMM: 65..128 rows
@@ -154,6 +160,22 @@ def test_gather_qmm_unsorted_and_sorted(dev, T, k, bits):
                       sorted_indices=True)
     assert ys.shape == (T * k, 1, N)
     assert_close(to_numpy(ys)[np.argsort(order)].reshape(T, k, 1, N), ref, what="sorted")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("M,N,K_", [(2, 100, 256), (7, 64, 768), (15, 200, 1280), (16, 1000, 4096),
+                                    (9, 64, 256 * 33)])
+def test_qmm_direct_lds_rows(dev, bits, group, M, N, K_):
+    """2..16 rows, 4/8 bits, groups of 32/64: the direct-to-LDS kernel.
+    Ragged N (rows past N read zeros), one chunk, odd chunk counts, and a
+    33-chunk K cut into 7 splits of 5 (the last split shorter)."""
+    rng = np.random.default_rng(31 * M + N + K_ + bits + group)
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (N, K_), bits, group, dev)
+    x = bf16_normal(rng, (M, K_))
+    y = K.quantized_matmul(to_torch(x, dev, BF), tw, ts, tb, True, group, bits)
+    ref = O.quantized_matmul(x, wq, s, b, True, group, bits, "float32")
+    assert_close(to_numpy(y), ref, what=f"M={M} N={N} K={K_} bits={bits} g={group}")
 
 
 @pytest.mark.parametrize("bits", [4, 8])
