@@ -423,6 +423,75 @@ def bench_mx_moe(T, calls, dev, mode="mxfp4"):
             "bound": "hbm", "bytes": nbytes, "flops": 2.0 * T * k * 3 * H * I}
 
 
+def ceilings(dev, headline_bytes):
+    """Measured ceilings beside the published peaks: the HBM read rate of a
+    plain read kernel (kmi_read_probe, 16-byte nontemporal loads, nothing
+    computed) over the headline's per-call bytes with the buffers rotated
+    past the Infinity Cache as the headline's are, and over 1 GiB; and the
+    bf16 GEMM rate of torch.matmul (hipBLASLt) on the prefill shapes with
+    unquantized bf16 weights."""
+    import ctypes
+    import torch
+    from knurlogic_amd import _abi
+    L = _abi.load()
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def read_rate(nbytes, wgs):
+        nbytes = nbytes // 16 * 16
+        n = max(4, math.ceil(ROTATE_BYTES / nbytes))
+        bufs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(n)]
+        calls = max(n, 40)
+
+        def run():
+            st = torch.cuda.current_stream().cuda_stream
+            for i in range(calls):
+                _abi.check(L.kmi_read_probe(ctypes.c_void_p(bufs[i % n].data_ptr()), nbytes, wgs,
+                                            ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(st)), "read_probe")
+
+        us = time_graph(run) * 1e3 / calls
+        del bufs
+        torch.cuda.empty_cache()
+        return nbytes / (us * 1e-6) / 1e9, us
+
+    res = {}
+    best = max((read_rate(headline_bytes, w) + (w,) for w in (512, 1024, 2048, 4096)), key=lambda t: t[0])
+    res["read_headline_bytes"] = {"bytes": headline_bytes // 16 * 16, "GBps": round(best[0], 1),
+                                  "us": round(best[1], 3), "workgroups": best[2],
+                                  "frac_of_published": round(best[0] / PEAK_HBM_GBS, 4)}
+    big = max((read_rate(1 << 30, w) + (w,) for w in (2048, 8192)), key=lambda t: t[0])
+    res["read_1GiB"] = {"GBps": round(big[0], 1), "us": round(big[1], 3), "workgroups": big[2],
+                        "frac_of_published": round(big[0] / PEAK_HBM_GBS, 4)}
+    for N, K in ((14336, 4096), (4096, 14336)):
+        g = torch.Generator(device=dev).manual_seed(N)
+        x = torch.randn(512, K, device=dev, generator=g).to(torch.bfloat16)
+        w = torch.randn(K, N, device=dev, generator=g).to(torch.bfloat16)     # [K, N]: no transposed view
+        y = torch.empty(512, N, device=dev, dtype=torch.bfloat16)
+        calls = 30
+
+        def mm():
+            for _ in range(calls):
+                torch.matmul(x, w, out=y)
+
+        us = time_graph(mm) * 1e3 / calls
+        tf = 2.0 * 512 * N * K / (us * 1e-6) / 1e12
+        res[f"bf16_gemm_512x{N}x{K}"] = {"us": round(us, 3), "TFLOPs": round(tf, 1),
+                                        "frac_of_published": round(tf / PEAK_BF16_TFLOPS, 4),
+                                        "what": "torch.matmul bf16 (hipBLASLt), unquantized weights, warm"}
+        del x, w, y
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 HEADLINE_PROFILE = ROOT / "profiles" / "qmv_4bit_14336x4096_m1.md"
 
 
@@ -458,7 +527,7 @@ def cpu_baseline(seconds=10.0):
     dt = (time.perf_counter() - t0) / n
     gbs = dense_bytes(1, N, K, 4) / dt / 1e9
     return {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "us_per_call": round(dt * 1e6, 1),
+            "cpu_model": cpu_model(), "us_per_call": round(dt * 1e6, 1),
             "sample": f"oracle quantized_matmul (C/OpenMP, float64 accumulate), 4-bit g64 "
                       f"[14336,4096] M=1, {n} calls in {seconds:.0f} s"}
 
@@ -472,6 +541,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="detail sections, comma-separated "
                                                 "(dense, kv8, kvcache, qsdpa, moe, vq); default all")
+    ap.add_argument("--no-ceilings", action="store_true",
+                    help="skip the measured read and bf16 GEMM ceilings")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 10 plain device copies of MIB MiB (the known-size kernel "
                          "that calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -555,6 +626,7 @@ def main():
         detail.append(bench_dense(4, 1, 4096, 4096, True, 200, dev))
         detail.append(bench_dense(4, 1, 4096, 4096, False, 200, dev))
 
+    ceil = None if (args.quick or args.no_ceilings) else ceilings(dev, nbytes)
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
@@ -569,7 +641,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": profiled_traffic(),
                      "algorithmic_bytes": nbytes, "launch_us": round(us, 3),
-                     "traffic_source": "profiles/qmv_4bit_14336x4096_m1.md"},
+                     "traffic_source": "profiles/qmv_4bit_14336x4096_m1.md",
+                     "measured_read_ceiling": (ceil or {}).get("read_headline_bytes")},
+        "ceilings": ceil,
         "cpu_baseline": cpu,
         "detail": detail,
     }

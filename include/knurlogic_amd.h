@@ -458,6 +458,17 @@ int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, con
                       int64_t E, int dtype, void* out, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/*
+ * Calibration only (no counterpart in the reference): reads `bytes` of
+ * device memory at `p` with `workgroups` workgroups of 16-byte nontemporal
+ * loads, as the GEMV kernels load their weights, and computes nothing, so
+ * a timed call gives the HBM read rate the GPU reaches at that size (the
+ * measured ceiling beside the published 8 TB/s).  `out` (one uint32) is
+ * written only for data whose XOR is a fixed value no test relies on.
+ * bytes: a positive multiple of 16 under 2 GiB.
+ */
+int kmi_read_probe(const void* p, int64_t bytes, int workgroups, uint32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
