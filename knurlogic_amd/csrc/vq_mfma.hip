@@ -56,6 +56,13 @@ __device__ __forceinline__ u32x4 bf16x8_to_f16x8(u32x4 v) {
 }
 
 constexpr uint32_t NONE = 0x80000000u;      // an offset past every buffer: reads 0
+
+// One direct-to-LDS load: lane i's 16 bytes at `voff` land at lds + 16 i
+// (a device function: the builtin inside a kernel template's lambda stops
+// hipcc emitting the host launch stubs).
+__device__ __forceinline__ void vq_dma16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
 constexpr int WG = 256;                     // 4 waves
 constexpr int TM = VQM_TILE_ROWS;           // tile rows (MFMA M)
 
@@ -99,10 +106,11 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
 
     const int xstride = K * 2 + 16;                  // bytes per staged x row (padded: rows on distinct banks)
     const bool two_cb = NSET == 2 && a.cb1 != a.cb0;
-    const int ncb = a.kc * (two_cb ? 2 : 1);         // codebook pieces (16 B each)
+    const int cbb = (a.kc + 63) / 64;                // 1 KB blocks per codebook
+    const int nblk = cbb * (two_cb ? 2 : 1);
     unsigned char* cbl0 = smem;
-    unsigned char* cbl1 = smem + (two_cb ? (size_t)a.kc * 16 : 0);
-    unsigned char* xs = smem + (size_t)ncb * 16;
+    unsigned char* cbl1 = smem + (two_cb ? (size_t)cbb * 1024 : 0);
+    unsigned char* xs = smem + (size_t)nblk * 1024;
     f32x4* red = (f32x4*)(xs + (size_t)a.tile_rows * xstride);   // [4 waves][NSET][64], KS > 1
 
     // Sorted row ids of the tile, by scalar loads (tracked apart from the
@@ -119,36 +127,44 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
         return a.lhs_magic ? (int)__umulhi(r, a.lhs_magic) : (int)r;
     };
 
-    // ---- staging: codebook entries (16 B) and the tile's x rows (8 bf16 ->
-    // 8 fp16 per piece).  The first codebook pieces and x rows 0 and 1 are
-    // loaded into registers ahead of the code stream (loads complete in
-    // issue order); anything more is staged before the stream is issued.
+    // ---- staging, every load issued before any wait:
+    //  1. the codebook(s) by direct-to-LDS loads (1 KB per wave instruction,
+    //     nothing through registers; entries past kc read 0 and are never
+    //     gathered: codes are clamped to kc - 1);
+    //  2. the first x pieces of the tile (8 bf16 -> 8 fp16 per piece, at most
+    //     XB per thread in flight);
+    //  3. this lane's codes and row scales (the HBM stream);
+    //  then the x pieces are converted into LDS and the rest of x staged.
     const __amdgpu_buffer_rsrc_t rcb0 = make_rsrc(a.cb0, (int64_t)a.kc * 16);
     const __amdgpu_buffer_rsrc_t rcb1 = make_rsrc(a.cb1, (int64_t)a.kc * 16);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.X * a.K * 2);
-    auto cb_load = [&](int p) -> u32x4 {
-        const bool second = p >= a.kc;
-        const uint32_t off = p < ncb ? (uint32_t)(p - (second ? a.kc : 0)) * 16u : NONE;
-        return __builtin_amdgcn_raw_buffer_load_b128(second ? rcb1 : rcb0, (int)off, 0, 0);
-    };
-    auto cb_store = [&](int p, u32x4 v) {
-        if (p < ncb) *(u32x4*)(cbl0 + (size_t)p * 16) = v;     // cbl1 follows cbl0 directly
-    };
-    auto x_load = [&](int xr, int k8) -> u32x4 {
-        const uint32_t off = (xr >= 0 && xr < a.X && k8 < CPR) ? (uint32_t)(((int64_t)xr * K + k8 * 8) * 2) : NONE;
-        return __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
-    };
-    auto x_store = [&](int m, int k8, u32x4 v) {
-        if (k8 < CPR) *(u32x4*)(xs + (size_t)m * xstride + k8 * 16) = bf16x8_to_f16x8(v);
-    };
-    for (int p = tid + 2 * WG; p < ncb; p += WG) cb_store(p, cb_load(p));
-    for (int m = 0; m < count; m++) {
-        const int xr = xrow_of(m);
-        for (int k8 = tid + (m < 2 ? WG : 0); k8 < CPR; k8 += WG) x_store(m, k8, x_load(xr, k8));
+    for (int j = wave; j < nblk; j += 4) {
+        const bool second = j >= cbb;
+        const int p = (j - (second ? cbb : 0)) * 64 + lane;
+        vq_dma16(second ? rcb1 : rcb0, smem + (size_t)j * 1024, p < a.kc ? (uint32_t)p * 16u : NONE);
     }
-    const int xr0 = xrow_of(0), xr1 = count > 1 ? xrow_of(1) : -1;
-    const u32x4 c0 = cb_load(tid), c1 = cb_load(tid + WG);
-    const u32x4 x0 = x_load(xr0, tid), x1 = x_load(xr1, tid);
+    // x pieces: a batch is rows m0 .. m0 + XB - 1 at piece k8 of each (row ids
+    // by scalar loads: m is uniform); rows past the tile read 0, unstored
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.X * a.K * 2);
+    constexpr int XB = 8;
+    auto x_batch_load = [&](int m0, int k8, u32x4 (&v)[XB]) {
+#pragma unroll
+        for (int i = 0; i < XB; i++) {
+            const int m = m0 + i;
+            uint32_t off = NONE;
+            if (m < count && k8 < CPR) {
+                const int xr = xrow_of(m);
+                if (xr >= 0 && xr < a.X) off = (uint32_t)(((int64_t)xr * K + k8 * 8) * 2);
+            }
+            v[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+        }
+    };
+    auto x_batch_store = [&](int m0, int k8, const u32x4 (&v)[XB]) {
+#pragma unroll
+        for (int i = 0; i < XB; i++)
+            if (m0 + i < count && k8 < CPR) *(u32x4*)(xs + (size_t)(m0 + i) * xstride + k8 * 16) = bf16x8_to_f16x8(v[i]);
+    };
+    u32x4 xv[XB];
+    x_batch_load(0, tid, xv);
 
     // ---- this lane's codes and row scale (the HBM stream)
     const int crow = row < a.N ? row : (int)a.N - 1;           // rows past N re-read row N-1, never stored
@@ -181,11 +197,15 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
         scl[s] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rsc, crow * 2, 0, 0));
     }
 
-    // ---- staging -> LDS
-    cb_store(tid, c0);
-    cb_store(tid + WG, c1);
-    x_store(0, tid, x0);
-    if (count > 1) x_store(1, tid, x1);
+    // ---- x -> LDS (the first batch waits for its own loads only), then
+    //      every DMA write in LDS, then the workgroup
+    x_batch_store(0, tid, xv);
+    for (int k0 = 0; k0 < CPR; k0 += WG)
+        for (int m0 = k0 ? 0 : XB; m0 < count; m0 += XB) {
+            x_batch_load(m0, k0 + tid, xv);
+            x_batch_store(m0, k0 + tid, xv);
+        }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
 
     // ---- MFMA over the lane's codes
@@ -242,7 +262,7 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
 }
 
 size_t vq_mfma_lds(int64_t K, int kc, bool two_cb, int tile_rows, int nset, int ks) {
-    return (size_t)kc * 16 * (two_cb ? 2 : 1) + (size_t)tile_rows * (K * 2 + 16) +
+    return (size_t)((kc + 63) / 64) * 1024 * (two_cb ? 2 : 1) + (size_t)tile_rows * (K * 2 + 16) +
            (ks > 1 ? (size_t)4 * nset * 64 * 16 : 0);
 }
 

@@ -65,6 +65,16 @@ __device__ __forceinline__ float vp_dot(const uint16_t* cbe, const uint16_t* xe,
     }
 }
 
+// 1 KB LDS blocks holding a codebook of kc entries of DIM fp16
+__host__ __device__ inline int vp_cb_blocks(int kc, int dim) { return (kc * dim * 2 + 1023) / 1024; }
+
+// One direct-to-LDS load: lane i's 16 bytes at `voff` land at lds + 16 i
+// (a device function: the builtin inside a kernel template's lambda stops
+// hipcc emitting the host launch stubs).
+__device__ __forceinline__ void vp_dma16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
 // field j (0..31) of a block of PB words
 template <int PB>
 __device__ __forceinline__ uint32_t vp_field(const uint32_t* w, int j) {
@@ -103,27 +113,55 @@ __global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
     // padding per block, so the lanes of a row (one block each) read
     // different banks (a block is a multiple of 256 bytes otherwise)
     constexpr int XBS = 33 * DIM;
+    const int cbytes = a.kc * DIM * 2;               // bytes of one codebook
+    const int cbb = vp_cb_blocks(a.kc, DIM);         // its 1 KB LDS blocks
     uint16_t* cbl0 = (uint16_t*)smem;
-    uint16_t* cbl1 = two_cb ? cbl0 + (size_t)a.kc * DIM : cbl0;
-    uint16_t* xl = cbl0 + (size_t)a.kc * DIM * (two_cb ? 2 : 1);
+    uint16_t* cbl1 = two_cb ? (uint16_t*)(smem + (size_t)cbb * 1024) : cbl0;
+    uint16_t* xl = (uint16_t*)(smem + (size_t)cbb * 1024 * (two_cb ? 2 : 1));
 
-    // codebook(s) and the x row (fp16) -> LDS
-    for (int s = 0; s < (two_cb ? 2 : 1); s++) {
-        uint16_t* dst = s ? cbl1 : cbl0;
-        const __amdgpu_buffer_rsrc_t rcb = make_rsrc(a.cb[s], (int64_t)a.kc * DIM * 2);
-        for (int i = tid; i < a.kc * DIM / 2; i += 256)
-            *(uint32_t*)(dst + 2 * i) = __builtin_amdgcn_raw_buffer_load_b32(rcb, i * 4, 0, 0);
+    // codebook(s) and the x row (fp16) -> LDS, every load issued before any
+    // wait: codebooks of whole 16-byte pieces by direct-to-LDS loads (1 KB per
+    // wave instruction, nothing through registers), others by dword copies;
+    // x in batches of 8 dwords per thread
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int ncb = two_cb ? 2 : 1;
+    if (cbytes % 16 == 0) {
+        for (int j = wave; j < cbb * ncb; j += 4) {
+            const int s = j >= cbb, p = (j - s * cbb) * 64 + lane;
+            vp_dma16(make_rsrc(a.cb[s], cbytes), smem + (size_t)j * 1024,
+                     p * 16 < cbytes ? (uint32_t)p * 16u : 0x80000000u);
+        }
+    } else {
+        for (int s = 0; s < ncb; s++) {
+            uint16_t* dst = s ? cbl1 : cbl0;
+            const __amdgpu_buffer_rsrc_t rcb = make_rsrc(a.cb[s], cbytes);
+            for (int i = tid; i < cbytes / 4; i += 256)
+                *(uint32_t*)(dst + 2 * i) = __builtin_amdgcn_raw_buffer_load_b32(rcb, i * 4, 0, 0);
+        }
     }
     {
         const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (ok_x ? xrow : 0) * a.K, ok_x ? a.K * 2 : 0);
-        for (int i = tid; i < (int)(Kp / 2); i += 256) {
-            const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(rx, i * 4, 0, 0);
-            const vp_f16x2 h = {(_Float16)bf16_to_f32((uint16_t)(v & 0xffffu)),
-                                (_Float16)bf16_to_f32((uint16_t)(v >> 16))};
-            const int e = 2 * i, blk = e / (32 * DIM);
-            *(uint32_t*)(xl + blk * XBS + (e - blk * 32 * DIM)) = __builtin_bit_cast(uint32_t, h);
+        const int nd = (int)(Kp / 2);
+        for (int i0 = tid; i0 < nd; i0 += 256 * 8) {
+            uint32_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + 256 * u;
+                v[u] = __builtin_amdgcn_raw_buffer_load_b32(rx, i < nd ? i * 4 : (int)0x80000000u, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + 256 * u;
+                if (i < nd) {
+                    const vp_f16x2 h = {(_Float16)bf16_to_f32((uint16_t)(v[u] & 0xffffu)),
+                                        (_Float16)bf16_to_f32((uint16_t)(v[u] >> 16))};
+                    const int e = 2 * i, blk = e / (32 * DIM);
+                    *(uint32_t*)(xl + blk * XBS + (e - blk * 32 * DIM)) = __builtin_bit_cast(uint32_t, h);
+                }
+            }
         }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the direct-to-LDS writes have landed
     __syncthreads();
 
     const int64_t row = (int64_t)blockIdx.x * RPWG + tid / SEG;
@@ -250,7 +288,7 @@ static int vp_check(int dtype, int pack_bits, int kc, int dim, int group, int64_
                   group);
     const int64_t W = (K / dim + 31) / 32 * pack_bits;
     KMI_CHECK_ARG(E * N * W * 4 < (1LL << 31) &&
-                      (size_t)kc * dim * 2 * 2 + (size_t)(W / pack_bits) * 33 * dim * 2 <= 160 * 1024,
+                      (size_t)vp_cb_blocks(kc, dim) * 1024 * 2 + (size_t)(W / pack_bits) * 33 * dim * 2 <= 160 * 1024,
                   "vq (packed): codes past 2 GiB or codebook + x past the LDS");
     return OK;
 }
@@ -261,7 +299,7 @@ static int run_vp(VpArgs& a, int pack_bits, int dim, hipStream_t st) {
     const int gpb = fpg >= 32 ? 1 : 32 / fpg;
     const int seg = vp_seg(nblk);
     const bool two_cb = a.nset == 2 && a.cb[1] != a.cb[0];
-    const size_t lds = (size_t)a.kc * dim * 2 * (two_cb ? 2 : 1) + (size_t)nblk * 33 * dim * 2;
+    const size_t lds = (size_t)vp_cb_blocks(a.kc, dim) * 1024 * (two_cb ? 2 : 1) + (size_t)nblk * 33 * dim * 2;
     int rc;
     switch (pack_bits) {
         case 8: rc = launch_vp_pb<8>(a, dim, gpb, seg, lds, st); break;

@@ -145,3 +145,19 @@ def test_vq_switch_glu_mfma_path_bad_experts(dev, T, kc):
     ok = (inds >= 0) & (inds < E)
     ref = O.switch_glu(x, np.where(ok, inds, 0), fn(hg), fn(hu), fn(hd))
     assert_close(got[ok], ref[ok], what="vq switch_glu (MFMA path)")
+
+
+@pytest.mark.parametrize("T,E,H,I,k,kc", [(64, 4, 4096, 256, 2, 256), (48, 3, 1024, 512, 2, 4096)])
+def test_vq_switch_glu_full_tiles_and_long_rows(dev, T, E, H, I, k, kc):
+    """Many rows per expert (16-row tiles: x staged in two batches of rows),
+    a 4096-long row (two passes over its pieces), and a codebook staged in
+    64 blocks per projection."""
+    rng = np.random.default_rng(T + E + H + kc)
+    (hg, gg), (hu, gu), (hd, gd) = [_vq(rng, E, n, kd, kc, 0, dev) for n, kd in ((I, H), (I, H), (H, I))]
+    glu = nn.VQSwitchGLU(*(nn.VQSwitchLinear(*g) for g in (gg, gu, gd)))
+    x = bf16_normal(rng, (T, H))
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    fn = lambda h: (lambda xs, e: O.vq_matmul(xs, h[0][e], h[1], h[2][e], 0, "bfloat16"))
+    ref = O.switch_glu(x, inds, fn(hg), fn(hu), fn(hd))
+    got = glu(to_torch(x, dev, BF), torch.from_numpy(inds).to(dev))
+    assert_close(to_numpy(got), ref, what=f"vq switch_glu T={T} H={H} kc={kc}")
