@@ -169,24 +169,32 @@ __global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
     const int64_t nblk = (nsub + 31) / 32;
     const int64_t gpr = a.K / a.group;                // scale groups per row
     const int64_t fpg = a.group / DIM;                // fields per group
-    const int64_t erow = (int64_t)(ok_e ? e : 0) * a.N + (row < a.N ? row : 0);
+    // the expert's views are workgroup-uniform (a per-lane descriptor would
+    // put every load in a loop over the wave's distinct rows); the row is in
+    // the lane's offset, and a row past N reads 0
+    const int64_t ebase = (int64_t)(ok_e ? e : 0) * a.N;
+    const bool row_ok = ok_e && row < a.N;
+    const uint32_t rowc = (uint32_t)(row < a.N ? row : 0);
     float res[2] = {0.f, 0.f};
     for (int s = 0; s < a.nset; s++) {
         const uint16_t* cbl = s ? cbl1 : cbl0;
-        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.codes[s] + erow * a.W, (ok_e && row < a.N) ? a.W * 4 : 0);
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sc[s] + erow * gpr, (ok_e && row < a.N) ? gpr * 2 : 0);
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.codes[s] + ebase * a.W, ok_e ? a.N * a.W * 4 : 0);
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sc[s] + ebase * gpr, ok_e ? a.N * gpr * 2 : 0);
+        const uint32_t cro = rowc * (uint32_t)a.W * 4u, sro = rowc * (uint32_t)gpr * 2u;
         float tot = 0.f;
-        for (int64_t b = seg; b < nblk; b += SEG) {
+        for (int b = seg; b < (int)nblk; b += SEG) {
             uint32_t w[PB + 1];
 #pragma unroll
             for (int q = 0; q < PB; q++)
-                w[q] = __builtin_amdgcn_raw_buffer_load_b32(rc, (int)((b * PB + q) * 4), 0, AUX_NT);
+                w[q] = __builtin_amdgcn_raw_buffer_load_b32(
+                    rc, row_ok ? (int)(cro + (uint32_t)(b * PB + q) * 4u) : (int)0x80000000u, 0, AUX_NT);
             w[PB] = 0;
             float sv[GPB];
 #pragma unroll
             for (int g = 0; g < GPB; g++) {
-                const int64_t gi = (b * 32 + g * FPG) / fpg;
-                sv[g] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rs, (int)(gi * 2), 0, 0));
+                const int gi = (int)((b * 32 + g * FPG) / fpg);
+                sv[g] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(
+                    rs, row_ok ? (int)(sro + (uint32_t)gi * 2u) : (int)0x80000000u, 0, 0));
             }
             const int64_t f0 = b * 32;
             const int nvalid = (int)(nsub - f0 < 32 ? nsub - f0 : 32);
