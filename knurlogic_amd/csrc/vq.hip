@@ -504,6 +504,20 @@ int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, con
         if (rc) return rc;
         KMI_CHECK_LAUNCH("vq_gemv(glu)");
     }
+    // a few tokens: the down projection token-major, with the combine in its
+    // epilogue (the same kernel writes y without scores, so both agree bit
+    // for bit)
+    if (m_down && P <= 16 && vq_down_tok_supported(I, code_bytes, kc, k)) {
+        VqdArgs d = {};
+        d.x = act; d.inds = inds; d.codes = codes_down; d.sc = (const uint16_t*)scales_down;
+        d.cb = (const uint16_t*)codebook_down; d.scores = (const uint16_t*)scores;
+        d.out = scores ? (uint16_t*)out : y;
+        d.E = E; d.N = H; d.K = I; d.T = T; d.k = k; d.kc = kc;
+        rc = launch_vq_down_tok(d, code_bytes, st);
+        if (rc) return rc;
+        KMI_CHECK_LAUNCH("vq_down_tok");
+        return OK;
+    }
     if (m_down) {
         VqmArgs d = {};
         d.x = act; d.X = P; d.lhs_magic = 0;

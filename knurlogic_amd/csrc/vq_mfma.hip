@@ -57,12 +57,6 @@ __device__ __forceinline__ u32x4 bf16x8_to_f16x8(u32x4 v) {
 
 constexpr uint32_t NONE = 0x80000000u;      // an offset past every buffer: reads 0
 
-// One direct-to-LDS load: lane i's 16 bytes at `voff` land at lds + 16 i
-// (a device function: the builtin inside a kernel template's lambda stops
-// hipcc emitting the host launch stubs).
-__device__ __forceinline__ void vq_dma16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t voff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
-}
 constexpr int WG = 256;                     // 4 waves
 constexpr int TM = VQM_TILE_ROWS;           // tile rows (MFMA M)
 
@@ -128,19 +122,28 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     };
 
     // ---- staging, every load issued before any wait:
-    //  1. the codebook(s) by direct-to-LDS loads (1 KB per wave instruction,
-    //     nothing through registers; entries past kc read 0 and are never
-    //     gathered: codes are clamped to kc - 1);
+    //  1. the codebook(s): each wave loads 8 KB blocks of 1 KB at once, then
+    //     stores them (entries past kc read 0 and are never gathered: codes
+    //     are clamped to kc - 1);
     //  2. the first x pieces of the tile (8 bf16 -> 8 fp16 per piece, at most
     //     XB per thread in flight);
     //  3. this lane's codes and row scales (the HBM stream);
     //  then the x pieces are converted into LDS and the rest of x staged.
     const __amdgpu_buffer_rsrc_t rcb0 = make_rsrc(a.cb0, (int64_t)a.kc * 16);
     const __amdgpu_buffer_rsrc_t rcb1 = make_rsrc(a.cb1, (int64_t)a.kc * 16);
-    for (int j = wave; j < nblk; j += 4) {
-        const bool second = j >= cbb;
-        const int p = (j - (second ? cbb : 0)) * 64 + lane;
-        vq_dma16(second ? rcb1 : rcb0, smem + (size_t)j * 1024, p < a.kc ? (uint32_t)p * 16u : NONE);
+    for (int j0 = wave; j0 < nblk; j0 += 32) {
+        u32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + 4 * u;
+            const bool second = j >= cbb;
+            const int p = (j - (second ? cbb : 0)) * 64 + lane;
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(second ? rcb1 : rcb0,
+                                                         j < nblk && p < a.kc ? p * 16 : (int)NONE, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (j0 + 4 * u < nblk) *(u32x4*)(smem + (size_t)(j0 + 4 * u) * 1024 + lane * 16) = v[u];
     }
     // x pieces: a batch is rows m0 .. m0 + XB - 1 at piece k8 of each (row ids
     // by scalar loads: m is uniform); rows past the tile read 0, unstored
@@ -198,14 +201,13 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     }
 
     // ---- x -> LDS (the first batch waits for its own loads only), then
-    //      every DMA write in LDS, then the workgroup
+    //      the workgroup
     x_batch_store(0, tid, xv);
     for (int k0 = 0; k0 < CPR; k0 += WG)
         for (int m0 = k0 ? 0 : XB; m0 < count; m0 += XB) {
             x_batch_load(m0, k0 + tid, xv);
             x_batch_store(m0, k0 + tid, xv);
         }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
 
     // ---- MFMA over the lane's codes
@@ -339,6 +341,183 @@ int launch_vq_mfma(const VqmArgs& a, int code_bytes, int nset, int64_t ntiles, h
 #undef KMI_VQM_LAUNCH
 #undef KMI_VQM_ONE
     set_error("vq_mfma: no kernel for K=%lld, %d-byte codes", (long long)a.K, code_bytes);
+    return EINVAL_ARG;
+}
+
+// =============================================================================
+// vq_down_tok: the down projection of a few tokens, token-major.  A
+// workgroup owns 16 output rows of one token; wave w takes the token's
+// slots w, w + 4, ..  Per slot, lane (n, q) holds its row's q-th quarter of
+// the codes and runs one MFMA per code with the slot's act row in every A
+// row (so D is the same in every row), gathering the codebook vector from
+// LDS as the B operand.  y = round(scale * acc); with scores the slots'
+// round(y * score) are summed in slot order in float64 and rounded once, as
+// moe_combine does, so the result is the combine of the y this kernel
+// writes without scores, bit for bit.  An out-of-range expert gives y = 0.
+template <int CB, int LW>
+__global__ __launch_bounds__(WG) void vq_down_tok(VqdArgs a) {
+    constexpr int CPL = LW * 4 / CB;                 // codes per lane
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15, q = lane >> 4;
+    const int t = (int)blockIdx.y;
+    const int64_t row0 = (int64_t)blockIdx.x * 16;
+    const int64_t row = row0 + n;
+    const int K = (int)a.K, CPR = K / 8, k = a.k;
+    const int xstride = K * 2 + 16;
+    const int cbb = (a.kc + 63) / 64;
+    unsigned char* xs = smem + (size_t)cbb * 1024;                      // [k][K] fp16
+    float* prod = (float*)(xs + (size_t)k * xstride);                   // [k][16]
+
+    // codebook and the token's k act rows (fp16) by batches of loads
+    const __amdgpu_buffer_rsrc_t rcb = make_rsrc(a.cb, (int64_t)a.kc * 16);
+    for (int j0 = wave; j0 < cbb; j0 += 16) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int j = j0 + 4 * u, p = j * 64 + lane;
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rcb, j < cbb && p < a.kc ? p * 16 : (int)NONE, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (j0 + 4 * u < cbb) *(u32x4*)(smem + (size_t)(j0 + 4 * u) * 1024 + lane * 16) = v[u];
+    }
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (int64_t)t * k * K, (int64_t)k * K * 2);
+    const int xitems = k * CPR;
+    for (int f0 = tid; f0 < xitems; f0 += WG * 4) {
+        u32x4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int f = f0 + WG * i;
+            v[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, f < xitems ? f * 16 : (int)NONE, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int f = f0 + WG * i;
+            if (f < xitems) *(u32x4*)(xs + (size_t)(f / CPR) * xstride + (f % CPR) * 16) = bf16x8_to_f16x8(v[i]);
+        }
+    }
+
+    // this wave's slots, two at a time: codes and scales of both issued together
+    const int crow = (int)(row < a.N ? row : a.N - 1);
+    const int cfirst = q * CPL;
+    auto load_slot = [&](int s, uint32_t (&cw)[LW], float& scl, bool& ok) {
+        const int e = s < k ? a.inds[(int64_t)t * k + s] : -1;
+        ok = e >= 0 && e < a.E;
+        const char* base = (const char*)a.codes + (int64_t)(ok ? e : 0) * a.N * CPR * CB;
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(base, ok ? a.N * CPR * CB : 0);
+        const uint32_t lo = (uint32_t)((crow * CPR + cfirst) * CB);
+        if constexpr (LW % 4 == 0) {
+#pragma unroll
+            for (int i = 0; i < LW; i += 4) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rc, (int)(lo + i * 4), 0, AUX_NT);
+                cw[i] = v.x; cw[i + 1] = v.y; cw[i + 2] = v.z; cw[i + 3] = v.w;
+            }
+        } else if constexpr (LW % 2 == 0) {
+#pragma unroll
+            for (int i = 0; i < LW; i += 2) {
+                const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(lo + i * 4), 0, AUX_NT);
+                cw[i] = v.x; cw[i + 1] = v.y;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < LW; i++) cw[i] = __builtin_amdgcn_raw_buffer_load_b32(rc, (int)(lo + i * 4), 0, AUX_NT);
+        }
+        const __amdgpu_buffer_rsrc_t rsc = make_rsrc(a.sc + (int64_t)(ok ? e : 0) * a.N, ok ? a.N * 2 : 0);
+        scl = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rsc, crow * 2, 0, 0));
+    };
+    const int nslot = (k - wave + 3) / 4;            // slots wave, wave + 4, ..
+    uint32_t cw[2][LW];
+    float scl[2];
+    bool okk[2];
+    load_slot(wave, cw[0], scl[0], okk[0]);
+    load_slot(wave + 4, cw[1], scl[1], okk[1]);
+
+    lds_barrier();
+
+    for (int j0 = 0; j0 < nslot; j0 += 2) {
+        if (j0 > 0) {
+            load_slot(wave + 4 * j0, cw[0], scl[0], okk[0]);
+            load_slot(wave + 4 * (j0 + 1), cw[1], scl[1], okk[1]);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int s = wave + 4 * (j0 + u);
+            if (j0 + u >= nslot) continue;
+            const unsigned char* xa = xs + (size_t)s * xstride + (size_t)cfirst * 16;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < CPL; kb++) {
+                const u32x4 av = *(const u32x4*)(xa + kb * 16);
+                uint32_t code;
+                if constexpr (CB == 1) code = (cw[u][kb >> 2] >> (8 * (kb & 3))) & 0xffu;
+                else code = (cw[u][kb >> 1] >> (16 * (kb & 1))) & 0xffffu;
+                code = code < (uint32_t)a.kc ? code : (uint32_t)(a.kc - 1);
+                const u32x4 bv = *(const u32x4*)(smem + code * 16);
+                acc = mfma_f16(av, bv, acc);
+            }
+            // D[m][n] is the same for every m: lanes q = 0 hold it in item 0
+            const float y = okk[u] ? vqm_bf16r(scl[u] * acc[0]) : 0.f;
+            if (q == 0) {
+                if (a.scores) {
+                    const float sc = bf16_to_f32(a.scores[(int64_t)t * k + s]);
+                    prod[s * 16 + n] = vqm_bf16r(y * sc);
+                } else if (row < a.N) {
+                    a.out[((int64_t)t * k + s) * a.N + row] = f32_to_bf16(y);
+                }
+            }
+        }
+    }
+    if (!a.scores) return;
+    lds_barrier();
+    if (tid < 16 && row0 + tid < a.N) {
+        double acc = 0.0;
+        for (int s = 0; s < k; s++) acc += (double)prod[s * 16 + tid];
+        a.out[(int64_t)t * a.N + row0 + tid] = f32_to_bf16(vqm_f32_kept(acc));
+    }
+}
+
+#define KMI_VQD_SHAPES(X)                                                        \
+    X(1, 1) X(1, 2) X(1, 3) X(1, 4) X(1, 6) X(1, 8) X(1, 12) X(1, 16)            \
+    X(2, 2) X(2, 4) X(2, 6) X(2, 8) X(2, 12) X(2, 16) X(2, 24) X(2, 32)
+
+static int vqd_lw(int64_t K, int code_bytes) {
+    const int64_t b = K * code_bytes;                // bytes of codes per row, 4 lanes
+    return b % 128 ? 0 : (int)(b / 128);
+}
+
+bool vq_down_tok_supported(int64_t K, int code_bytes, int kc, int k) {
+    const int lw = vqd_lw(K, code_bytes);
+    bool has = false;
+#define KMI_VQD_HAS(CB_, LW_) has = has || (code_bytes == CB_ && lw == LW_);
+    KMI_VQD_SHAPES(KMI_VQD_HAS)
+#undef KMI_VQD_HAS
+    return has && k >= 1 && k <= 64 && vq_down_tok_lds(K, kc, k) <= 160 * 1024;
+}
+
+size_t vq_down_tok_lds(int64_t K, int kc, int k) {
+    return (size_t)((kc + 63) / 64) * 1024 + (size_t)k * (K * 2 + 16) + (size_t)k * 16 * 4;
+}
+
+int launch_vq_down_tok(const VqdArgs& a, int code_bytes, hipStream_t st) {
+    const int lw = vqd_lw(a.K, code_bytes);
+    const size_t lds = vq_down_tok_lds(a.K, a.kc, a.k);
+    const dim3 grid((unsigned)ceil_div(a.N, 16), (unsigned)a.T);
+#define KMI_VQD_ONE(CB_, LW_)                                                                     \
+    if (code_bytes == CB_ && lw == LW_) {                                                         \
+        static bool attr = false;                                                                 \
+        if (!attr) {                                                                              \
+            (void)hipFuncSetAttribute((const void*)vq_down_tok<CB_, LW_>,                          \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);    \
+            attr = true;                                                                          \
+        }                                                                                         \
+        vq_down_tok<CB_, LW_><<<grid, WG, lds, st>>>(a);                                          \
+        return OK;                                                                                \
+    }
+    KMI_VQD_SHAPES(KMI_VQD_ONE)
+#undef KMI_VQD_ONE
+    set_error("vq_down_tok: no kernel for K=%lld, %d-byte codes", (long long)a.K, code_bytes);
     return EINVAL_ARG;
 }
 

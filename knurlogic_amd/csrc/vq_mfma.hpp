@@ -34,4 +34,25 @@ bool vq_mfma_supported(int64_t K, int code_bytes, int kc, bool two_cb);
 // ntiles: grid rows (tiles of the sort, or the row ids in pair mode)
 int launch_vq_mfma(const VqmArgs& a, int code_bytes, int nset, int64_t ntiles, hipStream_t st);
 
+// Down projection of a few tokens, token-major: every (token, slot) pair's
+// expert row block in one workgroup per (16 rows, token), and with scores
+// the weighted combine of the token's k slots in the epilogue.
+struct VqdArgs {
+    const uint16_t* x;          // act [T*k, K] bf16 (pair-major)
+    const int32_t* inds;        // [T*k] expert per pair
+    const void* codes;          // [E, N, K/8] (u8 or u16)
+    const uint16_t* sc;         // [E, N] fp16
+    const uint16_t* cb;         // [kc, 8] fp16
+    const uint16_t* scores;     // [T*k] bf16, or null: y [T*k, N] is written
+    uint16_t* out;              // [T, N] with scores, else [T*k, N]
+    int64_t E, N, K, T;
+    int k, kc;
+};
+
+// the shapes vq_down_tok covers (K a multiple of 128, K / 8 codes per row
+// split over 4 lanes in whole 32-bit words)
+bool vq_down_tok_supported(int64_t K, int code_bytes, int kc, int k);
+size_t vq_down_tok_lds(int64_t K, int kc, int k);
+int launch_vq_down_tok(const VqdArgs& a, int code_bytes, hipStream_t st);
+
 }  // namespace kmi
