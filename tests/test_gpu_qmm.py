@@ -104,6 +104,19 @@ def test_rows_are_independent_bit_for_bit(dev):
     assert torch.equal(y96, y128[:96])
 
 
+@pytest.mark.parametrize("M,shape", [(16, (14336, 4096)), (16, (4096, 14336)), (5, (14336, 4096))])
+def test_qmm_repeats_bit_for_bit(dev, M, shape):
+    """The same call four times gives the same bits (the skinny kernels'
+    LDS pipelines and the split-K reduction are deterministic)."""
+    g = torch.Generator(device=dev).manual_seed(M)
+    w = (torch.randn(*shape, device=dev, generator=g) * 0.02).to(BF)
+    wq, s, b = K.quantize(w, 64, 4)
+    x = torch.randn(M, shape[1], device=dev, generator=g).to(BF)
+    ys = [K.quantized_matmul(x, wq, s, b) for _ in range(4)]
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+
+
 def test_linearity_at_full_size(dev):
     """qmm(2x) == 2 qmm(x) bit for bit (power-of-two scaling is exact), and
     qmm(x1 + x2) ~ qmm(x1) + qmm(x2), at the [14336, 4096] 4-bit shape."""

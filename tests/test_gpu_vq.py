@@ -161,3 +161,18 @@ def test_vq_switch_glu_full_tiles_and_long_rows(dev, T, E, H, I, k, kc):
     ref = O.switch_glu(x, inds, fn(hg), fn(hu), fn(hd))
     got = glu(to_torch(x, dev, BF), torch.from_numpy(inds).to(dev))
     assert_close(to_numpy(got), ref, what=f"vq switch_glu T={T} H={H} kc={kc}")
+
+
+@pytest.mark.parametrize("T,kc", [(16, 4096), (1, 4096), (16, 256)])
+def test_vq_switch_glu_repeats_bit_for_bit(dev, T, kc):
+    """The same call twice gives the same bits: the sort's row order inside
+    an expert tile varies between calls, and no result may depend on it."""
+    rng = np.random.default_rng(5 * T + kc)
+    E, H, I, k = 128, 2048, 768, 8
+    (hg, gg), (hu, gu), (hd, gd) = [_vq(rng, E, n, kd, kc, 0, dev) for n, kd in ((I, H), (I, H), (H, I))]
+    glu = nn.VQSwitchGLU(*(nn.VQSwitchLinear(*g) for g in (gg, gu, gd)))
+    x = to_torch(bf16_normal(rng, (T, H)), dev, BF)
+    inds = torch.from_numpy(np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)).to(dev)
+    ys = [glu(x, inds) for _ in range(4)]
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
