@@ -377,9 +377,11 @@ def bench_vq_packed(T, calls, dev, dim=4, kc=2048, group=64):
 def bench_mx_moe(T, calls, dev, mode="mxfp4"):
     """MoE experts stored mxfp4 (E2M1 codes, E8M0 scales per 32 inputs, the
     routed-expert format of DeepSeek-V4 checkpoints) at the Qwen3.5-MoE
-    shape: router, gate and up (gather_qmm each), SwiGLU, down, weighted
-    combine.  Expert sets rotated past 1 GB.  Bytes: every routed expert's
-    codes and scales once, x and out."""
+    shape through SwitchGLU: router, then gate/up + SwiGLU and down + the
+    weighted combine (token-major kernels up to 16 pairs, else gather_qmm
+    for the stacked gate|up, SwiGLU, down and the combine).  Expert sets
+    rotated past 1 GB.  Bytes: every routed expert's codes and scales once,
+    x and out."""
     import torch
     import knurlogic_amd as KA
     from knurlogic_amd import nn
@@ -399,25 +401,21 @@ def bench_mx_moe(T, calls, dev, mode="mxfp4"):
         sc = torch.randint(118, 124, (E, N, K // 32), device=dev, generator=g, dtype=torch.int32).to(torch.uint8)
         return nn.QuantizedSwitchLinear(w, sc, None, None, 32, bits, mode)
 
-    sets = [(mat(I, H), mat(I, H), mat(H, I)) for _ in range(n)]
+    glus = [nn.SwitchGLU(mat(I, H), mat(I, H), mat(H, I)) for _ in range(n)]
     x = torch.randn(T, H, device=dev, generator=g).to(torch.bfloat16)
     logits = torch.randn(T, E, device=dev, generator=g).to(torch.bfloat16)
     inds, _ = KA.moe_route(logits, k)
     distinct = int(torch.unique(inds).numel())
-    xe = x[:, None, None, :]
 
     def run():
         for i in range(calls):
-            gp, up, dn = sets[i % n]
             ii, sc = KA.moe_route(logits, k)
-            act = KA.swiglu(gp(xe, ii), up(xe, ii))                     # [T, k, 1, I]
-            y = dn(act, ii)                                              # [T, k, 1, H]
-            KA.moe_combine(y.reshape(T, k, H), sc)
+            glus[i % n].combine(x, ii, sc)
 
     us = time_graph(run) / calls * 1e3
     nbytes = distinct * per_e + 2 * 2 * T * H
     gbs = nbytes / (us * 1e-6) / 1e9
-    del sets
+    del glus
     torch.cuda.empty_cache()
     return {"op": f"{mode}_moe_experts", "T": T, "experts_routed": distinct, "cache": "cold",
             "us": round(us, 3), "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),

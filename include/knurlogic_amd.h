@@ -344,7 +344,7 @@ int kmi_moe_shared_add(const void* y, const void* gate, const void* shared_y, in
  *   out: [T, H] = round(sum_s round(y[t, s] * scores[t, s])) when scores is
  *     given, else y [T, k, H] (SwitchGLU's own output).
  * Every intermediate rounds where the reference rounds: gate and up outputs,
- * silu, the activation, the down output, each weighted product.  Up to 256
+ * silu, the activation, the down output, each weighted product.  Up to 16
  * (token, slot) pairs run token-major (two kernels, no sort); more group
  * rows by expert.  workspace: kmi_switch_glu_workspace_bytes.
  */
@@ -356,6 +356,23 @@ int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const 
 
 size_t kmi_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k, int64_t E,
                                       int group_size, int bits);
+
+/*
+ * kmi_switch_glu for experts stored in an OCP microscaled mode -- the
+ * loader's mxfp4 / mxfp8 expert layers (src/knurlogic/engine/model/
+ * load_model.py:153-173, packed.py:20) behind the same SwitchGLU
+ * (switch_layers.py:172-193): mode 1 mxfp4 (E2M1 codes, 8 per uint32),
+ * mode 2 mxfp8 (E4M3, 4 per uint32), one uint8 E8M0 scale per 32 inputs,
+ * no biases.  w_gu [E, 2I, H*bits/32] and s_gu [E, 2I, H/32] stack gate
+ * (rows 0..I-1) and up; w_down [E, H, I*bits/32], s_down [E, H, I/32].
+ * Token-major sizes only (T * k <= 16; the Python mirror takes the
+ * gather_qmm path beyond).  Otherwise as kmi_switch_glu (workspace:
+ * kmi_switch_glu_workspace_bytes with group 32).
+ */
+int kmi_switch_glu_mx(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                      const void* scores, const uint32_t* w_gu, const uint8_t* s_gu, const uint32_t* w_down,
+                      const uint8_t* s_down, int64_t E, int dtype, int mode, void* out, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 /*
  * SparseMoeBlock's routed experts from the router logits, in one call

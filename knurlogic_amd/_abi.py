@@ -47,6 +47,7 @@ SIGNATURES = {
     "kmi_moe_shared_add": (I, [P, P, P, I, I64, I64, P, P]),
     "kmi_switch_glu": (I, [P, I64, I64, I64, I, P, P, P, P, P, P, P, P, I64, I, I, I, P, P, SZ, P]),
     "kmi_switch_glu_workspace_bytes": (SZ, [I64, I64, I64, I, I64, I, I]),
+    "kmi_switch_glu_mx": (I, [P, I64, I64, I64, I, P, P, P, P, P, P, I64, I, I, P, P, SZ, P]),
     "kmi_moe_experts": (I, [P, P, I64, I64, I64, I, I64, P, P, P, P, P, P, I, I, I, P, P, P, P, SZ, P]),
     "kmi_vq_gather_qmm": (I, [P, I64, I64, P, I, P, I, I, P, I, I64, I64, P, P, I64, I, P, P]),
     "kmi_vq_glu": (I, [P, I64, I64, I64, I, P, P, P, P, P, P, P, I, I, I, I, I64, I, P, P]),

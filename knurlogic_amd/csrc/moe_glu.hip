@@ -68,7 +68,7 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
                            const uint32_t* w_down, const void* s_down, const void* b_down,
                            int64_t E, int dtype, int group_size, int bits, void* out, void* workspace,
                            size_t workspace_bytes, void* stream, const void* route_logits,
-                           int32_t* route_inds, void* route_scores) {
+                           int32_t* route_inds, void* route_scores, int mx = 0) {
     KMI_CHECK_ARG(dtype == BF16, "switch_glu: only bfloat16 activations are implemented");
     KMI_CHECK_ARG(bits == 4 || bits == 8, "switch_glu: bits=%d (4 or 8)", bits);
     KMI_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
@@ -79,7 +79,7 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
                   "switch_glu: H=%lld, I=%lld must be multiples of 64 and of the group",
                   (long long)H, (long long)I);
     if (T == 0) return OK;
-    KMI_CHECK_ARG(x && inds && w_gu && s_gu && b_gu && w_down && s_down && b_down && out,
+    KMI_CHECK_ARG(x && inds && w_gu && s_gu && w_down && s_down && out && (mx || (b_gu && b_down)),
                   "switch_glu: null pointer");
     const int epw = 32 / bits;
     KMI_CHECK_ARG(E * 2 * I * (H / epw) * 4 < (1LL << 31) && E * H * (I / epw) * 4 < (1LL << 31),
@@ -88,6 +88,9 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
     KMI_CHECK_ARG(T * H * 2 < (1LL << 31) && T * k * (H > I ? H : I) * 2 < (1LL << 31),
                   "switch_glu: activations past 2 GiB");
     const GluPlan p = plan_glu(T, H, I, k, E);
+    KMI_CHECK_ARG(!mx || (p.tok && group_size == 32),
+                  "switch_glu (mx): %lld pairs, group %d (token-major sizes: at most %lld pairs, group 32)",
+                  (long long)(T * k), group_size, (long long)TOK_MAX_PAIRS);
     if (!workspace || workspace_bytes < p.total) {
         set_error("switch_glu: workspace of %zu bytes needed, %zu given", p.total, workspace_bytes);
         return EWORKSPACE;
@@ -104,17 +107,20 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
         g.inds_out = route_inds;
         g.scores_out = (uint16_t*)route_scores;
         g.x = (const uint16_t*)x;
+        // scales: bf16 (affine) or one byte (mx); the up rows start I rows in
+        const int64_t sbw = mx ? 1 : 2;
         g.w0 = w_gu; g.s0 = (const uint16_t*)s_gu; g.b0 = (const uint16_t*)b_gu;
-        g.w1 = w_gu + I * wpr_h; g.s1 = (const uint16_t*)s_gu + I * gpr_h; g.b1 = (const uint16_t*)b_gu + I * gpr_h;
+        g.w1 = w_gu + I * wpr_h; g.s1 = (const uint16_t*)((const char*)s_gu + I * gpr_h * sbw);
+        g.b1 = mx ? nullptr : (const uint16_t*)b_gu + I * gpr_h;
         g.inds = inds; g.out = act;
-        g.E = E; g.N = I; g.K = H; g.T = T; g.erows = 2 * I; g.k = k; g.gs_shift = gs_shift;
+        g.E = E; g.N = I; g.K = H; g.T = T; g.erows = 2 * I; g.k = k; g.gs_shift = gs_shift; g.mx = mx;
         int rc = launch_moe_glu_tok(g, bits, st);
         if (rc) return rc;
         KMI_CHECK_LAUNCH("moe_glu_tok");
         MoeTokArgs d = {};
         d.x = act; d.w0 = w_down; d.s0 = (const uint16_t*)s_down; d.b0 = (const uint16_t*)b_down;
         d.inds = inds; d.scores = (const uint16_t*)scores; d.out = (uint16_t*)out;
-        d.E = E; d.N = H; d.K = I; d.T = T; d.erows = H; d.k = k; d.gs_shift = gs_shift;
+        d.E = E; d.N = H; d.K = I; d.T = T; d.erows = H; d.k = k; d.gs_shift = gs_shift; d.mx = mx;
         rc = launch_moe_down_tok(d, bits, st);
         if (rc) return rc;
         KMI_CHECK_LAUNCH("moe_down_tok");
@@ -158,6 +164,17 @@ int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const 
     clear_error();
     return switch_glu_impl(x, T, H, I, k, inds, scores, w_gu, s_gu, b_gu, w_down, s_down, b_down, E, dtype,
                            group_size, bits, out, workspace, workspace_bytes, stream, nullptr, nullptr, nullptr);
+}
+
+int kmi_switch_glu_mx(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                      const void* scores, const uint32_t* w_gu, const uint8_t* s_gu, const uint32_t* w_down,
+                      const uint8_t* s_down, int64_t E, int dtype, int mode, void* out, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(mode == 1 || mode == 2, "switch_glu (mx): mode %d (1 mxfp4, 2 mxfp8)", mode);
+    return switch_glu_impl(x, T, H, I, k, inds, scores, w_gu, s_gu, nullptr, w_down, s_down, nullptr, E, dtype,
+                           32, mode == 1 ? 4 : 8, out, workspace, workspace_bytes, stream, nullptr, nullptr,
+                           nullptr, 1);
 }
 
 int kmi_moe_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k, int64_t E,

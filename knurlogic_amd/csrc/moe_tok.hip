@@ -46,9 +46,12 @@ __device__ __forceinline__ float f64_to_f32_kept(double v) {
 // ROUTE: the pair's expert comes from routing its token's logits in the
 // workgroup (route.hpp, the router kernel's arithmetic), after the x loads
 // are issued; workgroup 0 of each pair writes the expert and its score.
-template <int BITS, int RPW, int S, int WV, bool ROUTE>
+// MX: OCP microscaled codes (mxfp4 at BITS 4, mxfp8 at 8) with one E8M0
+// byte scale per 32 inputs and no biases, in place of the affine decode.
+template <int BITS, int RPW, int S, int WV, bool ROUTE, bool MX>
 __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
     constexpr int NT = 64 * WV, CK = 128 / BITS, XV = CK / 8, ROWS = WV * RPW;
+    constexpr uint32_t SB = MX ? 1 : 2;              // bytes per scale
     constexpr uint32_t NONE = QV_NONE;
     extern __shared__ __align__(16) unsigned char smem[];
     const int C = (int)(a.K / CK);
@@ -84,44 +87,50 @@ __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
     const int n0 = (int)blockIdx.x * ROWS + wave * RPW;
     const bool ok_e = e >= 0 && e < a.E;
     const int64_t eoff = (int64_t)(ok_e ? e : 0) * a.erows;
-    const int64_t wbytes = ok_e ? a.N * (int64_t)wpr * 4 : 0, sbytes = ok_e ? a.N * (int64_t)gpr * 2 : 0;
+    const int64_t wbytes = ok_e ? a.N * (int64_t)wpr * 4 : 0, sbytes = ok_e ? a.N * (int64_t)gpr * SB : 0;
     const __amdgpu_buffer_rsrc_t rw0 = make_rsrc(a.w0 + eoff * wpr, wbytes);
     const __amdgpu_buffer_rsrc_t rw1 = make_rsrc(a.w1 + eoff * wpr, wbytes);
-    const __amdgpu_buffer_rsrc_t rs0 = make_rsrc(a.s0 + eoff * gpr, sbytes);
-    const __amdgpu_buffer_rsrc_t rb0 = make_rsrc(a.b0 + eoff * gpr, sbytes);
-    const __amdgpu_buffer_rsrc_t rs1 = make_rsrc(a.s1 + eoff * gpr, sbytes);
-    const __amdgpu_buffer_rsrc_t rb1 = make_rsrc(a.b1 + eoff * gpr, sbytes);
+    const __amdgpu_buffer_rsrc_t rs0 = make_rsrc((const char*)a.s0 + eoff * gpr * SB, sbytes);
+    const __amdgpu_buffer_rsrc_t rb0 = make_rsrc((const char*)a.b0 + eoff * gpr * SB, MX ? 0 : sbytes);
+    const __amdgpu_buffer_rsrc_t rs1 = make_rsrc((const char*)a.s1 + eoff * gpr * SB, sbytes);
+    const __amdgpu_buffer_rsrc_t rb1 = make_rsrc((const char*)a.b1 + eoff * gpr * SB, MX ? 0 : sbytes);
 
     // (0) x pieces beyond two per thread (long rows), before any weight load
     if (P > 2 * NT) {
         for (int q = tid + 2 * NT; q - (tid & 3) < P; q += NT)
-            stage_x16<BITS>(q, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(q), 0, 0), P, C, xs, xm);
+            stage_x16<BITS, MX>(q, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xvo(q), 0, 0), P, C, xs, xm);
     }
     // (1) scales/biases and weights of both sets
     const int full = C >> 6;
     const bool in_tail = lane < (C & 63);
     const uint32_t vw = (uint32_t)lane * 16u;
-    const uint32_t vg = (uint32_t)((lane * CK) >> a.gs_shift) * 2u;
+    const uint32_t vg = (uint32_t)((lane * CK) >> a.gs_shift) * SB;
     const uint32_t vwt = in_tail ? vw : NONE, vgt = in_tail ? vg : NONE;
     uint32_t wrow[RPW], srow[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; r++) {           // rows past N re-read row N-1 (never stored)
         const uint32_t row = (uint32_t)(n0 + r < a.N ? n0 + r : a.N - 1);
         wrow[r] = row * (uint32_t)wpr * 4u;
-        srow[r] = row * (uint32_t)gpr * 2u;
+        srow[r] = row * (uint32_t)gpr * SB;
     }
     u32x4 W0[S][RPW], W1[S][RPW];
     uint32_t S0[S][RPW], B0[S][RPW], S1[S][RPW], B1[S][RPW];
 #pragma unroll
     for (int u = 0; u < S; u++) {
         const uint32_t vo = u < full ? vg : u == full ? vgt : NONE;
-        const uint32_t so = (uint32_t)(((64 * u * CK) >> a.gs_shift) * 2);
+        const uint32_t so = (uint32_t)(((64 * u * CK) >> a.gs_shift) * SB);
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            S0[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs0, (int)vo, (int)(srow[r] + so), 0);
-            B0[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb0, (int)vo, (int)(srow[r] + so), 0);
-            S1[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs1, (int)vo, (int)(srow[r] + so), 0);
-            B1[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb1, (int)vo, (int)(srow[r] + so), 0);
+            if constexpr (MX) {
+                S0[u][r] = __builtin_amdgcn_raw_buffer_load_b8(rs0, (int)vo, (int)(srow[r] + so), 0);
+                S1[u][r] = __builtin_amdgcn_raw_buffer_load_b8(rs1, (int)vo, (int)(srow[r] + so), 0);
+                B0[u][r] = B1[u][r] = 0u;
+            } else {
+                S0[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs0, (int)vo, (int)(srow[r] + so), 0);
+                B0[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb0, (int)vo, (int)(srow[r] + so), 0);
+                S1[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs1, (int)vo, (int)(srow[r] + so), 0);
+                B1[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb1, (int)vo, (int)(srow[r] + so), 0);
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -136,8 +145,8 @@ __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
     }
 
     // (2) x -> LDS
-    stage_x16<BITS>(tid, xr0, P, C, xs, xm);
-    if (P > NT) stage_x16<BITS>(tid + NT, xr1, P, C, xs, xm);
+    stage_x16<BITS, MX>(tid, xr0, P, C, xs, xm);
+    if (P > NT) stage_x16<BITS, MX>(tid + NT, xr1, P, C, xs, xm);
     lds_barrier();
 
     const Magic16 mk = magic16();
@@ -156,12 +165,18 @@ __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
         const float4 m = xm[cc];
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            const float q0 = chunk_qx<BITS>(W0[u][r], xv, m, mk);
-            const float q1 = chunk_qx<BITS>(W1[u][r], xv, m, mk);
-            const float g0 = __builtin_fmaf(__uint_as_float(S0[u][r] << 16), q0,
-                                            __builtin_fmaf(__uint_as_float(B0[u][r] << 16), m.z, acc0[r]));
-            const float g1 = __builtin_fmaf(__uint_as_float(S1[u][r] << 16), q1,
-                                            __builtin_fmaf(__uint_as_float(B1[u][r] << 16), m.z, acc1[r]));
+            float g0, g1;
+            if constexpr (MX) {
+                g0 = __builtin_fmaf(mx_scale(S0[u][r]), chunk_mx<BITS>(W0[u][r], xv, m), acc0[r]);
+                g1 = __builtin_fmaf(mx_scale(S1[u][r]), chunk_mx<BITS>(W1[u][r], xv, m), acc1[r]);
+            } else {
+                const float q0 = chunk_qx<BITS>(W0[u][r], xv, m, mk);
+                const float q1 = chunk_qx<BITS>(W1[u][r], xv, m, mk);
+                g0 = __builtin_fmaf(__uint_as_float(S0[u][r] << 16), q0,
+                                    __builtin_fmaf(__uint_as_float(B0[u][r] << 16), m.z, acc0[r]));
+                g1 = __builtin_fmaf(__uint_as_float(S1[u][r] << 16), q1,
+                                    __builtin_fmaf(__uint_as_float(B1[u][r] << 16), m.z, acc1[r]));
+            }
             acc0[r] = cok ? g0 : acc0[r];
             acc1[r] = cok ? g1 : acc1[r];
         }
@@ -185,9 +200,10 @@ __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
 // lane busy and all k experts' loads are in flight together.  The item's
 // expert differs per lane, so the expert part of an offset is per lane and
 // the row part (wave-uniform) is in the scalar operand.
-template <int BITS, int KMAX, int U, int RPW, int WV>
+template <int BITS, int KMAX, int U, int RPW, int WV, bool MX>
 __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
     constexpr int NT = 64 * WV, CK = 128 / BITS, XV = CK / 8;
+    constexpr uint32_t SB = MX ? 1 : 2;              // bytes per scale
     constexpr int XREG = 4;                          // x pieces per thread held in registers
     constexpr uint32_t NONE = QV_NONE;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -205,8 +221,8 @@ __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
     const int64_t t = blockIdx.y;
     const int n0 = (int)blockIdx.x * (WV * RPW) + wave * RPW;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w0, a.E * a.N * (int64_t)wpr * 4);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s0, a.E * a.N * (int64_t)gpr * 2);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b0, a.E * a.N * (int64_t)gpr * 2);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s0, a.E * a.N * (int64_t)gpr * SB);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b0, MX ? 0 : a.E * a.N * (int64_t)gpr * 2);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + t * k * a.K, (int64_t)k * a.K * 2);
 
     // x pieces q = tid + NT j of the k slot rows: slot q / P, piece q % P
@@ -220,7 +236,7 @@ __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
         int sl, pc;
         xq(q, sl, pc);
         const uint32_t o = pc < P ? (uint32_t)((sl * a.K + pc * 8) * 2) : NONE;
-        stage_x16<BITS>(pc, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)o, 0, 0), P, C, xs_of(sl), xm_of(sl));
+        stage_x16<BITS, MX>(pc, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)o, 0, 0), P, C, xs_of(sl), xm_of(sl));
     }
     u32x4 xr[XREG];
 #pragma unroll
@@ -253,14 +269,14 @@ __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
         const bool ok = sidx < k && e >= 0 && e < a.E;
         isl[u] = sidx < k ? sidx : -1;
         vwo[u] = ok ? (uint32_t)((((int64_t)e * a.N) * wpr + (int64_t)c * 4) * 4) : NONE;
-        vso[u] = ok ? (uint32_t)((((int64_t)e * a.N) * gpr + ((c * CK) >> a.gs_shift)) * 2) : NONE;
+        vso[u] = ok ? (uint32_t)((((int64_t)e * a.N) * gpr + ((c * CK) >> a.gs_shift)) * SB) : NONE;
     }
     uint32_t wrow[RPW], srow[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; r++) {           // rows past N re-read row N-1 (never stored)
         const uint32_t row = (uint32_t)(n0 + r < a.N ? n0 + r : a.N - 1);
         wrow[r] = row * (uint32_t)wpr * 4u;
-        srow[r] = row * (uint32_t)gpr * 2u;
+        srow[r] = row * (uint32_t)gpr * SB;
     }
     u32x4 W[U][RPW];
     uint32_t SC[U][RPW], BI[U][RPW];
@@ -268,8 +284,13 @@ __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
     for (int u = 0; u < U; u++)
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            SC[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)vso[u], (int)srow[r], 0);
-            BI[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)vso[u], (int)srow[r], 0);
+            if constexpr (MX) {
+                SC[u][r] = __builtin_amdgcn_raw_buffer_load_b8(rs, (int)vso[u], (int)srow[r], 0);
+                BI[u][r] = 0u;
+            } else {
+                SC[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)vso[u], (int)srow[r], 0);
+                BI[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)vso[u], (int)srow[r], 0);
+            }
         }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -284,7 +305,7 @@ __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
         if (j * NT >= k * P) break;                   // wave-uniform
         int sl, pc;
         xq(tid + j * NT, sl, pc);
-        stage_x16<BITS>(pc, xr[j], P, C, xs_of(sl), xm_of(sl));
+        stage_x16<BITS, MX>(pc, xr[j], P, C, xs_of(sl), xm_of(sl));
     }
     lds_barrier();
 
@@ -302,9 +323,13 @@ __global__ __launch_bounds__(64 * WV) void moe_down_tok(MoeTokArgs a) {
         const float4 m = xm_of(sl)[c];
 #pragma unroll
         for (int r = 0; r < RPW; r++) {
-            const float q = chunk_qx<BITS>(W[u][r], xv, m, mk);
-            const float v = __builtin_fmaf(__uint_as_float(SC[u][r] << 16), q,
-                                           __uint_as_float(BI[u][r] << 16) * m.z);
+            float v;
+            if constexpr (MX) {
+                v = mx_scale(SC[u][r]) * chunk_mx<BITS>(W[u][r], xv, m);
+            } else {
+                const float q = chunk_qx<BITS>(W[u][r], xv, m, mk);
+                v = __builtin_fmaf(__uint_as_float(SC[u][r] << 16), q, __uint_as_float(BI[u][r] << 16) * m.z);
+            }
             acc[u][r] = isl[u] < 0 ? 0.f : v;
         }
     }
@@ -357,9 +382,11 @@ int launch_moe_glu_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
     if (S <= 2 && a.N * pairs / 4 >= 2048) rpw = 4;
     const dim3 grid((unsigned)ceil_div(a.N, TOK_WV * rpw), (unsigned)pairs);
     const size_t lds = (size_t)a.K * 2 + (size_t)C * 16;
-#define KMI_GLU_R(R, SS, RT)                                                                \
-    if (bits == 4) moe_glu_tok<4, R, SS, TOK_WV, RT><<<grid, 64 * TOK_WV, lds, st>>>(a);    \
-    else moe_glu_tok<8, R, SS, TOK_WV, RT><<<grid, 64 * TOK_WV, lds, st>>>(a);
+#define KMI_GLU_M(R, SS, RT, M)                                                                 \
+    if (bits == 4) moe_glu_tok<4, R, SS, TOK_WV, RT, M><<<grid, 64 * TOK_WV, lds, st>>>(a);     \
+    else moe_glu_tok<8, R, SS, TOK_WV, RT, M><<<grid, 64 * TOK_WV, lds, st>>>(a);
+#define KMI_GLU_R(R, SS, RT)                                                                    \
+    if (a.mx) { KMI_GLU_M(R, SS, RT, true) } else { KMI_GLU_M(R, SS, RT, false) }
 #define KMI_GLU(R, SS)                                                                  \
     if (rpw == R && S == SS) {                                                          \
         if (a.logits) { KMI_GLU_R(R, SS, true) } else { KMI_GLU_R(R, SS, false) }       \
@@ -368,6 +395,7 @@ int launch_moe_glu_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
     KMI_GLU(1, 1) KMI_GLU(1, 2) KMI_GLU(1, 4) KMI_GLU(2, 1) KMI_GLU(2, 2) KMI_GLU(2, 4) KMI_GLU(4, 1) KMI_GLU(4, 2)
 #undef KMI_GLU
 #undef KMI_GLU_R
+#undef KMI_GLU_M
     set_error("switch_glu: no gate/up kernel for %lld chunks per row", (long long)C);
     return EINVAL_ARG;
 }
@@ -386,15 +414,18 @@ int launch_moe_down_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
         set_error("switch_glu: down experts past 2 GiB");
         return EINVAL_ARG;
     }
-#define KMI_DOWN(KM, UU, R)                                                             \
-    if (a.k <= KM && U == UU && rpw == R) {                                             \
-        if (bits == 4) moe_down_tok<4, KM, UU, R, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a); \
-        else moe_down_tok<8, KM, UU, R, TOK_WV><<<grid, 64 * TOK_WV, lds, st>>>(a);            \
-        return OK;                                                                      \
+#define KMI_DOWN_M(KM, UU, R, M)                                                                   \
+    if (bits == 4) moe_down_tok<4, KM, UU, R, TOK_WV, M><<<grid, 64 * TOK_WV, lds, st>>>(a);       \
+    else moe_down_tok<8, KM, UU, R, TOK_WV, M><<<grid, 64 * TOK_WV, lds, st>>>(a);
+#define KMI_DOWN(KM, UU, R)                                                                        \
+    if (a.k <= KM && U == UU && rpw == R) {                                                        \
+        if (a.mx) { KMI_DOWN_M(KM, UU, R, true) } else { KMI_DOWN_M(KM, UU, R, false) }            \
+        return OK;                                                                                 \
     }
     KMI_DOWN(8, 1, 1) KMI_DOWN(8, 2, 1) KMI_DOWN(8, 3, 1) KMI_DOWN(8, 4, 1) KMI_DOWN(8, 6, 1) KMI_DOWN(8, 8, 1)
     KMI_DOWN(8, 1, 2) KMI_DOWN(8, 2, 2) KMI_DOWN(8, 3, 2) KMI_DOWN(8, 4, 2)
 #undef KMI_DOWN
+#undef KMI_DOWN_M
     set_error("switch_glu: no down kernel for k=%d, %lld chunks per row", a.k, (long long)C);
     return EINVAL_ARG;
 }

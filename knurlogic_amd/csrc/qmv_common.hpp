@@ -152,7 +152,9 @@ constexpr uint32_t QV_NONE = 0x80000000u;   // a buffer offset past every buffer
 // Piece p (x[8p .. 8p+8)) of a row -> xs [XV][C] 16-byte fp16 slots and the
 // chunk record xm [C] = {scale, correction, sum}.  Every lane of the wave runs
 // this (the quad reductions read neighbours); only pieces p < P store.
-template <int BITS>
+// NAT: every dword holds the natural pair (x_2i, x_2i+1) (the microscaled
+// decode's order; 8-bit chunks use it anyway), and the correction is 0.
+template <int BITS, bool NAT = false>
 __device__ __forceinline__ void stage_x16(int p, u32x4 raw, int P, int C, u32x4* xs, float4* xm) {
     constexpr int XV = (128 / BITS) / 8;            // pieces per chunk: 4 or 2
     float f[8];
@@ -172,7 +174,7 @@ __device__ __forceinline__ void stage_x16(int p, u32x4 raw, int P, int C, u32x4*
     const float inv = __uint_as_float((uint32_t)(268 - e) << 23);   // 2^(141-e)
     u32x4 o;
     float lo, hi = 0.f;
-    if constexpr (BITS == 4) {
+    if constexpr (BITS == 4 && !NAT) {
         // dword i pairs (x_i, x_{i+4}): the codes one and-or places there
 #pragma unroll
         for (int i = 0; i < 4; i++) o[i] = pk_f16(f[i] * inv, f[i + 4] * inv);
@@ -193,10 +195,48 @@ __device__ __forceinline__ void stage_x16(int p, u32x4 raw, int P, int C, u32x4*
         const int c = p / XV, v = p % XV;
         xs[v * C + c] = o;
         if (v == 0) {
-            const float corr = BITS == 4 ? 1024.f * __builtin_fmaf(hi, 0.0625f, lo) : 1024.f * lo;
+            const float corr = NAT ? 0.f : BITS == 4 ? 1024.f * __builtin_fmaf(hi, 0.0625f, lo) : 1024.f * lo;
             xm[c] = make_float4(mult, corr, lo + hi, 0.f);
         }
     }
+}
+
+// ---- OCP microscaled chunks (mxfp4: E2M1, mxfp8: E4M3) ---------------------
+// A 16-byte chunk is 32 E2M1 or 16 E4M3 codes in mlx's packing (element j
+// at bits BITS*j); every element converts to fp16 exactly (the conversion's
+// scale is 1.0), and the chunk's dot with its x pieces (staged NAT) is
+// v_dot2_f32_f16 on natural pairs.  The E8M0 group scale (per 32 elements)
+// is applied by the caller.
+template <int BITS>
+__device__ __forceinline__ float chunk_mx(const u32x4& W, const u32x4* xv, const float4& m) {
+    float A = 0.f, B = 0.f;
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int wd = 0; wd < 4; wd++) {
+            const uint32_t w = W[wd];
+            A = fdot2_f16(xv[wd][0], __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.f, 0)), A);
+            B = fdot2_f16(xv[wd][1], __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.f, 1)), B);
+            A = fdot2_f16(xv[wd][2], __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.f, 2)), A);
+            B = fdot2_f16(xv[wd][3], __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.f, 3)), B);
+        }
+    } else {
+#pragma unroll
+        for (int wd = 0; wd < 4; wd++) {
+            const uint32_t w = W[wd];
+            A = fdot2_f16(xv[wd >> 1][(wd & 1) * 2],
+                          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, false)), A);
+            B = fdot2_f16(xv[wd >> 1][(wd & 1) * 2 + 1],
+                          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, true)), B);
+        }
+    }
+    return m.x * (A + B);
+}
+
+// E8M0 scale byte: 2^(e - 127); 255 is NaN
+__device__ __forceinline__ float mx_scale(uint32_t e) {
+    e &= 0xffu;
+    if (e == 255u) return __uint_as_float(0x7fc00000u);
+    return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
 }
 
 // The masks and the 1024.0 pair held in VGPRs (see vconst).

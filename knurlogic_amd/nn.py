@@ -24,9 +24,9 @@ import math
 
 import torch
 
-from .ops import (add_bias, gather_qmm, linear, moe_combine, moe_experts, moe_route, moe_shared_add, quantize,
-                  quantized_matmul, swiglu, switch_glu, vq_gather_qmm, vq_glu, vq_packed_gather_qmm,
-                  vq_packed_glu, vq_switch_glu)
+from .ops import (TOK_MAX_PAIRS, add_bias, gather_qmm, linear, moe_combine, moe_experts, moe_route,
+                  moe_shared_add, quantize, quantized_matmul, swiglu, switch_glu, switch_glu_mx, vq_gather_qmm,
+                  vq_glu, vq_packed_gather_qmm, vq_packed_glu, vq_switch_glu)
 
 
 class Linear:
@@ -105,7 +105,8 @@ class QuantizedSwitchLinear:
 def _stackable(a: QuantizedSwitchLinear, b: QuantizedSwitchLinear) -> bool:
     return (a.weight.shape == b.weight.shape and a.scales.shape == b.scales.shape
             and a.group_size == b.group_size and a.bits == b.bits and a.bias is None
-            and b.bias is None and a.weight.dtype == b.weight.dtype and a.scales.dtype == b.scales.dtype)
+            and b.bias is None and a.weight.dtype == b.weight.dtype and a.scales.dtype == b.scales.dtype
+            and a.mode == b.mode and (a.biases is None) == (b.biases is None))
 
 
 class SwitchGLU:
@@ -125,19 +126,20 @@ class SwitchGLU:
         self.down_proj = down_proj
         self.fused = None
         if _stackable(gate_proj, up_proj):
-            cat = lambda a, b: torch.cat([a, b], dim=1).contiguous()
+            cat = lambda a, b: None if a is None else torch.cat([a, b], dim=1).contiguous()
+            mode = gate_proj.mode
             self.fused = QuantizedSwitchLinear(cat(gate_proj.weight, up_proj.weight),
                                                cat(gate_proj.scales, up_proj.scales),
                                                cat(gate_proj.biases, up_proj.biases),
-                                               None, gate_proj.group_size, gate_proj.bits)
+                                               None, gate_proj.group_size, gate_proj.bits, mode)
             I = gate_proj.output_dims
-            view = lambda t, lo: t[:, lo:lo + I]
+            view = lambda t, lo: None if t is None else t[:, lo:lo + I]
             self.gate_proj = QuantizedSwitchLinear(view(self.fused.weight, 0), view(self.fused.scales, 0),
                                                    view(self.fused.biases, 0), None,
-                                                   gate_proj.group_size, gate_proj.bits)
+                                                   gate_proj.group_size, gate_proj.bits, mode)
             self.up_proj = QuantizedSwitchLinear(view(self.fused.weight, I), view(self.fused.scales, I),
                                                  view(self.fused.biases, I), None,
-                                                 up_proj.group_size, up_proj.bits)
+                                                 up_proj.group_size, up_proj.bits, mode)
         else:
             self.gate_proj, self.up_proj = gate_proj, up_proj
 
@@ -148,25 +150,36 @@ class SwitchGLU:
 
     def _one_call(self, k: int) -> bool:
         f, d = self.fused, self.down_proj
-        return (f is not None and d.bias is None and k <= 8 and f.bits == d.bits
-                and f.group_size == d.group_size and f.scales.dtype == torch.bfloat16)
+        return (f is not None and d.bias is None and k <= 8 and f.bits == d.bits and f.mode == "affine"
+                and d.mode == "affine" and f.group_size == d.group_size and f.scales.dtype == torch.bfloat16)
+
+    def _one_call_mx(self, x: torch.Tensor, k: int) -> bool:
+        """mxfp4 / mxfp8 experts at token-major sizes (kmi_switch_glu_mx)."""
+        f, d = self.fused, self.down_proj
+        return (f is not None and d.bias is None and k <= 8 and f.mode in ("mxfp4", "mxfp8")
+                and d.mode == f.mode and x.dtype == torch.bfloat16
+                and x.shape[-1] % 64 == 0 and (f.weight.shape[1] // 2) % 64 == 0
+                and math.prod(x.shape[:-1]) * k <= TOK_MAX_PAIRS)
 
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """x [..., H], indices [..., k] (int) -> [..., k, H]."""
-        if self._one_call(indices.shape[-1]) and x.dtype == torch.bfloat16:
-            f, d = self.fused, self.down_proj
-            return switch_glu(x, indices, f.weight, f.scales, f.biases, d.weight, d.scales, d.biases,
-                              None, f.group_size, f.bits)
-        return self.gathered(x, indices)
+        return self._experts(x, indices, None)
 
     def combine(self, x: torch.Tensor, indices: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
         """The experts' outputs weighted by ``scores`` and summed over the k
         slots (SparseMoeBlock's combine, qwen3_5.py:181-182) -> [..., H]."""
-        if self._one_call(indices.shape[-1]) and x.dtype == torch.bfloat16:
-            f, d = self.fused, self.down_proj
+        return self._experts(x, indices, scores)
+
+    def _experts(self, x, indices, scores):
+        k = indices.shape[-1]
+        f, d = self.fused, self.down_proj
+        if self._one_call(k) and x.dtype == torch.bfloat16:
             return switch_glu(x, indices, f.weight, f.scales, f.biases, d.weight, d.scales, d.biases,
                               scores, f.group_size, f.bits)
-        return moe_combine(self.gathered(x, indices), scores)
+        if self._one_call_mx(x, k):
+            return switch_glu_mx(x, indices, f.weight, f.scales, d.weight, d.scales, scores, f.mode)
+        y = self.gathered(x, indices)
+        return y if scores is None else moe_combine(y, scores)
 
     def gathered(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """The same through separate gather_qmm calls (any layer mix)."""
@@ -180,19 +193,19 @@ class SwitchGLU:
         if self.fused is not None:
             f = self.fused
             gu = gather_qmm(x3, f.weight, f.scales, f.biases, lhs_indices=tok, rhs_indices=rhs,
-                            group_size=f.group_size, bits=f.bits)              # [P, 1, 2I]
+                            group_size=f.group_size, bits=f.bits, mode=f.mode)  # [P, 1, 2I]
             act = swiglu(gu)                                                   # [P, 1, I]
         else:
             g, u = self.gate_proj, self.up_proj
             gate = gather_qmm(x3, g.weight, g.scales, g.biases, lhs_indices=tok, rhs_indices=rhs,
-                              group_size=g.group_size, bits=g.bits)
+                              group_size=g.group_size, bits=g.bits, mode=g.mode)
             up = gather_qmm(x3, u.weight, u.scales, u.biases, lhs_indices=tok, rhs_indices=rhs,
-                            group_size=u.group_size, bits=u.bits)
+                            group_size=u.group_size, bits=u.bits, mode=u.mode)
             act = swiglu(gate, up)
         d = self.down_proj
         pairs = torch.arange(P, device=x.device, dtype=torch.int32)
         y = gather_qmm(act, d.weight, d.scales, d.biases, lhs_indices=pairs, rhs_indices=rhs,
-                       group_size=d.group_size, bits=d.bits)                   # [P, 1, H]
+                       group_size=d.group_size, bits=d.bits, mode=d.mode)      # [P, 1, H]
         return y.reshape(*lead, k, y.shape[-1])
 
 

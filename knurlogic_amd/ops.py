@@ -693,6 +693,54 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, w_gu, s_gu, b_gu, w_down,
     return out
 
 
+#: (token, slot) pairs the token-major SwitchGLU kernels take (more: grouped by expert)
+TOK_MAX_PAIRS = 16
+
+
+def switch_glu_mx(x: torch.Tensor, indices: torch.Tensor, w_gu, s_gu, w_down, s_down,
+                  scores: torch.Tensor | None = None, mode: str = "mxfp4"):
+    """``switch_glu`` for experts in an OCP microscaled mode (kmi_switch_glu_mx):
+    mxfp4 (E2M1) or mxfp8 (E4M3) codes, uint8 E8M0 scales per 32 inputs, no
+    biases; gate and up stacked per expert (w_gu [E, 2I, H*bits/32], s_gu
+    [E, 2I, H/32]).  Token-major sizes only: T * k <= TOK_MAX_PAIRS."""
+    _on_gpu(x, indices, w_gu, s_gu, w_down, s_down, scores)
+    if mode not in _MX_BITS:
+        raise ValueError(f"switch_glu_mx: mode {mode!r} (mxfp4 or mxfp8)")
+    if x.dtype != torch.bfloat16:
+        raise ValueError("switch_glu_mx: only bfloat16 activations are implemented")
+    if s_gu.dtype != torch.uint8 or s_down.dtype != torch.uint8:
+        raise ValueError("switch_glu_mx: scales must be uint8 E8M0")
+    lead, H = tuple(x.shape[:-1]), x.shape[-1]
+    k = indices.shape[-1]
+    if tuple(indices.shape[:-1]) != lead:
+        raise ValueError("switch_glu_mx: indices [..., k] must match x [..., H]")
+    E, I2 = w_gu.shape[0], w_gu.shape[1]
+    I = I2 // 2
+    T = math.prod(lead)
+    if T * k > TOK_MAX_PAIRS:
+        raise ValueError(f"switch_glu_mx: {T * k} (token, slot) pairs (at most {TOK_MAX_PAIRS})")
+    xc = x.contiguous()
+    ic = indices.reshape(T, k).to(torch.int32).contiguous()
+    ts = [t.contiguous() for t in (w_gu, s_gu, w_down, s_down)]
+    sc = None
+    if scores is not None:
+        if scores.shape != indices.shape or scores.dtype != x.dtype:
+            raise ValueError("switch_glu_mx: scores must match indices in shape and x in dtype")
+        sc = scores.contiguous()
+        out = torch.empty(*lead, H, dtype=x.dtype, device=x.device)
+    else:
+        out = torch.empty(*lead, k, H, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out
+    L = _lib()
+    nbytes = L.kmi_switch_glu_workspace_bytes(T, H, I, k, E, 32, _MX_BITS[mode])
+    ws = _workspace(nbytes, x.device)
+    _abi.check(L.kmi_switch_glu_mx(_ptr(xc), T, H, I, k, _ptr(ic), _ptr(sc), *[_ptr(t) for t in ts], E,
+                                   DTYPE_CODE[x.dtype], 1 if mode == "mxfp4" else 2, _ptr(out), _ptr(ws),
+                                   nbytes, _stream(x)), "switch_glu_mx")
+    return out
+
+
 def moe_experts(x: torch.Tensor, logits: torch.Tensor, k: int, w_gu, s_gu, b_gu, w_down, s_down, b_down,
                 group_size: int = 64, bits: int = 4):
     """SparseMoeBlock's routed part from its router logits in one library

@@ -186,3 +186,41 @@ def test_quantize_mx_gives_the_references_checkpoint_back(dev):
         wq, sc = K.quantize(d, group_size=32, bits=4, mode="mxfp4")
         assert np.array_equal(sc.cpu().numpy(), s)
         assert np.array_equal(wq.view(torch.int32).cpu().numpy().view(np.uint32), w)
+
+
+@pytest.mark.parametrize("mode", ["mxfp4", "mxfp8"])
+@pytest.mark.parametrize("T,k", [(1, 8), (2, 8), (3, 4), (16, 8)])
+def test_switch_glu_mx_matches_the_oracle(dev, mode, T, k):
+    """SwitchGLU over mxfp4 / mxfp8 experts: up to 16 (token, slot) pairs in
+    the token-major kernels (one call, gate and up stacked), more through
+    gather_qmm; against the oracle's SwitchGLU over its mx matmul, and the
+    combine against moe_combine of the same y, bit for bit."""
+    rng = np.random.default_rng(T * 10 + k + (mode == "mxfp8"))
+    E, H, I = 16, 256, 128
+    bits = 4 if mode == "mxfp4" else 8
+    (hg, gg), (hu, gu), (hd, gd) = [_random_mx(rng, (E, n), kd, mode, dev) for n, kd in ((I, H), (I, H), (H, I))]
+    lin = lambda g: nn.QuantizedSwitchLinear(g[0], g[1], None, None, 32, bits, mode)
+    glu = nn.SwitchGLU(lin(gg), lin(gu), lin(gd))
+    x = bf16_normal(rng, (T, H))
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    fn = lambda h: (lambda xs, e: O.mx_quantized_matmul(xs, h[0][e], h[1][e], mode, True, "bfloat16"))
+    ref = O.switch_glu(x, inds, fn(hg), fn(hu), fn(hd))
+    tx, ti = to_torch(x, dev, BF), torch.from_numpy(inds).to(dev)
+    got = glu(tx, ti)
+    assert got.shape == (T, k, H)
+    assert_close(to_numpy(got), ref, what=f"{mode} switch_glu T={T} k={k}")
+    _, sc = O.route(bf16_normal(rng, (T, E)), k)
+    comb = glu.combine(tx, ti, to_torch(sc, dev, BF))
+    assert_close(to_numpy(comb), O.combine(ref, sc), what="combine")
+    assert torch.equal(comb, K.moe_combine(got, to_torch(sc, dev, BF)))
+
+
+def test_switch_glu_mx_refuses_what_it_must(dev):
+    rng = np.random.default_rng(9)
+    (hg, gg), (hd, gd) = _random_mx(rng, (4, 128), 64, "mxfp4", dev), _random_mx(rng, (4, 64), 64, "mxfp4", dev)
+    x = to_torch(bf16_normal(rng, (3, 64)), dev, BF)
+    inds = torch.zeros(3, 8, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):      # 24 pairs: past the token-major sizes
+        K.switch_glu_mx(x, inds, gg[0], gg[1], gd[0], gd[1], mode="mxfp4")
+    with pytest.raises(ValueError):
+        K.switch_glu_mx(x[:1], inds[:1], gg[0], gg[1], gd[0], gd[1], mode="nvfp4")
