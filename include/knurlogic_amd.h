@@ -365,9 +365,9 @@ size_t kmi_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k, in
  * mode 2 mxfp8 (E4M3, 4 per uint32), one uint8 E8M0 scale per 32 inputs,
  * no biases.  w_gu [E, 2I, H*bits/32] and s_gu [E, 2I, H/32] stack gate
  * (rows 0..I-1) and up; w_down [E, H, I*bits/32], s_down [E, H, I/32].
- * Token-major sizes only (T * k <= 16; the Python mirror takes the
- * gather_qmm path beyond).  Otherwise as kmi_switch_glu (workspace:
- * kmi_switch_glu_workspace_bytes with group 32).
+ * Up to 16 (token, slot) pairs run token-major, more grouped by expert,
+ * as kmi_switch_glu (workspace: kmi_switch_glu_workspace_bytes with group
+ * 32).
  */
 int kmi_switch_glu_mx(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
                       const void* scores, const uint32_t* w_gu, const uint8_t* s_gu, const uint32_t* w_down,

@@ -88,9 +88,7 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
     KMI_CHECK_ARG(T * H * 2 < (1LL << 31) && T * k * (H > I ? H : I) * 2 < (1LL << 31),
                   "switch_glu: activations past 2 GiB");
     const GluPlan p = plan_glu(T, H, I, k, E);
-    KMI_CHECK_ARG(!mx || (p.tok && group_size == 32),
-                  "switch_glu (mx): %lld pairs, group %d (token-major sizes: at most %lld pairs, group 32)",
-                  (long long)(T * k), group_size, (long long)TOK_MAX_PAIRS);
+    KMI_CHECK_ARG(!mx || group_size == 32, "switch_glu (mx): group %d (32)", group_size);
     if (!workspace || workspace_bytes < p.total) {
         set_error("switch_glu: workspace of %zu bytes needed, %zu given", p.total, workspace_bytes);
         return EWORKSPACE;
@@ -133,7 +131,7 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
     if (rc) return rc;
     QgArgs g = {};
     g.x = (const uint16_t*)x; g.xrows = T; g.w = w_gu; g.s = (const uint16_t*)s_gu;
-    g.b = (const uint16_t*)b_gu; g.E = E; g.N = I; g.K = H; g.erows = 2 * I; g.up_off = I;
+    g.b = (const uint16_t*)b_gu; g.E = E; g.N = I; g.K = H; g.erows = 2 * I; g.up_off = I; g.mx = mx;
     g.y = act; g.rows = P; g.tm = p.tm; g.tiles = sr.tiles; g.sorted = sr.sorted; g.lhs = nullptr;
     g.lhs_div = k; g.Mper = 1;
     const QgPlan pg = plan_qgemv_unsplit(I, H, sr.max_tiles, p.tm, group_size);
@@ -143,7 +141,7 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
     KMI_CHECK_LAUNCH("qgemv(gate|up)");
     QgArgs d = {};
     d.x = act; d.xrows = P; d.w = w_down; d.s = (const uint16_t*)s_down; d.b = (const uint16_t*)b_down;
-    d.E = E; d.N = H; d.K = I; d.erows = H; d.y = y; d.rows = P; d.tm = p.tm; d.tiles = sr.tiles;
+    d.E = E; d.N = H; d.K = I; d.erows = H; d.y = y; d.rows = P; d.tm = p.tm; d.tiles = sr.tiles; d.mx = mx;
     d.sorted = sr.sorted; d.lhs = nullptr; d.lhs_div = 1; d.Mper = 1;
     const QgPlan pd = plan_qgemv_unsplit(H, I, sr.max_tiles, p.tm, group_size);
     d.S = 1; d.gps = pd.gps;

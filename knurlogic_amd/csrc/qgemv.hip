@@ -58,6 +58,13 @@ __device__ __forceinline__ u32x4 x8_to_nibble_order(u32x4 v) {
 
 __device__ __forceinline__ float qg_bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
+// E8M0 scale byte (held in a 16-bit LDS slot): 2^(e - 127); 255 is NaN
+__device__ __forceinline__ float mx_scale_qg(uint32_t e) {
+    e &= 0xffu;
+    if (e == 255u) return __uint_as_float(0x7fc00000u);
+    return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
+}
+
 __device__ __forceinline__ float qg_f32_kept(double v) {
     float f = (float)v;
     asm volatile("" : "+v"(f));   // keep the float32 rounding (no fused f64 -> bf16 rounding)
@@ -83,9 +90,12 @@ constexpr size_t qg_lds_bytes() {
     return 2 * (S::W_BYTES + S::X_BYTES + (size_t)2 * NSET * QG_ROWS * (QG_KC / GS) * 2);
 }
 
-template <int BITS, int GS, int MC, bool GLU>
+// MX: microscaled codes (GS 32): the codes convert to bf16 exactly (E2M1,
+// E4M3), natural k order, one E8M0 scale per group and no bias term.
+template <int BITS, int GS, int MC, bool GLU, bool MX>
 __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
     constexpr int NSET = GLU ? 2 : 1;
+    constexpr int SB = MX ? 1 : 2;                       // bytes per scale
     using S = QgShape<BITS, NSET, MC>;
     constexpr int MT = S::MT, RB = S::RB, WST = S::WST, XST = S::XST;
     constexpr int WPIECES = S::WPIECES, WPASS = S::WPASS, XPASS = S::XPASS;
@@ -130,8 +140,8 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
     for (int set = 0; set < NSET; set++) {
         const int64_t r0 = (int64_t)expert * a.erows + (set ? a.up_off : 0);
         rw[set] = make_rsrc((const char*)a.w + r0 * rowbytes, a.N * rowbytes);
-        rs[set] = make_rsrc(a.s + r0 * G, a.N * G * 2);
-        rb[set] = make_rsrc(a.b + r0 * G, a.N * G * 2);
+        rs[set] = make_rsrc((const char*)a.s + r0 * G * SB, a.N * G * SB);
+        rb[set] = make_rsrc((const char*)a.b + r0 * G * SB, MX ? 0 : a.N * G * SB);
     }
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.xrows * K * 2);
     const __amdgpu_buffer_rsrc_t rz = make_rsrc(a.x, 0);
@@ -191,9 +201,14 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
                 const int idx = tid + 256 * q;
                 const int64_t row = n0 + idx / GPC, g = kc0 / GS + idx % GPC;
                 const bool ok = idx < QG_ROWS * GPC && row < a.N && g < G;
-                const int off = ok ? (int)((row * G + g) * 2) : (int)0x80000000u;
-                rsv[slot][set][q] = __builtin_amdgcn_raw_buffer_load_b16(live ? rs[set] : rz, off, 0, 0);
-                rbv[slot][set][q] = __builtin_amdgcn_raw_buffer_load_b16(live ? rb[set] : rz, off, 0, 0);
+                const int off = ok ? (int)((row * G + g) * SB) : (int)0x80000000u;
+                if constexpr (MX) {
+                    rsv[slot][set][q] = __builtin_amdgcn_raw_buffer_load_b8(live ? rs[set] : rz, off, 0, 0);
+                    rbv[slot][set][q] = 0u;
+                } else {
+                    rsv[slot][set][q] = __builtin_amdgcn_raw_buffer_load_b16(live ? rs[set] : rz, off, 0, 0);
+                    rbv[slot][set][q] = __builtin_amdgcn_raw_buffer_load_b16(live ? rb[set] : rz, off, 0, 0);
+                }
             }
 #pragma unroll
         for (int p = 0; p < XPASS; p++)
@@ -220,7 +235,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
 #pragma unroll
         for (int p = 0; p < XPASS; p++) {
             u32x4 v = rxv[slot][p];
-            if constexpr (BITS == 4) v = x8_to_nibble_order(v);
+            if constexpr (BITS == 4 && !MX) v = x8_to_nibble_order(v);
             *(u32x4*)(Xl(buf) + (p * 8 + tid / 32) * XST + 16 * (tid % 32)) = v;
         }
     };
@@ -261,15 +276,34 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
                 }
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
-                    if constexpr (BITS == 4) {
+                    if constexpr (MX && BITS == 4) {          // 8 E2M1 codes, natural order
+                        const uint32_t w = wv[t];
+                        B[set][t] = u32x4{
+                            __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.f, 0)),
+                            __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.f, 1)),
+                            __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.f, 2)),
+                            __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.f, 3))};
+                    } else if constexpr (MX) {                // 8 E4M3 codes
+                        const uint32_t w0 = wv[2 * t], w1 = wv[2 * t + 1];
+                        B[set][t] = u32x4{
+                            __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.f, false)),
+                            __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.f, true)),
+                            __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.f, false)),
+                            __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.f, true))};
+                    } else if constexpr (BITS == 4) {
                         B[set][t] = nib8_exact(wv[t]);
                     } else {
                         B[set][t] = u32x4{bytes_to_bf16x2(wv[2 * t], 0), bytes_to_bf16x2(wv[2 * t], 2),
                                           bytes_to_bf16x2(wv[2 * t + 1], 0), bytes_to_bf16x2(wv[2 * t + 1], 2)};
                     }
                 }
-                sc[set] = bf16_to_f32(Sl(buf, set, 0)[wr * GPC + gi]);
-                bi[set] = bf16_to_f32(Sl(buf, set, 1)[wr * GPC + gi]);
+                if constexpr (MX) {
+                    sc[set] = mx_scale_qg(Sl(buf, set, 0)[wr * GPC + gi]);
+                    bi[set] = 0.f;
+                } else {
+                    sc[set] = bf16_to_f32(Sl(buf, set, 0)[wr * GPC + gi]);
+                    bi[set] = bf16_to_f32(Sl(buf, set, 1)[wr * GPC + gi]);
+                }
             }
 #pragma unroll
             for (int c = 0; c < MC; c++) {
@@ -280,7 +314,7 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     const u32x4 A = *(const u32x4*)(Xl(buf) + (16 * c + nl) * XST + (gi * GS + j4 * RUN + 8 * t) * 2);
-                    X = mfma16x16x32(A, ones, X);
+                    if constexpr (!MX) X = mfma16x16x32(A, ones, X);
 #pragma unroll
                     for (int set = 0; set < NSET; set++) P[set] = mfma16x16x32(A, B[set][t], P[set]);
                 }
@@ -288,7 +322,8 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
                 for (int set = 0; set < NSET; set++)
 #pragma unroll
                     for (int e = 0; e < 4; e++)
-                        acc[set][c][e] = __builtin_fmaf(sc[set], P[set][e], __builtin_fmaf(bi[set], X[e], acc[set][c][e]));
+                        acc[set][c][e] = MX ? __builtin_fmaf(sc[set], P[set][e], acc[set][c][e])
+                                            : __builtin_fmaf(sc[set], P[set][e], __builtin_fmaf(bi[set], X[e], acc[set][c][e]));
             }
         }
     };
@@ -368,22 +403,24 @@ QgPlan plan_qgemv_unsplit(int64_t N, int64_t K, int64_t tiles, int tile_rows, in
     return p;
 }
 
-template <int B_, int G_, int M_, bool L_>
+template <int B_, int G_, int M_, bool L_, bool X_>
 static int launch_one(const QgArgs& a, dim3 grid, hipStream_t st) {
     constexpr size_t lds = qg_lds_bytes<B_, G_, L_ ? 2 : 1, M_>();
     static_assert(lds <= 160 * 1024, "qgemv tile exceeds the LDS");
     static bool attr = false;
     if (!attr) {
-        (void)hipFuncSetAttribute((const void*)qgemv_kernel<B_, G_, M_, L_>,
+        (void)hipFuncSetAttribute((const void*)qgemv_kernel<B_, G_, M_, L_, X_>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         attr = true;
     }
-    qgemv_kernel<B_, G_, M_, L_><<<grid, 256, lds, st>>>(a);
+    qgemv_kernel<B_, G_, M_, L_, X_><<<grid, 256, lds, st>>>(a);
     return OK;
 }
 
-#define KMI_QG_CASE(B_, G_, M_, L_) \
-    if (bits == B_ && gs == G_ && p.mc == M_ && glu == L_) return launch_one<B_, G_, M_, L_>(a, grid, st);
+#define KMI_QG_CASE(B_, G_, M_, L_)                                                                   \
+    if (!a.mx && bits == B_ && gs == G_ && p.mc == M_ && glu == L_) return launch_one<B_, G_, M_, L_, false>(a, grid, st);
+#define KMI_QG_MXC(B_, M_, L_)                                                                        \
+    if (a.mx && bits == B_ && gs == 32 && p.mc == M_ && glu == L_) return launch_one<B_, 32, M_, L_, true>(a, grid, st);
 #define KMI_QG_M(B_, G_, L_) KMI_QG_CASE(B_, G_, 1, L_) KMI_QG_CASE(B_, G_, 2, L_) KMI_QG_CASE(B_, G_, 4, L_)
 #define KMI_QG_G(B_, L_) KMI_QG_M(B_, 32, L_) KMI_QG_M(B_, 64, L_) KMI_QG_M(B_, 128, L_)
 
@@ -395,6 +432,10 @@ int launch_qgemv(const QgArgs& a, const QgPlan& p, int bits, int gs, bool glu, i
     }
     const dim3 grid((unsigned)ceil_div(a.N, QG_ROWS), (unsigned)p.S, (unsigned)ntiles);
     KMI_QG_G(4, false) KMI_QG_G(8, false) KMI_QG_G(4, true) KMI_QG_G(8, true)
+    KMI_QG_MXC(4, 1, false) KMI_QG_MXC(4, 2, false) KMI_QG_MXC(4, 4, false)
+    KMI_QG_MXC(4, 1, true) KMI_QG_MXC(4, 2, true) KMI_QG_MXC(4, 4, true)
+    KMI_QG_MXC(8, 1, false) KMI_QG_MXC(8, 2, false) KMI_QG_MXC(8, 4, false)
+    KMI_QG_MXC(8, 1, true) KMI_QG_MXC(8, 2, true) KMI_QG_MXC(8, 4, true)
     set_error("qgemv: no kernel for bits=%d gs=%d mc=%d", bits, gs, p.mc);
     return EINVAL_ARG;
 }
@@ -402,5 +443,6 @@ int launch_qgemv(const QgArgs& a, const QgPlan& p, int bits, int gs, bool glu, i
 #undef KMI_QG_G
 #undef KMI_QG_M
 #undef KMI_QG_CASE
+#undef KMI_QG_MXC
 
 }  // namespace kmi

@@ -29,6 +29,10 @@ struct QgArgs {
     const int32_t* lhs;
     int64_t lhs_div;
     int64_t Mper;
+    // 0: affine (bf16 scales and biases per group); 1: OCP microscaled codes
+    // (E2M1 at 4 bits, E4M3 at 8) with one uint8 E8M0 scale per 32 inputs in
+    // `s` and no biases (gs 32)
+    int mx;
 };
 
 // Launch shape: 64 weight rows per workgroup (16 per wave), K in chunks of

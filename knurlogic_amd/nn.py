@@ -24,7 +24,7 @@ import math
 
 import torch
 
-from .ops import (TOK_MAX_PAIRS, add_bias, gather_qmm, linear, moe_combine, moe_experts, moe_route,
+from .ops import (add_bias, gather_qmm, linear, moe_combine, moe_experts, moe_route,
                   moe_shared_add, quantize, quantized_matmul, swiglu, switch_glu, switch_glu_mx, vq_gather_qmm,
                   vq_glu, vq_packed_gather_qmm, vq_packed_glu, vq_switch_glu)
 
@@ -154,12 +154,11 @@ class SwitchGLU:
                 and d.mode == "affine" and f.group_size == d.group_size and f.scales.dtype == torch.bfloat16)
 
     def _one_call_mx(self, x: torch.Tensor, k: int) -> bool:
-        """mxfp4 / mxfp8 experts at token-major sizes (kmi_switch_glu_mx)."""
+        """mxfp4 / mxfp8 experts in one call (kmi_switch_glu_mx)."""
         f, d = self.fused, self.down_proj
         return (f is not None and d.bias is None and k <= 8 and f.mode in ("mxfp4", "mxfp8")
                 and d.mode == f.mode and x.dtype == torch.bfloat16
-                and x.shape[-1] % 64 == 0 and (f.weight.shape[1] // 2) % 64 == 0
-                and math.prod(x.shape[:-1]) * k <= TOK_MAX_PAIRS)
+                and x.shape[-1] % 64 == 0 and (f.weight.shape[1] // 2) % 64 == 0)
 
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
         """x [..., H], indices [..., k] (int) -> [..., k, H]."""

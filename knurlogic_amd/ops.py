@@ -693,16 +693,12 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, w_gu, s_gu, b_gu, w_down,
     return out
 
 
-#: (token, slot) pairs the token-major SwitchGLU kernels take (more: grouped by expert)
-TOK_MAX_PAIRS = 16
-
-
 def switch_glu_mx(x: torch.Tensor, indices: torch.Tensor, w_gu, s_gu, w_down, s_down,
                   scores: torch.Tensor | None = None, mode: str = "mxfp4"):
     """``switch_glu`` for experts in an OCP microscaled mode (kmi_switch_glu_mx):
     mxfp4 (E2M1) or mxfp8 (E4M3) codes, uint8 E8M0 scales per 32 inputs, no
     biases; gate and up stacked per expert (w_gu [E, 2I, H*bits/32], s_gu
-    [E, 2I, H/32]).  Token-major sizes only: T * k <= TOK_MAX_PAIRS."""
+    [E, 2I, H/32])."""
     _on_gpu(x, indices, w_gu, s_gu, w_down, s_down, scores)
     if mode not in _MX_BITS:
         raise ValueError(f"switch_glu_mx: mode {mode!r} (mxfp4 or mxfp8)")
@@ -717,8 +713,6 @@ def switch_glu_mx(x: torch.Tensor, indices: torch.Tensor, w_gu, s_gu, w_down, s_
     E, I2 = w_gu.shape[0], w_gu.shape[1]
     I = I2 // 2
     T = math.prod(lead)
-    if T * k > TOK_MAX_PAIRS:
-        raise ValueError(f"switch_glu_mx: {T * k} (token, slot) pairs (at most {TOK_MAX_PAIRS})")
     xc = x.contiguous()
     ic = indices.reshape(T, k).to(torch.int32).contiguous()
     ts = [t.contiguous() for t in (w_gu, s_gu, w_down, s_down)]

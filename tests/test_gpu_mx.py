@@ -189,11 +189,11 @@ def test_quantize_mx_gives_the_references_checkpoint_back(dev):
 
 
 @pytest.mark.parametrize("mode", ["mxfp4", "mxfp8"])
-@pytest.mark.parametrize("T,k", [(1, 8), (2, 8), (3, 4), (16, 8)])
+@pytest.mark.parametrize("T,k", [(1, 8), (2, 8), (3, 4), (16, 8), (70, 4)])
 def test_switch_glu_mx_matches_the_oracle(dev, mode, T, k):
-    """SwitchGLU over mxfp4 / mxfp8 experts: up to 16 (token, slot) pairs in
-    the token-major kernels (one call, gate and up stacked), more through
-    gather_qmm; against the oracle's SwitchGLU over its mx matmul, and the
+    """SwitchGLU over mxfp4 / mxfp8 experts in one call (gate and up
+    stacked): up to 16 (token, slot) pairs token-major, more grouped by
+    expert; against the oracle's SwitchGLU over its mx matmul, and the
     combine against moe_combine of the same y, bit for bit."""
     rng = np.random.default_rng(T * 10 + k + (mode == "mxfp8"))
     E, H, I = 16, 256, 128
@@ -220,7 +220,7 @@ def test_switch_glu_mx_refuses_what_it_must(dev):
     (hg, gg), (hd, gd) = _random_mx(rng, (4, 128), 64, "mxfp4", dev), _random_mx(rng, (4, 64), 64, "mxfp4", dev)
     x = to_torch(bf16_normal(rng, (3, 64)), dev, BF)
     inds = torch.zeros(3, 8, dtype=torch.int32, device=dev)
-    with pytest.raises(ValueError):      # 24 pairs: past the token-major sizes
-        K.switch_glu_mx(x, inds, gg[0], gg[1], gd[0], gd[1], mode="mxfp4")
     with pytest.raises(ValueError):
-        K.switch_glu_mx(x[:1], inds[:1], gg[0], gg[1], gd[0], gd[1], mode="nvfp4")
+        K.switch_glu_mx(x, inds, gg[0], gg[1], gd[0], gd[1], mode="nvfp4")
+    with pytest.raises(ValueError):      # scales must be E8M0 bytes
+        K.switch_glu_mx(x, inds, gg[0], gg[1].to(torch.bfloat16), gd[0], gd[1], mode="mxfp4")
