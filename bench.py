@@ -422,6 +422,39 @@ def bench_mx_moe(T, calls, dev, mode="mxfp4"):
             "bound": "hbm", "bytes": nbytes, "flops": 2.0 * T * k * 3 * H * I}
 
 
+def bench_mx_dense(mode, M, N, K, calls, dev):
+    """quantized_matmul over a microscaled weight [N, K] (mxfp4: E2M1 codes,
+    mxfp8: E4M3; one E8M0 scale byte per 32 inputs, no biases), weight sets
+    rotated past 1 GB.  Bytes: codes and scales once, x and y."""
+    import torch
+    import knurlogic_amd as KA
+    bits = 4 if mode == "mxfp4" else 8
+    per = N * (K * bits // 8 + K // 32)
+    n = max(4, math.ceil(ROTATE_BYTES / per))
+    g = torch.Generator(device=dev).manual_seed(7000 + M)
+    sets = []
+    for _ in range(n):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K * bits // 32), device=dev, generator=g,
+                          dtype=torch.int32).view(torch.uint32)
+        sc = torch.randint(118, 124, (N, K // 32), device=dev, generator=g, dtype=torch.int32).to(torch.uint8)
+        sets.append((w, sc))
+    x = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+
+    def run():
+        for i in range(calls):
+            w, sc = sets[i % n]
+            KA.quantized_matmul(x, w, sc, None, True, 32, bits, mode)
+
+    us = time_graph(run) / calls * 1e3
+    nbytes = per + 2 * M * K + 2 * M * N
+    gbs = nbytes / (us * 1e-6) / 1e9
+    del sets
+    torch.cuda.empty_cache()
+    return {"op": f"{mode}_quantized_matmul", "M": M, "N": N, "K": K, "cache": "cold", "us": round(us, 3),
+            "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm", "bytes": nbytes,
+            "flops": 2.0 * M * N * K}
+
+
 def ceilings(dev, headline_bytes):
     """Measured ceilings beside the published peaks: the HBM read rate of a
     plain read kernel (kmi_read_probe, 16-byte nontemporal loads, nothing
@@ -601,6 +634,10 @@ def main():
     if not args.quick and "moe" in only:
         for t_ in (1, 16):
             detail.append(bench_mx_moe(t_, 30, dev))
+    if not args.quick and "dense" in only:
+        for mode in ("mxfp4", "mxfp8"):
+            for m in (1, 16):
+                detail.append(bench_mx_dense(mode, m, 14336, 4096, 100, dev))
     if not args.quick and "moe" in only:
         for t_ in (1, 16, 256):
             for cold in (True, False):

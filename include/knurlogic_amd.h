@@ -143,6 +143,26 @@ int kmi_qmm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
 size_t kmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits);
 
 /*
+ * mx.quantized_matmul(x, w, scales, transpose=True, group_size=32, bits,
+ * mode="mxfp4" | "mxfp8") -- nn.QuantizedLinear of the loader's microscaled
+ * layers (src/knurlogic/engine/model/load_model.py:153-173):
+ *   y[M, N] = x[M, K] @ What[N, K]^T,  What = code * 2^(e - 127),
+ * codes E2M1 (mode 1, 4 bits, 8 per uint32) or E4M3 (mode 2, 8 bits, 4 per
+ * uint32), one uint8 E8M0 scale e per 32 inputs (scales [N, K/32]), no
+ * biases; fp32 accumulation, y rounded once to bf16 (x and y bf16).  Up to
+ * 64 rows with K a multiple of 64 run kmi_qmm's decode kernels (M = 1: the
+ * streaming GEMV; 2..16 rows with K a multiple of 256: the direct-to-LDS
+ * MFMA kernel; else the MFMA GEMV), anything else kmi_qmm_batched.  Each
+ * output row depends only on its own input row.  `workspace`
+ * (kmi_qmm_mx_workspace_bytes) holds split-K partials; it may be NULL when
+ * that size is 0.
+ */
+int kmi_qmm_mx(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w, const uint8_t* scales,
+               int dtype, int mode, void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+size_t kmi_qmm_mx_workspace_bytes(int64_t M, int64_t K, int64_t N, int mode);
+
+/*
  * kmi_qmm without a workspace argument, allocating nothing: no counterpart
  * in the reference.  It is for callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops that forbid hipMalloc).  The

@@ -23,6 +23,8 @@ SIGNATURES = {
     "kmi_dequantize_affine": (I, [P, P, P, I, I64, I64, I, I, P, I, I, P]),
     "kmi_qmm": (I, [P, I64, I64, I64, P, P, P, I, I, I, P, P, SZ, P]),
     "kmi_qmm_workspace_bytes": (SZ, [I64, I64, I64, I, I]),
+    "kmi_qmm_mx": (I, [P, I64, I64, I64, P, P, I, I, P, P, SZ, P]),
+    "kmi_qmm_mx_workspace_bytes": (SZ, [I64, I64, I64, I]),
     "kmi_qmm_noalloc_scratch_bytes": (SZ, []),
     "kmi_qmm_noalloc": (I, [P, I64, I64, I64, P, P, P, I, I, I, P, P]),
     "kmi_gather_qmm": (I, [P, I64, I64, I64, P, P, P, I64, I64, P, P, I64, I, I, I, I,

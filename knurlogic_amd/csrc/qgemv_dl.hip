@@ -70,7 +70,18 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, unsigned char* ld
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KMI_LDSP(lds), 4, voff, soff, 0, 0);
 }
 
-template <int BITS, int GS>
+// E8M0 scale byte: 2^(e - 127); 255 is NaN
+__device__ __forceinline__ float mx_scale_dl(uint32_t e) {
+    if (e == 255u) return __uint_as_float(0x7fc00000u);
+    return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
+}
+
+// MX: microscaled codes (E2M1 / E4M3, exact in bf16), one E8M0 byte scale
+// per 32 inputs and no biases.  A row's scales of one chunk are 8 bytes:
+// each wave moves its own 16 rows' in one 4-byte DMA block whose lanes
+// 32..63 read zeros into padding (256 bytes per wave).  The affine bf16
+// scales and biases move in 4-byte units, DPR blocks each.
+template <int BITS, int GS, bool MX>
 struct DlShape {
     static constexpr int RB = DL_KC * BITS / 8;          // weight bytes per row per chunk
     static constexpr int RPI = 1024 / RB;                // weight rows per DMA block
@@ -80,9 +91,10 @@ struct DlShape {
     static constexpr int XI = 8;                         // x blocks per chunk: 2 rows of 512 bytes each
     static constexpr int X_BYTES = 16 * DL_KC * 2;
     static constexpr int GPC = DL_KC / GS;               // groups per chunk
-    static constexpr int DPR = GPC / 2;                  // scale dwords per row per chunk
-    static constexpr int SBI = 2 * DPR;                  // scale + bias blocks per chunk
-    static constexpr int SB_BYTES = 2 * DL_ROWS * GPC * 2;
+    static constexpr int SB = MX ? 1 : 2;                // bytes per scale
+    static constexpr int DPR = MX ? 1 : GPC / 2;         // affine: 4-byte elements per row per chunk
+    static constexpr int SBI = MX ? 4 : 2 * DPR;         // scale (+ bias) blocks per chunk
+    static constexpr int SB_BYTES = MX ? 4 * 256 : 2 * DL_ROWS * GPC * 2;
     static constexpr int STAGE = W_BYTES + X_BYTES + SB_BYTES;
     static constexpr int PER_WAVE = WBLK / 4 + XI / 4 + SBI / 4;   // DMA loads per wave per chunk
     static constexpr int GB = GS * BITS / 8;             // bytes per row per group
@@ -90,13 +102,15 @@ struct DlShape {
     static constexpr int NT = GS / 32;                   // MFMAs per group
     static_assert(WBLK % 4 == 0 && XI % 4 == 0 && SBI % 4 == 0, "every wave issues the same loads");
     static_assert(LB == 4 || LB == 8 || LB == 16, "lane run of 4, 8 or 16 bytes");
+    static_assert(!MX || GPC == 8, "MX scales: 8 bytes per row and chunk");
 };
 
 }  // namespace
 
-template <int BITS, int GS>
+template <int BITS, int GS, bool MX>
 __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
-    using S_ = DlShape<BITS, GS>;
+    using S_ = DlShape<BITS, GS, MX>;
+    constexpr int SB = S_::SB;
     constexpr int RB = S_::RB, RPI = S_::RPI, WBLK = S_::WBLK, PPR = S_::PPR, W_BYTES = S_::W_BYTES;
     constexpr int X_BYTES = S_::X_BYTES, GPC = S_::GPC, DPR = S_::DPR, SBI = S_::SBI, STAGE = S_::STAGE;
     constexpr int GB = S_::GB, LB = S_::LB, NT = S_::NT;
@@ -109,8 +123,8 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
     const int64_t K = a.K, G = K / GS, M = a.rows;
     const uint32_t rowbytes = (uint32_t)(K * BITS / 8);
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w, a.N * (int64_t)rowbytes);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s, a.N * G * 2);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b, a.N * G * 2);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s, a.N * G * SB);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b, MX ? 0 : a.N * G * SB);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, M * K * 2);
     const int chunks = (int)(K / DL_KC);
     const int c0 = (int)blockIdx.y * a.gps;
@@ -133,11 +147,18 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
     int sbo[SBI / 4], sbw[SBI / 4];
 #pragma unroll
     for (int j = 0; j < SBI / 4; j++) {
-        const int q = wave + 4 * j, which = q / DPR, d = q % DPR;
-        const int row = d * (DL_ROWS / DPR) + lane / DPR;
-        sbv[j] = n0 + row < a.N ? (uint32_t)((n0 + row) * G * 2) + 4u * (uint32_t)(lane % DPR) : DL_NONE;
-        sbo[j] = which * (DL_ROWS * GPC * 2) + d * 256;
-        sbw[j] = which;
+        if constexpr (MX) {
+            const int row = wave * 16 + (lane >> 1);
+            sbv[j] = lane < 32 && n0 + row < a.N ? (uint32_t)((n0 + row) * G) + 4u * (uint32_t)(lane & 1) : DL_NONE;
+            sbo[j] = wave * 256;
+            sbw[j] = 0;
+        } else {
+            const int q = wave + 4 * j, which = q / DPR, d = q % DPR;
+            const int row = d * (DL_ROWS / DPR) + lane / DPR;
+            sbv[j] = n0 + row < a.N ? (uint32_t)((n0 + row) * G * 2) + 4u * (uint32_t)(lane % DPR) : DL_NONE;
+            sbo[j] = which * (DL_ROWS * GPC * 2) + d * 256;
+            sbw[j] = which;
+        }
     }
 
     // chunk i of this split into stage i % NS; past the split's chunks every
@@ -154,7 +175,7 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
             dma16(rx, base + W_BYTES + (wave + 4 * j) * 1024, live ? xv[j] : DL_NONE, c * (DL_KC * 2), 0);
 #pragma unroll
         for (int j = 0; j < SBI / 4; j++)
-            dma4(sbw[j] ? rb : rs, base + W_BYTES + X_BYTES + sbo[j], live ? sbv[j] : DL_NONE, c * (GPC * 2));
+            dma4(sbw[j] ? rb : rs, base + W_BYTES + X_BYTES + sbo[j], live ? sbv[j] : DL_NONE, c * (GPC * SB));
     };
 #pragma unroll
     for (int i = 0; i < DL_NS - 1; i++) issue(i);
@@ -191,8 +212,13 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
                     const int xp = gi * (GS / 8) + j4 * (GS / 32) + t;
                     A[g][t] = *(const u32x4*)(xl + 16 * (xp ^ (nl & 7)));
                 }
-                sc[g] = bf16_to_f32(sl[wr * GPC + gi]);
-                bi[g] = bf16_to_f32(sl[DL_ROWS * GPC + wr * GPC + gi]);
+                if constexpr (MX) {
+                    sc[g] = mx_scale_dl(((const uint8_t*)sl)[wave * 256 + nl * 8 + gi]);
+                    bi[g] = 0.f;
+                } else {
+                    sc[g] = bf16_to_f32(sl[wr * GPC + gi]);
+                    bi[g] = bf16_to_f32(sl[DL_ROWS * GPC + wr * GPC + gi]);
+                }
             }
             f32x4 P[GH], X[GH];
 #pragma unroll
@@ -205,17 +231,33 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
 #pragma unroll
                 for (int g = 0; g < GH; g++) {
                     u32x4 B;
-                    if constexpr (BITS == 4) B = nib8_natural(wd[g][t]);
-                    else B = u32x4{bytes_to_bf16x2(wd[g][2 * t], 0), bytes_to_bf16x2(wd[g][2 * t], 2),
-                                   bytes_to_bf16x2(wd[g][2 * t + 1], 0), bytes_to_bf16x2(wd[g][2 * t + 1], 2)};
-                    X[g] = mfma16x16x32(A[g][t], ones, X[g]);
+                    if constexpr (MX && BITS == 4) {
+                        const uint32_t w = wd[g][t];
+                        B = u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.f, 0)),
+                                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.f, 1)),
+                                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.f, 2)),
+                                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.f, 3))};
+                    } else if constexpr (MX) {
+                        const uint32_t w0 = wd[g][2 * t], w1 = wd[g][2 * t + 1];
+                        B = u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.f, false)),
+                                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.f, true)),
+                                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.f, false)),
+                                  __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.f, true))};
+                    } else if constexpr (BITS == 4) {
+                        B = nib8_natural(wd[g][t]);
+                    } else {
+                        B = u32x4{bytes_to_bf16x2(wd[g][2 * t], 0), bytes_to_bf16x2(wd[g][2 * t], 2),
+                                  bytes_to_bf16x2(wd[g][2 * t + 1], 0), bytes_to_bf16x2(wd[g][2 * t + 1], 2)};
+                    }
+                    if constexpr (!MX) X[g] = mfma16x16x32(A[g][t], ones, X[g]);
                     P[g] = mfma16x16x32(A[g][t], B, P[g]);
                 }
 #pragma unroll
             for (int g = 0; g < GH; g++)
 #pragma unroll
                 for (int e = 0; e < 4; e++)
-                    acc[e] = __builtin_fmaf(sc[g], P[g][e], __builtin_fmaf(bi[g], X[g][e], acc[e]));
+                    acc[e] = MX ? __builtin_fmaf(sc[g], P[g][e], acc[e])
+                                : __builtin_fmaf(sc[g], P[g][e], __builtin_fmaf(bi[g], X[g][e], acc[e]));
         }
         issue(i + DL_NS - 1);
     }
@@ -237,17 +279,17 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
 
 namespace {
 
-template <int BITS, int GS>
+template <int BITS, int GS, bool MX>
 int launch_dl(const QgArgs& a, dim3 grid, hipStream_t st) {
-    constexpr size_t lds = (size_t)DL_NS * DlShape<BITS, GS>::STAGE;
+    constexpr size_t lds = (size_t)DL_NS * DlShape<BITS, GS, MX>::STAGE;
     static_assert(lds <= 160 * 1024, "qgemv_dl stages exceed the LDS");
     static bool attr = false;
     if (!attr) {
-        (void)hipFuncSetAttribute((const void*)qgemv_dl_kernel<BITS, GS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (void)hipFuncSetAttribute((const void*)qgemv_dl_kernel<BITS, GS, MX>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)lds);
         attr = true;
     }
-    qgemv_dl_kernel<BITS, GS><<<grid, 256, lds, st>>>(a);
+    qgemv_dl_kernel<BITS, GS, MX><<<grid, 256, lds, st>>>(a);
     return OK;
 }
 
@@ -272,10 +314,15 @@ QgPlan plan_qgemv_dl(int64_t N, int64_t K) {
 
 int launch_qgemv_dl(const QgArgs& a, const QgPlan& p, int bits, int gs, hipStream_t st) {
     const dim3 grid((unsigned)ceil_div(a.N, DL_ROWS), (unsigned)p.S);
-    if (bits == 4 && gs == 64) return launch_dl<4, 64>(a, grid, st);
-    if (bits == 4 && gs == 32) return launch_dl<4, 32>(a, grid, st);
-    if (bits == 8 && gs == 64) return launch_dl<8, 64>(a, grid, st);
-    if (bits == 8 && gs == 32) return launch_dl<8, 32>(a, grid, st);
+    if (a.mx) {
+        if (bits == 4 && gs == 32) return launch_dl<4, 32, true>(a, grid, st);
+        if (bits == 8 && gs == 32) return launch_dl<8, 32, true>(a, grid, st);
+    } else {
+        if (bits == 4 && gs == 64) return launch_dl<4, 64, false>(a, grid, st);
+        if (bits == 4 && gs == 32) return launch_dl<4, 32, false>(a, grid, st);
+        if (bits == 8 && gs == 64) return launch_dl<8, 64, false>(a, grid, st);
+        if (bits == 8 && gs == 32) return launch_dl<8, 32, false>(a, grid, st);
+    }
     set_error("quantized_matmul: no direct-to-LDS kernel for %d bits, group %d", bits, gs);
     return EINVAL_ARG;
 }

@@ -348,6 +348,66 @@ int kmi_qmm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
     return run_skinny(a, p, bits, group_size, ntiles, workspace, nullptr, 1, dl, st);
 }
 
+// Microscaled dense decode: the decode kernels of kmi_qmm with the E2M1 /
+// E4M3 decode and byte scales; more than 64 rows, or K not a multiple of 64,
+// take the batched kernel (nd = 0).
+static bool mx_decode_shape(int64_t M, int64_t K) { return M <= SKINNY_MAX_M && K % 64 == 0; }
+
+size_t kmi_qmm_mx_workspace_bytes(int64_t M, int64_t K, int64_t N, int mode) {
+    if (M <= 0 || K <= 0 || N <= 0 || (mode != 1 && mode != 2)) return 0;
+    const int bits = mode == 1 ? 4 : 8;
+    if (!mx_decode_shape(M, K)) return kmi_qmm_batched_workspace_bytes(0, nullptr, M, K, N);
+    if (choose_kind(M, K, bits) != QmvKind::SKINNY) return 0;
+    return skinny_partial_bytes(dense_skinny_plan(M, K, N, bits, 32), M, N);
+}
+
+int kmi_qmm_mx(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w, const uint8_t* scales,
+               int dtype, int mode, void* y, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(mode == 1 || mode == 2, "quantized_matmul: mode %d is not microscaled (1 mxfp4, 2 mxfp8)", mode);
+    const int bits = mode == 1 ? 4 : 8;
+    KMI_CHECK_ARG(M >= 0 && K > 0 && K % 32 == 0 && N > 0,
+                  "quantized_matmul: M=%lld K=%lld N=%lld (K a multiple of 32)", (long long)M, (long long)K,
+                  (long long)N);
+    if (!mx_decode_shape(M, K)) {
+        const int64_t xs[1] = {K}, ws[1] = {K * bits / 32}, ss[1] = {K / 32};
+        return kmi_qmm_batched(x, xs, w, ws, scales, nullptr, ss, 0, nullptr, M, K, N, 1, dtype, 32, bits, mode,
+                               nullptr, nullptr, 0, 0, 1.0f, y, N, workspace, workspace_bytes, stream);
+    }
+    int rc = check_common(K, N, dtype, 32, bits);
+    if (rc) return rc;
+    KMI_CHECK_ARG(w && scales, "quantized_matmul: null pointer");
+    if (M == 0) return OK;
+    KMI_CHECK_ARG(x && y, "quantized_matmul: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    const QmvKind kind = choose_kind(M, K, bits);
+    if (kind != QmvKind::SKINNY) {
+        QmvArgs a = {};
+        a.x = (const uint16_t*)x; a.w = w; a.s = (const uint16_t*)scales; a.b = nullptr;
+        a.y = (uint16_t*)y; a.K = K; a.N = N; a.rows = M; a.Mper = 1; a.Xrows = M; a.S = 1;
+        a.gs_shift = 5; a.mx = 1;
+        const int tm = tile_rows(kind);
+        a.tile_m = tm;
+        const ValuShape v = valu_shape(N, K, bits, ceil_div(M, tm));
+        dim3 grid((unsigned)v.groups, 1, (unsigned)ceil_div(M, tm));
+        return launch_valu(a, bits, grid, valu_lds(K, bits), st, v);
+    }
+    const int tm = skinny_tile_rows(M);
+    const int64_t ntiles = ceil_div(M, tm);
+    const bool dl = use_dl(M, K, bits, 32);
+    const QgPlan p = dense_skinny_plan(M, K, N, bits, 32);
+    const size_t need = skinny_partial_bytes(p, M, N);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+        set_error("quantized_matmul: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+        return EWORKSPACE;
+    }
+    QgArgs a = {};
+    a.x = (const uint16_t*)x; a.xrows = M; a.w = w; a.s = (const uint16_t*)scales; a.b = nullptr;
+    a.E = 1; a.N = N; a.K = K; a.erows = N; a.y = (uint16_t*)y;
+    a.rows = M; a.tm = tm; a.lhs_div = 1; a.Mper = 1; a.mx = 1;
+    return run_skinny(a, p, bits, 32, ntiles, workspace, nullptr, 1, dl, st);
+}
+
 size_t kmi_gather_qmm_workspace_bytes(int64_t P, int64_t M, int64_t E, int64_t K,
                                       int64_t N, int group_size, int bits) {
     if (P <= 0 || M <= 0 || E <= 0 || K <= 0 || N <= 0 || group_size <= 0 || (bits != 4 && bits != 8))

@@ -24,6 +24,8 @@ struct QmvArgs {
     const int32_t* lhs;       // [P] x batch index per pair
     int64_t Mper;             // rows per pair (x [X, Mper, K])
     int64_t Xrows;            // X * Mper: rows of x, for bounds
+    int mx;                   // 1: OCP microscaled codes (E2M1 at 4 bits, E4M3 at 8), uint8
+                              // E8M0 scales per 32 inputs in s, no biases (gs_shift 5)
 };
 
 struct Tile {

@@ -39,9 +39,12 @@ constexpr uint32_t NONE = QV_NONE;
 // tile z is row z of a dense x, and no pointer-dependent branch delays the
 // first loads (each scalar round trip to the kernel arguments costs the
 // first wave of a CU most of a microsecond).
-template <int BITS, int RPW, int S, int WV, bool GATHER>
+// MX: microscaled codes (E2M1 / E4M3 converted exactly to fp16, x staged in
+// natural pair order), one E8M0 byte scale per 32 inputs, no bias term.
+template <int BITS, int RPW, int S, int WV, bool GATHER, bool MX>
 __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
     constexpr int NT = 64 * WV;                   // threads per workgroup
+    constexpr uint32_t SB = MX ? 1 : 2;           // bytes per scale
     constexpr int CK = 128 / BITS;                // k per 16-byte chunk: 32 or 16
     constexpr int XV = CK / 8;                    // 8-element x pieces per chunk: 4 or 2
     extern __shared__ __align__(16) unsigned char smem[];
@@ -68,8 +71,8 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
     const int n0 = (int)blockIdx.x * (WV * RPW) + wave * RPW;
     const int64_t eoff = (int64_t)t.expert * a.N;
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.w + eoff * wpr, a.N * (int64_t)wpr * 4);
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s + eoff * gpr, a.N * (int64_t)gpr * 2);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b + eoff * gpr, a.N * (int64_t)gpr * 2);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc((const char*)a.s + eoff * gpr * SB, a.N * (int64_t)gpr * SB);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc((const char*)a.b + eoff * gpr * SB, MX ? 0 : a.N * (int64_t)gpr * 2);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.Xrows * a.K * 2);
 
     const int64_t xrow = GATHER ? x_row_of(a, t.start) : t.start;
@@ -82,7 +85,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
     const uint32_t xso = xok ? (uint32_t)(xrow * a.K * 2) : 0u;
     auto xvo = [&](int p) -> uint32_t { return (xok && p < P) ? (uint32_t)p * 16u : NONE; };
 
-    auto stage = [&](int p, u32x4 raw) { stage_x16<BITS>(p, raw, P, C, xs, xm); };
+    auto stage = [&](int p, u32x4 raw) { stage_x16<BITS, MX>(p, raw, P, C, xs, xm); };
 
     // (0) pieces beyond two per thread (long rows): staged before any
     // weight load is issued, so their waits drain nothing
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
     const int full = C >> 6;
     const bool in_tail = lane < (C & 63);
     const uint32_t vw = (uint32_t)lane * 16u;
-    const uint32_t vg = (uint32_t)((lane * CK) >> a.gs_shift) * 2u;
+    const uint32_t vg = (uint32_t)((lane * CK) >> a.gs_shift) * SB;
     const uint32_t vwt = in_tail ? vw : NONE, vgt = in_tail ? vg : NONE;
     // rows past N (only in the last wave of the grid) re-read row N-1; their
     // results are never stored
@@ -110,7 +113,7 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
     for (int r = 0; r < RPW; r++) {
         const uint32_t row = (uint32_t)(n0 + r < a.N ? n0 + r : a.N - 1);
         wrow[r] = row * (uint32_t)wpr * 4u;
-        srow[r] = row * (uint32_t)gpr * 2u;
+        srow[r] = row * (uint32_t)gpr * SB;
     }
 
     u32x4 W[S][RPW];
@@ -123,11 +126,16 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
         for (int u = 0; u < S; u++) {
             const int su = nb * S + u;
             const uint32_t vo = su < full ? vg : su == full ? vgt : NONE;
-            const uint32_t so = (uint32_t)(((64 * su * CK) >> a.gs_shift) * 2);
+            const uint32_t so = (uint32_t)(((64 * su * CK) >> a.gs_shift) * SB);
 #pragma unroll
             for (int r = 0; r < RPW; r++) {
-                SC[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)vo, (int)(srow[r] + so), 0);
-                BI[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)vo, (int)(srow[r] + so), 0);
+                if constexpr (MX) {
+                    SC[u][r] = __builtin_amdgcn_raw_buffer_load_b8(rs, (int)vo, (int)(srow[r] + so), 0);
+                    BI[u][r] = 0u;
+                } else {
+                    SC[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)vo, (int)(srow[r] + so), 0);
+                    BI[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rb, (int)vo, (int)(srow[r] + so), 0);
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -168,9 +176,14 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
             const float4 m = xm[cc];
 #pragma unroll
             for (int r = 0; r < RPW; r++) {
-                const float q = chunk_qx<BITS>(W[u][r], xv, m, mk);
-                const float sv = __uint_as_float(SC[u][r] << 16), bv = __uint_as_float(BI[u][r] << 16);
-                const float nv = __builtin_fmaf(sv, q, __builtin_fmaf(bv, m.z, acc[r]));
+                float nv;
+                if constexpr (MX) {
+                    nv = __builtin_fmaf(mx_scale(SC[u][r]), chunk_mx<BITS>(W[u][r], xv, m), acc[r]);
+                } else {
+                    const float q = chunk_qx<BITS>(W[u][r], xv, m, mk);
+                    const float sv = __uint_as_float(SC[u][r] << 16), bv = __uint_as_float(BI[u][r] << 16);
+                    nv = __builtin_fmaf(sv, q, __builtin_fmaf(bv, m.z, acc[r]));
+                }
                 acc[r] = cok ? nv : acc[r];
             }
         }
@@ -187,12 +200,19 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
 template <int BITS, int RPW, int S>
 static bool launch_wv(const ValuShape& v, const QmvArgs& a, dim3 grid, size_t lds, hipStream_t st) {
     const bool g = a.tiles != nullptr;
+    if (a.mx) {                                   // dense only
+        if (g) return false;
+        if (v.WV == 4) qmv_valu_kernel<BITS, RPW, S, 4, false, true><<<grid, 256, lds, st>>>(a);
+        else if (v.WV == 8) qmv_valu_kernel<BITS, RPW, S, 8, false, true><<<grid, 512, lds, st>>>(a);
+        else return false;
+        return true;
+    }
     if (v.WV == 4) {
-        if (g) qmv_valu_kernel<BITS, RPW, S, 4, true><<<grid, 256, lds, st>>>(a);
-        else qmv_valu_kernel<BITS, RPW, S, 4, false><<<grid, 256, lds, st>>>(a);
+        if (g) qmv_valu_kernel<BITS, RPW, S, 4, true, false><<<grid, 256, lds, st>>>(a);
+        else qmv_valu_kernel<BITS, RPW, S, 4, false, false><<<grid, 256, lds, st>>>(a);
     } else if (v.WV == 8) {
-        if (g) qmv_valu_kernel<BITS, RPW, S, 8, true><<<grid, 512, lds, st>>>(a);
-        else qmv_valu_kernel<BITS, RPW, S, 8, false><<<grid, 512, lds, st>>>(a);
+        if (g) qmv_valu_kernel<BITS, RPW, S, 8, true, false><<<grid, 512, lds, st>>>(a);
+        else qmv_valu_kernel<BITS, RPW, S, 8, false, false><<<grid, 512, lds, st>>>(a);
     } else {
         return false;
     }

@@ -226,6 +226,8 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     Omitted group_size / bits take mlx's defaults for the mode."""
     _check_mode(mode, allow_mx=True)
     group_size, bits = _resolve(group_size, bits, mode)
+    if transpose and w.ndim == 2 and mode != "affine":
+        return _qmm_mx(x, w, scales, biases, group_size, bits, mode)
     if not transpose or w.ndim != 2 or bits not in (4, 8) or mode != "affine":
         return qmm_batched(x, w, scales, biases, transpose, group_size, bits, mode=mode)
     _check_affine_operands(x, w, scales, biases, group_size, bits, "quantized_matmul")
@@ -243,6 +245,36 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     _abi.check(L.kmi_qmm(_ptr(x2), M, K, N, _ptr(wc), _ptr(sc), _ptr(bc), DTYPE_CODE[x.dtype],
                          group_size, bits, _ptr(y), _ptr(ws), nbytes, _stream(x)),
                "quantized_matmul")
+    return y
+
+
+def _qmm_mx(x, w, scales, biases, group_size, bits, mode):
+    """Microscaled dense projection (kmi_qmm_mx): x [..., K] @ What[N, K]^T
+    with E2M1 / E4M3 codes and uint8 E8M0 scales [N, K/32]."""
+    what = "quantized_matmul"
+    _check_mx(what, scales, biases, group_size, bits, mode)
+    _on_gpu(x, w, scales)
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{what}: only bfloat16 activations are implemented")
+    if w.dtype not in (torch.uint32, torch.int32):
+        raise ValueError(f"{what}: w must be packed uint32")
+    K = x.shape[-1]
+    N = w.shape[0]
+    if K % 32 or w.shape[1] * 32 // bits != K or tuple(scales.shape) != (N, K // 32):
+        raise ValueError(f"{what}: x has {K} features; w {tuple(w.shape)} / scales "
+                         f"{tuple(scales.shape)} do not match a [{N}, {K}] {mode} weight")
+    x2 = x.contiguous()
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    M = x2.numel() // K if K else 0
+    y = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=x.device)
+    L = _lib()
+    code = 1 if mode == "mxfp4" else 2
+    nbytes = L.kmi_qmm_mx_workspace_bytes(M, K, N, code)
+    ws = _workspace(nbytes, x.device)
+    wc, sc = w.contiguous(), scales.contiguous()
+    _abi.check(L.kmi_qmm_mx(_ptr(x2), M, K, N, _ptr(wc), _ptr(sc), DTYPE_CODE[x.dtype], code, _ptr(y),
+                            _ptr(ws), nbytes, _stream(x)), what)
     return y
 
 

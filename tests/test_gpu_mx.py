@@ -92,6 +92,23 @@ def test_quantized_matmul_mx(dev, mode, transpose, M):
     assert_close(to_numpy(got), ref, what=f"{mode} transpose={transpose} M={M}")
 
 
+@pytest.mark.parametrize("mode", ["mxfp4", "mxfp8"])
+@pytest.mark.parametrize("M,K_,N", [(1, 4096, 200), (2, 512, 130), (5, 4096, 200), (9, 768, 64), (16, 4096, 72),
+                                    (16, 320, 200), (17, 512, 130), (40, 256, 96), (64, 1024, 64), (3, 96, 40)])
+def test_quantized_matmul_mx_decode_kernels(dev, mode, M, K_, N):
+    """kmi_qmm_mx's decode kernels (M = 1: the streaming GEMV; 2..16 rows
+    with K a multiple of 256: the direct-to-LDS kernel; other rows up to 64:
+    the MFMA GEMV; K not a multiple of 64: the batched kernel) against the
+    oracle, ragged N included."""
+    rng = np.random.default_rng(M * 100 + K_ + N + (mode == "mxfp8"))
+    h, g = _random_mx(rng, (N,), K_, mode, dev)
+    x = bf16_normal(rng, (M, K_))
+    got = K.quantized_matmul(to_torch(x, dev, BF), g[0], g[1], None, True, mode=mode)
+    assert got.shape == (M, N)
+    ref = O.mx_quantized_matmul(x, *h, mode, True, "float32")
+    assert_close(to_numpy(got), ref, what=f"{mode} M={M} K={K_} N={N}")
+
+
 def test_gather_with_a_bad_expert_gives_a_zero_row(dev):
     host, gpu = _fixture(dev)
     x = to_torch(bf16_normal(np.random.default_rng(3), (2, 1, 64)), dev, BF)
