@@ -196,10 +196,7 @@ __global__ __launch_bounds__(256) void dequantize_bytes_kernel(
 
 // mx.dequantize(mode="mxfp4" / "mxfp8"): E2M1 / E4M3 elements times the
 // E8M0 scale (2^(e - 127)) of their group of 32; one thread per packed word.
-__device__ __forceinline__ float mx_e8m0(uint32_t e) {
-    if (e == 255u) return __uint_as_float(0x7fc00000u);
-    return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
-}
+__device__ __forceinline__ float mx_e8m0(uint32_t e) { return e8m0_to_f32(e); }
 
 __device__ __forceinline__ float mx_elem(uint32_t c, int mode) {
     if (mode == 1) {                              // E2M1

@@ -42,6 +42,16 @@ void clear_error();
 
 // ---- bf16 / fp16 <-> fp32 (bit exact, round to nearest even) ----------------
 
+// E8M0 scale byte e -> 2^(e - 127) in fp32, without branches: e << 23 is
+// that float for e in 1..254; e = 0 (2^-127, the subnormal 0x00400000) and
+// e = 255 (NaN, 0x7fc00000) are e << 23 with bit 22 set, and exactly these
+// two values have (e + 1) & 0xfe == 0.
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+    e &= 0xffu;
+    const uint32_t special = ((((e + 1u) & 0xfeu) - 1u) >> 31) << 22;
+    return __uint_as_float((e << 23) | special);
+}
+
 __host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float(((uint32_t)h) << 16);
 }

@@ -59,11 +59,7 @@ __device__ __forceinline__ u32x4 x8_to_nibble_order(u32x4 v) {
 __device__ __forceinline__ float qg_bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 // E8M0 scale byte (held in a 16-bit LDS slot): 2^(e - 127); 255 is NaN
-__device__ __forceinline__ float mx_scale_qg(uint32_t e) {
-    e &= 0xffu;
-    if (e == 255u) return __uint_as_float(0x7fc00000u);
-    return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
-}
+__device__ __forceinline__ float mx_scale_qg(uint32_t e) { return e8m0_to_f32(e); }
 
 __device__ __forceinline__ float qg_f32_kept(double v) {
     float f = (float)v;

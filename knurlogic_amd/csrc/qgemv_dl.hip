@@ -9,11 +9,15 @@
 //   P[m, n, g] = sum_{k in g} x[m, k] q[n, k],   X[m, g] = sum_{k in g} x[m, k]
 //
 // A workgroup owns 64 weight rows (16 per wave: the n of
-// v_mfma_f32_16x16x32_bf16) and walks its share of K in chunks of 256 codes
-// through NS LDS stages, NS - 1 chunks in flight: the loads write LDS
-// directly, so the depth costs no registers, and the wait for a chunk is an
-// explicit vmcnt (the DMA loads return nothing to registers) followed by a
-// barrier.  The DMA writes a wave's 64 lanes as one contiguous 1 KB block, so
+// v_mfma_f32_16x16x32_bf16) and walks its share of K in chunks of 512 codes
+// (256 where K is not a multiple of 512) through 3 LDS stages, two chunks in
+// flight: the loads write LDS directly, so the depth costs no registers, and
+// the wait for a chunk is an explicit vmcnt (the DMA loads return nothing to
+// registers) followed by a barrier.  A 512-code chunk is two 256-code slices
+// worked by two sets of four waves (eight per workgroup, so two per SIMD to
+// hide each other's LDS and MFMA latencies), whose sums meet in the
+// epilogue; the E8M0 scales of the microscaled modes decode without
+// branches (e8m0_to_f32).  The DMA writes a wave's 64 lanes as one contiguous 1 KB block, so
 // the bank-conflict swizzles are applied on the global side: lane slot s of
 // a weight or x row holds the row's 16-byte piece s ^ (row & 7), and weight
 // blocks are padded by 16 bytes.  x is staged in its natural k order, so
@@ -30,9 +34,8 @@ namespace kmi {
 
 namespace {
 
-constexpr int DL_KC = 256;                // codes per chunk
+constexpr int DL_KC = 256;                // codes per chunk (least)
 constexpr int DL_ROWS = 64;               // weight rows per workgroup
-constexpr int DL_NS = 4;                  // LDS stages
 constexpr int DL_WBLK_BYTES = 1024 + 16;  // one DMA block of weight rows, padded
 constexpr uint32_t DL_NONE = 0x80000000u; // an offset past every buffer: reads 0
 
@@ -70,55 +73,66 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, unsigned char* ld
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KMI_LDSP(lds), 4, voff, soff, 0, 0);
 }
 
-// E8M0 scale byte: 2^(e - 127); 255 is NaN
-__device__ __forceinline__ float mx_scale_dl(uint32_t e) {
-    if (e == 255u) return __uint_as_float(0x7fc00000u);
-    return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
-}
-
+// A chunk is KS slices of 256 codes; the workgroup has 4 * KS waves, wave w
+// owning weight rows 16 (w % 4) .. + 15 of slice w / 4 of every chunk, and
+// the slices' partial sums are added in the epilogue (KS waves per SIMD,
+// without a second kernel).
 // MX: microscaled codes (E2M1 / E4M3, exact in bf16), one E8M0 byte scale
-// per 32 inputs and no biases.  A row's scales of one chunk are 8 bytes:
-// each wave moves its own 16 rows' in one 4-byte DMA block whose lanes
-// 32..63 read zeros into padding (256 bytes per wave).  The affine bf16
-// scales and biases move in 4-byte units, DPR blocks each.
-template <int BITS, int GS, bool MX>
+// per 32 inputs and no biases.  A row's scales of one chunk are GPC bytes:
+// each wave moves 16 / KS rows' (32 lanes of 4 bytes, the other 32 lanes
+// read zeros into padding: 256 bytes per wave).  The affine bf16 scales and
+// biases move in 4-byte units, DPR blocks each.
+template <int BITS, int GS, bool MX, int KS>
 struct DlShape {
-    static constexpr int RB = DL_KC * BITS / 8;          // weight bytes per row per chunk
+    static constexpr int KC = DL_KC * KS;               // codes per chunk
+    static constexpr int NW = 4 * KS;                    // waves
+    static constexpr int RB = KC * BITS / 8;             // weight bytes per row per chunk
     static constexpr int RPI = 1024 / RB;                // weight rows per DMA block
     static constexpr int WBLK = DL_ROWS / RPI;           // weight blocks per chunk
     static constexpr int PPR = RB / 16;                  // 16-byte pieces per weight row
     static constexpr int W_BYTES = WBLK * DL_WBLK_BYTES;
-    static constexpr int XI = 8;                         // x blocks per chunk: 2 rows of 512 bytes each
-    static constexpr int X_BYTES = 16 * DL_KC * 2;
-    static constexpr int GPC = DL_KC / GS;               // groups per chunk
+    static constexpr int XR = KC * 2;                    // x bytes per row per chunk
+    static constexpr int XPB = XR <= 1024 ? 1024 / XR : 1;   // x rows per DMA block
+    static constexpr int XBR = XR >= 1024 ? XR / 1024 : 1;   // DMA blocks per x row
+    static constexpr int XI = 16 * XBR / XPB;            // x blocks per chunk
+    static constexpr int X_BYTES = 16 * XR;
+    static constexpr int GPC = KC / GS;                  // groups per chunk
+    static constexpr int GPS = GPC / KS;                 // groups per slice
     static constexpr int SB = MX ? 1 : 2;                // bytes per scale
     static constexpr int DPR = MX ? 1 : GPC / 2;         // affine: 4-byte elements per row per chunk
-    static constexpr int SBI = MX ? 4 : 2 * DPR;         // scale (+ bias) blocks per chunk
-    static constexpr int SB_BYTES = MX ? 4 * 256 : 2 * DL_ROWS * GPC * 2;
+    static constexpr int SBI = MX ? NW : 2 * DPR;        // scale (+ bias) blocks per chunk
+    static constexpr int SB_BYTES = MX ? NW * 256 : 2 * DL_ROWS * GPC * 2;
+    static constexpr int MXL = GPC / 4;                  // MX: lanes per row
+    static constexpr int MXR = 32 / MXL;                 // MX: rows per block
     static constexpr int STAGE = W_BYTES + X_BYTES + SB_BYTES;
-    static constexpr int PER_WAVE = WBLK / 4 + XI / 4 + SBI / 4;   // DMA loads per wave per chunk
+    static constexpr int PER_WAVE = (WBLK + XI + SBI) / NW;   // DMA loads per wave per chunk
     static constexpr int GB = GS * BITS / 8;             // bytes per row per group
     static constexpr int LB = GB / 4;                    // bytes of a group per lane (k run)
     static constexpr int NT = GS / 32;                   // MFMAs per group
-    static_assert(WBLK % 4 == 0 && XI % 4 == 0 && SBI % 4 == 0, "every wave issues the same loads");
+    static_assert(WBLK % NW == 0 && XI % NW == 0 && SBI % NW == 0, "every wave issues the same loads");
     static_assert(LB == 4 || LB == 8 || LB == 16, "lane run of 4, 8 or 16 bytes");
-    static_assert(!MX || GPC == 8, "MX scales: 8 bytes per row and chunk");
+    static_assert(!MX || MXR * NW == DL_ROWS, "MX: one scale block per wave");
+    static_assert(XR == 512 || XR % 1024 == 0, "x rows of 512 bytes or whole 1 KB blocks");
+    static_assert(GPS >= 1 && GPS % (GPS < 4 ? GPS : 4) == 0, "whole group batches per slice");
 };
 
 }  // namespace
 
-template <int BITS, int GS, bool MX>
-__global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
-    using S_ = DlShape<BITS, GS, MX>;
+template <int BITS, int GS, bool MX, int NS, int KS>
+__global__ __launch_bounds__(256 * KS) void qgemv_dl_kernel(QgArgs a) {
+    using S_ = DlShape<BITS, GS, MX, KS>;
+    constexpr int KC = S_::KC, NW = S_::NW, XPB = S_::XPB, XBR = S_::XBR, XI = S_::XI, MXR = S_::MXR;
+    constexpr int MXL = S_::MXL;
     constexpr int SB = S_::SB;
     constexpr int RB = S_::RB, RPI = S_::RPI, WBLK = S_::WBLK, PPR = S_::PPR, W_BYTES = S_::W_BYTES;
-    constexpr int X_BYTES = S_::X_BYTES, GPC = S_::GPC, DPR = S_::DPR, SBI = S_::SBI, STAGE = S_::STAGE;
-    constexpr int GB = S_::GB, LB = S_::LB, NT = S_::NT;
+    constexpr int X_BYTES = S_::X_BYTES, GPC = S_::GPC, GPS = S_::GPS, DPR = S_::DPR, SBI = S_::SBI;
+    constexpr int STAGE = S_::STAGE, GB = S_::GB, LB = S_::LB, NT = S_::NT;
     constexpr int PER_WAVE = S_::PER_WAVE;
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rw4 = wave & 3, slice = wave >> 2;         // row block and K slice of this wave
     const int64_t n0 = (int64_t)blockIdx.x * DL_ROWS;
     const int64_t K = a.K, G = K / GS, M = a.rows;
     const uint32_t rowbytes = (uint32_t)(K * BITS / 8);
@@ -126,34 +140,36 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.s, a.N * G * SB);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.b, MX ? 0 : a.N * G * SB);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, M * K * 2);
-    const int chunks = (int)(K / DL_KC);
+    const int chunks = (int)(K / KC);
     const int c0 = (int)blockIdx.y * a.gps;
     const int nc = chunks - c0 < a.gps ? chunks - c0 : a.gps;
 
     // per-lane parts of the DMA offsets (rows past N / past M read zeros)
-    uint32_t wv[WBLK / 4];
+    uint32_t wv[WBLK / NW];
 #pragma unroll
-    for (int j = 0; j < WBLK / 4; j++) {
-        const int r = (wave + 4 * j) * RPI + lane / PPR, slot = lane % PPR;
+    for (int j = 0; j < WBLK / NW; j++) {
+        const int r = (wave + NW * j) * RPI + lane / PPR, slot = lane % PPR;
         wv[j] = n0 + r < a.N ? (uint32_t)(n0 + r) * rowbytes + 16u * (uint32_t)(slot ^ (r & 7)) : DL_NONE;
     }
-    uint32_t xv[2];
+    uint32_t xv[XI / NW];
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int m = 2 * (wave + 4 * j) + lane / 32, slot = lane % 32;
+    for (int j = 0; j < XI / NW; j++) {
+        const int b = wave + NW * j;                     // block b: x row b / XBR (XPB rows per block)
+        const int m = XPB * (b / XBR) + lane / (64 / XPB), slot = (b % XBR) * 64 + lane % (64 / XPB);
         xv[j] = m < M ? (uint32_t)(m * K * 2) + 16u * (uint32_t)(slot ^ (m & 7)) : DL_NONE;
     }
-    uint32_t sbv[SBI / 4];
-    int sbo[SBI / 4], sbw[SBI / 4];
+    uint32_t sbv[SBI / NW];
+    int sbo[SBI / NW], sbw[SBI / NW];
 #pragma unroll
-    for (int j = 0; j < SBI / 4; j++) {
+    for (int j = 0; j < SBI / NW; j++) {
         if constexpr (MX) {
-            const int row = wave * 16 + (lane >> 1);
-            sbv[j] = lane < 32 && n0 + row < a.N ? (uint32_t)((n0 + row) * G) + 4u * (uint32_t)(lane & 1) : DL_NONE;
+            const int row = wave * MXR + lane / MXL;
+            sbv[j] = lane < 32 && n0 + row < a.N ? (uint32_t)((n0 + row) * G) + 4u * (uint32_t)(lane % MXL)
+                                                 : DL_NONE;
             sbo[j] = wave * 256;
             sbw[j] = 0;
         } else {
-            const int q = wave + 4 * j, which = q / DPR, d = q % DPR;
+            const int q = wave + NW * j, which = q / DPR, d = q % DPR;
             const int row = d * (DL_ROWS / DPR) + lane / DPR;
             sbv[j] = n0 + row < a.N ? (uint32_t)((n0 + row) * G * 2) + 4u * (uint32_t)(lane % DPR) : DL_NONE;
             sbo[j] = which * (DL_ROWS * GPC * 2) + d * 256;
@@ -166,40 +182,42 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
     auto issue = [&](int i) {
         const bool live = i < nc;
         const uint32_t c = (uint32_t)(c0 + (live ? i : 0));
-        unsigned char* base = smem + (i % DL_NS) * STAGE;
+        unsigned char* base = smem + (i % NS) * STAGE;
 #pragma unroll
-        for (int j = 0; j < WBLK / 4; j++)
-            dma16(rw, base + (wave + 4 * j) * DL_WBLK_BYTES, live ? wv[j] : DL_NONE, c * RB, 1);
+        for (int j = 0; j < WBLK / NW; j++)
+            dma16(rw, base + (wave + NW * j) * DL_WBLK_BYTES, live ? wv[j] : DL_NONE, c * RB, 1);
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-            dma16(rx, base + W_BYTES + (wave + 4 * j) * 1024, live ? xv[j] : DL_NONE, c * (DL_KC * 2), 0);
+        for (int j = 0; j < XI / NW; j++)
+            dma16(rx, base + W_BYTES + (wave + NW * j) * 1024, live ? xv[j] : DL_NONE, c * (KC * 2), 0);
 #pragma unroll
-        for (int j = 0; j < SBI / 4; j++)
+        for (int j = 0; j < SBI / NW; j++)
             dma4(sbw[j] ? rb : rs, base + W_BYTES + X_BYTES + sbo[j], live ? sbv[j] : DL_NONE, c * (GPC * SB));
     };
 #pragma unroll
-    for (int i = 0; i < DL_NS - 1; i++) issue(i);
+    for (int i = 0; i < NS - 1; i++) issue(i);
 
     const int nl = lane & 15, j4 = lane >> 4;
-    const int wr = wave * 16 + nl;                       // this lane's weight row in the tile
+    const int wr = rw4 * 16 + nl;                        // this lane's weight row in the tile
+    const int g0 = slice * GPS;                          // this wave's first group of a chunk
+    const int sro = MX ? (wr / MXR) * 256 + (wr % MXR) * GPC : wr * GPC;   // row's scales in the stage
     const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int i = 0; i < nc; i++) {
-        wait_vmcnt<PER_WAVE * (DL_NS - 2)>();            // this wave's loads of chunk i are in LDS
+        wait_vmcnt<PER_WAVE * (NS - 2)>();               // this wave's loads of chunk i are in LDS
         __builtin_amdgcn_s_barrier();                    // and every wave's
-        const unsigned char* base = smem + (i % DL_NS) * STAGE;
+        const unsigned char* base = smem + (i % NS) * STAGE;
         const unsigned char* wl = base + (wr / RPI) * DL_WBLK_BYTES + (wr % RPI) * RB;
-        const unsigned char* xl = base + W_BYTES + nl * (DL_KC * 2);
-        const uint16_t* sl = (const uint16_t*)(base + W_BYTES + X_BYTES);
+        const unsigned char* xl = base + W_BYTES + nl * (KC * 2);
+        const unsigned char* sl = base + W_BYTES + X_BYTES;
+        constexpr int GH = GPS < 4 ? GPS : 4;
 #pragma unroll
-        for (int h = 0; h < GPC; h += 4) {
-            constexpr int GH = GPC < 4 ? GPC : 4;
+        for (int h = 0; h < GPS; h += GH) {
             u32x4 wd[GH];
             u32x4 A[GH][NT];
             float sc[GH], bi[GH];
 #pragma unroll
             for (int g = 0; g < GH; g++) {
-                const int gi = h + g;
+                const int gi = g0 + h + g;
                 const int off = gi * GB + j4 * LB;
                 const unsigned char* p = wl + 16 * ((off / 16) ^ (wr & 7)) + off % 16;
                 if constexpr (LB == 4) wd[g] = u32x4{*(const uint32_t*)p, 0u, 0u, 0u};
@@ -213,11 +231,11 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
                     A[g][t] = *(const u32x4*)(xl + 16 * (xp ^ (nl & 7)));
                 }
                 if constexpr (MX) {
-                    sc[g] = mx_scale_dl(((const uint8_t*)sl)[wave * 256 + nl * 8 + gi]);
+                    sc[g] = e8m0_to_f32(sl[sro + gi]);
                     bi[g] = 0.f;
                 } else {
-                    sc[g] = bf16_to_f32(sl[wr * GPC + gi]);
-                    bi[g] = bf16_to_f32(sl[DL_ROWS * GPC + wr * GPC + gi]);
+                    sc[g] = bf16_to_f32(((const uint16_t*)sl)[sro + gi]);
+                    bi[g] = bf16_to_f32(((const uint16_t*)sl)[DL_ROWS * GPC + sro + gi]);
                 }
             }
             f32x4 P[GH], X[GH];
@@ -259,9 +277,25 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
                     acc[e] = MX ? __builtin_fmaf(sc[g], P[g][e], acc[e])
                                 : __builtin_fmaf(sc[g], P[g][e], __builtin_fmaf(bi[g], X[g][e], acc[e]));
         }
-        issue(i + DL_NS - 1);
+        issue(i + NS - 1);
     }
     wait_vmcnt<0>();                                     // no LDS write may land after the workgroup ends
+
+    if constexpr (KS > 1) {
+        // slices 1.. hand their sums to slice 0 through LDS (the stages are
+        // free once every wave is past its last chunk), added in slice order
+        __syncthreads();
+        f32x4* red = (f32x4*)smem;
+        if (slice > 0) red[((slice - 1) * 4 + rw4) * 64 + lane] = acc;
+        __syncthreads();
+        if (slice > 0) return;
+#pragma unroll
+        for (int s = 1; s < KS; s++) {
+            const f32x4 v = red[((s - 1) * 4 + rw4) * 64 + lane];
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] += v[e];
+        }
+    }
 
     // D of the MFMA: item e is x row 4 * j4 + e, column nl (weight row wr)
     const int64_t n = n0 + wr;
@@ -279,18 +313,34 @@ __global__ __launch_bounds__(256) void qgemv_dl_kernel(QgArgs a) {
 
 namespace {
 
+template <int BITS, int GS, bool MX, int NS, int KS>
+int launch_dl_ns(const QgArgs& a, dim3 grid, hipStream_t st) {
+    constexpr size_t lds = (size_t)NS * DlShape<BITS, GS, MX, KS>::STAGE;
+    if constexpr (lds > 160 * 1024) {
+        set_error("qgemv_dl: %d stages of %d slices exceed the LDS", NS, KS);
+        return EINVAL_ARG;
+    } else {
+        static bool attr = false;
+        if (!attr) {
+            (void)hipFuncSetAttribute((const void*)qgemv_dl_kernel<BITS, GS, MX, NS, KS>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            attr = true;
+        }
+        qgemv_dl_kernel<BITS, GS, MX, NS, KS><<<grid, 256 * KS, lds, st>>>(a);
+        return OK;
+    }
+}
+
+// two K slices (8 waves, two per SIMD) wherever K holds whole 512-code chunks;
+// three stages (two chunks in flight) fit the LDS at either width
+constexpr int DL_NS = 3;
+
+int dl_ks(int64_t K) { return K % (2 * DL_KC) == 0 ? 2 : 1; }
+
 template <int BITS, int GS, bool MX>
 int launch_dl(const QgArgs& a, dim3 grid, hipStream_t st) {
-    constexpr size_t lds = (size_t)DL_NS * DlShape<BITS, GS, MX>::STAGE;
-    static_assert(lds <= 160 * 1024, "qgemv_dl stages exceed the LDS");
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute((const void*)qgemv_dl_kernel<BITS, GS, MX>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds);
-        attr = true;
-    }
-    qgemv_dl_kernel<BITS, GS, MX><<<grid, 256, lds, st>>>(a);
-    return OK;
+    if (dl_ks(a.K) == 2) return launch_dl_ns<BITS, GS, MX, DL_NS, 2>(a, grid, st);
+    return launch_dl_ns<BITS, GS, MX, DL_NS, 1>(a, grid, st);
 }
 
 }  // namespace
@@ -302,7 +352,7 @@ bool qgemv_dl_supported(int64_t M, int64_t K, int bits, int gs) {
 // K splits so the grid reaches about one workgroup per CU, each split
 // keeping at least 4 chunks
 QgPlan plan_qgemv_dl(int64_t N, int64_t K) {
-    const int64_t tiles = ceil_div(N, DL_ROWS), chunks = K / DL_KC;
+    const int64_t tiles = ceil_div(N, DL_ROWS), chunks = K / (DL_KC * dl_ks(K));
     int64_t S = 1;
     while (tiles * S * 2 <= 256 && chunks / (S * 2) >= 4) S *= 2;
     QgPlan p = {};

@@ -59,10 +59,7 @@ struct QbArgs {
 // OCP microscaling element and scale encodings (mxfp4: E2M1 elements,
 // mxfp8: E4M3, both with an E8M0 power-of-two scale per 32 elements), built
 // from their bit fields; every value is exact in fp32 (and in bf16).
-__device__ __forceinline__ float qb_e8m0(uint32_t e) {
-    if (e == 255u) return __uint_as_float(0x7fc00000u);
-    return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);     // 2^(e - 127)
-}
+__device__ __forceinline__ float qb_e8m0(uint32_t e) { return e8m0_to_f32(e); }     // 2^(e - 127)
 
 __device__ __forceinline__ float qb_e2m1(uint32_t c) {
     const uint32_t e = (c >> 1) & 3u, m = c & 1u;

@@ -235,11 +235,7 @@ __device__ __forceinline__ float chunk_mx(const u32x4& W, const u32x4* xv, const
 }
 
 // E8M0 scale byte: 2^(e - 127); 255 is NaN
-__device__ __forceinline__ float mx_scale(uint32_t e) {
-    e &= 0xffu;
-    if (e == 255u) return __uint_as_float(0x7fc00000u);
-    return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u);
-}
+__device__ __forceinline__ float mx_scale(uint32_t e) { return e8m0_to_f32(e); }
 
 // The masks and the 1024.0 pair held in VGPRs (see vconst).
 struct Magic16 {
