@@ -325,16 +325,20 @@ def bench_vq(T, kc, cold, calls, dev):
             "bytes": nbytes, "flops": 2.0 * T * k * 3 * H * I}
 
 
-def bench_vq_packed(T, calls, dev, dim=4, kc=2048, group=64):
-    """VQ experts in the artifacts' packed layout at the Qwen3.5-MoE shape:
-    11-bit fields (2048-entry codebook) of dim-4 vectors, per-group fp16
-    scales (64 inputs); router, gate/up + SwiGLU (one launch), down, weighted
-    combine.  Expert sets rotated past 1 GB.  Bytes: every routed expert's
-    packed words and scales once, the codebook, x and out."""
+def bench_vq_packed(T, calls, dev, dim=4, kc=2048, group=64, H=None, I=None):
+    """VQ experts in the artifacts' packed layout, by default at the
+    Qwen3.5-MoE shape: 11-bit fields (2048-entry codebook) of dim-4 vectors,
+    per-group fp16 scales (64 inputs); router, gate/up + SwiGLU (one launch),
+    down, weighted combine.  H / I / dim override the shape (the shipped
+    Gemma-4 26B artifact: 128 experts, 2816 -> 704, dim-2 vectors).  Expert
+    sets rotated past 1 GB.  Bytes: every routed expert's packed words and
+    scales once, the codebook, x and out."""
     import torch
     import knurlogic_amd as KA
     from knurlogic_amd import nn
-    E, k, H, I = MOE["E"], MOE["k"], MOE["H"], MOE["I"]
+    E, k = MOE["E"], MOE["k"]
+    H = MOE["H"] if H is None else H
+    I = MOE["I"] if I is None else I
     bits = (kc - 1).bit_length()
 
     def mat_bytes(N, K):
@@ -368,7 +372,7 @@ def bench_vq_packed(T, calls, dev, dim=4, kc=2048, group=64):
     gbs = nbytes / (us * 1e-6) / 1e9
     del glus
     torch.cuda.empty_cache()
-    return {"op": "vq_packed_moe_experts", "T": T, "codebook": f"{kc}x{dim} fp16", "field_bits": bits,
+    return {"op": "vq_packed_moe_experts", "T": T, "H": H, "I": I, "codebook": f"{kc}x{dim} fp16", "field_bits": bits,
             "experts_routed": distinct, "cache": "cold", "us": round(us, 3), "GBps": round(gbs, 1),
             "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm", "bytes": nbytes,
             "flops": 2.0 * T * k * 3 * H * I}
@@ -631,6 +635,8 @@ def main():
     if not args.quick and "vq" in only:
         for t_ in (1, 16):
             detail.append(bench_vq_packed(t_, 50, dev))
+        for t_ in (1, 16):      # the shipped Gemma-4 26B VQ artifact's expert shape
+            detail.append(bench_vq_packed(t_, 50, dev, dim=2, H=2816, I=704))
     if not args.quick and "moe" in only:
         for t_ in (1, 16):
             detail.append(bench_mx_moe(t_, 30, dev))

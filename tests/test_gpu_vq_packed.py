@@ -86,6 +86,48 @@ def test_packed_switch_glu_matches_the_oracle(dev, T, E, H, I, k):
     assert y.shape == (T * k, 1, H)
 
 
+@pytest.mark.parametrize("T", [1, 4])
+def test_packed_switch_glu_at_the_shipped_artifact_shape(dev, T):
+    """The expert layout the reference's Gemma-4 26B VQ artifact declares
+    (tests/support/artifacts/gemma-4-26b-a4b-it-VQ-6.2bpw/config.json,
+    vq_modules: 128 experts, gate/up 2816 -> 704, down 704 -> 2816, a
+    2048 x 2 codebook, 11-bit fields, scales per 64 inputs), top-8, full
+    size: random 11-bit fields (every value is a codebook entry), SwitchGLU
+    and its weighted combine against the oracle on the routed experts."""
+    E, H, I, k, dim, kc, bits, group = 128, 2816, 704, 8, 2, 2048, 11, 64
+    rng = np.random.default_rng(20 + T)
+    g = torch.Generator(device=dev).manual_seed(20 + T)
+    cb = (rng.standard_normal((kc, dim)) * 0.3).astype(np.float16)
+    tcb = torch.from_numpy(cb).to(dev)
+
+    def mat(N, IN):
+        W = (IN // dim + 31) // 32 * bits
+        words = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, N, W), device=dev, generator=g,
+                              dtype=torch.int32).view(torch.uint32)
+        sc = (torch.rand(E, N, IN // group, device=dev, generator=g) + 0.5).to(torch.float16)
+        return words, sc
+
+    mats = [mat(I, H), mat(I, H), mat(H, I)]
+    mods = [nn.VQSwitchLinear(w, tcb, sc, scale_group=group, pack_bits=bits, in_features=IN)
+            for (w, sc), IN in zip(mats, (H, H, I))]
+    glu = nn.VQSwitchGLU(*mods)
+    x = bf16_normal(rng, (T, H))
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    used = sorted(set(inds.reshape(-1).tolist()))
+    host = [{e: (w[e].view(torch.int32).cpu().numpy().view(np.uint32), sc[e].float().cpu().numpy())
+             for e in used} for w, sc in mats]
+    cbf = cb.astype(np.float32)
+    fn = lambda h: (lambda xs, e: O.vq_packed_matmul(xs, h[e][0], cbf, h[e][1], bits, group, "bfloat16"))
+    ref = O.switch_glu(x, inds, *(fn(h) for h in host))
+    tx, ti = to_torch(x, dev, BF), torch.from_numpy(inds).to(dev)
+    got = glu(tx, ti)
+    assert got.shape == (T, k, H)
+    assert_close(to_numpy(got), ref, what=f"artifact-shape packed vq switch_glu T={T}")
+    _, scores = O.route(bf16_normal(rng, (T, E)), k)
+    comb = glu.combine(tx, ti, to_torch(scores, dev, BF))
+    assert_close(to_numpy(comb), O.combine(ref, scores), what="artifact-shape packed combine")
+
+
 def test_packed_errors(dev):
     rng = np.random.default_rng(9)
     _, gpu = _packed(rng, 2, 8, 128, 4, 2048, 11, 64, dev)
