@@ -385,7 +385,7 @@ size_t kmi_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k, in
  * mode 2 mxfp8 (E4M3, 4 per uint32), one uint8 E8M0 scale per 32 inputs,
  * no biases.  w_gu [E, 2I, H*bits/32] and s_gu [E, 2I, H/32] stack gate
  * (rows 0..I-1) and up; w_down [E, H, I*bits/32], s_down [E, H, I/32].
- * Up to 16 (token, slot) pairs run token-major, more grouped by expert,
+ * Up to 64 (token, slot) pairs run token-major, more grouped by expert,
  * as kmi_switch_glu (workspace: kmi_switch_glu_workspace_bytes with group
  * 32).
  */

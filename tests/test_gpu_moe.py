@@ -98,10 +98,11 @@ def _experts(rng, E, H, I, dev, bits=4):
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("T,E,H,I,k", [(1, 16, 256, 128, 4), (5, 16, 256, 128, 4), (64, 16, 256, 128, 4),
                                        (100, 16, 256, 128, 4), (1, 128, 2048, 768, 8),
+                                       (8, 128, 2048, 768, 8), (9, 128, 2048, 768, 8),
                                        (16, 128, 2048, 768, 8), (40, 128, 2048, 768, 8),
                                        (256, 128, 2048, 768, 8)])
 def test_switch_glu_matches_the_oracle(dev, T, E, H, I, k, bits):
-    """One library call (token-major up to 16 (token, slot) pairs, grouped by
+    """One library call (token-major up to 64 (token, slot) pairs, grouped by
     expert above), the separate gather_qmm path, and the fused combine."""
     rng = np.random.default_rng(T * 7 + E + bits)
     glu, fns = _experts(rng, E, H, I, dev, bits)
@@ -166,7 +167,7 @@ def test_sparse_moe_block_matches_the_oracle(dev, T):
     assert_close(to_numpy(block.experts(to_torch(x, dev, BF), tl)), y, what="experts")
 
 
-@pytest.mark.parametrize("T", [1, 2, 5, 16])
+@pytest.mark.parametrize("T", [1, 2, 5, 8, 9, 16])
 def test_moe_experts_routes_in_the_kernel_like_the_router(dev, T):
     """kmi_moe_experts (one call from the router logits): at decode sizes
     the gate/up kernel routes each token itself.  The experts and scores
