@@ -160,8 +160,12 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
     d.sorted = sr.sorted; d.lhs = nullptr; d.lhs_div = 1; d.Mper = 1;
     const QgPlan pd = plan_qgemv_unsplit(H, I, sr.max_tiles, p.tm, group_size);
     d.S = 1; d.gps = pd.gps;
-    rc = launch_qgemv(d, pd, bits, group_size, false, sr.max_tiles, st);
-    if (rc) return rc;
+    // the down projection stages each tile's act rows once (qgemv_xs) where
+    // they fit; the gate|up x rows (H wide) take qgemv
+    if (launch_qgemv_xs(d, bits, group_size, false, pd.mc, sr.max_tiles, st) != 0) {
+        rc = launch_qgemv(d, pd, bits, group_size, false, sr.max_tiles, st);
+        if (rc) return rc;
+    }
     KMI_CHECK_LAUNCH("qgemv(down)");
     if (scores) return kmi_moe_combine(y, scores, dtype, T, k, H, out, stream);
     return OK;

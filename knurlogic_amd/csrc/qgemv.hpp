@@ -77,4 +77,9 @@ bool qgemv_dl_supported(int64_t M, int64_t K, int bits, int gs);
 QgPlan plan_qgemv_dl(int64_t N, int64_t K);
 int launch_qgemv_dl(const QgArgs& a, const QgPlan& p, int bits, int gs, hipStream_t st);
 
+// Rows grouped by expert with the tile's x rows staged once and G column
+// blocks per workgroup (qgemv_xs.hip): 0 when launched, 1 when the shape
+// does not fit that kernel (K not a multiple of 256, x tile past the LDS).
+int launch_qgemv_xs(const QgArgs& a, int bits, int gs, bool glu, int mc, int64_t ntiles, hipStream_t st);
+
 }  // namespace kmi

@@ -260,7 +260,10 @@ static size_t skinny_partial_bytes(const QgPlan& p, int64_t rows, int64_t N) {
 static int run_skinny(QgArgs& a, const QgPlan& p, int bits, int gs, int64_t ntiles, void* partial,
                       const int32_t* rhs, int64_t Mper, bool dl, hipStream_t st) {
     a.S = p.S; a.gps = p.gps; a.partial = (float*)partial;
-    int rc = dl ? launch_qgemv_dl(a, p, bits, gs, st) : launch_qgemv(a, p, bits, gs, false, ntiles, st);
+    int rc;
+    if (dl) rc = launch_qgemv_dl(a, p, bits, gs, st);
+    else if (a.tiles && p.S == 1 && launch_qgemv_xs(a, bits, gs, false, p.mc, ntiles, st) == 0) rc = OK;
+    else rc = launch_qgemv(a, p, bits, gs, false, ntiles, st);
     if (rc) return rc;
     KMI_CHECK_LAUNCH(dl ? "qgemv_dl" : "qgemv");
     if (p.S > 1) {
