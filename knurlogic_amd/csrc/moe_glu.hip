@@ -52,7 +52,10 @@ static GluPlan plan_glu(int64_t T, int64_t H, int64_t I, int k, int64_t E) {
     if (!p.tok) {
         const int64_t active = P < E ? P : E;
         const int64_t rpt = ceil_div(P, active);
-        p.tm = qgemv_gather_tile_rows(rpt);
+        // at one or two rows per active expert, 4-row tiles: both projections
+        // then stage their x rows once per workgroup (qgemv_xs) with two
+        // workgroups per CU
+        p.tm = rpt <= 2 ? 4 : qgemv_gather_tile_rows(rpt);
         p.y = align256((size_t)P * H * 2);
         p.idx = sort_index_bytes(P, E, p.tm);
     }
@@ -151,8 +154,10 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
     g.lhs_div = k; g.Mper = 1;
     const QgPlan pg = plan_qgemv_unsplit(I, H, sr.max_tiles, p.tm, group_size);
     g.S = 1; g.gps = pg.gps;
-    rc = launch_qgemv(g, pg, bits, group_size, true, sr.max_tiles, st);
-    if (rc) return rc;
+    if (p.tm != 4 || launch_qgemv_xs(g, bits, group_size, true, p.tm, sr.max_tiles, st) != 0) {
+        rc = launch_qgemv(g, pg, bits, group_size, true, sr.max_tiles, st);
+        if (rc) return rc;
+    }
     KMI_CHECK_LAUNCH("qgemv(gate|up)");
     QgArgs d = {};
     d.x = act; d.xrows = P; d.w = w_down; d.s = (const uint16_t*)s_down; d.b = (const uint16_t*)b_down;
@@ -161,8 +166,8 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
     const QgPlan pd = plan_qgemv_unsplit(H, I, sr.max_tiles, p.tm, group_size);
     d.S = 1; d.gps = pd.gps;
     // the down projection stages each tile's act rows once (qgemv_xs) where
-    // they fit; the gate|up x rows (H wide) take qgemv
-    if (launch_qgemv_xs(d, bits, group_size, false, pd.mc, sr.max_tiles, st) != 0) {
+    // they fit
+    if (launch_qgemv_xs(d, bits, group_size, false, p.tm, sr.max_tiles, st) != 0) {
         rc = launch_qgemv(d, pd, bits, group_size, false, sr.max_tiles, st);
         if (rc) return rc;
     }

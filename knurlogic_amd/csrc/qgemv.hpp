@@ -80,6 +80,7 @@ int launch_qgemv_dl(const QgArgs& a, const QgPlan& p, int bits, int gs, hipStrea
 // Rows grouped by expert with the tile's x rows staged once and G column
 // blocks per workgroup (qgemv_xs.hip): 0 when launched, 1 when the shape
 // does not fit that kernel (K not a multiple of 256, x tile past the LDS).
-int launch_qgemv_xs(const QgArgs& a, int bits, int gs, bool glu, int mc, int64_t ntiles, hipStream_t st);
+// tile_rows: rows per tile of the sort (4, 16, 32 or 64).
+int launch_qgemv_xs(const QgArgs& a, int bits, int gs, bool glu, int tile_rows, int64_t ntiles, hipStream_t st);
 
 }  // namespace kmi

@@ -8,7 +8,7 @@
 //   y[m, n] = sum_g ( s[n, g] * P[m, n, g] + b[n, g] * X[m, g] )
 //   P[m, n, g] = sum_{k in g} x[m, k] q[n, k],   X[m, g] = sum_{k in g} x[m, k]
 //
-// A workgroup owns one tile (expert e, up to 16*MC of its rows) and G
+// A workgroup owns one tile (expert e, up to XR of its rows) and G
 // consecutive 64-row column blocks of e's weight.  Its x rows (K bf16 each,
 // every row padded by 16 bytes so the 16 rows of an MFMA fragment read
 // different banks) are loaded into LDS once by direct-to-LDS loads; the
@@ -49,8 +49,10 @@ __device__ __forceinline__ float xs_f32_kept(double v) {
 }  // namespace
 
 // xrow: LDS bytes per staged x row (K * 2 + 16); xbytes: the x region (a
-// multiple of 1 KB, at least 16*MC rows); G: column blocks per workgroup.
-template <int BITS, int GS, bool MX, int MC, int NSET, int NS>
+// multiple of 1 KB, at least XR rows); G: column blocks per workgroup.  XR:
+// the tile's rows (4, 16, 32 or 64); a 4-row tile feeds the 16-row MFMA
+// fragments with its rows repeated (the extra outputs are never written).
+template <int BITS, int GS, bool MX, int XR, int NSET, int NS>
 __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t xrow, uint32_t xbytes) {
     using D = DlShape<BITS, GS, MX, 1>;
     using XS = XsShape<BITS, GS, MX, NSET>;
@@ -58,7 +60,7 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
     constexpr int GPC = D::GPC, DPR = D::DPR, SBI = D::SBI, SB = D::SB, MXR = D::MXR, MXL = D::MXL;
     constexpr int GB = D::GB, LB = D::LB, NT = D::NT;
     constexpr int SET = XS::SET, STAGE = XS::STAGE, PER_WAVE = XS::PER_WAVE;
-    constexpr int MT = 16 * MC;
+    constexpr int MT = XR, MC = XR < 16 ? 1 : XR / 16;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int32_t rid_s[MT];        // output row of tile row m (-1: none)
     __shared__ uint32_t xro_s[MT];       // byte offset of tile row m's x row (DL_NONE: none)
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
     const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
     const unsigned char* xl[MC];
 #pragma unroll
-    for (int cc = 0; cc < MC; cc++) xl[cc] = smem + (uint32_t)(16 * cc + nl) * xrow;
+    for (int cc = 0; cc < MC; cc++) xl[cc] = smem + (uint32_t)(16 * cc + (XR < 16 ? nl % XR : nl)) * xrow;
     f32x4 acc[NSET][MC];
 #pragma unroll
     for (int set = 0; set < NSET; set++)
@@ -315,9 +317,10 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
 
 namespace {
 
-// column blocks per workgroup: 4 (measured best at 128 experts x 2048
-// outputs from 16 to 256 tokens, top-8), fewer while the grid would have
-// under 512 workgroups (KMI_XS_G overrides: tuning; read once)
+// column blocks per workgroup: 4, fewer while the grid would have under
+// 1024 workgroups (measured at 128 experts, top-8, 2048 -> 768 -> 2048:
+// down takes 4 from 16 to 256 tokens, gate|up 2 at 16 tokens)
+// (KMI_XS_G overrides: tuning; read once)
 int xs_blocks_per_wg(int64_t NB, int64_t tiles) {
     static int ov = [] {
         const char* e = getenv("KMI_XS_G");
@@ -325,7 +328,7 @@ int xs_blocks_per_wg(int64_t NB, int64_t tiles) {
     }();
     if (ov > 0) return ov < NB ? ov : (int)NB;
     int64_t g = NB < 4 ? NB : 4;
-    while (g > 1 && ceil_div(NB, g) * tiles < 512) g--;
+    while (g > 1 && ceil_div(NB, g) * tiles < 1024) g--;
     return (int)g;
 }
 
@@ -340,66 +343,68 @@ bool xs_enabled() {
 
 constexpr size_t XS_LDS_MAX = 160 * 1024 - 1024;   // the static row tables stay below 1 KB
 
-template <int BITS, int GS, bool MX, int MC, int NSET, int NS>
+template <int BITS, int GS, bool MX, int XR, int NSET, int NS>
 int launch_xs_one(const QgArgs& a, int64_t ntiles, uint32_t xrow, uint32_t xbytes, hipStream_t st) {
     constexpr size_t stage = XsShape<BITS, GS, MX, NSET>::STAGE;
     const size_t lds = (size_t)xbytes + NS * stage;
     if (lds > XS_LDS_MAX) return 1;
     static bool attr = false;
     if (!attr) {
-        (void)hipFuncSetAttribute((const void*)qgemv_xs_kernel<BITS, GS, MX, MC, NSET, NS>,
+        (void)hipFuncSetAttribute((const void*)qgemv_xs_kernel<BITS, GS, MX, XR, NSET, NS>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)XS_LDS_MAX);
         attr = true;
     }
     const int64_t NB = (a.N + 63) / 64;
     const int G = xs_blocks_per_wg(NB, ntiles);
     const dim3 grid((unsigned)ceil_div(NB, G), 1, (unsigned)ntiles);
-    qgemv_xs_kernel<BITS, GS, MX, MC, NSET, NS><<<grid, 256, lds, st>>>(a, G, xrow, xbytes);
+    qgemv_xs_kernel<BITS, GS, MX, XR, NSET, NS><<<grid, 256, lds, st>>>(a, G, xrow, xbytes);
     return 0;
 }
 
 // stages: 4 where two workgroups per CU still fit, else 3
-template <int BITS, int GS, bool MX, int MC, int NSET>
+template <int BITS, int GS, bool MX, int XR, int NSET>
 int launch_xs_mc(const QgArgs& a, int64_t ntiles, uint32_t xrow, uint32_t xbytes, hipStream_t st) {
     constexpr size_t stage = XsShape<BITS, GS, MX, NSET>::STAGE;
-    if ((size_t)xbytes + 4 * stage <= 78 * 1024) return launch_xs_one<BITS, GS, MX, MC, NSET, 4>(a, ntiles, xrow, xbytes, st);
-    return launch_xs_one<BITS, GS, MX, MC, NSET, 3>(a, ntiles, xrow, xbytes, st);
+    if ((size_t)xbytes + 4 * stage <= 78 * 1024) return launch_xs_one<BITS, GS, MX, XR, NSET, 4>(a, ntiles, xrow, xbytes, st);
+    return launch_xs_one<BITS, GS, MX, XR, NSET, 3>(a, ntiles, xrow, xbytes, st);
 }
 
 template <int BITS, int GS, bool MX, int NSET>
-int launch_xs_set(const QgArgs& a, int mc, int64_t ntiles, uint32_t xrow, uint32_t xbytes, hipStream_t st) {
-    if (mc == 1) return launch_xs_mc<BITS, GS, MX, 1, NSET>(a, ntiles, xrow, xbytes, st);
-    if (mc == 2) return launch_xs_mc<BITS, GS, MX, 2, NSET>(a, ntiles, xrow, xbytes, st);
-    return launch_xs_mc<BITS, GS, MX, 4, NSET>(a, ntiles, xrow, xbytes, st);
+int launch_xs_set(const QgArgs& a, int tr, int64_t ntiles, uint32_t xrow, uint32_t xbytes, hipStream_t st) {
+    if (tr == 4) return launch_xs_mc<BITS, GS, MX, 4, NSET>(a, ntiles, xrow, xbytes, st);
+    if (tr == 16) return launch_xs_mc<BITS, GS, MX, 16, NSET>(a, ntiles, xrow, xbytes, st);
+    if (tr == 32) return launch_xs_mc<BITS, GS, MX, 32, NSET>(a, ntiles, xrow, xbytes, st);
+    return launch_xs_mc<BITS, GS, MX, 64, NSET>(a, ntiles, xrow, xbytes, st);
 }
 
 template <int BITS, int GS, bool MX>
-int launch_xs_glu(const QgArgs& a, bool glu, int mc, int64_t ntiles, uint32_t xrow, uint32_t xbytes,
+int launch_xs_glu(const QgArgs& a, bool glu, int tr, int64_t ntiles, uint32_t xrow, uint32_t xbytes,
                   hipStream_t st) {
-    if (glu) return launch_xs_set<BITS, GS, MX, 2>(a, mc, ntiles, xrow, xbytes, st);
-    return launch_xs_set<BITS, GS, MX, 1>(a, mc, ntiles, xrow, xbytes, st);
+    if (glu) return launch_xs_set<BITS, GS, MX, 2>(a, tr, ntiles, xrow, xbytes, st);
+    return launch_xs_set<BITS, GS, MX, 1>(a, tr, ntiles, xrow, xbytes, st);
 }
 
 }  // namespace
 
 // 0: launched; 1: this shape does not fit the kernel (the caller takes qgemv)
-int launch_qgemv_xs(const QgArgs& a, int bits, int gs, bool glu, int mc, int64_t ntiles, hipStream_t st) {
+int launch_qgemv_xs(const QgArgs& a, int bits, int gs, bool glu, int tile_rows, int64_t ntiles, hipStream_t st) {
     if (!xs_enabled() || !a.tiles || !a.sorted || a.S != 1 || a.K % DL_KC != 0) return 1;
-    if (!(mc == 1 || mc == 2 || mc == 4) || !(bits == 4 || bits == 8)) return 1;
+    const int tr = tile_rows;
+    if (!(tr == 4 || tr == 16 || tr == 32 || tr == 64) || !(bits == 4 || bits == 8)) return 1;
     if (glu && a.up_off <= 0) return 1;
     const uint32_t xrow = (uint32_t)(a.K * 2 + 16);
-    const uint64_t xb = ((uint64_t)16 * mc * xrow + 1023) / 1024 * 1024;
+    const uint64_t xb = ((uint64_t)tr * xrow + 1023) / 1024 * 1024;
     if (xb > XS_LDS_MAX || a.xrows * a.K * 2 >= (1LL << 31)) return 1;
     const uint32_t xbytes = (uint32_t)xb;
     if (a.mx) {
         if (gs != 32) return 1;
-        if (bits == 4) return launch_xs_glu<4, 32, true>(a, glu, mc, ntiles, xrow, xbytes, st);
-        return launch_xs_glu<8, 32, true>(a, glu, mc, ntiles, xrow, xbytes, st);
+        if (bits == 4) return launch_xs_glu<4, 32, true>(a, glu, tr, ntiles, xrow, xbytes, st);
+        return launch_xs_glu<8, 32, true>(a, glu, tr, ntiles, xrow, xbytes, st);
     }
-    if (bits == 4 && gs == 64) return launch_xs_glu<4, 64, false>(a, glu, mc, ntiles, xrow, xbytes, st);
-    if (bits == 4 && gs == 32) return launch_xs_glu<4, 32, false>(a, glu, mc, ntiles, xrow, xbytes, st);
-    if (bits == 8 && gs == 64) return launch_xs_glu<8, 64, false>(a, glu, mc, ntiles, xrow, xbytes, st);
-    if (bits == 8 && gs == 32) return launch_xs_glu<8, 32, false>(a, glu, mc, ntiles, xrow, xbytes, st);
+    if (bits == 4 && gs == 64) return launch_xs_glu<4, 64, false>(a, glu, tr, ntiles, xrow, xbytes, st);
+    if (bits == 4 && gs == 32) return launch_xs_glu<4, 32, false>(a, glu, tr, ntiles, xrow, xbytes, st);
+    if (bits == 8 && gs == 64) return launch_xs_glu<8, 64, false>(a, glu, tr, ntiles, xrow, xbytes, st);
+    if (bits == 8 && gs == 32) return launch_xs_glu<8, 32, false>(a, glu, tr, ntiles, xrow, xbytes, st);
     return 1;
 }
 

@@ -262,7 +262,7 @@ static int run_skinny(QgArgs& a, const QgPlan& p, int bits, int gs, int64_t ntil
     a.S = p.S; a.gps = p.gps; a.partial = (float*)partial;
     int rc;
     if (dl) rc = launch_qgemv_dl(a, p, bits, gs, st);
-    else if (a.tiles && p.S == 1 && launch_qgemv_xs(a, bits, gs, false, p.mc, ntiles, st) == 0) rc = OK;
+    else if (a.tiles && p.S == 1 && launch_qgemv_xs(a, bits, gs, false, 16 * p.mc, ntiles, st) == 0) rc = OK;
     else rc = launch_qgemv(a, p, bits, gs, false, ntiles, st);
     if (rc) return rc;
     KMI_CHECK_LAUNCH(dl ? "qgemv_dl" : "qgemv");
