@@ -24,6 +24,8 @@
 #include "common.hpp"
 #include "vq_mfma.hpp"
 
+#include <cstdlib>
+
 namespace kmi {
 
 namespace {
@@ -65,7 +67,10 @@ constexpr int TM = VQM_TILE_ROWS;           // tile rows (MFMA M)
 // CB: index bytes (1, 2); NSET: row sets (2: gate, up + SwiGLU); LW: 32-bit
 // words of codes per lane; KS: waves sharing a 16-row group, each over
 // 1/KS of K (partials summed in LDS), so small grids still fill the chip.
-template <int CB, int NSET, int LW, int KS>
+// MB: several column blocks per workgroup (a.cblk), the next block's codes
+// loaded into a second register set while a block computes; else one block
+// and one register set (fewer registers: more waves to cover the gathers).
+template <int CB, int NSET, int LW, int KS, bool MB>
 __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     constexpr int CPL = LW * 4 / CB;                 // codes per lane
     constexpr int RW = 64 / KS;                      // weight rows per workgroup
@@ -90,11 +95,18 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rg = wave / KS, kp = wave % KS;        // row group, K part
     const int n = lane & 15, q = lane >> 4;
-    const int row = (int)blockIdx.x * RW + rg * 16 + n;
     const int K = (int)a.K, CPR = K / 8;
+    // this workgroup's column blocks of RW weight rows: cblk of them (1 at KS > 1)
+    const int nbt = (int)((a.N + RW - 1) / RW);
+    const int b0 = (int)blockIdx.x * a.cblk;
+    const int nb = MB ? (nbt - b0 < a.cblk ? nbt - b0 : a.cblk) : 1;
+    auto row_of = [&](int g) { return (b0 + g) * RW + rg * 16 + n; };
 
     if (e < 0 || e >= a.E) {                         // pair mode: an out-of-range expert gives 0
-        if (kp == 0 && q == 0 && row < a.N) a.y[(int64_t)start * a.N + row] = 0;
+        for (int g = 0; g < nb; g++) {
+            const int row = row_of(g);
+            if (kp == 0 && q == 0 && row < a.N) a.y[(int64_t)start * a.N + row] = 0;
+        }
         return;
     }
 
@@ -169,36 +181,43 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     u32x4 xv[XB];
     x_batch_load(0, tid, xv);
 
-    // ---- this lane's codes and row scale (the HBM stream)
-    const int crow = row < a.N ? row : (int)a.N - 1;           // rows past N re-read row N-1, never stored
+    // ---- this lane's codes and row scale of column block g (the HBM
+    //      stream), into register set `slot`
     const int64_t ebase = (int64_t)e * a.erows;
     const int cfirst = kp * (CPR / KS) + q * CPL;              // this lane's first code of its row
-    uint32_t cw[NSET][LW];
-    float scl[NSET];
+    uint32_t cw[MB ? 2 : 1][NSET][LW];
+    float scl[MB ? 2 : 1][NSET];
+    auto load_codes = [&](int g, int slot_) {
+        const int slot = MB ? slot_ : 0;
+        const int row = row_of(g);
+        const int crow = row < a.N ? row : (int)a.N - 1;       // rows past N re-read row N-1, never stored
 #pragma unroll
-    for (int s = 0; s < NSET; s++) {
-        const char* cb = (const char*)(s ? a.codes1 : a.codes0) + ebase * CPR * CB;
-        const __amdgpu_buffer_rsrc_t rc = make_rsrc(cb, a.N * CPR * CB);
-        const uint32_t lo = (uint32_t)((crow * CPR + cfirst) * CB);
-        if constexpr (LW % 4 == 0) {
+        for (int s = 0; s < NSET; s++) {
+            const char* cb = (const char*)(s ? a.codes1 : a.codes0) + ebase * CPR * CB;
+            const __amdgpu_buffer_rsrc_t rc = make_rsrc(cb, a.N * CPR * CB);
+            const uint32_t lo = (uint32_t)((crow * CPR + cfirst) * CB);
+            if constexpr (LW % 4 == 0) {
 #pragma unroll
-            for (int i = 0; i < LW; i += 4) {
-                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rc, (int)(lo + i * 4), 0, AUX_NT);
-                cw[s][i] = v.x; cw[s][i + 1] = v.y; cw[s][i + 2] = v.z; cw[s][i + 3] = v.w;
+                for (int i = 0; i < LW; i += 4) {
+                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rc, (int)(lo + i * 4), 0, AUX_NT);
+                    cw[slot][s][i] = v.x; cw[slot][s][i + 1] = v.y; cw[slot][s][i + 2] = v.z; cw[slot][s][i + 3] = v.w;
+                }
+            } else if constexpr (LW % 2 == 0) {
+#pragma unroll
+                for (int i = 0; i < LW; i += 2) {
+                    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(lo + i * 4), 0, AUX_NT);
+                    cw[slot][s][i] = v.x; cw[slot][s][i + 1] = v.y;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < LW; i++)
+                    cw[slot][s][i] = __builtin_amdgcn_raw_buffer_load_b32(rc, (int)(lo + i * 4), 0, AUX_NT);
             }
-        } else if constexpr (LW % 2 == 0) {
-#pragma unroll
-            for (int i = 0; i < LW; i += 2) {
-                const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rc, (int)(lo + i * 4), 0, AUX_NT);
-                cw[s][i] = v.x; cw[s][i + 1] = v.y;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < LW; i++) cw[s][i] = __builtin_amdgcn_raw_buffer_load_b32(rc, (int)(lo + i * 4), 0, AUX_NT);
+            const __amdgpu_buffer_rsrc_t rsc = make_rsrc((s ? a.sc1 : a.sc0) + ebase, a.N * 2);
+            scl[slot][s] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rsc, crow * 2, 0, 0));
         }
-        const __amdgpu_buffer_rsrc_t rsc = make_rsrc((s ? a.sc1 : a.sc0) + ebase, a.N * 2);
-        scl[s] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rsc, crow * 2, 0, 0));
-    }
+    };
+    load_codes(0, 0);
 
     // ---- x -> LDS (the first batch waits for its own loads only), then
     //      the workgroup
@@ -210,56 +229,75 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
         }
     lds_barrier();
 
-    // ---- MFMA over the lane's codes
-    f32x4 acc[NSET];
-#pragma unroll
-    for (int s = 0; s < NSET; s++) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int mrow = n < count ? n : count - 1;                 // A rows past the tile repeat a real row
     const unsigned char* xa = xs + (size_t)mrow * xstride + (size_t)cfirst * 16;
+    // ---- column block g from register set `slot`: MFMA over the lane's
+    //      codes, the K parts summed, the epilogue
+    auto compute = [&](int g, int slot_) {
+        const int slot = MB ? slot_ : 0;
+        const int row = row_of(g);
+        f32x4 acc[NSET];
 #pragma unroll
-    for (int kb = 0; kb < CPL; kb++) {
-        const u32x4 av = *(const u32x4*)(xa + kb * 16);
+        for (int s = 0; s < NSET; s++) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < NSET; s++) {
-            uint32_t code;
-            if constexpr (CB == 1) code = (cw[s][kb >> 2] >> (8 * (kb & 3))) & 0xffu;
-            else code = (cw[s][kb >> 1] >> (16 * (kb & 1))) & 0xffffu;
-            code = code < (uint32_t)a.kc ? code : (uint32_t)(a.kc - 1);
-            const u32x4 bv = *(const u32x4*)((s ? cbl1 : cbl0) + code * 16);
-            acc[s] = mfma_f16(av, bv, acc[s]);
-        }
-    }
-
-    // ---- K parts of a row group summed in LDS, in part order
-    if constexpr (KS > 1) {
+        for (int kb = 0; kb < CPL; kb++) {
+            const u32x4 av = *(const u32x4*)(xa + kb * 16);
 #pragma unroll
-        for (int s = 0; s < NSET; s++) red[(wave * NSET + s) * 64 + lane] = acc[s];
-        lds_barrier();
-        if (kp != 0) return;
-#pragma unroll
-        for (int s = 0; s < NSET; s++) {
-            f32x4 t = red[(wave * NSET + s) * 64 + lane];
-#pragma unroll
-            for (int j = 1; j < KS; j++) t += red[((wave + j) * NSET + s) * 64 + lane];
-            acc[s] = t;
-        }
-    }
-
-    // ---- epilogue: lane holds D[m = 4q + i][n]
-    if (row < a.N) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 4 * q + i;
-            if (m >= count) continue;
-            float out = vqm_bf16r(scl[0] * acc[0][i]);
-            if constexpr (NSET == 2) {     // round(round(silu_f32(gate)) * up)
-                const float up = vqm_bf16r(scl[1] * acc[1][i]);
-                const double g = (double)out;
-                out = vqm_bf16r(vqm_f32_kept(g / (1.0 + exp(-g)))) * up;
+            for (int s = 0; s < NSET; s++) {
+                uint32_t code;
+                if constexpr (CB == 1) code = (cw[slot][s][kb >> 2] >> (8 * (kb & 3))) & 0xffu;
+                else code = (cw[slot][s][kb >> 1] >> (16 * (kb & 1))) & 0xffffu;
+                code = code < (uint32_t)a.kc ? code : (uint32_t)(a.kc - 1);
+                const u32x4 bv = *(const u32x4*)((s ? cbl1 : cbl0) + code * 16);
+                acc[s] = mfma_f16(av, bv, acc[s]);
             }
-            const int64_t r = a.tiles ? a.sorted[start + m] : start;
-            a.y[r * a.N + row] = f32_to_bf16(out);
         }
+
+        // K parts of a row group summed in LDS, in part order (one column
+        // block per workgroup at KS > 1)
+        if constexpr (KS > 1) {
+#pragma unroll
+            for (int s = 0; s < NSET; s++) red[(wave * NSET + s) * 64 + lane] = acc[s];
+            lds_barrier();
+            if (kp != 0) return;
+#pragma unroll
+            for (int s = 0; s < NSET; s++) {
+                f32x4 t = red[(wave * NSET + s) * 64 + lane];
+#pragma unroll
+                for (int j = 1; j < KS; j++) t += red[((wave + j) * NSET + s) * 64 + lane];
+                acc[s] = t;
+            }
+        }
+
+        // epilogue: lane holds D[m = 4q + i][n]
+        if (row < a.N) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int m = 4 * q + i;
+                if (m >= count) continue;
+                float out = vqm_bf16r(scl[slot][0] * acc[0][i]);
+                if constexpr (NSET == 2) {     // round(round(silu_f32(gate)) * up)
+                    const float up = vqm_bf16r(scl[slot][1] * acc[1][i]);
+                    const double gg = (double)out;
+                    out = vqm_bf16r(vqm_f32_kept(gg / (1.0 + exp(-gg)))) * up;
+                }
+                const int64_t r = a.tiles ? a.sorted[start + m] : start;
+                a.y[r * a.N + row] = f32_to_bf16(out);
+            }
+        }
+    };
+    if constexpr (MB) {
+        // two register sets: block g + 1's codes stream in while block g computes
+        for (int g = 0; g < nb; g += 2) {
+            if (g + 1 < nb) load_codes(g + 1, 1);
+            compute(g, 0);
+            if (g + 1 < nb) {
+                if (g + 2 < nb) load_codes(g + 2, 0);
+                compute(g + 1, 1);
+            }
+        }
+    } else {
+        compute(0, 0);
     }
 }
 
@@ -305,7 +343,22 @@ bool vq_mfma_supported(int64_t K, int code_bytes, int kc, bool two_cb) {
     return any && vq_mfma_lds(K, kc, two_cb, TM, 2, 4) <= 160 * 1024;
 }
 
-int launch_vq_mfma(const VqmArgs& a, int code_bytes, int nset, int64_t ntiles, hipStream_t st) {
+// column blocks per workgroup for 2-byte codes without a K split: 4, so a
+// workgroup's 64 KB codebook staging and x staging serve 256 weight rows
+// (measured at 128 experts, 16 tokens, 4096 x 8: 103 -> 90 us); 1-byte codes
+// keep one block (4 KB codebooks; the smaller register set runs more waves)
+// (KMI_VQ_G overrides: tuning; read once)
+static int vq_cblk(int64_t nbt) {
+    static int ov = [] {
+        const char* e = getenv("KMI_VQ_G");
+        return e ? atoi(e) : 0;
+    }();
+    const int64_t g = ov > 0 ? ov : 4;
+    return (int)(g < nbt ? g : nbt);
+}
+
+int launch_vq_mfma(const VqmArgs& a_in, int code_bytes, int nset, int64_t ntiles, hipStream_t st) {
+    VqmArgs a = a_in;
     const bool two_cb = nset == 2 && a.cb1 != a.cb0;
     if (a.tile_rows < 1 || a.tile_rows > TM || (!a.tiles && a.tile_rows != 1)) {
         set_error("vq_mfma: tile rows %d", a.tile_rows);
@@ -324,16 +377,20 @@ int launch_vq_mfma(const VqmArgs& a, int code_bytes, int nset, int64_t ntiles, h
     }
     const int lw = vq_lw(a.K, code_bytes, ks);
     const size_t lds = vq_mfma_lds(a.K, a.kc, two_cb, a.tile_rows, nset, ks);
-    const dim3 grid((unsigned)ceil_div(a.N, 64 / ks), (unsigned)ntiles);
+    const int64_t nbt = ceil_div(a.N, 64 / ks);
+    const bool mb = code_bytes == 2 && ks == 1;
+    a.cblk = mb ? vq_cblk(nbt) : 1;
+    const dim3 grid((unsigned)ceil_div(nbt, a.cblk), (unsigned)ntiles);
 #define KMI_VQM_ONE(CB_, NS_, LW_, KS_)                                                          \
     if (code_bytes == CB_ && nset == NS_ && lw == LW_ && ks == KS_) {                            \
+        constexpr bool MB_ = CB_ == 2 && KS_ == 1;                                               \
         static bool attr = false;                                                                \
         if (!attr) {                                                                             \
-            (void)hipFuncSetAttribute((const void*)vq_mfma<CB_, NS_, LW_, KS_>,                  \
+            (void)hipFuncSetAttribute((const void*)vq_mfma<CB_, NS_, LW_, KS_, MB_>,             \
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);   \
             attr = true;                                                                         \
         }                                                                                        \
-        vq_mfma<CB_, NS_, LW_, KS_><<<grid, WG, lds, st>>>(a);                                   \
+        vq_mfma<CB_, NS_, LW_, KS_, MB_><<<grid, WG, lds, st>>>(a);                              \
         return OK;                                                                               \
     }
 #define KMI_VQM_LAUNCH(CB_, LW_, KS_) KMI_VQM_ONE(CB_, 1, LW_, KS_) KMI_VQM_ONE(CB_, 2, LW_, KS_)

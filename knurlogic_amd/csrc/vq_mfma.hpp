@@ -26,6 +26,7 @@ struct VqmArgs {
     uint16_t* y;                // [row ids, N] bf16
     int64_t N, K, erows;
     int tile_rows;              // largest tile count the launch stages (<= 16): sizes the LDS
+    int cblk;                   // column blocks per workgroup (set by launch_vq_mfma)
 };
 
 size_t vq_mfma_lds(int64_t K, int kc, bool two_cb, int tile_rows, int nset, int ks);
