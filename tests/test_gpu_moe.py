@@ -121,6 +121,26 @@ def test_switch_glu_matches_the_oracle(dev, T, E, H, I, k, bits):
     assert_close(to_numpy(comb), O.combine(ref, sc), what="combine")
 
 
+@pytest.mark.parametrize("T", [16, 40, 256])
+def test_switch_glu_repeats_and_ignores_row_positions(dev, T):
+    """Grouped SwitchGLU (4-, 16- and 32-row expert tiles): the same call
+    gives the same bits, and permuting the tokens -- which moves rows to other
+    positions inside their expert tiles -- permutes the output bit for bit
+    (no row's result depends on where the sort put it)."""
+    rng = np.random.default_rng(600 + T)
+    E, H, I, k = 128, 2048, 768, 8
+    glu, _ = _experts(rng, E, H, I, dev)
+    x = bf16_normal(rng, (T, H))
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    tx, ti = to_torch(x, dev, BF), torch.from_numpy(inds).to(dev)
+    ys = [glu(tx, ti) for _ in range(3)]
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+    perm = torch.from_numpy(rng.permutation(T)).to(dev)
+    yp = glu(tx[perm].contiguous(), ti[perm].contiguous())
+    assert torch.equal(yp, ys[0][perm])
+
+
 def test_switch_glu_unstacked_gate_and_up_agree(dev):
     """Without the stacked weight (gate and up that cannot be stacked):
     separate gate and up gather_qmm calls, the same SwiGLU and result."""

@@ -206,14 +206,15 @@ def test_quantize_mx_gives_the_references_checkpoint_back(dev):
 
 
 @pytest.mark.parametrize("mode", ["mxfp4", "mxfp8"])
-@pytest.mark.parametrize("T,k", [(1, 8), (2, 8), (3, 4), (16, 8), (70, 4)])
-def test_switch_glu_mx_matches_the_oracle(dev, mode, T, k):
+@pytest.mark.parametrize("T,k,E", [(1, 8, 16), (2, 8, 16), (3, 4, 16), (16, 8, 16), (70, 4, 16), (16, 8, 128)])
+def test_switch_glu_mx_matches_the_oracle(dev, mode, T, k, E):
     """SwitchGLU over mxfp4 / mxfp8 experts in one call (gate and up
-    stacked): up to 16 (token, slot) pairs token-major, more grouped by
-    expert; against the oracle's SwitchGLU over its mx matmul, and the
-    combine against moe_combine of the same y, bit for bit."""
-    rng = np.random.default_rng(T * 10 + k + (mode == "mxfp8"))
-    E, H, I = 16, 256, 128
+    stacked): up to 64 (token, slot) pairs token-major, more grouped by
+    expert (4-row expert tiles at 128 experts); against the oracle's
+    SwitchGLU over its mx matmul, and the combine against moe_combine of the
+    same y, bit for bit."""
+    rng = np.random.default_rng(T * 10 + k + (mode == "mxfp8") + E)
+    H, I = 256, 128
     bits = 4 if mode == "mxfp4" else 8
     (hg, gg), (hu, gu), (hd, gd) = [_random_mx(rng, (E, n), kd, mode, dev) for n, kd in ((I, H), (I, H), (H, I))]
     lin = lambda g: nn.QuantizedSwitchLinear(g[0], g[1], None, None, 32, bits, mode)
