@@ -487,6 +487,28 @@ int kmi_vq_packed_glu(const void* x, int64_t X, int64_t H, int64_t I, const uint
                       int64_t E, const int32_t* rows, int64_t rows_div, const int32_t* experts, int64_t R,
                       int dtype, void* act, void* stream);
 
+/*
+ * A whole SwitchGLU over packed VQ experts (the artifact model.py's
+ * VQSwitchGLU over VQSwitchLinear, named at tests/engine/test_deepseek_v4_mtp.py:
+ * 249,360; gate/up/down as switch_layers.py:172-193) in one call, the
+ * weighted combine of qwen3_5.py:181-182 when scores [T, k] bf16 are given:
+ *   act = SwiGLU over gate / up as kmi_vq_packed_glu (x row = pair / k),
+ *   y[p] = act[p] @ Down_{inds[p]}^T, out = combine(y, scores) [T, H] or y [T*k, H].
+ * Codes / scales / codebooks as kmi_vq_packed_gather_qmm (gate and up
+ * [E, I, *] over H inputs, down [E, H, *] over I).  Up to 16 pairs run per
+ * pair; more are grouped by expert on the GPU (an expert-tile MFMA kernel
+ * where the shape allows: dim 2 / 4 / 8, groups of 32 / 64 / 128 inputs,
+ * K a multiple of 32 * dim), so pairs that share an expert share its
+ * decode.  workspace: kmi_vq_packed_switch_glu_workspace_bytes.
+ */
+size_t kmi_vq_packed_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k);
+int kmi_vq_packed_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                             const void* scores, const uint32_t* codes_gate, const void* scales_gate,
+                             const void* codebook_gate, const uint32_t* codes_up, const void* scales_up,
+                             const void* codebook_up, const uint32_t* codes_down, const void* scales_down,
+                             const void* codebook_down, int pack_bits, int kc, int dim, int group, int64_t E,
+                             int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream);
+
 int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
                       const void* scores, const void* codes_gate, const void* scales_gate,
                       const void* codebook_gate, const void* codes_up, const void* scales_up,

@@ -22,6 +22,8 @@
 // scaled once per group.  With two row sets (gate and up) the epilogue is
 // Qwen3.5's _SwiGLU with its roundings.
 #include "common.hpp"
+#include "qgemv.hpp"
+#include "vq_packed_mfma.hpp"
 #include "../../include/knurlogic_amd.h"
 
 namespace kmi {
@@ -374,6 +376,100 @@ int kmi_vq_packed_glu(const void* x, int64_t X, int64_t H, int64_t I, const uint
     a.nset = 2; a.kc = kc; a.E = E; a.N = I; a.K = H; a.W = (H / dim + 31) / 32 * pack_bits; a.group = group;
     a.y = (uint16_t*)act;
     return run_vp(a, pack_bits, dim, (hipStream_t)stream);
+}
+
+// SwitchGLU over packed VQ experts in one call.  Workspace: act [T*k, I],
+// y [T*k, H] for the combine, then the expert sort (sized for up to 4096
+// experts at any tile height).
+static size_t vps_act_bytes(int64_t P, int64_t I) { return ((size_t)P * I * 2 + 255) & ~(size_t)255; }
+static size_t vps_y_bytes(int64_t P, int64_t H) { return ((size_t)P * H * 2 + 255) & ~(size_t)255; }
+
+size_t kmi_vq_packed_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k) {
+    if (T <= 0 || H <= 0 || I <= 0 || k <= 0) return 0;
+    const int64_t P = T * k;
+    return vps_act_bytes(P, I) + vps_y_bytes(P, H) + sort_index_bytes(P, 4096, 1);
+}
+
+int kmi_vq_packed_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                             const void* scores, const uint32_t* codes_gate, const void* scales_gate,
+                             const void* codebook_gate, const uint32_t* codes_up, const void* scales_up,
+                             const void* codebook_up, const uint32_t* codes_down, const void* scales_down,
+                             const void* codebook_down, int pack_bits, int kc, int dim, int group, int64_t E,
+                             int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = vp_check(dtype, pack_bits, kc, dim, group, H, I, E);
+    if (rc) return rc;
+    rc = vp_check(dtype, pack_bits, kc, dim, group, I, H, E);
+    if (rc) return rc;
+    KMI_CHECK_ARG(T >= 0 && k >= 1 && k <= 64, "vq_packed_switch_glu: bad sizes");
+    if (T == 0) return OK;
+    KMI_CHECK_ARG(x && inds && codes_gate && scales_gate && codebook_gate && codes_up && scales_up &&
+                      codebook_up && codes_down && scales_down && codebook_down && out,
+                  "vq_packed_switch_glu: null pointer");
+    const int64_t P = T * k;
+    KMI_CHECK_ARG(P < 65536 && T * H * 2 < (1LL << 31) && P * (H > I ? H : I) * 2 < (1LL << 31),
+                  "vq_packed_switch_glu: %lld (token, slot) pairs (at most 65535)", (long long)P);
+    const size_t need = kmi_vq_packed_switch_glu_workspace_bytes(T, H, I, k);
+    if (!workspace || workspace_bytes < need) {
+        set_error("vq_packed_switch_glu: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+        return EWORKSPACE;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    uint16_t* act = (uint16_t*)workspace;
+    uint16_t* y = scores ? (uint16_t*)((char*)workspace + vps_act_bytes(P, I)) : (uint16_t*)out;
+    const int64_t Wg = (H / dim + 31) / 32 * pack_bits, Wd = (I / dim + 31) / 32 * pack_bits;
+    // Expert-major on MFMA beyond 16 pairs where the kernel covers the shape
+    // (pairs that share an expert then share its decode); per pair below.
+    const bool two_cb = codebook_up != codebook_gate;
+    const bool grouped = P > 16 && E <= 4096 && E * I * Wg >= 4 && E * H * Wd >= 4 &&
+                         vpm_supported(pack_bits, dim, group, H, kc, two_cb) &&
+                         vpm_supported(pack_bits, dim, group, I, kc, false);
+    if (grouped) {
+        const int64_t avg = ceil_div(P, E < P ? E : P);
+        const int tile_rows = (int)(avg <= 4 ? (P < 8 ? P : 8) : VPM_TILE);
+        SortedRows sr;
+        void* index_ws = (char*)workspace + vps_act_bytes(P, I) + vps_y_bytes(P, H);
+        // the sort zeroes y's rows of out-of-range experts (no tile holds them)
+        rc = launch_sort_rows(inds, P, 1, (int)E, tile_rows, index_ws, y, H, st, &sr);
+        if (rc) return rc;
+        VpmArgs g = {};
+        g.x = (const uint16_t*)x; g.X = T; g.lhs_div = k; g.tiles = sr.tiles; g.sorted = sr.sorted; g.E = E;
+        g.codes[0] = codes_gate; g.codes[1] = codes_up;
+        g.sc[0] = (const uint16_t*)scales_gate; g.sc[1] = (const uint16_t*)scales_up;
+        g.cb[0] = (const uint16_t*)codebook_gate; g.cb[1] = (const uint16_t*)codebook_up;
+        g.kc = kc; g.N = I; g.K = H; g.W = Wg; g.y = act; g.tile_rows = tile_rows;
+        rc = launch_vpm(g, pack_bits, dim, group, 2, sr.max_tiles, st);
+        if (rc) return rc;
+        KMI_CHECK_LAUNCH("vq_packed_mfma(glu)");
+        VpmArgs d = {};
+        d.x = act; d.X = P; d.lhs_div = 1; d.tiles = sr.tiles; d.sorted = sr.sorted; d.E = E;
+        d.codes[0] = d.codes[1] = codes_down;
+        d.sc[0] = d.sc[1] = (const uint16_t*)scales_down;
+        d.cb[0] = d.cb[1] = (const uint16_t*)codebook_down;
+        d.kc = kc; d.N = H; d.K = I; d.W = Wd; d.y = y; d.tile_rows = tile_rows;
+        rc = launch_vpm(d, pack_bits, dim, group, 1, sr.max_tiles, st);
+        if (rc) return rc;
+        KMI_CHECK_LAUNCH("vq_packed_mfma(down)");
+    } else {
+        VpArgs g = {};
+        g.x = (const uint16_t*)x; g.X = T; g.rows = nullptr; g.rows_div = k; g.experts = inds; g.R = P;
+        g.codes[0] = codes_gate; g.codes[1] = codes_up;
+        g.sc[0] = (const uint16_t*)scales_gate; g.sc[1] = (const uint16_t*)scales_up;
+        g.cb[0] = (const uint16_t*)codebook_gate; g.cb[1] = (const uint16_t*)codebook_up;
+        g.nset = 2; g.kc = kc; g.E = E; g.N = I; g.K = H; g.W = Wg; g.group = group; g.y = act;
+        rc = run_vp(g, pack_bits, dim, st);
+        if (rc) return rc;
+        VpArgs d = {};
+        d.x = act; d.X = P; d.rows = nullptr; d.rows_div = 1; d.experts = inds; d.R = P;
+        d.codes[0] = d.codes[1] = codes_down;
+        d.sc[0] = d.sc[1] = (const uint16_t*)scales_down;
+        d.cb[0] = d.cb[1] = (const uint16_t*)codebook_down;
+        d.nset = 1; d.kc = kc; d.E = E; d.N = H; d.K = I; d.W = Wd; d.group = group; d.y = y;
+        rc = run_vp(d, pack_bits, dim, st);
+        if (rc) return rc;
+    }
+    if (scores) return kmi_moe_combine(y, scores, dtype, T, k, H, out, stream);
+    return OK;
 }
 
 }  // extern "C"

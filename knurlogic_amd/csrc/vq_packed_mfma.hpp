@@ -1,0 +1,34 @@
+// Arguments and launcher of the MFMA VQ expert matmul over the bit-packed
+// code layout (vq_packed_mfma.hip).
+#pragma once
+
+#include "common.hpp"
+
+namespace kmi {
+
+constexpr int VPM_TILE = 16;   // most rows (tokens or pairs) per expert tile
+
+struct VpmArgs {
+    const uint16_t* x;          // bf16 [X, K]
+    int64_t X;
+    int64_t lhs_div;            // x row = row id / lhs_div
+    const int32_t* tiles;       // [ntiles][3] (expert, start, count <= tile_rows) over `sorted`
+    const int32_t* sorted;      // row ids grouped by expert
+    int64_t E;
+    const uint32_t* codes[2];   // [E, N, W] packed fields (set 1: the up rows)
+    const uint16_t* sc[2];      // [E, N, K / group] fp16
+    const uint16_t* cb[2];      // [kc, DIM] fp16
+    int kc;
+    int64_t N, K, W;            // W: words per row
+    uint16_t* y;                // [row ids, N] bf16
+    int tile_rows;              // largest tile the launch stages (<= 16): sizes the LDS
+};
+
+// the shapes the kernel covers: dim 2 / 4 / 8, scale groups of 32 / 64 / 128
+// inputs, K a multiple of the group and of 32 * dim, a lane's fields of one
+// group inside one 16-byte load, codebooks and 16 x rows inside the LDS
+bool vpm_supported(int pack_bits, int dim, int group, int64_t K, int kc, bool two_cb);
+// nset 2: gate and up rows + SwiGLU; ntiles: tiles of the sort (grid rows)
+int launch_vpm(const VpmArgs& a, int pack_bits, int dim, int group, int nset, int64_t ntiles, hipStream_t st);
+
+}  // namespace kmi

@@ -26,7 +26,7 @@ import torch
 
 from .ops import (add_bias, gather_qmm, linear, moe_combine, moe_experts, moe_route,
                   moe_shared_add, quantize, quantized_matmul, swiglu, switch_glu, switch_glu_mx, vq_gather_qmm,
-                  vq_glu, vq_packed_gather_qmm, vq_packed_glu, vq_switch_glu)
+                  vq_glu, vq_packed_gather_qmm, vq_packed_glu, vq_packed_switch_glu, vq_switch_glu)
 
 
 class Linear:
@@ -266,20 +266,28 @@ class VQSwitchGLU:
         return self.gate_proj.pack_bits or self.up_proj.pack_bits or self.down_proj.pack_bits
 
     def __call__(self, x: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
-        """x [..., H], indices [..., k] -> [..., k, H]: one library call
-        (two for the packed layout: gate/up + SwiGLU, then down)."""
+        """x [..., H], indices [..., k] -> [..., k, H]: one library call."""
         if self._packed():
-            return self._packed_call(x, indices)
+            return self._packed_one_call(x, indices)
         return vq_switch_glu(x, indices, *self._mats(), self.gate_proj.scale_group)
 
     def combine(self, x, indices, scores):
         """(self(x, indices) * scores[..., None]).sum(-2) with the reference's
         roundings, in the same library call."""
         if self._packed():
-            return moe_combine(self._packed_call(x, indices), scores)
+            return self._packed_one_call(x, indices, scores)
         return vq_switch_glu(x, indices, *self._mats(), self.gate_proj.scale_group, scores=scores)
 
+    def _packed_one_call(self, x, indices, scores=None):
+        g, u, d = self.gate_proj, self.up_proj, self.down_proj
+        if not (g.pack_bits == u.pack_bits == d.pack_bits) or not (g.scale_group == u.scale_group == d.scale_group):
+            raise ValueError("VQSwitchGLU: gate, up and down must share the packed layout")
+        return vq_packed_switch_glu(x, indices, (g.codes, g.codebook, g.scales), (u.codes, u.codebook, u.scales),
+                                    (d.codes, d.codebook, d.scales), g.pack_bits, g.scale_group, scores=scores)
+
     def _packed_call(self, x, indices):
+        """The packed SwitchGLU through the separate ops (gate/up + SwiGLU,
+        then the down gather)."""
         g, u, d = self.gate_proj, self.up_proj, self.down_proj
         if not (g.pack_bits == u.pack_bits == d.pack_bits) or g.scale_group != u.scale_group:
             raise ValueError("VQSwitchGLU: gate, up and down must share the packed layout")

@@ -936,6 +936,52 @@ def vq_packed_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, pack_bits: i
     return act
 
 
+def vq_packed_switch_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, down, pack_bits: int, group: int,
+                         scores: torch.Tensor | None = None):
+    """SwitchGLU over packed VQ experts in one library call
+    (kmi_vq_packed_switch_glu): gate/up with the _SwiGLU epilogue, down, and
+    with scores [..., k] the weighted combine.  gate / up / down = (codes,
+    codebook, scales).  x [..., H], indices [..., k] -> [..., k, H], or
+    [..., H] with scores."""
+    _on_gpu(x, indices, *gate, *up, *down, scores)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("vq_packed_switch_glu: only bfloat16 activations are implemented")
+    H = x.shape[-1]
+    kc, dim = _vq_packed_operands(gate[0], gate[1], gate[2], pack_bits, group, H, "vq_packed_switch_glu")
+    _vq_packed_operands(up[0], up[1], up[2], pack_bits, group, H, "vq_packed_switch_glu")
+    if up[0].shape != gate[0].shape or up[1].shape != gate[1].shape:
+        raise ValueError("vq_packed_switch_glu: gate and up differ in shape")
+    E, I = gate[0].shape[0], gate[0].shape[1]
+    kd, dd = _vq_packed_operands(down[0], down[1], down[2], pack_bits, group, I, "vq_packed_switch_glu")
+    if down[0].shape[0] != E or down[0].shape[1] != H or kd != kc or dd != dim:
+        raise ValueError("vq_packed_switch_glu: down must be [E, H, *] over I inputs with gate's codebook shape")
+    lead, k = tuple(indices.shape[:-1]), indices.shape[-1]
+    if tuple(x.shape[:-1]) != lead:
+        raise ValueError("vq_packed_switch_glu: x [..., H] and indices [..., k] must share leading dimensions")
+    T = math.prod(lead)
+    sc = None
+    if scores is not None:
+        if scores.shape != indices.shape or scores.dtype != x.dtype:
+            raise ValueError("vq_packed_switch_glu: scores must match indices in shape and x in dtype")
+        sc = scores.contiguous()
+        out = torch.empty(*lead, H, dtype=x.dtype, device=x.device)
+    else:
+        out = torch.empty(*lead, k, H, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out
+    xc = x.reshape(T, H).contiguous()
+    ic = indices.reshape(T, k).to(torch.int32).contiguous()
+    g, u, d = (tuple(t.contiguous() for t in m) for m in (gate, up, down))
+    L = _lib()
+    nbytes = L.kmi_vq_packed_switch_glu_workspace_bytes(T, H, I, k)
+    ws = _workspace(nbytes, x.device)
+    _abi.check(L.kmi_vq_packed_switch_glu(
+        _ptr(xc), T, H, I, k, _ptr(ic), _ptr(sc), _ptr(g[0]), _ptr(g[2]), _ptr(g[1]), _ptr(u[0]), _ptr(u[2]),
+        _ptr(u[1]), _ptr(d[0]), _ptr(d[2]), _ptr(d[1]), pack_bits, kc, dim, group, E, DTYPE_CODE[x.dtype],
+        _ptr(out), _ptr(ws), nbytes, _stream(x)), "vq_packed_switch_glu")
+    return out
+
+
 def _vq_indices(x, E, lhs_indices, rhs_indices):
     dev = x.device
     xbatch = tuple(x.shape[:-2])

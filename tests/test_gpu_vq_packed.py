@@ -61,8 +61,12 @@ def test_packed_gather_matches_the_oracle(dev, case):
     assert_close(to_numpy(got), ref, what=f"packed case {case}")
 
 
-@pytest.mark.parametrize("T,E,H,I,k", [(1, 16, 512, 256, 4), (3, 32, 2048, 768, 8)])
+@pytest.mark.parametrize("T,E,H,I,k", [(1, 16, 512, 256, 4), (3, 32, 2048, 768, 8), (16, 32, 2048, 768, 8),
+                                       (40, 16, 512, 256, 4)])
 def test_packed_switch_glu_matches_the_oracle(dev, T, E, H, I, k):
+    """One library call: up to 16 pairs per pair, more grouped by expert on
+    the MFMA kernel (8- and 16-row tiles, experts over several tiles); the
+    separate ops agree."""
     rng = np.random.default_rng(T + E)
     bits, kc, dim, group = 11, 2048, 4, 64
     (hg, gg), (hu, gu), (hd, gd) = [_packed(rng, E, n, kd, dim, kc, bits, group, dev)
@@ -77,6 +81,7 @@ def test_packed_switch_glu_matches_the_oracle(dev, T, E, H, I, k):
     got = glu(tx, ti)
     assert got.shape == (T, k, H)
     assert_close(to_numpy(got), ref, what="packed vq switch_glu")
+    assert_close(to_numpy(glu._packed_call(tx, ti)), ref, what="packed vq switch_glu (separate ops)")
     _, sc = O.route(bf16_normal(rng, (T, E)), k)
     comb = glu.combine(tx, ti, to_torch(sc, dev, BF))
     assert_close(to_numpy(comb), O.combine(ref, sc), what="packed combine")
@@ -86,7 +91,58 @@ def test_packed_switch_glu_matches_the_oracle(dev, T, E, H, I, k):
     assert y.shape == (T * k, 1, H)
 
 
-@pytest.mark.parametrize("T", [1, 4])
+GROUPED = [  # (bits, kc, dim, group, H, I): shapes of the expert-tile kernel
+    (11, 2048, 4, 64, 512, 256),
+    (11, 2048, 2, 64, 512, 192),
+    (12, 4096, 2, 32, 256, 128),
+    (8, 256, 4, 128, 512, 256),
+    (16, 5000, 8, 64, 512, 256),
+    (9, 300, 8, 32, 256, 512),
+    (10, 1024, 4, 32, 384, 128),
+]
+
+
+@pytest.mark.parametrize("case", range(len(GROUPED)))
+def test_packed_switch_glu_grouped_shapes(dev, case):
+    """The expert-tile MFMA kernel across field widths, vector lengths and
+    scale groups (20 tokens x top-4 over 8 experts: tiles of 16 rows, most
+    experts over two tiles), SwitchGLU and combine against the oracle."""
+    bits, kc, dim, group, H, I = GROUPED[case]
+    rng = np.random.default_rng(100 + case)
+    T, E, k = 20, 8, 4
+    (hg, gg), (hu, gu), (hd, gd) = [_packed(rng, E, n, kd, dim, kc, bits, group, dev)
+                                    for n, kd in ((I, H), (I, H), (H, I))]
+    glu = nn.VQSwitchGLU(*(nn.VQSwitchLinear(*g, scale_group=group, pack_bits=bits) for g in (gg, gu, gd)))
+    x = bf16_normal(rng, (T, H))
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    fn = lambda h: (lambda xs, e: O.vq_packed_matmul(xs, h[0][e], h[1], h[2][e], bits, group, "bfloat16"))
+    ref = O.switch_glu(x, inds, fn(hg), fn(hu), fn(hd))
+    tx, ti = to_torch(x, dev, BF), torch.from_numpy(inds).to(dev)
+    assert_close(to_numpy(glu(tx, ti)), ref, what=f"grouped packed case {case}")
+    _, sc = O.route(bf16_normal(rng, (T, E)), k)
+    comb = glu.combine(tx, ti, to_torch(sc, dev, BF))
+    assert_close(to_numpy(comb), O.combine(ref, sc), what=f"grouped packed combine {case}")
+
+
+def test_packed_switch_glu_repeats_and_ignores_row_positions(dev):
+    """Grouped packed SwitchGLU: the same call gives the same bits, and
+    permuting the tokens (rows move inside their expert tiles) permutes the
+    output bit for bit."""
+    rng = np.random.default_rng(77)
+    T, E, H, I, k, bits, kc, dim, group = 24, 32, 2048, 768, 8, 11, 2048, 4, 64
+    mods = [nn.VQSwitchLinear(*_packed(rng, E, n, kd, dim, kc, bits, group, dev)[1], scale_group=group,
+                              pack_bits=bits) for n, kd in ((I, H), (I, H), (H, I))]
+    glu = nn.VQSwitchGLU(*mods)
+    tx = to_torch(bf16_normal(rng, (T, H)), dev, BF)
+    ti = torch.from_numpy(np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)).to(dev)
+    ys = [glu(tx, ti) for _ in range(3)]
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+    perm = torch.from_numpy(rng.permutation(T)).to(dev)
+    assert torch.equal(glu(tx[perm].contiguous(), ti[perm].contiguous()), ys[0][perm])
+
+
+@pytest.mark.parametrize("T", [1, 4, 16])
 def test_packed_switch_glu_at_the_shipped_artifact_shape(dev, T):
     """The expert layout the reference's Gemma-4 26B VQ artifact declares
     (tests/support/artifacts/gemma-4-26b-a4b-it-VQ-6.2bpw/config.json,
