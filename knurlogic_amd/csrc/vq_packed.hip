@@ -26,6 +26,8 @@
 #include "vq_packed_mfma.hpp"
 #include "../../include/knurlogic_amd.h"
 
+#include <cstdlib>
+
 namespace kmi {
 
 typedef _Float16 vp_f16x2 __attribute__((ext_vector_type(2)));
@@ -421,12 +423,19 @@ int kmi_vq_packed_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int
     // Expert-major on MFMA beyond 16 pairs where the kernel covers the shape
     // (pairs that share an expert then share its decode); per pair below.
     const bool two_cb = codebook_up != codebook_gate;
-    const bool grouped = P > 16 && E <= 4096 && E * I * Wg >= 4 && E * H * Wd >= 4 &&
-                         vpm_supported(pack_bits, dim, group, H, kc, two_cb) &&
+    const bool grouped = P > 16 && E <= 4096 && vpm_supported(pack_bits, dim, group, H, kc, two_cb) &&
                          vpm_supported(pack_bits, dim, group, I, kc, false);
     if (grouped) {
         const int64_t avg = ceil_div(P, E < P ? E : P);
-        const int tile_rows = (int)(avg <= 4 ? (P < 8 ? P : 8) : VPM_TILE);
+        // tiles sized to the rows an expert sees: the LDS holds a tile's x rows,
+        // so small tiles fit more workgroups per CU (T = 16 of 128 experts,
+        // top-8, 2048 x 4: 8-row tiles 146 us, 4-row 117 us)
+        int tile_rows = (int)(avg <= 2 ? 4 : avg <= 4 ? 8 : VPM_TILE);
+        if (tile_rows > P) tile_rows = (int)P;
+        if (const char* ev = getenv("KMI_VPM_TR")) {          // tuning: 1..16
+            const int v = atoi(ev);
+            if (v >= 1 && v <= VPM_TILE) tile_rows = v;
+        }
         SortedRows sr;
         void* index_ws = (char*)workspace + vps_act_bytes(P, I) + vps_y_bytes(P, H);
         // the sort zeroes y's rows of out-of-range experts (no tile holds them)

@@ -27,6 +27,8 @@
 #include "vq_packed_mfma.hpp"
 #include "../../include/knurlogic_amd.h"
 
+#include <cstdlib>
+
 namespace kmi {
 
 namespace {
@@ -84,7 +86,6 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, q = lane >> 4;
-    const int row = (int)blockIdx.x * 64 + wave * 16 + n;
     const int K = (int)a.K, G = K / GRP;
     const bool two_cb = NSET == 2 && a.cb[1] != a.cb[0];
     const int cbytes = a.kc * DIM * 2;
@@ -144,115 +145,112 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
     }
     __syncthreads();
 
-    // ---- per scale group: the lane's field run, the codebook gathers, SPG MFMAs
-    const int crow = row < a.N ? row : (int)a.N - 1;   // rows past N re-read row N-1, never stored
+    // ---- per column block of 64 rows (a.cblk of them share the staging),
+    //      per scale group: the lane's field run, the codebook gathers, SPG MFMAs
+    const int nbt = (int)((a.N + 63) / 64);
+    const int b0 = (int)blockIdx.x * a.cblk;
+    const int nb = nbt - b0 < a.cblk ? nbt - b0 : a.cblk;
     const int64_t ebase = (int64_t)e * a.N;
     const int mrow = n < count ? n : count - 1;        // A rows past the tile repeat a real row
     const unsigned char* xa = xs + (size_t)mrow * xstride + (size_t)q * (GRP / 4) * 2;
-    f32x4 acc[NSET];
-    // codes: one view of the whole tensor (a lane's 16-byte load may run up
-    // to 3 words past its row; only at the tensor's end is it pulled back)
+    // a lane's 16-byte load may run up to 3 words past its row: past the
+    // expert's last word the view returns 0 for each word out of range
     __amdgpu_buffer_rsrc_t rc[NSET], rs[NSET];
-    const uint32_t total_words = (uint32_t)(a.E * a.N * a.W);
 #pragma unroll
     for (int s = 0; s < NSET; s++) {
-        acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-        rc[s] = make_rsrc(a.codes[s], (int64_t)total_words * 4);
+        rc[s] = make_rsrc(a.codes[s] + ebase * a.W, a.N * a.W * 4);
         rs[s] = make_rsrc(a.sc[s] + ebase * G, a.N * (int64_t)G * 2);
     }
-    const uint32_t rowword = (uint32_t)((ebase + crow) * a.W);
+    const uint32_t kcm1 = (uint32_t)(a.kc - 1);
     // bit of the lane's first field in group g within its row (rows start
     // on word boundaries): field g * GRP / DIM + q * FPL
     auto run_bit = [&](int g) -> uint32_t { return (uint32_t)(g * (GRP / DIM) + q * FPL) * (uint32_t)PB; };
-    constexpr int GB = 4;                              // groups whose loads are issued together
-    for (int g0 = 0; g0 < G; g0 += GB) {
-        u32x4 wv[NSET][GB];
-        uint32_t sv[NSET][GB];
+    for (int cbk = 0; cbk < nb; cbk++) {
+        const int row = (b0 + cbk) * 64 + wave * 16 + n;
+        const int crow = row < a.N ? row : (int)a.N - 1;   // rows past N re-read row N-1, never stored
+        const uint32_t rowword = (uint32_t)crow * (uint32_t)a.W;
+        f32x4 acc[NSET];
 #pragma unroll
-        for (int s = 0; s < NSET; s++)
+        for (int s = 0; s < NSET; s++) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+        constexpr int GB = 4;                              // groups whose loads are issued together
+        for (int g0 = 0; g0 < G; g0 += GB) {
+            u32x4 wv[NSET][GB];
+            uint32_t sv[NSET][GB];
+#pragma unroll
+            for (int s = 0; s < NSET; s++)
+#pragma unroll
+                for (int j = 0; j < GB; j++) {
+                    const int g = g0 + j;
+                    const uint32_t w0 = rowword + (run_bit(g < G ? g : G - 1) >> 5);
+                    wv[s][j] = __builtin_amdgcn_raw_buffer_load_b128(rc[s], g < G ? (int)(w0 * 4u) : (int)VPM_NONE,
+                                                                     0, 0);
+                    sv[s][j] = __builtin_amdgcn_raw_buffer_load_b16(
+                        rs[s], g < G ? (int)((uint32_t)crow * (uint32_t)G * 2u + (uint32_t)g * 2u) : (int)VPM_NONE, 0, 0);
+                }
 #pragma unroll
             for (int j = 0; j < GB; j++) {
-                const int g = g0 + j;
-                const uint32_t w0 = rowword + (run_bit(g < G ? g : G - 1) >> 5);
-                const uint32_t wl = w0 + 4u <= total_words ? w0 : total_words - 4u;   // total_words >= 4: checked
-                wv[s][j] = __builtin_amdgcn_raw_buffer_load_b128(rc[s], g < G ? (int)(wl * 4u) : (int)VPM_NONE,
-                                                                 0, 0);
-                sv[s][j] = __builtin_amdgcn_raw_buffer_load_b16(
-                    rs[s], g < G ? (int)((uint32_t)crow * (uint32_t)G * 2u + (uint32_t)g * 2u) : (int)VPM_NONE, 0, 0);
-            }
+                // a group past G (the last batch of a row) reads zero codes and a
+                // zero scale at the last group's addresses: it adds 0
+                const int g = g0 + j < G ? g0 + j : G - 1;
+                const uint32_t sh = run_bit(g) & 31u;
+                u32x4 A[SPG];
 #pragma unroll
-        for (int j = 0; j < GB; j++) {
-            const int g = g0 + j;
-            if (g >= G) break;                         // uniform
-            const uint32_t sh = run_bit(g) & 31u;
-            const uint32_t w0 = rowword + (run_bit(g) >> 5);
-            const uint32_t back = w0 + 4u <= total_words ? 0u : w0 + 4u - total_words;   // 0 but at the end
-            u32x4 A[SPG];
+                for (int t = 0; t < SPG; t++) A[t] = *(const u32x4*)(xa + (size_t)(g * GRP + 8 * t) * 2);
 #pragma unroll
-            for (int t = 0; t < SPG; t++) A[t] = *(const u32x4*)(xa + (size_t)(g * GRP + 8 * t) * 2);
+                for (int s = 0; s < NSET; s++) {
+                    const u32x4 w = wv[s][j];
+                    // the run at bit 0: r0 | r1 << 32 | r2 << 64 (funnel shifts by the run's offset)
+                    const uint32_t r0 = __builtin_amdgcn_alignbit(w.y, w.x, sh);
+                    const uint32_t r1 = __builtin_amdgcn_alignbit(w.z, w.y, sh);
+                    const uint32_t r2 = __builtin_amdgcn_alignbit(w.w, w.z, sh);
+                    const unsigned char* cbl = s ? cbl1 : cbl0;
+                    f32x4 P = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < NSET; s++) {
-                u32x4 w = wv[s][j];
-                if (back) {              // the last row's last groups: the run starts `back` words in
-                    const uint32_t v0 = w.x, v1 = w.y, v2 = w.z, v3 = w.w;
-                    w.x = back == 1 ? v1 : back == 2 ? v2 : v3;
-                    w.y = back == 1 ? v2 : back == 2 ? v3 : 0u;
-                    w.z = back == 1 ? v3 : 0u;
-                    w.w = 0u;
-                }
-                // the run at bit 0: r0 | r1 << 32 | r2 << 64 (funnel shifts by the run's offset)
-                const uint32_t r0 = __builtin_amdgcn_alignbit(w.y, w.x, sh);
-                const uint32_t r1 = __builtin_amdgcn_alignbit(w.z, w.y, sh);
-                const uint32_t r2 = __builtin_amdgcn_alignbit(w.w, w.z, sh);
-                const unsigned char* cbl = s ? cbl1 : cbl0;
-                f32x4 P = {0.f, 0.f, 0.f, 0.f};
+                    for (int t = 0; t < SPG; t++) {
+                        uint32_t bw[4];
 #pragma unroll
-                for (int t = 0; t < SPG; t++) {
-                    uint32_t bw[4];
-#pragma unroll
-                    for (int f = 0; f < FPS; f++) {
-                        const int fi = t * FPS + f;            // field of the run
-                        const int bo = fi * PB, wi = bo >> 5, bs = bo & 31;
-                        uint32_t c;
-                        const uint32_t lo = wi == 0 ? r0 : wi == 1 ? r1 : r2;
-                        const uint32_t hi = wi == 0 ? r1 : wi == 1 ? r2 : 0u;
-                        c = (bs + PB <= 32) ? (lo >> bs) : __builtin_amdgcn_alignbit(hi, lo, (uint32_t)bs);
-                        c &= (1u << PB) - 1u;
-                        c = c < (uint32_t)a.kc ? c : (uint32_t)(a.kc - 1);
-                        if constexpr (DIM == 2) {
-                            bw[f] = *(const uint32_t*)(cbl + c * 4);
-                        } else if constexpr (DIM == 4) {
-                            const u32x2 v = *(const u32x2*)(cbl + c * 8);
-                            bw[2 * f] = v.x;
-                            bw[2 * f + 1] = v.y;
-                        } else {
-                            const u32x4 v = *(const u32x4*)(cbl + c * 16);
-                            bw[0] = v.x; bw[1] = v.y; bw[2] = v.z; bw[3] = v.w;
+                        for (int f = 0; f < FPS; f++) {
+                            const int fi = t * FPS + f;            // field of the run
+                            const int bo = fi * PB, wi = bo >> 5, bs = bo & 31;
+                            const uint32_t lo = wi == 0 ? r0 : wi == 1 ? r1 : r2;
+                            const uint32_t hi = wi == 0 ? r1 : wi == 1 ? r2 : 0u;
+                            uint32_t c = (bs + PB <= 32) ? (lo >> bs) : __builtin_amdgcn_alignbit(hi, lo, (uint32_t)bs);
+                            c = __builtin_elementwise_min(c & ((1u << PB) - 1u), kcm1);
+                            if constexpr (DIM == 2) {
+                                bw[f] = *(const uint32_t*)(cbl + c * 4);
+                            } else if constexpr (DIM == 4) {
+                                const u32x2 v = *(const u32x2*)(cbl + c * 8);
+                                bw[2 * f] = v.x;
+                                bw[2 * f + 1] = v.y;
+                            } else {
+                                const u32x4 v = *(const u32x4*)(cbl + c * 16);
+                                bw[0] = v.x; bw[1] = v.y; bw[2] = v.z; bw[3] = v.w;
+                            }
                         }
+                        P = vpm_mfma(A[t], u32x4{bw[0], bw[1], bw[2], bw[3]}, P);
                     }
-                    P = vpm_mfma(A[t], u32x4{bw[0], bw[1], bw[2], bw[3]}, P);
-                }
-                const float scl = f16_to_f32((uint16_t)sv[s][j]);
+                    const float scl = f16_to_f32((uint16_t)sv[s][j]);
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[s][i] = __builtin_fmaf(scl, P[i], acc[s][i]);
+                    for (int i = 0; i < 4; i++) acc[s][i] = __builtin_fmaf(scl, P[i], acc[s][i]);
+                }
             }
         }
-    }
 
-    // ---- epilogue: lane holds D[m = 4q + i][n]
-    if (row < a.N) {
+        // ---- epilogue: lane holds D[m = 4q + i][n]
+        if (row < a.N) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = 4 * q + i;
-            if (m >= count) continue;
-            float out = vpm_bf16r(acc[0][i]);
-            if constexpr (NSET == 2) {     // round(round(silu_f32(gate)) * up)
-                const float up = vpm_bf16r(acc[1][i]);
-                const double gg = (double)out;
-                out = vpm_bf16r(vpm_f32_kept(gg / (1.0 + exp(-gg)))) * up;
+            for (int i = 0; i < 4; i++) {
+                const int m = 4 * q + i;
+                if (m >= count) continue;
+                float out = vpm_bf16r(acc[0][i]);
+                if constexpr (NSET == 2) {     // round(round(silu_f32(gate)) * up)
+                    const float up = vpm_bf16r(acc[1][i]);
+                    const double gg = (double)out;
+                    out = vpm_bf16r(vpm_f32_kept(gg / (1.0 + exp(-gg)))) * up;
+                }
+                const int64_t r = a.sorted[start + m];
+                a.y[r * a.N + row] = f32_to_bf16(out);
             }
-            const int64_t r = a.sorted[start + m];
-            a.y[r * a.N + row] = f32_to_bf16(out);
         }
     }
 }
@@ -305,18 +303,31 @@ int vpm_launch_pb(const VpmArgs& a, int dim, int group, dim3 grid, size_t lds, h
     return EINVAL_ARG;
 }
 
+// column blocks of 64 rows per workgroup (KMI_VPM_G overrides: tuning; read once)
+int vpm_cblk(int64_t nbt) {
+    static int ov = [] {
+        const char* e = getenv("KMI_VPM_G");
+        return e ? atoi(e) : 0;
+    }();
+    const int64_t g = ov > 0 ? ov : 1;
+    return (int)(g < nbt ? g : nbt);
+}
+
 }  // namespace
 
 // ntiles: grid rows (tiles of the sort)
 int launch_vpm(const VpmArgs& a, int pack_bits, int dim, int group, int nset, int64_t ntiles, hipStream_t st) {
     const bool two_cb = nset == 2 && a.cb[1] != a.cb[0];
     const size_t lds = vpm_lds_bytes(a.K, a.kc, dim, two_cb, a.tile_rows);
-    const dim3 grid((unsigned)ceil_div(a.N, 64), (unsigned)ntiles);
+    const int64_t nbt = ceil_div(a.N, 64);
+    VpmArgs b = a;
+    b.cblk = vpm_cblk(nbt);
+    const dim3 grid((unsigned)ceil_div(nbt, b.cblk), (unsigned)ntiles);
     int rc = EINVAL_ARG;
 #define KMI_VPM_PB(PB_)                                                                                 \
     if (pack_bits == PB_)                                                                               \
-        rc = nset == 2 ? vpm_launch_pb<PB_, 2>(a, dim, group, grid, lds, st)                            \
-                       : vpm_launch_pb<PB_, 1>(a, dim, group, grid, lds, st);
+        rc = nset == 2 ? vpm_launch_pb<PB_, 2>(b, dim, group, grid, lds, st)                            \
+                       : vpm_launch_pb<PB_, 1>(b, dim, group, grid, lds, st);
     KMI_VPM_PB(8) KMI_VPM_PB(9) KMI_VPM_PB(10) KMI_VPM_PB(11) KMI_VPM_PB(12) KMI_VPM_PB(16)
 #undef KMI_VPM_PB
     if (rc) set_error("vq (packed, MFMA): no kernel for %d-bit fields, dim %d, group %d", pack_bits, dim, group);

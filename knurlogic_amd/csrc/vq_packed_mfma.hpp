@@ -22,6 +22,7 @@ struct VpmArgs {
     int64_t N, K, W;            // W: words per row
     uint16_t* y;                // [row ids, N] bf16
     int tile_rows;              // largest tile the launch stages (<= 16): sizes the LDS
+    int cblk;                   // 64-row column blocks per workgroup (set by launch_vpm)
 };
 
 // the shapes the kernel covers: dim 2 / 4 / 8, scale groups of 32 / 64 / 128
