@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void vq_gemv(VqArgs a) {
 #pragma unroll
         for (int j = 0; j < CPS; j++) {
             uint32_t c = code_at<CB>(cw[s], j);
-            c = c < (uint32_t)a.kc ? c : (uint32_t)(a.kc - 1);
+            c = __builtin_elementwise_min(c, (uint32_t)(a.kc - 1));
             const u32x4 cv = *(const u32x4*)(cbl + c * 8);
             const u32x4 xv = *(const u32x4*)(xl + (seg * CPS + j) * 8);
             acc[SGC ? j / SGC : 0] = dot8_f16(cv, xv, acc[SGC ? j / SGC : 0]);
@@ -470,10 +470,10 @@ int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, con
     // one token: its k pairs are their own tiles (pair mode), no sort
     const bool pair_mode = T == 1;
     // Tile rows: LDS holds a tile's x rows, sized for the largest tile, so
-    // few routed rows per expert take 8-row tiles (more workgroups fit a
+    // few routed rows per expert take 4- or 8-row tiles (more workgroups fit a
     // CU); the sort cuts every expert's rows into tiles of at most this.
     const int64_t avg = ceil_div(P, E < P ? E : P);
-    int tile_rows = avg <= 4 ? 8 : VQM_TILE_ROWS;
+    int tile_rows = avg <= 2 ? 4 : avg <= 4 ? 8 : VQM_TILE_ROWS;
     if (tile_rows > P) tile_rows = (int)P;
     if (pair_mode) tile_rows = 1;
     SortedRows sr = {};

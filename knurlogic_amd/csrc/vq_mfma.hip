@@ -247,7 +247,7 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
                 uint32_t code;
                 if constexpr (CB == 1) code = (cw[slot][s][kb >> 2] >> (8 * (kb & 3))) & 0xffu;
                 else code = (cw[slot][s][kb >> 1] >> (16 * (kb & 1))) & 0xffffu;
-                code = code < (uint32_t)a.kc ? code : (uint32_t)(a.kc - 1);
+                code = __builtin_elementwise_min(code, (uint32_t)(a.kc - 1));
                 const u32x4 bv = *(const u32x4*)((s ? cbl1 : cbl0) + code * 16);
                 acc[s] = mfma_f16(av, bv, acc[s]);
             }
@@ -510,7 +510,7 @@ __global__ __launch_bounds__(WG) void vq_down_tok(VqdArgs a) {
                 uint32_t code;
                 if constexpr (CB == 1) code = (cw[u][kb >> 2] >> (8 * (kb & 3))) & 0xffu;
                 else code = (cw[u][kb >> 1] >> (16 * (kb & 1))) & 0xffffu;
-                code = code < (uint32_t)a.kc ? code : (uint32_t)(a.kc - 1);
+                code = __builtin_elementwise_min(code, (uint32_t)(a.kc - 1));
                 const u32x4 bv = *(const u32x4*)(smem + code * 16);
                 acc = mfma_f16(av, bv, acc);
             }

@@ -210,14 +210,14 @@ __global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
 #pragma unroll
                 for (int j = 0; j < 32; j++) {
                     uint32_t c = vp_field<PB>(w, j);
-                    c = c < (uint32_t)a.kc ? c : (uint32_t)(a.kc - 1);
+                    c = __builtin_elementwise_min(c, (uint32_t)(a.kc - 1));
                     acc[j / FPG] = vp_dot<DIM>(cbl + c * DIM, xb + j * DIM, acc[j / FPG]);
                 }
             } else {                 // the last, partial block of a row
 #pragma unroll
                 for (int j = 0; j < 32; j++) {
                     uint32_t c = vp_field<PB>(w, j);
-                    c = c < (uint32_t)a.kc ? c : (uint32_t)(a.kc - 1);
+                    c = __builtin_elementwise_min(c, (uint32_t)(a.kc - 1));
                     const float d = vp_dot<DIM>(cbl + c * DIM, xb + j * DIM, 0.f);
                     acc[j / FPG] += j < nvalid ? d : 0.f;
                 }
