@@ -239,18 +239,38 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
         f32x4 acc[NSET];
 #pragma unroll
         for (int s = 0; s < NSET; s++) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // operands of KB codes per group, group j + 1's LDS reads issued
+        // before group j's MFMAs (the scheduling barriers keep them there):
+        // one LDS round trip per group instead of one per code (left to
+        // itself the compiler waits for each gather before its MFMA)
+        constexpr int KB = CPL % 4 == 0 ? 4 : CPL % 2 == 0 ? 2 : 1;
+        u32x4 av[2][KB], bv[2][NSET][KB];
+        auto fetch = [&](int kb0, int buf) {
 #pragma unroll
-        for (int kb = 0; kb < CPL; kb++) {
-            const u32x4 av = *(const u32x4*)(xa + kb * 16);
+            for (int j = 0; j < KB; j++) {
+                const int kb = kb0 + j;
+                av[buf][j] = *(const u32x4*)(xa + kb * 16);
 #pragma unroll
-            for (int s = 0; s < NSET; s++) {
-                uint32_t code;
-                if constexpr (CB == 1) code = (cw[slot][s][kb >> 2] >> (8 * (kb & 3))) & 0xffu;
-                else code = (cw[slot][s][kb >> 1] >> (16 * (kb & 1))) & 0xffffu;
-                code = __builtin_elementwise_min(code, (uint32_t)(a.kc - 1));
-                const u32x4 bv = *(const u32x4*)((s ? cbl1 : cbl0) + code * 16);
-                acc[s] = mfma_f16(av, bv, acc[s]);
+                for (int s = 0; s < NSET; s++) {
+                    uint32_t code;
+                    if constexpr (CB == 1) code = (cw[slot][s][kb >> 2] >> (8 * (kb & 3))) & 0xffu;
+                    else code = (cw[slot][s][kb >> 1] >> (16 * (kb & 1))) & 0xffffu;
+                    code = __builtin_elementwise_min(code, (uint32_t)(a.kc - 1));
+                    bv[buf][s][j] = *(const u32x4*)((s ? cbl1 : cbl0) + code * 16);
+                }
             }
+        };
+        fetch(0, 0);
+#pragma unroll
+        for (int kb0 = 0; kb0 < CPL; kb0 += KB) {
+            const int buf = (kb0 / KB) & 1;
+            if (kb0 + KB < CPL) fetch(kb0 + KB, buf ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < KB; j++)
+#pragma unroll
+                for (int s = 0; s < NSET; s++) acc[s] = mfma_f16(av[buf][j], bv[buf][s][j], acc[s]);
+            __builtin_amdgcn_sched_barrier(0);
         }
 
         // K parts of a row group summed in LDS, in part order (one column
@@ -504,15 +524,30 @@ __global__ __launch_bounds__(WG) void vq_down_tok(VqdArgs a) {
             if (j0 + u >= nslot) continue;
             const unsigned char* xa = xs + (size_t)s * xstride + (size_t)cfirst * 16;
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            // groups of KB codes, group j + 1's reads issued before group j's MFMAs
+            constexpr int KB = CPL % 4 == 0 ? 4 : CPL % 2 == 0 ? 2 : 1;
+            u32x4 av[2][KB], bv[2][KB];
+            auto fetch = [&](int kb0, int buf) {
 #pragma unroll
-            for (int kb = 0; kb < CPL; kb++) {
-                const u32x4 av = *(const u32x4*)(xa + kb * 16);
-                uint32_t code;
-                if constexpr (CB == 1) code = (cw[u][kb >> 2] >> (8 * (kb & 3))) & 0xffu;
-                else code = (cw[u][kb >> 1] >> (16 * (kb & 1))) & 0xffffu;
-                code = __builtin_elementwise_min(code, (uint32_t)(a.kc - 1));
-                const u32x4 bv = *(const u32x4*)(smem + code * 16);
-                acc = mfma_f16(av, bv, acc);
+                for (int j = 0; j < KB; j++) {
+                    const int kb = kb0 + j;
+                    av[buf][j] = *(const u32x4*)(xa + kb * 16);
+                    uint32_t code;
+                    if constexpr (CB == 1) code = (cw[u][kb >> 2] >> (8 * (kb & 3))) & 0xffu;
+                    else code = (cw[u][kb >> 1] >> (16 * (kb & 1))) & 0xffffu;
+                    code = __builtin_elementwise_min(code, (uint32_t)(a.kc - 1));
+                    bv[buf][j] = *(const u32x4*)(smem + code * 16);
+                }
+            };
+            fetch(0, 0);
+#pragma unroll
+            for (int kb0 = 0; kb0 < CPL; kb0 += KB) {
+                const int buf = (kb0 / KB) & 1;
+                if (kb0 + KB < CPL) fetch(kb0 + KB, buf ^ 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < KB; j++) acc = mfma_f16(av[buf][j], bv[buf][j], acc);
+                __builtin_amdgcn_sched_barrier(0);
             }
             // D[m][n] is the same for every m: lanes q = 0 hold it in item 0
             const float y = okk[u] ? vqm_bf16r(scl[u] * acc[0]) : 0.f;
