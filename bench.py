@@ -285,7 +285,8 @@ def bench_vq(T, kc, cold, calls, dev):
     """VQ experts at the Qwen3.5-MoE shape: 8-element vectors into a per-layer
     fp16 codebook (256 x 8 with uint8 indices, or 4096 x 8 with uint16),
     per-output-channel fp16 scales U(0.5, 1.5); router from N(0, 1) logits,
-    fused gate/up + SwiGLU, down, weighted combine.  Bytes: every routed
+    fused gate/up + SwiGLU, down, weighted combine (one ``experts`` call:
+    at one token the gate/up kernel routes it).  Bytes: every routed
     expert's indices and scales once, the codebook, x and out."""
     import torch
     import knurlogic_amd as KA
@@ -311,8 +312,7 @@ def bench_vq(T, kc, cold, calls, dev):
 
     def run():
         for i in range(calls):
-            ii, sc = KA.moe_route(logits, k)
-            glus[i % n].combine(x, ii, sc)
+            glus[i % n].experts(x, logits, k)
 
     us = time_graph(run) / calls * 1e3
     nbytes = distinct * vq_expert_bytes(H, I, cb_bytes) + kc * 16 + 2 * 2 * T * H

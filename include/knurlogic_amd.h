@@ -518,6 +518,24 @@ int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, con
                       void* stream);
 
 /*
+ * The VQ experts of a SparseMoeBlock from its router logits, in one call
+ * (qwen3_5.py:174-182 over VQSwitchLinear experts): the router of
+ * kmi_moe_route (inds [T, k] int32 and scores [T, k] bf16 written, bit for
+ * bit as kmi_moe_route gives them), then kmi_vq_switch_glu with the
+ * weighted combine into out [T, H].  logits [T, E] bf16.  For one token on
+ * the MFMA path (per-channel scales, E <= 256) the gate/up kernel routes
+ * the token itself, so the call is two kernel launches; otherwise it
+ * routes first.  k <= 8, E <= 1024.  workspace:
+ * kmi_vq_switch_glu_workspace_bytes(T, H, I, k).
+ */
+int kmi_vq_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k,
+                   const void* codes_gate, const void* scales_gate, const void* codebook_gate,
+                   const void* codes_up, const void* scales_up, const void* codebook_up,
+                   const void* codes_down, const void* scales_down, const void* codebook_down, int code_bytes,
+                   int kc, int dim, int scale_group, int64_t E, int dtype, void* out, int32_t* inds,
+                   void* scores, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Calibration only (no counterpart in the reference): reads `bytes` of
  * device memory at `p` with `workgroups` workgroups of 16-byte nontemporal
  * loads, as the GEMV kernels load their weights, and computes nothing, so

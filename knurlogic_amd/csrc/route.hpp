@@ -21,13 +21,16 @@ constexpr int ROUTE_THREADS = 256;
 constexpr int ROUTE_MAX_E = 1024;             // 4 experts per thread
 constexpr int ROUTE_MAX_K = 64;
 
-struct RouteLds {
-    uint64_t keys[ROUTE_MAX_E];
+// MAXE: the most experts a kernel routes (sizes the key table)
+template <int MAXE = ROUTE_MAX_E>
+struct RouteLdsT {
+    uint64_t keys[MAXE];
     float red[8];
     double dred[4];
     float sel_p[ROUTE_MAX_K];
     int sel_e[ROUTE_MAX_K];
 };
+using RouteLds = RouteLdsT<>;
 
 // A float64 result rounded to float32 and kept there (no fused rounding
 // with a later one to a narrower type).
@@ -80,17 +83,23 @@ __device__ __forceinline__ double route_wave_sum(double v) {
 // already rounded to T.  Every thread of the 256 must call it (barriers).
 // E <= ROUTE_MAX_E, k <= min(E, ROUTE_MAX_K).
 // PER: experts per thread (E <= 256 * PER).
+// route_token in two parts, so a kernel can issue the logits load early and
+// route later: route_load reads this thread's logits, route_from routes them.
 template <class T, int PER>
-__device__ __forceinline__ void route_token(const typename T::storage* __restrict__ lg, int E, int k, RouteLds& sm) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    float x[PER];
-    float mx = -INFINITY;
+__device__ __forceinline__ void route_load(const typename T::storage* __restrict__ lg, int E, float (&x)[PER]) {
 #pragma unroll
     for (int j = 0; j < PER; j++) {
-        const int i = tid + ROUTE_THREADS * j;
+        const int i = threadIdx.x + ROUTE_THREADS * j;
         x[j] = i < E ? T::load(lg[i]) : -INFINITY;
-        mx = fmaxf(mx, x[j]);
     }
+}
+
+template <class T, int PER, class SM>
+__device__ __forceinline__ void route_from(const float (&x)[PER], int E, int k, SM& sm) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; j++) mx = fmaxf(mx, x[j]);
     mx = route_wave_max(mx);
     if (lane == 0) sm.red[w] = mx;
     __syncthreads();
@@ -152,6 +161,13 @@ __device__ __forceinline__ void route_token(const typename T::storage* __restric
     __syncthreads();                                   // every thread has read sel_p
     if (tid < k) sm.sel_p[tid] = T::round(route_f32((double)sm.sel_p[tid] / tt));
     __syncthreads();
+}
+
+template <class T, int PER, class SM>
+__device__ __forceinline__ void route_token(const typename T::storage* __restrict__ lg, int E, int k, SM& sm) {
+    float x[PER];
+    route_load<T, PER>(lg, E, x);
+    route_from<T, PER>(x, E, k, sm);
 }
 
 }  // namespace kmi

@@ -22,6 +22,7 @@
 #include "common.hpp"
 #include "qgemv.hpp"
 #include "vq_mfma.hpp"
+#include "route.hpp"
 #include "../../include/knurlogic_amd.h"
 
 namespace kmi {
@@ -433,14 +434,24 @@ size_t kmi_vq_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k)
     return vq_act_bytes(T, I, k) + vq_y_bytes(T, H, k) + sort_index_bytes(T * k, 4096, 1);   // any tile size
 }
 
-int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
-                      const void* scores, const void* codes_gate, const void* scales_gate,
-                      const void* codebook_gate, const void* codes_up, const void* scales_up,
-                      const void* codebook_up, const void* codes_down, const void* scales_down,
-                      const void* codebook_down, int code_bytes, int kc, int dim, int scale_group,
-                      int64_t E, int dtype, void* out, void* workspace, size_t workspace_bytes,
-                      void* stream) {
-    clear_error();
+}  // extern "C"
+
+// The VQ SwitchGLU; with logits (one token, the MFMA gate/up path) its
+// pair-mode gate/up kernel routes the token and writes inds / scores, which
+// the down kernel then reads.  vq_route_in_kernel says when that applies.
+static bool vq_route_in_kernel(int64_t T, int64_t H, int k, int64_t E, int code_bytes, int kc, int scale_group,
+                               bool two_cb) {
+    return T == 1 && k >= 1 && k <= 8 && E >= k && E <= ROUTE_THREADS && scale_group == 0 &&
+           vq_mfma_supported(H, code_bytes, kc, two_cb);
+}
+
+static int vq_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                              const void* scores, const void* codes_gate, const void* scales_gate,
+                              const void* codebook_gate, const void* codes_up, const void* scales_up,
+                              const void* codebook_up, const void* codes_down, const void* scales_down,
+                              const void* codebook_down, int code_bytes, int kc, int dim, int scale_group,
+                              int64_t E, int dtype, void* out, void* workspace, size_t workspace_bytes,
+                              void* stream, const void* logits) {
     int rc = vq_check(dtype, code_bytes, kc, dim, scale_group, H, I, E);
     if (rc) return rc;
     rc = vq_check(dtype, code_bytes, kc, dim, scale_group, I, H, E);
@@ -466,6 +477,10 @@ int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, con
     const bool m_glu = sortable && vq_mfma_supported(H, code_bytes, kc, two_cb) && al16(codes_gate) &&
                        al16(codes_up);
     const bool m_down = sortable && vq_mfma_supported(I, code_bytes, kc, false) && al16(codes_down);
+    if (logits && !(m_glu && T == 1)) {
+        set_error("vq_switch_glu: in-kernel routing needs one token on the MFMA gate/up path");
+        return EINVAL_ARG;
+    }
     uint16_t* y = scores ? (uint16_t*)((char*)workspace + vq_act_bytes(T, I, k)) : (uint16_t*)out;
     // one token: its k pairs are their own tiles (pair mode), no sort
     const bool pair_mode = T == 1;
@@ -490,6 +505,12 @@ int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, con
         g.codes0 = codes_gate; g.sc0 = (const uint16_t*)scales_gate; g.cb0 = (const uint16_t*)codebook_gate;
         g.codes1 = codes_up; g.sc1 = (const uint16_t*)scales_up; g.cb1 = (const uint16_t*)codebook_up;
         g.kc = kc; g.y = act; g.N = I; g.K = H; g.erows = I; g.tile_rows = tile_rows;
+        if (logits) {   // pair mode: the kernel routes its token and writes inds / scores
+            g.logits = (const uint16_t*)logits;
+            g.inds_out = (int32_t*)inds;
+            g.scores_out = (uint16_t*)scores;
+            g.k = k;
+        }
         rc = launch_vq_mfma(g, code_bytes, 2, pair_mode ? P : sr.max_tiles, st);
         if (rc) return rc;
         KMI_CHECK_LAUNCH("vq_mfma(glu)");
@@ -541,6 +562,49 @@ int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, con
     }
     if (scores) return kmi_moe_combine(y, scores, dtype, T, k, H, out, stream);
     return OK;
+}
+
+extern "C" {
+
+int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                      const void* scores, const void* codes_gate, const void* scales_gate,
+                      const void* codebook_gate, const void* codes_up, const void* scales_up,
+                      const void* codebook_up, const void* codes_down, const void* scales_down,
+                      const void* codebook_down, int code_bytes, int kc, int dim, int scale_group,
+                      int64_t E, int dtype, void* out, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+    clear_error();
+    return vq_switch_glu_impl(x, T, H, I, k, inds, scores, codes_gate, scales_gate, codebook_gate, codes_up,
+                              scales_up, codebook_up, codes_down, scales_down, codebook_down, code_bytes, kc, dim,
+                              scale_group, E, dtype, out, workspace, workspace_bytes, stream, nullptr);
+}
+
+int kmi_vq_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k,
+                   const void* codes_gate, const void* scales_gate, const void* codebook_gate,
+                   const void* codes_up, const void* scales_up, const void* codebook_up,
+                   const void* codes_down, const void* scales_down, const void* codebook_down, int code_bytes,
+                   int kc, int dim, int scale_group, int64_t E, int dtype, void* out, int32_t* inds,
+                   void* scores, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(dtype == BF16, "vq_experts: only bfloat16 activations and logits are implemented");
+    KMI_CHECK_ARG(E >= 1 && E <= ROUTE_MAX_E && k >= 1 && k <= 8 && k <= E,
+                  "vq_experts: top-%d of %lld experts (k <= 8, E <= %d)", k, (long long)E, ROUTE_MAX_E);
+    KMI_CHECK_ARG(T >= 0, "vq_experts: T=%lld", (long long)T);
+    if (T == 0) return OK;
+    KMI_CHECK_ARG(logits && inds && scores, "vq_experts: null pointer");
+    const bool two_cb = codebook_up != codebook_gate;
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+    if (vq_route_in_kernel(T, H, k, E, code_bytes, kc, scale_group, two_cb) && al16(codes_gate) && al16(codes_up) &&
+        vq_check(dtype, code_bytes, kc, dim, scale_group, H, I, E) == OK)
+        return vq_switch_glu_impl(x, T, H, I, k, inds, scores, codes_gate, scales_gate, codebook_gate, codes_up,
+                                  scales_up, codebook_up, codes_down, scales_down, codebook_down, code_bytes, kc, dim,
+                                  scale_group, E, dtype, out, workspace, workspace_bytes, stream, logits);
+    clear_error();
+    int rc = kmi_moe_route(logits, dtype, T, (int)E, k, inds, scores, stream);
+    if (rc) return rc;
+    return vq_switch_glu_impl(x, T, H, I, k, inds, scores, codes_gate, scales_gate, codebook_gate, codes_up,
+                              scales_up, codebook_up, codes_down, scales_down, codebook_down, code_bytes, kc, dim,
+                              scale_group, E, dtype, out, workspace, workspace_bytes, stream, nullptr);
 }
 
 }  // extern "C"

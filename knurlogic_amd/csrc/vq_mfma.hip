@@ -23,6 +23,7 @@
 // below 6e-5), as in vq.hip.
 #include "common.hpp"
 #include "vq_mfma.hpp"
+#include "route.hpp"
 
 #include <cstdlib>
 
@@ -70,7 +71,9 @@ constexpr int TM = VQM_TILE_ROWS;           // tile rows (MFMA M)
 // MB: several column blocks per workgroup (a.cblk), the next block's codes
 // loaded into a second register set while a block computes; else one block
 // and one register set (fewer registers: more waves to cover the gathers).
-template <int CB, int NSET, int LW, int KS, bool MB>
+// RT (pair mode only): the pair's expert from routing its token's logits in
+// the workgroup (E <= 256), not from rhs.
+template <int CB, int NSET, int LW, int KS, bool MB, bool RT = false>
 __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     constexpr int CPL = LW * 4 / CB;                 // codes per lane
     constexpr int RW = 64 / KS;                      // weight rows per workgroup
@@ -88,7 +91,14 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     } else {
         start = (int)blockIdx.y;
         count = 1;
-        e = a.rhs[start];
+        // RT: the expert is routed below, once the loads that do not need it
+        // (codebook, x) are in flight; the logits load goes first
+        e = RT ? 0 : a.rhs[start];
+    }
+    float rlog[1];
+    if constexpr (RT) {
+        static_assert(WG == ROUTE_THREADS, "the in-kernel router takes 256 threads");
+        route_load<TBF16, 1>(a.logits + (int64_t)(start / a.k) * a.E, (int)a.E, rlog);
     }
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -180,6 +190,17 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     };
     u32x4 xv[XB];
     x_batch_load(0, tid, xv);
+
+    if constexpr (RT) {
+        __shared__ RouteLdsT<ROUTE_THREADS> rsm;     // E <= 256
+        route_from<TBF16, 1>(rlog, (int)a.E, a.k, rsm);
+        const int s = start % a.k;
+        e = __builtin_amdgcn_readfirstlane(rsm.sel_e[s]);
+        if (blockIdx.x == 0 && tid == 0) {
+            a.inds_out[start] = e;
+            a.scores_out[start] = f32_to_bf16(rsm.sel_p[s]);
+        }
+    }
 
     // ---- this lane's codes and row scale of column block g (the HBM
     //      stream), into register set `slot`
@@ -363,6 +384,16 @@ bool vq_mfma_supported(int64_t K, int code_bytes, int kc, bool two_cb) {
     return any && vq_mfma_lds(K, kc, two_cb, TM, 2, 4) <= 160 * 1024;
 }
 
+// Lets a kernel take all of the LDS its static allocation leaves (the
+// router's state is static in the routing variants), and leaves no error
+// behind for the launch check.
+static void vq_allow_lds(const void* f) {
+    hipFuncAttributes fa = {};
+    const size_t stat = hipFuncGetAttributes(&fa, f) == hipSuccess ? fa.sharedSizeBytes : 0;
+    (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(160 * 1024 - stat));
+    (void)hipGetLastError();
+}
+
 // column blocks per workgroup for 2-byte codes without a K split: 4, so a
 // workgroup's 64 KB codebook staging and x staging serve 256 weight rows
 // (measured at 128 experts, 16 tokens, 4096 x 8: 103 -> 90 us); 1-byte codes
@@ -398,25 +429,37 @@ int launch_vq_mfma(const VqmArgs& a_in, int code_bytes, int nset, int64_t ntiles
     const int lw = vq_lw(a.K, code_bytes, ks);
     const size_t lds = vq_mfma_lds(a.K, a.kc, two_cb, a.tile_rows, nset, ks);
     const int64_t nbt = ceil_div(a.N, 64 / ks);
-    const bool mb = code_bytes == 2 && ks == 1;
+    const bool rt = a.logits != nullptr;
+    if (rt && (a.tiles || nset != 2 || a.E > ROUTE_THREADS || a.k < 1 || a.k > 8)) {
+        set_error("vq_mfma: in-kernel routing is for pair mode, gate/up, E <= %d, k <= 8", ROUTE_THREADS);
+        return EINVAL_ARG;
+    }
+    const bool mb = code_bytes == 2 && ks == 1 && !rt;
     a.cblk = mb ? vq_cblk(nbt) : 1;
     const dim3 grid((unsigned)ceil_div(nbt, a.cblk), (unsigned)ntiles);
+#define KMI_VQM_GO(CB_, NS_, LW_, KS_, MB_, RT_)                                                  \
+    {                                                                                            \
+        static bool attr = false;                                                                \
+        if (!attr) {                                                                             \
+            vq_allow_lds((const void*)vq_mfma<CB_, NS_, LW_, KS_, MB_, RT_>);                    \
+            attr = true;                                                                         \
+        }                                                                                        \
+        vq_mfma<CB_, NS_, LW_, KS_, MB_, RT_><<<grid, WG, lds, st>>>(a);                         \
+        return OK;                                                                               \
+    }
 #define KMI_VQM_ONE(CB_, NS_, LW_, KS_)                                                          \
     if (code_bytes == CB_ && nset == NS_ && lw == LW_ && ks == KS_) {                            \
         constexpr bool MB_ = CB_ == 2 && KS_ == 1;                                               \
-        static bool attr = false;                                                                \
-        if (!attr) {                                                                             \
-            (void)hipFuncSetAttribute((const void*)vq_mfma<CB_, NS_, LW_, KS_, MB_>,             \
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);   \
-            attr = true;                                                                         \
+        if constexpr (NS_ == 2) {                                                                \
+            if (rt) KMI_VQM_GO(CB_, NS_, LW_, KS_, false, true)                                  \
         }                                                                                        \
-        vq_mfma<CB_, NS_, LW_, KS_, MB_><<<grid, WG, lds, st>>>(a);                              \
-        return OK;                                                                               \
+        KMI_VQM_GO(CB_, NS_, LW_, KS_, MB_, false)                                               \
     }
 #define KMI_VQM_LAUNCH(CB_, LW_, KS_) KMI_VQM_ONE(CB_, 1, LW_, KS_) KMI_VQM_ONE(CB_, 2, LW_, KS_)
     KMI_VQM_SHAPES(KMI_VQM_LAUNCH)
 #undef KMI_VQM_LAUNCH
 #undef KMI_VQM_ONE
+#undef KMI_VQM_GO
     set_error("vq_mfma: no kernel for K=%lld, %d-byte codes", (long long)a.K, code_bytes);
     return EINVAL_ARG;
 }

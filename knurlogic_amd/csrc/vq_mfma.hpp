@@ -27,6 +27,13 @@ struct VqmArgs {
     int64_t N, K, erows;
     int tile_rows;              // largest tile count the launch stages (<= 16): sizes the LDS
     int cblk;                   // column blocks per workgroup (set by launch_vq_mfma)
+    // pair mode with router logits: each workgroup routes its pair's token
+    // (route.hpp, the router kernel's arithmetic) in place of reading rhs,
+    // and column block 0 writes the pair's expert and score
+    const uint16_t* logits;     // [X, E] bf16, or null
+    int32_t* inds_out;          // [X * k] experts (read by the down kernel)
+    uint16_t* scores_out;       // [X * k] bf16 scores
+    int k;                      // slots per token (pair = token * k + slot)
 };
 
 size_t vq_mfma_lds(int64_t K, int kc, bool two_cb, int tile_rows, int nset, int ks);

@@ -26,7 +26,7 @@ import torch
 
 from .ops import (add_bias, gather_qmm, linear, moe_combine, moe_experts, moe_route,
                   moe_shared_add, quantize, quantized_matmul, swiglu, switch_glu, switch_glu_mx, vq_gather_qmm,
-                  vq_glu, vq_packed_gather_qmm, vq_packed_glu, vq_packed_switch_glu, vq_switch_glu)
+                  vq_experts, vq_glu, vq_packed_gather_qmm, vq_packed_glu, vq_packed_switch_glu, vq_switch_glu)
 
 
 class Linear:
@@ -277,6 +277,15 @@ class VQSwitchGLU:
         if self._packed():
             return self._packed_one_call(x, indices, scores)
         return vq_switch_glu(x, indices, *self._mats(), self.gate_proj.scale_group, scores=scores)
+
+    def experts(self, x, logits, k: int):
+        """Route (the router of ``moe_route``), SwitchGLU and the weighted
+        combine from router logits in one library call.  Returns (out,
+        inds, scores)."""
+        if self._packed():
+            inds, scores = moe_route(logits, k)
+            return self._packed_one_call(x, inds, scores), inds, scores
+        return vq_experts(x, logits, k, *self._mats(), self.gate_proj.scale_group)
 
     def _packed_one_call(self, x, indices, scores=None):
         g, u, d = self.gate_proj, self.up_proj, self.down_proj

@@ -1061,3 +1061,42 @@ def vq_switch_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, down, scale_
                                         DTYPE_CODE[x.dtype], _ptr(out), _ptr(ws), nbytes, _stream(x)),
                "vq_switch_glu")
     return out
+
+
+def vq_experts(x: torch.Tensor, logits: torch.Tensor, k: int, gate, up, down, scale_group: int = 0):
+    """The VQ experts of a SparseMoeBlock from its router logits in one
+    library call (kmi_vq_experts): route (as ``moe_route``), VQ SwitchGLU,
+    weighted combine.  x [..., H] and logits [..., E] bf16; gate / up / down
+    = (codes, codebook, scales).  Returns (out [..., H], inds [..., k]
+    int32, scores [..., k])."""
+    (cg, bg, sg_), (cu, bu, su), (cd, bd, sd) = gate, up, down
+    cbytes, kc, dim = _vq_operands(cg, bg, sg_)
+    if (_vq_operands(cu, bu, su) != (cbytes, kc, dim) or _vq_operands(cd, bd, sd) != (cbytes, kc, dim)
+            or cu.shape != cg.shape):
+        raise ValueError("vq_experts: gate, up and down differ in layout")
+    _on_gpu(x, logits, cg, bg, sg_, cu, bu, su, cd, bd, sd)
+    if x.dtype != torch.bfloat16 or logits.dtype != torch.bfloat16:
+        raise ValueError("vq_experts: bfloat16 activations and logits only")
+    lead, H = tuple(x.shape[:-1]), x.shape[-1]
+    if tuple(logits.shape[:-1]) != lead:
+        raise ValueError("vq_experts: logits [..., E] must match x [..., H]")
+    E, I = cg.shape[0], cg.shape[1]
+    if logits.shape[-1] != E:
+        raise ValueError(f"vq_experts: {logits.shape[-1]} logits for {E} experts")
+    if cd.shape[0] != E or cd.shape[1] != H or cd.shape[2] * dim != I:
+        raise ValueError(f"vq_experts: down codes {tuple(cd.shape)} do not match [E, H, I/dim]")
+    T = math.prod(lead)
+    out = torch.empty(*lead, H, dtype=x.dtype, device=x.device)
+    inds = torch.empty(*lead, k, dtype=torch.int32, device=x.device)
+    scores = torch.empty(*lead, k, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out, inds, scores
+    xc, lc = x.reshape(T, H).contiguous(), logits.reshape(T, E).contiguous()
+    ops = [t.contiguous() for t in (cg, sg_, bg, cu, su, bu, cd, sd, bd)]
+    L = _lib()
+    nbytes = L.kmi_vq_switch_glu_workspace_bytes(T, H, I, k)
+    ws = _workspace(nbytes, x.device)
+    _abi.check(L.kmi_vq_experts(_ptr(xc), _ptr(lc), T, H, I, k, *[_ptr(t) for t in ops], cbytes, kc, dim,
+                                scale_group, E, DTYPE_CODE[x.dtype], _ptr(out), _ptr(inds), _ptr(scores), _ptr(ws),
+                                nbytes, _stream(x)), "vq_experts")
+    return out, inds, scores

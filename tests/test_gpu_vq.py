@@ -176,3 +176,29 @@ def test_vq_switch_glu_repeats_bit_for_bit(dev, T, kc):
     ys = [glu(x, inds) for _ in range(4)]
     for y in ys[1:]:
         assert torch.equal(y, ys[0])
+
+
+@pytest.mark.parametrize("T,E,kc", [(1, 128, 256), (1, 128, 4096), (1, 300, 256), (3, 128, 4096), (16, 128, 256)])
+def test_vq_experts_from_logits(dev, T, E, kc):
+    """vq_experts (route, VQ SwitchGLU, combine in one call; at one token and
+    E <= 256 the gate/up kernel routes the token itself) gives the routing of
+    moe_route and the output of the separate route and combine calls, bit
+    for bit, and that output matches the oracle's routed SwitchGLU."""
+    rng = np.random.default_rng(11 * T + E + kc)
+    H, I, k = 2048, 768, 8
+    (hg, gg), (hu, gu), (hd, gd) = [_vq(rng, E, n, kd, kc, 0, dev) for n, kd in ((I, H), (I, H), (H, I))]
+    glu = nn.VQSwitchGLU(*(nn.VQSwitchLinear(*g) for g in (gg, gu, gd)))
+    x, lg = bf16_normal(rng, (T, H)), bf16_normal(rng, (T, E))
+    tx, tl = to_torch(x, dev, BF), to_torch(lg, dev, BF)
+    out, inds, scores = glu.experts(tx, tl, k)
+    ri, rs = K.moe_route(tl, k)
+    assert torch.equal(inds, ri) and torch.equal(scores, rs), "routing differs from moe_route"
+    assert torch.equal(out, glu.combine(tx, ri, rs)), "one call and route + combine differ"
+    oi, osc = O.route(lg, k)
+    assert np.array_equal(to_numpy(inds), oi)
+    fn = lambda h: (lambda xs, e: O.vq_matmul(xs, h[0][e], h[1], h[2][e], 0, "bfloat16"))
+    ref = O.combine(O.switch_glu(x, oi, fn(hg), fn(hu), fn(hd)), osc)
+    assert_close(to_numpy(out), ref, what="vq experts")
+    # a second call on the same inputs repeats the bits
+    again, _, _ = glu.experts(tx, tl, k)
+    assert torch.equal(again, out)
