@@ -364,8 +364,7 @@ def bench_vq_packed(T, calls, dev, dim=4, kc=2048, group=64, H=None, I=None):
 
     def run():
         for i in range(calls):
-            ii, sc = KA.moe_route(logits, k)
-            glus[i % n].combine(x, ii, sc)
+            glus[i % n].experts(x, logits, k)
 
     us = time_graph(run) / calls * 1e3
     nbytes = distinct * per_e + kc * dim * 2 + 2 * 2 * T * H

@@ -509,6 +509,24 @@ int kmi_vq_packed_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int
                              const void* codebook_down, int pack_bits, int kc, int dim, int group, int64_t E,
                              int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * The packed VQ experts of a SparseMoeBlock from its router logits, in one
+ * call (qwen3_5.py:174-182 over the artifact's packed VQSwitchLinear
+ * experts): the router of kmi_moe_route (inds [T, k] int32 and scores
+ * [T, k] bf16 written, bit for bit as kmi_moe_route gives them), then
+ * kmi_vq_packed_switch_glu with the weighted combine into out [T, H].
+ * logits [T, E] bf16.  Up to 16 (token, slot) pairs with E <= 256 the
+ * gate/up kernel routes each pair's token itself (no router launch);
+ * otherwise it routes first.
+ * k <= 8, E <= 1024.  workspace: kmi_vq_packed_switch_glu_workspace_bytes.
+ */
+int kmi_vq_packed_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k,
+                          const uint32_t* codes_gate, const void* scales_gate, const void* codebook_gate,
+                          const uint32_t* codes_up, const void* scales_up, const void* codebook_up,
+                          const uint32_t* codes_down, const void* scales_down, const void* codebook_down,
+                          int pack_bits, int kc, int dim, int group, int64_t E, int dtype, void* out,
+                          int32_t* inds, void* scores, void* workspace, size_t workspace_bytes, void* stream);
+
 int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
                       const void* scores, const void* codes_gate, const void* scales_gate,
                       const void* codebook_gate, const void* codes_up, const void* scales_up,

@@ -59,6 +59,8 @@ SIGNATURES = {
     "kmi_vq_experts": (I, [P, P, I64, I64, I64, I, P, P, P, P, P, P, P, P, P, I, I, I, I, I64, I, P, P, P,
                            P, SZ, P]),
     "kmi_vq_packed_switch_glu_workspace_bytes": (SZ, [I64, I64, I64, I]),
+    "kmi_vq_packed_experts": (I, [P, P, I64, I64, I64, I, P, P, P, P, P, P, P, P, P, I, I, I, I, I64, I, P, P,
+                                  P, P, SZ, P]),
     "kmi_vq_packed_switch_glu": (I, [P, I64, I64, I64, I, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I64, I,
                                      P, P, SZ, P]),
     "kmi_read_probe": (I, [P, I64, I, P, P]),

@@ -46,6 +46,15 @@ void clear_error();
 // that float for e in 1..254; e = 0 (2^-127, the subnormal 0x00400000) and
 // e = 255 (NaN, 0x7fc00000) are e << 23 with bit 22 set, and exactly these
 // two values have (e + 1) & 0xfe == 0.
+// Lets kernel f take all the LDS its static allocation leaves (160 KB per
+// workgroup on gfx950), and leaves no error behind for the launch check.
+inline void allow_dynamic_lds(const void* f) {
+    hipFuncAttributes fa = {};
+    const size_t stat = hipFuncGetAttributes(&fa, f) == hipSuccess ? fa.sharedSizeBytes : 0;
+    (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(160 * 1024 - stat));
+    (void)hipGetLastError();
+}
+
 __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
     e &= 0xffu;
     const uint32_t special = ((((e + 1u) & 0xfeu) - 1u) >> 31) << 22;

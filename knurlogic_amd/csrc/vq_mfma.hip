@@ -384,16 +384,6 @@ bool vq_mfma_supported(int64_t K, int code_bytes, int kc, bool two_cb) {
     return any && vq_mfma_lds(K, kc, two_cb, TM, 2, 4) <= 160 * 1024;
 }
 
-// Lets a kernel take all of the LDS its static allocation leaves (the
-// router's state is static in the routing variants), and leaves no error
-// behind for the launch check.
-static void vq_allow_lds(const void* f) {
-    hipFuncAttributes fa = {};
-    const size_t stat = hipFuncGetAttributes(&fa, f) == hipSuccess ? fa.sharedSizeBytes : 0;
-    (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(160 * 1024 - stat));
-    (void)hipGetLastError();
-}
-
 // column blocks per workgroup for 2-byte codes without a K split: 4, so a
 // workgroup's 64 KB codebook staging and x staging serve 256 weight rows
 // (measured at 128 experts, 16 tokens, 4096 x 8: 103 -> 90 us); 1-byte codes
@@ -434,6 +424,10 @@ int launch_vq_mfma(const VqmArgs& a_in, int code_bytes, int nset, int64_t ntiles
         set_error("vq_mfma: in-kernel routing is for pair mode, gate/up, E <= %d, k <= 8", ROUTE_THREADS);
         return EINVAL_ARG;
     }
+    if (lds + (rt ? sizeof(RouteLdsT<ROUTE_THREADS>) : 0) > 160 * 1024) {   // the router's state is static LDS
+        set_error("vq_mfma: %zu bytes of LDS", lds);
+        return EINVAL_ARG;
+    }
     const bool mb = code_bytes == 2 && ks == 1 && !rt;
     a.cblk = mb ? vq_cblk(nbt) : 1;
     const dim3 grid((unsigned)ceil_div(nbt, a.cblk), (unsigned)ntiles);
@@ -441,7 +435,7 @@ int launch_vq_mfma(const VqmArgs& a_in, int code_bytes, int nset, int64_t ntiles
     {                                                                                            \
         static bool attr = false;                                                                \
         if (!attr) {                                                                             \
-            vq_allow_lds((const void*)vq_mfma<CB_, NS_, LW_, KS_, MB_, RT_>);                    \
+            allow_dynamic_lds((const void*)vq_mfma<CB_, NS_, LW_, KS_, MB_, RT_>);                    \
             attr = true;                                                                         \
         }                                                                                        \
         vq_mfma<CB_, NS_, LW_, KS_, MB_, RT_><<<grid, WG, lds, st>>>(a);                         \

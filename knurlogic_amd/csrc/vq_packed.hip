@@ -24,6 +24,7 @@
 #include "common.hpp"
 #include "qgemv.hpp"
 #include "vq_packed_mfma.hpp"
+#include "route.hpp"
 #include "../../include/knurlogic_amd.h"
 
 #include <cstdlib>
@@ -47,6 +48,14 @@ struct VpArgs {
     int64_t E, N, K, W;         // W: words per row
     int group;
     uint16_t* y;                // [R, N] bf16
+    // In-kernel routing (gate/up over one token's pairs, rows_div = k): each
+    // workgroup routes its pair's token from logits [X, E] bf16 (route.hpp,
+    // E <= 256) in place of reading experts; column block 0 writes the
+    // pair's expert and score.
+    const uint16_t* logits;
+    int32_t* inds_out;
+    uint16_t* scores_out;
+    int k;
 };
 
 __device__ __forceinline__ float vp_dot2(uint32_t a, uint32_t b, float acc) {
@@ -106,8 +115,10 @@ __global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x;
     const int64_t r = blockIdx.y;
-    const int e = a.experts[r];
-    const bool ok_e = e >= 0 && e < a.E;
+    const bool route = a.logits != nullptr;
+    int e = route ? 0 : a.experts[r];
+    float rlog[1];
+    if (route) route_load<TBF16, 1>(a.logits + (r / a.k) * a.E, (int)a.E, rlog);
     const int64_t xrow = a.rows ? (int64_t)a.rows[r] : r / a.rows_div;
     const bool ok_x = xrow >= 0 && xrow < a.X;
     const bool two_cb = a.nset == 2 && a.cb[1] != a.cb[0];
@@ -167,6 +178,21 @@ __global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the direct-to-LDS writes have landed
     __syncthreads();
+    // past the codebooks and x (16-byte aligned): the router's state when
+    // routing (the host sizes the LDS for it only then)
+    unsigned char* extra = smem + (((size_t)cbb * 1024 * (two_cb ? 2 : 1) + (size_t)((nsub + 31) / 32) * XBS * 2 + 15) &
+                                   ~(size_t)15);
+    if (route) {     // once the codebook and x are staged (uniform branch: every thread routes)
+        RouteLdsT<ROUTE_THREADS>& rsm = *(RouteLdsT<ROUTE_THREADS>*)extra;
+        route_from<TBF16, 1>(rlog, (int)a.E, a.k, rsm);
+        const int s = (int)(r % a.k);
+        e = __builtin_amdgcn_readfirstlane(rsm.sel_e[s]);
+        if (blockIdx.x == 0 && tid == 0) {
+            a.inds_out[r] = e;
+            a.scores_out[r] = f32_to_bf16(rsm.sel_p[s]);
+        }
+    }
+    const bool ok_e = e >= 0 && e < a.E;
 
     const int64_t row = (int64_t)blockIdx.x * RPWG + tid / SEG;
     const int seg = tid % SEG;
@@ -254,8 +280,7 @@ static int launch_vp3(const VpArgs& a, int seg, size_t lds, hipStream_t st) {
     if (seg == S_) {                                                                                    \
         static bool attr = false;                                                                       \
         if (!attr) {                                                                                    \
-            (void)hipFuncSetAttribute((const void*)vq_packed_gemv<PB, DIM, GPB, S_>,                    \
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);          \
+            allow_dynamic_lds((const void*)vq_packed_gemv<PB, DIM, GPB, S_>);                           \
             attr = true;                                                                                \
         }                                                                                               \
         const dim3 grid((unsigned)ceil_div(a.N, 256 / S_), (unsigned)a.R);                              \
@@ -305,13 +330,26 @@ static int vp_check(int dtype, int pack_bits, int kc, int dim, int group, int64_
     return OK;
 }
 
+// LDS of vq_packed_gemv: the codebook(s) and x, then (16-byte aligned) the
+// router's state when it routes
+static size_t vp_lds(int64_t K, int kc, int dim, bool two_cb, bool route) {
+    const int64_t nblk = (K / dim + 31) / 32;
+    size_t b = (size_t)vp_cb_blocks(kc, dim) * 1024 * (two_cb ? 2 : 1) + (size_t)nblk * 33 * dim * 2;
+    if (route) b = ((b + 15) & ~(size_t)15) + sizeof(RouteLdsT<ROUTE_THREADS>);
+    return b;
+}
+
 static int run_vp(VpArgs& a, int pack_bits, int dim, hipStream_t st) {
     const int64_t nsub = a.K / dim, nblk = (nsub + 31) / 32;
     const int fpg = a.group / dim;
     const int gpb = fpg >= 32 ? 1 : 32 / fpg;
     const int seg = vp_seg(nblk);
     const bool two_cb = a.nset == 2 && a.cb[1] != a.cb[0];
-    const size_t lds = (size_t)vp_cb_blocks(a.kc, dim) * 1024 * (two_cb ? 2 : 1) + (size_t)nblk * 33 * dim * 2;
+    const size_t lds = vp_lds(a.K, a.kc, dim, two_cb, a.logits != nullptr);
+    if (lds > 160 * 1024) {
+        set_error("vq (packed): %zu bytes of LDS", lds);
+        return EINVAL_ARG;
+    }
     int rc;
     switch (pack_bits) {
         case 8: rc = launch_vp_pb<8>(a, dim, gpb, seg, lds, st); break;
@@ -392,13 +430,35 @@ size_t kmi_vq_packed_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I,
     return vps_act_bytes(P, I) + vps_y_bytes(P, H) + sort_index_bytes(P, 4096, 1);
 }
 
-int kmi_vq_packed_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
-                             const void* scores, const uint32_t* codes_gate, const void* scales_gate,
-                             const void* codebook_gate, const uint32_t* codes_up, const void* scales_up,
-                             const void* codebook_up, const uint32_t* codes_down, const void* scales_down,
-                             const void* codebook_down, int pack_bits, int kc, int dim, int group, int64_t E,
-                             int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream) {
-    clear_error();
+}  // extern "C"
+
+// Below 17 (token, slot) pairs (or where the expert-tile kernel does not
+// cover the shape) each pair runs on its own; beyond, rows are grouped by
+// expert.
+static bool vps_grouped(int64_t P, int64_t E, int pack_bits, int dim, int group, int64_t H, int64_t I, int kc,
+                        bool two_cb) {
+    return P > 16 && E <= 4096 && vpm_supported(pack_bits, dim, group, H, kc, two_cb) &&
+           vpm_supported(pack_bits, dim, group, I, kc, false);
+}
+
+// In-kernel routing: the per-pair path, E <= 256, k <= 8, and the router's
+// state beside the gate/up kernel's codebooks and x in the LDS.
+static bool vps_route_fits(int64_t P, int64_t E, int k, int pack_bits, int dim, int group, int64_t H, int64_t I,
+                           int kc, bool two_cb) {
+    return E <= ROUTE_THREADS && k >= 1 && k <= 8 && !vps_grouped(P, E, pack_bits, dim, group, H, I, kc, two_cb) &&
+           vp_lds(H, kc, dim, two_cb, true) <= 160 * 1024;
+}
+
+// The packed SwitchGLU.  With logits (per-pair path, E <= 256, k <= 8) the
+// gate/up kernel routes each pair's token and writes inds / scores, which
+// the down kernel and the combine read.
+static int vps_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                               const void* scores, const uint32_t* codes_gate, const void* scales_gate,
+                               const void* codebook_gate, const uint32_t* codes_up, const void* scales_up,
+                               const void* codebook_up, const uint32_t* codes_down, const void* scales_down,
+                               const void* codebook_down, int pack_bits, int kc, int dim, int group, int64_t E,
+                               int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream,
+                               const void* logits) {
     int rc = vp_check(dtype, pack_bits, kc, dim, group, H, I, E);
     if (rc) return rc;
     rc = vp_check(dtype, pack_bits, kc, dim, group, I, H, E);
@@ -423,8 +483,11 @@ int kmi_vq_packed_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int
     // Expert-major on MFMA beyond 16 pairs where the kernel covers the shape
     // (pairs that share an expert then share its decode); per pair below.
     const bool two_cb = codebook_up != codebook_gate;
-    const bool grouped = P > 16 && E <= 4096 && vpm_supported(pack_bits, dim, group, H, kc, two_cb) &&
-                         vpm_supported(pack_bits, dim, group, I, kc, false);
+    const bool grouped = vps_grouped(P, E, pack_bits, dim, group, H, I, kc, two_cb);
+    if (logits && !vps_route_fits(P, E, k, pack_bits, dim, group, H, I, kc, two_cb)) {
+        set_error("vq_packed_switch_glu: in-kernel routing is for the per-pair path, E <= %d, k <= 8", ROUTE_THREADS);
+        return EINVAL_ARG;
+    }
     if (grouped) {
         const int64_t avg = ceil_div(P, E < P ? E : P);
         // tiles sized to the rows an expert sees: the LDS holds a tile's x rows,
@@ -466,6 +529,12 @@ int kmi_vq_packed_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int
         g.sc[0] = (const uint16_t*)scales_gate; g.sc[1] = (const uint16_t*)scales_up;
         g.cb[0] = (const uint16_t*)codebook_gate; g.cb[1] = (const uint16_t*)codebook_up;
         g.nset = 2; g.kc = kc; g.E = E; g.N = I; g.K = H; g.W = Wg; g.group = group; g.y = act;
+        if (logits) {
+            g.logits = (const uint16_t*)logits;
+            g.inds_out = (int32_t*)inds;
+            g.scores_out = (uint16_t*)scores;
+            g.k = k;
+        }
         rc = run_vp(g, pack_bits, dim, st);
         if (rc) return rc;
         VpArgs d = {};
@@ -479,6 +548,45 @@ int kmi_vq_packed_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int
     }
     if (scores) return kmi_moe_combine(y, scores, dtype, T, k, H, out, stream);
     return OK;
+}
+
+extern "C" {
+
+int kmi_vq_packed_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
+                             const void* scores, const uint32_t* codes_gate, const void* scales_gate,
+                             const void* codebook_gate, const uint32_t* codes_up, const void* scales_up,
+                             const void* codebook_up, const uint32_t* codes_down, const void* scales_down,
+                             const void* codebook_down, int pack_bits, int kc, int dim, int group, int64_t E,
+                             int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    return vps_switch_glu_impl(x, T, H, I, k, inds, scores, codes_gate, scales_gate, codebook_gate, codes_up,
+                               scales_up, codebook_up, codes_down, scales_down, codebook_down, pack_bits, kc, dim,
+                               group, E, dtype, out, workspace, workspace_bytes, stream, nullptr);
+}
+
+int kmi_vq_packed_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k,
+                          const uint32_t* codes_gate, const void* scales_gate, const void* codebook_gate,
+                          const uint32_t* codes_up, const void* scales_up, const void* codebook_up,
+                          const uint32_t* codes_down, const void* scales_down, const void* codebook_down,
+                          int pack_bits, int kc, int dim, int group, int64_t E, int dtype, void* out,
+                          int32_t* inds, void* scores, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    KMI_CHECK_ARG(dtype == BF16, "vq_packed_experts: only bfloat16 activations and logits are implemented");
+    KMI_CHECK_ARG(E >= 1 && E <= ROUTE_MAX_E && k >= 1 && k <= 8 && k <= E,
+                  "vq_packed_experts: top-%d of %lld experts (k <= 8, E <= %d)", k, (long long)E, ROUTE_MAX_E);
+    KMI_CHECK_ARG(T >= 0, "vq_packed_experts: T=%lld", (long long)T);
+    if (T == 0) return OK;
+    KMI_CHECK_ARG(logits && inds && scores, "vq_packed_experts: null pointer");
+    const bool two_cb = codebook_up != codebook_gate;
+    const bool in_kernel = vps_route_fits(T * k, E, k, pack_bits, dim, group, H, I, kc, two_cb);
+    if (!in_kernel) {
+        const int rc = kmi_moe_route(logits, dtype, T, (int)E, k, inds, scores, stream);
+        if (rc) return rc;
+    }
+    return vps_switch_glu_impl(x, T, H, I, k, inds, scores, codes_gate, scales_gate, codebook_gate, codes_up,
+                               scales_up, codebook_up, codes_down, scales_down, codebook_down, pack_bits, kc, dim,
+                               group, E, dtype, out, workspace, workspace_bytes, stream,
+                               in_kernel ? logits : nullptr);
 }
 
 }  // extern "C"

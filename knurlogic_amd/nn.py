@@ -26,7 +26,8 @@ import torch
 
 from .ops import (add_bias, gather_qmm, linear, moe_combine, moe_experts, moe_route,
                   moe_shared_add, quantize, quantized_matmul, swiglu, switch_glu, switch_glu_mx, vq_gather_qmm,
-                  vq_experts, vq_glu, vq_packed_gather_qmm, vq_packed_glu, vq_packed_switch_glu, vq_switch_glu)
+                  vq_experts, vq_glu, vq_packed_experts, vq_packed_gather_qmm, vq_packed_glu, vq_packed_switch_glu,
+                  vq_switch_glu)
 
 
 class Linear:
@@ -283,8 +284,11 @@ class VQSwitchGLU:
         combine from router logits in one library call.  Returns (out,
         inds, scores)."""
         if self._packed():
-            inds, scores = moe_route(logits, k)
-            return self._packed_one_call(x, inds, scores), inds, scores
+            g, u, d = self.gate_proj, self.up_proj, self.down_proj
+            if not (g.pack_bits == u.pack_bits == d.pack_bits) or not (g.scale_group == u.scale_group == d.scale_group):
+                raise ValueError("VQSwitchGLU: gate, up and down must share the packed layout")
+            return vq_packed_experts(x, logits, k, (g.codes, g.codebook, g.scales), (u.codes, u.codebook, u.scales),
+                                     (d.codes, d.codebook, d.scales), g.pack_bits, g.scale_group)
         return vq_experts(x, logits, k, *self._mats(), self.gate_proj.scale_group)
 
     def _packed_one_call(self, x, indices, scores=None):

@@ -982,6 +982,45 @@ def vq_packed_switch_glu(x: torch.Tensor, indices: torch.Tensor, gate, up, down,
     return out
 
 
+def vq_packed_experts(x: torch.Tensor, logits: torch.Tensor, k: int, gate, up, down, pack_bits: int, group: int):
+    """The packed VQ experts of a SparseMoeBlock from its router logits in one
+    library call (kmi_vq_packed_experts): route (as ``moe_route``), packed
+    VQ SwitchGLU, weighted combine.  x [..., H] and logits [..., E] bf16;
+    gate / up / down = (codes, codebook, scales).  Returns (out [..., H],
+    inds [..., k] int32, scores [..., k])."""
+    _on_gpu(x, logits, *gate, *up, *down)
+    if x.dtype != torch.bfloat16 or logits.dtype != torch.bfloat16:
+        raise ValueError("vq_packed_experts: bfloat16 activations and logits only")
+    H = x.shape[-1]
+    kc, dim = _vq_packed_operands(gate[0], gate[1], gate[2], pack_bits, group, H, "vq_packed_experts")
+    _vq_packed_operands(up[0], up[1], up[2], pack_bits, group, H, "vq_packed_experts")
+    if up[0].shape != gate[0].shape or up[1].shape != gate[1].shape:
+        raise ValueError("vq_packed_experts: gate and up differ in shape")
+    E, I = gate[0].shape[0], gate[0].shape[1]
+    kd, dd = _vq_packed_operands(down[0], down[1], down[2], pack_bits, group, I, "vq_packed_experts")
+    if down[0].shape[0] != E or down[0].shape[1] != H or kd != kc or dd != dim:
+        raise ValueError("vq_packed_experts: down must be [E, H, *] over I inputs with gate's codebook shape")
+    lead = tuple(x.shape[:-1])
+    if tuple(logits.shape) != lead + (E,):
+        raise ValueError(f"vq_packed_experts: logits must be [..., {E}] over x's leading dimensions")
+    T = math.prod(lead)
+    out = torch.empty(*lead, H, dtype=x.dtype, device=x.device)
+    inds = torch.empty(*lead, k, dtype=torch.int32, device=x.device)
+    scores = torch.empty(*lead, k, dtype=x.dtype, device=x.device)
+    if T == 0:
+        return out, inds, scores
+    xc, lc = x.reshape(T, H).contiguous(), logits.reshape(T, E).contiguous()
+    g, u, d = (tuple(t.contiguous() for t in m) for m in (gate, up, down))
+    L = _lib()
+    nbytes = L.kmi_vq_packed_switch_glu_workspace_bytes(T, H, I, k)
+    ws = _workspace(nbytes, x.device)
+    _abi.check(L.kmi_vq_packed_experts(
+        _ptr(xc), _ptr(lc), T, H, I, k, _ptr(g[0]), _ptr(g[2]), _ptr(g[1]), _ptr(u[0]), _ptr(u[2]), _ptr(u[1]),
+        _ptr(d[0]), _ptr(d[2]), _ptr(d[1]), pack_bits, kc, dim, group, E, DTYPE_CODE[x.dtype], _ptr(out),
+        _ptr(inds), _ptr(scores), _ptr(ws), nbytes, _stream(x)), "vq_packed_experts")
+    return out, inds, scores
+
+
 def _vq_indices(x, E, lhs_indices, rhs_indices):
     dev = x.device
     xbatch = tuple(x.shape[:-2])

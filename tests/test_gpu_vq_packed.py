@@ -223,3 +223,51 @@ def test_a_written_artifact_loads_and_matches_the_oracle(dev, tmp_path):
     ref = np.stack([O.vq_packed_matmul(xv[p], host[0][rhs[p]], host[1], host[2][rhs[p]], bits, group, "float32")
                     for p in range(2)])
     assert_close(to_numpy(gv), ref, what="loaded vq")
+
+
+@pytest.mark.parametrize("T,E,H,I,dim", [(1, 128, 2048, 768, 4), (1, 128, 2816, 704, 2), (2, 128, 2048, 768, 4),
+                                         (1, 300, 512, 256, 4), (3, 128, 2048, 768, 4)])
+def test_packed_experts_from_logits(dev, T, E, H, I, dim):
+    """vq_packed_experts (route, packed SwitchGLU, combine in one call; up to
+    16 pairs with E <= 256 the gate/up kernel routes each pair's token) gives
+    moe_route's routing and the bits of the separate route, SwitchGLU and
+    moe_combine calls, and matches
+    the oracle's routed SwitchGLU and combine.  Random 11-bit words (every
+    field a codebook entry)."""
+    k, kc, bits, group = 8, 2048, 11, 64
+    rng = np.random.default_rng(40 + 7 * T + E + dim)
+    g = torch.Generator(device=dev).manual_seed(40 + T + E)
+    cb = (rng.standard_normal((kc, dim)) * 0.3).astype(np.float16)
+    tcb = torch.from_numpy(cb).to(dev)
+
+    def mat(N, IN):
+        W = (IN // dim + 31) // 32 * bits
+        words = torch.randint(-2 ** 31, 2 ** 31 - 1, (E, N, W), device=dev, generator=g,
+                              dtype=torch.int32).view(torch.uint32)
+        sc = (torch.rand(E, N, IN // group, device=dev, generator=g) + 0.5).to(torch.float16)
+        return words, sc
+
+    mats = [mat(I, H), mat(I, H), mat(H, I)]
+    mods = [nn.VQSwitchLinear(w, tcb, sc, scale_group=group, pack_bits=bits, in_features=IN)
+            for (w, sc), IN in zip(mats, (H, H, I))]
+    glu = nn.VQSwitchGLU(*mods)
+    x, lg = bf16_normal(rng, (T, H)), bf16_normal(rng, (T, E))
+    tx, tl = to_torch(x, dev, BF), to_torch(lg, dev, BF)
+    out, inds, scores = glu.experts(tx, tl, k)
+    ri, rs = K.moe_route(tl, k)
+    assert torch.equal(inds, ri) and torch.equal(scores, rs), "routing differs from moe_route"
+    y = glu(tx, ri)
+    assert torch.equal(out, glu.combine(tx, ri, rs)), "one call and route + combine differ"
+    assert torch.equal(out, K.moe_combine(y, rs)), "the down kernel's combine differs from moe_combine"
+    oi, osc = O.route(lg, k)
+    assert np.array_equal(to_numpy(inds), oi)
+    used = sorted(set(oi.reshape(-1).tolist()))
+    host = [{e: (w[e].view(torch.int32).cpu().numpy().view(np.uint32), sc[e].float().cpu().numpy())
+             for e in used} for w, sc in mats]
+    cbf = cb.astype(np.float32)
+    fn = lambda h: (lambda xs, e: O.vq_packed_matmul(xs, h[e][0], cbf, h[e][1], bits, group, "bfloat16"))
+    ref = O.switch_glu(x, oi, *(fn(h) for h in host))
+    assert_close(to_numpy(y), ref, what="packed experts y")
+    assert_close(to_numpy(out), O.combine(ref, osc), what="packed experts combine")
+    again, _, _ = glu.experts(tx, tl, k)
+    assert torch.equal(again, out)
