@@ -401,8 +401,9 @@ int kmi_switch_glu_mx(const void* x, int64_t T, int64_t H, int64_t I, int k, con
  * weighted combine.  logits [T, E] bf16; inds [T, k] int32 and scores
  * [T, k] bf16 are written (the routing, as kmi_moe_route gives it bit for
  * bit); out [T, H] bf16; the weights as kmi_switch_glu takes them.  At
- * decode sizes (T * k <= 16, E <= 256) the gate/up kernel routes its own
- * token, so the call is two kernel launches; otherwise it routes first.
+ * decode sizes (up to 64 (token, slot) pairs, E <= 256) the gate/up kernel
+ * routes its own token, so the call is two kernel launches; otherwise it
+ * routes first.
  * k <= 8, E <= 1024.  workspace: kmi_switch_glu_workspace_bytes.
  */
 int kmi_moe_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k, int64_t E,

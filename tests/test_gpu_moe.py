@@ -187,7 +187,7 @@ def test_sparse_moe_block_matches_the_oracle(dev, T):
     assert_close(to_numpy(block.experts(to_torch(x, dev, BF), tl)), y, what="experts")
 
 
-@pytest.mark.parametrize("T", [1, 2, 5, 8, 9, 16])
+@pytest.mark.parametrize("T", [1, 2, 5, 8, 9, 16, 64, 65])
 def test_moe_experts_routes_in_the_kernel_like_the_router(dev, T):
     """kmi_moe_experts (one call from the router logits): at decode sizes
     the gate/up kernel routes each token itself.  The experts and scores
@@ -212,3 +212,4 @@ def test_moe_experts_routes_in_the_kernel_like_the_router(dev, T):
     # and the block's routed part takes this call
     block = nn.SparseMoeBlock(None, glu, k)
     assert torch.equal(block.experts(tx, tl), out)
+
