@@ -306,6 +306,201 @@ static int launch_vp_pb(const VpArgs& a, int dim, int gpb, int seg, size_t lds, 
     return EINVAL_ARG;
 }
 
+// ---- down projection + weighted combine for a few tokens, token-major ----
+// grid (ceil(N / rows per workgroup), T).  A workgroup owns a few output
+// rows of one token; lane (row r, slot s, segment g), SEG lanes per (row,
+// slot) as vq_packed_gemv puts them on a row (same blocks per lane, same
+// sums, same shuffle tree), so y[t*k+s, n] is the per-pair kernel's value
+// bit for bit; the token's k act rows are staged once.  Each slot's
+// round(y * score) meets in LDS and lane r sums them in slot order in
+// float64, rounded once: out[t, n], as moe_combine gives from those y.
+struct VpdArgs {
+    const uint16_t* act;        // [T*k, K] bf16 (pair-major)
+    const int32_t* inds;        // [T*k] expert per pair
+    const uint16_t* scores;     // [T*k] bf16
+    const uint32_t* codes;      // [E, N, W]
+    const uint16_t* sc;         // [E, N, K / group]
+    const uint16_t* cb;         // [kc, dim]
+    uint16_t* out;              // [T, N] bf16
+    int64_t E, N, K, W, T;
+    int k, kc, group, seg;
+};
+
+constexpr int VPD_SLOTS = 8;    // slots per token (k <= 8)
+
+template <int PB, int DIM, int GPB>
+__global__ __launch_bounds__(256) void vq_packed_down_tok(VpdArgs a) {
+    constexpr int FPG = 32 / GPB;
+    constexpr int XBS = 33 * DIM;                    // x block stride (elements), as vq_packed_gemv
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int SEG = a.seg, rpwg = 256 / (VPD_SLOTS * SEG);
+    const int g = tid % SEG, s = (tid / SEG) % VPD_SLOTS, r = tid / (VPD_SLOTS * SEG);
+    const int64_t t = blockIdx.y;
+    const int k = a.k;
+    const int64_t nsub = a.K / DIM, nblk = (nsub + 31) / 32;
+    const int64_t Kp = nblk * 32 * DIM;
+    const int cbytes = a.kc * DIM * 2, cbb = vp_cb_blocks(a.kc, DIM);
+    uint16_t* cbl = (uint16_t*)smem;
+    uint16_t* xl = (uint16_t*)(smem + (size_t)cbb * 1024);                    // [k][nblk * XBS]
+    float* prod = (float*)(smem + (size_t)cbb * 1024 + (size_t)k * nblk * XBS * 2);   // [rpwg][8]
+
+    // codebook (direct-to-LDS when whole 16-byte pieces) and the k act rows (fp16)
+    if (cbytes % 16 == 0) {
+        for (int j = wave; j < cbb; j += 4) {
+            const int p = j * 64 + lane;
+            vp_dma16(make_rsrc(a.cb, cbytes), smem + (size_t)j * 1024, p * 16 < cbytes ? (uint32_t)p * 16u : 0x80000000u);
+        }
+    } else {
+        const __amdgpu_buffer_rsrc_t rcb = make_rsrc(a.cb, cbytes);
+        for (int i = tid; i < cbytes / 4; i += 256)
+            *(uint32_t*)(cbl + 2 * i) = __builtin_amdgcn_raw_buffer_load_b32(rcb, i * 4, 0, 0);
+    }
+    {
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.act + t * k * a.K, (int64_t)k * a.K * 2);
+        const int nd = (int)(Kp / 2);                 // dwords per staged row
+        const int total = k * nd;
+        for (int i0 = tid; i0 < total; i0 += 256 * 8) {
+            uint32_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + 256 * u, j = i / nd, d = i - j * nd;
+                v[u] = __builtin_amdgcn_raw_buffer_load_b32(
+                    rx, i < total && 2 * d < a.K ? (int)((j * a.K + 2 * d) * 2) : (int)0x80000000u, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + 256 * u;
+                if (i < total) {
+                    const int j = i / nd, d = i - j * nd;
+                    const vp_f16x2 h = {(_Float16)bf16_to_f32((uint16_t)(v[u] & 0xffffu)),
+                                        (_Float16)bf16_to_f32((uint16_t)(v[u] >> 16))};
+                    const int e = 2 * d, blk = e / (32 * DIM);
+                    *(uint32_t*)(xl + (size_t)j * nblk * XBS + blk * XBS + (e - blk * 32 * DIM)) =
+                        __builtin_bit_cast(uint32_t, h);
+                }
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the direct-to-LDS writes have landed
+    __syncthreads();
+
+    const int64_t row = (int64_t)blockIdx.x * rpwg + r;
+    const bool slot_ok = s < k;
+    const int e = slot_ok ? a.inds[t * k + s] : -1;
+    const bool ok_e = e >= 0 && e < a.E;
+    const int64_t gpr = a.K / a.group, fpg = a.group / DIM;
+    const bool row_ok = ok_e && row < a.N;
+    // one view of all experts (a wave's lanes hold several slots, and a
+    // per-lane view would put every load in a loop over the wave's distinct
+    // views): the expert and row in the lane's 32-bit offset (the host keeps
+    // the codes under 2 GiB)
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(a.codes, a.E * a.N * a.W * 4);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.sc, a.E * a.N * gpr * 2);
+    const uint32_t erow = (uint32_t)((ok_e ? e : 0) * a.N + (row < a.N ? row : 0));
+    const uint32_t cro = erow * (uint32_t)a.W * 4u, sro = erow * (uint32_t)gpr * 2u;
+    const uint16_t* xs = xl + (size_t)(slot_ok ? s : 0) * nblk * XBS;
+    float tot = 0.f;
+    for (int b = g; b < (int)nblk; b += SEG) {
+        uint32_t w[PB + 1];
+#pragma unroll
+        for (int q = 0; q < PB; q++)
+            w[q] = __builtin_amdgcn_raw_buffer_load_b32(
+                rc, row_ok ? (int)(cro + (uint32_t)(b * PB + q) * 4u) : (int)0x80000000u, 0, AUX_NT);
+        w[PB] = 0;
+        float sv[GPB];
+#pragma unroll
+        for (int gg = 0; gg < GPB; gg++) {
+            const int gi = (int)((b * 32 + gg * FPG) / fpg);
+            sv[gg] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(
+                rs, row_ok ? (int)(sro + (uint32_t)gi * 2u) : (int)0x80000000u, 0, 0));
+        }
+        const int64_t f0 = b * 32;
+        const int nvalid = (int)(nsub - f0 < 32 ? nsub - f0 : 32);
+        const uint16_t* xb = xs + b * XBS;
+        float acc[GPB];
+#pragma unroll
+        for (int gg = 0; gg < GPB; gg++) acc[gg] = 0.f;
+        if (nvalid == 32) {
+#pragma unroll
+            for (int j = 0; j < 32; j++) {
+                uint32_t c = vp_field<PB>(w, j);
+                c = __builtin_elementwise_min(c, (uint32_t)(a.kc - 1));
+                acc[j / FPG] = vp_dot<DIM>(cbl + c * DIM, xb + j * DIM, acc[j / FPG]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 32; j++) {
+                uint32_t c = vp_field<PB>(w, j);
+                c = __builtin_elementwise_min(c, (uint32_t)(a.kc - 1));
+                const float d = vp_dot<DIM>(cbl + c * DIM, xb + j * DIM, 0.f);
+                acc[j / FPG] += j < nvalid ? d : 0.f;
+            }
+        }
+#pragma unroll
+        for (int gg = 0; gg < GPB; gg++) tot = __builtin_fmaf(sv[gg], acc[gg], tot);
+    }
+    for (int o = SEG / 2; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    const float y = ok_e ? vp_bf16r(tot) : 0.f;
+    if (g == 0 && slot_ok) prod[r * VPD_SLOTS + s] = vp_bf16r(y * bf16_to_f32(a.scores[t * k + s]));
+    __syncthreads();
+    if (tid < rpwg) {
+        const int64_t n = (int64_t)blockIdx.x * rpwg + tid;
+        if (n < a.N) {
+            double acc = 0.0;
+            for (int j = 0; j < k; j++) acc += (double)prod[tid * VPD_SLOTS + j];
+            a.out[t * a.N + n] = f32_to_bf16(vp_f32_kept(acc));
+        }
+    }
+}
+
+static size_t vpd_lds(int64_t K, int kc, int dim, int k) {
+    const int64_t nblk = (K / dim + 31) / 32;
+    return (size_t)vp_cb_blocks(kc, dim) * 1024 + (size_t)k * nblk * 33 * dim * 2 + 256 * sizeof(float);
+}
+
+template <int PB>
+static int launch_vpd_pb(const VpdArgs& a, int dim, int gpb, size_t lds, hipStream_t st) {
+    const int rpwg = 256 / (VPD_SLOTS * a.seg);
+    const dim3 grid((unsigned)ceil_div(a.N, rpwg), (unsigned)a.T);
+#define KMI_VPD(D_, G_)                                                         \
+    if (dim == D_ && gpb == G_) {                                               \
+        static bool attr = false;                                               \
+        if (!attr) {                                                            \
+            allow_dynamic_lds((const void*)vq_packed_down_tok<PB, D_, G_>);     \
+            attr = true;                                                        \
+        }                                                                       \
+        vq_packed_down_tok<PB, D_, G_><<<grid, 256, lds, st>>>(a);              \
+        return OK;                                                              \
+    }
+    KMI_VPD(2, 1) KMI_VPD(2, 2) KMI_VPD(4, 1) KMI_VPD(4, 2) KMI_VPD(4, 4)
+    KMI_VPD(8, 1) KMI_VPD(8, 2) KMI_VPD(8, 4) KMI_VPD(8, 8)
+#undef KMI_VPD
+    return EINVAL_ARG;
+}
+
+// Token-major down + combine for a few tokens (k <= 8, the LDS holding the
+// codebook and the token's k act rows): 0 launched, 1 not covered.
+static int run_vpd(VpdArgs& a, int pack_bits, int dim, hipStream_t st) {
+    const int64_t nsub = a.K / dim, nblk = (nsub + 31) / 32;
+    const int fpg = a.group / dim;
+    const int gpb = fpg >= 32 ? 1 : 32 / fpg;
+    a.seg = vp_seg(nblk);                     // the per-pair kernel's lanes per row
+    const size_t lds = vpd_lds(a.K, a.kc, dim, a.k);
+    if (a.k < 1 || a.k > VPD_SLOTS || VPD_SLOTS * a.seg > 256 || lds > 160 * 1024) return 1;
+    int rc;
+    switch (pack_bits) {
+        case 8: rc = launch_vpd_pb<8>(a, dim, gpb, lds, st); break;
+        case 9: rc = launch_vpd_pb<9>(a, dim, gpb, lds, st); break;
+        case 10: rc = launch_vpd_pb<10>(a, dim, gpb, lds, st); break;
+        case 11: rc = launch_vpd_pb<11>(a, dim, gpb, lds, st); break;
+        case 12: rc = launch_vpd_pb<12>(a, dim, gpb, lds, st); break;
+        default: rc = launch_vpd_pb<16>(a, dim, gpb, lds, st); break;
+    }
+    return rc == OK ? 0 : 1;
+}
+
 static int vp_check(int dtype, int pack_bits, int kc, int dim, int group, int64_t K, int64_t N, int64_t E) {
     KMI_CHECK_ARG(dtype == BF16, "vq (packed): only bfloat16 activations are implemented");
     KMI_CHECK_ARG(pack_bits == 8 || pack_bits == 9 || pack_bits == 10 || pack_bits == 11 || pack_bits == 12 ||
@@ -543,6 +738,16 @@ static int vps_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, i
         d.sc[0] = d.sc[1] = (const uint16_t*)scales_down;
         d.cb[0] = d.cb[1] = (const uint16_t*)codebook_down;
         d.nset = 1; d.kc = kc; d.E = E; d.N = H; d.K = I; d.W = Wd; d.group = group; d.y = y;
+        if (scores) {    // token-major down with the combine in its epilogue, where it fits
+            VpdArgs td = {};
+            td.act = act; td.inds = inds; td.scores = (const uint16_t*)scores; td.codes = codes_down;
+            td.sc = (const uint16_t*)scales_down; td.cb = (const uint16_t*)codebook_down; td.out = (uint16_t*)out;
+            td.E = E; td.N = H; td.K = I; td.W = Wd; td.T = T; td.k = k; td.kc = kc; td.group = group;
+            if (run_vpd(td, pack_bits, dim, st) == 0) {
+                KMI_CHECK_LAUNCH("vq_packed_down_tok");
+                return OK;
+            }
+        }
         rc = run_vp(d, pack_bits, dim, st);
         if (rc) return rc;
     }
