@@ -497,7 +497,9 @@ int kmi_vq_packed_glu(const void* x, int64_t X, int64_t H, int64_t I, const uint
  *   y[p] = act[p] @ Down_{inds[p]}^T, out = combine(y, scores) [T, H] or y [T*k, H].
  * Codes / scales / codebooks as kmi_vq_packed_gather_qmm (gate and up
  * [E, I, *] over H inputs, down [E, H, *] over I).  Up to 16 pairs run per
- * pair; more are grouped by expert on the GPU (an expert-tile MFMA kernel
+ * pair (with scores, k <= 8: the down projection token-major with the
+ * combine in its epilogue, the same bits as the separate combine); more
+ * are grouped by expert on the GPU (an expert-tile MFMA kernel
  * where the shape allows: dim 2 / 4 / 8, groups of 32 / 64 / 128 inputs,
  * K a multiple of 32 * dim), so pairs that share an expert share its
  * decode.  workspace: kmi_vq_packed_switch_glu_workspace_bytes.
