@@ -308,7 +308,7 @@ static int launch_vp_pb(const VpArgs& a, int dim, int gpb, int seg, size_t lds, 
 
 // ---- down projection + weighted combine for a few tokens, token-major ----
 // grid (ceil(N / rows per workgroup), T).  A workgroup owns a few output
-// rows of one token; lane (row r, slot s, segment g), SEG lanes per (row,
+// rows of one token; lane (slot s, row r, segment g), SEG lanes per (row,
 // slot) as vq_packed_gemv puts them on a row (same blocks per lane, same
 // sums, same shuffle tree), so y[t*k+s, n] is the per-pair kernel's value
 // bit for bit; the token's k act rows are staged once.  Each slot's
@@ -336,7 +336,9 @@ __global__ __launch_bounds__(256) void vq_packed_down_tok(VpdArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int SEG = a.seg, rpwg = 256 / (VPD_SLOTS * SEG);
-    const int g = tid % SEG, s = (tid / SEG) % VPD_SLOTS, r = tid / (VPD_SLOTS * SEG);
+    // rows fastest after the segments: a wave's lanes cover consecutive rows
+    // of one or two slots' experts (their words lie together)
+    const int g = tid % SEG, r = (tid / SEG) % rpwg, s = tid / (SEG * rpwg);
     const int64_t t = blockIdx.y;
     const int k = a.k;
     const int64_t nsub = a.K / DIM, nblk = (nsub + 31) / 32;
