@@ -98,6 +98,57 @@ __device__ __forceinline__ uint32_t vp_field(const uint32_t* w, int j) {
     return v & ((1u << PB) - 1u);
 }
 
+// A full 32-field block: fields decoded, codebook vectors and x read from
+// LDS in batches of 8 -- the next batch's reads issued before the current
+// batch's dot products (the scheduling barriers keep them there) -- and
+// each group's sum formed in field order, as vp_dot field by field.
+template <int DIM>
+struct VpVec;
+template <> struct VpVec<2> { typedef uint32_t T; };
+template <> struct VpVec<4> { typedef u32x2 T; };
+template <> struct VpVec<8> { typedef u32x4 T; };
+
+template <int DIM>
+__device__ __forceinline__ float vp_dotv(typename VpVec<DIM>::T c, typename VpVec<DIM>::T v, float acc) {
+    if constexpr (DIM == 2) {
+        return vp_dot2(c, v, acc);
+    } else if constexpr (DIM == 4) {
+        return vp_dot2(c.y, v.y, vp_dot2(c.x, v.x, acc));
+    } else {
+        acc = vp_dot2(c.x, v.x, acc);
+        acc = vp_dot2(c.y, v.y, acc);
+        acc = vp_dot2(c.z, v.z, acc);
+        return vp_dot2(c.w, v.w, acc);
+    }
+}
+
+template <int PB, int DIM, int GPB>
+__device__ __forceinline__ void vp_block_full(const uint32_t (&w)[PB + 1], const uint16_t* cbl, const uint16_t* xb,
+                                              uint32_t kcm1, float (&acc)[GPB]) {
+    typedef typename VpVec<DIM>::T V;
+    constexpr int FB = 8, FPG = 32 / GPB;
+    V cv[2][FB], xv[2][FB];
+    auto fetch = [&](int j0, int b) {
+#pragma unroll
+        for (int f = 0; f < FB; f++) {
+            const int j = j0 + f;
+            const uint32_t c = __builtin_elementwise_min(vp_field<PB>(w, j), kcm1);
+            cv[b][f] = *(const V*)(cbl + c * DIM);
+            xv[b][f] = *(const V*)(xb + j * DIM);
+        }
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int j0 = 0; j0 < 32; j0 += FB) {
+        const int b = (j0 / FB) & 1;
+        if (j0 + FB < 32) fetch(j0 + FB, b ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < FB; f++) acc[(j0 + f) / FPG] = vp_dotv<DIM>(cv[b][f], xv[b][f], acc[(j0 + f) / FPG]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 __device__ __forceinline__ float vp_bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 __device__ __forceinline__ float vp_f32_kept(double v) {
@@ -233,12 +284,7 @@ __global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
 #pragma unroll
             for (int g = 0; g < GPB; g++) acc[g] = 0.f;
             if (nvalid == 32) {
-#pragma unroll
-                for (int j = 0; j < 32; j++) {
-                    uint32_t c = vp_field<PB>(w, j);
-                    c = __builtin_elementwise_min(c, (uint32_t)(a.kc - 1));
-                    acc[j / FPG] = vp_dot<DIM>(cbl + c * DIM, xb + j * DIM, acc[j / FPG]);
-                }
+                vp_block_full<PB, DIM, GPB>(w, cbl, xb, (uint32_t)(a.kc - 1), acc);
             } else {                 // the last, partial block of a row
 #pragma unroll
                 for (int j = 0; j < 32; j++) {
@@ -425,12 +471,7 @@ __global__ __launch_bounds__(256) void vq_packed_down_tok(VpdArgs a) {
 #pragma unroll
         for (int gg = 0; gg < GPB; gg++) acc[gg] = 0.f;
         if (nvalid == 32) {
-#pragma unroll
-            for (int j = 0; j < 32; j++) {
-                uint32_t c = vp_field<PB>(w, j);
-                c = __builtin_elementwise_min(c, (uint32_t)(a.kc - 1));
-                acc[j / FPG] = vp_dot<DIM>(cbl + c * DIM, xb + j * DIM, acc[j / FPG]);
-            }
+            vp_block_full<PB, DIM, GPB>(w, cbl, xb, (uint32_t)(a.kc - 1), acc);
         } else {
 #pragma unroll
             for (int j = 0; j < 32; j++) {
