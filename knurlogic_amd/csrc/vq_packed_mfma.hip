@@ -196,6 +196,10 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
                 u32x4 A[SPG];
 #pragma unroll
                 for (int t = 0; t < SPG; t++) A[t] = *(const u32x4*)(xa + (size_t)(g * GRP + 8 * t) * 2);
+                // every gather of the group (both row sets, all SPG steps)
+                // issued before its first MFMA (the scheduling barrier keeps
+                // them there): one LDS round trip per group
+                u32x4 B[NSET][SPG];
 #pragma unroll
                 for (int s = 0; s < NSET; s++) {
                     const u32x4 w = wv[s][j];
@@ -204,7 +208,6 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
                     const uint32_t r1 = __builtin_amdgcn_alignbit(w.z, w.y, sh);
                     const uint32_t r2 = __builtin_amdgcn_alignbit(w.w, w.z, sh);
                     const unsigned char* cbl = s ? cbl1 : cbl0;
-                    f32x4 P = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int t = 0; t < SPG; t++) {
                         uint32_t bw[4];
@@ -227,8 +230,15 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
                                 bw[0] = v.x; bw[1] = v.y; bw[2] = v.z; bw[3] = v.w;
                             }
                         }
-                        P = vpm_mfma(A[t], u32x4{bw[0], bw[1], bw[2], bw[3]}, P);
+                        B[s][t] = u32x4{bw[0], bw[1], bw[2], bw[3]};
                     }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int s = 0; s < NSET; s++) {
+                    f32x4 P = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int t = 0; t < SPG; t++) P = vpm_mfma(A[t], B[s][t], P);
                     const float scl = f16_to_f32((uint16_t)sv[s][j]);
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc[s][i] = __builtin_fmaf(scl, P[i], acc[s][i]);
