@@ -3,11 +3,19 @@
 Headline (``value``): the 4-bit, group-64 quantized GEMV (M = 1) over a
 [14336, 4096] weight with inputs resident in HBM and the weight buffers
 rotated past the 256 MB Infinity Cache (cold), as achieved HBM GB/s of
-algorithmic bytes.  ``detail`` holds the whole dense workload (4- and 8-bit,
-W [14336, 4096] and [4096, 14336], M = 1, 16, 512, cold and warm) plus the
-[4096, 4096] GEMV.  Timed with HIP events around a HIP-graph replay of the
-calls (one graph = ``--steps`` calls), so CPU launch cost is excluded while
-every kernel of each call (GEMV + split-K reduce) is included.
+algorithmic bytes.  One step is one decode token through a stack of 32 such
+layers (each layer its own weight), so ``ms_per_step`` covers 32 GEMV calls
+and ``config.us_per_layer`` is one call.  Timed with HIP events around a
+HIP-graph replay of exactly ``--steps`` steps, so CPU launch cost is
+excluded while every kernel of each call is included.
+
+``detail`` holds the BASELINE workloads: the dense [4096, 4096] GEMV and the
+4- and 8-bit [14336, 4096] / [4096, 14336] matmuls at M = 1, 16, 512 (cold
+and warm), the mx modes, KV append and quantized SDPA, packed VQ, then the
+MoE experts (T = 1, 16, 256), the VQ experts (both codebooks, T = 1, 16) and
+the KV8 decode (8k / 32k keys, L = 1 / 4).  ``summary``, the line's last
+key, gives each configuration's µs and % of its bounding peak in one short
+string.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
 """
@@ -567,14 +575,53 @@ def cpu_baseline(seconds=10.0):
                       f"[14336,4096] M=1, {n} calls in {seconds:.0f} s"}
 
 
+#: the headline step: one decode token through a stack of this many layers,
+#: each a [14336, 4096] 4-bit GEMV over its own weight (a Llama-3-8B-sized
+#: MLP projection per layer; the weight sets rotate past 1 GB, so every
+#: layer's weight comes from HBM)
+LAYERS_PER_STEP = 32
+
+
+def _pct(r):
+    if r.get("bound") == "mfma":
+        return f"{100 * r['mfma_frac']:.1f}%mfma"
+    return f"{100 * r['hbm_frac']:.1f}%hbm"
+
+
+def summary(detail):
+    """One short string per BASELINE workload row (cold where both were
+    measured): config number, shape, µs per call and % of the bounding
+    peak.  Printed last in the JSON line."""
+    out = {}
+    for r in detail:
+        if r.get("cache") == "warm":
+            continue
+        op = r["op"]
+        if op == "quantized_matmul":
+            if (r["N"], r["K"]) == (4096, 4096):
+                key = f"c1 {r['bits']}b 4096x4096 M{r['M']}"
+            else:
+                key = f"c2 {r['bits']}b {r['N']}x{r['K']} M{r['M']}"
+        elif op == "moe_experts":
+            key = f"c3 moe T{r['T']}"
+        elif op == "vq_moe_experts":
+            key = f"c4 vq {r['codebook'].split()[0]} T{r['T']}"
+        elif op == "kv8_decode":
+            key = f"c5 kv8 {r['N'] // 1024}k L{r['L']}"
+        else:
+            continue
+        out[key] = f"{r['us']}us {_pct(r)}"
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # 2000 steps (~16 ms): one graph launch's fixed start-up cost, spread over
-    # 200 steps, read as +0.3-0.4 us per step (measured 8.23-8.33 us at 200
-    # steps, 7.84-7.95 us at 1000-3000 on the same box)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=20)
+    # steps of LAYERS_PER_STEP calls each, all in one HIP graph: the graph
+    # launch's fixed start-up (measured +0.3-0.4 us per call when spread over
+    # 200 calls) is spread over steps x 32 calls
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only, no detail table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="detail sections, comma-separated "
@@ -605,83 +652,89 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     bits, M, N, K = 4, 1, 14336, 4096
+    Lps = LAYERS_PER_STEP
 
-    # headline: warmup W eager calls, then one graph of exactly K calls
+    # headline: W untimed steps eagerly, then one graph of exactly K steps
+    # (K x 32 layer calls)
     sets = make_sets(N, K, bits, True, dev)
     x = torch.randn(M, K, device=dev).to(torch.bfloat16)
-    for i in range(args.warmup):
+    for i in range(args.warmup * Lps):
         KA.quantized_matmul(x, *sets[i % len(sets)], transpose=True, group_size=64, bits=bits)
     torch.cuda.synchronize()
 
     def run():
-        for i in range(args.steps):
+        for i in range(args.steps * Lps):
             wq, s, b = sets[i % len(sets)]
             KA.quantized_matmul(x, wq, s, b, transpose=True, group_size=64, bits=bits)
 
     # untimed replays first (the GPU leaves its idle clocks), then exactly
-    # `steps` calls timed
+    # `steps` steps timed
     ms_total = time_graph(run, replays=1, warm=4)
     del sets
     torch.cuda.empty_cache()
-    us = ms_total * 1e3 / args.steps
+    ms_step = ms_total / args.steps
+    us = ms_step * 1e3 / Lps                       # per layer call
     nbytes = dense_bytes(M, N, K, bits)
     gbs = nbytes / (us * 1e-6) / 1e9
 
     detail = []
     only = set(args.only.split(",")) if args.only else {"dense", "kv8", "kvcache", "qsdpa", "moe", "vq"}
-    if not args.quick and "vq" in only:
-        for kc_ in (256, 4096):
-            for t_ in (1, 16):
-                for cold in (True, False):
-                    detail.append(bench_vq(t_, kc_, cold, 50, dev))
-    if not args.quick and "vq" in only:
-        for t_ in (1, 16):
-            detail.append(bench_vq_packed(t_, 50, dev))
-        for t_ in (1, 16):      # the shipped Gemma-4 26B VQ artifact's expert shape
-            detail.append(bench_vq_packed(t_, 50, dev, dim=2, H=2816, I=704))
-    if not args.quick and "moe" in only:
-        for t_ in (1, 16):
-            detail.append(bench_mx_moe(t_, 30, dev))
-    if not args.quick and "dense" in only:
-        for mode in ("mxfp4", "mxfp8"):
-            for m in (1, 16):
-                detail.append(bench_mx_dense(mode, m, 14336, 4096, 100, dev))
-    if not args.quick and "moe" in only:
-        for t_ in (1, 16, 256):
-            for cold in (True, False):
-                detail.append(bench_moe(t_, cold, 50 if t_ < 256 else 20, dev))
-    if not args.quick and "kv8" in only:
-        for n_ in (8192, 32768):
-            for l_ in (1, 4):
-                for cold in (True, False):
-                    detail.append(bench_kv8(4, 32, 4, l_, n_, 128, cold, 50, dev))
-    if not args.quick and "kvcache" in only:
-        for s_ in (1, 512):
-            detail.append(bench_kv_append(4, 4, s_, 128, 8, 200 if s_ == 1 else 50, dev))
-    if not args.quick and "qsdpa" in only:
-        for n_ in (8192, 32768):
-            for l_ in (1, 4):
-                detail.append(bench_qsdpa(4, 32, 4, l_, n_, 128, 8, 30, dev))
-    if not args.quick and "dense" in only:
+    full = not args.quick
+    # the dense configurations (1, 2) first; the MoE, VQ and KV8 rows
+    # (configurations 3-5) last, so they end the line
+    if full and "dense" in only:
+        detail.append(bench_dense(4, 1, 4096, 4096, True, 200, dev))
+        detail.append(bench_dense(4, 1, 4096, 4096, False, 200, dev))
         for b_ in (4, 8):
             for shape in ((14336, 4096), (4096, 14336)):
                 for m in (1, 16, 512):
                     for cold in (True, False):
                         calls = 100 if m < 512 else 30
                         detail.append(bench_dense(b_, m, shape[0], shape[1], cold, calls, dev))
-        detail.append(bench_dense(4, 1, 4096, 4096, True, 200, dev))
-        detail.append(bench_dense(4, 1, 4096, 4096, False, 200, dev))
+        for mode in ("mxfp4", "mxfp8"):
+            for m in (1, 16):
+                detail.append(bench_mx_dense(mode, m, 14336, 4096, 100, dev))
+    if full and "kvcache" in only:
+        for s_ in (1, 512):
+            detail.append(bench_kv_append(4, 4, s_, 128, 8, 200 if s_ == 1 else 50, dev))
+    if full and "qsdpa" in only:
+        for n_ in (8192, 32768):
+            for l_ in (1, 4):
+                detail.append(bench_qsdpa(4, 32, 4, l_, n_, 128, 8, 30, dev))
+    if full and "vq" in only:
+        for t_ in (1, 16):
+            detail.append(bench_vq_packed(t_, 50, dev))
+        for t_ in (1, 16):      # the shipped Gemma-4 26B VQ artifact's expert shape
+            detail.append(bench_vq_packed(t_, 50, dev, dim=2, H=2816, I=704))
+    if full and "moe" in only:
+        for t_ in (1, 16):
+            detail.append(bench_mx_moe(t_, 30, dev))
+        for t_ in (1, 16, 256):
+            for cold in (True, False):
+                detail.append(bench_moe(t_, cold, 50 if t_ < 256 else 20, dev))
+    if full and "vq" in only:
+        for kc_ in (256, 4096):
+            for t_ in (1, 16):
+                for cold in (True, False):
+                    detail.append(bench_vq(t_, kc_, cold, 50, dev))
+    if full and "kv8" in only:
+        for n_ in (8192, 32768):
+            for l_ in (1, 4):
+                for cold in (True, False):
+                    detail.append(bench_kv8(4, 32, 4, l_, n_, 128, cold, 50, dev))
 
     ceil = None if (args.quick or args.no_ceilings) else ceilings(dev, nbytes)
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(us / 1e3, 6),
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 6),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u4",
         "data": "synthetic: W ~ N(0, 0.02) quantized on the GPU (affine, 4-bit, group 64), "
                 "x ~ N(0, 1) bf16",
         "config": {"workload": "affine 4-bit g64 quantized_matmul, W [14336,4096], M=1 "
-                               "(decode GEMV), bf16 activations, fp32 accumulate",
+                               "(decode GEMV), bf16 activations, fp32 accumulate; one step = one "
+                               f"decode token through {Lps} layers, each its own weight",
+                   "layers_per_step": Lps, "bytes_per_step": nbytes * Lps,
                    "us_per_layer": round(us, 3), "cache": "cold (weight sets rotated past 1 GB)",
                    "device": torch.cuda.get_device_name(dev)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
@@ -692,6 +745,7 @@ def main():
         "ceilings": ceil,
         "cpu_baseline": cpu,
         "detail": detail,
+        "summary": summary(detail),
     }
     print(json.dumps(line))
 

@@ -24,8 +24,45 @@ FLAGS = [
 EXTRA = {"qgemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
+# The compiler's per-kernel resource remarks (registers, scratch, occupancy),
+# parsed after each compile.
+RESOURCE_REMARKS = "-Rpass-analysis=kernel-resource-usage"
+
+# Kernels that stage through direct-to-LDS loads wait for them with counted
+# `s_waitcnt vmcnt(N)`: N counts the vector-memory operations the wave issued
+# after the stage's loads, which holds only while nothing else -- a register
+# spill's scratch store or load above all -- sits among them.  Every kernel
+# compiled from a source (or a local header it includes) that names one of
+# these must use no scratch.
+DMA_MARKERS = ("buffer_load_lds", "wait_vmcnt<")
+
+
 def sources():
     return sorted(SRC.glob("*.hip"))
+
+
+def uses_lds_dma(src: Path) -> bool:
+    """Whether src, or a csrc header it includes, issues direct-to-LDS loads
+    or counted vmcnt waits."""
+    texts = [src.read_text()]
+    for line in texts[0].splitlines():
+        line = line.strip()
+        if line.startswith("#include \"") and line.endswith(".hpp\""):
+            h = SRC / line.split("\"")[1]
+            if h.exists():
+                texts.append(h.read_text())
+    return any(m in t for t in texts for m in DMA_MARKERS)
+
+
+def kernel_scratch(remarks: str) -> dict:
+    """{mangled kernel name: scratch bytes per lane} from the resource remarks."""
+    out, name = {}, None
+    for line in remarks.splitlines():
+        if "remark: Function Name: " in line:
+            name = line.split("remark: Function Name: ")[1].split()[0]
+        elif "ScratchSize [bytes/lane]: " in line and name is not None:
+            out[name] = int(line.split("ScratchSize [bytes/lane]: ")[1].split()[0])
+    return out
 
 
 def _run(cmd):
@@ -34,6 +71,19 @@ def _run(cmd):
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed ({r.returncode}): {' '.join(cmd)}\n{err}")
     return err
+
+
+def check_scratch(src: Path, remarks: str) -> dict:
+    """The scratch each kernel of src uses; raises when a kernel of a
+    direct-to-LDS source spills (its counted waits would no longer count
+    only its stage loads)."""
+    sc = kernel_scratch(remarks)
+    if uses_lds_dma(src):
+        bad = {k: v for k, v in sc.items() if v}
+        if bad:
+            raise RuntimeError(f"{src.name}: kernels with direct-to-LDS loads and counted vmcnt waits use "
+                               f"scratch (a spill breaks the waits' count): {bad}")
+    return sc
 
 
 def build(verbose: bool = False, jobs: int = 8) -> Path:
@@ -46,9 +96,16 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     srcs = sources()
     objs = [objdir / (p.stem + ".o") for p in srcs]
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        errs = list(ex.map(lambda so: _run(["hipcc", *cflags, *EXTRA.get(so[0].name, []), "-c", str(so[0]),
-                                            "-o", str(so[1])]),
+        errs = list(ex.map(lambda so: _run(["hipcc", *cflags, *EXTRA.get(so[0].name, []), RESOURCE_REMARKS,
+                                            "-c", str(so[0]), "-o", str(so[1])]),
                            zip(srcs, objs)))
+    spills = {}
+    for src, e in zip(srcs, errs):
+        spills.update({k: v for k, v in check_scratch(src, e).items() if v})
+    errs = ["\n".join(l for l in e.splitlines() if "kernel-resource-usage" not in l) for e in errs]
+    if verbose and spills:
+        print("kernels using scratch (bytes per lane): " + ", ".join(f"{k} {v}" for k, v in sorted(spills.items())),
+              file=sys.stderr)
     tmp = OUT.with_suffix(".so.tmp")
     errs.append(_run(["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC",
                       *map(str, objs), "-o", str(tmp)]))

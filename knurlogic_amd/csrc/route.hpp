@@ -10,7 +10,11 @@
 // Quotients and products of two floats are formed in float64 and rounded
 // once, which is the correctly rounded float32 result.  Used by the router
 // kernel and by the SwitchGLU kernels that route their own token, so both
-// give the same experts and scores bit for bit.
+// give the same experts and scores bit for bit.  mlx forms exp with a SIMD
+// polynomial a few float32 ulp from the correctly rounded value, so at
+// probabilities that close (and at exact ties, which its argpartition
+// breaks in its own order) mlx may select a different expert than this
+// rule does: top-k membership there is not pinned to mlx.
 #pragma once
 
 #include "common.hpp"

@@ -64,7 +64,9 @@ def reset(on: bool = True) -> None:
 
 
 def count(hit: bool, why: str = "") -> None:
-    """One decode attention: through the kernel (hit) or not (miss)."""
+    """Tally one dispatch in ``STATS``: ``hit`` when the 8-bit kernel ran,
+    else a miss with its reason.  The first hit and the first miss are
+    logged once per ``reset``."""
     if hit:
         STATS["hits"] += 1
     else:
@@ -73,9 +75,10 @@ def count(hit: bool, why: str = "") -> None:
     if hit not in _LOGGED:
         _LOGGED.add(hit)
         if hit:
-            logger.info("kv kernel: live -- 8-bit decode reads the packed K/V")
+            logger.info("8-bit KV decode kernel in use (kmi_kv8_decode on the packed cache)")
         else:
-            logger.warning("kv kernel: a decode step fell back to dequantize + sdpa: %s", why)
+            logger.warning("8-bit KV decode kernel not taken for a step, fallback path "
+                           "instead (%s)", why)
 
 
 def _dims(q, K, V, bits):
@@ -278,21 +281,23 @@ def _packed(kv):
     return None
 
 
-def sdpa(queries, keys, values, cache, scale, mask, sinks=None):
+def sdpa(queries, keys, values, cache, scale, mask, sinks=None, base=None):
     """The dispatch a model's attention calls (kvattn.sdpa): the 8-bit
     kernel when ``cache`` just handed back exactly these keys for a short
     query (its ``kv8_fetch``); otherwise quantized K/V through
-    ``quantized_sdpa`` on their packed triples, and dense K/V through the
-    model's own attention function (recorded by ``patch_model``)."""
+    ``quantized_sdpa`` on their packed triples, and dense K/V through
+    ``base`` -- the calling module's own attention function, which the
+    wrapper ``patch_model`` installed passes in -- or, for a direct call,
+    the first attention function the last ``patch_model`` replaced."""
     hit = getattr(cache, "kv8_fetch", None)
     if hit is not None:
         cache.kv8_fetch = None
         kret, K, V, g = hit
         if kret is not keys:
-            count(False, "keys changed between the cache and the attention")
+            count(False, "the attention was handed other keys than the cache fetched")
         elif not supports(queries, K, V, 8, g, mask, sinks):
-            count(False, f"unsupported: q {tuple(queries.shape)}, mask "
-                         f"{getattr(mask, 'shape', mask)}, sinks {sinks is not None}")
+            count(False, f"shape outside the kernel (q {tuple(queries.shape)}, mask "
+                         f"{getattr(mask, 'shape', mask)}, sinks given: {sinks is not None})")
         else:
             count(True)
             return decode_sdpa(queries, K, V, scale, mask, g, 8, same_layout=True)
@@ -307,11 +312,30 @@ def sdpa(queries, keys, values, cache, scale, mask, sinks=None):
     if (pk is not None and pv is not None and sinks is None and queries.dtype == torch.bfloat16
             and pk[1:] == pv[1:] and mask_ok):
         return quantized_sdpa(queries, pk[0], pv[0], scale, mask, pk[1], pk[2])
-    base = _BASE["fn"]
+    if base is None:
+        base = _BASE["fn"]
     if base is None:
         raise ValueError("kvattn.sdpa: dense (or fp16 / fp32) attention runs in the model's own "
                          "scaled_dot_product_attention, which patch_model records; call patch_model first")
     return base(queries, keys, values, cache=cache, scale=scale, mask=mask, sinks=sinks)
+
+
+class ModuleSdpa:
+    """``sdpa`` as installed in one Python module by ``patch_model``: it
+    carries that module's own attention function (``base``), so dense K/V
+    met in that module go back to exactly the function it held."""
+
+    __slots__ = ("base", "module")
+
+    def __init__(self, base, module: str):
+        self.base = base
+        self.module = module
+
+    def __call__(self, queries, keys, values, cache=None, scale=1.0, mask=None, sinks=None):
+        return sdpa(queries, keys, values, cache, scale, mask, sinks, base=self.base)
+
+    def __repr__(self):
+        return f"kvattn.ModuleSdpa({self.module}, base={getattr(self.base, '__qualname__', self.base)!r})"
 
 
 def _model_modules(model):
@@ -321,24 +345,31 @@ def _model_modules(model):
 
 
 def patch_model(model) -> int:
-    """Rebind ``scaled_dot_product_attention`` to ``sdpa`` in every Python
-    module that defines one of the model's (sub)module classes, where it
-    is the model's original attention function (the first one met, which
-    is kept as the base for dense K/V) or already ``sdpa``.  Idempotent;
-    harmless for unquantized caches.  Returns how many modules."""
+    """Rebind ``scaled_dot_product_attention`` in every Python module that
+    defines one of the model's (sub)module classes to a ``ModuleSdpa``
+    carrying that module's own function, so each module's dense K/V go back
+    to the attention it had (modules with different functions keep theirs).
+    Idempotent (a module already holding a ``ModuleSdpa`` keeps it);
+    harmless for unquantized caches.  The first function replaced by this
+    call also serves direct calls of ``sdpa``.  Returns how many modules
+    hold the dispatch afterwards."""
     names = sorted({type(m).__module__ for m in _model_modules(model)} | {type(model).__module__})
-    base, n = _BASE["fn"], 0
+    first, n = None, 0
     for name in names:
         mod = sys.modules.get(name)
         f = getattr(mod, "scaled_dot_product_attention", None)
-        if f is None:
+        if f is None or not callable(f):
             continue
-        if f is not sdpa:
-            if base is None:
-                base = f
-            if f is not base:
-                continue
-            mod.scaled_dot_product_attention = sdpa
+        if isinstance(f, ModuleSdpa):
+            base = f.base
+        elif f is sdpa:
+            base = None
+        else:
+            base = f
+            mod.scaled_dot_product_attention = ModuleSdpa(f, name)
+        if first is None and base is not None:
+            first = base
         n += 1
-    _BASE["fn"] = base
+    if first is not None:
+        _BASE["fn"] = first
     return n

@@ -645,7 +645,7 @@ def quantize_cache_list(caches, bits: int, table=None):
 def install(model, bits, table=None) -> int:
     """Wrap ``model.make_cache`` so every new cache list stores attention
     K/V at ``bits`` (8, 6 or 4), and rebind the model's attention modules
-    to ``kvattn.sdpa``.  At 8 bits with the kernel enabled (``kvattn.ENV``)
+    to ``kvattn.sdpa`` (``kvattn.patch_model``).  At 8 bits with the kernel enabled (``kvattn.ENV``)
     the new caches hand their packed K/V to the decode kernel;
     ``model.kv8_kernel`` records whether.  Returns how many caches
     of a probe list are quantized (0: none of this model's caches can be,

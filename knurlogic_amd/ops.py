@@ -65,6 +65,37 @@ def _check_mx(what, scales, biases, group_size, bits, mode):
         raise ValueError(f"{what}: {mode} takes group_size 32 and {_MX_BITS[mode]} bits")
 
 
+def _check_experts(what, H, E, w_gu, s_gu, b_gu, w_down, s_down, b_down, group_size, bits):
+    """Stacked SwitchGLU experts against x's width H and E experts: gate|up
+    w_gu [E, 2I, H*bits/32], s_gu (/ b_gu) [E, 2I, H/group]; down w_down
+    [E, H, I*bits/32], s_down (/ b_down) [E, H, I/group].  The kernels take
+    only the sizes, so a tensor smaller than these would be read past its
+    end.  Returns I."""
+    if w_gu.dim() != 3 or w_down.dim() != 3:
+        raise ValueError(f"{what}: w_gu and w_down must be [E, rows, words]")
+    I2 = w_gu.shape[1]
+    if I2 % 2:
+        raise ValueError(f"{what}: w_gu has {I2} rows (gate and up stacked: 2I)")
+    I = I2 // 2
+    if H % group_size or I % group_size or (H * bits) % 32 or (I * bits) % 32:
+        raise ValueError(f"{what}: H={H}, I={I} do not divide into groups of {group_size} and whole words")
+    want = {
+        "w_gu": (w_gu, (E, 2 * I, H * bits // 32)),
+        "s_gu": (s_gu, (E, 2 * I, H // group_size)),
+        "w_down": (w_down, (E, H, I * bits // 32)),
+        "s_down": (s_down, (E, H, I // group_size)),
+    }
+    if b_gu is not None or b_down is not None:
+        want["b_gu"] = (b_gu, (E, 2 * I, H // group_size))
+        want["b_down"] = (b_down, (E, H, I // group_size))
+    for name, (t, shape) in want.items():
+        if t is None or tuple(t.shape) != shape:
+            got = None if t is None else tuple(t.shape)
+            raise ValueError(f"{what}: {name} is {got}, expected {shape} "
+                             f"(E={E}, H={H}, I={I}, bits={bits}, group {group_size})")
+    return I
+
+
 def _resolve(group_size, bits, mode: str):
     """mlx's mode-dependent defaults for an omitted group_size / bits: affine
     64 and 4, mxfp4 32 and 4, mxfp8 32 and 8."""
@@ -700,8 +731,8 @@ def switch_glu(x: torch.Tensor, indices: torch.Tensor, w_gu, s_gu, b_gu, w_down,
     k = indices.shape[-1]
     if tuple(indices.shape[:-1]) != lead:
         raise ValueError("switch_glu: indices [..., k] must match x [..., H]")
-    E, I2 = w_gu.shape[0], w_gu.shape[1]
-    I = I2 // 2
+    E = w_gu.shape[0]
+    I = _check_experts("switch_glu", H, E, w_gu, s_gu, b_gu, w_down, s_down, b_down, group_size, bits)
     T = math.prod(lead)
     xc = x.contiguous()
     ic = indices.reshape(T, k).to(torch.int32).contiguous()
@@ -742,8 +773,8 @@ def switch_glu_mx(x: torch.Tensor, indices: torch.Tensor, w_gu, s_gu, w_down, s_
     k = indices.shape[-1]
     if tuple(indices.shape[:-1]) != lead:
         raise ValueError("switch_glu_mx: indices [..., k] must match x [..., H]")
-    E, I2 = w_gu.shape[0], w_gu.shape[1]
-    I = I2 // 2
+    E = w_gu.shape[0]
+    I = _check_experts("switch_glu_mx", H, E, w_gu, s_gu, None, w_down, s_down, None, 32, _MX_BITS[mode])
     T = math.prod(lead)
     xc = x.contiguous()
     ic = indices.reshape(T, k).to(torch.int32).contiguous()
@@ -780,7 +811,10 @@ def moe_experts(x: torch.Tensor, logits: torch.Tensor, k: int, w_gu, s_gu, b_gu,
     if tuple(logits.shape[:-1]) != lead:
         raise ValueError("moe_experts: logits [..., E] must match x [..., H]")
     E = logits.shape[-1]
-    I = w_gu.shape[1] // 2
+    if w_gu.shape[0] != E or w_down.shape[0] != E:
+        raise ValueError(f"moe_experts: {E} logits per token for {w_gu.shape[0]} gate/up and "
+                         f"{w_down.shape[0]} down experts")
+    I = _check_experts("moe_experts", H, E, w_gu, s_gu, b_gu, w_down, s_down, b_down, group_size, bits)
     T = math.prod(lead)
     out = torch.empty(*lead, H, dtype=x.dtype, device=x.device)
     inds = torch.empty(*lead, k, dtype=torch.int32, device=x.device)

@@ -446,9 +446,13 @@ def route(logits, k: int, out_dtype: str = "bfloat16"):
     bit without it: exp is the correctly rounded float32 exp (mlx uses its
     SIMD polynomial, within a few ulp), and both sums are the exact sum
     rounded once to float32 (mlx adds in SIMD-lane order).  Differences of
-    an ulp or two in float32 only reach the rounded scores at a bf16 / fp16
-    rounding boundary.  The top-k set is order-free (argpartition); ties go
-    to the lower expert index.
+    an ulp or two in float32 reach the rounded scores at a bf16 / fp16
+    rounding boundary, and they can also reorder two probabilities that lie
+    within those ulps of each other and so change which expert is selected:
+    top-k membership at such near-ties (and at exact ties, which mlx's
+    argpartition breaks in its own order) is parity unpinned.  Here the
+    top-k set follows the rounded probabilities; ties go to the lower
+    expert index.
     Returns (inds [T, k] int32 in descending-probability order, scores)."""
     x = np.asarray(logits, np.float32)
     m = x.max(axis=-1, keepdims=True)

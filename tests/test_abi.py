@@ -117,3 +117,22 @@ def test_noalloc_scratch_covers_every_planned_qmm():
                 for bits in (4, 8):
                     worst = max(worst, L.kmi_qmm_workspace_bytes(M, K, N, 64, bits))
     assert worst == cap      # reached (M = 512, K = 14336, N = 4096) and never passed
+
+
+def test_build_refuses_a_spilling_kernel_with_counted_lds_waits():
+    """The build's scratch rule: a kernel compiled from a direct-to-LDS
+    source must report no scratch (a spill's scratch traffic would sit among
+    the loads its counted vmcnt waits count)."""
+    from knurlogic_amd import build as B
+    remarks = ("x.hip:1:1: remark: Function Name: _Z4kernv [-Rpass-analysis=kernel-resource-usage]\n"
+               "x.hip:1:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]\n"
+               "x.hip:9:1: remark: Function Name: _Z5otherv [-Rpass-analysis=kernel-resource-usage]\n"
+               "x.hip:9:1: remark:     ScratchSize [bytes/lane]: 68 [-Rpass-analysis=kernel-resource-usage]\n")
+    assert B.kernel_scratch(remarks) == {"_Z4kernv": 0, "_Z5otherv": 68}
+    dl = B.SRC / "qgemv_dl.hip"
+    assert B.uses_lds_dma(dl) and B.uses_lds_dma(B.SRC / "qgemv_xs.hip") and B.uses_lds_dma(B.SRC / "vq_packed.hip")
+    assert not B.uses_lds_dma(B.SRC / "kv8.hip")
+    with pytest.raises(RuntimeError, match="scratch"):
+        B.check_scratch(dl, remarks)
+    # a source without direct-to-LDS loads may spill (reported, not refused)
+    assert B.check_scratch(B.SRC / "kv8.hip", remarks)["_Z5otherv"] == 68

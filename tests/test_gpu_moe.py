@@ -48,6 +48,17 @@ def test_route_ties_go_to_the_lower_expert(dev):
     _bits_equal(to_numpy(scores), rs)
 
 
+def test_route_orders_a_one_ulp_near_tie_like_the_oracle(dev):
+    """Probabilities one float32 ulp apart (logits 1, 0, 2^-23, -8): the
+    router kernel takes expert 2 ahead of expert 1, as the oracle does."""
+    lg = np.tile(np.array([[1.0, 0.0, 2.0 ** -23, -8.0]], np.float32), (3, 1))
+    inds, scores = K.moe_route(to_torch(lg, dev, BF), 2)
+    ri, rs = O.route(lg, 2, "bfloat16")
+    assert (ri[:, :2] == [0, 2]).all()
+    np.testing.assert_array_equal(inds.cpu().numpy(), ri)
+    _bits_equal(to_numpy(scores), rs)
+
+
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16", "float32"])
 def test_swiglu_bit_for_bit(dev, dtype):
     rng = np.random.default_rng(1)

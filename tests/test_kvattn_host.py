@@ -27,10 +27,72 @@ def test_patch_model_rebinds_the_models_attention_and_keeps_it_as_the_base(toy):
     orig = toy.scaled_dot_product_attention
     model = toy.Model()
     assert kvattn.patch_model(model) == 1
-    assert toy.scaled_dot_product_attention is kvattn.sdpa
+    bound = toy.scaled_dot_product_attention
+    assert isinstance(bound, kvattn.ModuleSdpa) and bound.base is orig
     assert kvattn._BASE["fn"] is orig
     assert kvattn.patch_model(model) == 1                    # idempotent
+    assert toy.scaled_dot_product_attention is bound and bound.base is orig
     assert kvattn._BASE["fn"] is orig
+
+
+def _other_module(monkeypatch, name, factor):
+    """A second model module whose own attention function differs from the
+    toy's (it scales the toy's output), with one module class in it."""
+    import types
+    mod = types.ModuleType(name)
+    calls = []
+
+    def attention(queries, keys, values, cache=None, scale=1.0, mask=None, sinks=None):
+        calls.append(name)
+        from tests.toy_attention import scaled_dot_product_attention as plain
+        return plain(queries, keys, values, cache=cache, scale=scale, mask=mask) * factor
+
+    class Block(torch.nn.Module):
+        pass
+
+    Block.__module__ = name
+    mod.scaled_dot_product_attention = attention
+    mod.Block = Block
+    mod.calls = calls
+    monkeypatch.setitem(sys.modules, name, mod)
+    return mod
+
+
+def test_modules_with_different_attention_keep_their_own_base(toy, monkeypatch):
+    other = _other_module(monkeypatch, "tests._toy_other_attention", 2.0)
+    third = _other_module(monkeypatch, "tests._toy_third_attention", 3.0)
+    own = {m.__name__: m.scaled_dot_product_attention for m in (toy, other, third)}
+    model = toy.Model(layers=1)
+    model.extra = other.Block()
+    model.more = third.Block()
+    assert kvattn.patch_model(model) == 3
+    for m in (toy, other, third):
+        f = m.scaled_dot_product_attention
+        assert isinstance(f, kvattn.ModuleSdpa) and f.base is own[m.__name__]
+    # dense K/V dispatched from each module reach that module's own function
+    q, k = torch.randn(1, 2, 1, 16), torch.randn(1, 2, 5, 16)
+    want = own[toy.__name__](q, k, k, scale=0.25)
+    assert torch.equal(toy.scaled_dot_product_attention(q, k, k, cache=None, scale=0.25), want)
+    assert torch.equal(other.scaled_dot_product_attention(q, k, k, cache=None, scale=0.25), want * 2)
+    assert torch.equal(third.scaled_dot_product_attention(q, k, k, cache=None, scale=0.25), want * 3)
+    assert other.calls == ["tests._toy_other_attention"] and third.calls == ["tests._toy_third_attention"]
+
+
+def test_a_second_model_patched_later_serves_direct_calls(toy, monkeypatch):
+    toy_orig = toy.scaled_dot_product_attention
+    kvattn.patch_model(toy.Model(layers=1))
+    assert kvattn._BASE["fn"] is toy_orig
+    other = _other_module(monkeypatch, "tests._toy_other_attention", 2.0)
+    other_orig = other.scaled_dot_product_attention
+
+    class Second(torch.nn.Module):
+        pass
+
+    Second.__module__ = other.__name__
+    assert kvattn.patch_model(Second()) == 1
+    assert kvattn._BASE["fn"] is other_orig
+    # the first model's module still holds its own base
+    assert toy.scaled_dot_product_attention.base is toy_orig
 
 
 def test_dense_kv_go_back_to_the_models_own_attention(toy):
@@ -61,7 +123,7 @@ def test_enabled_follows_the_switch(monkeypatch):
 def test_install_quantizes_plain_caches_and_marks_the_kernel(toy, monkeypatch):
     model = toy.Model()
     assert KC.install(model, 8) == 2
-    assert model.kv8_kernel is True and toy.scaled_dot_product_attention is kvattn.sdpa
+    assert model.kv8_kernel is True and isinstance(toy.scaled_dot_product_attention, kvattn.ModuleSdpa)
     caches = model.make_cache()
     assert all(type(c) is KC.QuantKVCache and c.kv_bits == 8 and c.kv8_kernel for c in caches)
     # the switch off: quantized caches, no kernel

@@ -283,6 +283,30 @@ def test_route_uniform_rows_by_hand():
     assert scores.sum() == np.float32(1.0)
 
 
+def test_route_one_ulp_apart_is_ordered_by_the_rounded_probabilities():
+    """Two experts whose float32 probabilities differ by exactly one ulp:
+    logits (bf16) 1, 0, 2^-23, -8.  exp(-1 + 2^-23) and exp(-1), each
+    correctly rounded, are 0x3E590343 and 0x3E590342 after the reciprocal
+    multiply, so top-2 is experts 0 and 2 -- not 0 and 1, which the
+    lower-index tie rule would give were they equal.  (mlx's own SIMD exp
+    is within a few ulp of this, so whether mlx picks expert 1 or 2 on such
+    a row is not fixed by this rule: top-k membership at one-ulp near-ties
+    is parity unpinned.)"""
+    lg = np.array([[1.0, 0.0, 2.0 ** -23, -8.0]], np.float32)
+    assert (O.bf16_round(lg) == lg).all()
+    inds, scores = O.route(lg, 2, "float32")
+    assert list(inds[0]) == [0, 2]
+    # the two probabilities, as the oracle forms them, one ulp apart
+    e = np.exp((lg - lg.max()).astype(np.float64)).astype(np.float32)
+    n = e.astype(np.float64).sum().astype(np.float32)
+    pr = e * (np.float32(1.0) / n)
+    assert pr[0, 2].view(np.uint32) == 0x3E590343 and pr[0, 1].view(np.uint32) == 0x3E590342
+    # a planted mistake: exp rounded through float32 arithmetic on a coarser
+    # grid (x - m in bf16) makes the two equal and flips the choice to 1
+    coarse = O.bf16_round((lg - lg.max()).astype(np.float32))
+    assert coarse[0, 1] == coarse[0, 2]
+
+
 def test_route_agrees_with_an_independent_fp32_router():
     """HF transformers' Qwen MoE router on torch's CPU kernels (softmax in
     float32, top-k, p / sum(p) in float32, cast to bf16) -- the

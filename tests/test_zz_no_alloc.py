@@ -1,7 +1,8 @@
 """kmi_qmm_noalloc (the entry point that allocates nothing) against kmi_qmm
 with a caller workspace, through the C ABI: bit for bit, on two calls in a
 row, the second smaller than the first, so the second runs over what the
-first left in the shared scratch array."""
+first left in the shared scratch array; and recorded into a HIP graph,
+replayed with new inputs."""
 import ctypes
 
 import numpy as np
@@ -42,6 +43,42 @@ def _both(dev, M, K, N, bits, seed):
                "qmm_noalloc")
     torch.cuda.synchronize()
     return need, y_ws, y_na
+
+
+def test_noalloc_captured_in_a_graph_replays_like_qmm(dev):
+    """kmi_qmm_noalloc recorded into a HIP graph (torch.cuda.CUDAGraph) and
+    replayed with new x contents written eagerly between replays: every
+    replay equals kmi_qmm with a workspace, bit for bit.  This test runs
+    first in its file and no other test calls the no-alloc entry, so the
+    capture also covers the first call's per-device scratch lookup."""
+    torch.cuda.set_device(dev)
+    L = _abi.load()
+    M, K, N, bits = 16, 4096, 4096, 8          # a K-split shape: the partials sit in the scratch array
+    x, w, s, b = _operands(dev, M, K, N, bits, 7)
+    need = L.kmi_qmm_workspace_bytes(M, K, N, 64, bits)
+    assert need > 0
+    y = torch.full((M, N), float("nan"), dtype=BF, device=dev)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        rc = L.kmi_qmm_noalloc(_ptr(x), M, K, N, _ptr(w), _ptr(s), _ptr(b), 0, 64, bits, _ptr(y),
+                               ctypes.c_void_p(side.cuda_stream))
+    _abi.check(rc, "qmm_noalloc (captured)")
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    ref = torch.empty(M, N, dtype=BF, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    rng = np.random.default_rng(8)
+    for i in range(4):
+        x.copy_(to_torch(bf16_normal(rng, (M, K)), dev, BF))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        _abi.check(L.kmi_qmm(_ptr(x), M, K, N, _ptr(w), _ptr(s), _ptr(b), 0, 64, bits, _ptr(ref), _ptr(ws),
+                             need, st), "qmm")
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), f"replay {i}"
+    del graph
 
 
 def test_noalloc_matches_qmm_on_two_calls_in_a_row(dev):
