@@ -73,6 +73,21 @@ def _run(cmd):
     return err
 
 
+def _drop_remarks(text: str) -> str:
+    """The compiler output without the resource remarks and the source
+    excerpts ("  157 | ...", "      | ^") clang prints under each."""
+    out, skip = [], False
+    for line in text.splitlines():
+        if "kernel-resource-usage" in line:
+            skip = True
+            continue
+        if skip and line.lstrip()[:1] in ("|",) or (skip and line.strip().split(" |")[0].isdigit()):
+            continue
+        skip = False
+        out.append(line)
+    return "\n".join(out)
+
+
 def check_scratch(src: Path, remarks: str) -> dict:
     """The scratch each kernel of src uses; raises when a kernel of a
     direct-to-LDS source spills (its counted waits would no longer count
@@ -102,7 +117,7 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     spills = {}
     for src, e in zip(srcs, errs):
         spills.update({k: v for k, v in check_scratch(src, e).items() if v})
-    errs = ["\n".join(l for l in e.splitlines() if "kernel-resource-usage" not in l) for e in errs]
+    errs = [_drop_remarks(e) for e in errs]
     if verbose and spills:
         print("kernels using scratch (bytes per lane): " + ", ".join(f"{k} {v}" for k, v in sorted(spills.items())),
               file=sys.stderr)

@@ -7,6 +7,10 @@
 #include <stdio.h>
 #include <stdarg.h>
 
+#include <mutex>
+#include <set>
+#include <utility>
+
 namespace kmi {
 
 // dtype codes of the C ABI (include/knurlogic_amd.h)
@@ -53,6 +57,20 @@ inline void allow_dynamic_lds(const void* f) {
     const size_t stat = hipFuncGetAttributes(&fa, f) == hipSuccess ? fa.sharedSizeBytes : 0;
     (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(160 * 1024 - stat));
     (void)hipGetLastError();
+}
+
+// allow_dynamic_lds for kernel f on the current device, once per (kernel,
+// device): the attribute is a property of the function on each device.
+inline void allow_dynamic_lds_once(const void* f) {
+    static std::mutex mu;
+    static std::set<std::pair<const void*, int>> done;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        dev = -1;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.insert({f, dev}).second) allow_dynamic_lds(f);
 }
 
 __device__ __forceinline__ float e8m0_to_f32(uint32_t e) {

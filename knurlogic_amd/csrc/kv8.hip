@@ -569,12 +569,7 @@ static Kv8Plan plan_kv8(int B, int Hk, int N, int D, int R) {
 template <int D, int RT, class ST>
 static void launch_partial(const Kv8Args& a, dim3 grid, hipStream_t st) {
     constexpr size_t lds = KvShape<D, RT>::lds;
-    static bool attr_set = false;
-    if (!attr_set) {
-        (void)hipFuncSetAttribute((const void*)kv8_partial<D, RT, ST>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        attr_set = true;
-    }
+    allow_dynamic_lds_once((const void*)kv8_partial<D, RT, ST>);
     kv8_partial<D, RT, ST><<<grid, 256, lds, st>>>(a);
 }
 

@@ -403,12 +403,7 @@ template <int B_, int G_, int M_, bool L_, bool X_>
 static int launch_one(const QgArgs& a, dim3 grid, hipStream_t st) {
     constexpr size_t lds = qg_lds_bytes<B_, G_, L_ ? 2 : 1, M_>();
     static_assert(lds <= 160 * 1024, "qgemv tile exceeds the LDS");
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute((const void*)qgemv_kernel<B_, G_, M_, L_, X_>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        attr = true;
-    }
+    allow_dynamic_lds_once((const void*)qgemv_kernel<B_, G_, M_, L_, X_>);
     qgemv_kernel<B_, G_, M_, L_, X_><<<grid, 256, lds, st>>>(a);
     return OK;
 }

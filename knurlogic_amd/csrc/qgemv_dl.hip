@@ -232,12 +232,7 @@ int launch_dl_ns(const QgArgs& a, dim3 grid, hipStream_t st) {
         set_error("qgemv_dl: %d stages of %d slices exceed the LDS", NS, KS);
         return EINVAL_ARG;
     } else {
-        static bool attr = false;
-        if (!attr) {
-            (void)hipFuncSetAttribute((const void*)qgemv_dl_kernel<BITS, GS, MX, NS, KS>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            attr = true;
-        }
+        allow_dynamic_lds_once((const void*)qgemv_dl_kernel<BITS, GS, MX, NS, KS>);
         qgemv_dl_kernel<BITS, GS, MX, NS, KS><<<grid, 256 * KS, lds, st>>>(a);
         return OK;
     }

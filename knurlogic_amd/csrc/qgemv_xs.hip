@@ -348,12 +348,7 @@ int launch_xs_one(const QgArgs& a, int64_t ntiles, uint32_t xrow, uint32_t xbyte
     constexpr size_t stage = XsShape<BITS, GS, MX, NSET>::STAGE;
     const size_t lds = (size_t)xbytes + NS * stage;
     if (lds > XS_LDS_MAX) return 1;
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute((const void*)qgemv_xs_kernel<BITS, GS, MX, XR, NSET, NS>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)XS_LDS_MAX);
-        attr = true;
-    }
+    allow_dynamic_lds_once((const void*)qgemv_xs_kernel<BITS, GS, MX, XR, NSET, NS>);
     const int64_t NB = (a.N + 63) / 64;
     const int G = xs_blocks_per_wg(NB, ntiles);
     const dim3 grid((unsigned)ceil_div(NB, G), 1, (unsigned)ntiles);

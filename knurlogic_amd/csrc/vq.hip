@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void vq_gemv(VqArgs a) {
 
     // this lane's index words and scales first, so their loads fly during staging
     uint32_t cw[NSET][NW];
-    float sv[NSET][NG];
+    uint16_t sv[NSET][NG];     // fp16 bits, converted at use (not at the load: no early wait)
 #pragma unroll
     for (int s = 0; s < NSET; s++) {
         const __amdgpu_buffer_rsrc_t rc = make_rsrc((const char*)(s ? a.codes1 : a.codes0) + erow * cpr * CB, cbytes);
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void vq_gemv(VqArgs a) {
 #pragma unroll
         for (int g = 0; g < NG; g++) {
             const int64_t gi = SGC ? (int64_t)row * gpr + ((int64_t)seg * CPS) / SGC + g : row;
-            sv[s][g] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rsc, (int)(gi * 2), 0, 0));
+            sv[s][g] = __builtin_amdgcn_raw_buffer_load_b16(rsc, (int)(gi * 2), 0, 0);
         }
     }
     // codebook(s) and the x row -> LDS
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256) void vq_gemv(VqArgs a) {
         }
         float v = 0.f;
 #pragma unroll
-        for (int g = 0; g < NG; g++) v = __builtin_fmaf(sv[s][g], acc[g], v);
+        for (int g = 0; g < NG; g++) v = __builtin_fmaf(f16_to_f32(sv[s][g]), acc[g], v);
 #pragma unroll
         for (int o = SEG / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
         r[s] = vq_bf16r(v);

@@ -25,7 +25,6 @@
 #include "vq_mfma.hpp"
 #include "route.hpp"
 
-#include <cstdlib>
 
 namespace kmi {
 
@@ -207,16 +206,25 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     const int64_t ebase = (int64_t)e * a.erows;
     const int cfirst = kp * (CPR / KS) + q * CPL;              // this lane's first code of its row
     uint32_t cw[MB ? 2 : 1][NSET][LW];
-    float scl[MB ? 2 : 1][NSET];
+    // row scales kept as loaded (fp16 bits) and converted where the epilogue
+    // uses them: a conversion at the load makes the compiler wait for that
+    // load -- and, loads completing in order, for the block's code loads
+    // before it -- right where the next block's codes are prefetched
+    uint16_t scl[MB ? 2 : 1][NSET];
+    // A block past the workgroup's last (g >= nb) loads nothing: every
+    // offset is past its buffer.  So the next block's loads can be issued on
+    // every path -- behind a branch, the compiler's vmcnt waits would take the
+    // path without them and wait for the prefetch right after issuing it.
     auto load_codes = [&](int g, int slot_) {
         const int slot = MB ? slot_ : 0;
         const int row = row_of(g);
         const int crow = row < a.N ? row : (int)a.N - 1;       // rows past N re-read row N-1, never stored
+        const bool live = g < nb;
 #pragma unroll
         for (int s = 0; s < NSET; s++) {
             const char* cb = (const char*)(s ? a.codes1 : a.codes0) + ebase * CPR * CB;
             const __amdgpu_buffer_rsrc_t rc = make_rsrc(cb, a.N * CPR * CB);
-            const uint32_t lo = (uint32_t)((crow * CPR + cfirst) * CB);
+            const uint32_t lo = live ? (uint32_t)((crow * CPR + cfirst) * CB) : NONE;
             if constexpr (LW % 4 == 0) {
 #pragma unroll
                 for (int i = 0; i < LW; i += 4) {
@@ -235,7 +243,7 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
                     cw[slot][s][i] = __builtin_amdgcn_raw_buffer_load_b32(rc, (int)(lo + i * 4), 0, AUX_NT);
             }
             const __amdgpu_buffer_rsrc_t rsc = make_rsrc((s ? a.sc1 : a.sc0) + ebase, a.N * 2);
-            scl[slot][s] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rsc, crow * 2, 0, 0));
+            scl[slot][s] = __builtin_amdgcn_raw_buffer_load_b16(rsc, live ? crow * 2 : (int)NONE, 0, 0);
         }
     };
     load_codes(0, 0);
@@ -253,10 +261,13 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     const int mrow = n < count ? n : count - 1;                 // A rows past the tile repeat a real row
     const unsigned char* xa = xs + (size_t)mrow * xstride + (size_t)cfirst * 16;
     // ---- column block g from register set `slot`: MFMA over the lane's
-    //      codes, the K parts summed, the epilogue
-    auto compute = [&](int g, int slot_) {
+    //      codes, the K parts summed, the epilogue's values (bf16) into res;
+    //      false for the waves whose K part another wave finishes.  The
+    //      stores wait for the end of the kernel: a store pending beside the
+    //      next block's loads makes the compiler's vmcnt waits drain them all
+    //      (loads and stores do not complete in one order).
+    auto compute = [&](int g, int slot_, uint16_t (&res)[4]) -> bool {
         const int slot = MB ? slot_ : 0;
-        const int row = row_of(g);
         f32x4 acc[NSET];
 #pragma unroll
         for (int s = 0; s < NSET; s++) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -300,7 +311,7 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
 #pragma unroll
             for (int s = 0; s < NSET; s++) red[(wave * NSET + s) * 64 + lane] = acc[s];
             lds_barrier();
-            if (kp != 0) return;
+            if (kp != 0) return false;
 #pragma unroll
             for (int s = 0; s < NSET; s++) {
                 f32x4 t = red[(wave * NSET + s) * 64 + lane];
@@ -311,36 +322,50 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
         }
 
         // epilogue: lane holds D[m = 4q + i][n]
-        if (row < a.N) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = 4 * q + i;
-                if (m >= count) continue;
-                float out = vqm_bf16r(scl[slot][0] * acc[0][i]);
-                if constexpr (NSET == 2) {     // round(round(silu_f32(gate)) * up)
-                    const float up = vqm_bf16r(scl[slot][1] * acc[1][i]);
-                    const double gg = (double)out;
-                    out = vqm_bf16r(vqm_f32_kept(gg / (1.0 + exp(-gg)))) * up;
-                }
-                const int64_t r = a.tiles ? a.sorted[start + m] : start;
-                a.y[r * a.N + row] = f32_to_bf16(out);
+        for (int i = 0; i < 4; i++) {
+            float out = vqm_bf16r(f16_to_f32(scl[slot][0]) * acc[0][i]);
+            if constexpr (NSET == 2) {     // round(round(silu_f32(gate)) * up)
+                const float up = vqm_bf16r(f16_to_f32(scl[slot][1]) * acc[1][i]);
+                const double gg = (double)out;
+                out = vqm_bf16r(vqm_f32_kept(gg / (1.0 + exp(-gg)))) * up;
             }
+            res[i] = f32_to_bf16(out);
+        }
+        return true;
+    };
+    auto store = [&](int g, const uint16_t (&res)[4]) {
+        const int row = row_of(g);
+        if (row >= a.N) return;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = 4 * q + i;
+            if (m >= count) continue;
+            const int64_t r = a.tiles ? a.sorted[start + m] : start;
+            a.y[r * a.N + row] = res[i];
         }
     };
     if constexpr (MB) {
-        // two register sets: block g + 1's codes stream in while block g computes
-        for (int g = 0; g < nb; g += 2) {
-            if (g + 1 < nb) load_codes(g + 1, 1);
-            compute(g, 0);
-            if (g + 1 < nb) {
-                if (g + 2 < nb) load_codes(g + 2, 0);
-                compute(g + 1, 1);
-            }
+        // two register sets: block g + 1's codes stream in while block g
+        // computes; the loads of a block past nb read nothing, so they are
+        // issued on every path (a load behind a branch would leave the
+        // compiler's vmcnt count at the path without it, and the next
+        // block's prefetch would be waited for right after its issue)
+        uint16_t res[VQM_MAX_CBLK][4];
+#pragma unroll
+        for (int g = 0; g < VQM_MAX_CBLK; g++) {
+            load_codes(g + 1, (g + 1) & 1);
+            if (g < nb) compute(g, g & 1, res[g]);
         }
+#pragma unroll
+        for (int g = 0; g < VQM_MAX_CBLK; g++)
+            if (g < nb) store(g, res[g]);
     } else {
-        compute(0, 0);
+        uint16_t res[4];
+        if (compute(0, 0, res)) store(0, res);
     }
 }
+
 
 size_t vq_mfma_lds(int64_t K, int kc, bool two_cb, int tile_rows, int nset, int ks) {
     return (size_t)((kc + 63) / 64) * 1024 * (two_cb ? 2 : 1) + (size_t)tile_rows * (K * 2 + 16) +
@@ -384,19 +409,12 @@ bool vq_mfma_supported(int64_t K, int code_bytes, int kc, bool two_cb) {
     return any && vq_mfma_lds(K, kc, two_cb, TM, 2, 4) <= 160 * 1024;
 }
 
-// column blocks per workgroup for 2-byte codes without a K split: 4, so a
-// workgroup's 64 KB codebook staging and x staging serve 256 weight rows
-// (measured at 128 experts, 16 tokens, 4096 x 8: 103 -> 90 us); 1-byte codes
-// keep one block (4 KB codebooks; the smaller register set runs more waves)
-// (KMI_VQ_G overrides: tuning; read once)
-static int vq_cblk(int64_t nbt) {
-    static int ov = [] {
-        const char* e = getenv("KMI_VQ_G");
-        return e ? atoi(e) : 0;
-    }();
-    const int64_t g = ov > 0 ? ov : 4;
-    return (int)(g < nbt ? g : nbt);
-}
+// column blocks per workgroup for 2-byte codes without a K split:
+// VQM_MAX_CBLK (4), so a workgroup's 64 KB codebook staging and x staging
+// serve 256 weight rows (measured at 128 experts, 16 tokens, 4096 x 8: 103
+// -> 90 us; 2, 3, 6 and 8 blocks were slower); 1-byte codes keep one block
+// (4 KB codebooks; the smaller register set runs more waves)
+static int vq_cblk(int64_t nbt) { return (int)(VQM_MAX_CBLK < nbt ? VQM_MAX_CBLK : nbt); }
 
 int launch_vq_mfma(const VqmArgs& a_in, int code_bytes, int nset, int64_t ntiles, hipStream_t st) {
     VqmArgs a = a_in;
@@ -433,11 +451,7 @@ int launch_vq_mfma(const VqmArgs& a_in, int code_bytes, int nset, int64_t ntiles
     const dim3 grid((unsigned)ceil_div(nbt, a.cblk), (unsigned)ntiles);
 #define KMI_VQM_GO(CB_, NS_, LW_, KS_, MB_, RT_)                                                  \
     {                                                                                            \
-        static bool attr = false;                                                                \
-        if (!attr) {                                                                             \
-            allow_dynamic_lds((const void*)vq_mfma<CB_, NS_, LW_, KS_, MB_, RT_>);                    \
-            attr = true;                                                                         \
-        }                                                                                        \
+        allow_dynamic_lds_once((const void*)vq_mfma<CB_, NS_, LW_, KS_, MB_, RT_>);              \
         vq_mfma<CB_, NS_, LW_, KS_, MB_, RT_><<<grid, WG, lds, st>>>(a);                         \
         return OK;                                                                               \
     }
@@ -516,7 +530,9 @@ __global__ __launch_bounds__(WG) void vq_down_tok(VqdArgs a) {
     // this wave's slots, two at a time: codes and scales of both issued together
     const int crow = (int)(row < a.N ? row : a.N - 1);
     const int cfirst = q * CPL;
-    auto load_slot = [&](int s, uint32_t (&cw)[LW], float& scl, bool& ok) {
+    // the scale stays as loaded (fp16 bits) until the epilogue, so the next
+    // slots' prefetch is not waited for at its issue
+    auto load_slot = [&](int s, uint32_t (&cw)[LW], uint16_t& scl, bool& ok) {
         const int e = s < k ? a.inds[(int64_t)t * k + s] : -1;
         ok = e >= 0 && e < a.E;
         const char* base = (const char*)a.codes + (int64_t)(ok ? e : 0) * a.N * CPR * CB;
@@ -539,11 +555,11 @@ __global__ __launch_bounds__(WG) void vq_down_tok(VqdArgs a) {
             for (int i = 0; i < LW; i++) cw[i] = __builtin_amdgcn_raw_buffer_load_b32(rc, (int)(lo + i * 4), 0, AUX_NT);
         }
         const __amdgpu_buffer_rsrc_t rsc = make_rsrc(a.sc + (int64_t)(ok ? e : 0) * a.N, ok ? a.N * 2 : 0);
-        scl = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rsc, crow * 2, 0, 0));
+        scl = __builtin_amdgcn_raw_buffer_load_b16(rsc, crow * 2, 0, 0);
     };
     const int nslot = (k - wave + 3) / 4;            // slots wave, wave + 4, ..
     uint32_t cw[2][LW];
-    float scl[2];
+    uint16_t scl[2];
     bool okk[2];
     load_slot(wave, cw[0], scl[0], okk[0]);
     load_slot(wave + 4, cw[1], scl[1], okk[1]);
@@ -587,7 +603,7 @@ __global__ __launch_bounds__(WG) void vq_down_tok(VqdArgs a) {
                 __builtin_amdgcn_sched_barrier(0);
             }
             // D[m][n] is the same for every m: lanes q = 0 hold it in item 0
-            const float y = okk[u] ? vqm_bf16r(scl[u] * acc[0]) : 0.f;
+            const float y = okk[u] ? vqm_bf16r(f16_to_f32(scl[u]) * acc[0]) : 0.f;
             if (q == 0) {
                 if (a.scores) {
                     const float sc = bf16_to_f32(a.scores[(int64_t)t * k + s]);
@@ -635,12 +651,7 @@ int launch_vq_down_tok(const VqdArgs& a, int code_bytes, hipStream_t st) {
     const dim3 grid((unsigned)ceil_div(a.N, 16), (unsigned)a.T);
 #define KMI_VQD_ONE(CB_, LW_)                                                                     \
     if (code_bytes == CB_ && lw == LW_) {                                                         \
-        static bool attr = false;                                                                 \
-        if (!attr) {                                                                              \
-            (void)hipFuncSetAttribute((const void*)vq_down_tok<CB_, LW_>,                          \
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);    \
-            attr = true;                                                                          \
-        }                                                                                         \
+        allow_dynamic_lds_once((const void*)vq_down_tok<CB_, LW_>);                              \
         vq_down_tok<CB_, LW_><<<grid, WG, lds, st>>>(a);                                          \
         return OK;                                                                                \
     }

@@ -6,6 +6,7 @@
 namespace kmi {
 
 constexpr int VQM_TILE_ROWS = 16;   // rows (tokens or pairs) per expert tile
+constexpr int VQM_MAX_CBLK = 4;     // column blocks of 64 rows per workgroup (2-byte codes)
 
 struct VqmArgs {
     const uint16_t* x;          // bf16 [X, K]

@@ -324,11 +324,7 @@ template <int PB, int DIM, int GPB>
 static int launch_vp3(const VpArgs& a, int seg, size_t lds, hipStream_t st) {
 #define KMI_VP_SEG(S_)                                                                                  \
     if (seg == S_) {                                                                                    \
-        static bool attr = false;                                                                       \
-        if (!attr) {                                                                                    \
-            allow_dynamic_lds((const void*)vq_packed_gemv<PB, DIM, GPB, S_>);                           \
-            attr = true;                                                                                \
-        }                                                                                               \
+        allow_dynamic_lds_once((const void*)vq_packed_gemv<PB, DIM, GPB, S_>);                   \
         const dim3 grid((unsigned)ceil_div(a.N, 256 / S_), (unsigned)a.R);                              \
         vq_packed_gemv<PB, DIM, GPB, S_><<<grid, 256, lds, st>>>(a);                                    \
         return OK;                                                                                      \
@@ -509,11 +505,7 @@ static int launch_vpd_pb(const VpdArgs& a, int dim, int gpb, size_t lds, hipStre
     const dim3 grid((unsigned)ceil_div(a.N, rpwg), (unsigned)a.T);
 #define KMI_VPD(D_, G_)                                                         \
     if (dim == D_ && gpb == G_) {                                               \
-        static bool attr = false;                                               \
-        if (!attr) {                                                            \
-            allow_dynamic_lds((const void*)vq_packed_down_tok<PB, D_, G_>);     \
-            attr = true;                                                        \
-        }                                                                       \
+        allow_dynamic_lds_once((const void*)vq_packed_down_tok<PB, D_, G_>);                     \
         vq_packed_down_tok<PB, D_, G_><<<grid, 256, lds, st>>>(a);              \
         return OK;                                                              \
     }

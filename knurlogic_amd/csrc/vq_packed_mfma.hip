@@ -292,12 +292,7 @@ int vpm_launch4(const VpmArgs& a, dim3 grid, size_t lds, hipStream_t st) {
     if constexpr (GRP / (4 * DIM) < 1 || (GRP / (4 * DIM)) * PB + 31 > 128) {
         return EINVAL_ARG;
     } else {
-        static bool attr = false;
-        if (!attr) {
-            (void)hipFuncSetAttribute((const void*)vq_packed_mfma<PB, DIM, GRP, NSET>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-            attr = true;
-        }
+        allow_dynamic_lds_once((const void*)vq_packed_mfma<PB, DIM, GRP, NSET>);
         vq_packed_mfma<PB, DIM, GRP, NSET><<<grid, VPM_WG, lds, st>>>(a);
         return OK;
     }

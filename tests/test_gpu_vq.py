@@ -163,6 +163,53 @@ def test_vq_switch_glu_full_tiles_and_long_rows(dev, T, E, H, I, k, kc):
     assert_close(to_numpy(got), ref, what=f"vq switch_glu T={T} H={H} kc={kc}")
 
 
+@pytest.mark.parametrize("T,E,H,I,k,kc", [
+    (8, 32, 1024, 512, 4, 100),      # a codebook of fewer than 256 entries
+    (4, 4, 512, 256, 2, 256),        # experts over several 4-row tiles, a 256-wide down
+    (8, 64, 2816, 704, 8, 256),      # the Gemma-4 26B expert widths; down on the VALU kernel (704 % 128)
+    (2, 128, 2048, 768, 8, 256),     # 16 pairs: the token-major down with its combine
+])
+@pytest.mark.parametrize("shared", [True, False])
+def test_vq_switch_glu_small_tiles_match_the_oracle(dev, T, E, H, I, k, kc, shared):
+    """1-byte codes at one or two routed rows per expert: SwitchGLU and its
+    combine against the oracle across tile splits, chunk counts and a short
+    codebook, with one codebook for the layer (shared) or one per
+    projection."""
+    rng = np.random.default_rng(T + E + H + I + kc)
+    (hg, gg), (hu, gu), (hd, gd) = [_vq(rng, E, n, kd, kc, 0, dev) for n, kd in ((I, H), (I, H), (H, I))]
+    if shared:                      # the gate's codebook for all three projections
+        hu, hd = (hu[0], hg[1], hu[2]), (hd[0], hg[1], hd[2])
+        gu, gd = (gu[0], gg[1], gu[2]), (gd[0], gg[1], gd[2])
+    glu = nn.VQSwitchGLU(*(nn.VQSwitchLinear(*g) for g in (gg, gu, gd)))
+    x = bf16_normal(rng, (T, H))
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    fn = lambda h: (lambda xs, e: O.vq_matmul(xs, h[0][e], h[1], h[2][e], 0, "bfloat16"))
+    ref = O.switch_glu(x, inds, fn(hg), fn(hu), fn(hd))
+    tx, ti = to_torch(x, dev, BF), torch.from_numpy(inds).to(dev)
+    got = glu(tx, ti)
+    assert_close(to_numpy(got), ref, what=f"vq T={T} E={E} H={H} kc={kc}")
+    _, sc = O.route(bf16_normal(rng, (T, E)), k)
+    comb = glu.combine(tx, ti, to_torch(sc, dev, BF))
+    assert_close(to_numpy(comb), O.combine(ref, sc), what="combine")
+
+
+def test_vq_clamps_codes_past_the_codebook(dev):
+    """Codes at or past a short codebook's size read its last entry (the
+    clamp every VQ kernel applies, so such codes never read past the staged
+    codebook): the same output as the codes clamped on the host."""
+    rng = np.random.default_rng(77)
+    T, E, H, I, k, kc = 8, 32, 1024, 512, 4, 100
+    (hg, gg), (hu, gu), (hd, gd) = [_vq(rng, E, n, kd, kc, 0, dev) for n, kd in ((I, H), (I, H), (H, I))]
+    wild = [g[0].clone() for g in (gg, gu, gd)]
+    for w in wild:
+        w[:, ::3, ::5] = 255                                   # past the 100 entries
+    clamped = [torch.clamp(w, max=kc - 1) for w in wild]
+    x = to_torch(bf16_normal(rng, (T, H)), dev, BF)
+    inds = torch.from_numpy(np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)).to(dev)
+    mk = lambda codes: nn.VQSwitchGLU(*(nn.VQSwitchLinear(c, g[1], g[2]) for c, g in zip(codes, (gg, gu, gd))))
+    assert torch.equal(mk(wild)(x, inds), mk(clamped)(x, inds))
+
+
 @pytest.mark.parametrize("T,kc", [(16, 4096), (1, 4096), (16, 256)])
 def test_vq_switch_glu_repeats_bit_for_bit(dev, T, kc):
     """The same call twice gives the same bits: the sort's row order inside
