@@ -40,6 +40,12 @@ ROTATE_BYTES = 1 << 30         # rotate weight sets past this for cold numbers
 METRIC = "quantized GEMV/MoE µs per layer + achieved HBM GB/s (% of peak) at M=1,16,512"
 
 
+def _bound(nbytes, flops):
+    """The roofline that bounds a call: MFMA when its FLOPs per byte exceed
+    the ratio of the two published peaks (312.5), else HBM."""
+    return "mfma" if flops / nbytes > (PEAK_BF16_TFLOPS * 1e12) / (PEAK_HBM_GBS * 1e9) else "hbm"
+
+
 def dense_bytes(M, N, K, bits, gs=64):
     w = N * K * bits // 8 + 2 * 2 * N * (K // gs)      # packed + bf16 scales + biases
     return w + 2 * M * K + 2 * M * N
@@ -160,7 +166,8 @@ def bench_kv8(B, H, Hk, L, N, D, cold, calls, dev):
     return {"op": "kv8_decode", "B": B, "H": H, "Hk": Hk, "L": L, "N": N, "D": D,
             "cache": "cold" if cold else "warm", "us": round(us, 3),
             "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
-            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2), "bound": "hbm",
+            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
+            "mfma_frac": round(flops / (us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4), "bound": _bound(nbytes, flops),
             "bytes": nbytes, "flops": flops}
 
 
@@ -280,7 +287,8 @@ def bench_moe(T, cold, calls, dev):
     return {"op": "moe_experts", "T": T, "E": E, "top_k": k, "H": H, "I": I, "bits": bits,
             "experts_routed": distinct, "cache": "cold" if cold else "warm", "us": round(us, 3),
             "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
-            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2), "bound": "hbm",
+            "TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
+            "mfma_frac": round(flops / (us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4), "bound": _bound(nbytes, flops),
             "bytes": nbytes, "flops": flops}
 
 
@@ -329,8 +337,10 @@ def bench_vq(T, kc, cold, calls, dev):
     torch.cuda.empty_cache()
     return {"op": "vq_moe_experts", "T": T, "codebook": f"{kc}x8 fp16", "index_bytes": cb_bytes,
             "experts_routed": distinct, "cache": "cold" if cold else "warm", "us": round(us, 3),
-            "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bound": "hbm",
-            "bytes": nbytes, "flops": 2.0 * T * k * 3 * H * I}
+            "GBps": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+            "TFLOPs": round(2.0 * T * k * 3 * H * I / (us * 1e-6) / 1e12, 2),
+            "mfma_frac": round(2.0 * T * k * 3 * H * I / (us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "bound": _bound(nbytes, 2.0 * T * k * 3 * H * I), "bytes": nbytes, "flops": 2.0 * T * k * 3 * H * I}
 
 
 def bench_vq_packed(T, calls, dev, dim=4, kc=2048, group=64, H=None, I=None):
@@ -603,9 +613,10 @@ def summary(detail):
             else:
                 key = f"c2 {r['bits']}b {r['N']}x{r['K']} M{r['M']}"
         elif op == "moe_experts":
-            key = f"c3 moe T{r['T']}"
+            key = f"c3 moe T{r['T']}" if r["T"] <= 256 else f"prefill moe T{r['T']}"
         elif op == "vq_moe_experts":
-            key = f"c4 vq {r['codebook'].split()[0]} T{r['T']}"
+            key = (f"c4 vq {r['codebook'].split()[0]} T{r['T']}" if r["T"] <= 16
+                   else f"prefill vq {r['codebook'].split()[0]} T{r['T']}")
         elif op == "kv8_decode":
             key = f"c5 kv8 {r['N'] // 1024}k L{r['L']}"
         else:
@@ -709,6 +720,13 @@ def main():
     if full and "moe" in only:
         for t_ in (1, 16):
             detail.append(bench_mx_moe(t_, 30, dev))
+        for t_ in (512, 2048):             # prefill chunks (not a BASELINE row)
+            detail.append(bench_moe(t_, True, 5, dev))
+    if full and "vq" in only:
+        for kc_ in (256, 4096):
+            for t_ in (512, 2048):         # prefill chunks (not a BASELINE row)
+                detail.append(bench_vq(t_, kc_, True, 5, dev))
+    if full and "moe" in only:
         for t_ in (1, 16, 256):
             for cold in (True, False):
                 detail.append(bench_moe(t_, cold, 50 if t_ < 256 else 20, dev))

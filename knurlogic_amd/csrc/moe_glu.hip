@@ -39,12 +39,18 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct GluPlan {
     bool tok;
+    bool gemm;      // expert tiles of 128 or 256 rows on the grouped GEMM (moe_gemm.hip)
     int tm;
     size_t act, y, idx, total;
 };
 
+// Rows per active expert from which both projections run as a grouped GEMM
+// (prefill chunks: 64 rows fill four 16-row fragments of the skinny kernels)
+constexpr int64_t GEMM_MIN_ROWS = 64;
+
 // rows per tile: the average routed pairs per active expert, in 16-row chunks
-static GluPlan plan_glu(int64_t T, int64_t H, int64_t I, int k, int64_t E) {
+// (gemm_ok: the grouped GEMM takes these weights)
+static GluPlan plan_glu(int64_t T, int64_t H, int64_t I, int k, int64_t E, bool gemm_ok) {
     GluPlan p = {};
     const int64_t P = T * k;
     p.tok = P <= tok_max_pairs();
@@ -55,9 +61,13 @@ static GluPlan plan_glu(int64_t T, int64_t H, int64_t I, int k, int64_t E) {
         // at one or two rows per active expert, 4-row tiles: both projections
         // then stage their x rows once per workgroup (qgemv_xs) with two
         // workgroups per CU
-        p.tm = rpt <= 2 ? 4 : qgemv_gather_tile_rows(rpt);
+        const int tm_skinny = rpt <= 2 ? 4 : qgemv_gather_tile_rows(rpt);
+        p.gemm = gemm_ok && rpt >= GEMM_MIN_ROWS;
+        p.tm = p.gemm ? (rpt <= 128 ? 128 : 256) : tm_skinny;
         p.y = align256((size_t)P * H * 2);
-        p.idx = sort_index_bytes(P, E, p.tm);
+        // sized for either tiling, so the workspace query need not know the mode
+        const size_t a = sort_index_bytes(P, E, tm_skinny), b = sort_index_bytes(P, E, p.gemm ? p.tm : tm_skinny);
+        p.idx = a > b ? a : b;
     }
     p.total = p.act + p.y + p.idx;
     return p;
@@ -72,8 +82,7 @@ extern "C" {
 size_t kmi_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k, int64_t E,
                                       int group_size, int bits) {
     if (T <= 0 || H <= 0 || I <= 0 || k <= 0 || E <= 0) return 0;
-    (void)group_size; (void)bits;
-    return plan_glu(T, H, I, k, E).total;
+    return plan_glu(T, H, I, k, E, moe_gemm_supported(H, I, bits, group_size, 0)).total;
 }
 
 }  // extern "C"
@@ -105,7 +114,7 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
     KMI_CHECK_ARG(E <= 4096, "switch_glu: %lld experts (at most 4096)", (long long)E);
     KMI_CHECK_ARG(T * H * 2 < (1LL << 31) && T * k * (H > I ? H : I) * 2 < (1LL << 31),
                   "switch_glu: activations past 2 GiB");
-    const GluPlan p = plan_glu(T, H, I, k, E);
+    const GluPlan p = plan_glu(T, H, I, k, E, moe_gemm_supported(H, I, bits, group_size, mx));
     KMI_CHECK_ARG(!mx || group_size == 32, "switch_glu (mx): group %d (32)", group_size);
     if (!workspace || workspace_bytes < p.total) {
         set_error("switch_glu: workspace of %zu bytes needed, %zu given", p.total, workspace_bytes);
@@ -152,26 +161,36 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
     g.b = (const uint16_t*)b_gu; g.E = E; g.N = I; g.K = H; g.erows = 2 * I; g.up_off = I; g.mx = mx;
     g.y = act; g.rows = P; g.tm = p.tm; g.tiles = sr.tiles; g.sorted = sr.sorted; g.lhs = nullptr;
     g.lhs_div = k; g.Mper = 1;
-    const QgPlan pg = plan_qgemv_unsplit(I, H, sr.max_tiles, p.tm, group_size);
-    g.S = 1; g.gps = pg.gps;
-    if (p.tm != 4 || launch_qgemv_xs(g, bits, group_size, true, p.tm, sr.max_tiles, st) != 0) {
-        rc = launch_qgemv(g, pg, bits, group_size, true, sr.max_tiles, st);
+    if (p.gemm) {
+        rc = launch_moe_gemm(g, bits, group_size, true, p.tm, sr.max_tiles, st);
         if (rc) return rc;
+    } else {
+        const QgPlan pg = plan_qgemv_unsplit(I, H, sr.max_tiles, p.tm, group_size);
+        g.S = 1; g.gps = pg.gps;
+        if (p.tm != 4 || launch_qgemv_xs(g, bits, group_size, true, p.tm, sr.max_tiles, st) != 0) {
+            rc = launch_qgemv(g, pg, bits, group_size, true, sr.max_tiles, st);
+            if (rc) return rc;
+        }
     }
-    KMI_CHECK_LAUNCH("qgemv(gate|up)");
+    KMI_CHECK_LAUNCH(p.gemm ? "moe_gemm(gate|up)" : "qgemv(gate|up)");
     QgArgs d = {};
     d.x = act; d.xrows = P; d.w = w_down; d.s = (const uint16_t*)s_down; d.b = (const uint16_t*)b_down;
     d.E = E; d.N = H; d.K = I; d.erows = H; d.y = y; d.rows = P; d.tm = p.tm; d.tiles = sr.tiles; d.mx = mx;
     d.sorted = sr.sorted; d.lhs = nullptr; d.lhs_div = 1; d.Mper = 1;
-    const QgPlan pd = plan_qgemv_unsplit(H, I, sr.max_tiles, p.tm, group_size);
-    d.S = 1; d.gps = pd.gps;
-    // the down projection stages each tile's act rows once (qgemv_xs) where
-    // they fit
-    if (launch_qgemv_xs(d, bits, group_size, false, p.tm, sr.max_tiles, st) != 0) {
-        rc = launch_qgemv(d, pd, bits, group_size, false, sr.max_tiles, st);
+    if (p.gemm) {
+        rc = launch_moe_gemm(d, bits, group_size, false, p.tm, sr.max_tiles, st);
         if (rc) return rc;
+    } else {
+        const QgPlan pd = plan_qgemv_unsplit(H, I, sr.max_tiles, p.tm, group_size);
+        d.S = 1; d.gps = pd.gps;
+        // the down projection stages each tile's act rows once (qgemv_xs)
+        // where they fit
+        if (launch_qgemv_xs(d, bits, group_size, false, p.tm, sr.max_tiles, st) != 0) {
+            rc = launch_qgemv(d, pd, bits, group_size, false, sr.max_tiles, st);
+            if (rc) return rc;
+        }
     }
-    KMI_CHECK_LAUNCH("qgemv(down)");
+    KMI_CHECK_LAUNCH(p.gemm ? "moe_gemm(down)" : "qgemv(down)");
     if (scores) return kmi_moe_combine(y, scores, dtype, T, k, H, out, stream);
     return OK;
 }
@@ -209,7 +228,7 @@ int kmi_moe_experts(const void* x, const void* logits, int64_t T, int64_t H, int
                   "moe_experts: top-%d of %lld experts (k <= 8, E <= %d)", k, (long long)E, ROUTE_MAX_E);
     if (T == 0) return OK;
     KMI_CHECK_ARG(logits && inds && scores, "moe_experts: null pointer");
-    const GluPlan p = plan_glu(T, H, I, k, E);
+    const GluPlan p = plan_glu(T, H, I, k, E, false);
     if (p.tok && E <= ROUTE_THREADS)   // decode sizes: the gate/up kernel routes its own token
         return switch_glu_impl(x, T, H, I, k, inds, scores, w_gu, s_gu, b_gu, w_down, s_down, b_down, E, dtype,
                                group_size, bits, out, workspace, workspace_bytes, stream, logits, inds, scores);

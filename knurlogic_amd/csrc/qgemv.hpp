@@ -67,6 +67,13 @@ size_t sort_index_bytes(int64_t rows, int64_t E, int tm);     // a multiple of 2
 int launch_sort_rows(const int32_t* rhs, int64_t P, int64_t Mper, int E, int tm, void* index_ws,
                      uint16_t* y, int64_t N, hipStream_t st, SortedRows* out);
 
+// Expert tiles of 128 or 256 rows as a grouped GEMM (moe_gemm.hip): affine
+// 4/8-bit weights, group 32/64/128, K % 64 == 0; glu: gate rows at 0, up rows
+// at a.up_off, out = SwiGLU(gate, up); x row = row id / a.lhs_div
+bool moe_gemm_supported(int64_t H, int64_t I, int bits, int gs, int mx);
+int launch_moe_gemm(const QgArgs& a, int bits, int gs, bool glu, int tile_rows, int64_t tile_slots,
+                    hipStream_t st);
+
 // glu: gate rows at 0, up rows at a.up_off, out = SwiGLU(gate, up) in bf16
 int launch_qgemv(const QgArgs& a, const QgPlan& p, int bits, int gs, bool glu, int64_t ntiles,
                  hipStream_t st);

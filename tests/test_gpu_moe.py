@@ -111,10 +111,13 @@ def _experts(rng, E, H, I, dev, bits=4):
                                        (100, 16, 256, 128, 4), (1, 128, 2048, 768, 8),
                                        (8, 128, 2048, 768, 8), (9, 128, 2048, 768, 8),
                                        (16, 128, 2048, 768, 8), (40, 128, 2048, 768, 8),
-                                       (256, 128, 2048, 768, 8)])
+                                       (256, 128, 2048, 768, 8), (256, 4, 512, 320, 2),
+                                       (600, 4, 256, 192, 2), (150, 8, 1024, 128, 4)])
 def test_switch_glu_matches_the_oracle(dev, T, E, H, I, k, bits):
     """One library call (token-major up to 64 (token, slot) pairs, grouped by
-    expert above), the separate gather_qmm path, and the fused combine."""
+    expert above: skinny expert tiles, or the grouped GEMM from 64 rows per
+    expert -- 128-row tiles, 256-row tiles with an expert over two, column
+    tiles past N), the separate gather_qmm path, and the fused combine."""
     rng = np.random.default_rng(T * 7 + E + bits)
     glu, fns = _experts(rng, E, H, I, dev, bits)
     assert glu.fused is not None
