@@ -618,7 +618,8 @@ def summary(detail):
             key = (f"c4 vq {r['codebook'].split()[0]} T{r['T']}" if r["T"] <= 16
                    else f"prefill vq {r['codebook'].split()[0]} T{r['T']}")
         elif op == "kv8_decode":
-            key = f"c5 kv8 {r['N'] // 1024}k L{r['L']}"
+            key = f"c5 kv8 {r['N'] // 1024}k L{r['L']}" + (f" D{r['D']} R{r['H'] // r['Hk'] * r['L']}"
+                                                          if r["D"] != 128 else "")
         else:
             continue
         out[key] = f"{r['us']}us {_pct(r)}"
@@ -740,6 +741,10 @@ def main():
             for l_ in (1, 4):
                 for cold in (True, False):
                     detail.append(bench_kv8(4, 32, 4, l_, n_, 128, cold, 50, dev))
+        # head dims 256 and 512 (16 query heads over 4 KV heads), and 64 query
+        # rows per KV head at 512 (16 heads over 1, 4 tokens): cold only
+        for h_, hk_, l_, d_ in ((16, 4, 1, 256), (16, 4, 1, 512), (16, 1, 4, 512)):
+            detail.append(bench_kv8(4, h_, hk_, l_, 32768, d_, True, 20, dev))
 
     ceil = None if (args.quick or args.no_ceilings) else ceilings(dev, nbytes)
     cpu = None if args.no_cpu else cpu_baseline()

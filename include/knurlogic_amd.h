@@ -215,9 +215,11 @@ size_t kmi_gather_qmm_workspace_bytes(int64_t P, int64_t M, int64_t E, int64_t K
  *   Query head h reads KV head h / (H/Hk); q is pre-multiplied by `scale`.
  *   mask: [B, L, N] uint8 (1 = visible) or NULL; causal (L > 1): row l sees
  *   keys n <= N - L + l.  A row that sees no key is 0.
- * D in {128, 256}; group divides D and is at least D/4; (H/Hk)*L <= 64
- * (<= 32 at D = 256); 8-bit only.  `workspace` (kmi_kv8_workspace_bytes)
- * holds the per-block partials.
+ * D in {128, 256, 384, 512}; group divides D and is a multiple of 16 (the
+ * reference takes multiples of D/32 -- kvattn.py:221-222 -- which adds
+ * groups of 4 and 8 at D = 128 and of 8 at D = 256, sizes mlx's quantize
+ * does not make); (H/Hk)*L <= 64; 8-bit only.  `workspace`
+ * (kmi_kv8_workspace_bytes) holds the per-block partials.
  */
 int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
                    const uint32_t* kw, const void* ks, const void* kb,

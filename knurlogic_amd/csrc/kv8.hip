@@ -23,10 +23,14 @@
 // partial per workgroup: o / l in fp16 (a convex combination of dequantized
 // V rows, so it is bounded like V) and (m, l) in fp32.  kv8_combine merges
 // the blocks' partials (log-sum-exp) and writes q's dtype.
+//
+// kv8_partial keeps every row's state of the KV head in a wave's registers,
+// which holds for D = 128 (up to 64 rows) and D = 256 (up to 32) with one
+// group per D/4-wide lane run; kv8_wide takes the other shapes (D up to
+// 512, 64 rows, groups of 16 and up) one 16-row tile per workgroup.
 #include "common.hpp"
 #include "../../include/knurlogic_amd.h"
 
-#include <stdlib.h>
 
 namespace kmi {
 
@@ -456,6 +460,351 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
     }
 }
 
+// =============================================================================
+// kv8_wide: the shapes whose state kv8_partial's registers do not hold --
+// head dims up to 512 (D = 128 DC), up to 64 query rows per KV head at any
+// head dim, and groups down to 16 (the reference's rule, kvattn.py:221-228,
+// for every group size that is a multiple of 16).
+//
+// One workgroup per (b, hk, key block, 16-row tile): its O accumulators are
+// one row tile over all of D (D / 4 fp32 per lane), and R / 16 workgroups
+// share a key block, their numbering keeping the row tiles of a block on one
+// XCD so the block's K/V bytes come from HBM once and from L2 after.  The 4
+// waves take interleaved 32-key steps as in kv8_partial, and a step walks D
+// in chunks of 128: K^ chunk -> MFMA A operands (lane (key, run jg) owns
+// d in [128 c + 32 jg, +32), a group per 16-d half), S^T += K^ Q^T over the
+// chunk; the online softmax over the step's keys; then per chunk V^ into
+// the wave's [128][32] V^T tile (P^T key order) and O^T += V^T P^T.  Every
+// unit's raw loads (a K chunk, a V chunk) are issued one unit ahead, into
+// the register set the previous unit has just freed.  The waves merge in
+// LDS as in kv8_partial, and kv8_combine merges the blocks.
+// =============================================================================
+// Q^T operands of kv8_wide for row r (0 past R): the 8 q values of d run
+// 128 c + 32 jg + 8 kk, times `scale`, in fp16.  All loads issue before any use.
+template <class QT, int DC>
+__device__ __forceinline__ void load_q_wide(u32x4 (&qop)[DC][4], const Kv8Args& a, int b, int hk,
+                                            int r, int jg) {
+    constexpr int D = 128 * DC;
+    constexpr int QES = (int)sizeof(typename QT::storage);
+    constexpr int V16 = QES / 2;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q, (int64_t)a.B * a.H * a.L * D * QES);
+    const bool rok = r < a.R;
+    const int rr = rok ? r : 0;
+    const int h = hk * (a.H / a.Hk) + rr / a.L, lq = rr % a.L;
+    const uint32_t e0 = (uint32_t)((((b * a.H + h) * a.L + lq) * D) + 32 * jg);
+    u32x4 raw[DC][4][V16];
+#pragma unroll
+    for (int c = 0; c < DC; c++)
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int v = 0; v < V16; v++)
+                raw[c][kk][v] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rq, (int)((e0 + 128 * c + 8 * kk) * (uint32_t)QES + 16u * v), 0, 0);
+#pragma unroll
+    for (int c = 0; c < DC; c++)
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            float x[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                if constexpr (QES == 4) {
+                    x[e] = __uint_as_float(raw[c][kk][e / 4][e % 4]);
+                } else {
+                    const uint32_t w = raw[c][kk][0][e / 2];
+                    x[e] = QT::load((uint16_t)(e % 2 ? w >> 16 : w & 0xffffu));
+                }
+            }
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = rok ? pack_f16(x[2 * e] * a.scale, x[2 * e + 1] * a.scale) : 0u;
+            qop[c][kk] = o;
+        }
+}
+
+template <int DC, class ST>
+__global__ __launch_bounds__(256, 1) void kv8_wide(Kv8Args a, int nrt) {
+    constexpr int D = 128 * DC;
+    constexpr int ES = (int)sizeof(typename ST::storage);
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, jg = lane >> 4;
+    // workgroup -> (key block, row tile): the row tiles of a block share an XCD
+    const int xid = (int)blockIdx.x, xcd = xid & 7, rest = xid >> 3;
+    const int rtile = rest % nrt, blk = (rest / nrt) * 8 + xcd;
+    if (blk >= a.nblk) return;
+    const int bh = blockIdx.y;
+    const int b = bh / a.Hk, hk = bh % a.Hk;
+    const int R = a.R, N = a.N, L = a.L;
+    const int r = 16 * rtile + l16;                      // this lane's query row
+    const bool rok = r < R;
+
+    const char* bp[6];
+#pragma unroll
+    for (int i = 0; i < 6; i++) {
+        const int es = (i == 0 || i == 3) ? 4 : ES;
+        bp[i] = (const char*)a.base[i] + (b * a.st[i][0] + hk * a.st[i][1]) * es;
+    }
+    const uint32_t kst = (uint32_t)a.st[0][2] * 4u, vst = (uint32_t)a.st[3][2] * 4u;
+    const uint32_t kss = (uint32_t)a.st[1][2], kbs = (uint32_t)a.st[2][2];
+    const uint32_t vss = (uint32_t)a.st[4][2], vbs = (uint32_t)a.st[5][2];
+
+    const int steps = a.keys_per_wg / KV_WG_KEYS;
+    const int kbase = blk * a.keys_per_wg + wave * KV_STEP;
+
+    // ---- raw data of one unit, issued a unit ahead --------------------------------
+    u32x4 kr[2][2];                 // K chunk: key tile nt, 16-byte half of the lane's 32-d run
+    uint32_t ksr[2][2], kbr[2][2];
+    u32x4 vr[4];                    // V chunk: the lane's (key quad, 16-byte piece), 4 keys
+    uint32_t vsr[4], vbr[4];
+    const int vquad = lane >> 3, vpiece = lane & 7;     // 8 quads x 8 pieces of a 128-d chunk
+    auto views = [&](bool live, __amdgpu_buffer_rsrc_t (&rs)[6]) {
+#pragma unroll
+        for (int i = 0; i < 6; i++) rs[i] = make_rsrc(bp[i], live ? a.ext[i] : 0);
+    };
+    auto issue_k = [&](int j, int c) {
+        const bool live = j < steps;
+        __amdgpu_buffer_rsrc_t rs[6];
+        views(live, rs);
+        const uint32_t n0 = (uint32_t)(kbase + (live ? j : 0) * KV_WG_KEYS);
+        const uint32_t d0 = (uint32_t)(128 * c + 32 * jg);
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const uint32_t n = n0 + 16u * nt + l16;
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const uint32_t g = (d0 + 16u * hh) / (uint32_t)a.group;
+                kr[nt][hh] = __builtin_amdgcn_raw_buffer_load_b128(rs[0], (int)(n * kst + d0 + 16u * hh), 0, AUX_NT);
+                ksr[nt][hh] = load_scale_raw<ST>(rs[1], n * kss + g);
+                kbr[nt][hh] = load_scale_raw<ST>(rs[2], n * kbs + g);
+            }
+        }
+    };
+    auto issue_v = [&](int j, int c) {
+        const bool live = j < steps;
+        __amdgpu_buffer_rsrc_t rs[6];
+        views(live, rs);
+        const uint32_t n0 = (uint32_t)(kbase + (live ? j : 0) * KV_WG_KEYS);
+        const uint32_t d0 = (uint32_t)(128 * c + 16 * vpiece);
+        const uint32_t g = d0 / (uint32_t)a.group;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const uint32_t n = n0 + 4u * vquad + kk;
+            vr[kk] = __builtin_amdgcn_raw_buffer_load_b128(rs[3], (int)(n * vst + d0), 0, AUX_NT);
+            vsr[kk] = load_scale_raw<ST>(rs[4], n * vss + g);
+            vbr[kk] = load_scale_raw<ST>(rs[5], n * vbs + g);
+        }
+    };
+    issue_k(0, 0);
+
+    // ---- Q^T operands (fp16, pre-scaled): row r, d = 128 c + 32 jg + 8 kk .. +8 ---
+    u32x4 qop[DC][4];
+    if (a.qdt == F32) load_q_wide<TF32, DC>(qop, a, b, hk, r, jg);
+    else if (a.qdt == F16) load_q_wide<TF16, DC>(qop, a, b, hk, r, jg);
+    else load_q_wide<TBF16, DC>(qop, a, b, hk, r, jg);
+
+    float m = -INFINITY, lsum = 0.f;
+    f32x4 O[DC][8];
+#pragma unroll
+    for (int c = 0; c < DC; c++)
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) O[c][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    _Float16* vt = (_Float16*)smem + wave * 128 * KV_STEP;   // [128][32] V^T in P^T key order
+    const bool has_mask = a.mask != nullptr;
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.mask, (int64_t)a.B * L * N);
+    const int lq = (rok ? r : 0) % L;
+
+    for (int j = 0; j < steps; j++) {
+        const int n0 = kbase + j * KV_WG_KEYS;
+        uint32_t mraw[8];
+        if (has_mask) {
+            const uint32_t row = (uint32_t)((b * L + lq) * N);
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                mraw[e] = __builtin_amdgcn_raw_buffer_load_b8(
+                    rm, (int)(row + (uint32_t)(n0 + 16 * (e >> 2) + 4 * jg + (e & 3))), 0, 0);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) mraw[e] = 1u;
+        }
+
+        // ---- S^T = K^ Q^T, chunk by chunk -------------------------------------------
+        f32x4 S[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int c = 0; c < DC; c++) {
+            u32x4 kop[2][4];
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) {
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    const float sc = scale_val<ST>(ksr[nt][kk >> 1]), bi = scale_val<ST>(kbr[nt][kk >> 1]);
+                    u32x4 o;
+#pragma unroll
+                    for (int w2 = 0; w2 < 2; w2++) {
+                        const uint32_t wd = kr[nt][kk >> 1][2 * (kk & 1) + w2];
+                        o[2 * w2] = pack_f16(__builtin_fmaf(sc, byte_f(wd, 0), bi), __builtin_fmaf(sc, byte_f(wd, 1), bi));
+                        o[2 * w2 + 1] = pack_f16(__builtin_fmaf(sc, byte_f(wd, 2), bi), __builtin_fmaf(sc, byte_f(wd, 3), bi));
+                    }
+                    kop[nt][kk] = o;
+                }
+            }
+            if (c + 1 < DC) issue_k(j, c + 1);
+            else issue_v(j, 0);
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) S[nt] = mfma_f16(kop[nt][kk], qop[c][kk], S[nt]);
+        }
+
+        // ---- online softmax over the step's keys, row r -------------------------------
+        u32x4 P;
+        {
+            float sv[8];
+            float bm = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int n = n0 + 16 * (e >> 2) + 4 * jg + (e & 3);
+                const bool ok = (n < N) & rok & (!a.causal | (n <= N - L + lq)) & (mraw[e] != 0);
+                const float v = ok ? S[e >> 2][e & 3] : -INFINITY;
+                sv[e] = v;
+                bm = fmaxf(bm, v);
+            }
+            bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+            const float mn = fmaxf(m, bm);
+            float corr = 1.f, ps = 0.f;
+            float pv[8];
+            if (mn == -INFINITY) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) pv[e] = 0.f;
+            } else {
+                corr = __expf(m - mn);   // m = -inf -> 0
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    pv[e] = __expf(sv[e] - mn);
+                    ps += pv[e];
+                }
+            }
+            ps += __shfl_xor(ps, 16, 64);
+            ps += __shfl_xor(ps, 32, 64);
+            lsum = lsum * corr + ps;
+            m = mn;
+#pragma unroll
+            for (int c = 0; c < DC; c++)
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) O[c][dt] *= corr;
+            P = u32x4{pack_f16(pv[0], pv[1]), pack_f16(pv[2], pv[3]), pack_f16(pv[4], pv[5]), pack_f16(pv[6], pv[7])};
+        }
+
+        // ---- O^T += V^T P^T, chunk by chunk: quad q (keys 4q..4q+3) at fp16
+        //      offset 8 (q & 3) + 4 (q >> 2) of a V^T row
+#pragma unroll
+        for (int c = 0; c < DC; c++) {
+            {
+                const int slot = 8 * (vquad & 3) + 4 * (vquad >> 2);
+                float sc[4], bi[4];
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    sc[kk] = scale_val<ST>(vsr[kk]);
+                    bi[kk] = scale_val<ST>(vbr[kk]);
+                }
+#pragma unroll
+                for (int w = 0; w < 4; w++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        float f[4];
+#pragma unroll
+                        for (int kk = 0; kk < 4; kk++) f[kk] = __builtin_fmaf(sc[kk], byte_f(vr[kk][w], e), bi[kk]);
+                        const int d = 16 * vpiece + 4 * w + e;
+                        *(u32x2*)(vt + d * KV_STEP + slot) = u32x2{pack_f16(f[0], f[1]), pack_f16(f[2], f[3])};
+                    }
+            }
+            if (c + 1 < DC) issue_v(j, c + 1);
+            else issue_k(j + 1, 0);
+            wave_lds_sync();
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const u32x4 A = *(const u32x4*)(vt + (16 * dt + l16) * KV_STEP + 8 * jg);
+                O[c][dt] = mfma_f16(A, P, O[c][dt]);
+            }
+        }
+    }
+
+    // ---- merge the 4 waves in a fixed order: (2 -> 0, 3 -> 1), then 1 -> 0 ------
+    __syncthreads();
+    constexpr int OP = D + 4, SLOT = 16 * OP;
+    float* mw = (float*)smem;                          // [4][16]
+    float* lw = mw + KV_WAVES * 16;                    // [4][16]
+    float* slot = lw + KV_WAVES * 16;                  // [2][16][OP]
+    if (jg == 0) {
+        mw[wave * 16 + l16] = m;
+        lw[wave * 16 + l16] = lsum;
+    }
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < KV_WAVES; w++) M = fmaxf(M, mw[w * 16 + l16]);
+    float Ls = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < KV_WAVES; w++) {
+            const float mv = mw[w * 16 + l16];
+            if (mv != -INFINITY) Ls += lw[w * 16 + l16] * __expf(mv - M);
+        }
+    }
+    {
+        const float f = m == -INFINITY ? 0.f : __expf(m - M);
+#pragma unroll
+        for (int c = 0; c < DC; c++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) O[c][dt] *= f;
+    }
+    if (wave >= 2) {
+        float* sl = slot + (wave - 2) * SLOT;
+#pragma unroll
+        for (int c = 0; c < DC; c++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+                *(f32x4*)(sl + l16 * OP + 128 * c + 16 * dt + 4 * jg) = O[c][dt];
+    }
+    __syncthreads();
+    if (wave < 2) {
+        float* sl = slot + wave * SLOT;
+#pragma unroll
+        for (int c = 0; c < DC; c++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                f32x4* pp = (f32x4*)(sl + l16 * OP + 128 * c + 16 * dt + 4 * jg);
+                O[c][dt] += *pp;
+                if (wave == 1) *pp = O[c][dt];   // same wave, same address: in order
+            }
+    }
+    __syncthreads();
+    if (wave == 0 && rok) {
+        const float* sl = slot + SLOT;
+        const int64_t pb = ((int64_t)bh * a.nblk + blk) * R;
+        const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+        _Float16* orow = a.po + (pb + r) * D;
+#pragma unroll
+        for (int c = 0; c < DC; c++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const f32x4 v = (O[c][dt] + *(const f32x4*)(sl + l16 * OP + 128 * c + 16 * dt + 4 * jg)) * inv;
+                *(u32x2*)(orow + 128 * c + 16 * dt + 4 * jg) = u32x2{pack_f16(v[0], v[1]), pack_f16(v[2], v[3])};
+            }
+        if (jg == 0) a.pml[pb + r] = make_float2(M, Ls);
+    }
+}
+
+template <int DC>
+constexpr size_t kv8_wide_lds() {
+    constexpr size_t vt = (size_t)KV_WAVES * 128 * KV_STEP * 2;
+    constexpr size_t merge = (size_t)(2 * KV_WAVES * 16 + 2 * 16 * (128 * DC + 4)) * 4;
+    return vt > merge ? vt : merge;
+}
+
 // out[b, h, l, :] = sum_blk w_blk o_blk / sum_blk w_blk, w_blk = l_blk exp(m_blk - max m),
 // with o_blk stored as o / l; 0 when no block saw a key (the reference kernel's rule).
 // One wave per (b, hk, row r); blocks merged 32 at a time with online rescaling,
@@ -465,7 +814,8 @@ __global__ __launch_bounds__(64) void kv8_combine(const _Float16* __restrict__ p
                                                   const float2* __restrict__ pml, int nblk, int R,
                                                   int H, int Hk, int L, int qdt, void* __restrict__ out,
                                                   int64_t po_bytes, int64_t pml_bytes) {
-    constexpr int PER = D / 64;          // d per lane (2 or 4)
+    constexpr int PER = D / 64;          // d per lane (2, 4, 6 or 8)
+    constexpr int W = PER / 2;           // 32-bit words per lane and block
     constexpr int CH = 32;               // blocks per chunk
     const int row = blockIdx.x;          // (b*Hk + hk) * R + r
     const int bh = row / R, r = row % R;
@@ -477,16 +827,25 @@ __global__ __launch_bounds__(64) void kv8_combine(const _Float16* __restrict__ p
 #pragma unroll
     for (int e = 0; e < PER; e++) num[e] = 0.f;
     for (int i0 = 0; i0 < nblk; i0 += CH) {
-        uint32_t ov[CH][PER / 2];
+        uint32_t ov[CH][W];
 #pragma unroll
         for (int t = 0; t < CH; t++) {
             const uint32_t off = (uint32_t)((((int64_t)bh * nblk + i0 + t) * R + r) * D + lane * PER) * 2u;
-            if constexpr (PER == 2) {
+            if constexpr (W == 1) {
                 ov[t][0] = __builtin_amdgcn_raw_buffer_load_b32(rp, (int)off, 0, 0);
-            } else {
+            } else if constexpr (W == 2) {
                 const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rp, (int)off, 0, 0);
                 ov[t][0] = v.x;
                 ov[t][1] = v.y;
+            } else if constexpr (W == 3) {
+                const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rp, (int)off, 0, 0);
+                ov[t][0] = v.x;
+                ov[t][1] = v.y;
+                ov[t][2] = __builtin_amdgcn_raw_buffer_load_b32(rp, (int)(off + 8u), 0, 0);
+            } else {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)off, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++) ov[t][e] = v[e];
             }
         }
         const int i = i0 + lane;
@@ -507,7 +866,7 @@ __global__ __launch_bounds__(64) void kv8_combine(const _Float16* __restrict__ p
         for (int t = 0; t < CH; t++) {
             const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), t));
 #pragma unroll
-            for (int e = 0; e < PER / 2; e++) {
+            for (int e = 0; e < W; e++) {
                 const f16x2 hv = __builtin_bit_cast(f16x2, ov[t][e]);
                 num[2 * e] += c * (float)hv[0];
                 num[2 * e + 1] += c * (float)hv[1];
@@ -539,21 +898,22 @@ struct Kv8Plan {
     size_t po_bytes, pml_off, pml_bytes, total;
 };
 
-// Workgroups per call the key blocks aim at (KMI_KV8_WGS overrides; read once).
-static int kv8_target_wgs() {
-    static int v = [] {
-        const char* e = getenv("KMI_KV8_WGS");
-        const int x = e ? atoi(e) : 0;
-        return x > 0 ? x : 512;
-    }();
-    return v;
-}
+// Workgroups per call the key blocks aim at: 512 for kv8_partial (256 / 512
+// / 1024 measured alike at 8k keys); for kv8_wide one round of the chip --
+// 256 CUs times the workgroups a CU holds (2 at D = 128, else 1) -- over the
+// key blocks times the row tiles (at D = 512: 166 us at 512, 155 at 256; at
+// 64 rows 160 -> 148).
+constexpr int KV8_TARGET_WGS = 512;
 
-static Kv8Plan plan_kv8(int B, int Hk, int N, int D, int R) {
+// The key blocks of a call.  kv8_wide's plan (wide_tiles = its row tiles)
+// has at most as many blocks as kv8_partial's, so the workspace
+// kmi_kv8_workspace_bytes sizes by the latter holds either.
+static Kv8Plan plan_kv8(int B, int Hk, int N, int D, int R, int wide_tiles = 0) {
     Kv8Plan p;
     p.rt = (R + 15) / 16;
     const int64_t pairs = (int64_t)B * Hk;
-    const int64_t want_blk = ceil_div(kv8_target_wgs(), pairs);
+    const int64_t target = wide_tiles ? (D == 128 ? 512 : 256) / wide_tiles : KV8_TARGET_WGS;
+    const int64_t want_blk = ceil_div(target, pairs);
     int64_t kpw = ceil_div(N > 0 ? N : 1, want_blk);
     kpw = ceil_div(kpw, KV_WG_KEYS) * KV_WG_KEYS;
     p.keys_per_wg = (int)kpw;
@@ -581,9 +941,40 @@ static void launch_partial_st(const Kv8Args& a, int D, int rt, dim3 grid, hipStr
         else if (rt == 3) launch_partial<128, 3, ST>(a, grid, st);
         else launch_partial<128, 4, ST>(a, grid, st);
     } else {
-        if (rt == 1) launch_partial<256, 1, ST>(a, grid, st);
-        else launch_partial<256, 2, ST>(a, grid, st);
+        launch_partial<256, 2, ST>(a, grid, st);   // 17-32 rows (partial_covers)
     }
+}
+
+template <int DC, class ST>
+static void launch_wide_dc(const Kv8Args& a, int nrt, hipStream_t st) {
+    constexpr size_t lds = kv8_wide_lds<DC>();
+    allow_dynamic_lds_once((const void*)kv8_wide<DC, ST>);
+    const dim3 grid((unsigned)(8 * nrt * ceil_div(a.nblk, 8)), (unsigned)(a.B * a.Hk));
+    kv8_wide<DC, ST><<<grid, 256, lds, st>>>(a, nrt);
+}
+
+template <class ST>
+static void launch_wide(const Kv8Args& a, int D, hipStream_t st) {
+    const int nrt = (a.R + 15) / 16;
+    if (D == 128) launch_wide_dc<1, ST>(a, nrt, st);
+    else if (D == 256) launch_wide_dc<2, ST>(a, nrt, st);
+    else if (D == 384) launch_wide_dc<3, ST>(a, nrt, st);
+    else launch_wide_dc<4, ST>(a, nrt, st);
+}
+
+// kv8_partial holds all R rows' state of a wave in registers: D = 128 up to
+// 64 rows, D = 256 up to 32, one group per D/4-wide lane run.  At D = 256
+// it takes 17-32 rows only: with one row tile kv8_wide is faster (4 x 16
+// heads, 32k keys, 4 rows: 90 vs 100 us; at 32 rows 86 vs 73).
+static bool partial_covers(int D, int group, int R) {
+    return (D == 128 || (D == 256 && R > 16 && R <= 32)) && group >= D / 4;
+}
+
+template <int D>
+static void launch_combine(const Kv8Args& a, const Kv8Plan& p, int q_dtype, void* out, hipStream_t st) {
+    kv8_combine<D><<<(unsigned)(a.B * a.Hk * a.R), 64, 0, st>>>(a.po, a.pml, p.nblk, a.R, a.H, a.Hk, a.L,
+                                                                q_dtype, out, (int64_t)p.po_bytes,
+                                                                (int64_t)p.pml_bytes);
 }
 
 }  // namespace kmi
@@ -607,14 +998,13 @@ int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
     clear_error();
     KMI_CHECK_ARG(q && kw && ks && kb && vw && vs && vb && out && strides, "kv8_decode: null pointer");
     KMI_CHECK_ARG(B > 0 && H > 0 && L > 0 && Hk > 0 && H % Hk == 0, "kv8_decode: bad head counts");
-    KMI_CHECK_ARG(D == 128 || D == 256, "kv8_decode: head dim %d not in {128, 256}", D);
-    KMI_CHECK_ARG(group >= D / 4 && D % group == 0,
-                  "kv8_decode: group %d must divide D=%d and be at least D/4", group, D);
+    KMI_CHECK_ARG(D > 0 && D % 128 == 0 && D <= 512, "kv8_decode: head dim %d not in {128, 256, 384, 512}", D);
+    KMI_CHECK_ARG(group > 0 && group % 16 == 0 && D % group == 0,
+                  "kv8_decode: group %d must divide D=%d and be a multiple of 16", group, D);
     KMI_CHECK_ARG(q_dtype >= BF16 && q_dtype <= F32 && scale_dtype >= BF16 && scale_dtype <= F32,
                   "kv8_decode: bad dtype");
     const int R = (H / Hk) * L;
     KMI_CHECK_ARG(R <= 64, "kv8_decode: %d query rows per KV head (at most 64)", R);
-    KMI_CHECK_ARG(!(D == 256 && R > 32), "kv8_decode: head dim 256 takes at most 32 rows per KV head");
     KMI_CHECK_ARG(N >= 0, "kv8_decode: N=%d", N);
     hipStream_t st = (hipStream_t)stream;
     const int qes = q_dtype == F32 ? 4 : 2;
@@ -624,7 +1014,8 @@ int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
         KMI_CHECK_LAUNCH("kv8_decode(empty)");
         return OK;
     }
-    Kv8Plan p = plan_kv8(B, Hk, N, D, R);
+    const bool wide = !partial_covers(D, group, R);
+    Kv8Plan p = plan_kv8(B, Hk, N, D, R, wide ? (R + 15) / 16 : 0);
     if (!workspace || workspace_bytes < p.total) {
         set_error("kv8_decode: workspace of %zu bytes needed, %zu given", p.total, workspace_bytes);
         return EWORKSPACE;
@@ -657,19 +1048,22 @@ int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
     a.qdt = q_dtype;
     a.B = B; a.H = H; a.Hk = Hk; a.L = L; a.N = N; a.group = group; a.R = R;
     a.causal = causal && L > 1; a.keys_per_wg = p.keys_per_wg; a.nblk = p.nblk; a.scale = scale;
-    dim3 grid((unsigned)p.nblk, (unsigned)(B * Hk));
-    if (scale_dtype == BF16) launch_partial_st<TBF16>(a, D, p.rt, grid, st);
-    else if (scale_dtype == F16) launch_partial_st<TF16>(a, D, p.rt, grid, st);
-    else launch_partial_st<TF32>(a, D, p.rt, grid, st);
-    KMI_CHECK_LAUNCH("kv8_partial");
-    if (D == 128)
-        kv8_combine<128><<<(unsigned)(B * Hk * R), 64, 0, st>>>(a.po, a.pml, p.nblk, R, H, Hk, L, q_dtype,
-                                                               out, (int64_t)p.po_bytes,
-                                                               (int64_t)p.pml_bytes);
-    else
-        kv8_combine<256><<<(unsigned)(B * Hk * R), 64, 0, st>>>(a.po, a.pml, p.nblk, R, H, Hk, L, q_dtype,
-                                                               out, (int64_t)p.po_bytes,
-                                                               (int64_t)p.pml_bytes);
+    if (!wide) {
+        dim3 grid((unsigned)p.nblk, (unsigned)(B * Hk));
+        if (scale_dtype == BF16) launch_partial_st<TBF16>(a, D, p.rt, grid, st);
+        else if (scale_dtype == F16) launch_partial_st<TF16>(a, D, p.rt, grid, st);
+        else launch_partial_st<TF32>(a, D, p.rt, grid, st);
+        KMI_CHECK_LAUNCH("kv8_partial");
+    } else {
+        if (scale_dtype == BF16) launch_wide<TBF16>(a, D, st);
+        else if (scale_dtype == F16) launch_wide<TF16>(a, D, st);
+        else launch_wide<TF32>(a, D, st);
+        KMI_CHECK_LAUNCH("kv8_wide");
+    }
+    if (D == 128) launch_combine<128>(a, p, q_dtype, out, st);
+    else if (D == 256) launch_combine<256>(a, p, q_dtype, out, st);
+    else if (D == 384) launch_combine<384>(a, p, q_dtype, out, st);
+    else launch_combine<512>(a, p, q_dtype, out, st);
     KMI_CHECK_LAUNCH("kv8_combine");
     return OK;
 }

@@ -91,16 +91,19 @@ def _dims(q, K, V, bits):
 
 def supports(q, K, V, bits: int, group: int, mask=None, sinks=None) -> bool:
     """Whether ``decode_sdpa`` takes these shapes (else the caller falls
-    back to dequantize + sdpa).  The rule of kvattn.supports, narrowed to
-    the head dims this build's kernel covers (128 and 256) and to groups of
-    at least D/4 (kvquant's caches use 64, or 32 when D % 64 != 0)."""
+    back to dequantize + sdpa).  The rule of kvattn.supports
+    (engine/kvattn.py:213-239): head dims 128, 256, 384 and 512, up to 64
+    query rows per KV head, groups dividing D -- here multiples of 16, where
+    the reference takes multiples of D/32, which adds groups of 4 and 8 that
+    mlx's quantize does not make -- plus the last-axis-contiguous triples
+    and matching scale/bias dtypes the C ABI reads."""
     if bits != 8 or sinks is not None or q.dim() != 4:
         return False
     B, H, L, D, Hk, Dk, Dv = _dims(q, K, V, bits)
-    if Dk != D or Dv != D or D not in (128, 256) or H % Hk:
+    if Dk != D or Dv != D or D % 128 or D > 512 or H % Hk:
         return False
-    # the kernel's lanes own D/4-wide runs of a key row: one group per run
-    if D % group or group < D // 4 or K[0].shape[0] != B:
+    # a lane's 16-d run of a key row lies in one group
+    if group <= 0 or D % group or group % 16 or K[0].shape[0] != B:
         return False
     for w, sc, bi in (K, V):
         if sc.shape != bi.shape or tuple(sc.shape[:3]) != tuple(w.shape[:3]):
@@ -110,7 +113,7 @@ def supports(q, K, V, bits: int, group: int, mask=None, sinks=None) -> bool:
         if sc.dtype != K[1].dtype or bi.dtype != K[1].dtype:
             return False
     R = (H // Hk) * L
-    if R > MAX_ROWS or (D == 256 and R > 32):
+    if R > MAX_ROWS:
         return False
     if q.dtype not in DTYPE_CODE or K[1].dtype not in DTYPE_CODE:
         return False

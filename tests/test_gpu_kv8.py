@@ -47,7 +47,7 @@ def _check(host, gpu, mask, tmask=None, dtype="bfloat16"):
     return got, ref
 
 
-@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("D", [128, 256, 512])
 @pytest.mark.parametrize("H,Hk", [(4, 4), (8, 2), (16, 2), (16, 1)])
 @pytest.mark.parametrize("N", [1, 7, 256, 1000, 4099])
 def test_a_decode_step_matches_the_oracle(dev, D, H, Hk, N):
@@ -69,13 +69,20 @@ def test_other_group_sizes(dev, g):
     _check(*_case(dev, 1, 8, 2, 1, 500, 128, g=g), None)
 
 
-def test_a_group_narrower_than_a_lane_run_falls_back(dev):
-    (q, K, V, g), (tq, tK, tV) = _case(dev, 1, 8, 2, 1, 64, 256, g=32)
-    assert not kvattn.supports(tq, tK, tV, 8, g)
-    # the fallback: mlx-lm's quantized attention over the packed triples
-    got = kvattn.quantized_sdpa(tq, tK, tV, 256 ** -0.5, None, g, 8)
-    assert_close(to_numpy(got), O.quantized_sdpa(q, K, V, 256 ** -0.5, None, g, 8), what="fallback")
-    assert_close(to_numpy(got), O.kv8_decode(q, K, V, 256 ** -0.5, None, g, 8, "float32"), what="vs kernel semantics")
+@pytest.mark.parametrize("D,g", [(256, 32), (128, 16), (512, 32), (512, 16), (384, 128), (512, 512)])
+def test_groups_narrower_than_a_lane_run_and_other_head_dims(dev, D, g):
+    """The shapes kv8_partial's per-wave state does not cover, taken by the
+    16-row-tile kernel: groups below D/4, head dims 384 and 512."""
+    _check(*_case(dev, 1, 8, 2, 1, 1000, D, g=g, seed=D + g), None)
+
+
+@pytest.mark.parametrize("D,L,H,Hk", [(256, 1, 48, 1), (256, 4, 16, 1), (512, 2, 32, 1), (384, 4, 8, 2),
+                                      (128, 1, 64, 2), (256, 2, 16, 1), (256, 3, 8, 1), (512, 8, 16, 2)])
+def test_many_rows_per_kv_head_at_wide_head_dims(dev, D, L, H, Hk):
+    """17 to 64 query rows per KV head at head dims 256-512 (and 32 rows
+    at 128), causal where L > 1: the 16-row-tile kernel, and at D = 256 with
+    17-32 rows the all-rows-per-wave one."""
+    _check(*_case(dev, 1, H, Hk, L, 900, D, seed=L * H), "causal" if L > 1 else None)
 
 
 def test_many_blocks_per_head(dev):

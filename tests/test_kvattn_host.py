@@ -168,3 +168,27 @@ def test_quantize_cache_list_recurses_and_leaves_the_rest():
     assert type(out[2].caches[1]) is Recurrent
     assert out[3] is filled
     assert type(out[4]) is KC.BatchQuantKVCache
+
+
+def _triples(B, H, Hk, L, N, D, g, dtype=torch.bfloat16):
+    q = torch.zeros(B, H, L, D, dtype=dtype)
+    w = torch.zeros(B, Hk, N, D // 4, dtype=torch.int32)
+    sc = torch.zeros(B, Hk, N, D // g, dtype=dtype)
+    return q, (w, sc, sc), (w, sc.clone(), sc.clone())
+
+
+@pytest.mark.parametrize("D,g,H,Hk,L,ok", [
+    (128, 64, 8, 2, 1, True), (256, 32, 8, 2, 1, True), (128, 16, 8, 2, 1, True),
+    (384, 128, 8, 2, 1, True), (512, 16, 8, 2, 1, True), (512, 512, 8, 2, 1, True),
+    (256, 64, 64, 1, 1, True), (512, 64, 16, 1, 4, True),      # 64 rows per KV head
+    (128, 8, 8, 2, 1, False), (256, 8, 8, 2, 1, False),        # groups mlx does not make
+    (512, 48, 8, 2, 1, False),                                  # does not divide D
+    (64, 32, 8, 2, 1, False), (640, 64, 8, 2, 1, False),       # head dims outside 128..512
+    (128, 64, 32, 1, 3, False),                                 # 96 rows per KV head
+])
+def test_the_shape_rule(D, g, H, Hk, L, ok):
+    """kvattn.supports: the reference's rule (engine/kvattn.py:213-239) on
+    head dims, rows per KV head and groups, with groups narrowed to
+    multiples of 16."""
+    q, K, V = _triples(1, H, Hk, L, 64, D, g)
+    assert kvattn.supports(q, K, V, 8, g) is ok
