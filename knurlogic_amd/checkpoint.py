@@ -37,35 +37,54 @@ SCALED_MODES = {4: "mxfp4", 8: "mxfp8"}
 
 
 def artifact_quantization(model_path) -> dict[str, Any]:
-    """The ``quantization`` (or ``quantization_config``) block of an
-    artifact's config.json, {} without one (packed.py:23-30)."""
-    p = Path(str(model_path)) / "config.json"
-    if not p.is_file():
+    """The artifact's quantization settings: config.json's ``quantization``
+    block, else its ``quantization_config`` block, else {} (also when there
+    is no config.json) -- packed.py:23-30."""
+    cfg_file = Path(str(model_path)) / "config.json"
+    if not cfg_file.is_file():
         return {}
-    cfg = json.loads(p.read_text())
-    return cfg.get("quantization") or cfg.get("quantization_config") or {}
+    cfg = json.loads(cfg_file.read_text())
+    for key in ("quantization", "quantization_config"):
+        if cfg.get(key):
+            return cfg[key]
+    return {}
+
+
+def _declared_mode(quant: dict, key: str):
+    """The mode the settings give layer ``key``: its own entry's, else the
+    top-level one (either may be absent)."""
+    entry = quant.get(key)
+    if isinstance(entry, dict) and entry.get("mode"):
+        return entry["mode"]
+    return quant.get("mode")
 
 
 def recipe(weights: dict, path: str, in_dims: int, quant: dict | None = None,
            prefix: str = "") -> dict | None:
-    """{group_size, bits, mode} the packed ``path`` was written with, or
-    None when ``weights`` holds it unpacked (packed.recipe, :33-64).
+    """How the packed layer ``path`` was quantized -- {group_size, bits,
+    mode} -- read off its tensors' shapes, or None when ``weights`` holds it
+    unpacked (no ``.scales``); packed.recipe, packed.py:33-64.  A layer with
+    biases is affine; one without takes the mode the settings declare for
+    it (``prefix + path``, then the top level) unless that is affine or
+    absent, in which case its width decides (4 -> mxfp4, 8 -> mxfp8).
     ``weights`` may hold anything with a ``.shape``."""
-    s = weights.get(f"{path}.scales")
-    if s is None:
+    scales = weights.get(f"{path}.scales")
+    if scales is None:
         return None
-    bits = int(weights[f"{path}.weight"].shape[-1]) * 32 // int(in_dims)
-    gs = int(in_dims) // int(s.shape[-1])
+    in_dims = int(in_dims)
+    words = int(weights[f"{path}.weight"].shape[-1])
+    out = {"group_size": in_dims // int(scales.shape[-1]), "bits": words * 32 // in_dims}
     if f"{path}.biases" in weights:
-        kind = "affine"
-    else:
-        quant = quant or {}
-        layer = quant.get(prefix + path)
-        mode = (layer.get("mode") if isinstance(layer, dict) else None) or quant.get("mode")
-        kind = mode if mode not in (None, "affine") else SCALED_MODES.get(bits)
-        if kind is None:
-            raise ValueError(f"{path}: {bits}-bit without biases is neither affine nor mxfp4/mxfp8")
-    return {"group_size": gs, "bits": bits, "mode": kind}
+        out["mode"] = "affine"
+        return out
+    mode = _declared_mode(quant or {}, prefix + path)
+    if mode in (None, "affine"):
+        mode = SCALED_MODES.get(out["bits"])
+    if mode is None:
+        raise ValueError(f"{path}: packed at {out['bits']} bits without biases, which is neither affine "
+                         f"nor mxfp4/mxfp8")
+    out["mode"] = mode
+    return out
 
 
 def in_dims_from_config(weights: dict, path: str, quant: dict) -> int | None:

@@ -9,7 +9,6 @@
 // both projections run over the same tiles (qgemv.hip), so each routed
 // expert's weights are read once per call: gate|up with the SwiGLU
 // epilogue, then down, then the weighted combine.
-#include <cstdlib>
 
 #include "moe_tok.hpp"
 #include "qgemv.hpp"
@@ -24,16 +23,6 @@ namespace kmi {
 // 46 us grouped, T = 8 60 vs 64 us) and loses above (T = 16 105 vs 83 us:
 // each pair re-reads its expert).
 constexpr int64_t TOK_MAX_PAIRS = 64;
-
-// pairs that still run token-major (KMI_TOK_MAX_PAIRS overrides; read once)
-static int64_t tok_max_pairs() {
-    static int64_t v = [] {
-        const char* e = getenv("KMI_TOK_MAX_PAIRS");
-        const long long x = e ? atoll(e) : -1;
-        return x >= 0 ? (int64_t)x : TOK_MAX_PAIRS;
-    }();
-    return v;
-}
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -53,7 +42,7 @@ constexpr int64_t GEMM_MIN_ROWS = 64;
 static GluPlan plan_glu(int64_t T, int64_t H, int64_t I, int k, int64_t E, bool gemm_ok) {
     GluPlan p = {};
     const int64_t P = T * k;
-    p.tok = P <= tok_max_pairs();
+    p.tok = P <= TOK_MAX_PAIRS;
     p.act = align256((size_t)P * I * 2);
     if (!p.tok) {
         const int64_t active = P < E ? P : E;

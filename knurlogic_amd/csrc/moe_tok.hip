@@ -22,7 +22,6 @@
 #include "moe_tok.hpp"
 #include "route.hpp"
 
-#include <cstdlib>
 #include "../../include/knurlogic_amd.h"
 
 namespace kmi {
@@ -403,11 +402,8 @@ int launch_moe_glu_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
 int launch_moe_down_tok(const MoeTokArgs& a, int bits, hipStream_t st) {
     const int64_t CK = 128 / bits, C = a.K / CK;
     const int U = (int)ceil_div((int64_t)a.k * C, 64);
-    // two rows per wave while the grid keeps >= 2048 waves (KMI_DOWN_RPW
-    // overrides: tuning)
-    int rpw = U <= 4 && a.N * a.T / 2 >= 2048 ? 2 : 1;
-    const char* ov = getenv("KMI_DOWN_RPW");
-    if (ov && *ov) rpw = atoi(ov) == 2 && U <= 4 ? 2 : 1;
+    // two rows per wave while the grid keeps >= 2048 waves
+    const int rpw = U <= 4 && a.N * a.T / 2 >= 2048 ? 2 : 1;
     const dim3 grid((unsigned)ceil_div(a.N, TOK_WV * rpw), (unsigned)a.T);
     const size_t lds = (size_t)a.k * ((size_t)a.K * 2 + (size_t)C * 16);
     if (a.E * a.N * (a.K * bits / 8) >= (1LL << 31)) {

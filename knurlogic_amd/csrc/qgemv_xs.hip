@@ -24,7 +24,6 @@
 #include "qgemv_dl.hpp"
 #include "../../include/knurlogic_amd.h"
 
-#include <cstdlib>
 
 namespace kmi {
 
@@ -320,25 +319,10 @@ namespace {
 // column blocks per workgroup: 4, fewer while the grid would have under
 // 1024 workgroups (measured at 128 experts, top-8, 2048 -> 768 -> 2048:
 // down takes 4 from 16 to 256 tokens, gate|up 2 at 16 tokens)
-// (KMI_XS_G overrides: tuning; read once)
 int xs_blocks_per_wg(int64_t NB, int64_t tiles) {
-    static int ov = [] {
-        const char* e = getenv("KMI_XS_G");
-        return e ? atoi(e) : 0;
-    }();
-    if (ov > 0) return ov < NB ? ov : (int)NB;
     int64_t g = NB < 4 ? NB : 4;
     while (g > 1 && ceil_div(NB, g) * tiles < 1024) g--;
     return (int)g;
-}
-
-// KMI_XS=0 keeps every call on qgemv (comparisons; read once)
-bool xs_enabled() {
-    static bool v = [] {
-        const char* e = getenv("KMI_XS");
-        return !(e && *e == '0');
-    }();
-    return v;
 }
 
 constexpr size_t XS_LDS_MAX = 160 * 1024 - 1024;   // the static row tables stay below 1 KB
@@ -383,7 +367,7 @@ int launch_xs_glu(const QgArgs& a, bool glu, int tr, int64_t ntiles, uint32_t xr
 
 // 0: launched; 1: this shape does not fit the kernel (the caller takes qgemv)
 int launch_qgemv_xs(const QgArgs& a, int bits, int gs, bool glu, int tile_rows, int64_t ntiles, hipStream_t st) {
-    if (!xs_enabled() || !a.tiles || !a.sorted || a.S != 1 || a.K % DL_KC != 0) return 1;
+    if (!a.tiles || !a.sorted || a.S != 1 || a.K % DL_KC != 0) return 1;
     const int tr = tile_rows;
     if (!(tr == 4 || tr == 16 || tr == 32 || tr == 64) || !(bits == 4 || bits == 8)) return 1;
     if (glu && a.up_off <= 0) return 1;

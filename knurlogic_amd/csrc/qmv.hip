@@ -13,7 +13,6 @@
 #include "qgemv.hpp"
 #include "../../include/knurlogic_amd.h"
 
-#include <cstdlib>
 
 namespace kmi {
 // y[r, n] = bf16(sum_s partial[s, r, n]), slices summed in order.  Rows of
@@ -175,17 +174,11 @@ static size_t valu_lds(int64_t K, int bits) {
     return (size_t)K * 2 + (size_t)(K / (128 / bits)) * 16;
 }
 
-static int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 // Launch shape of the VALU kernel.  S: 16-byte chunk slots per lane, all of
 // K up to 8 slots (one load batch).  RPW: weight rows per wave, as many as
 // keep S * RPW <= 8 loads in registers while the grid still has >= 4096
 // waves (4 per SIMD) to spread over the chip.  WV: waves per workgroup,
-// which amortizes the x staging over WV * RPW rows.  KMI_QMV_RPW and
-// KMI_QMV_WV override the choice (tuning).
+// which amortizes the x staging over WV * RPW rows.
 static ValuShape valu_shape(int64_t N, int64_t K, int bits, int64_t tiles) {
     const int64_t C = K / (128 / bits);
     const int64_t slots = ceil_div(C, 64);
@@ -195,14 +188,10 @@ static ValuShape valu_shape(int64_t N, int64_t K, int bits, int64_t tiles) {
     v.RPW = 1;
     if (v.S <= 4 && N * T / 2 >= 4096) v.RPW = 2;
     if (v.S <= 2 && N * T / 4 >= 4096) v.RPW = 4;
-    const int rpw = env_int("KMI_QMV_RPW", 0);
-    if (rpw == 1 || (rpw == 2 && v.S <= 4) || (rpw == 4 && v.S <= 2)) v.RPW = rpw;
     // 4 waves while each thread stages at most two x pieces (K <= 4096):
     // smaller workgroups start sooner; longer rows need 8 waves to keep the
     // staging ahead of the weight stream short
     v.WV = K <= 4096 ? 4 : 8;
-    const int wv = env_int("KMI_QMV_WV", 0);
-    if (wv == 4 || wv == 8) v.WV = wv;
     // no more waves per workgroup than the rows need
     while (v.WV > 4 && (int64_t)(v.WV / 2) * v.RPW >= N) v.WV /= 2;
     v.groups = ceil_div(N, (int64_t)v.WV * v.RPW);
@@ -275,11 +264,9 @@ static int run_skinny(QgArgs& a, const QgPlan& p, int bits, int gs, int64_t ntil
     return OK;
 }
 
-// Dense 2..16-row calls take the direct-to-LDS kernel where it has a
-// variant (KMI_QGEMV_DL=0 keeps them on qgemv, for comparisons)
+// Dense 2..16-row calls take the direct-to-LDS kernel where it has a variant
 static bool use_dl(int64_t M, int64_t K, int bits, int gs) {
-    static const int on = env_int("KMI_QGEMV_DL", 1);
-    return on != 0 && qgemv_dl_supported(M, K, bits, gs);
+    return qgemv_dl_supported(M, K, bits, gs);
 }
 
 static QgPlan dense_skinny_plan(int64_t M, int64_t K, int64_t N, int bits, int gs) {

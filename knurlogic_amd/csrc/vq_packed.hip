@@ -27,7 +27,6 @@
 #include "route.hpp"
 #include "../../include/knurlogic_amd.h"
 
-#include <cstdlib>
 
 namespace kmi {
 
@@ -725,10 +724,6 @@ static int vps_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, i
         // top-8, 2048 x 4: 8-row tiles 146 us, 4-row 117 us)
         int tile_rows = (int)(avg <= 2 ? 4 : avg <= 4 ? 8 : VPM_TILE);
         if (tile_rows > P) tile_rows = (int)P;
-        if (const char* ev = getenv("KMI_VPM_TR")) {          // tuning: 1..16
-            const int v = atoi(ev);
-            if (v >= 1 && v <= VPM_TILE) tile_rows = v;
-        }
         SortedRows sr;
         void* index_ws = (char*)workspace + vps_act_bytes(P, I) + vps_y_bytes(P, H);
         // the sort zeroes y's rows of out-of-range experts (no tile holds them)

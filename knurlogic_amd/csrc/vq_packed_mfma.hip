@@ -27,7 +27,6 @@
 #include "vq_packed_mfma.hpp"
 #include "../../include/knurlogic_amd.h"
 
-#include <cstdlib>
 
 namespace kmi {
 
@@ -308,15 +307,8 @@ int vpm_launch_pb(const VpmArgs& a, int dim, int group, dim3 grid, size_t lds, h
     return EINVAL_ARG;
 }
 
-// column blocks of 64 rows per workgroup (KMI_VPM_G overrides: tuning; read once)
-int vpm_cblk(int64_t nbt) {
-    static int ov = [] {
-        const char* e = getenv("KMI_VPM_G");
-        return e ? atoi(e) : 0;
-    }();
-    const int64_t g = ov > 0 ? ov : 1;
-    return (int)(g < nbt ? g : nbt);
-}
+// column blocks of 64 rows per workgroup: one
+int vpm_cblk(int64_t nbt) { return nbt < 1 ? (int)nbt : 1; }
 
 }  // namespace
 
