@@ -480,7 +480,8 @@ def ceilings(dev, headline_bytes):
     """Measured ceilings beside the published peaks: the HBM read rate of a
     plain read kernel (kmi_read_probe, 16-byte nontemporal loads, nothing
     computed) over the headline's per-call bytes with the buffers rotated
-    past the Infinity Cache as the headline's are, and over 1 GiB; and the
+    past the Infinity Cache as the headline's are, over the [4096, 4096]
+    M = 1 call's bytes, over 64 KB (one launch's floor) and over 1 GiB; and the
     bf16 GEMM rate of torch.matmul (hipBLASLt) on the prefill shapes with
     unquantized bf16 weights."""
     import ctypes
@@ -511,6 +512,14 @@ def ceilings(dev, headline_bytes):
     res["read_headline_bytes"] = {"bytes": headline_bytes // 16 * 16, "GBps": round(best[0], 1),
                                   "us": round(best[1], 3), "workgroups": best[2],
                                   "frac_of_published": round(best[0] / PEAK_HBM_GBS, 4)}
+    # the [4096, 4096] M = 1 call's bytes, and the floor of one launch in a
+    # graph (64 KB read by 256 workgroups)
+    c1 = dense_bytes(1, 4096, 4096, 4)
+    best1 = max((read_rate(c1, w) + (w,) for w in (256, 512, 1024, 2048)), key=lambda t: t[0])
+    res["read_4096x4096_m1_bytes"] = {"bytes": c1 // 16 * 16, "GBps": round(best1[0], 1),
+                                      "us": round(best1[1], 3), "workgroups": best1[2],
+                                      "frac_of_published": round(best1[0] / PEAK_HBM_GBS, 4)}
+    res["launch_floor_us"] = round(read_rate(1 << 16, 256)[1], 3)
     big = max((read_rate(1 << 30, w) + (w,) for w in (2048, 8192)), key=lambda t: t[0])
     res["read_1GiB"] = {"GBps": round(big[0], 1), "us": round(big[1], 3), "workgroups": big[2],
                         "frac_of_published": round(big[0] / PEAK_HBM_GBS, 4)}
@@ -637,7 +646,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no detail table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="detail sections, comma-separated "
-                                                "(dense, kv8, kvcache, qsdpa, moe, vq); default all")
+                                                "(c1, dense, kv8, kvcache, qsdpa, moe, vq; c1 = the "
+                                                "[4096, 4096] M = 1 rows alone); default all")
     ap.add_argument("--no-ceilings", action="store_true",
                     help="skip the measured read and bf16 GEMM ceilings")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -690,13 +700,14 @@ def main():
     gbs = nbytes / (us * 1e-6) / 1e9
 
     detail = []
-    only = set(args.only.split(",")) if args.only else {"dense", "kv8", "kvcache", "qsdpa", "moe", "vq"}
+    only = set(args.only.split(",")) if args.only else {"c1", "dense", "kv8", "kvcache", "qsdpa", "moe", "vq"}
     full = not args.quick
     # the dense configurations (1, 2) first; the MoE, VQ and KV8 rows
     # (configurations 3-5) last, so they end the line
-    if full and "dense" in only:
+    if full and ("c1" in only or "dense" in only):
         detail.append(bench_dense(4, 1, 4096, 4096, True, 200, dev))
         detail.append(bench_dense(4, 1, 4096, 4096, False, 200, dev))
+    if full and "dense" in only:
         for b_ in (4, 8):
             for shape in ((14336, 4096), (4096, 14336)):
                 for m in (1, 16, 512):

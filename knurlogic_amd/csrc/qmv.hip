@@ -177,8 +177,11 @@ static size_t valu_lds(int64_t K, int bits) {
 // Launch shape of the VALU kernel.  S: 16-byte chunk slots per lane, all of
 // K up to 8 slots (one load batch).  RPW: weight rows per wave, as many as
 // keep S * RPW <= 8 loads in registers while the grid still has >= 4096
-// waves (4 per SIMD) to spread over the chip.  WV: waves per workgroup,
-// which amortizes the x staging over WV * RPW rows.
+// waves (4 per SIMD) to spread over the chip; 2 rows from 2048 waves for a
+// dense call (one tile), whose every workgroup stages the same x (4-bit
+// [4096, 4096]: 4.55 us at 1 row per wave, 4.36 at 2; [14336, 4096] stays
+// at 2: 8.0 us, 8.6 at 4).  WV: waves per workgroup, which
+// amortizes the x staging over WV * RPW rows.
 static ValuShape valu_shape(int64_t N, int64_t K, int bits, int64_t tiles) {
     const int64_t C = K / (128 / bits);
     const int64_t slots = ceil_div(C, 64);
@@ -186,7 +189,7 @@ static ValuShape valu_shape(int64_t N, int64_t K, int bits, int64_t tiles) {
     v.S = slots <= 1 ? 1 : slots <= 2 ? 2 : slots <= 4 ? 4 : 8;
     const int64_t T = tiles > 0 ? tiles : 1;
     v.RPW = 1;
-    if (v.S <= 4 && N * T / 2 >= 4096) v.RPW = 2;
+    if (v.S <= 4 && N * T / 2 >= (tiles <= 1 ? 2048 : 4096)) v.RPW = 2;
     if (v.S <= 2 && N * T / 4 >= 4096) v.RPW = 4;
     // 4 waves while each thread stages at most two x pieces (K <= 4096):
     // smaller workgroups start sooner; longer rows need 8 waves to keep the
