@@ -316,12 +316,21 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
 
 namespace {
 
-// column blocks per workgroup: 4, fewer while the grid would have under
-// 1024 workgroups (measured at 128 experts, top-8, 2048 -> 768 -> 2048:
-// down takes 4 from 16 to 256 tokens, gate|up 2 at 16 tokens)
-int xs_blocks_per_wg(int64_t NB, int64_t tiles) {
+// column blocks per workgroup: 4, fewer while the grid (tile slots, empty
+// ones included) would have under `floor` workgroups: 1024 for down, 900
+// for gate|up.  Measured at 128 experts, top-8, 2048 -> 768 -> 2048, µs per
+// call: down flat within 2 µs over 1-8 blocks from 16 to 256 tokens;
+// gate|up (12 column blocks) by tokens and blocks --
+//   T =  9:  1 60.0   2 63.7   3 63.7   4 72.6
+//   T = 12:  1 67.0   2 66.0   3 77.5   4 72.5
+//   T = 16:  1 73.6   2 69.8   3 81.4   4 76.4
+//   T = 24:  1 84.8   2 90.7   3 88.5   4 100.6
+//   T = 32:  1 93.6   2 92.5   3 90.9   4 103.0
+// (the floor of 900 picks 1, 1, 2, 2, 2 there).
+int xs_blocks_per_wg(int64_t NB, int64_t tiles, bool glu) {
+    const int64_t floor = glu ? 900 : 1024;
     int64_t g = NB < 4 ? NB : 4;
-    while (g > 1 && ceil_div(NB, g) * tiles < 1024) g--;
+    while (g > 1 && ceil_div(NB, g) * tiles < floor) g--;
     return (int)g;
 }
 
@@ -334,7 +343,7 @@ int launch_xs_one(const QgArgs& a, int64_t ntiles, uint32_t xrow, uint32_t xbyte
     if (lds > XS_LDS_MAX) return 1;
     allow_dynamic_lds_once((const void*)qgemv_xs_kernel<BITS, GS, MX, XR, NSET, NS>);
     const int64_t NB = (a.N + 63) / 64;
-    const int G = xs_blocks_per_wg(NB, ntiles);
+    const int G = xs_blocks_per_wg(NB, ntiles, NSET == 2);
     const dim3 grid((unsigned)ceil_div(NB, G), 1, (unsigned)ntiles);
     qgemv_xs_kernel<BITS, GS, MX, XR, NSET, NS><<<grid, 256, lds, st>>>(a, G, xrow, xbytes);
     return 0;

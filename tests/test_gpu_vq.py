@@ -225,7 +225,8 @@ def test_vq_switch_glu_repeats_bit_for_bit(dev, T, kc):
         assert torch.equal(y, ys[0])
 
 
-@pytest.mark.parametrize("T,E,kc", [(1, 128, 256), (1, 128, 4096), (1, 300, 256), (3, 128, 4096), (16, 128, 256)])
+@pytest.mark.parametrize("T,E,kc", [(1, 128, 256), (1, 128, 4096), (1, 300, 256), (3, 128, 4096), (16, 128, 256),
+                                    (16, 256, 256), (16, 300, 256), (64, 128, 256)])
 def test_vq_experts_from_logits(dev, T, E, kc):
     """vq_experts (route, VQ SwitchGLU, combine in one call; at one token and
     E <= 256 the gate/up kernel routes the token itself) gives the routing of
