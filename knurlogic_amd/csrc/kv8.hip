@@ -78,6 +78,15 @@ __device__ __forceinline__ uint32_t load_scale_raw(__amdgpu_buffer_rsrc_t r, uin
         return __builtin_amdgcn_raw_buffer_load_b16(r, (int)(elem * 2u), 0, 0);
 }
 
+// the same at a byte offset
+template <class ST>
+__device__ __forceinline__ uint32_t load_scale_at(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    if constexpr (sizeof(typename ST::storage) == 4)
+        return __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0);
+    else
+        return __builtin_amdgcn_raw_buffer_load_b16(r, (int)byte_off, 0, 0);
+}
+
 template <class ST>
 __device__ __forceinline__ float scale_val(uint32_t raw) {
     if constexpr (sizeof(typename ST::storage) == 4) return __uint_as_float(raw);
@@ -199,6 +208,32 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
     u32x4 vr[VIT][4];
     uint32_t vsr[VIT][4], vbr[VIT][4];
 
+    // Per-lane parts of every load's byte offset, formed once: a step adds
+    // its first key times the row stride (a scalar), one v_add per stream.
+    const uint32_t kssb = kss * ES, kbsb = kbs * ES, vssb = vss * ES, vbsb = vbs * ES;
+    uint32_t kwo[2], kso[2], kbo[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        const uint32_t n = 16u * nt + l16;
+        kwo[nt] = n * kst + (uint32_t)(DL * jg);
+        kso[nt] = n * kssb + kgi * ES;
+        kbo[nt] = n * kbsb + kgi * ES;
+    }
+    uint32_t vwo[VIT][4], vso[VIT][4], vbo[VIT][4];
+#pragma unroll
+    for (int it = 0; it < VIT; it++) {
+        const int idx = lane + 64 * it;
+        const int quad = idx / VP, piece = idx % VP;
+        const uint32_t g = (uint32_t)((16 * piece) / a.group);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const uint32_t n = 4u * quad + kk;
+            vwo[it][kk] = n * vst + 16u * piece;
+            vso[it][kk] = n * vssb + g * ES;
+            vbo[it][kk] = n * vbsb + g * ES;
+        }
+    }
+
     // Loads of step j.  Issued unconditionally, so the loop carries no
     // "loaded or not" state: past the last step the views have extent 0 and
     // the loads return 0 without touching memory.
@@ -207,31 +242,26 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
         __amdgpu_buffer_rsrc_t rs[6];
 #pragma unroll
         for (int i = 0; i < 6; i++) rs[i] = make_rsrc(bp[i], live ? a.ext[i] : 0);
-        const uint32_t n0 = (uint32_t)(kbase + (live ? j : 0) * KV_WG_KEYS);
+        const uint32_t n0 = (uint32_t)(kbase + (live ? j : 0) * KV_WG_KEYS);   // wave-uniform
+        const uint32_t ukw = n0 * kst, uks = n0 * kssb, ukb = n0 * kbsb;
+        const uint32_t uvw = n0 * vst, uvs = n0 * vssb, uvb = n0 * vbsb;
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
-            const uint32_t n = n0 + 16u * nt + l16;
+            const uint32_t wo = kwo[nt] + ukw;
 #pragma unroll
             for (int c = 0; c < KC; c++)
-                kr[nt][c] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rs[0], (int)(n * kst + (uint32_t)(DL * jg + 16 * c)), 0, AUX_NT);
-            ksr[nt] = load_scale_raw<ST>(rs[1], n * kss + kgi);
-            kbr[nt] = load_scale_raw<ST>(rs[2], n * kbs + kgi);
+                kr[nt][c] = __builtin_amdgcn_raw_buffer_load_b128(rs[0], (int)(wo + 16u * c), 0, AUX_NT);
+            ksr[nt] = load_scale_at<ST>(rs[1], kso[nt] + uks);
+            kbr[nt] = load_scale_at<ST>(rs[2], kbo[nt] + ukb);
         }
 #pragma unroll
-        for (int it = 0; it < VIT; it++) {
-            const int idx = lane + 64 * it;
-            const int quad = idx / VP, piece = idx % VP;
-            const uint32_t g = (uint32_t)((16 * piece) / a.group);
+        for (int it = 0; it < VIT; it++)
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                const uint32_t n = n0 + 4u * quad + kk;
-                vr[it][kk] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rs[3], (int)(n * vst + 16u * piece), 0, AUX_NT);
-                vsr[it][kk] = load_scale_raw<ST>(rs[4], n * vss + g);
-                vbr[it][kk] = load_scale_raw<ST>(rs[5], n * vbs + g);
+                vr[it][kk] = __builtin_amdgcn_raw_buffer_load_b128(rs[3], (int)(vwo[it][kk] + uvw), 0, AUX_NT);
+                vsr[it][kk] = load_scale_at<ST>(rs[4], vso[it][kk] + uvs);
+                vbr[it][kk] = load_scale_at<ST>(rs[5], vbo[it][kk] + uvb);
             }
-        }
     };
     issue(0);
 
