@@ -179,6 +179,7 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
     constexpr int DL = S_::DL, KC = S_::KC, KSTEPS = S_::KSTEPS, DT = S_::DT;
     constexpr int VP = S_::VP, VIT = S_::VIT;
     constexpr int ES = (int)sizeof(typename ST::storage);
+    constexpr bool RESCALE_ALWAYS = D == 256 && RT == 2;
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -208,30 +209,21 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
     u32x4 vr[VIT][4];
     uint32_t vsr[VIT][4], vbr[VIT][4];
 
-    // Per-lane parts of every load's byte offset, formed once: a step adds
-    // its first key times the row stride (a scalar), one v_add per stream.
+    // Per-lane parts of every load's byte offset, formed once (the first key
+    // of the lane's group of rows); a load adds the wave-uniform rest -- its
+    // key's offset from there times the row stride, a scalar -- in one v_add.
     const uint32_t kssb = kss * ES, kbsb = kbs * ES, vssb = vss * ES, vbsb = vbs * ES;
-    uint32_t kwo[2], kso[2], kbo[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        const uint32_t n = 16u * nt + l16;
-        kwo[nt] = n * kst + (uint32_t)(DL * jg);
-        kso[nt] = n * kssb + kgi * ES;
-        kbo[nt] = n * kbsb + kgi * ES;
-    }
-    uint32_t vwo[VIT][4], vso[VIT][4], vbo[VIT][4];
+    const uint32_t kwo = (uint32_t)l16 * kst + (uint32_t)(DL * jg);
+    const uint32_t kso = (uint32_t)l16 * kssb + kgi * ES, kbo = (uint32_t)l16 * kbsb + kgi * ES;
+    uint32_t vwo[VIT], vso[VIT], vbo[VIT];
 #pragma unroll
     for (int it = 0; it < VIT; it++) {
         const int idx = lane + 64 * it;
         const int quad = idx / VP, piece = idx % VP;
         const uint32_t g = (uint32_t)((16 * piece) / a.group);
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const uint32_t n = 4u * quad + kk;
-            vwo[it][kk] = n * vst + 16u * piece;
-            vso[it][kk] = n * vssb + g * ES;
-            vbo[it][kk] = n * vbsb + g * ES;
-        }
+        vwo[it] = 4u * quad * vst + 16u * piece;
+        vso[it] = 4u * quad * vssb + g * ES;
+        vbo[it] = 4u * quad * vbsb + g * ES;
     }
 
     // Loads of step j.  Issued unconditionally, so the loop carries no
@@ -243,24 +235,24 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
 #pragma unroll
         for (int i = 0; i < 6; i++) rs[i] = make_rsrc(bp[i], live ? a.ext[i] : 0);
         const uint32_t n0 = (uint32_t)(kbase + (live ? j : 0) * KV_WG_KEYS);   // wave-uniform
-        const uint32_t ukw = n0 * kst, uks = n0 * kssb, ukb = n0 * kbsb;
-        const uint32_t uvw = n0 * vst, uvs = n0 * vssb, uvb = n0 * vbsb;
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
-            const uint32_t wo = kwo[nt] + ukw;
+            const uint32_t n = n0 + 16u * nt;
+            const uint32_t wo = kwo + n * kst;
 #pragma unroll
             for (int c = 0; c < KC; c++)
                 kr[nt][c] = __builtin_amdgcn_raw_buffer_load_b128(rs[0], (int)(wo + 16u * c), 0, AUX_NT);
-            ksr[nt] = load_scale_at<ST>(rs[1], kso[nt] + uks);
-            kbr[nt] = load_scale_at<ST>(rs[2], kbo[nt] + ukb);
+            ksr[nt] = load_scale_at<ST>(rs[1], kso + n * kssb);
+            kbr[nt] = load_scale_at<ST>(rs[2], kbo + n * kbsb);
         }
 #pragma unroll
         for (int it = 0; it < VIT; it++)
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                vr[it][kk] = __builtin_amdgcn_raw_buffer_load_b128(rs[3], (int)(vwo[it][kk] + uvw), 0, AUX_NT);
-                vsr[it][kk] = load_scale_at<ST>(rs[4], vso[it][kk] + uvs);
-                vbr[it][kk] = load_scale_at<ST>(rs[5], vbo[it][kk] + uvb);
+                const uint32_t n = n0 + kk;
+                vr[it][kk] = __builtin_amdgcn_raw_buffer_load_b128(rs[3], (int)(vwo[it] + n * vst), 0, AUX_NT);
+                vsr[it][kk] = load_scale_at<ST>(rs[4], vso[it] + n * vssb);
+                vbr[it][kk] = load_scale_at<ST>(rs[5], vbo[it] + n * vbsb);
             }
     };
     issue(0);
@@ -401,8 +393,12 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
             ps += __shfl_xor(ps, 32, 64);
             lsum[rt] = lsum[rt] * corr + ps;
             m[rt] = mn;
+            // wave-uniform skip while no row's max moved -- except with the
+            // 256-wide 2-tile state, whose registers the branch would spill
+            if (RESCALE_ALWAYS || __any(corr != 1.f)) {
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) O[dt][rt] *= corr;
+                for (int dt = 0; dt < DT; dt++) O[dt][rt] *= corr;
+            }
             P[rt] = u32x4{pack_f16(p[0], p[1]), pack_f16(p[2], p[3]), pack_f16(p[4], p[5]), pack_f16(p[6], p[7])};
         }
 
@@ -721,10 +717,12 @@ __global__ __launch_bounds__(256, 1) void kv8_wide(Kv8Args a, int nrt) {
             ps += __shfl_xor(ps, 32, 64);
             lsum = lsum * corr + ps;
             m = mn;
+            if (__any(corr != 1.f)) {   // wave-uniform: skipped while no row's max moved
 #pragma unroll
-            for (int c = 0; c < DC; c++)
+                for (int c = 0; c < DC; c++)
 #pragma unroll
-                for (int dt = 0; dt < 8; dt++) O[c][dt] *= corr;
+                    for (int dt = 0; dt < 8; dt++) O[c][dt] *= corr;
+            }
             P = u32x4{pack_f16(pv[0], pv[1]), pack_f16(pv[2], pv[3]), pack_f16(pv[4], pv[5]), pack_f16(pv[6], pv[7])};
         }
 
