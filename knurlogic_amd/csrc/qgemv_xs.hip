@@ -317,8 +317,10 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
 namespace {
 
 // column blocks per workgroup: 4, fewer while the grid (tile slots, empty
-// ones included) would have under `floor` workgroups: 1024 for down, 900
-// for gate|up.  Measured at 128 experts, top-8, 2048 -> 768 -> 2048, µs per
+// ones included) would have under `floor` workgroups: 1024 for down and
+// the microscaled gate|up (mxfp4 at 16 tokens: 84.3 us at 900, 76.7 at
+// 1024), 900 for the affine gate|up.  Measured at 128 experts, top-8,
+// 2048 -> 768 -> 2048, affine 4-bit, µs per
 // call: down flat within 2 µs over 1-8 blocks from 16 to 256 tokens;
 // gate|up (12 column blocks) by tokens and blocks --
 //   T =  9:  1 60.0   2 63.7   3 63.7   4 72.6
@@ -327,8 +329,8 @@ namespace {
 //   T = 24:  1 84.8   2 90.7   3 88.5   4 100.6
 //   T = 32:  1 93.6   2 92.5   3 90.9   4 103.0
 // (the floor of 900 picks 1, 1, 2, 2, 2 there).
-int xs_blocks_per_wg(int64_t NB, int64_t tiles, bool glu) {
-    const int64_t floor = glu ? 900 : 1024;
+int xs_blocks_per_wg(int64_t NB, int64_t tiles, bool affine_glu) {
+    const int64_t floor = affine_glu ? 900 : 1024;
     int64_t g = NB < 4 ? NB : 4;
     while (g > 1 && ceil_div(NB, g) * tiles < floor) g--;
     return (int)g;
@@ -343,7 +345,7 @@ int launch_xs_one(const QgArgs& a, int64_t ntiles, uint32_t xrow, uint32_t xbyte
     if (lds > XS_LDS_MAX) return 1;
     allow_dynamic_lds_once((const void*)qgemv_xs_kernel<BITS, GS, MX, XR, NSET, NS>);
     const int64_t NB = (a.N + 63) / 64;
-    const int G = xs_blocks_per_wg(NB, ntiles, NSET == 2);
+    const int G = xs_blocks_per_wg(NB, ntiles, NSET == 2 && !MX);
     const dim3 grid((unsigned)ceil_div(NB, G), 1, (unsigned)ntiles);
     qgemv_xs_kernel<BITS, GS, MX, XR, NSET, NS><<<grid, 256, lds, st>>>(a, G, xrow, xbytes);
     return 0;
