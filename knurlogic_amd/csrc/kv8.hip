@@ -19,6 +19,9 @@
 //   - dequantizes V into a wave-private V^T tile in LDS ([d][32 keys],
 //     keys stored in the order the P^T operand holds them, so each MFMA A
 //     operand is one 16-byte read) and accumulates O^T[d, r] += V^T P^T.
+//     A lane dequantizes (4-key quad, 16-d piece) items; lanes 8 i .. 8 i + 7
+//     take the 8 quads of one piece, so an 8-byte V^T write of 8 lanes fills
+//     one 64-byte row (consecutive pieces, rows 16 d apart, share banks).
 // The 4 waves' states merge in LDS (fixed order: deterministic) into one
 // partial per workgroup: o / l in fp16 (a convex combination of dequantized
 // V rows, so it is bounded like V) and (m, l) in fp32.  kv8_combine merges
@@ -26,8 +29,10 @@
 //
 // kv8_partial keeps every row's state of the KV head in a wave's registers,
 // which holds for D = 128 (up to 64 rows) and D = 256 (up to 32) with one
-// group per D/4-wide lane run; kv8_wide takes the other shapes (D up to
-// 512, 64 rows, groups of 16 and up) one 16-row tile per workgroup.
+// group per D/4-wide lane run; the other shapes (D up to 512, 64 rows,
+// groups of 16 and up) go to kv8_wide (up to 16 rows: one row tile per
+// workgroup, its waves splitting the keys) or kv8_rows (17-64 rows: a row
+// tile per wave over K/V steps the workgroup dequantizes once into LDS).
 #include "common.hpp"
 #include "../../include/knurlogic_amd.h"
 
@@ -219,7 +224,7 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
 #pragma unroll
     for (int it = 0; it < VIT; it++) {
         const int idx = lane + 64 * it;
-        const int quad = idx / VP, piece = idx % VP;
+        const int quad = idx % 8, piece = idx / 8;   // lanes 8 i .. 8 i + 7: the 8 quads of a piece
         const uint32_t g = (uint32_t)((16 * piece) / a.group);
         vwo[it] = 4u * quad * vst + 16u * piece;
         vso[it] = 4u * quad * vssb + g * ES;
@@ -322,7 +327,7 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
 #pragma unroll
         for (int it = 0; it < VIT; it++) {
             const int idx = lane + 64 * it;
-            const int quad = idx / VP, piece = idx % VP;
+            const int quad = idx % 8, piece = idx / 8;
             const int slot = 8 * (quad & 3) + 4 * (quad >> 2);
             float s[4], bi[4];
 #pragma unroll
@@ -584,7 +589,7 @@ __global__ __launch_bounds__(256, 1) void kv8_wide(Kv8Args a, int nrt) {
     uint32_t ksr[2][2], kbr[2][2];
     u32x4 vr[4];                    // V chunk: the lane's (key quad, 16-byte piece), 4 keys
     uint32_t vsr[4], vbr[4];
-    const int vquad = lane >> 3, vpiece = lane & 7;     // 8 quads x 8 pieces of a 128-d chunk
+    const int vquad = lane & 7, vpiece = lane >> 3;     // 8 quads x 8 pieces of a 128-d chunk
     auto views = [&](bool live, __amdgpu_buffer_rsrc_t (&rs)[6]) {
 #pragma unroll
         for (int i = 0; i < 6; i++) rs[i] = make_rsrc(bp[i], live ? a.ext[i] : 0);
@@ -833,6 +838,298 @@ constexpr size_t kv8_wide_lds() {
     return vt > merge ? vt : merge;
 }
 
+// =============================================================================
+// kv8_rows: kv8_wide's shapes with 17 to 64 query rows per KV head.  One
+// workgroup per (b, hk, key block) with all R rows: wave w owns row tile w
+// (rows 16 w ..) over every key of the block, so no wave state is merged,
+// and per 32-key step the whole workgroup dequantizes the step's K and V
+// once into LDS -- K^ [32 keys][D] row-major, V^T [D][32 keys] in P^T key
+// order -- which every row tile then reads as MFMA operands.  LDS holds two
+// such steps: the step after the current one is dequantized (its raw loads
+// issued a step earlier) while the row tiles compute on the current one.
+// Row stride paddings of 16 bytes keep 8 consecutive rows' 16-byte reads on
+// distinct banks.  Raw-load mapping: K as 16-byte pieces (key idx / (D/16),
+// piece idx % (D/16)), DC per thread; V as (key quad, 16-byte piece) items,
+// D / 2 of them, one per thread.
+// =============================================================================
+constexpr int KR_KP = 8;            // fp16 padding of a K^ row
+constexpr int KR_VS = KV_STEP + 8;  // fp16 per V^T row (32 keys + padding)
+
+template <int DC>
+constexpr size_t kv8_rows_buf() {
+    return (size_t)KV_STEP * (128 * DC + KR_KP) * 2 + (size_t)128 * DC * KR_VS * 2;
+}
+
+// Q^T operands for row r (0 past R) in natural d order: qop[ks] = the 8 q
+// values of d = 32 ks + 8 jg .. +8, times `scale`, in fp16.
+template <class QT, int DC>
+__device__ __forceinline__ void load_q_rows(u32x4 (&qop)[4 * DC], const Kv8Args& a, int b, int hk, int r,
+                                            int jg) {
+    constexpr int D = 128 * DC;
+    constexpr int QES = (int)sizeof(typename QT::storage);
+    constexpr int V16 = QES / 2;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q, (int64_t)a.B * a.H * a.L * D * QES);
+    const bool rok = r < a.R;
+    const int rr = rok ? r : 0;
+    const int h = hk * (a.H / a.Hk) + rr / a.L, lq = rr % a.L;
+    const uint32_t e0 = (uint32_t)((((b * a.H + h) * a.L + lq) * D) + 8 * jg);
+    u32x4 raw[4 * DC][V16];
+#pragma unroll
+    for (int ks = 0; ks < 4 * DC; ks++)
+#pragma unroll
+        for (int v = 0; v < V16; v++)
+            raw[ks][v] = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)((e0 + 32 * ks) * (uint32_t)QES + 16u * v),
+                                                               0, 0);
+#pragma unroll
+    for (int ks = 0; ks < 4 * DC; ks++) {
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            if constexpr (QES == 4) {
+                x[e] = __uint_as_float(raw[ks][e / 4][e % 4]);
+            } else {
+                const uint32_t w = raw[ks][0][e / 2];
+                x[e] = QT::load((uint16_t)(e % 2 ? w >> 16 : w & 0xffffu));
+            }
+        }
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[e] = rok ? pack_f16(x[2 * e] * a.scale, x[2 * e + 1] * a.scale) : 0u;
+        qop[ks] = o;
+    }
+}
+
+template <int DC, class ST>
+__global__ __launch_bounds__(256, 1) void kv8_rows(Kv8Args a) {
+    constexpr int D = 128 * DC;
+    constexpr int ES = (int)sizeof(typename ST::storage);
+    constexpr int KS = D + KR_KP;                   // fp16 per K^ row
+    constexpr int PPR = D / 16;                     // 16-byte pieces per key row
+    constexpr int KPT = DC;                         // K pieces per thread per step (2 D / 256)
+    constexpr int NV = D / 2;                       // V items per step
+    constexpr size_t BUF = kv8_rows_buf<DC>();
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, jg = lane >> 4;
+    const int bh = blockIdx.y, blk = blockIdx.x;
+    const int b = bh / a.Hk, hk = bh % a.Hk;
+    const int R = a.R, N = a.N, L = a.L;
+    const int r = 16 * wave + l16;                  // this lane's query row
+    const bool rok = r < R;
+    const bool active = 16 * wave < R;              // wave-uniform: the wave has rows
+
+    const char* bp[6];
+#pragma unroll
+    for (int i = 0; i < 6; i++) {
+        const int es = (i == 0 || i == 3) ? 4 : ES;
+        bp[i] = (const char*)a.base[i] + (b * a.st[i][0] + hk * a.st[i][1]) * es;
+    }
+    const uint32_t kst = (uint32_t)a.st[0][2] * 4u, vst = (uint32_t)a.st[3][2] * 4u;
+    const uint32_t kssb = (uint32_t)a.st[1][2] * ES, kbsb = (uint32_t)a.st[2][2] * ES;
+    const uint32_t vssb = (uint32_t)a.st[4][2] * ES, vbsb = (uint32_t)a.st[5][2] * ES;
+    const int steps = a.keys_per_wg / KV_STEP;
+    const int kbase = blk * a.keys_per_wg;
+
+    // ---- raw loads of a step: K pieces and the V item, lane bases formed once ----
+    int kkey[KPT], kpc[KPT];
+    uint32_t kwo[KPT], kgo[KPT];
+#pragma unroll
+    for (int i = 0; i < KPT; i++) {
+        const int idx = tid + 256 * i;
+        kkey[i] = idx / PPR;
+        kpc[i] = idx % PPR;
+        kwo[i] = (uint32_t)kkey[i] * kst + 16u * kpc[i];
+        kgo[i] = (uint32_t)((16 * kpc[i]) / a.group) * ES;
+    }
+    const bool vthr = tid < NV;
+    const int vquad = vthr ? tid % 8 : 0, vpiece = vthr ? tid / 8 : 0;
+    const uint32_t vwo = 4u * vquad * vst + 16u * vpiece;
+    const uint32_t vgo = (uint32_t)((16 * vpiece) / a.group) * ES;
+    const uint32_t vkey0 = 4u * vquad;
+
+    u32x4 kr[KPT];
+    uint32_t ksr[KPT], kbr[KPT];
+    u32x4 vr[4];
+    uint32_t vsr[4], vbr[4];
+    auto issue = [&](int j) {
+        const bool live = j < steps;
+        __amdgpu_buffer_rsrc_t rs[6];
+#pragma unroll
+        for (int i = 0; i < 6; i++) rs[i] = make_rsrc(bp[i], live ? a.ext[i] : 0);
+        const uint32_t n0 = (uint32_t)(kbase + (live ? j : 0) * KV_STEP);   // wave-uniform
+#pragma unroll
+        for (int i = 0; i < KPT; i++) {
+            kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rs[0], (int)(kwo[i] + n0 * kst), 0, AUX_NT);
+            const uint32_t n = n0 + (uint32_t)kkey[i];
+            ksr[i] = load_scale_at<ST>(rs[1], n * kssb + kgo[i]);
+            kbr[i] = load_scale_at<ST>(rs[2], n * kbsb + kgo[i]);
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const uint32_t n = n0 + vkey0 + kk;
+            vr[kk] = __builtin_amdgcn_raw_buffer_load_b128(rs[3], (int)(vwo + (n0 + kk) * vst), 0, AUX_NT);
+            vsr[kk] = load_scale_at<ST>(rs[4], n * vssb + vgo);
+            vbr[kk] = load_scale_at<ST>(rs[5], n * vbsb + vgo);
+        }
+    };
+    // the raw step -> K^ and V^T of LDS buffer `buf`
+    auto dequant = [&](int buf) {
+        _Float16* kd = (_Float16*)(smem + buf * BUF);
+        _Float16* vt = kd + KV_STEP * KS;
+#pragma unroll
+        for (int i = 0; i < KPT; i++) {
+            const float sc = scale_val<ST>(ksr[i]), bi = scale_val<ST>(kbr[i]);
+            u32x4 o[2];
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const uint32_t wd = kr[i][w];
+                o[w >> 1][2 * (w & 1)] = pack_f16(__builtin_fmaf(sc, byte_f(wd, 0), bi), __builtin_fmaf(sc, byte_f(wd, 1), bi));
+                o[w >> 1][2 * (w & 1) + 1] = pack_f16(__builtin_fmaf(sc, byte_f(wd, 2), bi), __builtin_fmaf(sc, byte_f(wd, 3), bi));
+            }
+            u32x4* dst = (u32x4*)(kd + kkey[i] * KS + 16 * kpc[i]);
+            dst[0] = o[0];
+            dst[1] = o[1];
+        }
+        if (vthr) {
+            const int slot = 8 * (vquad & 3) + 4 * (vquad >> 2);
+            float sc[4], bi[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                sc[kk] = scale_val<ST>(vsr[kk]);
+                bi[kk] = scale_val<ST>(vbr[kk]);
+            }
+#pragma unroll
+            for (int w = 0; w < 4; w++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float f[4];
+#pragma unroll
+                    for (int kk = 0; kk < 4; kk++) f[kk] = __builtin_fmaf(sc[kk], byte_f(vr[kk][w], e), bi[kk]);
+                    const int d = 16 * vpiece + 4 * w + e;
+                    *(u32x2*)(vt + d * KR_VS + slot) = u32x2{pack_f16(f[0], f[1]), pack_f16(f[2], f[3])};
+                }
+        }
+    };
+
+    issue(0);
+    u32x4 qop[4 * DC];
+    if (a.qdt == F32) load_q_rows<TF32, DC>(qop, a, b, hk, r, jg);
+    else if (a.qdt == F16) load_q_rows<TF16, DC>(qop, a, b, hk, r, jg);
+    else load_q_rows<TBF16, DC>(qop, a, b, hk, r, jg);
+    dequant(0);
+    issue(1);
+    __syncthreads();
+
+    float m = -INFINITY, lsum = 0.f;
+    f32x4 O[DC][8];
+#pragma unroll
+    for (int c = 0; c < DC; c++)
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) O[c][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const bool has_mask = a.mask != nullptr;
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.mask, (int64_t)a.B * L * N);
+    const int lq = (rok ? r : 0) % L;
+
+    for (int j = 0; j < steps; j++) {
+        const int n0 = kbase + j * KV_STEP;
+        const _Float16* kd = (const _Float16*)(smem + (j & 1) * BUF);
+        const _Float16* vt = kd + KV_STEP * KS;
+        if (active) {
+            uint32_t mraw[8];
+            if (has_mask) {
+                const uint32_t row = (uint32_t)((b * L + lq) * N);
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    mraw[e] = __builtin_amdgcn_raw_buffer_load_b8(
+                        rm, (int)(row + (uint32_t)(n0 + 16 * (e >> 2) + 4 * jg + (e & 3))), 0, 0);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) mraw[e] = 1u;
+            }
+            // S^T = K^ Q^T: A = K^ rows 16 nt + l16, d 32 ks + 8 jg
+            f32x4 S[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                for (int ks = 0; ks < 4 * DC; ks++) {
+                    const u32x4 A = *(const u32x4*)(kd + (16 * nt + l16) * KS + 32 * ks + 8 * jg);
+                    S[nt] = mfma_f16(A, qop[ks], S[nt]);
+                }
+            // online softmax over the step's keys, row r
+            u32x4 P;
+            {
+                float sv[8];
+                float bm = -INFINITY;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int n = n0 + 16 * (e >> 2) + 4 * jg + (e & 3);
+                    const bool ok = (n < N) & rok & (!a.causal | (n <= N - L + lq)) & (mraw[e] != 0);
+                    const float v = ok ? S[e >> 2][e & 3] : -INFINITY;
+                    sv[e] = v;
+                    bm = fmaxf(bm, v);
+                }
+                bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+                bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+                const float mn = fmaxf(m, bm);
+                float corr = 1.f, ps = 0.f;
+                float pv[8];
+                if (mn == -INFINITY) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) pv[e] = 0.f;
+                } else {
+                    corr = __expf(m - mn);   // m = -inf -> 0
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        pv[e] = __expf(sv[e] - mn);
+                        ps += pv[e];
+                    }
+                }
+                ps += __shfl_xor(ps, 16, 64);
+                ps += __shfl_xor(ps, 32, 64);
+                lsum = lsum * corr + ps;
+                m = mn;
+                if (__any(corr != 1.f)) {   // wave-uniform: skipped while no row's max moved
+#pragma unroll
+                    for (int c = 0; c < DC; c++)
+#pragma unroll
+                        for (int dt = 0; dt < 8; dt++) O[c][dt] *= corr;
+                }
+                P = u32x4{pack_f16(pv[0], pv[1]), pack_f16(pv[2], pv[3]), pack_f16(pv[4], pv[5]),
+                          pack_f16(pv[6], pv[7])};
+            }
+            // O^T += V^T P^T: A = V^T rows 128 c + 16 dt + l16, keys 8 jg ..
+#pragma unroll
+            for (int c = 0; c < DC; c++)
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) {
+                    const u32x4 A = *(const u32x4*)(vt + (128 * c + 16 * dt + l16) * KR_VS + 8 * jg);
+                    O[c][dt] = mfma_f16(A, P, O[c][dt]);
+                }
+        }
+        if (j + 1 < steps) {      // workgroup-uniform
+            dequant((j + 1) & 1);
+            issue(j + 2);
+        }
+        __syncthreads();
+    }
+
+    // ---- this wave's rows: o / l and (m, l) of the block --------------------------
+    if (rok) {
+        const int64_t pb = ((int64_t)bh * a.nblk + blk) * R;
+        const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+        _Float16* orow = a.po + (pb + r) * D;
+#pragma unroll
+        for (int c = 0; c < DC; c++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const f32x4 v = O[c][dt] * inv;
+                *(u32x2*)(orow + 128 * c + 16 * dt + 4 * jg) = u32x2{pack_f16(v[0], v[1]), pack_f16(v[2], v[3])};
+            }
+        if (jg == 0) a.pml[pb + r] = make_float2(m, lsum);
+    }
+}
+
 // out[b, h, l, :] = sum_blk w_blk o_blk / sum_blk w_blk, w_blk = l_blk exp(m_blk - max m),
 // with o_blk stored as o / l; 0 when no block saw a key (the reference kernel's rule).
 // One wave per (b, hk, row r); blocks merged 32 at a time with online rescaling,
@@ -927,21 +1224,21 @@ struct Kv8Plan {
 };
 
 // Workgroups per call the key blocks aim at: 512 for kv8_partial (256 / 512
-// / 1024 measured alike at 8k keys); for kv8_wide one round of the chip --
-// 256 CUs times the workgroups a CU holds (2 at D = 128, else 1) -- over the
-// key blocks times the row tiles (at D = 512: 166 us at 512, 155 at 256; at
-// 64 rows 160 -> 148).
+// / 1024 measured alike at 8k keys); for kv8_wide and kv8_rows one round of
+// the chip -- 256 CUs times the workgroups a CU holds (2 up to D = 128 for
+// kv8_wide, up to D = 256 for kv8_rows, else 1) -- kv8_wide's over the key
+// blocks times its row tiles (at D = 512: 166 us at 512, 155 at 256).
 constexpr int KV8_TARGET_WGS = 512;
 
-// The key blocks of a call.  kv8_wide's plan (wide_tiles = its row tiles)
-// has at most as many blocks as kv8_partial's, so the workspace
-// kmi_kv8_workspace_bytes sizes by the latter holds either.
-static Kv8Plan plan_kv8(int B, int Hk, int N, int D, int R, int wide_tiles = 0) {
+// The key blocks of a call, aiming at `target` workgroups of `tiles` row
+// tiles per key block.  Every plan has at most as many blocks as
+// kv8_partial's (target 512, one tile), so the workspace that
+// kmi_kv8_workspace_bytes sizes by the latter holds any of them.
+static Kv8Plan plan_kv8(int B, int Hk, int N, int D, int R, int target = KV8_TARGET_WGS, int tiles = 1) {
     Kv8Plan p;
     p.rt = (R + 15) / 16;
     const int64_t pairs = (int64_t)B * Hk;
-    const int64_t target = wide_tiles ? (D == 128 ? 512 : 256) / wide_tiles : KV8_TARGET_WGS;
-    const int64_t want_blk = ceil_div(target, pairs);
+    const int64_t want_blk = ceil_div(target / tiles > 0 ? target / tiles : 1, pairs);
     int64_t kpw = ceil_div(N > 0 ? N : 1, want_blk);
     kpw = ceil_div(kpw, KV_WG_KEYS) * KV_WG_KEYS;
     p.keys_per_wg = (int)kpw;
@@ -988,6 +1285,21 @@ static void launch_wide(const Kv8Args& a, int D, hipStream_t st) {
     else if (D == 256) launch_wide_dc<2, ST>(a, nrt, st);
     else if (D == 384) launch_wide_dc<3, ST>(a, nrt, st);
     else launch_wide_dc<4, ST>(a, nrt, st);
+}
+
+template <int DC, class ST>
+static void launch_rows_dc(const Kv8Args& a, hipStream_t st) {
+    constexpr size_t lds = 2 * kv8_rows_buf<DC>();
+    allow_dynamic_lds_once((const void*)kv8_rows<DC, ST>);
+    kv8_rows<DC, ST><<<dim3((unsigned)a.nblk, (unsigned)(a.B * a.Hk)), 256, lds, st>>>(a);
+}
+
+template <class ST>
+static void launch_rows(const Kv8Args& a, int D, hipStream_t st) {
+    if (D == 128) launch_rows_dc<1, ST>(a, st);
+    else if (D == 256) launch_rows_dc<2, ST>(a, st);
+    else if (D == 384) launch_rows_dc<3, ST>(a, st);
+    else launch_rows_dc<4, ST>(a, st);
 }
 
 // kv8_partial holds all R rows' state of a wave in registers: D = 128 up to
@@ -1042,8 +1354,13 @@ int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
         KMI_CHECK_LAUNCH("kv8_decode(empty)");
         return OK;
     }
+    // kv8_partial where its registers hold the rows; else one row tile:
+    // kv8_wide, more: kv8_rows
     const bool wide = !partial_covers(D, group, R);
-    Kv8Plan p = plan_kv8(B, Hk, N, D, R, wide ? (R + 15) / 16 : 0);
+    const bool rows = wide && R > 16;
+    Kv8Plan p = !wide ? plan_kv8(B, Hk, N, D, R)
+                : rows ? plan_kv8(B, Hk, N, D, R, D <= 256 ? 512 : 256)
+                       : plan_kv8(B, Hk, N, D, R, D == 128 ? 512 : 256, (R + 15) / 16);
     if (!workspace || workspace_bytes < p.total) {
         set_error("kv8_decode: workspace of %zu bytes needed, %zu given", p.total, workspace_bytes);
         return EWORKSPACE;
@@ -1082,6 +1399,11 @@ int kmi_kv8_decode(const void* q, int q_dtype, int B, int H, int L, int D,
         else if (scale_dtype == F16) launch_partial_st<TF16>(a, D, p.rt, grid, st);
         else launch_partial_st<TF32>(a, D, p.rt, grid, st);
         KMI_CHECK_LAUNCH("kv8_partial");
+    } else if (rows) {
+        if (scale_dtype == BF16) launch_rows<TBF16>(a, D, st);
+        else if (scale_dtype == F16) launch_rows<TF16>(a, D, st);
+        else launch_rows<TF32>(a, D, st);
+        KMI_CHECK_LAUNCH("kv8_rows");
     } else {
         if (scale_dtype == BF16) launch_wide<TBF16>(a, D, st);
         else if (scale_dtype == F16) launch_wide<TF16>(a, D, st);

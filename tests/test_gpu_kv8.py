@@ -77,11 +77,14 @@ def test_groups_narrower_than_a_lane_run_and_other_head_dims(dev, D, g):
 
 
 @pytest.mark.parametrize("D,L,H,Hk", [(256, 1, 48, 1), (256, 4, 16, 1), (512, 2, 32, 1), (384, 4, 8, 2),
-                                      (128, 1, 64, 2), (256, 2, 16, 1), (256, 3, 8, 1), (512, 8, 16, 2)])
+                                      (128, 1, 64, 2), (256, 2, 16, 1), (256, 3, 8, 1), (512, 8, 16, 2),
+                                      (384, 2, 24, 1), (512, 1, 20, 1)])
 def test_many_rows_per_kv_head_at_wide_head_dims(dev, D, L, H, Hk):
     """17 to 64 query rows per KV head at head dims 256-512 (and 32 rows
-    at 128), causal where L > 1: the 16-row-tile kernel, and at D = 256 with
-    17-32 rows the all-rows-per-wave one."""
+    at 128), causal where L > 1: a row tile per wave over shared K/V steps
+    (33-64 rows at D = 256, 17-64 at 384 / 512; 20 rows: a partial second
+    tile), the 16-row-tile kernel at 16, and at D = 256 with 17-32 rows the
+    all-rows-per-wave one."""
     _check(*_case(dev, 1, H, Hk, L, 900, D, seed=L * H), "causal" if L > 1 else None)
 
 
@@ -91,12 +94,13 @@ def test_many_blocks_per_head(dev):
     _check(*_case(dev, 1, 16, 1, 1, 20000, 128, seed=9), None)
 
 
-@pytest.mark.parametrize("L", [1, 2])
-def test_a_ragged_left_padded_batch(dev, L):
+@pytest.mark.parametrize("L,H,Hk,D", [(1, 16, 2, 256), (2, 16, 2, 256), (2, 16, 1, 512), (3, 16, 1, 384)])
+def test_a_ragged_left_padded_batch(dev, L, H, Hk, D):
     """Rows of different lengths, the left padding masked out; one row fully
-    padded but the last keys (tests/engine/test_kvattn.py:103-113)."""
+    padded but the last keys (tests/engine/test_kvattn.py:103-113); also
+    with 32 and 48 rows per KV head at D = 512 / 384 (the row-tile kernel)."""
     B, N = 3, 1200
-    host, gpu = _case(dev, B, 16, 2, L, N, 256, seed=3)
+    host, gpu = _case(dev, B, H, Hk, L, N, D, seed=3)
     pad = np.array([0, 513, N - L - 1])
     m = np.zeros((B, 1, L, N), bool)
     for b in range(B):
@@ -105,9 +109,10 @@ def test_a_ragged_left_padded_batch(dev, L):
     _check(host, gpu, m, torch.from_numpy(m).to(dev))
 
 
-def test_sparse_holes_and_a_row_that_sees_nothing(dev):
+@pytest.mark.parametrize("H,Hk,D,g", [(8, 2, 128, 64), (32, 1, 128, 16), (24, 1, 256, 32)])
+def test_sparse_holes_and_a_row_that_sees_nothing(dev, H, Hk, D, g):
     B, N = 3, 65
-    host, gpu = _case(dev, B, 8, 2, 1, N, 128, seed=4)
+    host, gpu = _case(dev, B, H, Hk, 1, N, D, g=g, seed=4)
     m = np.ones((B, 1, 1, N), bool)
     m[..., np.arange(N) % 5 == 2] = False
     m[2] = False
