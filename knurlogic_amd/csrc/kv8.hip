@@ -853,6 +853,7 @@ constexpr size_t kv8_wide_lds() {
 // D / 2 of them, one per thread.
 // =============================================================================
 constexpr int KR_KP = 8;            // fp16 padding of a K^ row
+constexpr float KV_LAZY = 8.f;      // kv8_rows: how far a step's max may pass the reference max
 constexpr int KR_VS = KV_STEP + 8;  // fp16 per V^T row (32 keys + padding)
 
 template <int DC>
@@ -1049,13 +1050,20 @@ __global__ __launch_bounds__(256, 1) void kv8_rows(Kv8Args a) {
             }
             // S^T = K^ Q^T: A = K^ rows 16 nt + l16, d 32 ks + 8 jg
             f32x4 S[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+            // 4 k-steps of both key tiles read ahead of their 8 MFMAs
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++)
+            for (int kb = 0; kb < 4 * DC; kb += 4) {
+                u32x4 A[2][4];
 #pragma unroll
-                for (int ks = 0; ks < 4 * DC; ks++) {
-                    const u32x4 A = *(const u32x4*)(kd + (16 * nt + l16) * KS + 32 * ks + 8 * jg);
-                    S[nt] = mfma_f16(A, qop[ks], S[nt]);
-                }
+                for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                    for (int k4 = 0; k4 < 4; k4++)
+                        A[nt][k4] = *(const u32x4*)(kd + (16 * nt + l16) * KS + 32 * (kb + k4) + 8 * jg);
+#pragma unroll
+                for (int k4 = 0; k4 < 4; k4++)
+#pragma unroll
+                    for (int nt = 0; nt < 2; nt++) S[nt] = mfma_f16(A[nt][k4], qop[kb + k4], S[nt]);
+            }
             // online softmax over the step's keys, row r
             u32x4 P;
             {
@@ -1071,14 +1079,19 @@ __global__ __launch_bounds__(256, 1) void kv8_rows(Kv8Args a) {
                 }
                 bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
                 bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-                const float mn = fmaxf(m, bm);
+                // the reference max m moves only when a step's max passes it
+                // by more than KV_LAZY (p = exp(s - m) then stays <= e^8 in
+                // fp16), so O -- in AGPRs here, three instructions per value
+                // to scale -- is rescaled rarely; o / l is unchanged by m
+                const bool grow = bm > m + KV_LAZY;   // m = -inf: any key seen
+                const float mn = grow ? bm : m;
                 float corr = 1.f, ps = 0.f;
                 float pv[8];
                 if (mn == -INFINITY) {
 #pragma unroll
                     for (int e = 0; e < 8; e++) pv[e] = 0.f;
                 } else {
-                    corr = __expf(m - mn);   // m = -inf -> 0
+                    corr = grow ? __expf(m - mn) : 1.f;   // m = -inf -> 0
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
                         pv[e] = __expf(sv[e] - mn);
@@ -1089,7 +1102,7 @@ __global__ __launch_bounds__(256, 1) void kv8_rows(Kv8Args a) {
                 ps += __shfl_xor(ps, 32, 64);
                 lsum = lsum * corr + ps;
                 m = mn;
-                if (__any(corr != 1.f)) {   // wave-uniform: skipped while no row's max moved
+                if (__any(grow)) {   // wave-uniform
 #pragma unroll
                     for (int c = 0; c < DC; c++)
 #pragma unroll
@@ -1100,12 +1113,14 @@ __global__ __launch_bounds__(256, 1) void kv8_rows(Kv8Args a) {
             }
             // O^T += V^T P^T: A = V^T rows 128 c + 16 dt + l16, keys 8 jg ..
 #pragma unroll
-            for (int c = 0; c < DC; c++)
+            for (int c = 0; c < DC; c++) {
+                u32x4 A[8];   // the chunk's 8 d-tiles read ahead of their MFMAs
 #pragma unroll
-                for (int dt = 0; dt < 8; dt++) {
-                    const u32x4 A = *(const u32x4*)(vt + (128 * c + 16 * dt + l16) * KR_VS + 8 * jg);
-                    O[c][dt] = mfma_f16(A, P, O[c][dt]);
-                }
+                for (int dt = 0; dt < 8; dt++)
+                    A[dt] = *(const u32x4*)(vt + (128 * c + 16 * dt + l16) * KR_VS + 8 * jg);
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) O[c][dt] = mfma_f16(A[dt], P, O[c][dt]);
+            }
         }
         if (j + 1 < steps) {      // workgroup-uniform
             dequant((j + 1) & 1);
