@@ -58,6 +58,9 @@ struct Kv8Args {
 constexpr int KV_WAVES = 4;
 constexpr int KV_STEP = 32;            // keys per wave step
 constexpr int KV_WG_KEYS = KV_WAVES * KV_STEP;
+// kv8_rows: how far a step's max may pass a row's reference max before the
+// reference moves (p = exp(s - m) <= e^8 in fp16)
+constexpr float KV_LAZY = 8.f;
 
 __device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
     f16x2 v = {(_Float16)lo, (_Float16)hi};
@@ -853,7 +856,6 @@ constexpr size_t kv8_wide_lds() {
 // D / 2 of them, one per thread.
 // =============================================================================
 constexpr int KR_KP = 8;            // fp16 padding of a K^ row
-constexpr float KV_LAZY = 8.f;      // kv8_rows: how far a step's max may pass the reference max
 constexpr int KR_VS = KV_STEP + 8;  // fp16 per V^T row (32 keys + padding)
 
 template <int DC>
