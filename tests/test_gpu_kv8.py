@@ -60,8 +60,12 @@ def test_a_short_causal_query(dev, L, H, Hk):
 
 
 @pytest.mark.parametrize("dtype", ["float32", "float16"])
-def test_float32_and_float16_queries(dev, dtype):
-    _check(*_case(dev, 2, 8, 2, 1, 900, 128, dtype=dtype), None, dtype=dtype)
+@pytest.mark.parametrize("D,H,Hk,L", [(128, 8, 2, 1), (512, 8, 2, 1), (384, 32, 1, 1)])
+def test_float32_and_float16_queries(dev, dtype, D, H, Hk, L):
+    """q, scales and biases in float32 / float16, on each kernel: all rows
+    per wave (D = 128), one row tile per workgroup (D = 512, 4 rows), a row
+    tile per wave (D = 384, 32 rows)."""
+    _check(*_case(dev, 2, H, Hk, L, 900, D, dtype=dtype), None, dtype=dtype)
 
 
 @pytest.mark.parametrize("g", [32, 128])
