@@ -9,13 +9,13 @@ and ``config.us_per_layer`` is one call.  Timed with HIP events around a
 HIP-graph replay of exactly ``--steps`` steps, so CPU launch cost is
 excluded while every kernel of each call is included.
 
-``detail`` holds the BASELINE workloads: the dense [4096, 4096] GEMV and the
-4- and 8-bit [14336, 4096] / [4096, 14336] matmuls at M = 1, 16, 512 (cold
-and warm), the mx modes, KV append and quantized SDPA, packed VQ, then the
-MoE experts (T = 1, 16, 256), the VQ experts (both codebooks, T = 1, 16) and
-the KV8 decode (8k / 32k keys, L = 1 / 4).  ``summary``, the line's last
-key, gives each configuration's µs and % of its bounding peak in one short
-string.
+``detail`` holds the benchmark workloads: the dense [4096, 4096] GEMV and
+the 4- and 8-bit [14336, 4096] / [4096, 14336] matmuls at M = 1, 16, 512
+(cold and warm), the mx modes, KV append and quantized SDPA, packed VQ, then
+the MoE experts (T = 1, 16, 256), the VQ experts (both codebooks, T = 1, 16)
+and the KV8 decode (8k / 32k keys, L = 1 / 4; head dims 256 / 512).
+``summary``, the line's last key, gives each workload's µs and % of its
+bounding peak in one short string.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick]
 """
@@ -514,9 +514,9 @@ def ceilings(dev, headline_bytes):
                                   "frac_of_published": round(best[0] / PEAK_HBM_GBS, 4)}
     # the [4096, 4096] M = 1 call's bytes, and the floor of one launch in a
     # graph (64 KB read by 256 workgroups)
-    c1 = dense_bytes(1, 4096, 4096, 4)
-    best1 = max((read_rate(c1, w) + (w,) for w in (256, 512, 1024, 2048)), key=lambda t: t[0])
-    res["read_4096x4096_m1_bytes"] = {"bytes": c1 // 16 * 16, "GBps": round(best1[0], 1),
+    b4k = dense_bytes(1, 4096, 4096, 4)
+    best1 = max((read_rate(b4k, w) + (w,) for w in (256, 512, 1024, 2048)), key=lambda t: t[0])
+    res["read_4096x4096_m1_bytes"] = {"bytes": b4k // 16 * 16, "GBps": round(best1[0], 1),
                                       "us": round(best1[1], 3), "workgroups": best1[2],
                                       "frac_of_published": round(best1[0] / PEAK_HBM_GBS, 4)}
     res["launch_floor_us"] = round(read_rate(1 << 16, 256)[1], 3)
@@ -608,9 +608,9 @@ def _pct(r):
 
 
 def summary(detail):
-    """One short string per BASELINE workload row (cold where both were
-    measured): config number, shape, µs per call and % of the bounding
-    peak.  Printed last in the JSON line."""
+    """One short string per workload row (cold where both were measured):
+    workload and shape, µs per call and % of the bounding peak.  Printed
+    last in the JSON line."""
     out = {}
     for r in detail:
         if r.get("cache") == "warm":
@@ -618,16 +618,16 @@ def summary(detail):
         op = r["op"]
         if op == "quantized_matmul":
             if (r["N"], r["K"]) == (4096, 4096):
-                key = f"c1 {r['bits']}b 4096x4096 M{r['M']}"
+                key = f"gemv {r['bits']}b 4096x4096 M{r['M']}"
             else:
-                key = f"c2 {r['bits']}b {r['N']}x{r['K']} M{r['M']}"
+                key = f"qmm {r['bits']}b {r['N']}x{r['K']} M{r['M']}"
         elif op == "moe_experts":
-            key = f"c3 moe T{r['T']}" if r["T"] <= 256 else f"prefill moe T{r['T']}"
+            key = f"moe T{r['T']}" if r["T"] <= 256 else f"prefill moe T{r['T']}"
         elif op == "vq_moe_experts":
-            key = (f"c4 vq {r['codebook'].split()[0]} T{r['T']}" if r["T"] <= 16
+            key = (f"vq {r['codebook'].split()[0]} T{r['T']}" if r["T"] <= 16
                    else f"prefill vq {r['codebook'].split()[0]} T{r['T']}")
         elif op == "kv8_decode":
-            key = f"c5 kv8 {r['N'] // 1024}k L{r['L']}" + (f" D{r['D']} R{r['H'] // r['Hk'] * r['L']}"
+            key = f"kv8 {r['N'] // 1024}k L{r['L']}" + (f" D{r['D']} R{r['H'] // r['Hk'] * r['L']}"
                                                           if r["D"] != 128 else "")
         else:
             continue
@@ -646,7 +646,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only, no detail table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="detail sections, comma-separated "
-                                                "(c1, dense, kv8, kvcache, qsdpa, moe, vq; c1 = the "
+                                                "(gemv4k, dense, kv8, kvcache, qsdpa, moe, vq; gemv4k = the "
                                                 "[4096, 4096] M = 1 rows alone); default all")
     ap.add_argument("--no-ceilings", action="store_true",
                     help="skip the measured read and bf16 GEMM ceilings")
@@ -700,11 +700,11 @@ def main():
     gbs = nbytes / (us * 1e-6) / 1e9
 
     detail = []
-    only = set(args.only.split(",")) if args.only else {"c1", "dense", "kv8", "kvcache", "qsdpa", "moe", "vq"}
+    only = set(args.only.split(",")) if args.only else {"gemv4k", "dense", "kv8", "kvcache", "qsdpa", "moe", "vq"}
     full = not args.quick
     # the dense configurations (1, 2) first; the MoE, VQ and KV8 rows
     # (configurations 3-5) last, so they end the line
-    if full and ("c1" in only or "dense" in only):
+    if full and ("gemv4k" in only or "dense" in only):
         detail.append(bench_dense(4, 1, 4096, 4096, True, 200, dev))
         detail.append(bench_dense(4, 1, 4096, 4096, False, 200, dev))
     if full and "dense" in only:
@@ -732,11 +732,11 @@ def main():
     if full and "moe" in only:
         for t_ in (1, 16):
             detail.append(bench_mx_moe(t_, 30, dev))
-        for t_ in (512, 2048):             # prefill chunks (not a BASELINE row)
+        for t_ in (512, 2048):             # prefill chunks (not a decode-step row)
             detail.append(bench_moe(t_, True, 5, dev))
     if full and "vq" in only:
         for kc_ in (256, 4096):
-            for t_ in (512, 2048):         # prefill chunks (not a BASELINE row)
+            for t_ in (512, 2048):         # prefill chunks (not a decode-step row)
                 detail.append(bench_vq(t_, kc_, True, 5, dev))
     if full and "moe" in only:
         for t_ in (1, 16, 256):
