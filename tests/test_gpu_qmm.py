@@ -45,7 +45,7 @@ def _big_weights(bits, shape):
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("M", [1, 16, 512])
 @pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336)])
-def test_qmm_baseline_shapes(dev, bits, M, shape):
+def test_qmm_decode_and_prefill_shapes(dev, bits, M, shape):
     """The dense workload: W [14336, 4096] and its reverse, M = 1, 16, 512,
     every output element against the oracle (the GEMV, the skinny kernel's
     K split and the GEMM's 128-column blocks and 4-way K split alike)."""
