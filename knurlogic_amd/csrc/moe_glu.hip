@@ -11,6 +11,7 @@
 // epilogue, then down, then the weighted combine.
 
 #include "moe_tok.hpp"
+#include "pair_tiles.hpp"
 #include "qgemv.hpp"
 #include "route.hpp"
 #include "../../include/knurlogic_amd.h"
@@ -78,13 +79,15 @@ size_t kmi_switch_glu_workspace_bytes(int64_t T, int64_t H, int64_t I, int k, in
 
 // SwitchGLU + combine; with route_logits (token-major only) the gate/up
 // kernel routes each token itself and writes route_inds / route_scores,
-// which the down kernel then reads as inds / scores.
+// which the down kernel then reads as inds / scores.  routed: inds come
+// from the router (every expert in range), so at a few pairs the expert
+// kernels form their tiles themselves and no sort runs.
 static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
                            const void* scores, const uint32_t* w_gu, const void* s_gu, const void* b_gu,
                            const uint32_t* w_down, const void* s_down, const void* b_down,
                            int64_t E, int dtype, int group_size, int bits, void* out, void* workspace,
                            size_t workspace_bytes, void* stream, const void* route_logits,
-                           int32_t* route_inds, void* route_scores, int mx = 0) {
+                           int32_t* route_inds, void* route_scores, int mx = 0, bool routed = false) {
     KMI_CHECK_ARG(dtype == BF16, "switch_glu: only bfloat16 activations are implemented");
     KMI_CHECK_ARG(bits == 4 || bits == 8, "switch_glu: bits=%d (4 or 8)", bits);
     KMI_CHECK_ARG(group_size == 32 || group_size == 64 || group_size == 128,
@@ -140,24 +143,47 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
         KMI_CHECK_LAUNCH("moe_down_tok");
         return OK;
     }
-    // grouped by expert: one sort, gate|up + SwiGLU, down, combine
+    // grouped by expert: one sort (or, for a few routed pairs, tiles formed
+    // in the x-staged kernels), gate|up + SwiGLU, down, combine
     uint16_t* y = scores ? (uint16_t*)(ws + p.act) : (uint16_t*)out;    // [P, H]
-    SortedRows sr;
-    int rc = launch_sort_rows(inds, P, 1, (int)E, p.tm, ws + p.act + p.y, y, H, st, &sr);
+    SortedRows sr = {};
+    bool have_sort = false;
+    auto sort = [&]() -> int {       // once, where a kernel needs the sort's list
+        if (have_sort) return OK;
+        have_sort = true;
+        return launch_sort_rows(inds, P, 1, (int)E, p.tm, ws + p.act + p.y, y, H, st, &sr);
+    };
+    const bool formed = routed && !p.gemm && p.tm == 4 && pair_tiles_fit(P, E, p.tm);
+    int rc = formed ? OK : sort();
     if (rc) return rc;
+    const int64_t max_tiles = sort_max_tiles(P, E, p.tm);
+    auto take_sort = [&](QgArgs& a) -> int {
+        const int r = sort();
+        a.tiles = sr.tiles; a.sorted = sr.sorted; a.route = nullptr;
+        return r;
+    };
     QgArgs g = {};
     g.x = (const uint16_t*)x; g.xrows = T; g.w = w_gu; g.s = (const uint16_t*)s_gu;
     g.b = (const uint16_t*)b_gu; g.E = E; g.N = I; g.K = H; g.erows = 2 * I; g.up_off = I; g.mx = mx;
     g.y = act; g.rows = P; g.tm = p.tm; g.tiles = sr.tiles; g.sorted = sr.sorted; g.lhs = nullptr;
     g.lhs_div = k; g.Mper = 1;
+    // formed tiles: the gate|up kernel also writes the sort's list (in the
+    // sort's place in the workspace) for the down kernel
+    int32_t* const list = (int32_t*)(ws + p.act + p.y);
+    if (formed) {
+        g.route = inds;
+        g.sorted_out = list;
+        g.tiles_out = list + P;
+    }
     if (p.gemm) {
-        rc = launch_moe_gemm(g, bits, group_size, true, p.tm, sr.max_tiles, st);
+        rc = launch_moe_gemm(g, bits, group_size, true, p.tm, max_tiles, st);
         if (rc) return rc;
     } else {
-        const QgPlan pg = plan_qgemv_unsplit(I, H, sr.max_tiles, p.tm, group_size);
+        const QgPlan pg = plan_qgemv_unsplit(I, H, max_tiles, p.tm, group_size);
         g.S = 1; g.gps = pg.gps;
-        if (p.tm != 4 || launch_qgemv_xs(g, bits, group_size, true, p.tm, sr.max_tiles, st) != 0) {
-            rc = launch_qgemv(g, pg, bits, group_size, true, sr.max_tiles, st);
+        if (p.tm != 4 || launch_qgemv_xs(g, bits, group_size, true, p.tm, max_tiles, st) != 0) {
+            if ((rc = take_sort(g)) != OK) return rc;
+            rc = launch_qgemv(g, pg, bits, group_size, true, max_tiles, st);
             if (rc) return rc;
         }
     }
@@ -166,16 +192,21 @@ static int switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, int k
     d.x = act; d.xrows = P; d.w = w_down; d.s = (const uint16_t*)s_down; d.b = (const uint16_t*)b_down;
     d.E = E; d.N = H; d.K = I; d.erows = H; d.y = y; d.rows = P; d.tm = p.tm; d.tiles = sr.tiles; d.mx = mx;
     d.sorted = sr.sorted; d.lhs = nullptr; d.lhs_div = 1; d.Mper = 1;
+    if (formed && !have_sort) {     // the list the gate|up kernel wrote
+        d.sorted = list;
+        d.tiles = list + P;
+    }
     if (p.gemm) {
-        rc = launch_moe_gemm(d, bits, group_size, false, p.tm, sr.max_tiles, st);
+        rc = launch_moe_gemm(d, bits, group_size, false, p.tm, max_tiles, st);
         if (rc) return rc;
     } else {
-        const QgPlan pd = plan_qgemv_unsplit(H, I, sr.max_tiles, p.tm, group_size);
+        const QgPlan pd = plan_qgemv_unsplit(H, I, max_tiles, p.tm, group_size);
         d.S = 1; d.gps = pd.gps;
         // the down projection stages each tile's act rows once (qgemv_xs)
         // where they fit
-        if (launch_qgemv_xs(d, bits, group_size, false, p.tm, sr.max_tiles, st) != 0) {
-            rc = launch_qgemv(d, pd, bits, group_size, false, sr.max_tiles, st);
+        if (launch_qgemv_xs(d, bits, group_size, false, p.tm, max_tiles, st) != 0) {
+            if ((rc = take_sort(d)) != OK) return rc;
+            rc = launch_qgemv(d, pd, bits, group_size, false, max_tiles, st);
             if (rc) return rc;
         }
     }
@@ -224,7 +255,8 @@ int kmi_moe_experts(const void* x, const void* logits, int64_t T, int64_t H, int
     int rc = kmi_moe_route(logits, dtype, T, (int)E, k, inds, scores, stream);
     if (rc) return rc;
     return switch_glu_impl(x, T, H, I, k, inds, scores, w_gu, s_gu, b_gu, w_down, s_down, b_down, E, dtype,
-                           group_size, bits, out, workspace, workspace_bytes, stream, nullptr, nullptr, nullptr);
+                           group_size, bits, out, workspace, workspace_bytes, stream, nullptr, nullptr, nullptr, 0,
+                           true);
 }
 
 }  // extern "C"

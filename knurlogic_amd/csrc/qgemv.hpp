@@ -26,6 +26,13 @@ struct QgArgs {
     // row id r: p = r / Mper, (lhs ? lhs[p] : p / lhs_div) * Mper + r % Mper
     const int32_t* tiles;
     const int32_t* sorted;
+    // qgemv_xs with tiles == null: the expert of each of the `rows` routed
+    // pairs (row id = pair), tiles of tm rows formed in the kernel
+    // (pair_tiles.hpp); every expert in range.  With tiles_out, column
+    // block 0 writes the sort's list of those tiles (tiles_out, sorted_out)
+    const int32_t* route;
+    int32_t* tiles_out;
+    int32_t* sorted_out;
     const int32_t* lhs;
     int64_t lhs_div;
     int64_t Mper;

@@ -22,6 +22,7 @@
 // s * P + b * X; after a block's last chunk it writes the block's outputs
 // (SwiGLU of the gate and up sums for GLU) and starts the next block.
 #include "qgemv_dl.hpp"
+#include "pair_tiles.hpp"
 #include "../../include/knurlogic_amd.h"
 
 
@@ -64,9 +65,23 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
     __shared__ int32_t rid_s[MT];        // output row of tile row m (-1: none)
     __shared__ uint32_t xro_s[MT];       // byte offset of tile row m's x row (DL_NONE: none)
 
-    const int32_t* tp = a.tiles + 3 * (int64_t)blockIdx.z;
-    const int count = tp[2], expert = tp[0], start = tp[1];
-    if (count <= 0 || expert < 0 || expert >= a.E) return;
+    // the tile: from the sort's list, or formed here from the routed pairs
+    // (its working space over the x region, which is filled after the
+    // tile's rows are read)
+    int count, expert, start = 0;
+    if (a.tiles) {
+        const int32_t* tp = a.tiles + 3 * (int64_t)blockIdx.z;
+        count = tp[2];
+        expert = tp[0];
+        start = tp[1];
+    } else {
+        const int pe = pair_tile_load(a.route, (int)a.rows);
+        count = pair_tile_from(pe, (int)a.rows, (int)a.E, a.tm, (int)blockIdx.z, *(PairTileLds*)smem, rid_s,
+                               expert, start);
+        if (a.tiles_out && blockIdx.x == 0)     // the sort's list, for the next launch
+            pair_tile_store(a.tiles_out, a.sorted_out, (int)blockIdx.z, expert, start, count, rid_s);
+    }
+    if (count <= 0 || count > MT || expert < 0 || expert >= a.E) return;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -151,7 +166,7 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
         int32_t rid = -1;
         uint32_t xo = DL_NONE;
         if (m < count) {
-            rid = a.sorted[start + m];
+            rid = a.tiles ? a.sorted[start + m] : rid_s[m];
             const uint32_t mper = (uint32_t)a.Mper, ldiv = (uint32_t)a.lhs_div, ur = (uint32_t)rid;
             const uint32_t pr = mper == 1 ? ur : ur / mper;
             const uint32_t xb = a.lhs ? (uint32_t)a.lhs[pr] : (ldiv == 1 ? pr : pr / ldiv);
@@ -378,12 +393,16 @@ int launch_xs_glu(const QgArgs& a, bool glu, int tr, int64_t ntiles, uint32_t xr
 
 // 0: launched; 1: this shape does not fit the kernel (the caller takes qgemv)
 int launch_qgemv_xs(const QgArgs& a, int bits, int gs, bool glu, int tile_rows, int64_t ntiles, hipStream_t st) {
-    if (!a.tiles || !a.sorted || a.S != 1 || a.K % DL_KC != 0) return 1;
+    const bool formed = !a.tiles && a.route;      // tiles formed in the kernel
+    if (!(a.tiles && a.sorted) && !formed) return 1;
+    if (a.S != 1 || a.K % DL_KC != 0) return 1;
     const int tr = tile_rows;
     if (!(tr == 4 || tr == 16 || tr == 32 || tr == 64) || !(bits == 4 || bits == 8)) return 1;
+    if (formed && (a.tm != tr || !pair_tiles_fit(a.rows, a.E, tr))) return 1;
     if (glu && a.up_off <= 0) return 1;
     const uint32_t xrow = (uint32_t)(a.K * 2 + 16);
-    const uint64_t xb = ((uint64_t)tr * xrow + 1023) / 1024 * 1024;
+    uint64_t xb = ((uint64_t)tr * xrow + 1023) / 1024 * 1024;
+    if (formed && xb < (sizeof(PairTileLds) + 1023) / 1024 * 1024) xb = (sizeof(PairTileLds) + 1023) / 1024 * 1024;
     if (xb > XS_LDS_MAX || a.xrows * a.K * 2 >= (1LL << 31)) return 1;
     const uint32_t xbytes = (uint32_t)xb;
     if (a.mx) {

@@ -22,6 +22,7 @@
 #include "common.hpp"
 #include "qgemv.hpp"
 #include "vq_mfma.hpp"
+#include "pair_tiles.hpp"
 #include "route.hpp"
 #include "../../include/knurlogic_amd.h"
 
@@ -451,7 +452,7 @@ static int vq_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, in
                               const void* codebook_up, const void* codes_down, const void* scales_down,
                               const void* codebook_down, int code_bytes, int kc, int dim, int scale_group,
                               int64_t E, int dtype, void* out, void* workspace, size_t workspace_bytes,
-                              void* stream, const void* logits) {
+                              void* stream, const void* logits, bool routed = false) {
     int rc = vq_check(dtype, code_bytes, kc, dim, scale_group, H, I, E);
     if (rc) return rc;
     rc = vq_check(dtype, code_bytes, kc, dim, scale_group, I, H, E);
@@ -491,9 +492,12 @@ static int vq_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, in
     int tile_rows = avg <= 2 ? 4 : avg <= 4 ? 8 : VQM_TILE_ROWS;
     if (tile_rows > P) tile_rows = (int)P;
     if (pair_mode) tile_rows = 1;
+    // inds from the router (every expert in range) and few pairs: the MFMA
+    // kernels form their tiles themselves, no sort
+    const bool formed = routed && !pair_mode && pair_tiles_fit(P, E, tile_rows);
     SortedRows sr = {};
-    if ((m_glu || m_down) && !pair_mode) {
-        void* index_ws = (char*)workspace + vq_act_bytes(T, I, k) + vq_y_bytes(T, H, k);
+    void* index_ws = (char*)workspace + vq_act_bytes(T, I, k) + vq_y_bytes(T, H, k);
+    if ((m_glu || m_down) && !pair_mode && !formed) {
         // the sort zeroes y's rows of out-of-range experts (no tile holds them)
         rc = launch_sort_rows(inds, P, 1, (int)E, tile_rows, index_ws, m_down ? y : nullptr, H, st, &sr);
         if (rc) return rc;
@@ -501,7 +505,12 @@ static int vq_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, in
     if (m_glu) {
         VqmArgs g = {};
         g.x = (const uint16_t*)x; g.X = T; g.lhs_magic = k > 1 ? (uint32_t)((0x100000000ULL + k - 1) / k) : 0u;
-        g.tiles = pair_mode ? nullptr : sr.tiles; g.sorted = sr.sorted; g.rhs = inds; g.E = E;
+        g.tiles = pair_mode || formed ? nullptr : sr.tiles; g.sorted = sr.sorted; g.rhs = inds; g.E = E;
+        g.pairs = formed ? (int)P : 0;
+        if (formed && m_down) {     // the gate/up kernel writes the sort's list for the down kernel
+            g.sorted_out = (int32_t*)index_ws;
+            g.tiles_out = (int32_t*)index_ws + P;
+        }
         g.codes0 = codes_gate; g.sc0 = (const uint16_t*)scales_gate; g.cb0 = (const uint16_t*)codebook_gate;
         g.codes1 = codes_up; g.sc1 = (const uint16_t*)scales_up; g.cb1 = (const uint16_t*)codebook_up;
         g.kc = kc; g.y = act; g.N = I; g.K = H; g.erows = I; g.tile_rows = tile_rows;
@@ -511,7 +520,7 @@ static int vq_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, in
             g.scores_out = (uint16_t*)scores;
             g.k = k;
         }
-        rc = launch_vq_mfma(g, code_bytes, 2, pair_mode ? P : sr.max_tiles, st);
+        rc = launch_vq_mfma(g, code_bytes, 2, pair_mode ? P : sort_max_tiles(P, E, tile_rows), st);
         if (rc) return rc;
         KMI_CHECK_LAUNCH("vq_mfma(glu)");
     } else {
@@ -543,10 +552,16 @@ static int vq_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, in
         VqmArgs d = {};
         d.x = act; d.X = P; d.lhs_magic = 0;
         d.tiles = pair_mode ? nullptr : sr.tiles; d.sorted = sr.sorted; d.rhs = inds; d.E = E;
+        if (formed && m_glu) {      // the list the gate/up kernel wrote
+            d.sorted = (const int32_t*)index_ws;
+            d.tiles = (const int32_t*)index_ws + P;
+        } else if (formed) {
+            d.pairs = (int)P;
+        }
         d.codes0 = codes_down; d.sc0 = (const uint16_t*)scales_down; d.cb0 = (const uint16_t*)codebook_down;
         d.codes1 = nullptr; d.sc1 = nullptr; d.cb1 = d.cb0;
         d.kc = kc; d.y = y; d.N = H; d.K = I; d.erows = H; d.tile_rows = tile_rows;
-        rc = launch_vq_mfma(d, code_bytes, 1, pair_mode ? P : sr.max_tiles, st);
+        rc = launch_vq_mfma(d, code_bytes, 1, pair_mode ? P : sort_max_tiles(P, E, tile_rows), st);
         if (rc) return rc;
         KMI_CHECK_LAUNCH("vq_mfma(down)");
     } else {
@@ -604,7 +619,7 @@ int kmi_vq_experts(const void* x, const void* logits, int64_t T, int64_t H, int6
     if (rc) return rc;
     return vq_switch_glu_impl(x, T, H, I, k, inds, scores, codes_gate, scales_gate, codebook_gate, codes_up,
                               scales_up, codebook_up, codes_down, scales_down, codebook_down, code_bytes, kc, dim,
-                              scale_group, E, dtype, out, workspace, workspace_bytes, stream, nullptr);
+                              scale_group, E, dtype, out, workspace, workspace_bytes, stream, nullptr, true);
 }
 
 }  // extern "C"

@@ -23,6 +23,7 @@
 // below 6e-5), as in vq.hip.
 #include "common.hpp"
 #include "vq_mfma.hpp"
+#include "pair_tiles.hpp"
 #include "route.hpp"
 
 
@@ -78,15 +79,27 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     constexpr int RW = 64 / KS;                      // weight rows per workgroup
     extern __shared__ __align__(16) unsigned char smem[];
 
-    // tile: (expert, first sorted row, rows) from the sort, or in pair mode
-    // (no tiles) pair blockIdx.y alone, its expert straight from rhs
+    // tile: (expert, first sorted row, rows) from the sort; formed in the
+    // workgroup from a.pairs routed pairs, before anything is staged (a slot
+    // past the last tile ends here; the working space lies over the x rows,
+    // staged later); or in pair mode (no tiles) pair blockIdx.y alone, its
+    // expert straight from rhs
     int e, start, count;
+    __shared__ int32_t prow_s[TM];                   // row ids of a tile formed here
     if (a.tiles) {
         const int32_t* tp = a.tiles + 3 * (int64_t)blockIdx.y;
         count = tp[2];
         if (count <= 0 || count > a.tile_rows) return;   // a tile never exceeds the staged rows
         e = tp[0];
         start = tp[1];
+    } else if (a.pairs) {
+        const int pe = pair_tile_load(a.rhs, a.pairs);
+        const size_t cbl = (size_t)((a.kc + 63) / 64) * 1024 * (NSET == 2 && a.cb1 != a.cb0 ? 2 : 1);
+        count = pair_tile_from(pe, a.pairs, (int)a.E, a.tile_rows, (int)blockIdx.y, *(PairTileLds*)(smem + cbl),
+                               prow_s, e, start);
+        if (a.tiles_out && blockIdx.x == 0)     // the sort's list, for the next launch
+            pair_tile_store(a.tiles_out, a.sorted_out, (int)blockIdx.y, e, start, count, prow_s);
+        if (count <= 0 || count > a.tile_rows) return;
     } else {
         start = (int)blockIdx.y;
         count = 1;
@@ -136,7 +149,9 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     // ids the host admits).
     typedef const __attribute__((address_space(4))) int32_t* cint_p;
     const cint_p srt = (cint_p)(a.tiles ? a.sorted + start : nullptr);
-    auto rowid = [&](int m) -> uint32_t { return a.tiles ? (uint32_t)srt[m] : (uint32_t)start; };
+    auto rowid = [&](int m) -> uint32_t {
+        return a.tiles ? (uint32_t)srt[m] : a.pairs ? (uint32_t)prow_s[m] : (uint32_t)start;
+    };
     auto xrow_of = [&](int m) -> int {
         const uint32_t r = rowid(m);
         return a.lhs_magic ? (int)__umulhi(r, a.lhs_magic) : (int)r;
@@ -341,7 +356,7 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
         for (int i = 0; i < 4; i++) {
             const int m = 4 * q + i;
             if (m >= count) continue;
-            const int64_t r = a.tiles ? a.sorted[start + m] : start;
+            const int64_t r = a.tiles ? a.sorted[start + m] : a.pairs ? prow_s[m] : start;
             a.y[r * a.N + row] = res[i];
         }
     };
@@ -419,8 +434,12 @@ static int vq_cblk(int64_t nbt) { return (int)(VQM_MAX_CBLK < nbt ? VQM_MAX_CBLK
 int launch_vq_mfma(const VqmArgs& a_in, int code_bytes, int nset, int64_t ntiles, hipStream_t st) {
     VqmArgs a = a_in;
     const bool two_cb = nset == 2 && a.cb1 != a.cb0;
-    if (a.tile_rows < 1 || a.tile_rows > TM || (!a.tiles && a.tile_rows != 1)) {
+    if (a.tile_rows < 1 || a.tile_rows > TM || (!a.tiles && !a.pairs && a.tile_rows != 1)) {
         set_error("vq_mfma: tile rows %d", a.tile_rows);
+        return EINVAL_ARG;
+    }
+    if (a.pairs && (a.tiles || a.logits || !pair_tiles_fit(a.pairs, a.E, a.tile_rows))) {
+        set_error("vq_mfma: %d pairs over %lld experts: no tiles formed in the kernel", a.pairs, (long long)a.E);
         return EINVAL_ARG;
     }
     // widest K split (up to 4) that the grid needs to reach ~512 workgroups
@@ -435,7 +454,9 @@ int launch_vq_mfma(const VqmArgs& a_in, int code_bytes, int nset, int64_t ntiles
         return EINVAL_ARG;
     }
     const int lw = vq_lw(a.K, code_bytes, ks);
-    const size_t lds = vq_mfma_lds(a.K, a.kc, two_cb, a.tile_rows, nset, ks);
+    size_t lds = vq_mfma_lds(a.K, a.kc, two_cb, a.tile_rows, nset, ks);
+    const size_t cbl = (size_t)((a.kc + 63) / 64) * 1024 * (two_cb ? 2 : 1);
+    if (a.pairs && lds < cbl + sizeof(PairTileLds)) lds = cbl + sizeof(PairTileLds);   // the tile's working space
     const int64_t nbt = ceil_div(a.N, 64 / ks);
     const bool rt = a.logits != nullptr;
     if (rt && (a.tiles || nset != 2 || a.E > ROUTE_THREADS || a.k < 1 || a.k > 8)) {

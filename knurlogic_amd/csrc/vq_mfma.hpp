@@ -16,6 +16,11 @@ struct VqmArgs {
                                 // pair mode, tile z = row id z alone with expert rhs[z]
     const int32_t* sorted;      // row ids grouped by expert
     const int32_t* rhs;         // pair mode: expert per row id
+    int pairs;                  // tiles == null and pairs > 0: the tiles (of tile_rows) formed in
+                                // each workgroup from rhs[0 .. pairs) (pair_tiles.hpp), every
+                                // expert in range; row id = pair
+    int32_t* tiles_out;         // with pairs: if set, column block 0 writes the sort's list of
+    int32_t* sorted_out;        // the formed tiles, for the next launch
     int64_t E;
     const void* codes0;         // [E, erows, K/8] (u8 or u16)
     const uint16_t* sc0;        // [E, erows] fp16, one scale per output row

@@ -24,6 +24,7 @@
 #include "common.hpp"
 #include "qgemv.hpp"
 #include "vq_packed_mfma.hpp"
+#include "pair_tiles.hpp"
 #include "route.hpp"
 #include "../../include/knurlogic_amd.h"
 
@@ -687,7 +688,7 @@ static int vps_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, i
                                const void* codebook_up, const uint32_t* codes_down, const void* scales_down,
                                const void* codebook_down, int pack_bits, int kc, int dim, int group, int64_t E,
                                int dtype, void* out, void* workspace, size_t workspace_bytes, void* stream,
-                               const void* logits) {
+                               const void* logits, bool routed = false) {
     int rc = vp_check(dtype, pack_bits, kc, dim, group, H, I, E);
     if (rc) return rc;
     rc = vp_check(dtype, pack_bits, kc, dim, group, I, H, E);
@@ -724,27 +725,43 @@ static int vps_switch_glu_impl(const void* x, int64_t T, int64_t H, int64_t I, i
         // top-8, 2048 x 4: 8-row tiles 146 us, 4-row 117 us)
         int tile_rows = (int)(avg <= 2 ? 4 : avg <= 4 ? 8 : VPM_TILE);
         if (tile_rows > P) tile_rows = (int)P;
-        SortedRows sr;
-        void* index_ws = (char*)workspace + vps_act_bytes(P, I) + vps_y_bytes(P, H);
-        // the sort zeroes y's rows of out-of-range experts (no tile holds them)
-        rc = launch_sort_rows(inds, P, 1, (int)E, tile_rows, index_ws, y, H, st, &sr);
-        if (rc) return rc;
+        // inds from the router (every expert in range) and few pairs: the
+        // kernels form their tiles themselves, no sort
+        const bool formed = routed && pair_tiles_fit(P, E, tile_rows);
+        SortedRows sr = {};
+        int32_t* const list = (int32_t*)((char*)workspace + vps_act_bytes(P, I) + vps_y_bytes(P, H));
+        if (!formed) {
+            void* index_ws = list;
+            // the sort zeroes y's rows of out-of-range experts (no tile holds them)
+            rc = launch_sort_rows(inds, P, 1, (int)E, tile_rows, index_ws, y, H, st, &sr);
+            if (rc) return rc;
+        }
+        const int64_t max_tiles = sort_max_tiles(P, E, tile_rows);
         VpmArgs g = {};
         g.x = (const uint16_t*)x; g.X = T; g.lhs_div = k; g.tiles = sr.tiles; g.sorted = sr.sorted; g.E = E;
+        g.rhs = inds; g.pairs = (int)P;
+        if (formed) {       // the gate/up kernel writes the sort's list for the down kernel
+            g.sorted_out = list;
+            g.tiles_out = list + P;
+        }
         g.codes[0] = codes_gate; g.codes[1] = codes_up;
         g.sc[0] = (const uint16_t*)scales_gate; g.sc[1] = (const uint16_t*)scales_up;
         g.cb[0] = (const uint16_t*)codebook_gate; g.cb[1] = (const uint16_t*)codebook_up;
         g.kc = kc; g.N = I; g.K = H; g.W = Wg; g.y = act; g.tile_rows = tile_rows;
-        rc = launch_vpm(g, pack_bits, dim, group, 2, sr.max_tiles, st);
+        rc = launch_vpm(g, pack_bits, dim, group, 2, max_tiles, st);
         if (rc) return rc;
         KMI_CHECK_LAUNCH("vq_packed_mfma(glu)");
         VpmArgs d = {};
         d.x = act; d.X = P; d.lhs_div = 1; d.tiles = sr.tiles; d.sorted = sr.sorted; d.E = E;
+        if (formed) {       // the list the gate/up kernel wrote
+            d.sorted = list;
+            d.tiles = list + P;
+        }
         d.codes[0] = d.codes[1] = codes_down;
         d.sc[0] = d.sc[1] = (const uint16_t*)scales_down;
         d.cb[0] = d.cb[1] = (const uint16_t*)codebook_down;
         d.kc = kc; d.N = H; d.K = I; d.W = Wd; d.y = y; d.tile_rows = tile_rows;
-        rc = launch_vpm(d, pack_bits, dim, group, 1, sr.max_tiles, st);
+        rc = launch_vpm(d, pack_bits, dim, group, 1, max_tiles, st);
         if (rc) return rc;
         KMI_CHECK_LAUNCH("vq_packed_mfma(down)");
     } else {
@@ -821,7 +838,7 @@ int kmi_vq_packed_experts(const void* x, const void* logits, int64_t T, int64_t 
     return vps_switch_glu_impl(x, T, H, I, k, inds, scores, codes_gate, scales_gate, codebook_gate, codes_up,
                                scales_up, codebook_up, codes_down, scales_down, codebook_down, pack_bits, kc, dim,
                                group, E, dtype, out, workspace, workspace_bytes, stream,
-                               in_kernel ? logits : nullptr);
+                               in_kernel ? logits : nullptr, true);
 }
 
 }  // extern "C"

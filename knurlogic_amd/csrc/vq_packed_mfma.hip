@@ -25,6 +25,7 @@
 // kernels).  The codebooks are staged through registers.
 #include "common.hpp"
 #include "vq_packed_mfma.hpp"
+#include "pair_tiles.hpp"
 #include "../../include/knurlogic_amd.h"
 
 
@@ -78,9 +79,27 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
     static_assert(RUN + 31 <= 128, "a lane's run of fields spans one 16-byte load");
     extern __shared__ __align__(16) unsigned char smem[];
 
-    const int32_t* tp = a.tiles + 3 * (int64_t)blockIdx.y;
-    const int count = tp[2], e = tp[0], start = tp[1];
-    if (count <= 0 || count > a.tile_rows || e < 0 || e >= a.E) return;
+    // the tile: from the sort's list, or formed in the workgroup from
+    // a.pairs routed pairs before anything is staged (a slot past the last
+    // tile ends here; the working space lies over the x rows, staged later)
+    int count = 0, e = 0, start = 0;
+    __shared__ int32_t prow_s[VPM_TILE];             // row ids of a tile formed here
+    if (a.tiles) {
+        const int32_t* tp = a.tiles + 3 * (int64_t)blockIdx.y;
+        count = tp[2];
+        e = tp[0];
+        start = tp[1];
+        if (count <= 0 || count > a.tile_rows || e < 0 || e >= a.E) return;
+    } else {
+        const int pe = pair_tile_load(a.rhs, a.pairs);
+        const int cbs = (a.kc * DIM * 2 + 15) & ~15;
+        const int cbl = cbs * (NSET == 2 && a.cb[1] != a.cb[0] ? 2 : 1);
+        count = pair_tile_from(pe, a.pairs, (int)a.E, a.tile_rows, (int)blockIdx.y, *(PairTileLds*)(smem + cbl),
+                               prow_s, e, start);
+        if (a.tiles_out && blockIdx.x == 0)     // the sort's list, for the next launch
+            pair_tile_store(a.tiles_out, a.sorted_out, (int)blockIdx.y, e, start, count, prow_s);
+        if (count <= 0 || count > a.tile_rows) return;
+    }
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -123,7 +142,7 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
         const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.X * a.K * 2);
         const int P8 = K / 8;                          // 16-byte pieces per row
         for (int m = 0; m < count; m++) {
-            const uint32_t rid = (uint32_t)a.sorted[start + m];
+            const uint32_t rid = (uint32_t)(a.tiles ? a.sorted[start + m] : prow_s[m]);
             const uint32_t xr = a.lhs_div == 1 ? rid : rid / (uint32_t)a.lhs_div;
             const bool ok = xr < (uint64_t)a.X;
             for (int p0 = tid; p0 < P8; p0 += VPM_WG * 4) {
@@ -257,7 +276,7 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
                     const double gg = (double)out;
                     out = vpm_bf16r(vpm_f32_kept(gg / (1.0 + exp(-gg)))) * up;
                 }
-                const int64_t r = a.sorted[start + m];
+                const int64_t r = a.tiles ? a.sorted[start + m] : prow_s[m];
                 a.y[r * a.N + row] = f32_to_bf16(out);
             }
         }
@@ -315,7 +334,14 @@ int vpm_cblk(int64_t nbt) { return nbt < 1 ? (int)nbt : 1; }
 // ntiles: grid rows (tiles of the sort)
 int launch_vpm(const VpmArgs& a, int pack_bits, int dim, int group, int nset, int64_t ntiles, hipStream_t st) {
     const bool two_cb = nset == 2 && a.cb[1] != a.cb[0];
-    const size_t lds = vpm_lds_bytes(a.K, a.kc, dim, two_cb, a.tile_rows);
+    if (!a.tiles && !(a.rhs && pair_tiles_fit(a.pairs, a.E, a.tile_rows))) {
+        set_error("vq (packed, MFMA): no tiles, and %d pairs over %lld experts are not formed in the kernel",
+                  a.pairs, (long long)a.E);
+        return EINVAL_ARG;
+    }
+    size_t lds = vpm_lds_bytes(a.K, a.kc, dim, two_cb, a.tile_rows);
+    const size_t cbl = (((size_t)a.kc * dim * 2 + 15) & ~(size_t)15) * (two_cb ? 2 : 1);
+    if (!a.tiles && lds < cbl + sizeof(PairTileLds)) lds = cbl + sizeof(PairTileLds);   // the tile's working space
     const int64_t nbt = ceil_div(a.N, 64);
     VpmArgs b = a;
     b.cblk = vpm_cblk(nbt);

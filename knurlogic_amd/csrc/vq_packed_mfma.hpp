@@ -14,6 +14,11 @@ struct VpmArgs {
     int64_t lhs_div;            // x row = row id / lhs_div
     const int32_t* tiles;       // [ntiles][3] (expert, start, count <= tile_rows) over `sorted`
     const int32_t* sorted;      // row ids grouped by expert
+    const int32_t* rhs;         // tiles == null: the tiles (of tile_rows) formed in each
+    int pairs;                  // workgroup from rhs[0 .. pairs) (pair_tiles.hpp), every expert
+                                // in range; row id = pair
+    int32_t* tiles_out;         // if set, column block 0 writes the sort's list of the formed
+    int32_t* sorted_out;        // tiles, for the next launch
     int64_t E;
     const uint32_t* codes[2];   // [E, N, W] packed fields (set 1: the up rows)
     const uint16_t* sc[2];      // [E, N, K / group] fp16

@@ -227,3 +227,37 @@ def test_moe_experts_routes_in_the_kernel_like_the_router(dev, T):
     block = nn.SparseMoeBlock(None, glu, k)
     assert torch.equal(block.experts(tx, tl), out)
 
+
+
+@pytest.mark.parametrize("T,E,H,I,pattern", [(16, 128, 2048, 768, "same"), (16, 128, 2048, 768, "half"),
+                                              (32, 128, 2048, 768, "random"), (12, 256, 512, 256, "same")])
+def test_moe_experts_tiles_formed_in_the_kernel(dev, T, E, H, I, pattern):
+    """From the router logits, at up to 256 (token, slot) pairs over up to
+    256 experts, the expert kernels form their 4-row tiles themselves (no
+    sort launch).  With skewed routing -- every token, or half of them, on
+    the same 8 experts, so one expert spans several tiles -- the output
+    equals route + SwitchGLU (the sort's tiles) bit for bit and matches the
+    oracle."""
+    rng = np.random.default_rng(500 + T + E)
+    k = 8
+    glu, fns = _experts(rng, E, H, I, dev)
+    x = bf16_normal(rng, (T, H))
+    logits = bf16_normal(rng, (T, E))
+    if pattern == "same":
+        logits[:] = logits[0]
+    elif pattern == "half":
+        logits[: T // 2] = logits[0]
+    tx, tl = to_torch(x, dev, BF), to_torch(logits, dev, BF)
+    f, d = glu.fused, glu.down_proj
+    out, inds, scores = K.moe_experts(tx, tl, k, f.weight, f.scales, f.biases, d.weight, d.scales, d.biases)
+    ri, rs = K.moe_route(tl, k)
+    assert torch.equal(inds, ri) and torch.equal(scores, rs)
+    assert torch.equal(out, glu.combine(tx, ri, rs)), "formed tiles and the sort's tiles differ"
+    oi, os_ = O.route(logits, k)
+    np.testing.assert_array_equal(inds.cpu().numpy(), oi)
+    if pattern == "same":
+        assert len(set(oi.reshape(-1).tolist())) == k
+    ref = O.combine(O.switch_glu(x, oi, *fns), os_)
+    assert_close(to_numpy(out), ref, what=f"moe_experts T={T} {pattern}")
+    again, _, _ = K.moe_experts(tx, tl, k, f.weight, f.scales, f.biases, d.weight, d.scales, d.biases)
+    assert torch.equal(again, out)

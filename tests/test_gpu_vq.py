@@ -225,18 +225,29 @@ def test_vq_switch_glu_repeats_bit_for_bit(dev, T, kc):
         assert torch.equal(y, ys[0])
 
 
-@pytest.mark.parametrize("T,E,kc", [(1, 128, 256), (1, 128, 4096), (1, 300, 256), (3, 128, 4096), (16, 128, 256),
-                                    (16, 256, 256), (16, 300, 256), (64, 128, 256)])
-def test_vq_experts_from_logits(dev, T, E, kc):
+@pytest.mark.parametrize("T,E,kc,pattern", [(1, 128, 256, "random"), (1, 128, 4096, "random"),
+                                            (1, 300, 256, "random"), (3, 128, 4096, "random"),
+                                            (16, 128, 256, "random"), (16, 256, 256, "random"),
+                                            (16, 300, 256, "random"), (64, 128, 256, "random"),
+                                            (16, 128, 256, "same"), (16, 128, 4096, "half"),
+                                            (32, 128, 256, "random")])
+def test_vq_experts_from_logits(dev, T, E, kc, pattern):
     """vq_experts (route, VQ SwitchGLU, combine in one call; at one token and
-    E <= 256 the gate/up kernel routes the token itself) gives the routing of
-    moe_route and the output of the separate route and combine calls, bit
-    for bit, and that output matches the oracle's routed SwitchGLU."""
+    E <= 256 the gate/up kernel routes the token itself; at up to 256 pairs
+    over up to 256 experts the expert kernels form their tiles themselves,
+    without the sort) gives the routing of moe_route and the output of the
+    separate route and combine calls, bit for bit, and that output matches
+    the oracle's routed SwitchGLU.  Skewed routing (every token, or half of
+    them, on the same 8 experts) puts an expert's rows in several tiles."""
     rng = np.random.default_rng(11 * T + E + kc)
     H, I, k = 2048, 768, 8
     (hg, gg), (hu, gu), (hd, gd) = [_vq(rng, E, n, kd, kc, 0, dev) for n, kd in ((I, H), (I, H), (H, I))]
     glu = nn.VQSwitchGLU(*(nn.VQSwitchLinear(*g) for g in (gg, gu, gd)))
     x, lg = bf16_normal(rng, (T, H)), bf16_normal(rng, (T, E))
+    if pattern == "same":
+        lg[:] = lg[0]
+    elif pattern == "half":
+        lg[: T // 2] = lg[0]
     tx, tl = to_torch(x, dev, BF), to_torch(lg, dev, BF)
     out, inds, scores = glu.experts(tx, tl, k)
     ri, rs = K.moe_route(tl, k)

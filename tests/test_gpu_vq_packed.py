@@ -225,15 +225,20 @@ def test_a_written_artifact_loads_and_matches_the_oracle(dev, tmp_path):
     assert_close(to_numpy(gv), ref, what="loaded vq")
 
 
-@pytest.mark.parametrize("T,E,H,I,dim", [(1, 128, 2048, 768, 4), (1, 128, 2816, 704, 2), (2, 128, 2048, 768, 4),
-                                         (1, 300, 512, 256, 4), (3, 128, 2048, 768, 4)])
-def test_packed_experts_from_logits(dev, T, E, H, I, dim):
+@pytest.mark.parametrize("T,E,H,I,dim,pattern", [(1, 128, 2048, 768, 4, "random"), (1, 128, 2816, 704, 2, "random"),
+                                                 (2, 128, 2048, 768, 4, "random"), (1, 300, 512, 256, 4, "random"),
+                                                 (3, 128, 2048, 768, 4, "random"), (16, 128, 2048, 768, 4, "same"),
+                                                 (16, 128, 2048, 768, 4, "half")])
+def test_packed_experts_from_logits(dev, T, E, H, I, dim, pattern):
     """vq_packed_experts (route, packed SwitchGLU, combine in one call; up to
-    16 pairs with E <= 256 the gate/up kernel routes each pair's token) gives
-    moe_route's routing and the bits of the separate route, SwitchGLU and
-    moe_combine calls, and matches
-    the oracle's routed SwitchGLU and combine.  Random 11-bit words (every
-    field a codebook entry)."""
+    16 pairs with E <= 256 the gate/up kernel routes each pair's token;
+    beyond, at up to 256 pairs over up to 256 experts, the expert-tile
+    kernels form their tiles themselves, without the sort) gives moe_route's
+    routing and the bits of the separate route, SwitchGLU and moe_combine
+    calls, and matches the oracle's routed SwitchGLU and combine.  Random
+    11-bit words (every field a codebook entry); skewed routing (every
+    token, or half of them, on the same 8 experts) puts an expert's rows in
+    several tiles."""
     k, kc, bits, group = 8, 2048, 11, 64
     rng = np.random.default_rng(40 + 7 * T + E + dim)
     g = torch.Generator(device=dev).manual_seed(40 + T + E)
@@ -252,6 +257,10 @@ def test_packed_experts_from_logits(dev, T, E, H, I, dim):
             for (w, sc), IN in zip(mats, (H, H, I))]
     glu = nn.VQSwitchGLU(*mods)
     x, lg = bf16_normal(rng, (T, H)), bf16_normal(rng, (T, E))
+    if pattern == "same":
+        lg[:] = lg[0]
+    elif pattern == "half":
+        lg[: T // 2] = lg[0]
     tx, tl = to_torch(x, dev, BF), to_torch(lg, dev, BF)
     out, inds, scores = glu.experts(tx, tl, k)
     ri, rs = K.moe_route(tl, k)
