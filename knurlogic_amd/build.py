@@ -19,9 +19,13 @@ FLAGS = [
 ]
 
 
-# Per-source flags.  qgemv: MFMA results in VGPRs (the FMAs that consume them
-# each group would otherwise copy them out of AGPRs first).
-EXTRA = {"qgemv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source flags: MFMA results in VGPRs where VALU code consumes them --
+# the skinny kernels' per-group scale FMAs, and the KV8 kernels' softmax
+# rescale of O -- which would otherwise copy them out of AGPRs first
+# (MoE 16 tokens 67.5 -> 64.9 us, 256 tokens 153.6 -> 148.2; KV8 64 rows at
+# D = 512 97.4 -> 80.2; the GEMMs and the VQ kernels measured even or slower
+# with it, and keep their accumulators in AGPRs).
+EXTRA = {f: ["-mllvm", "-amdgpu-mfma-vgpr-form"] for f in ("qgemv.hip", "qgemv_xs.hip", "qgemv_dl.hip", "kv8.hip")}
 
 
 # The compiler's per-kernel resource remarks (registers, scratch, occupancy),

@@ -124,17 +124,19 @@ def test_sparse_holes_and_a_row_that_sees_nothing(dev, H, Hk, D, g):
     assert (got[2] == 0).all()
 
 
-def test_the_bias_is_read_with_its_own_strides(dev):
+@pytest.mark.parametrize("H,Hk,L,D", [(8, 2, 1, 128), (8, 2, 1, 512), (16, 1, 4, 256)])
+def test_the_bias_is_read_with_its_own_strides(dev, H, Hk, L, D):
     """A bias that is a strided view, not laid out like its scale
     (tests/engine/test_kvattn.py:201-211); and K/V that are views of a
-    larger slab, as the quantized cache hands them out."""
-    host, (tq, tK, tV) = _case(dev, 1, 8, 2, 1, 300, 128, seed=5)
+    larger slab, as the quantized cache hands them out -- on the all-rows,
+    one-tile and row-tile kernels."""
+    host, (tq, tK, tV) = _case(dev, 2, H, Hk, L, 300, D, seed=5)
     wide = torch.cat([tK[2], tK[2]], dim=-1)
     Kv = (tK[0], tK[1], wide[..., :tK[2].shape[-1]])
     assert torch.equal(Kv[2], tK[2]) and Kv[2].stride() != tK[2].stride()
     slab = tuple(torch.cat([t, t[:, :, :56]], dim=2) for t in tV)
     Vv = tuple(t[:, :, :300] for t in slab)
-    _check(host, (tq, Kv, Vv), None)
+    _check(host, (tq, Kv, Vv), "causal" if L > 1 else None)
 
 
 def test_unsupported_shapes_are_refused_and_fall_back(dev):
