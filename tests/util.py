@@ -49,7 +49,10 @@ def to_numpy(t):
 
 def u32_to_torch(a, dev):
     import torch
-    return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).to(dev).view(torch.uint32)
+    a = np.ascontiguousarray(a, np.uint32)
+    if not a.flags.writeable:
+        a = a.copy()
+    return torch.from_numpy(a.view(np.int32)).to(dev).view(torch.uint32)
 
 
 def u32_to_numpy(t):
