@@ -10,7 +10,8 @@
 //   - has the step's packed K/V, scales and biases already in registers (the
 //     raw buffer loads for step j+1 are issued before step j's math, and a
 //     key past N reads 0 instead of branching);
-//   - dequantizes K (fp32 scale*q + bias, one fp16 rounding) straight into
+//   - dequantizes K (scale*q + bias formed in fp32 by v_fma_mix from the
+//     code as fp16 1024 + q, one fp16 rounding) straight into
 //     v_mfma_f32_16x16x32_f16 A operands: lane (key l16, run jg) owns d in
 //     [jg*D/4, (jg+1)*D/4), so its bytes are contiguous and no LDS is used;
 //     the pre-scaled Q^T operands use the same d order, which leaves the dot
@@ -101,7 +102,60 @@ __device__ __forceinline__ float scale_val(uint32_t raw) {
     else return ST::load((uint16_t)raw);
 }
 
+// ---- byte codes -> fp16 -------------------------------------------------------
+// A code byte c becomes the fp16 1024 + c (a v_perm puts the byte 0x64
+// above it: exact), and a mixed-precision FMA (v_fma_mix) forms
+// s * (1024 + c) + (b - 1024 s) in float32 and rounds it to fp16: s * c + b
+// up to the float32 rounding of the offset b - 1024 s (at most 2^-14 |s|)
+// and one fp16 rounding -- three instructions per two codes where the
+// float32 form (convert, FMA, FMA, pack) takes five.
+__device__ __forceinline__ float deq_off(float s, float b) { return __builtin_fmaf(-1024.f, s, b); }
+
+// a code byte as float32 (the form kv8_rows keeps: its 256-register state
+// leaves no room for the fp16 pairs)
 __device__ __forceinline__ float byte_f(uint32_t w, int e) { return (float)((w >> (8 * e)) & 0xffu); }
+
+// bytes 2 hf and 2 hf + 1 of w as the fp16 pair (1024 + c0, 1024 + c1)
+template <int HF>
+__device__ __forceinline__ f16x2 magic2(uint32_t w) {
+    return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, HF ? 0x04030402u : 0x04010400u));
+}
+
+__device__ __forceinline__ _Float16 deq1(float s, _Float16 m, float off) {
+    return (_Float16)__builtin_fmaf(s, (float)m, off);
+}
+
+__device__ __forceinline__ uint32_t h2bits(_Float16 lo, _Float16 hi) {
+    const f16x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// the four codes of word w under one scale, as two fp16 pairs (codes 0, 1 and 2, 3)
+__device__ __forceinline__ void deq4(uint32_t w, float s, float off, uint32_t& lo, uint32_t& hi) {
+    const f16x2 a = magic2<0>(w), c = magic2<1>(w);
+    lo = h2bits(deq1(s, a.x, off), deq1(s, a.y, off));
+    hi = h2bits(deq1(s, c.x, off), deq1(s, c.y, off));
+}
+
+// V^T pieces of four keys: w[kk] is a word of key kk (d = 4i .. 4i + 3 for
+// some i); out[e] = the keys' values at d = 4i + e as fp16 pairs (k0, k1), (k2, k3)
+__device__ __forceinline__ void deq_vt4(const uint32_t (&w)[4], const float (&s)[4], const float (&off)[4],
+                                        u32x2 (&out)[4]) {
+    f16x2 m[4][2];
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+        m[kk][0] = magic2<0>(w[kk]);
+        m[kk][1] = magic2<1>(w[kk]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        _Float16 c[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) c[kk] = (e & 1) ? m[kk][e >> 1].y : m[kk][e >> 1].x;
+        out[e] = u32x2{h2bits(deq1(s[0], c[0], off[0]), deq1(s[1], c[1], off[1])),
+                       h2bits(deq1(s[2], c[2], off[2]), deq1(s[3], c[3], off[3]))};
+    }
+}
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
@@ -311,7 +365,7 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
         u32x4 kop[2][KSTEPS];
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
-            const float s = scale_val<ST>(ksr[nt]), bi = scale_val<ST>(kbr[nt]);
+            const float s = scale_val<ST>(ksr[nt]), off = deq_off(s, scale_val<ST>(kbr[nt]));
 #pragma unroll
             for (int c = 0; c < KC; c++)
 #pragma unroll
@@ -319,9 +373,10 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
                     u32x4 o;
 #pragma unroll
                     for (int w2 = 0; w2 < 2; w2++) {
-                        const uint32_t wd = kr[nt][c][2 * hh + w2];
-                        o[2 * w2] = pack_f16(__builtin_fmaf(s, byte_f(wd, 0), bi), __builtin_fmaf(s, byte_f(wd, 1), bi));
-                        o[2 * w2 + 1] = pack_f16(__builtin_fmaf(s, byte_f(wd, 2), bi), __builtin_fmaf(s, byte_f(wd, 3), bi));
+                        uint32_t lo, hi;
+                        deq4(kr[nt][c][2 * hh + w2], s, off, lo, hi);
+                        o[2 * w2] = lo;
+                        o[2 * w2 + 1] = hi;
                     }
                     kop[nt][2 * c + hh] = o;
                 }
@@ -332,22 +387,20 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
             const int idx = lane + 64 * it;
             const int quad = idx % 8, piece = idx / 8;
             const int slot = 8 * (quad & 3) + 4 * (quad >> 2);
-            float s[4], bi[4];
+            float s[4], off[4];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
                 s[kk] = scale_val<ST>(vsr[it][kk]);
-                bi[kk] = scale_val<ST>(vbr[it][kk]);
+                off[kk] = deq_off(s[kk], scale_val<ST>(vbr[it][kk]));
             }
 #pragma unroll
-            for (int w = 0; w < 4; w++)
+            for (int w = 0; w < 4; w++) {
+                const uint32_t wk[4] = {vr[it][0][w], vr[it][1][w], vr[it][2][w], vr[it][3][w]};
+                u32x2 pr[4];
+                deq_vt4(wk, s, off, pr);
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    float f[4];
-#pragma unroll
-                    for (int kk = 0; kk < 4; kk++) f[kk] = __builtin_fmaf(s[kk], byte_f(vr[it][kk][w], e), bi[kk]);
-                    const int d = 16 * piece + 4 * w + e;
-                    *(u32x2*)(vt + d * KV_STEP + slot) = u32x2{pack_f16(f[0], f[1]), pack_f16(f[2], f[3])};
-                }
+                for (int e = 0; e < 4; e++) *(u32x2*)(vt + (16 * piece + 4 * w + e) * KV_STEP + slot) = pr[e];
+            }
         }
 
         issue(j + 1);   // next step's bytes stream in during this step's math
@@ -366,6 +419,9 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
             }
 
         // ---- online softmax over this step's keys, per row --------------------------
+        // every key of the step visible to every row (no mask, inside N and,
+        // causal, below every row's diagonal): no per-key test
+        const bool plain = !has_mask && n0 + KV_STEP + (a.causal ? L - 1 : 0) <= N;
         u32x4 P[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
@@ -373,13 +429,22 @@ __global__ __launch_bounds__(256, (kv8_min_blocks<D, RT>())) void kv8_partial(Kv
             const int lq = (r < R ? r : 0) % L;
             float sv[8];
             float bm = -INFINITY;
+            if (plain) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int n = n0 + 16 * (e >> 2) + 4 * jg + (e & 3);
-                const bool ok = (n < N) & (r < R) & (!a.causal | (n <= N - L + lq)) & (mraw[rt][e] != 0);
-                const float v = ok ? S[e >> 2][rt][e & 3] : -INFINITY;
-                sv[e] = v;
-                bm = fmaxf(bm, v);
+                for (int e = 0; e < 8; e++) {
+                    const float v = r < R ? S[e >> 2][rt][e & 3] : -INFINITY;
+                    sv[e] = v;
+                    bm = fmaxf(bm, v);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int n = n0 + 16 * (e >> 2) + 4 * jg + (e & 3);
+                    const bool ok = (n < N) & (r < R) & (!a.causal | (n <= N - L + lq)) & (mraw[rt][e] != 0);
+                    const float v = ok ? S[e >> 2][rt][e & 3] : -INFINITY;
+                    sv[e] = v;
+                    bm = fmaxf(bm, v);
+                }
             }
             bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
             bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
@@ -673,13 +738,15 @@ __global__ __launch_bounds__(256, 1) void kv8_wide(Kv8Args a, int nrt) {
             for (int nt = 0; nt < 2; nt++) {
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++) {
-                    const float sc = scale_val<ST>(ksr[nt][kk >> 1]), bi = scale_val<ST>(kbr[nt][kk >> 1]);
+                    const float sc = scale_val<ST>(ksr[nt][kk >> 1]);
+                    const float off = deq_off(sc, scale_val<ST>(kbr[nt][kk >> 1]));
                     u32x4 o;
 #pragma unroll
                     for (int w2 = 0; w2 < 2; w2++) {
-                        const uint32_t wd = kr[nt][kk >> 1][2 * (kk & 1) + w2];
-                        o[2 * w2] = pack_f16(__builtin_fmaf(sc, byte_f(wd, 0), bi), __builtin_fmaf(sc, byte_f(wd, 1), bi));
-                        o[2 * w2 + 1] = pack_f16(__builtin_fmaf(sc, byte_f(wd, 2), bi), __builtin_fmaf(sc, byte_f(wd, 3), bi));
+                        uint32_t lo, hi;
+                        deq4(kr[nt][kk >> 1][2 * (kk & 1) + w2], sc, off, lo, hi);
+                        o[2 * w2] = lo;
+                        o[2 * w2 + 1] = hi;
                     }
                     kop[nt][kk] = o;
                 }
@@ -740,22 +807,20 @@ __global__ __launch_bounds__(256, 1) void kv8_wide(Kv8Args a, int nrt) {
         for (int c = 0; c < DC; c++) {
             {
                 const int slot = 8 * (vquad & 3) + 4 * (vquad >> 2);
-                float sc[4], bi[4];
+                float sc[4], off[4];
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++) {
                     sc[kk] = scale_val<ST>(vsr[kk]);
-                    bi[kk] = scale_val<ST>(vbr[kk]);
+                    off[kk] = deq_off(sc[kk], scale_val<ST>(vbr[kk]));
                 }
 #pragma unroll
-                for (int w = 0; w < 4; w++)
+                for (int w = 0; w < 4; w++) {
+                    const uint32_t wk[4] = {vr[0][w], vr[1][w], vr[2][w], vr[3][w]};
+                    u32x2 pr[4];
+                    deq_vt4(wk, sc, off, pr);
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        float f[4];
-#pragma unroll
-                        for (int kk = 0; kk < 4; kk++) f[kk] = __builtin_fmaf(sc[kk], byte_f(vr[kk][w], e), bi[kk]);
-                        const int d = 16 * vpiece + 4 * w + e;
-                        *(u32x2*)(vt + d * KV_STEP + slot) = u32x2{pack_f16(f[0], f[1]), pack_f16(f[2], f[3])};
-                    }
+                    for (int e = 0; e < 4; e++) *(u32x2*)(vt + (16 * vpiece + 4 * w + e) * KV_STEP + slot) = pr[e];
+                }
             }
             if (c + 1 < DC) issue_v(j, c + 1);
             else issue_k(j + 1, 0);

@@ -34,6 +34,26 @@ __device__ __forceinline__ u32x4 nib8_natural(uint32_t w) {
     return r;
 }
 
+// 8 codes (code i at bits 4i) -> 8 exact bf16 in the order [0,2,4,6,1,3,5,7]
+// (the low nibbles of the four bytes, then the high ones): no byte shuffle,
+// for x staged in the same order (x8_paired)
+__device__ __forceinline__ u32x4 nib8_paired(uint32_t w) {
+    const uint32_t lo = w & 0x0F0F0F0Fu;            // codes 0, 2, 4, 6
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;     // codes 1, 3, 5, 7
+    u32x4 r;
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.f, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.f, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.f, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.f, true));
+    return r;
+}
+
+// 8 bf16 in natural k order -> the order [0,2,4,6,1,3,5,7]
+__device__ __forceinline__ u32x4 x8_paired(u32x4 v) {
+    return u32x4{__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x05040100u),
+                 __builtin_amdgcn_perm(v.y, v.x, 0x07060302u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u)};
+}
+
 template <int N_>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N_ >= 0 && N_ < 64, "vmcnt");

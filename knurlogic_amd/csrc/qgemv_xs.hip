@@ -19,8 +19,13 @@
 // re-staging x each time.  Per chunk a wave (16 weight rows) decodes its
 // codes exactly to bf16 (integers < 256; E2M1 / E4M3 in the microscaled
 // modes), runs the per-group MFMA chains against the staged x and adds
-// s * P + b * X; after a block's last chunk it writes the block's outputs
-// (SwiGLU of the gate and up sums for GLU) and starts the next block.
+// s * P; the bias term sum_g b * X of the chunk's groups is one fp32 MFMA
+// (v_mfma_f32_16x16x4_f32: X of the tile rows by group, from a table formed
+// once per workgroup, against the rows' biases).  4-bit codes decode in
+// the order [0,2,4,6,1,3,5,7] of each run of 8 (no byte shuffle), and the
+// staged x is put in that order once, while the X table is summed.  After
+// a block's last chunk the wave writes the block's outputs (SwiGLU of the
+// gate and up sums for GLU) and starts the next block.
 #include "qgemv_dl.hpp"
 #include "pair_tiles.hpp"
 #include "../../include/knurlogic_amd.h"
@@ -52,6 +57,7 @@ __device__ __forceinline__ float xs_f32_kept(double v) {
 // multiple of 1 KB, at least XR rows); G: column blocks per workgroup.  XR:
 // the tile's rows (4, 16, 32 or 64); a 4-row tile feeds the 16-row MFMA
 // fragments with its rows repeated (the extra outputs are never written).
+// LDS: the x region, NS stages, then (affine) the X table [K / GS][XR] fp32.
 template <int BITS, int GS, bool MX, int XR, int NSET, int NS>
 __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t xrow, uint32_t xbytes) {
     using D = DlShape<BITS, GS, MX, 1>;
@@ -192,7 +198,6 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
     const int nl = lane & 15, j4 = lane >> 4;
     const int wr = wave * 16 + nl;                       // this lane's weight row in a block
     const int sro = MX ? (wr / MXR) * 256 + (wr % MXR) * GPC : wr * GPC;   // row's scales in the stage
-    const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
     const unsigned char* xl[MC];
 #pragma unroll
     for (int cc = 0; cc < MC; cc++) xl[cc] = smem + (uint32_t)(16 * cc + (XR < 16 ? nl % XR : nl)) * xrow;
@@ -202,13 +207,58 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
 #pragma unroll
         for (int cc = 0; cc < MC; cc++) acc[set][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    wait_vmcnt<0>();                                     // chunks 0 .. NS - 2 and the x rows
+    __builtin_amdgcn_s_barrier();                        // of every wave
+    // affine: X[g][m] = the sum of tile row m's x over group g (the bias
+    // term's operand), and at 4 bits the staged x put in the decode's order
+    float* const xtab = (float*)(smem + xbytes + NS * STAGE);
+    if constexpr (!MX) {
+        const int Gk = (int)(K / GS);
+        for (int it = tid; it < count * Gk; it += 256) {
+            const int m = it / Gk, g = it - (it / Gk) * Gk;
+            unsigned char* xp = smem + (uint32_t)m * xrow + (uint32_t)g * (GS * 2);
+            float sum = 0.f;
+#pragma unroll
+            for (int q = 0; q < GS / 8; q++) {
+                const u32x4 v = *(const u32x4*)(xp + 16 * q);
+#pragma unroll
+                for (int e = 0; e < 4; e++) sum += __uint_as_float(v[e] << 16) + __uint_as_float(v[e] & 0xffff0000u);
+                if constexpr (BITS == 4) *(u32x4*)(xp + 16 * q) = x8_paired(v);
+            }
+            xtab[g * XR + m] = sum;
+        }
+        lds_barrier();
+    }
+
     for (int i = 0; i < total; i++) {
-        if (i == 0) wait_vmcnt<0>();                     // chunk 0 and the x rows (issued after it)
-        else wait_vmcnt<PER_WAVE * (NS - 2)>();          // this wave's loads of chunk i
-        __builtin_amdgcn_s_barrier();                    // and every wave's
+        if (i > 0) {
+            wait_vmcnt<PER_WAVE * (NS - 2)>();           // this wave's loads of chunk i
+            __builtin_amdgcn_s_barrier();                // and every wave's
+        }
         const unsigned char* base = smem + xbytes + (i % NS) * STAGE;
         const int c = i % C;
         const uint32_t kb = (uint32_t)c * (DL_KC * 2);    // x byte offset of the chunk
+        // affine: the bias term of the chunk's groups, lane (n, j4) holding
+        // X[tile row n][group 4 q + j4] and that group's bias of weight row n
+        if constexpr (!MX) {
+#pragma unroll
+            for (int q = 0; q < (GPC + 3) / 4; q++) {
+                const int gq = 4 * q + j4;
+                const bool ok = gq < GPC;
+                float xa[MC];
+#pragma unroll
+                for (int cc = 0; cc < MC; cc++)
+                    xa[cc] = ok ? xtab[(c * GPC + gq) * XR + (XR < 16 ? nl % XR : 16 * cc + nl)] : 0.f;
+#pragma unroll
+                for (int set = 0; set < NSET; set++) {
+                    const uint16_t* sl = (const uint16_t*)(base + set * SET + W_BYTES);
+                    const float bv = ok ? bf16_to_f32(sl[DL_ROWS * GPC + sro + gq]) : 0.f;
+#pragma unroll
+                    for (int cc = 0; cc < MC; cc++)
+                        acc[set][cc] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[cc], bv, acc[set][cc], 0, 0, 0);
+                }
+            }
+        }
         // groups whose reads are issued together: fewer at larger tiles, so
         // the fragments of a batch stay within the register budget
         constexpr int GH0 = MC * NSET >= 4 ? 1 : MC * NSET >= 2 ? 2 : 4;
@@ -217,7 +267,7 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
         for (int h = 0; h < GPC; h += GH) {
             u32x4 wd[NSET][GH];
             u32x4 A[MC][GH][NT];
-            float sc[NSET][GH], bi[NSET][GH];
+            float sc[NSET][GH];
 #pragma unroll
             for (int g = 0; g < GH; g++) {
                 const int gi = h + g;
@@ -232,13 +282,8 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
                         wd[set][g] = u32x4{t.x, t.y, 0u, 0u};
                     } else wd[set][g] = *(const u32x4*)p;
                     const unsigned char* sl = base + set * SET + W_BYTES;
-                    if constexpr (MX) {
-                        sc[set][g] = e8m0_to_f32(sl[sro + gi]);
-                        bi[set][g] = 0.f;
-                    } else {
-                        sc[set][g] = bf16_to_f32(((const uint16_t*)sl)[sro + gi]);
-                        bi[set][g] = bf16_to_f32(((const uint16_t*)sl)[DL_ROWS * GPC + sro + gi]);
-                    }
+                    if constexpr (MX) sc[set][g] = e8m0_to_f32(sl[sro + gi]);
+                    else sc[set][g] = bf16_to_f32(((const uint16_t*)sl)[sro + gi]);
                 }
 #pragma unroll
                 for (int cc = 0; cc < MC; cc++)
@@ -268,7 +313,7 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
                                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.f, false)),
                                 __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.f, true))};
                         } else if constexpr (BITS == 4) {
-                            B[set][t] = nib8_natural(wd[set][g][t]);
+                            B[set][t] = nib8_paired(wd[set][g][t]);
                         } else {
                             B[set][t] = u32x4{bytes_to_bf16x2(wd[set][g][2 * t], 0),
                                               bytes_to_bf16x2(wd[set][g][2 * t], 2),
@@ -278,23 +323,17 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
                     }
 #pragma unroll
                 for (int cc = 0; cc < MC; cc++) {
-                    f32x4 X = {0.f, 0.f, 0.f, 0.f};
                     f32x4 P[NSET];
 #pragma unroll
                     for (int set = 0; set < NSET; set++) P[set] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int t = 0; t < NT; t++) {
-                        if constexpr (!MX) X = mfma16x16x32(A[cc][g][t], ones, X);
+                    for (int t = 0; t < NT; t++)
 #pragma unroll
                         for (int set = 0; set < NSET; set++) P[set] = mfma16x16x32(A[cc][g][t], B[set][t], P[set]);
-                    }
 #pragma unroll
                     for (int set = 0; set < NSET; set++)
 #pragma unroll
-                        for (int e = 0; e < 4; e++)
-                            acc[set][cc][e] = MX ? __builtin_fmaf(sc[set][g], P[set][e], acc[set][cc][e])
-                                                 : __builtin_fmaf(sc[set][g], P[set][e],
-                                                                  __builtin_fmaf(bi[set][g], X[e], acc[set][cc][e]));
+                        for (int e = 0; e < 4; e++) acc[set][cc][e] = __builtin_fmaf(sc[set][g], P[set][e], acc[set][cc][e]);
                 }
             }
         }
@@ -353,10 +392,14 @@ int xs_blocks_per_wg(int64_t NB, int64_t tiles, bool affine_glu) {
 
 constexpr size_t XS_LDS_MAX = 160 * 1024 - 1024;   // the static row tables stay below 1 KB
 
+// the affine kernels' X table: [K / GS][XR] fp32
+template <int GS, bool MX, int XR>
+size_t xs_xtab_bytes(int64_t K) { return MX ? 0 : (size_t)(K / GS) * XR * 4; }
+
 template <int BITS, int GS, bool MX, int XR, int NSET, int NS>
 int launch_xs_one(const QgArgs& a, int64_t ntiles, uint32_t xrow, uint32_t xbytes, hipStream_t st) {
     constexpr size_t stage = XsShape<BITS, GS, MX, NSET>::STAGE;
-    const size_t lds = (size_t)xbytes + NS * stage;
+    const size_t lds = (size_t)xbytes + NS * stage + xs_xtab_bytes<GS, MX, XR>(a.K);
     if (lds > XS_LDS_MAX) return 1;
     allow_dynamic_lds_once((const void*)qgemv_xs_kernel<BITS, GS, MX, XR, NSET, NS>);
     const int64_t NB = (a.N + 63) / 64;
@@ -370,7 +413,8 @@ int launch_xs_one(const QgArgs& a, int64_t ntiles, uint32_t xrow, uint32_t xbyte
 template <int BITS, int GS, bool MX, int XR, int NSET>
 int launch_xs_mc(const QgArgs& a, int64_t ntiles, uint32_t xrow, uint32_t xbytes, hipStream_t st) {
     constexpr size_t stage = XsShape<BITS, GS, MX, NSET>::STAGE;
-    if ((size_t)xbytes + 4 * stage <= 78 * 1024) return launch_xs_one<BITS, GS, MX, XR, NSET, 4>(a, ntiles, xrow, xbytes, st);
+    if ((size_t)xbytes + 4 * stage + xs_xtab_bytes<GS, MX, XR>(a.K) <= 78 * 1024)
+        return launch_xs_one<BITS, GS, MX, XR, NSET, 4>(a, ntiles, xrow, xbytes, st);
     return launch_xs_one<BITS, GS, MX, XR, NSET, 3>(a, ntiles, xrow, xbytes, st);
 }
 
