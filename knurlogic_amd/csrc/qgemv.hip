@@ -17,11 +17,13 @@
 // instruction and is bound by L1 tag lookups, not by HBM.)
 //
 // Codes become bf16 without rounding (integers < 256), so P is a plain
-// MFMA with fp32 accumulation; X comes from the same A operand against a
-// matrix of ones, which leaves X[m, g] in exactly the D layout of P; scale
-// and bias are then two FMAs per output per group.  The only rounding is the
-// fp32 accumulation and the final bf16.  A row's arithmetic is the same at
-// any number of rows.
+// MFMA with fp32 accumulation and the scale one FMA per output per group.
+// X is summed while x is staged (bf16 dot products with ones, then across
+// the lanes holding a group's pieces) into a small LDS table, and the
+// bias term sum_g b[n, g] X[m, g] of a chunk is one fp32 MFMA
+// (v_mfma_f32_16x16x4_f32) per 4 groups into the same accumulators.  The
+// only rounding is fp32 accumulation and the final bf16.  A row's
+// arithmetic is the same at any number of rows.
 //
 // 4-bit codes decode 8 per 7 instructions into the k order
 // [0,2,4,6,1,3,5,7] (low nibbles, then high nibbles, of each byte), and x is
@@ -83,7 +85,8 @@ struct QgShape {
 template <int BITS, int GS, int NSET, int MC>
 constexpr size_t qg_lds_bytes() {
     using S = QgShape<BITS, NSET, MC>;
-    return 2 * (S::W_BYTES + S::X_BYTES + (size_t)2 * NSET * QG_ROWS * (QG_KC / GS) * 2);
+    return 2 * (S::W_BYTES + S::X_BYTES + (size_t)2 * NSET * QG_ROWS * (QG_KC / GS) * 2 +
+                (size_t)(QG_KC / GS) * S::MT * 4);
 }
 
 // MX: microscaled codes (GS 32): the codes convert to bf16 exactly (E2M1,
@@ -108,6 +111,9 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
     auto Sl = [&](int buf, int set, int which) {       // which: 0 scales, 1 biases
         return sbase + ((buf * NSET + set) * 2 + which) * (QG_ROWS * GPC);
     };
+    // X[g][m]: the sum of tile row m's x over group g of the chunk (affine)
+    float* xtbase = (float*)(sbase + 2 * NSET * 2 * (QG_ROWS * GPC));
+    auto Xt = [&](int buf) { return xtbase + buf * (GPC * MT); };
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -231,6 +237,25 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
 #pragma unroll
         for (int p = 0; p < XPASS; p++) {
             u32x4 v = rxv[slot][p];
+            if constexpr (!MX) {
+                // the piece's 8 values summed (dot products with ones), then
+                // over the GS / 8 consecutive lanes holding the group's pieces
+                typedef __bf16 qg_bf2 __attribute__((ext_vector_type(2)));
+                const qg_bf2 one = __builtin_bit_cast(qg_bf2, 0x3F803F80u);
+                // (each element copied to a scalar first: a bit cast of a vector
+                // element v[e] reads element 0 in this compiler)
+                const uint32_t ve[4] = {v.x, v.y, v.z, v.w};
+                float ps = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) ps = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(qg_bf2, ve[e]), one, ps, false);
+                ps += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ps), 0xb1, 0xf, 0xf, false));  // lane ^ 1
+                ps += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ps), 0x4e, 0xf, 0xf, false));  // lane ^ 2
+                if constexpr (GS >= 64)
+                    ps += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ps), 0x141, 0xf, 0xf, false));  // 8-lane mirror
+                if constexpr (GS >= 128)
+                    ps += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ps), 0x140, 0xf, 0xf, false));  // 16-lane mirror
+                if (tid % (GS / 8) == 0) Xt(buf)[((tid % 32) / (GS / 8)) * MT + p * 8 + tid / 32] = ps;
+            }
             if constexpr (BITS == 4 && !MX) v = x8_to_nibble_order(v);
             *(u32x4*)(Xl(buf) + (p * 8 + tid / 32) * XST + 16 * (tid % 32)) = v;
         }
@@ -241,7 +266,6 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
     for (int set = 0; set < NSET; set++)
 #pragma unroll
         for (int c = 0; c < MC; c++) acc[set][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
     const int wr = wave * 16 + nl;                       // this lane's weight row in the tile
 
     // groups unrolled UF at a time: their LDS reads, decodes and MFMA chains
@@ -250,10 +274,30 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
     constexpr int UF0 = 4 / (MC * NSET) > 0 ? 4 / (MC * NSET) : 1;
     constexpr int UF = UF0 < GPC ? UF0 : GPC;
     auto compute = [&](int buf) {
+        // affine: the chunk's bias term sum_g b * X, one fp32 MFMA per 4
+        // groups (lane (n, j4): X of tile row n and the bias of weight row
+        // n, at group 4 q + j4)
+        if constexpr (!MX) {
+#pragma unroll
+            for (int q = 0; q < (GPC + 3) / 4; q++) {
+                const int gq = 4 * q + j4;
+                const bool ok = gq < GPC;
+                float xa[MC];
+#pragma unroll
+                for (int c = 0; c < MC; c++) xa[c] = ok ? Xt(buf)[gq * MT + 16 * c + nl] : 0.f;
+#pragma unroll
+                for (int set = 0; set < NSET; set++) {
+                    const float bv = ok ? bf16_to_f32(Sl(buf, set, 1)[wr * GPC + gq]) : 0.f;
+#pragma unroll
+                    for (int c = 0; c < MC; c++)
+                        acc[set][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[c], bv, acc[set][c], 0, 0, 0);
+                }
+            }
+        }
 #pragma unroll UF
         for (int gi = 0; gi < GPC; gi++) {
             u32x4 B[NSET][NT];
-            float sc[NSET], bi[NSET];
+            float sc[NSET];
 #pragma unroll
             for (int set = 0; set < NSET; set++) {
                 const unsigned char* wp = Wl(buf, set) + wr * WST + gi * (GS * BITS / 8) + j4 * LB;
@@ -293,33 +337,24 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
                                           bytes_to_bf16x2(wv[2 * t + 1], 0), bytes_to_bf16x2(wv[2 * t + 1], 2)};
                     }
                 }
-                if constexpr (MX) {
-                    sc[set] = mx_scale_qg(Sl(buf, set, 0)[wr * GPC + gi]);
-                    bi[set] = 0.f;
-                } else {
-                    sc[set] = bf16_to_f32(Sl(buf, set, 0)[wr * GPC + gi]);
-                    bi[set] = bf16_to_f32(Sl(buf, set, 1)[wr * GPC + gi]);
-                }
+                if constexpr (MX) sc[set] = mx_scale_qg(Sl(buf, set, 0)[wr * GPC + gi]);
+                else sc[set] = bf16_to_f32(Sl(buf, set, 0)[wr * GPC + gi]);
             }
 #pragma unroll
             for (int c = 0; c < MC; c++) {
-                f32x4 X = {0.f, 0.f, 0.f, 0.f};
                 f32x4 P[NSET];
 #pragma unroll
                 for (int set = 0; set < NSET; set++) P[set] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     const u32x4 A = *(const u32x4*)(Xl(buf) + (16 * c + nl) * XST + (gi * GS + j4 * RUN + 8 * t) * 2);
-                    if constexpr (!MX) X = mfma16x16x32(A, ones, X);
 #pragma unroll
                     for (int set = 0; set < NSET; set++) P[set] = mfma16x16x32(A, B[set][t], P[set]);
                 }
 #pragma unroll
                 for (int set = 0; set < NSET; set++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        acc[set][c][e] = MX ? __builtin_fmaf(sc[set], P[set][e], acc[set][c][e])
-                                            : __builtin_fmaf(sc[set], P[set][e], __builtin_fmaf(bi[set], X[e], acc[set][c][e]));
+                    for (int e = 0; e < 4; e++) acc[set][c][e] = __builtin_fmaf(sc[set], P[set][e], acc[set][c][e]);
             }
         }
     };
