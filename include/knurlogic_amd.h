@@ -366,9 +366,10 @@ int kmi_moe_shared_add(const void* y, const void* gate, const void* shared_y, in
  *   out: [T, H] = round(sum_s round(y[t, s] * scores[t, s])) when scores is
  *     given, else y [T, k, H] (SwitchGLU's own output).
  * Every intermediate rounds where the reference rounds: gate and up outputs,
- * silu, the activation, the down output, each weighted product.  Up to 16
+ * silu, the activation, the down output, each weighted product.  Up to 64
  * (token, slot) pairs run token-major (two kernels, no sort); more group
- * rows by expert.  workspace: kmi_switch_glu_workspace_bytes.
+ * rows by expert (a GPU sort of the pairs into expert tiles).  workspace:
+ * kmi_switch_glu_workspace_bytes.
  */
 int kmi_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, const int32_t* inds,
                    const void* scores, const uint32_t* w_gu, const void* s_gu, const void* b_gu,
@@ -405,7 +406,8 @@ int kmi_switch_glu_mx(const void* x, int64_t T, int64_t H, int64_t I, int k, con
  * bit); out [T, H] bf16; the weights as kmi_switch_glu takes them.  At
  * decode sizes (up to 64 (token, slot) pairs, E <= 256) the gate/up kernel
  * routes its own token, so the call is two kernel launches; otherwise it
- * routes first.
+ * routes first, and up to 256 pairs over up to 256 experts the expert
+ * kernels form their tiles from the routed experts (no sort launch).
  * k <= 8, E <= 1024.  workspace: kmi_switch_glu_workspace_bytes.
  */
 int kmi_moe_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k, int64_t E,
@@ -522,7 +524,9 @@ int kmi_vq_packed_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int
  * kmi_vq_packed_switch_glu with the weighted combine into out [T, H].
  * logits [T, E] bf16.  Up to 16 (token, slot) pairs with E <= 256 the
  * gate/up kernel routes each pair's token itself (no router launch);
- * otherwise it routes first.
+ * otherwise it routes first, and up to 256 pairs over up to 256 experts
+ * the expert-tile kernels form their tiles from the routed experts (no
+ * sort launch).
  * k <= 8, E <= 1024.  workspace: kmi_vq_packed_switch_glu_workspace_bytes.
  */
 int kmi_vq_packed_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k,
@@ -548,7 +552,9 @@ int kmi_vq_switch_glu(const void* x, int64_t T, int64_t H, int64_t I, int k, con
  * weighted combine into out [T, H].  logits [T, E] bf16.  For one token on
  * the MFMA path (per-channel scales, E <= 256) the gate/up kernel routes
  * the token itself, so the call is two kernel launches; otherwise it
- * routes first.  k <= 8, E <= 1024.  workspace:
+ * routes first, and up to 256 pairs over up to 256 experts the expert
+ * kernels form their tiles from the routed experts (no sort launch).
+ * k <= 8, E <= 1024.  workspace:
  * kmi_vq_switch_glu_workspace_bytes(T, H, I, k).
  */
 int kmi_vq_experts(const void* x, const void* logits, int64_t T, int64_t H, int64_t I, int k,
