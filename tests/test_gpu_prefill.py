@@ -85,3 +85,30 @@ def test_vq_switch_glu_at_prefill_sizes(dev, T, kc):
     ref = O.switch_glu(x[s], inds[s], fn(hg), fn(hu), fn(hd))
     assert_close(got[s], ref, what=f"vq switch_glu T={T} kc={kc}")
     assert_close(comb[s], O.combine(ref, sc[s]), what=f"vq combine T={T} kc={kc}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_grouped_gemm_with_k_tiles_past_a_group(dev, bits):
+    """The grouped expert GEMM (from 64 routed rows per expert) on experts
+    whose K runs 9 (gate/up, H = 576) and 5 (down, I = 320) k-tiles, which
+    end part-way through the 4-deep load ring; 8 experts, top-2, 512 tokens
+    (128 rows per expert)."""
+    rng = np.random.default_rng(9200 + bits)
+    e, h, i_, k, T = 8, 576, 320, 2, 512
+    mats = []
+    for N, Kd in ((i_, h), (i_, h), (h, i_)):
+        wq = np.frombuffer(rng.bytes(e * N * Kd * bits // 8), np.uint32).reshape(e, N, Kd * bits // 32)
+        sc = O.bf16_round(rng.uniform(0.004, 0.008, (e, N, Kd // 64)).astype(np.float32) / (1 << (bits - 4)))
+        bi = O.bf16_round((-0.5 * ((1 << bits) - 1) * sc + rng.normal(0, 0.002, sc.shape)).astype(np.float32))
+        mats.append((wq, sc, bi))
+    q = lambda m: nn.QuantizedSwitchLinear(u32_to_torch(m[0], dev), to_torch(m[1], dev, BF),
+                                           to_torch(m[2], dev, BF), None, 64, bits)
+    glu = nn.SwitchGLU(*(q(m) for m in mats))
+    fns = [lambda xs, ex, m=m: O.quantized_matmul(xs, m[0][ex], m[1][ex], m[2][ex], True, 64, bits, "bfloat16")
+           for m in mats]
+    x = bf16_normal(rng, (T, h))
+    inds = np.argsort(rng.random((T, e)), axis=1)[:, :k].astype(np.int32)
+    got = to_numpy(glu(to_torch(x, dev, BF), torch.from_numpy(inds).to(dev)))
+    assert got.shape == (T, k, h) and np.isfinite(got).all()
+    s = _sample(rng, T)
+    assert_close(got[s], O.switch_glu(x[s], inds[s], *fns), what=f"grouped gemm {bits}-bit")

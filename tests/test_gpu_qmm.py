@@ -275,10 +275,11 @@ def test_strided_views_are_read_as_their_values(dev):
 
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("M,N,K_", [(129, 200, 512), (300, 200, 4096), (256, 4096, 14336 // 4),
-                                    (513, 130, 1024)])
+                                    (513, 130, 1024), (300, 200, 576), (257, 1030, 2880)])
 def test_large_m_tiles_and_split_k(dev, bits, M, N, K_):
     """The 256 x 128 GEMM: ragged M and N edges, and K split across
-    workgroups (fp32 partials summed in split order) when tiles are few."""
+    workgroups (fp32 partials summed in split order) when tiles are few; K of
+    9 and 45 k-tiles, which end part-way through the 4-deep load ring."""
     rng = np.random.default_rng(M * 31 + N + K_ + bits)
     (wq, s, b), (tw, ts, tb) = _weights(rng, (N, K_), bits, 64, dev)
     x = bf16_normal(rng, (M, K_))
