@@ -481,9 +481,10 @@ def ceilings(dev, headline_bytes):
     plain read kernel (kmi_read_probe, 16-byte nontemporal loads, nothing
     computed) over the headline's per-call bytes with the buffers rotated
     past the Infinity Cache as the headline's are, over the [4096, 4096]
-    M = 1 call's bytes, over 64 KB (one launch's floor) and over 1 GiB; and the
-    bf16 GEMM rate of torch.matmul (hipBLASLt) on the prefill shapes with
-    unquantized bf16 weights."""
+    M = 1 call's bytes, over 64 KB (one launch's floor) and over 1 GiB; the
+    bf16 MFMA rate and clock of the GEMM's matrix-core work alone
+    (mfma_rate); and the bf16 GEMM rate of torch.matmul (hipBLASLt) on the
+    prefill shapes with unquantized bf16 weights."""
     import ctypes
     import torch
     from knurlogic_amd import _abi
@@ -523,6 +524,7 @@ def ceilings(dev, headline_bytes):
     big = max((read_rate(1 << 30, w) + (w,) for w in (2048, 8192)), key=lambda t: t[0])
     res["read_1GiB"] = {"GBps": round(big[0], 1), "us": round(big[1], 3), "workgroups": big[2],
                         "frac_of_published": round(big[0] / PEAK_HBM_GBS, 4)}
+    res["mfma_bf16"] = mfma_rate(dev, L)
     for N, K in ((14336, 4096), (4096, 14336)):
         g = torch.Generator(device=dev).manual_seed(N)
         x = torch.randn(512, K, device=dev, generator=g).to(torch.bfloat16)
@@ -542,6 +544,40 @@ def ceilings(dev, headline_bytes):
         del x, w, y
     torch.cuda.empty_cache()
     return res
+
+
+def mfma_rate(dev, L=None, rounds=2048):
+    """The bf16 MFMA rate the matrix cores reach on the prefill GEMM's
+    instruction and wave layout alone (kmi_mfma_probe: one workgroup of 8
+    waves per CU, 16 v_mfma_f32_32x32x16_bf16 per wave per round on register
+    operands), and the shader clock under that load from the probe's cycle
+    and 100 MHz counters; peak_at_clock is 1024 FLOPs per SIMD per cycle at
+    that clock."""
+    import ctypes
+    import torch
+    from knurlogic_amd import _abi
+    L = L or _abi.load()
+    ncu = torch.cuda.get_device_properties(dev).multi_processor_count
+    seed = torch.full((64,), 0x3C003C00, dtype=torch.int32, device=dev)     # bf16 pairs of 2^-7
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    stamps = torch.zeros(2, dtype=torch.int64, device=dev)
+    calls = 4
+
+    def run():
+        st = torch.cuda.current_stream().cuda_stream
+        for _ in range(calls):
+            _abi.check(L.kmi_mfma_probe(ctypes.c_void_p(seed.data_ptr()), ncu, rounds, ctypes.c_void_p(out.data_ptr()),
+                                        ctypes.c_void_p(stamps.data_ptr()), ctypes.c_void_p(st)), "mfma_probe")
+
+    us = time_graph(run) * 1e3 / calls
+    flops = ncu * 8 * rounds * 16 * 2.0 * 32 * 32 * 16
+    tf = flops / (us * 1e-6) / 1e12
+    cyc, ticks = (int(v) for v in stamps.cpu())
+    mhz = cyc * 100.0 / ticks if ticks > 0 else None
+    return {"TFLOPs": round(tf, 1), "us": round(us, 3), "workgroups": ncu, "frac_of_published": round(tf / PEAK_BF16_TFLOPS, 4),
+            "clock_MHz": round(mhz, 0) if mhz else None,
+            "peak_at_clock_TFLOPs": round(ncu * 4 * 1024 * mhz * 1e6 / 1e12, 1) if mhz else None,
+            "what": "kmi_mfma_probe: v_mfma_f32_32x32x16_bf16 on register operands, 8 waves per CU"}
 
 
 def cpu_model():

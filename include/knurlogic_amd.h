@@ -575,6 +575,20 @@ int kmi_vq_experts(const void* x, const void* logits, int64_t T, int64_t H, int6
  */
 int kmi_read_probe(const void* p, int64_t bytes, int workgroups, uint32_t* out, void* stream);
 
+/*
+ * Calibration only (no counterpart in the reference): `workgroups`
+ * workgroups of 8 waves (two per SIMD, as the prefill GEMM runs) each issue
+ * `iters` rounds of 16 v_mfma_f32_32x32x16_bf16 per wave into 2 x 2
+ * accumulators on register operands (from the 64 uint32 at `seed`), so a
+ * timed call gives the bf16 MFMA rate the GPU reaches (2 x 32 x 32 x 16
+ * FLOPs per MFMA).  stamps (two uint64, device memory) receive workgroup
+ * 0's first wave's shader-clock cycles and 100 MHz counter ticks around its
+ * loop: their ratio is the clock under that load.  `out` (one uint32) is
+ * written only for a sum no caller relies on.  iters: 1 .. 2^24.
+ */
+int kmi_mfma_probe(const uint32_t* seed, int workgroups, int iters, uint32_t* out, uint64_t* stamps,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

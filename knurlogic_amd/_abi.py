@@ -64,6 +64,7 @@ SIGNATURES = {
     "kmi_vq_packed_switch_glu": (I, [P, I64, I64, I64, I, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I64, I,
                                      P, P, SZ, P]),
     "kmi_read_probe": (I, [P, I64, I, P, P]),
+    "kmi_mfma_probe": (I, [P, I, I, P, P, P]),
 }
 
 ABI_VERSION = 1
