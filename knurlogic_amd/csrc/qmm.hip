@@ -356,19 +356,44 @@ __global__ __launch_bounds__(512, 1) void qmm5_kernel(QgemmArgs a) {
     }
 
     // D of block (i, j): row 32 i + 8 (r / 4) + 4 h + r % 4, column 32 j + l32.
+    // Stored through a buffer view of the output: the lane's column and the
+    // wave's first row in the offset register, the rest of the row (the same
+    // for the wave) in the scalar offset, so an output costs a conversion
+    // and a store.  A row past M lands past the view and is dropped; a
+    // column past N takes an offset past every view.  (Rows r and r + 1 of a
+    // lane are adjacent rows: one v_cvt_pk_bf16_f32 per pair.)
+    const int64_t N = a.N;
+    const int64_t row0 = bm + wm + 4 * h;
+    if (a.splits == 1) {
+        const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, a.M * N * 2);
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int64_t col = bn + wn + 32 * j + l32;
-        if (col >= a.N) continue;
+        for (int j = 0; j < 2; j++) {
+            const int64_t col = bn + wn + 32 * j + l32;
+            const uint32_t vo = col < N ? (uint32_t)((row0 * N + col) * 2) : DEAD;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+            for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int64_t row = bm + wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-                if (row >= a.M) continue;
-                if (a.splits == 1) a.y[row * a.N + col] = f32_to_bf16(acc[i][j][r]);
-                else a.partial[((int64_t)blockIdx.y * a.M + row) * a.N + col] = acc[i][j][r];
-            }
+                for (int r = 0; r < 16; r += 2) {
+                    const uint32_t so = (uint32_t)((32 * i + 8 * (r / 4) + r % 4) * N * 2);
+                    const uint32_t v = cvt_pk_bf16(acc[i][j][r], acc[i][j][r + 1]);
+                    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)v, ry, (int)vo, (int)so, 0);
+                    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(v >> 16), ry, (int)vo, (int)(so + N * 2), 0);
+                }
+        }
+    } else {
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partial + (int64_t)blockIdx.y * a.M * N, a.M * N * 4);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int64_t col = bn + wn + 32 * j + l32;
+            const uint32_t vo = col < N ? (uint32_t)((row0 * N + col) * 4) : DEAD;
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t so = (uint32_t)((32 * i + 8 * (r / 4) + r % 4) * N * 4);
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), rp, (int)vo, (int)so, 0);
+                }
+        }
     }
 }
 
@@ -421,6 +446,7 @@ int qmm_gemm(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w,
         KMI_CHECK_ARG(M * K * 2 < (1LL << 31) && N * K * bits / 8 < (1LL << 31),
                       "quantized_matmul: x or w past 2 GiB");
         const QgemmPlan p = plan_gemm(M, N, K);
+        KMI_CHECK_ARG(M * N * (p.splits > 1 ? 4 : 2) < (1LL << 31), "quantized_matmul: y past 2 GiB");
         if (p.ws > 0 && (!workspace || workspace_bytes < p.ws)) {
             set_error("quantized_matmul: workspace of %zu bytes needed, %zu given", p.ws, workspace_bytes);
             return EWORKSPACE;
