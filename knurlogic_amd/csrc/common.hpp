@@ -119,6 +119,27 @@ struct TF32 {
     static __device__ __forceinline__ float round(float f) { return f; }
 };
 
+// silu(g) = g / (1 + e^-g) of a bf16 value g, rounded to float32 and then to
+// bf16: the SwiGLU epilogues' round(silu_f32(g)), silu evaluated exactly
+// and rounded once to float32.  Float32 arithmetic (an accurate expf and a
+// reciprocal, a few float32 ulps from that rounding) gives the same bf16
+// unless its low 16 bits lie within SILU_WINDOW of the bf16 rounding
+// midpoint, or |g| > 64 (e^-g past float32's range): those lanes take the
+// float64 evaluation.  Checked on every bf16 value of g (kmi_swiglu in
+// bf16 runs it; its test covers all 65536 gate patterns).
+constexpr int SILU_WINDOW = 16;
+__device__ __forceinline__ float silu_bf16r(float g) {
+    const float t = g * __builtin_amdgcn_rcpf(1.0f + expf(-g));
+    const int lo = (int)(__float_as_uint(t) & 0xffffu) - 0x8000;
+    if (__builtin_expect((lo >= -SILU_WINDOW && lo <= SILU_WINDOW) || !(__builtin_fabsf(g) <= 64.0f), 0)) {
+        const double gd = (double)g;
+        float f = (float)(gd / (1.0 + exp(-gd)));
+        asm volatile("" : "+v"(f));      // keep the float32 rounding (no fused f64 -> bf16 rounding)
+        return bf16_to_f32(f32_to_bf16(f));
+    }
+    return bf16_to_f32(f32_to_bf16(t));
+}
+
 // ---- MFMA operand vector types ------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));

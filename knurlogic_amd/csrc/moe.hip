@@ -4,6 +4,8 @@
 // reference's SparseMoeBlock / SwitchGLU arithmetic
 // (src/knurlogic/engine/families/qwen/architecture/qwen3_5.py:35-40,108-112,
 // 170-192), each rounding step where the reference rounds.
+#include <type_traits>
+
 #include "common.hpp"
 #include "route.hpp"
 #include "../../include/knurlogic_amd.h"
@@ -44,7 +46,9 @@ __global__ __launch_bounds__(ROUTE_THREADS) void moe_route_kernel(const void* __
 }
 
 // act[r, i] = round(round(silu(gate[r, i])) * up[r, i]), silu in float32
-// (evaluated in float64, rounded once): _SwiGLU with qwen3_5.py's _silu.
+// (evaluated in float64, rounded once; in bf16 by silu_bf16r, the expert
+// kernels' epilogue, which gives the same values): _SwiGLU with
+// qwen3_5.py's _silu.
 template <class T>
 __global__ __launch_bounds__(256) void swiglu_kernel(const void* __restrict__ gate, const void* __restrict__ up,
                                                      int64_t ld_in, int64_t rows, int64_t I,
@@ -53,8 +57,13 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const void* __restrict__ ga
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
          idx += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = idx / I, i = idx % I;
-        const double g = (double)ld_dt<T>(gate, r * ld_in + i);
-        const float s = T::round(f64_to_f32(g / (1.0 + exp(-g))));
+        float s;
+        if constexpr (std::is_same<T, TBF16>::value) {
+            s = silu_bf16r(ld_dt<T>(gate, r * ld_in + i));    // the expert kernels' epilogue arithmetic
+        } else {
+            const double g = (double)ld_dt<T>(gate, r * ld_in + i);
+            s = T::round(f64_to_f32(g / (1.0 + exp(-g))));
+        }
         st_dt<T>(out, idx, s * ld_dt<T>(up, r * ld_in + i));
     }
 }

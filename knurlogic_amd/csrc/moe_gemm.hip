@@ -245,9 +245,8 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_kernel(QgArgs a, int n_tiles,
                 for (int r = 0; r < 16; r++) {
                     const int m = wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
                     if (m >= count) continue;
-                    // act = round(round(silu_f32(round(gate))) * round(up)), silu in float64 rounded once
-                    const double gd = (double)mg_bf16r(acc[i][0][r]);
-                    const float sl = mg_bf16r(mg_f32_kept(gd / (1.0 + exp(-gd))));
+                    // act = round(round(silu_f32(round(gate))) * round(up))
+                    const float sl = silu_bf16r(mg_bf16r(acc[i][0][r]));
                     a.y[(int64_t)rid_s[m] * a.N + col] = f32_to_bf16(sl * mg_bf16r(acc[i][1][r]));
                 }
         }

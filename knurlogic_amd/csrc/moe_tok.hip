@@ -185,8 +185,7 @@ __global__ __launch_bounds__(64 * WV) void moe_glu_tok(MoeTokArgs a) {
         const float g = bf16r(wave_sum(acc0[r]));
         const float u = bf16r(wave_sum(acc1[r]));
         if (lane == 0 && n0 + r < a.N) {
-            const double gd = (double)g;
-            const float s = bf16r(f64_to_f32_kept(gd / (1.0 + exp(-gd))));
+            const float s = silu_bf16r(g);
             a.out[(int64_t)p * a.N + n0 + r] = ok_e ? f32_to_bf16(s * u) : (uint16_t)0;
         }
     }

@@ -392,9 +392,8 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
             if (m >= count) continue;
             const int64_t row = a.sorted ? (int64_t)a.sorted[start + m] : start + m;
             if constexpr (GLU) {
-                // act = round(round(silu_f32(round(gate))) * round(up)), silu in float64 rounded once
-                const double gd = (double)qg_bf16r(acc[0][c][e]);
-                const float sl = qg_bf16r(qg_f32_kept(gd / (1.0 + exp(-gd))));
+                // act = round(round(silu_f32(round(gate))) * round(up))
+                const float sl = silu_bf16r(qg_bf16r(acc[0][c][e]));
                 a.y[row * a.N + n] = f32_to_bf16(sl * qg_bf16r(acc[1][c][e]));
             } else if (a.S == 1) {
                 a.y[row * a.N + n] = f32_to_bf16(acc[0][c][e]);

@@ -350,9 +350,8 @@ __global__ __launch_bounds__(256) void qgemv_xs_kernel(QgArgs a, int G, uint32_t
                         if (m >= count) continue;
                         const int64_t row = rid_s[m];
                         if constexpr (NSET == 2) {
-                            // act = round(round(silu_f32(round(gate))) * round(up)), silu in float64 rounded once
-                            const double gd = (double)xs_bf16r(acc[0][cc][e]);
-                            const float sl = xs_bf16r(xs_f32_kept(gd / (1.0 + exp(-gd))));
+                            // act = round(round(silu_f32(round(gate))) * round(up))
+                            const float sl = silu_bf16r(xs_bf16r(acc[0][cc][e]));
                             a.y[row * a.N + n] = f32_to_bf16(sl * xs_bf16r(acc[1][cc][e]));
                         } else {
                             a.y[row * a.N + n] = f32_to_bf16(acc[0][cc][e]);

@@ -176,8 +176,7 @@ __global__ __launch_bounds__(256) void vq_gemv(VqArgs a) {
     if (seg == 0 && row < a.N) {
         float out = r[0];
         if constexpr (NSET == 2) {     // round(round(silu_f32(gate)) * up)
-            const double g = (double)r[0];
-            out = vq_bf16r(vq_f32_kept(g / (1.0 + exp(-g)))) * r[1];
+            out = silu_bf16r(r[0]) * r[1];
         }
         a.y[p * a.N + row] = (ok_e && ok_x) ? f32_to_bf16(out) : (uint16_t)0;
     }

@@ -342,8 +342,7 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
             float out = vqm_bf16r(f16_to_f32(scl[slot][0]) * acc[0][i]);
             if constexpr (NSET == 2) {     // round(round(silu_f32(gate)) * up)
                 const float up = vqm_bf16r(f16_to_f32(scl[slot][1]) * acc[1][i]);
-                const double gg = (double)out;
-                out = vqm_bf16r(vqm_f32_kept(gg / (1.0 + exp(-gg)))) * up;
+                out = silu_bf16r(out) * up;
             }
             res[i] = f32_to_bf16(out);
         }

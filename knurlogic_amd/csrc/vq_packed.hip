@@ -304,8 +304,7 @@ __global__ __launch_bounds__(256) void vq_packed_gemv(VpArgs a) {
     if (seg == 0 && row < a.N) {
         float out = res[0];
         if (a.nset == 2) {           // round(round(silu_f32(gate)) * up)
-            const double g = (double)res[0];
-            out = vp_bf16r(vp_f32_kept(g / (1.0 + exp(-g)))) * res[1];
+            out = silu_bf16r(res[0]) * res[1];
         }
         a.y[r * a.N + row] = (ok_e && ok_x) ? f32_to_bf16(out) : (uint16_t)0;
     }

@@ -273,8 +273,7 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
                 float out = vpm_bf16r(acc[0][i]);
                 if constexpr (NSET == 2) {     // round(round(silu_f32(gate)) * up)
                     const float up = vpm_bf16r(acc[1][i]);
-                    const double gg = (double)out;
-                    out = vpm_bf16r(vpm_f32_kept(gg / (1.0 + exp(-gg)))) * up;
+                    out = silu_bf16r(out) * up;
                 }
                 const int64_t r = a.tiles ? a.sorted[start + m] : prow_s[m];
                 a.y[r * a.N + row] = f32_to_bf16(out);

@@ -72,6 +72,22 @@ def test_swiglu_bit_for_bit(dev, dtype):
     _bits_equal(to_numpy(K.swiglu(gu)), ref)
 
 
+def test_swiglu_every_bf16_gate(dev):
+    """silu on every finite bf16 gate value (65280 patterns), bit for bit
+    with the oracle's float64 evaluation, with up = 1 and with random up:
+    the bf16 SwiGLU runs the float32 arithmetic every expert kernel's
+    epilogue shares (a float64 fallback only near bf16 rounding midpoints
+    and past |gate| = 64), so this covers their activation on all inputs."""
+    bits = np.arange(1 << 16, dtype=np.uint32)
+    g = (bits[((bits >> 7) & 0xFF) != 0xFF] << 16).view(np.float32).reshape(1, -1)
+    rng = np.random.default_rng(4)
+    for u in (np.ones_like(g), O.round_to(rng.standard_normal(g.shape).astype(np.float32), "bfloat16")):
+        with np.errstate(over="ignore"):
+            ref = O.swiglu(u, g, "bfloat16")
+        got = K.swiglu(to_torch(g, dev, BF), to_torch(u, dev, BF))
+        _bits_equal(to_numpy(got), ref)
+
+
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
 def test_combine_bit_for_bit(dev, dtype):
     rng = np.random.default_rng(2)
