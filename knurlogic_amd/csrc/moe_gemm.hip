@@ -235,32 +235,45 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_kernel(QgArgs a, int n_tiles,
         }
     }
 
-    // D of block (i, j): tile row 32 i + 8 (r / 4) + 4 h + r % 4, B row 32 j + l32
+    // D of block (i, j): tile row 32 i + 8 (r / 4) + 4 h + r % 4, B row 32 j + l32.
+    // Stored through a buffer view of y: a row's offset from its row id in
+    // 32 bits, and a row past the tile (row id -1) or a column past N at an
+    // offset past the view, so no branch; one v_cvt_pk_bf16_f32 per two rows
+    // (tile rows m and m + 1 of a lane).
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, a.rows * a.N * 2);
+    const uint32_t rowb = (uint32_t)a.N * 2;
+    auto off = [&](int m, bool col_ok, int64_t col) -> uint32_t {
+        const int rid = rid_s[m];
+        return col_ok && rid >= 0 ? (uint32_t)rid * rowb + (uint32_t)col * 2 : MG_DEAD;
+    };
     if constexpr (GLU) {
         const int64_t col = (int64_t)nt * (BN / 2) + wn / 2 + l32;
-        if (col < a.N) {
+        const bool cok = col < a.N;
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int m = wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-                    if (m >= count) continue;
-                    // act = round(round(silu_f32(round(gate))) * round(up))
-                    const float sl = silu_bf16r(mg_bf16r(acc[i][0][r]));
-                    a.y[(int64_t)rid_s[m] * a.N + col] = f32_to_bf16(sl * mg_bf16r(acc[i][1][r]));
-                }
-        }
+            for (int r = 0; r < 16; r += 2) {
+                const int m = wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
+                // act = round(round(silu_f32(round(gate))) * round(up))
+                const float p0 = silu_bf16r(mg_bf16r(acc[i][0][r])) * mg_bf16r(acc[i][1][r]);
+                const float p1 = silu_bf16r(mg_bf16r(acc[i][0][r + 1])) * mg_bf16r(acc[i][1][r + 1]);
+                const uint32_t v = cvt_pk_bf16(p0, p1);
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)v, ry, (int)off(m, cok, col), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(v >> 16), ry, (int)off(m + 1, cok, col), 0, 0);
+            }
     } else {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int64_t col = (int64_t)nt * BN + wn + 32 * j + l32;
-            if (col >= a.N) continue;
+            const bool cok = col < a.N;
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
+                for (int r = 0; r < 16; r += 2) {
                     const int m = wm + 32 * i + 8 * (r / 4) + 4 * h + (r % 4);
-                    if (m < count) a.y[(int64_t)rid_s[m] * a.N + col] = f32_to_bf16(acc[i][j][r]);
+                    const uint32_t v = cvt_pk_bf16(acc[i][j][r], acc[i][j][r + 1]);
+                    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)v, ry, (int)off(m, cok, col), 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(v >> 16), ry, (int)off(m + 1, cok, col), 0, 0);
                 }
         }
     }
@@ -309,8 +322,9 @@ int launch_moe_gemm(const QgArgs& a, int bits, int gs, bool glu, int tile_rows, 
         set_error("moe_gemm: expert tiles of affine weights, K %% 64 == 0");
         return EINVAL_ARG;
     }
-    if (a.xrows * a.K * 2 >= (1LL << 31) || a.erows * (a.K * bits / 8) >= (1LL << 31)) {
-        set_error("moe_gemm: x or an expert's weights past 2 GiB");
+    if (a.xrows * a.K * 2 >= (1LL << 31) || a.erows * (a.K * bits / 8) >= (1LL << 31) ||
+        a.rows * a.N * 2 >= (1LL << 31)) {
+        set_error("moe_gemm: x, y or an expert's weights past 2 GiB");
         return EINVAL_ARG;
     }
     if (tile_rows == 128) return launch_mg_bm<128>(a, bits, gs, glu, tile_slots, st);
