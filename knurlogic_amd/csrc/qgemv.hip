@@ -159,11 +159,15 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
     // x row of each staged row (row ids, pairs and x rows all < 2^31, checked
     // on the host, so 32-bit arithmetic; the divisions by one are skipped)
     const uint32_t mper = (uint32_t)a.Mper, ldiv = (uint32_t)a.lhs_div;
+    // and the output row id of each tile row (-1 past the tile) into LDS,
+    // for the epilogue
+    __shared__ int32_t orow_s[XPASS * 8];
     uint32_t xoff[XPASS];
 #pragma unroll
     for (int p = 0; p < XPASS; p++) {
         const int r = p * 8 + tid / 32;
         xoff[p] = 0x80000000u;
+        if (tid % 32 == 0) orow_s[r] = r < count ? (a.sorted ? a.sorted[start + r] : (int32_t)(start + r)) : -1;
         if (r < count) {
             const uint32_t rid = a.sorted ? (uint32_t)a.sorted[start + r] : (uint32_t)(start + r);
             const uint32_t pr = mper == 1 ? rid : rid / mper;
@@ -382,25 +386,48 @@ __global__ __launch_bounds__(256) void qgemv_kernel(QgArgs a) {
         }
     }
 
+    // Stored through a buffer view of y (or of this split's partials): 32-bit
+    // offsets from the row ids, a row past the tile or a column past N at an
+    // offset past the view (no branch); rows e and e + 1 of a lane share one
+    // v_cvt_pk_bf16_f32.
     const int64_t n = n0 + wr;
-    if (n >= a.N) return;
+    const bool nok = n < a.N;
+    if (GLU || a.S == 1) {
+        const __amdgpu_buffer_rsrc_t ry = make_rsrc(a.y, a.rows * a.N * 2);
+        const uint32_t rowb = (uint32_t)a.N * 2, colb = (uint32_t)n * 2;
 #pragma unroll
-    for (int c = 0; c < MC; c++)
+        for (int c = 0; c < MC; c++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int64_t m = 16 * c + 4 * j4 + e;
-            if (m >= count) continue;
-            const int64_t row = a.sorted ? (int64_t)a.sorted[start + m] : start + m;
-            if constexpr (GLU) {
-                // act = round(round(silu_f32(round(gate))) * round(up))
-                const float sl = silu_bf16r(qg_bf16r(acc[0][c][e]));
-                a.y[row * a.N + n] = f32_to_bf16(sl * qg_bf16r(acc[1][c][e]));
-            } else if (a.S == 1) {
-                a.y[row * a.N + n] = f32_to_bf16(acc[0][c][e]);
-            } else {
-                a.partial[((int64_t)blockIdx.y * a.rows + row) * a.N + n] = acc[0][c][e];
+            for (int e = 0; e < 4; e += 2) {
+                float v0, v1;
+                if constexpr (GLU) {
+                    // act = round(round(silu_f32(round(gate))) * round(up))
+                    v0 = silu_bf16r(qg_bf16r(acc[0][c][e])) * qg_bf16r(acc[1][c][e]);
+                    v1 = silu_bf16r(qg_bf16r(acc[0][c][e + 1])) * qg_bf16r(acc[1][c][e + 1]);
+                } else {
+                    v0 = acc[0][c][e];
+                    v1 = acc[0][c][e + 1];
+                }
+                const uint32_t v = cvt_pk_bf16(v0, v1);
+                const int32_t r0 = orow_s[16 * c + 4 * j4 + e], r1 = orow_s[16 * c + 4 * j4 + e + 1];
+                const uint32_t o0 = nok && r0 >= 0 ? (uint32_t)r0 * rowb + colb : 0x80000000u;
+                const uint32_t o1 = nok && r1 >= 0 ? (uint32_t)r1 * rowb + colb : 0x80000000u;
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)v, ry, (int)o0, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(v >> 16), ry, (int)o1, 0, 0);
             }
-        }
+    } else {
+        const __amdgpu_buffer_rsrc_t rp =
+            make_rsrc(a.partial + (int64_t)blockIdx.y * a.rows * a.N, a.rows * a.N * 4);
+        const uint32_t rowb = (uint32_t)a.N * 4, colb = (uint32_t)n * 4;
+#pragma unroll
+        for (int c = 0; c < MC; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int32_t r = orow_s[16 * c + 4 * j4 + e];
+                const uint32_t o = nok && r >= 0 ? (uint32_t)r * rowb + colb : 0x80000000u;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[0][c][e]), rp, (int)o, 0, 0);
+            }
+    }
 }
 
 // ---- host side ----------------------------------------------------------------
@@ -453,6 +480,10 @@ int launch_qgemv(const QgArgs& a, const QgPlan& p, int bits, int gs, bool glu, i
                  hipStream_t st) {
     if (glu && p.S != 1) {
         set_error("qgemv: the SwiGLU epilogue needs an unsplit K");
+        return EINVAL_ARG;
+    }
+    if (a.rows * a.N * (p.S > 1 ? 4 : 2) >= (1LL << 31)) {
+        set_error("qgemv: an output (or a split's partials) past 2 GiB");
         return EINVAL_ARG;
     }
     const dim3 grid((unsigned)ceil_div(a.N, QG_ROWS), (unsigned)p.S, (unsigned)ntiles);
