@@ -85,13 +85,15 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
     // staged later); or in pair mode (no tiles) pair blockIdx.y alone, its
     // expert straight from rhs
     int e, start, count;
-    __shared__ int32_t prow_s[TM];                   // row ids of a tile formed here
+    __shared__ int32_t prow_s[TM];                   // row ids of the tile (sorted or formed here)
     if (a.tiles) {
         const int32_t* tp = a.tiles + 3 * (int64_t)blockIdx.y;
         count = tp[2];
         if (count <= 0 || count > a.tile_rows) return;   // a tile never exceeds the staged rows
         e = tp[0];
         start = tp[1];
+        // the tile's row ids for the stores (LDS, ordered by the staging barrier)
+        if ((int)threadIdx.x < count) prow_s[threadIdx.x] = a.sorted[start + threadIdx.x];
     } else if (a.pairs) {
         const int pe = pair_tile_load(a.rhs, a.pairs);
         const size_t cbl = (size_t)((a.kc + 63) / 64) * 1024 * (NSET == 2 && a.cb1 != a.cb0 ? 2 : 1);
@@ -355,7 +357,7 @@ __global__ __launch_bounds__(WG) void vq_mfma(VqmArgs a) {
         for (int i = 0; i < 4; i++) {
             const int m = 4 * q + i;
             if (m >= count) continue;
-            const int64_t r = a.tiles ? a.sorted[start + m] : a.pairs ? prow_s[m] : start;
+            const int64_t r = a.tiles || a.pairs ? prow_s[m] : start;
             a.y[r * a.N + row] = res[i];
         }
     };

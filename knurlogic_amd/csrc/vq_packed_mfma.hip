@@ -83,13 +83,15 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
     // a.pairs routed pairs before anything is staged (a slot past the last
     // tile ends here; the working space lies over the x rows, staged later)
     int count = 0, e = 0, start = 0;
-    __shared__ int32_t prow_s[VPM_TILE];             // row ids of a tile formed here
+    __shared__ int32_t prow_s[VPM_TILE];             // row ids of the tile (sorted or formed here)
     if (a.tiles) {
         const int32_t* tp = a.tiles + 3 * (int64_t)blockIdx.y;
         count = tp[2];
         e = tp[0];
         start = tp[1];
         if (count <= 0 || count > a.tile_rows || e < 0 || e >= a.E) return;
+        // the tile's row ids for the stores (LDS, ordered by the staging barrier)
+        if ((int)threadIdx.x < count) prow_s[threadIdx.x] = a.sorted[start + threadIdx.x];
     } else {
         const int pe = pair_tile_load(a.rhs, a.pairs);
         const int cbs = (a.kc * DIM * 2 + 15) & ~15;
@@ -275,7 +277,7 @@ __global__ __launch_bounds__(VPM_WG) void vq_packed_mfma(VpmArgs a) {
                     const float up = vpm_bf16r(acc[1][i]);
                     out = silu_bf16r(out) * up;
                 }
-                const int64_t r = a.tiles ? a.sorted[start + m] : prow_s[m];
+                const int64_t r = prow_s[m];
                 a.y[r * a.N + row] = f32_to_bf16(out);
             }
         }
@@ -333,6 +335,10 @@ int vpm_cblk(int64_t nbt) { return nbt < 1 ? (int)nbt : 1; }
 // ntiles: grid rows (tiles of the sort)
 int launch_vpm(const VpmArgs& a, int pack_bits, int dim, int group, int nset, int64_t ntiles, hipStream_t st) {
     const bool two_cb = nset == 2 && a.cb[1] != a.cb[0];
+    if (a.tile_rows < 1 || a.tile_rows > VPM_TILE) {
+        set_error("vq (packed, MFMA): tile rows %d (1 .. %d)", a.tile_rows, VPM_TILE);
+        return EINVAL_ARG;
+    }
     if (!a.tiles && !(a.rhs && pair_tiles_fit(a.pairs, a.E, a.tile_rows))) {
         set_error("vq (packed, MFMA): no tiles, and %d pairs over %lld experts are not formed in the kernel",
                   a.pairs, (long long)a.E);
