@@ -85,6 +85,50 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
     }
 }
 
+// The bf16 combine with 8 columns per thread: 16-byte loads of each slot's
+// row (a token's slots loaded 8 at a time, before any is summed) and one
+// 16-byte store, the same arithmetic per output (each product rounded to
+// bf16, summed in float64 in slot order, rounded once).  One wave per
+// workgroup; the grid's y dimension walks the tokens.  For H % 8 == 0 and
+// 16-byte aligned y and out.
+__global__ __launch_bounds__(64) void moe_combine_bf16x8(const uint16_t* __restrict__ y,
+                                                         const uint16_t* __restrict__ scores, int64_t T_, int k,
+                                                         int64_t H, uint16_t* __restrict__ out) {
+    const int64_t c = (int64_t)blockIdx.x * 64 + threadIdx.x;      // 8-column group
+    if (c >= H / 8) return;
+    for (int64_t t = blockIdx.y; t < T_; t += gridDim.y) {
+        double acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] = 0.0;
+        for (int s0 = 0; s0 < k; s0 += 8) {
+            u32x4 v[8];
+            float sc[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int s = s0 + j < k ? s0 + j : k - 1;             // past k: a real row, not summed
+                sc[j] = bf16_to_f32(scores[t * k + s]);
+                v[j] = *(const u32x4*)(y + (t * k + s) * H + c * 8);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (s0 + j >= k) break;
+                const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};   // scalars before any bit reinterpretation
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float yv = __uint_as_float(e % 2 ? w[e / 2] & 0xffff0000u : w[e / 2] << 16);
+                    acc[e] += (double)TBF16::round(yv * sc[j]);
+                }
+            }
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            o[e] = (uint32_t)f32_to_bf16(f64_to_f32(acc[2 * e])) |
+                   ((uint32_t)f32_to_bf16(f64_to_f32(acc[2 * e + 1])) << 16);
+        *(u32x4*)(out + t * H + c * 8) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+}
+
 // out[t, h] = round(y[t, h] + round(round(sigmoid_f32(g[t])) * sy[t, h])):
 // SparseMoeBlock's shared expert, gated by sigmoid(shared_expert_gate(x))
 // and added to the routed experts' combine (qwen3_5.py:184-187).
@@ -162,6 +206,12 @@ int kmi_moe_combine(const void* y, const void* scores, int dtype, int64_t T, int
     if (T == 0 || H == 0) return OK;
     KMI_CHECK_ARG(y && scores && out, "moe_combine: null pointer");
     hipStream_t st = (hipStream_t)stream;
+    if (dtype == BF16 && H % 8 == 0 && ((uintptr_t)y | (uintptr_t)out) % 16 == 0) {
+        const dim3 g2((unsigned)ceil_div(H / 8, 64), (unsigned)(T < 65535 ? T : 65535));
+        moe_combine_bf16x8<<<g2, 64, 0, st>>>((const uint16_t*)y, (const uint16_t*)scores, T, k, H, (uint16_t*)out);
+        KMI_CHECK_LAUNCH("moe_combine");
+        return OK;
+    }
     const unsigned grid = grid_for(T * H);
     if (dtype == BF16) moe_combine_kernel<TBF16><<<grid, 256, 0, st>>>(y, scores, T, k, H, out);
     else if (dtype == F16) moe_combine_kernel<TF16><<<grid, 256, 0, st>>>(y, scores, T, k, H, out);
