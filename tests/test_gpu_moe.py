@@ -88,11 +88,12 @@ def test_swiglu_every_bf16_gate(dev):
         _bits_equal(to_numpy(got), ref)
 
 
-@pytest.mark.parametrize("T,H", [(19, 200), (19, 203), (70000, 16)])
+@pytest.mark.parametrize("T,H", [(19, 200), (19, 203), (70000, 16), (600, 2048)])
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
 def test_combine_bit_for_bit(dev, dtype, T, H):
-    """H % 8 == 0 takes the 8-column bf16 kernel (with more tokens than one
-    grid dimension holds at T = 70000), H = 203 the per-element one."""
+    """From 2^20 outputs with H % 8 == 0 the bf16 combine takes the
+    8-column kernel (with more tokens than one grid dimension holds at
+    T = 70000); below that, or at H = 203, the per-element one."""
     rng = np.random.default_rng(2)
     y = O.round_to(rng.standard_normal((T, 8, H)).astype(np.float32), dtype)
     _, sc = O.route(O.round_to(rng.standard_normal((T, 32)).astype(np.float32), dtype), 8, dtype)
