@@ -38,6 +38,20 @@ def test_route_matches_the_oracle_bit_for_bit(dev, dtype, T, E, k):
     _bits_equal(to_numpy(scores), rs)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+@pytest.mark.parametrize("E,k", [(128, 8), (256, 8), (200, 8), (65, 1), (8, 8), (300, 8), (128, 9)])
+def test_route_many_tokens_matches_the_oracle(dev, dtype, E, k):
+    """4096 tokens, experts from 8 to 300 (a partly filled last wave of 64,
+    two experts per thread past 256) and k up to 9: the router gives the
+    oracle's experts and scores bit for bit."""
+    rng = np.random.default_rng(E * 10 + k)
+    logits = O.round_to((rng.standard_normal((4096, E)) * 2).astype(np.float32), dtype)
+    inds, scores = K.moe_route(to_torch(logits, dev, DT[dtype]), k)
+    ri, rs = O.route(logits, k, dtype)
+    np.testing.assert_array_equal(inds.cpu().numpy(), ri)
+    _bits_equal(to_numpy(scores), rs)
+
+
 def test_route_ties_go_to_the_lower_expert(dev):
     """Logits on a coarse grid: many exact ties inside and at the top-k edge."""
     rng = np.random.default_rng(5)
