@@ -163,6 +163,30 @@ def test_vq_switch_glu_full_tiles_and_long_rows(dev, T, E, H, I, k, kc):
     assert_close(to_numpy(got), ref, what=f"vq switch_glu T={T} H={H} kc={kc}")
 
 
+@pytest.mark.parametrize("shared", [True, False])
+def test_vq_switch_glu_tiles_across_16_rows(dev, shared):
+    """Tens of rows per expert with 1-byte codes: experts of 17, 32, 33 and 46
+    rows cut into 16-row tiles (the last one 1, 16, 1 and 14 rows deep);
+    every output checked."""
+    rng = np.random.default_rng(4242 + shared)
+    T, E, H, I, k, kc = 64, 4, 1024, 512, 2, 256
+    (hg, gg), (hu, gu), (hd, gd) = [_vq(rng, E, n, kd, kc, 0, dev) for n, kd in ((I, H), (I, H), (H, I))]
+    if shared:
+        hu, hd = (hu[0], hg[1], hu[2]), (hd[0], hg[1], hd[2])
+        gu, gd = (gu[0], gg[1], gu[2]), (gd[0], gg[1], gd[2])
+    glu = nn.VQSwitchGLU(*(nn.VQSwitchLinear(*g) for g in (gg, gu, gd)))
+    x = bf16_normal(rng, (T, H))
+    order = np.repeat(np.arange(E), [17, 32, 33, 46]).astype(np.int32)
+    inds = np.stack([order[:T], order[T:]], axis=1)          # two distinct experts per token
+    perm = rng.permutation(T)
+    inds = inds[perm]
+    assert (inds[:, 0] != inds[:, 1]).all()
+    fn = lambda h: (lambda xs, e: O.vq_matmul(xs, h[0][e], h[1], h[2][e], 0, "bfloat16"))
+    ref = O.switch_glu(x, inds, fn(hg), fn(hu), fn(hd))
+    got = glu(to_torch(x, dev, BF), torch.from_numpy(inds).to(dev))
+    assert_close(to_numpy(got), ref, what=f"vq switch_glu, tiles across 16 rows, shared={shared}")
+
+
 @pytest.mark.parametrize("T,E,H,I,k,kc", [
     (8, 32, 1024, 512, 4, 100),      # a codebook of fewer than 256 entries
     (4, 4, 512, 256, 2, 256),        # experts over several 4-row tiles, a 256-wide down
