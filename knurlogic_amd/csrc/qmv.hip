@@ -182,7 +182,7 @@ static size_t valu_lds(int64_t K, int bits) {
 // [4096, 4096]: 4.55 us at 1 row per wave, 4.36 at 2; [14336, 4096] stays
 // at 2: 8.0 us, 8.6 at 4).  WV: waves per workgroup, which
 // amortizes the x staging over WV * RPW rows.
-static ValuShape valu_shape(int64_t N, int64_t K, int bits, int64_t tiles) {
+static ValuShape valu_shape(int64_t N, int64_t K, int bits, int64_t tiles, bool mx = false) {
     const int64_t C = K / (128 / bits);
     const int64_t slots = ceil_div(C, 64);
     ValuShape v;
@@ -195,6 +195,11 @@ static ValuShape valu_shape(int64_t N, int64_t K, int bits, int64_t tiles) {
     // smaller workgroups start sooner; longer rows need 8 waves to keep the
     // staging ahead of the weight stream short
     v.WV = K <= 4096 ? 4 : 8;
+    // affine rows of more than 8 slots (two batches of loads) and over 1024
+    // x pieces: 16 waves, which stage at most two pieces per thread (8-bit
+    // [4096, 14336] 13.75 -> 12.9 us; measured slower at 16: rows of one
+    // batch, 4-bit 9.55 -> 10.0, and mxfp8 14.35 -> 14.6)
+    if (!mx && v.RPW == 1 && v.S == 8 && slots > 8 && K / 8 > 2 * 512) v.WV = 16;
     // no more waves per workgroup than the rows need
     while (v.WV > 4 && (int64_t)(v.WV / 2) * v.RPW >= N) v.WV /= 2;
     v.groups = ceil_div(N, (int64_t)v.WV * v.RPW);
@@ -381,7 +386,7 @@ int kmi_qmm_mx(const void* x, int64_t M, int64_t K, int64_t N, const uint32_t* w
         a.gs_shift = 5; a.mx = 1;
         const int tm = tile_rows(kind);
         a.tile_m = tm;
-        const ValuShape v = valu_shape(N, K, bits, ceil_div(M, tm));
+        const ValuShape v = valu_shape(N, K, bits, ceil_div(M, tm), true);
         dim3 grid((unsigned)v.groups, 1, (unsigned)ceil_div(M, tm));
         return launch_valu(a, bits, grid, valu_lds(K, bits), st, v);
     }

@@ -200,6 +200,8 @@ __global__ __launch_bounds__(64 * WV) void qmv_valu_kernel(QmvArgs a) {
 template <int BITS, int RPW, int S>
 static bool launch_wv(const ValuShape& v, const QmvArgs& a, dim3 grid, size_t lds, hipStream_t st) {
     const bool g = a.tiles != nullptr;
+    // 16 waves (affine): one row per wave, eight slots per batch (long rows)
+    constexpr bool W16 = RPW == 1 && S == 8;
     if (a.mx) {                                   // dense only
         if (g) return false;
         if (v.WV == 4) qmv_valu_kernel<BITS, RPW, S, 4, false, true><<<grid, 256, lds, st>>>(a);
@@ -213,6 +215,10 @@ static bool launch_wv(const ValuShape& v, const QmvArgs& a, dim3 grid, size_t ld
     } else if (v.WV == 8) {
         if (g) qmv_valu_kernel<BITS, RPW, S, 8, true, false><<<grid, 512, lds, st>>>(a);
         else qmv_valu_kernel<BITS, RPW, S, 8, false, false><<<grid, 512, lds, st>>>(a);
+    } else if constexpr (W16) {
+        if (v.WV != 16) return false;
+        if (g) qmv_valu_kernel<BITS, RPW, S, 16, true, false><<<grid, 1024, lds, st>>>(a);
+        else qmv_valu_kernel<BITS, RPW, S, 16, false, false><<<grid, 1024, lds, st>>>(a);
     } else {
         return false;
     }

@@ -94,7 +94,8 @@ def test_quantized_matmul_mx(dev, mode, transpose, M):
 
 @pytest.mark.parametrize("mode", ["mxfp4", "mxfp8"])
 @pytest.mark.parametrize("M,K_,N", [(1, 4096, 200), (2, 512, 130), (5, 4096, 200), (9, 768, 64), (16, 4096, 72),
-                                    (16, 320, 200), (17, 512, 130), (40, 256, 96), (64, 1024, 64), (3, 96, 40)])
+                                    (16, 320, 200), (17, 512, 130), (40, 256, 96), (64, 1024, 64), (3, 96, 40),
+                                    (1, 14336, 200)])
 def test_quantized_matmul_mx_decode_kernels(dev, mode, M, K_, N):
     """kmi_qmm_mx's decode kernels (M = 1: the streaming GEMV; 2..16 rows
     with K a multiple of 256: the direct-to-LDS kernel; other rows up to 64:

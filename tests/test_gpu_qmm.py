@@ -221,6 +221,22 @@ def test_gather_qmm_many_rows_per_expert(dev, bits):
     assert_close(to_numpy(y), ref, what="many rows per expert")
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gather_qmm_long_rows(dev, bits):
+    """One row per expert tile with 14336-long rows (4-bit rows in one batch
+    of loads on 8-wave workgroups, 8-bit rows in two on 16-wave ones) and
+    200 output rows (the last workgroup partly past N), against the
+    oracle."""
+    rng = np.random.default_rng(14336 + bits)
+    E, N, K_, T, k = 3, 200, 14336, 3, 2
+    (wq, s, b), (tw, ts, tb) = _weights(rng, (E, N, K_), bits, 64, dev)
+    x = bf16_normal(rng, (T, 1, 1, K_))
+    inds = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    y = K.gather_qmm(to_torch(x, dev, BF), tw, ts, tb, rhs_indices=torch.from_numpy(inds).to(dev), bits=bits)
+    ref = O.gather_qmm(x, wq, s, b, rhs_indices=inds, bits=bits, out_dtype="float32")
+    assert_close(to_numpy(y), ref, what=f"gather_qmm K={K_} bits={bits}")
+
+
 def test_gather_qmm_with_lhs_indices_and_bad_experts(dev):
     rng = np.random.default_rng(21)
     E, N, K_ = 4, 64, 128
